@@ -1,0 +1,18 @@
+"""barracuda_amd -- MI355X (gfx950) implementation of barraCuda's dense ML-ops
+hot path: f32 matmul / batched matmul, row softmax, fused attention forward.
+
+The compute lives in libbarracuda_hip.so (C ABI: include/barracuda_hip.h);
+this package is the host side that mirrors the reference's op API.
+"""
+from .error import (BarracudaError, DeviceError, DeviceLost, DeviceNotAvailable, ExecutionError,
+                    InvalidInput, InvalidOperation, OutOfMemory, ShapeMismatch,
+                    UnsupportedOperation)
+from .tensor import (Attention, BatchMatMul, CausalAttention, FlashAttention, HipDevice, LcgStream,
+                     MatMul, MatmulTiled, ScaledDotProductAttention, Softmax, Tensor, get_device)
+
+__all__ = [
+    "BarracudaError", "DeviceError", "DeviceLost", "DeviceNotAvailable", "ExecutionError",
+    "InvalidInput", "InvalidOperation", "OutOfMemory", "ShapeMismatch", "UnsupportedOperation",
+    "Attention", "BatchMatMul", "CausalAttention", "FlashAttention", "HipDevice", "MatMul",
+    "MatmulTiled", "ScaledDotProductAttention", "Softmax", "Tensor", "get_device", "LcgStream",
+]

@@ -1,0 +1,94 @@
+"""Build libbarracuda_hip.so (gfx950) in-tree, plus the code object used by
+the dispatch_binary path and the CPU oracle used by the tests.
+
+    python -m barracuda_amd.build          # or __graft_entry__.build()
+
+Outputs (git-ignored, shipped with the tree):
+    barracuda_amd/lib/libbarracuda_hip.so
+    barracuda_amd/lib/bch_softmax_rows.hsaco
+    oracle/libbc_oracle.so                  (test infrastructure only)
+"""
+from __future__ import annotations
+
+import concurrent.futures as cf
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+ROOT = PKG.parent
+CSRC = PKG / "csrc"
+LIB = PKG / "lib"
+OBJ = PKG / "lib" / "obj"
+ARCH = os.environ.get("BARRACUDA_HIP_ARCH", "gfx950")
+
+HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+# Packed-FP32 VALU ops are disabled for all device code.
+DEVICE_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall", "-Wno-unused-function", "-Wno-unused-result",
+]
+SOURCES = ["bch_runtime.hip", "softmax_rows.hip", "sgemm_mfma.hip",
+           "sgemm_skinny.hip", "sdpa_fwd.hip", "rng_fill.hip"]
+
+
+def _run(cmd: list[str]) -> None:
+    r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    out = "\n".join(l for l in r.stdout.splitlines()
+                    if "packed-fp32-ops' is not a recognized feature" not in l)
+    if r.returncode != 0:
+        raise RuntimeError(f"command failed ({r.returncode}): {' '.join(cmd)}\n{out}")
+    if out.strip():
+        print(out)
+
+
+def build_hip(verbose: bool = True) -> Path:
+    OBJ.mkdir(parents=True, exist_ok=True)
+    jobs = []
+    for src in SOURCES:
+        obj = OBJ / (Path(src).stem + ".o")
+        jobs.append([HIPCC, *DEVICE_FLAGS, "-c", str(CSRC / src), "-o", str(obj)])
+    # the code object for bch_launch_code_object (dispatch_binary)
+    hsaco = LIB / "bch_softmax_rows.hsaco"
+    jobs.append([HIPCC, f"--offload-arch={ARCH}", "-O3", "-std=c++17", "--genco",
+                 "--no-gpu-bundle-output",
+                 "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+                 str(CSRC / "softmax_rows.hip"), "-o", str(hsaco)])
+    workers = min(len(jobs), max(1, min(8, os.cpu_count() or 1)))
+    with cf.ThreadPoolExecutor(workers) as ex:
+        for f in [ex.submit(_run, j) for j in jobs]:
+            f.result()
+    so = LIB / "libbarracuda_hip.so"
+    tmp = LIB / "libbarracuda_hip.so.tmp"
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp),
+          *[str(OBJ / (Path(s).stem + ".o")) for s in SOURCES],
+          "-Wl,-rpath,/opt/rocm/lib", "-ldl"])
+    os.replace(tmp, so)
+    if verbose:
+        print(f"built {so.relative_to(ROOT)} and {hsaco.relative_to(ROOT)} for {ARCH}")
+    return so
+
+
+def build_oracle(verbose: bool = True) -> Path:
+    odir = ROOT / "oracle"
+    _run(["make", "-s", "-B", "-C", str(odir)])
+    so = odir / "libbc_oracle.so"
+    if verbose:
+        print(f"built {so.relative_to(ROOT)}")
+    return so
+
+
+def build_all(verbose: bool = True) -> None:
+    build_oracle(verbose)
+    build_hip(verbose)
+
+
+if __name__ == "__main__":
+    build_all()
+    sys.exit(0)

@@ -1,0 +1,62 @@
+// bch_internal.h -- launchers shared between the C-ABI (bch_runtime.hip) and
+// the kernel translation units.  Not part of the public ABI.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <stdint.h>
+
+namespace bch {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// 128-bit loads/stores with the non-temporal hint (streamed once; keep them
+// from displacing reusable lines in L2 / the Infinity Cache).
+__device__ __forceinline__ float4 load_nt(const float4* p) {
+  const f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
+  return make_float4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ void store_nt(float4 r, float4* p) {
+  const f32x4 v = {r.x, r.y, r.z, r.w};
+  __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(p));
+}
+
+// Row softmax over a contiguous [rows, cols] f32 matrix (in may equal out).
+hipError_t launch_softmax_rows(hipStream_t s, long long rows, long long cols,
+                               const float* in, float* out);
+// Softmax along the middle axis of [outer, axis, inner].
+hipError_t launch_softmax_axis(hipStream_t s, long long outer, long long axis,
+                               long long inner, const float* in, float* out);
+const char* softmax_kernel_name(long long rows, long long cols);
+
+// C[b] = A[b] . B[b] (row-major), b < batch.  ws/ws_bytes: device scratch
+// of at least sgemm_workspace_bytes(batch, m, n, k) bytes.
+hipError_t launch_sgemm(hipStream_t s, int batch, int m, int n, int k,
+                        const float* A, int lda, long long sA,
+                        const float* B, int ldb, long long sB,
+                        float* C, int ldc, long long sC, void* ws,
+                        size_t ws_bytes);
+size_t sgemm_workspace_bytes(int batch, int m, int n, int k);
+const char* sgemm_kernel_name(int m, int n, int k);
+
+// Skinny (m <= 32) GEMM: streams B once; split-k partials go to ws.
+hipError_t launch_sgemm_skinny(hipStream_t s, int m, int n, int k,
+                               const float* A, int lda, const float* B,
+                               int ldb, float* C, int ldc, void* ws,
+                               size_t ws_bytes);
+size_t sgemm_skinny_workspace_bytes(int m, int n, int k);
+bool sgemm_skinny_applies(int m, int n, int k, const float* A, int lda,
+                          const float* B, int ldb);
+
+// Seeded fills (rng.rs LCG / lattice Box-Muller); state is the value before.
+hipError_t launch_fill_uniform(hipStream_t s, float* out, uint64_t n, uint64_t state, double lo,
+                               double hi);
+hipError_t launch_fill_normal(hipStream_t s, float* out, uint64_t n, uint64_t state, double mu,
+                              double sigma);
+uint64_t lcg_advance(uint64_t state, uint64_t inc, uint64_t n);
+
+// Fused attention forward over [B,H,S,D].
+hipError_t launch_sdpa(hipStream_t s, int B, int H, int Sq, int Skv, int D,
+                       float scale, int causal, const float* q,
+                       const float* k, const float* v, float* o);
+
+}  // namespace bch

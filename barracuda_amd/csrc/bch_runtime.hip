@@ -1,0 +1,457 @@
+// bch_runtime.hip -- the C ABI of libbarracuda_hip.so (include/barracuda_hip.h).
+//
+// A context = one device + one HIP stream + a grow-only scratch workspace +
+// a cache of loaded code objects.  This is the device half of the
+// reference's GpuBackend (crates/barracuda/src/device/backend.rs:244-444):
+// alloc_buffer / upload / download / dispatch, with status codes that map
+// onto BarracudaError (crates/barracuda/src/error.rs:14-130).  Argument and
+// shape validation happens before any HIP call so that it behaves the same
+// with or without a GPU.
+#include <hip/hip_runtime.h>
+
+#include <dlfcn.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <map>
+#include <mutex>
+#include <string>
+
+#include "../../include/barracuda_hip.h"
+#include "bch_internal.h"
+
+struct bch_ctx {
+  int device = -1;
+  hipStream_t stream = nullptr;
+  std::string last_error;
+  std::string co_dir;
+  std::map<std::string, hipModule_t> modules;
+  void* ws = nullptr;
+  size_t ws_bytes = 0;
+};
+
+struct bch_event {
+  hipEvent_t ev = nullptr;
+  int device = -1;
+};
+
+namespace {
+
+thread_local std::string t_last_error;
+
+bch_status fail(bch_ctx* ctx, bch_status st, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  if (ctx) ctx->last_error = buf;
+  t_last_error = buf;
+  return st;
+}
+
+bch_status from_hip(bch_ctx* ctx, hipError_t e, const char* what) {
+  if (e == hipSuccess) return BCH_OK;
+  bch_status st = BCH_E_DEVICE;
+  if (e == hipErrorOutOfMemory) st = BCH_E_OOM;
+  else if (e == hipErrorNoDevice || e == hipErrorInvalidDevice) st = BCH_E_NO_DEVICE;
+  else if (e == hipErrorInvalidImage || e == hipErrorInvalidKernelFile ||
+           e == hipErrorNotFound || e == hipErrorSharedObjectInitFailed ||
+           e == hipErrorNoBinaryForGpu || e == hipErrorFileNotFound)
+    st = BCH_E_MODULE;
+  else if (e == hipErrorLaunchFailure || e == hipErrorLaunchOutOfResources ||
+           e == hipErrorInvalidConfiguration)
+    st = BCH_E_LAUNCH;
+  return fail(ctx, st, "%s: %s (%d)", what, hipGetErrorString(e), (int)e);
+}
+
+bch_status use(bch_ctx* ctx) {
+  hipError_t e = hipSetDevice(ctx->device);
+  return from_hip(ctx, e, "hipSetDevice");
+}
+
+std::string lib_dir() {
+  Dl_info info;
+  if (dladdr(reinterpret_cast<void*>(&bch_status_string), &info) && info.dli_fname) {
+    std::string p(info.dli_fname);
+    size_t s = p.rfind('/');
+    if (s != std::string::npos) return p.substr(0, s);
+  }
+  return ".";
+}
+
+bch_status ensure_ws(bch_ctx* ctx, size_t bytes) {
+  if (bytes <= ctx->ws_bytes) return BCH_OK;
+  if (ctx->ws) {
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) return from_hip(ctx, e, "hipStreamSynchronize");
+    (void)hipFree(ctx->ws);
+    ctx->ws = nullptr;
+    ctx->ws_bytes = 0;
+  }
+  size_t want = bytes < ((size_t)1 << 20) ? ((size_t)1 << 20) : bytes;
+  hipError_t e = hipMalloc(&ctx->ws, want);
+  if (e != hipSuccess) {
+    ctx->ws = nullptr;
+    return from_hip(ctx, e, "workspace hipMalloc");
+  }
+  ctx->ws_bytes = want;
+  return BCH_OK;
+}
+
+bool fail_alloc_injected() {
+  const char* v = getenv("BARRACUDA_HIP_FAIL_ALLOC");
+  return v && v[0] == '1';
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* bch_status_string(bch_status s) {
+  switch (s) {
+    case BCH_OK: return "ok";
+    case BCH_E_INVALID: return "invalid argument";
+    case BCH_E_SHAPE: return "shape mismatch";
+    case BCH_E_NO_DEVICE: return "no device available";
+    case BCH_E_OOM: return "out of device memory";
+    case BCH_E_MODULE: return "code object missing or invalid";
+    case BCH_E_LAUNCH: return "kernel launch failed";
+    case BCH_E_DEVICE: return "device error";
+    case BCH_E_UNSUPPORTED: return "unsupported operation";
+    default: return "unknown status";
+  }
+}
+
+const char* bch_last_error(const bch_ctx* ctx) {
+  if (ctx) return ctx->last_error.c_str();
+  return t_last_error.c_str();
+}
+
+bch_status bch_device_count(int* count) {
+  if (!count) return fail(nullptr, BCH_E_INVALID, "bch_device_count: count is NULL");
+  *count = 0;
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess || n <= 0) {
+    (void)hipGetLastError();
+    return fail(nullptr, BCH_E_NO_DEVICE, "no HIP device available (hipGetDeviceCount: %s)",
+                hipGetErrorString(e));
+  }
+  *count = n;
+  return BCH_OK;
+}
+
+bch_status bch_ctx_create(int device, const char* code_object_dir, bch_ctx** out) {
+  if (!out) return fail(nullptr, BCH_E_INVALID, "bch_ctx_create: out is NULL");
+  *out = nullptr;
+  if (device < 0) {
+    const char* env = getenv("BARRACUDA_HIP_DEVICE");
+    device = env ? atoi(env) : 0;
+  }
+  int n = 0;
+  bch_status st = bch_device_count(&n);
+  if (st != BCH_OK) return st;
+  if (device >= n)
+    return fail(nullptr, BCH_E_NO_DEVICE, "bch_ctx_create: device %d not present (%d visible)", device, n);
+  bch_ctx* ctx = new bch_ctx();
+  ctx->device = device;
+  ctx->co_dir = code_object_dir ? code_object_dir : lib_dir();
+  hipError_t e = hipSetDevice(device);
+  if (e == hipSuccess) e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
+  if (e != hipSuccess) {
+    st = from_hip(nullptr, e, "bch_ctx_create");
+    delete ctx;
+    return st;
+  }
+  *out = ctx;
+  return BCH_OK;
+}
+
+void bch_ctx_destroy(bch_ctx* ctx) {
+  if (!ctx) return;
+  (void)hipSetDevice(ctx->device);
+  if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+  for (auto& kv : ctx->modules) (void)hipModuleUnload(kv.second);
+  if (ctx->ws) (void)hipFree(ctx->ws);
+  if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
+  delete ctx;
+}
+
+bch_status bch_alloc(bch_ctx* ctx, size_t bytes, void** dptr) {
+  if (!ctx || !dptr) return fail(ctx, BCH_E_INVALID, "bch_alloc: NULL argument");
+  *dptr = nullptr;
+  if (bytes == 0) return BCH_OK;
+  if (fail_alloc_injected())
+    return fail(ctx, BCH_E_OOM, "bch_alloc: allocation of %zu bytes failed (injected by BARRACUDA_HIP_FAIL_ALLOC)", bytes);
+  bch_status st = use(ctx);
+  if (st != BCH_OK) return st;
+  hipError_t e = hipMalloc(dptr, bytes);
+  if (e != hipSuccess) {
+    *dptr = nullptr;
+    (void)hipGetLastError();
+    return from_hip(ctx, e, "bch_alloc");
+  }
+  return BCH_OK;
+}
+
+bch_status bch_free(bch_ctx* ctx, void* dptr) {
+  if (!ctx) return fail(ctx, BCH_E_INVALID, "bch_free: ctx is NULL");
+  if (!dptr) return BCH_OK;
+  bch_status st = use(ctx);
+  if (st != BCH_OK) return st;
+  // Work queued on this context may still read the buffer.
+  hipError_t e = hipStreamSynchronize(ctx->stream);
+  if (e == hipSuccess) e = hipFree(dptr);
+  return from_hip(ctx, e, "bch_free");
+}
+
+bch_status bch_upload(bch_ctx* ctx, void* dst, const void* src, size_t bytes) {
+  if (!ctx || (bytes && (!dst || !src))) return fail(ctx, BCH_E_INVALID, "bch_upload: NULL argument");
+  if (!bytes) return BCH_OK;
+  bch_status st = use(ctx);
+  if (st != BCH_OK) return st;
+  hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);  // src may be reused at once
+  return from_hip(ctx, e, "bch_upload");
+}
+
+bch_status bch_download(bch_ctx* ctx, void* dst, const void* src, size_t bytes) {
+  if (!ctx || (bytes && (!dst || !src))) return fail(ctx, BCH_E_INVALID, "bch_download: NULL argument");
+  if (!bytes) return BCH_OK;
+  bch_status st = use(ctx);
+  if (st != BCH_OK) return st;
+  hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  return from_hip(ctx, e, "bch_download");
+}
+
+bch_status bch_memset(bch_ctx* ctx, void* dst, int value, size_t bytes) {
+  if (!ctx || (bytes && !dst)) return fail(ctx, BCH_E_INVALID, "bch_memset: NULL argument");
+  if (!bytes) return BCH_OK;
+  bch_status st = use(ctx);
+  if (st != BCH_OK) return st;
+  return from_hip(ctx, hipMemsetAsync(dst, value, bytes, ctx->stream), "bch_memset");
+}
+
+bch_status bch_sync(bch_ctx* ctx) {
+  if (!ctx) return fail(ctx, BCH_E_INVALID, "bch_sync: ctx is NULL");
+  bch_status st = use(ctx);
+  if (st != BCH_OK) return st;
+  return from_hip(ctx, hipStreamSynchronize(ctx->stream), "bch_sync");
+}
+
+bch_status bch_sgemm_strided_batched(bch_ctx* ctx, int batch, int m, int n, int k,
+                                     const float* A, long long strideA, const float* B,
+                                     long long strideB, float* C, long long strideC);
+
+bch_status bch_sgemm(bch_ctx* ctx, int m, int n, int k, const float* A, int lda,
+                     const float* B, int ldb, float* C, int ldc) {
+  if (m < 0 || n < 0 || k < 0)
+    return fail(ctx, BCH_E_SHAPE, "matmul: negative dimension (m=%d, n=%d, k=%d)", m, n, k);
+  if (lda < (k > 1 ? k : 1) || ldb < (n > 1 ? n : 1) || ldc < (n > 1 ? n : 1))
+    return fail(ctx, BCH_E_SHAPE, "matmul: leading dimension too small (lda=%d k=%d, ldb=%d n=%d, ldc=%d n=%d)",
+                lda, k, ldb, n, ldc, n);
+  if (!ctx) return fail(ctx, BCH_E_INVALID, "matmul: ctx is NULL");
+  if (m == 0 || n == 0) return BCH_OK;
+  if (!C || (k > 0 && (!A || !B))) return fail(ctx, BCH_E_INVALID, "matmul: NULL buffer");
+  bch_status st = use(ctx);
+  if (st != BCH_OK) return st;
+  size_t wsb = bch::sgemm_workspace_bytes(1, m, n, k);
+  if (wsb) {
+    st = ensure_ws(ctx, wsb);
+    if (st != BCH_OK) return st;
+  }
+  hipError_t e = bch::launch_sgemm(ctx->stream, 1, m, n, k, A, lda, 0, B, ldb, 0, C, ldc, 0,
+                                   ctx->ws, ctx->ws_bytes);
+  return from_hip(ctx, e, "matmul launch");
+}
+
+bch_status bch_sgemm_strided_batched(bch_ctx* ctx, int batch, int m, int n, int k,
+                                     const float* A, long long strideA, const float* B,
+                                     long long strideB, float* C, long long strideC) {
+  if (batch < 0 || m < 0 || n < 0 || k < 0)
+    return fail(ctx, BCH_E_SHAPE, "batch_matmul: negative dimension (batch=%d, m=%d, n=%d, k=%d)", batch, m, n, k);
+  if (batch > 1 && (strideA < (long long)m * k || strideB < (long long)k * n || strideC < (long long)m * n))
+    return fail(ctx, BCH_E_SHAPE, "batch_matmul: batch stride smaller than one matrix (sA=%lld, sB=%lld, sC=%lld)",
+                strideA, strideB, strideC);
+  if (!ctx) return fail(ctx, BCH_E_INVALID, "batch_matmul: ctx is NULL");
+  if (batch == 0 || m == 0 || n == 0) return BCH_OK;
+  if (!C || (k > 0 && (!A || !B))) return fail(ctx, BCH_E_INVALID, "batch_matmul: NULL buffer");
+  if (batch > 65535) return fail(ctx, BCH_E_UNSUPPORTED, "batch_matmul: batch %d > 65535", batch);
+  bch_status st = use(ctx);
+  if (st != BCH_OK) return st;
+  size_t wsb = bch::sgemm_workspace_bytes(batch, m, n, k);
+  if (wsb) {
+    st = ensure_ws(ctx, wsb);
+    if (st != BCH_OK) return st;
+  }
+  const int lda = k > 0 ? k : 1, ldb = n, ldc = n;
+  hipError_t e = bch::launch_sgemm(ctx->stream, batch, m, n, k, A, lda, strideA, B, ldb, strideB, C,
+                                   ldc, strideC, ctx->ws, ctx->ws_bytes);
+  return from_hip(ctx, e, "batch_matmul launch");
+}
+
+bch_status bch_softmax_rows(bch_ctx* ctx, long long rows, long long cols, const float* in, float* out) {
+  if (rows < 1 || cols < 1)
+    return fail(ctx, BCH_E_SHAPE, "softmax: empty dimension (rows=%lld, cols=%lld)", rows, cols);
+  if (!ctx) return fail(ctx, BCH_E_INVALID, "softmax: ctx is NULL");
+  if (!in || !out) return fail(ctx, BCH_E_INVALID, "softmax: NULL buffer");
+  bch_status st = use(ctx);
+  if (st != BCH_OK) return st;
+  return from_hip(ctx, bch::launch_softmax_rows(ctx->stream, rows, cols, in, out), "softmax launch");
+}
+
+bch_status bch_softmax_axis(bch_ctx* ctx, long long outer, long long axis, long long inner,
+                            const float* in, float* out) {
+  if (outer < 1 || axis < 1 || inner < 1)
+    return fail(ctx, BCH_E_SHAPE, "softmax_dim: empty dimension (outer=%lld, axis=%lld, inner=%lld)", outer,
+                axis, inner);
+  if (!ctx) return fail(ctx, BCH_E_INVALID, "softmax_dim: ctx is NULL");
+  if (!in || !out) return fail(ctx, BCH_E_INVALID, "softmax_dim: NULL buffer");
+  bch_status st = use(ctx);
+  if (st != BCH_OK) return st;
+  return from_hip(ctx, bch::launch_softmax_axis(ctx->stream, outer, axis, inner, in, out),
+                  "softmax_dim launch");
+}
+
+bch_status bch_sdpa_fwd(bch_ctx* ctx, int B, int H, int Sq, int Skv, int D, float scale, int causal,
+                        const float* q, const float* k, const float* v, float* o) {
+  if (B < 1 || H < 1 || Sq < 1 || Skv < 1 || D < 1)
+    return fail(ctx, BCH_E_SHAPE, "attention: empty dimension (B=%d, H=%d, Sq=%d, Skv=%d, D=%d)", B, H, Sq,
+                Skv, D);
+  if (causal && Sq != Skv)
+    return fail(ctx, BCH_E_SHAPE, "attention: causal mask needs Sq == Skv (shape mismatch %d vs %d)", Sq, Skv);
+  if (D > 128) return fail(ctx, BCH_E_UNSUPPORTED, "attention: head dimension %d > 128", D);
+  if (!ctx) return fail(ctx, BCH_E_INVALID, "attention: ctx is NULL");
+  if (!q || !k || !v || !o) return fail(ctx, BCH_E_INVALID, "attention: NULL buffer");
+  bch_status st = use(ctx);
+  if (st != BCH_OK) return st;
+  return from_hip(ctx, bch::launch_sdpa(ctx->stream, B, H, Sq, Skv, D, scale, causal, q, k, v, o),
+                  "attention launch");
+}
+
+bch_status bch_fill_uniform(bch_ctx* ctx, float* dst, size_t n, unsigned long long* state, double lo,
+                            double hi) {
+  if (!ctx || !state || (n && !dst)) return fail(ctx, BCH_E_INVALID, "fill_uniform: NULL argument");
+  if (!(hi >= lo)) return fail(ctx, BCH_E_INVALID, "fill_uniform: hi < lo");
+  bch_status st = use(ctx);
+  if (st != BCH_OK) return st;
+  st = from_hip(ctx, bch::launch_fill_uniform(ctx->stream, dst, n, *state, lo, hi), "fill_uniform launch");
+  if (st == BCH_OK) *state = bch::lcg_advance(*state, 1, n);
+  return st;
+}
+
+bch_status bch_fill_normal(bch_ctx* ctx, float* dst, size_t n, unsigned long long* state, double mu,
+                           double sigma) {
+  if (!ctx || !state || (n && !dst)) return fail(ctx, BCH_E_INVALID, "fill_normal: NULL argument");
+  bch_status st = use(ctx);
+  if (st != BCH_OK) return st;
+  st = from_hip(ctx, bch::launch_fill_normal(ctx->stream, dst, n, *state, mu, sigma), "fill_normal launch");
+  if (st == BCH_OK) *state = bch::lcg_advance(*state, 1442695040888963407ULL, 2 * (uint64_t)n);
+  return st;
+}
+
+bch_status bch_launch_code_object(bch_ctx* ctx, const void* code_object, size_t len, const char* entry,
+                                  const unsigned grid[3], const unsigned block[3], void** args, size_t nargs,
+                                  size_t shared_bytes) {
+  if (!ctx || !code_object || !entry || !grid || !block || (nargs && !args))
+    return fail(ctx, BCH_E_INVALID, "dispatch_binary: NULL argument");
+  for (int i = 0; i < 3; ++i)
+    if (grid[i] == 0 || block[i] == 0)
+      return fail(ctx, BCH_E_SHAPE, "dispatch_binary: zero grid/block dimension %d", i);
+  if ((unsigned long long)block[0] * block[1] * block[2] > 1024)
+    return fail(ctx, BCH_E_SHAPE, "dispatch_binary: block of %u x %u x %u threads exceeds 1024", block[0],
+                block[1], block[2]);
+  bch_status st = use(ctx);
+  if (st != BCH_OK) return st;
+  std::string key;
+  if (len == 0) {
+    std::string path(static_cast<const char*>(code_object));
+    if (!path.empty() && path[0] != '/') path = ctx->co_dir + "/" + path;
+    key = "file:" + path;
+    if (!ctx->modules.count(key)) {
+      FILE* f = fopen(path.c_str(), "rb");
+      if (!f) return fail(ctx, BCH_E_MODULE, "dispatch_binary: cannot open code object %s", path.c_str());
+      fclose(f);
+      hipModule_t mod;
+      hipError_t e = hipModuleLoad(&mod, path.c_str());
+      if (e != hipSuccess) return from_hip(ctx, e, "hipModuleLoad");
+      ctx->modules[key] = mod;
+    }
+  } else {
+    // Key in-memory images by address + length + a cheap content hash.
+    const unsigned char* p = static_cast<const unsigned char*>(code_object);
+    unsigned long long h = 1469598103934665603ULL;
+    for (size_t i = 0; i < len; ++i) h = (h ^ p[i]) * 1099511628211ULL;
+    char kb[64];
+    snprintf(kb, sizeof(kb), "mem:%zu:%llx", len, h);
+    key = kb;
+    if (!ctx->modules.count(key)) {
+      // A code object is an ELF image or a clang offload bundle of them;
+      // reject anything else before HIP sees it.
+      static const char kBundle[] = "__CLANG_OFFLOAD_BUNDLE__";
+      const bool elf = len >= 4 && p[0] == 0x7f && p[1] == 'E' && p[2] == 'L' && p[3] == 'F';
+      const bool bundle = len >= sizeof(kBundle) - 1 && memcmp(p, kBundle, sizeof(kBundle) - 1) == 0;
+      if (!elf && !bundle)
+        return fail(ctx, BCH_E_MODULE, "dispatch_binary: image is not an ELF code object");
+      hipModule_t mod;
+      hipError_t e = hipModuleLoadData(&mod, code_object);
+      if (e != hipSuccess) return from_hip(ctx, e, "hipModuleLoadData");
+      ctx->modules[key] = mod;
+    }
+  }
+  hipFunction_t fn;
+  hipError_t e = hipModuleGetFunction(&fn, ctx->modules[key], entry);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(ctx, BCH_E_MODULE, "dispatch_binary: entry point '%s' not found in code object", entry);
+  }
+  e = hipModuleLaunchKernel(fn, grid[0], grid[1], grid[2], block[0], block[1], block[2],
+                            (unsigned)shared_bytes, ctx->stream, args, nullptr);
+  return from_hip(ctx, e, "hipModuleLaunchKernel");
+}
+
+bch_status bch_event_create(bch_ctx* ctx, bch_event** ev) {
+  if (!ctx || !ev) return fail(ctx, BCH_E_INVALID, "bch_event_create: NULL argument");
+  *ev = nullptr;
+  bch_status st = use(ctx);
+  if (st != BCH_OK) return st;
+  bch_event* x = new bch_event();
+  x->device = ctx->device;
+  hipError_t e = hipEventCreate(&x->ev);
+  if (e != hipSuccess) {
+    delete x;
+    return from_hip(ctx, e, "hipEventCreate");
+  }
+  *ev = x;
+  return BCH_OK;
+}
+
+bch_status bch_event_record(bch_ctx* ctx, bch_event* ev) {
+  if (!ctx || !ev) return fail(ctx, BCH_E_INVALID, "bch_event_record: NULL argument");
+  bch_status st = use(ctx);
+  if (st != BCH_OK) return st;
+  return from_hip(ctx, hipEventRecord(ev->ev, ctx->stream), "hipEventRecord");
+}
+
+bch_status bch_event_elapsed_ms(bch_event* start, bch_event* stop, float* ms) {
+  if (!start || !stop || !ms) return fail(nullptr, BCH_E_INVALID, "bch_event_elapsed_ms: NULL argument");
+  hipError_t e = hipSetDevice(stop->device);
+  if (e == hipSuccess) e = hipEventSynchronize(stop->ev);
+  if (e == hipSuccess) e = hipEventElapsedTime(ms, start->ev, stop->ev);
+  return from_hip(nullptr, e, "hipEventElapsedTime");
+}
+
+void bch_event_destroy(bch_event* ev) {
+  if (!ev) return;
+  (void)hipSetDevice(ev->device);
+  (void)hipEventDestroy(ev->ev);
+  delete ev;
+}
+
+const char* bch_sgemm_kernel_name(int m, int n, int k) { return bch::sgemm_kernel_name(m, n, k); }
+
+}  // extern "C"

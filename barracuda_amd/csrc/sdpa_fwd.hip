@@ -1,0 +1,296 @@
+// sdpa_fwd.hip -- fused scaled-dot-product attention forward for gfx950.
+//
+// Replaces the reference's three-pass attention (crates/barracuda/src/ops/
+// attention/compute.rs:21-111: K6 shaders/math/attention_matmul_f64.wgsl
+// writes the [B,H,Sq,Skv] scores, K7 activation/attention_softmax_f64.wgsl
+// normalises them, K9 attention/attention_apply_f64.wgsl multiplies by V),
+// its causal variant (ops/causal_attn/compute.rs:24-115 with K8, and the CPU
+// ops/causal_attention.rs:52-134) and FlashAttention (ops/flash_attention.rs
+// :96-145, K13).  Contract: o[b,h,i,:] = sum_j softmax_j(scale q_i . k_j) v_j,
+// j <= i when causal.  The score matrix is never written to memory.
+//
+// Layout: q [B,H,Sq,D], k and v [B,H,Skv,D], o [B,H,Sq,D], f32 row-major.
+//
+// Design (FP32 MFMA for both products, v_mfma_f32_32x32x2_f32):
+//   * A workgroup = 4 wavefronts = 128 queries of one (b,h); wavefront w owns
+//     queries q0 + 32w .. +31, lane l's query is l % 32.  Key blocks of 32 are
+//     streamed through LDS, double-buffered, one barrier per block.
+//   * Scores are computed transposed, S^T = K Q^T (32 keys x 32 queries), so
+//     each lane holds 16 scores of ITS query: the row max and row sum are
+//     in-lane plus one exchange between the two lane halves.  The q operand
+//     stays in registers for the whole kernel, pre-multiplied by
+//     scale*log2(e) so the softmax uses exp2 directly.
+//   * The PV product is computed as O^T += V^T P^T, whose B operand is
+//     exactly the P values the lane already holds (value r of the S^T block
+//     is key 8(r/4) + 4(l/32) + r%4), so P never leaves registers.  V is
+//     stored transposed in LDS ([d][key]) so the A operand is one 128-bit
+//     LDS read per four MFMAs; K is stored [key][d] for the same reason.
+//   * Online softmax (running max m and sum l per query, O rescaled by
+//     2^(m_old - m_new)); the final O is divided by l.
+//   * Causal: key blocks past the workgroup's last query are not loaded;
+//     blocks entirely above a wavefront's diagonal are skipped by that
+//     wavefront; the diagonal block is masked per element.  Workgroups are
+//     issued longest-first.
+#include "bch_internal.h"
+
+#include <math.h>
+
+namespace {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kBQ = 128;  // queries per workgroup
+constexpr int kBKV = 32;  // keys per block
+constexpr int kVLD = kBKV + 4;
+constexpr float kLog2E = 1.44269504088896340736f;
+
+template <int DP>
+struct SdpaCfg {
+  static constexpr int KLD = DP + 4;
+  static constexpr int K_F4 = kBKV * DP / 4 / 256;     // float4 of K per thread
+  static constexpr int V_BLK = kBKV * DP / 16;          // 4x4 V blocks per tile
+  static constexpr int LDS_FLOATS = 2 * (kBKV * KLD + DP * kVLD);
+  static_assert(K_F4 >= 1, "K tile must cover the workgroup");
+};
+
+template <int DP, bool FULL>
+__global__ __launch_bounds__(256) void sdpa_fwd_kernel(
+    int Sq, int Skv, int D, float qscale, int causal, const float* __restrict__ q,
+    const float* __restrict__ k, const float* __restrict__ v, float* __restrict__ o,
+    int qblocks) {
+  using G = SdpaCfg<DP>;
+  constexpr int KLD = G::KLD;
+  extern __shared__ float4 smem4[];
+  float* smem = reinterpret_cast<float*>(smem4);
+  float* Ks = smem;                        // [2][kBKV][KLD]
+  float* Vt = smem + 2 * kBKV * KLD;       // [2][DP][kVLD]
+
+  int qb = blockIdx.x % qblocks;
+  const int bh = blockIdx.x / qblocks;
+  if (causal) qb = qblocks - 1 - qb;  // longest rows first
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int li = lane & 31, lh = lane >> 5;
+  const int q0w = qb * kBQ + wave * 32;  // first query of this wavefront
+  const int myq = q0w + li;
+
+  const float* qh = q + (long long)bh * Sq * D;
+  const float* kh = k + (long long)bh * Skv * D;
+  const float* vh = v + (long long)bh * Skv * D;
+  float* oh = o + (long long)bh * Sq * D;
+
+  // ---- q operand: qf[c] = q[myq][8c + 4lh .. +3] * scale * log2(e) ----
+  float4 qf[DP / 8];
+#pragma unroll
+  for (int c = 0; c < DP / 8; ++c) {
+    const int d0 = 8 * c + 4 * lh;
+    float t[4];
+    if (FULL) {
+      const float4 x = *reinterpret_cast<const float4*>(qh + (long long)myq * D + d0);
+      t[0] = x.x; t[1] = x.y; t[2] = x.z; t[3] = x.w;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        t[e] = (myq < Sq && d0 + e < D) ? qh[(long long)myq * D + d0 + e] : 0.0f;
+    }
+    qf[c] = make_float4(t[0] * qscale, t[1] * qscale, t[2] * qscale, t[3] * qscale);
+  }
+
+  // ---- key/value tile staging ----
+  float4 rk[G::K_F4];
+  float4 rv[4];
+  constexpr int KD4 = DP / 4;  // float4 per K row
+  auto load_kv = [&](int kb) {
+#pragma unroll
+    for (int f = 0; f < G::K_F4; ++f) {
+      const int idx = tid + f * 256;
+      const int key = idx / KD4, d0 = (idx % KD4) * 4;
+      const int gk = kb + key;
+      if (FULL) {
+        rk[f] = *reinterpret_cast<const float4*>(kh + (long long)gk * D + d0);
+      } else {
+        float t[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) t[e] = (gk < Skv && d0 + e < D) ? kh[(long long)gk * D + d0 + e] : 0.0f;
+        rk[f] = make_float4(t[0], t[1], t[2], t[3]);
+      }
+    }
+    if (tid < G::V_BLK) {
+      const int kq = tid / KD4, dq = tid % KD4;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int gk = kb + 4 * kq + e, d0 = 4 * dq;
+        if (FULL) {
+          rv[e] = *reinterpret_cast<const float4*>(vh + (long long)gk * D + d0);
+        } else {
+          float t[4];
+#pragma unroll
+          for (int c = 0; c < 4; ++c) t[c] = (gk < Skv && d0 + c < D) ? vh[(long long)gk * D + d0 + c] : 0.0f;
+          rv[e] = make_float4(t[0], t[1], t[2], t[3]);
+        }
+      }
+    }
+  };
+  auto store_kv = [&](int buf) {
+    float* ks = Ks + buf * kBKV * KLD;
+    float* vt = Vt + buf * DP * kVLD;
+#pragma unroll
+    for (int f = 0; f < G::K_F4; ++f) {
+      const int idx = tid + f * 256;
+      const int key = idx / KD4, d0 = (idx % KD4) * 4;
+      *reinterpret_cast<float4*>(ks + key * KLD + d0) = rk[f];
+    }
+    if (tid < G::V_BLK) {
+      const int kq = tid / KD4, dq = tid % KD4;
+      float* base = vt + (4 * dq) * kVLD + 4 * kq;
+      *reinterpret_cast<float4*>(base + 0 * kVLD) = make_float4(rv[0].x, rv[1].x, rv[2].x, rv[3].x);
+      *reinterpret_cast<float4*>(base + 1 * kVLD) = make_float4(rv[0].y, rv[1].y, rv[2].y, rv[3].y);
+      *reinterpret_cast<float4*>(base + 2 * kVLD) = make_float4(rv[0].z, rv[1].z, rv[2].z, rv[3].z);
+      *reinterpret_cast<float4*>(base + 3 * kVLD) = make_float4(rv[0].w, rv[1].w, rv[2].w, rv[3].w);
+    }
+  };
+
+  f32x16 oacc[DP / 32];
+#pragma unroll
+  for (int b = 0; b < DP / 32; ++b)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) oacc[b][r] = 0.0f;
+  float m_run = -INFINITY, l_run = 0.0f;
+
+  int kend = Skv;
+  if (causal) kend = min(Skv, qb * kBQ + kBQ);
+  const int nkb = (kend + kBKV - 1) / kBKV;
+
+  if (nkb > 0) {
+    load_kv(0);
+    store_kv(0);
+  }
+  __syncthreads();
+
+  for (int t = 0; t < nkb; ++t) {
+    const int cur = t & 1;
+    const int kb = t * kBKV;
+    if (t + 1 < nkb) load_kv(kb + kBKV);
+
+    // wave-uniform: skip blocks fully above this wavefront's diagonal and
+    // wavefronts whose queries are all past Sq
+    const bool active = (q0w < Sq) && !(causal && kb > q0w + 31);
+    if (active) {
+      const float* ks = Ks + cur * kBKV * KLD + li * KLD + 4 * lh;
+      f32x16 s;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[r] = 0.0f;
+#pragma unroll
+      for (int c = 0; c < DP / 8; ++c) {
+        const float4 kf = *reinterpret_cast<const float4*>(ks + 8 * c);
+        s = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.x, qf[c].x, s, 0, 0, 0);
+        s = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.y, qf[c].y, s, 0, 0, 0);
+        s = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.z, qf[c].z, s, 0, 0, 0);
+        s = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.w, qf[c].w, s, 0, 0, 0);
+      }
+      // value r: key kb + 8(r/4) + 4lh + r%4, query myq
+      const bool need_mask = (!FULL && kb + kBKV > Skv) || (causal && kb + kBKV - 1 > q0w);
+      if (need_mask) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = kb + 8 * (r >> 2) + 4 * lh + (r & 3);
+          if (key >= Skv || (causal && key > myq)) s[r] = -INFINITY;
+        }
+      }
+      float bm = s[0];
+#pragma unroll
+      for (int r = 1; r < 16; ++r) bm = fmaxf(bm, s[r]);
+      bm = fmaxf(bm, __shfl_xor(bm, 32));
+      const float m_new = fmaxf(m_run, bm);
+      const float m_use = (m_new == -INFINITY) ? 0.0f : m_new;
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+      float rs = 0.0f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        s[r] = __builtin_amdgcn_exp2f(s[r] - m_use);
+        rs += s[r];
+      }
+      rs += __shfl_xor(rs, 32);
+      l_run = l_run * alpha + rs;
+      m_run = m_new;
+#pragma unroll
+      for (int b = 0; b < DP / 32; ++b)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) oacc[b][r] *= alpha;
+
+      const float* vs = Vt + cur * DP * kVLD + li * kVLD + 4 * lh;
+#pragma unroll
+      for (int b = 0; b < DP / 32; ++b) {
+#pragma unroll
+        for (int a = 0; a < 4; ++a) {
+          const float4 vf = *reinterpret_cast<const float4*>(vs + b * 32 * kVLD + 8 * a);
+          oacc[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(vf.x, s[4 * a + 0], oacc[b], 0, 0, 0);
+          oacc[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(vf.y, s[4 * a + 1], oacc[b], 0, 0, 0);
+          oacc[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(vf.z, s[4 * a + 2], oacc[b], 0, 0, 0);
+          oacc[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(vf.w, s[4 * a + 3], oacc[b], 0, 0, 0);
+        }
+      }
+    }
+    if (t + 1 < nkb) store_kv(cur ^ 1);
+    __syncthreads();
+  }
+
+  // ---- epilogue: value r of block b is d = 32b + 8(r/4) + 4lh + r%4 ----
+  if (myq < Sq) {
+    const float inv = 1.0f / l_run;
+#pragma unroll
+    for (int b = 0; b < DP / 32; ++b) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int d = 32 * b + 8 * (r >> 2) + 4 * lh + (r & 3);
+        if (FULL || d < D) oh[(long long)myq * D + d] = oacc[b][r] * inv;
+      }
+    }
+  }
+}
+
+template <int DP, bool FULL>
+hipError_t launch_dp(hipStream_t s, int B, int H, int Sq, int Skv, int D, float scale, int causal,
+                     const float* q, const float* k, const float* v, float* o) {
+  const int qblocks = (Sq + kBQ - 1) / kBQ;
+  const long long blocks = (long long)B * H * qblocks;
+  if (blocks > 0x7fffffffLL) return hipErrorInvalidValue;
+  const size_t lds = sizeof(float) * SdpaCfg<DP>::LDS_FLOATS;
+  auto kern = sdpa_fwd_kernel<DP, FULL>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), lds, s, Sq, Skv, D, scale * kLog2E,
+                     causal, q, k, v, o, qblocks);
+  return hipGetLastError();
+}
+
+template <int DP>
+hipError_t launch_d(hipStream_t s, int B, int H, int Sq, int Skv, int D, float scale, int causal,
+                    const float* q, const float* k, const float* v, float* o) {
+  const bool full = D == DP && Sq % kBQ == 0 && Skv % kBKV == 0 &&
+                    (reinterpret_cast<uintptr_t>(q) & 15) == 0 &&
+                    (reinterpret_cast<uintptr_t>(k) & 15) == 0 &&
+                    (reinterpret_cast<uintptr_t>(v) & 15) == 0;
+  if (full) return launch_dp<DP, true>(s, B, H, Sq, Skv, D, scale, causal, q, k, v, o);
+  return launch_dp<DP, false>(s, B, H, Sq, Skv, D, scale, causal, q, k, v, o);
+}
+
+}  // namespace
+
+namespace bch {
+
+hipError_t launch_sdpa(hipStream_t s, int B, int H, int Sq, int Skv, int D, float scale, int causal,
+                       const float* q, const float* k, const float* v, float* o) {
+  if (D <= 32) return launch_d<32>(s, B, H, Sq, Skv, D, scale, causal, q, k, v, o);
+  if (D <= 64) return launch_d<64>(s, B, H, Sq, Skv, D, scale, causal, q, k, v, o);
+  if (D <= 128) return launch_d<128>(s, B, H, Sq, Skv, D, scale, causal, q, k, v, o);
+  return hipErrorInvalidValue;
+}
+
+}  // namespace bch

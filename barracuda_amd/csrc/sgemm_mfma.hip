@@ -1,0 +1,304 @@
+// sgemm_mfma.hip -- f32 GEMM on the gfx950 FP32 matrix cores.
+//
+// Replaces MatMul::execute (crates/barracuda/src/ops/matmul.rs:89-214; WGSL
+// kernels K1 shaders/math/matmul_gpu_evolved_f64.wgsl, K2
+// matmul_cpu_tiled_f64.wgsl, K3 matmul_tiled_f64.wgsl), MatmulTiled
+// (ops/matmul_tiled.rs:62-122) and BatchMatMul (ops/batch_matmul.rs:47-144,
+// K5 batch_matmul_f64.wgsl).  Contract: C[m,n] = sum_p A[m,p] B[p,n], f32
+// inputs, f32 accumulation, row-major.
+//
+// Design:
+//   * v_mfma_f32_32x32x2_f32: a wavefront multiplies a 32x2 A block by a 2x32
+//     B block into a 32x32 f32 accumulator (16 values per lane).  Lane l
+//     supplies A[l%32][l/32] and B[l/32][l%32]; result value r of lane l is
+//     C[8*(r/4) + 4*(l/32) + r%4][l%32].
+//   * The k index each lane half feeds is free (the MFMA sums over it), so
+//     lane half h takes k = 8c + 4h + s in MFMA step s of 8-wide chunk c.
+//     Both operands are then 4 consecutive k values per lane: one
+//     ds_read_b128 per 32-row block feeds four MFMAs.  To make that true for
+//     B as well, B tiles are stored k-contiguous ([n][k]) in LDS: each thread
+//     loads a 4(k) x 4(n) block with four 128-bit global loads and writes it
+//     transposed with four 128-bit LDS stores.
+//   * Block tile BM x BN x BK, four wavefronts in a 2x2 grid, each owning a
+//     (BM/2) x (BN/2) sub-tile of (BM/64) x (BN/64) MFMA blocks.  LDS rows
+//     are padded by 4 floats so the 128-bit reads of 32 consecutive rows do
+//     not collide on banks.  LDS is double-buffered: the global loads of
+//     tile t+1 are issued before the MFMAs of tile t and land in registers,
+//     then go to the other LDS buffer; one barrier per k-tile.
+//   * Workgroup -> tile mapping is XCD-aware: gfx950 dispatches workgroups
+//     round-robin over 8 XCDs, so consecutive workgroup ids are remapped to
+//     one XCD's contiguous range of tiles, then walked in groups of 8 tile
+//     rows so concurrently running tiles share A and B panels in that
+//     XCD's L2.
+//   * CHECK=false needs m % BM == 0, n % BN == 0, k % BK == 0, lda/ldb/
+//     strides multiples of 4 and 16-byte aligned A/B; CHECK=true guards
+//     every load (zero fill) and store and handles any shape and alignment.
+#include "bch_internal.h"
+
+#include <stdint.h>
+
+namespace {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kThreads = 256;
+
+template <int BM, int BN, int BK>
+struct Cfg {
+  static constexpr int LDK = BK + 4;                 // padded LDS row (floats)
+  static constexpr int A_F4 = BM * BK / 4 / kThreads;  // float4 of A per thread
+  static constexpr int B_BLK = BK * BN / 16 / kThreads;  // 4x4 B blocks per thread
+  static constexpr int TM = BM / 64;                 // MFMA blocks per wave (m)
+  static constexpr int TN = BN / 64;                 // MFMA blocks per wave (n)
+  static constexpr int LDS_FLOATS = 2 * (BM + BN) * LDK;
+  static_assert(BM % 64 == 0 && BN % 64 == 0, "tile must be a multiple of 64");
+  static_assert(BK % 8 == 0, "BK must be a multiple of 8");
+  static_assert(A_F4 * kThreads * 4 == BM * BK, "A tile must split evenly");
+  static_assert(B_BLK * kThreads * 16 == BK * BN, "B tile must split evenly");
+};
+
+__device__ __forceinline__ float4 ld4(const float* p) {
+  return *reinterpret_cast<const float4*>(p);
+}
+
+template <int BM, int BN, int BK, bool CHECK>
+__global__ __launch_bounds__(kThreads) void sgemm_mfma_kernel(
+    int M, int N, int K, const float* __restrict__ A, int lda, long long sA,
+    const float* __restrict__ B, int ldb, long long sB, float* __restrict__ C,
+    int ldc, long long sC, int tiles_m, int tiles_n) {
+  using G = Cfg<BM, BN, BK>;
+  constexpr int LDK = G::LDK;
+  extern __shared__ float4 smem4[];
+  float* smem = reinterpret_cast<float*>(smem4);
+  float* As = smem;                      // [2][BM][LDK]
+  float* Bs = smem + 2 * BM * LDK;       // [2][BN][LDK], k-contiguous
+
+  // ---- tile mapping (XCD-aware, grouped) ----
+  const int ntiles = tiles_m * tiles_n;
+  int p = blockIdx.x;
+  int lt = p;
+  if ((ntiles & 7) == 0) lt = (p & 7) * (ntiles >> 3) + (p >> 3);
+  constexpr int GROUP = 8;
+  const int group_size = GROUP * tiles_n;
+  const int g = lt / group_size;
+  const int first_m = g * GROUP;
+  const int gm = min(tiles_m - first_m, GROUP);
+  const int within = lt - g * group_size;
+  const int tile_m = first_m + within % gm;
+  const int tile_n = within / gm;
+  const int m0 = tile_m * BM, n0 = tile_n * BN;
+
+  const long long bz = blockIdx.y;
+  A += bz * sA;
+  B += bz * sB;
+  C += bz * sC;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int li = lane & 31, lh = lane >> 5;
+  const int wm = (wave >> 1) * (BM / 2);
+  const int wn = (wave & 1) * (BN / 2);
+
+  // ---- global -> register staging ----
+  // A: float4 f covers row (tid / (BK/4)) + f * (kThreads / (BK/4)), cols
+  //    4*(tid % (BK/4)) .. +3 of the k-tile.
+  constexpr int A_TPR = BK / 4;                 // threads per A row
+  constexpr int A_RSTEP = kThreads / A_TPR;     // rows per float4 round
+  const int a_r = tid / A_TPR, a_c = (tid % A_TPR) * 4;
+  // B: 4x4 block q covers k rows 4*kq .. +3 and n cols 4*nq .. +3 where
+  //    blk = tid + q*kThreads, nq = blk % (BN/4), kq = blk / (BN/4).
+  constexpr int B_NQ = BN / 4;
+
+  float4 ra[G::A_F4];
+  float4 rb[G::B_BLK][4];
+
+  auto load_tile = [&](int k0) {
+#pragma unroll
+    for (int f = 0; f < G::A_F4; ++f) {
+      const int r = a_r + f * A_RSTEP;
+      const int gr = m0 + r, gc = k0 + a_c;
+      if (!CHECK) {
+        ra[f] = ld4(A + (long long)gr * lda + gc);
+      } else {
+        float t[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          t[e] = (gr < M && gc + e < K) ? A[(long long)gr * lda + gc + e] : 0.0f;
+        ra[f] = make_float4(t[0], t[1], t[2], t[3]);
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < G::B_BLK; ++q) {
+      const int blk = tid + q * kThreads;
+      const int nq = blk % B_NQ, kq = blk / B_NQ;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int gk = k0 + 4 * kq + e, gn = n0 + 4 * nq;
+        if (!CHECK) {
+          rb[q][e] = ld4(B + (long long)gk * ldb + gn);
+        } else {
+          float t[4];
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+            t[c] = (gk < K && gn + c < N) ? B[(long long)gk * ldb + gn + c] : 0.0f;
+          rb[q][e] = make_float4(t[0], t[1], t[2], t[3]);
+        }
+      }
+    }
+  };
+
+  auto store_tile = [&](int buf) {
+    float* as = As + buf * BM * LDK;
+    float* bs = Bs + buf * BN * LDK;
+#pragma unroll
+    for (int f = 0; f < G::A_F4; ++f) {
+      const int r = a_r + f * A_RSTEP;
+      *reinterpret_cast<float4*>(as + r * LDK + a_c) = ra[f];
+    }
+#pragma unroll
+    for (int q = 0; q < G::B_BLK; ++q) {
+      const int blk = tid + q * kThreads;
+      const int nq = blk % B_NQ, kq = blk / B_NQ;
+      // transpose the 4(k) x 4(n) block: column c of rb -> LDS row n
+      float* base = bs + (4 * nq) * LDK + 4 * kq;
+      *reinterpret_cast<float4*>(base + 0 * LDK) =
+          make_float4(rb[q][0].x, rb[q][1].x, rb[q][2].x, rb[q][3].x);
+      *reinterpret_cast<float4*>(base + 1 * LDK) =
+          make_float4(rb[q][0].y, rb[q][1].y, rb[q][2].y, rb[q][3].y);
+      *reinterpret_cast<float4*>(base + 2 * LDK) =
+          make_float4(rb[q][0].z, rb[q][1].z, rb[q][2].z, rb[q][3].z);
+      *reinterpret_cast<float4*>(base + 3 * LDK) =
+          make_float4(rb[q][0].w, rb[q][1].w, rb[q][2].w, rb[q][3].w);
+    }
+  };
+
+  f32x16 acc[G::TM][G::TN];
+#pragma unroll
+  for (int i = 0; i < G::TM; ++i)
+#pragma unroll
+    for (int j = 0; j < G::TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  const int nk = (K + BK - 1) / BK;
+  if (nk > 0) {
+    load_tile(0);
+    store_tile(0);
+  }
+  __syncthreads();
+
+  for (int t = 0; t < nk; ++t) {
+    const int cur = t & 1;
+    if (t + 1 < nk) load_tile((t + 1) * BK);
+    const float* as = As + cur * BM * LDK + (wm + li) * LDK + 4 * lh;
+    const float* bs = Bs + cur * BN * LDK + (wn + li) * LDK + 4 * lh;
+#pragma unroll
+    for (int c = 0; c < BK / 8; ++c) {
+      float4 a[G::TM], b[G::TN];
+#pragma unroll
+      for (int i = 0; i < G::TM; ++i) a[i] = *reinterpret_cast<const float4*>(as + i * 32 * LDK + 8 * c);
+#pragma unroll
+      for (int j = 0; j < G::TN; ++j) b[j] = *reinterpret_cast<const float4*>(bs + j * 32 * LDK + 8 * c);
+#pragma unroll
+      for (int i = 0; i < G::TM; ++i)
+#pragma unroll
+        for (int j = 0; j < G::TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i].x, b[j].x, acc[i][j], 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < G::TM; ++i)
+#pragma unroll
+        for (int j = 0; j < G::TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i].y, b[j].y, acc[i][j], 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < G::TM; ++i)
+#pragma unroll
+        for (int j = 0; j < G::TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i].z, b[j].z, acc[i][j], 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < G::TM; ++i)
+#pragma unroll
+        for (int j = 0; j < G::TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i].w, b[j].w, acc[i][j], 0, 0, 0);
+    }
+    if (t + 1 < nk) store_tile(cur ^ 1);
+    __syncthreads();
+  }
+
+  // ---- epilogue: value r of lane l is row 8*(r/4) + 4*lh + r%4, col li ----
+#pragma unroll
+  for (int i = 0; i < G::TM; ++i) {
+#pragma unroll
+    for (int j = 0; j < G::TN; ++j) {
+      const int col = n0 + wn + j * 32 + li;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = m0 + wm + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+        if (!CHECK || (row < M && col < N)) C[(long long)row * ldc + col] = acc[i][j][r];
+      }
+    }
+  }
+}
+
+template <int BM, int BN, int BK, bool CHECK>
+hipError_t launch_tiles(hipStream_t s, int batch, int m, int n, int k,
+                        const float* A, int lda, long long sA, const float* B,
+                        int ldb, long long sB, float* C, int ldc, long long sC) {
+  using G = Cfg<BM, BN, BK>;
+  const int tm = (m + BM - 1) / BM, tn = (n + BN - 1) / BN;
+  const size_t lds = sizeof(float) * G::LDS_FLOATS;
+  auto kern = sgemm_mfma_kernel<BM, BN, BK, CHECK>;
+  static bool attr_set = false;  // per instantiation
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  if (batch > 65535) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(kern, dim3(tm * tn, batch), dim3(kThreads), lds, s, m, n, k,
+                     A, lda, sA, B, ldb, sB, C, ldc, sC, tm, tn);
+  return hipGetLastError();
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+constexpr int kBM = 128, kBN = 128, kBK = 32;
+
+bool fast_ok(int m, int n, int k, const float* A, int lda, long long sA,
+             const float* B, int ldb, long long sB) {
+  return m % kBM == 0 && n % kBN == 0 && k % kBK == 0 && lda % 4 == 0 &&
+         ldb % 4 == 0 && sA % 4 == 0 && sB % 4 == 0 && aligned16(A) && aligned16(B);
+}
+
+}  // namespace
+
+namespace bch {
+
+const char* sgemm_kernel_name(int m, int n, int k) {
+  if (m <= 32 && sgemm_skinny_applies(m, n, k, nullptr, k, nullptr, n))
+    return "sgemm_skinny";
+  if (m % kBM == 0 && n % kBN == 0 && k % kBK == 0)
+    return "sgemm_mfma_kernel<128,128,32,false>";
+  return "sgemm_mfma_kernel<128,128,32,true>";
+}
+
+size_t sgemm_workspace_bytes(int batch, int m, int n, int k) {
+  if (batch == 1 && sgemm_skinny_applies(m, n, k, nullptr, k, nullptr, n))
+    return sgemm_skinny_workspace_bytes(m, n, k);
+  return 0;
+}
+
+hipError_t launch_sgemm(hipStream_t s, int batch, int m, int n, int k,
+                        const float* A, int lda, long long sA, const float* B,
+                        int ldb, long long sB, float* C, int ldc, long long sC,
+                        void* ws, size_t ws_bytes) {
+  if (batch <= 0 || m <= 0 || n <= 0) return hipSuccess;
+  if (batch == 1 && sgemm_skinny_applies(m, n, k, A, lda, B, ldb))
+    return launch_sgemm_skinny(s, m, n, k, A, lda, B, ldb, C, ldc, ws, ws_bytes);
+  if (fast_ok(m, n, k, A, lda, sA, B, ldb, sB))
+    return launch_tiles<kBM, kBN, kBK, false>(s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC);
+  return launch_tiles<kBM, kBN, kBK, true>(s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC);
+}
+
+}  // namespace bch

@@ -1,0 +1,485 @@
+"""Host side of the hot path: barraCuda's op API over libbarracuda_hip.so.
+
+Mirrors the reference's Rust surface for this path (same method names,
+argument meaning and error variants), with every computation routed through
+the C ABI to the gfx950 kernels.  There is no CPU fallback: if the library
+or the device is missing, the call raises.
+
+Reference (crates/barracuda/src/):
+  Tensor::{from_data, shape, to_vec}            tensor/mod.rs:185, 409, 448
+  Tensor::matmul / matmul_ref, MatMul            ops/matmul.rs:49-243
+  Tensor::matmul_tiled, MatmulTiled              ops/matmul_tiled.rs:45-171
+  Tensor::batch_matmul, BatchMatMul              ops/batch_matmul.rs:24-163
+  Tensor::softmax, Softmax (global)              ops/softmax.rs:31-144
+  Tensor::softmax_dim                            ops/tensor_axis_ops.rs:67-126
+  Tensor::attention, Attention                   ops/attention/mod.rs:84-206
+  Tensor::scaled_dot_product_attention           ops/scaled_dot_product_attention/mod.rs:81-226
+  Tensor::causal_attention, CausalAttention      ops/causal_attn/mod.rs:64-158
+  FlashAttention                                 ops/flash_attention.rs:45-146
+"""
+from __future__ import annotations
+
+import ctypes as C
+import math
+import threading
+from pathlib import Path
+from typing import Sequence
+
+import numpy as np
+
+from . import _native as N
+from .error import (BarracudaError, DeviceError, DeviceNotAvailable, InvalidInput,
+                    InvalidOperation, ShapeMismatch, UnsupportedOperation, from_status)
+
+__all__ = [
+    "HipDevice", "get_device", "Tensor", "MatMul", "MatmulTiled", "BatchMatMul",
+    "Softmax", "Attention", "ScaledDotProductAttention", "CausalAttention",
+    "FlashAttention", "LcgStream",
+]
+
+
+class HipDevice:
+    """One bch_ctx (device + stream).  Plays the role of the reference's
+    WgpuDevice behind GpuBackend (device/backend.rs:244-444).  Calls are
+    serialised with a lock: a context is not re-entrant."""
+
+    def __init__(self, device: int = -1, code_object_dir: str | None = None):
+        self._lib = N.load()
+        self._lock = threading.RLock()
+        ctx = C.c_void_p()
+        st = self._lib.bch_ctx_create(device, code_object_dir.encode() if code_object_dir else None,
+                                      C.byref(ctx))
+        if st != N.BCH_OK:
+            raise from_status(st, N.last_error(None), "device")
+        self._ctx = ctx
+        self.ordinal = device
+
+    # -- plumbing --------------------------------------------------------
+    @property
+    def ctx(self) -> C.c_void_p:
+        return self._ctx
+
+    def name(self) -> str:
+        return "hip:gfx950"
+
+    def check(self, status: int, op: str) -> None:
+        if status != N.BCH_OK:
+            raise from_status(status, N.last_error(self._ctx), op, self.name())
+
+    def alloc(self, nbytes: int) -> int:
+        p = C.c_void_p()
+        with self._lock:
+            self.check(self._lib.bch_alloc(self._ctx, nbytes, C.byref(p)), "alloc_buffer")
+        return p.value or 0
+
+    def free(self, ptr: int) -> None:
+        if ptr and self._ctx:
+            with self._lock:
+                self.check(self._lib.bch_free(self._ctx, C.c_void_p(ptr)), "free")
+
+    def upload(self, ptr: int, host: np.ndarray) -> None:
+        host = np.ascontiguousarray(host)
+        with self._lock:
+            self.check(self._lib.bch_upload(self._ctx, C.c_void_p(ptr), host.ctypes.data_as(C.c_void_p),
+                                            host.nbytes), "upload")
+
+    def download(self, ptr: int, nbytes: int) -> np.ndarray:
+        out = np.empty(nbytes // 4, dtype=np.float32)
+        with self._lock:
+            self.check(self._lib.bch_download(self._ctx, out.ctypes.data_as(C.c_void_p), C.c_void_p(ptr),
+                                              nbytes), "download")
+        return out
+
+    def sync(self) -> None:
+        with self._lock:
+            self.check(self._lib.bch_sync(self._ctx), "sync")
+
+    def dispatch_binary(self, binary: bytes | str | Path, entry: str, workgroups: Sequence[int],
+                        block: Sequence[int], args: Sequence[C._SimpleCData],
+                        shared_bytes: int = 0) -> None:
+        """GpuBackend::dispatch_binary (device/backend.rs:344-354): launch a
+        precompiled gfx950 code object.  `binary` is the image bytes or a
+        path; `args` are ctypes scalars / c_void_p in kernel-argument order."""
+        grid = (C.c_uint * 3)(*workgroups)
+        blk = (C.c_uint * 3)(*block)
+        argv = (C.c_void_p * max(1, len(args)))(*[C.cast(C.pointer(a), C.c_void_p) for a in args])
+        if isinstance(binary, (str, Path)):
+            img = C.c_char_p(str(binary).encode())
+            length = 0
+        else:
+            img = C.create_string_buffer(bytes(binary), len(binary))
+            length = len(binary)
+        with self._lock:
+            self.check(self._lib.bch_launch_code_object(self._ctx, C.cast(img, C.c_void_p), length,
+                                                        entry.encode(), grid, blk, argv, len(args),
+                                                        shared_bytes), "dispatch_binary")
+
+    def close(self) -> None:
+        if self._ctx:
+            with self._lock:
+                self._lib.bch_ctx_destroy(self._ctx)
+            self._ctx = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+_default: HipDevice | None = None
+_default_lock = threading.Lock()
+
+
+def get_device() -> HipDevice:
+    """The process-wide default device (BARRACUDA_HIP_DEVICE or 0)."""
+    global _default
+    with _default_lock:
+        if _default is None:
+            _default = HipDevice(-1)
+        return _default
+
+
+class _Buffer:
+    """Owned device allocation (RAII free), shared between Tensor clones."""
+
+    __slots__ = ("device", "ptr", "nbytes", "__weakref__")
+
+    def __init__(self, device: HipDevice, nbytes: int):
+        self.device = device
+        self.nbytes = nbytes
+        self.ptr = device.alloc(nbytes) if nbytes else 0
+
+    def __del__(self):
+        try:
+            if self.ptr:
+                self.device.free(self.ptr)
+        except Exception:
+            pass
+
+
+def _numel(shape: Sequence[int]) -> int:
+    n = 1
+    for s in shape:
+        n *= int(s)
+    return n
+
+
+class Tensor:
+    """f32 tensor resident in HBM (tensor/mod.rs:47-60, with a HIP buffer)."""
+
+    def __init__(self, buffer: _Buffer, shape: Sequence[int], device: HipDevice):
+        self._buf = buffer
+        self._shape = [int(s) for s in shape]
+        self._device = device
+
+    # -- construction / readback ------------------------------------------
+    @classmethod
+    def from_data(cls, data, shape: Sequence[int], device: HipDevice | None = None) -> "Tensor":
+        """tensor/mod.rs:185 from_data: upload f32 data with a shape."""
+        device = device or get_device()
+        arr = np.ascontiguousarray(np.asarray(data, dtype=np.float32).reshape(-1))
+        if arr.size != _numel(shape):
+            raise ShapeMismatch([_numel(shape)], [arr.size])
+        buf = _Buffer(device, arr.nbytes)
+        if arr.nbytes:
+            device.upload(buf.ptr, arr)
+        return cls(buf, shape, device)
+
+    from_vec_on = from_data
+
+    @classmethod
+    def empty(cls, shape: Sequence[int], device: HipDevice | None = None) -> "Tensor":
+        device = device or get_device()
+        return cls(_Buffer(device, 4 * _numel(shape)), shape, device)
+
+    def shape(self) -> list[int]:
+        return list(self._shape)
+
+    def len(self) -> int:
+        return _numel(self._shape)
+
+    def device(self) -> HipDevice:
+        return self._device
+
+    @property
+    def ptr(self) -> int:
+        return self._buf.ptr
+
+    def to_vec(self) -> np.ndarray:
+        """tensor/mod.rs:448 to_vec: blocking readback, flat f32."""
+        if self._buf.nbytes == 0:
+            return np.empty(0, dtype=np.float32)
+        return self._device.download(self._buf.ptr, self._buf.nbytes)
+
+    def to_numpy(self) -> np.ndarray:
+        return self.to_vec().reshape(self._shape)
+
+    def clone(self) -> "Tensor":
+        """Shares the buffer, as Tensor::clone bumps a refcount (tensor/mod.rs:267-278)."""
+        return Tensor(self._buf, self._shape, self._device)
+
+    # -- ops (same names as the reference) -----------------------------------
+    def matmul(self, other: "Tensor") -> "Tensor":
+        return MatMul(self, other).execute()
+
+    def matmul_ref(self, other: "Tensor") -> "Tensor":
+        return MatMul(self, other).execute()
+
+    def matmul_tiled(self, other: "Tensor") -> "Tensor":
+        return MatmulTiled(self, other).execute()
+
+    def batch_matmul(self, other: "Tensor") -> "Tensor":
+        return BatchMatMul(self, other).execute()
+
+    def softmax(self) -> "Tensor":
+        return Softmax(self).execute()
+
+    def softmax_dim(self, axis: int) -> "Tensor":
+        """ops/tensor_axis_ops.rs:67-126: softmax along `axis`."""
+        shape = self._shape
+        if not shape:
+            raise InvalidOperation("softmax_dim", "Empty tensor not supported")
+        if axis >= len(shape) or axis < 0:
+            raise InvalidOperation("softmax_dim", f"Axis {axis} out of bounds for shape {shape}")
+        out = Tensor.empty(shape, self._device)
+        outer = _numel(shape[:axis])
+        inner = _numel(shape[axis + 1:])
+        if outer * shape[axis] * inner == 0:
+            return out
+        dev = self._device
+        with dev._lock:
+            dev.check(dev._lib.bch_softmax_axis(dev.ctx, outer, shape[axis], inner,
+                                                C.c_void_p(self.ptr), C.c_void_p(out.ptr)),
+                      "softmax_dim")
+        return out
+
+    def attention(self, key: "Tensor", value: "Tensor") -> "Tensor":
+        return Attention(self, key, value).execute()
+
+    def scaled_dot_product_attention(self, key: "Tensor", value: "Tensor") -> "Tensor":
+        return ScaledDotProductAttention(self, key, value).execute()
+
+    def causal_attention(self, key: "Tensor", value: "Tensor") -> "Tensor":
+        return CausalAttention(self, key, value).execute()
+
+
+class LcgStream:
+    """Seeded input stream over the reference's generators, filled in HBM
+    (bch_fill_uniform / bch_fill_normal).  Successive tensors continue one
+    stream, as the reference fills arrays in argument order: uniform is
+    rng.rs:20-70, normal is ops/lattice/constants.rs:38-49 (Box-Muller)."""
+
+    def __init__(self, seed: int, device: HipDevice | None = None):
+        self.state = C.c_ulonglong(seed)
+        self.device = device or get_device()
+
+    def uniform(self, shape: Sequence[int], lo: float = -1.0, hi: float = 1.0) -> Tensor:
+        t = Tensor.empty(shape, self.device)
+        dev = self.device
+        with dev._lock:
+            dev.check(dev._lib.bch_fill_uniform(dev.ctx, C.c_void_p(t.ptr), t.len(), C.byref(self.state),
+                                                lo, hi), "fill_uniform")
+        return t
+
+    def normal(self, shape: Sequence[int], mu: float = 0.0, sigma: float = 1.0) -> Tensor:
+        t = Tensor.empty(shape, self.device)
+        dev = self.device
+        with dev._lock:
+            dev.check(dev._lib.bch_fill_normal(dev.ctx, C.c_void_p(t.ptr), t.len(), C.byref(self.state),
+                                               mu, sigma), "fill_normal")
+        return t
+
+
+def _same_device(*ts: Tensor) -> HipDevice:
+    dev = ts[0].device()
+    for t in ts[1:]:
+        if t.device() is not dev:
+            raise DeviceError("tensors live on different devices")
+    return dev
+
+
+def _sgemm(dev: HipDevice, m: int, n: int, k: int, a: Tensor, b: Tensor, op: str) -> Tensor:
+    out = Tensor.empty([m, n], dev)
+    if m * n == 0:
+        return out
+    with dev._lock:
+        dev.check(dev._lib.bch_sgemm(dev.ctx, m, n, k, C.c_void_p(a.ptr), max(k, 1), C.c_void_p(b.ptr),
+                                     max(n, 1), C.c_void_p(out.ptr), max(n, 1)), op)
+    return out
+
+
+class MatMul:
+    """ops/matmul.rs:49-214: C[m,n] = A[m,k] B[k,n]."""
+
+    def __init__(self, lhs: Tensor, rhs: Tensor):
+        self.lhs, self.rhs = lhs, rhs
+
+    def execute(self) -> Tensor:
+        ls, rs = self.lhs.shape(), self.rhs.shape()
+        if len(ls) < 2 or len(rs) < 2:
+            raise InvalidOperation("matmul", f"requires 2D+ tensors, got shapes {ls} and {rs}")
+        # >= 3-D inputs use shape[0], shape[1] (matmul.rs:103-107)
+        m, k = ls[0], ls[1]
+        k_rhs, n = rs[0], rs[1]
+        if k != k_rhs:
+            raise ShapeMismatch(ls, rs)
+        dev = _same_device(self.lhs, self.rhs)
+        return _sgemm(dev, m, n, k, self.lhs, self.rhs, "matmul")
+
+
+class MatmulTiled(MatMul):
+    """ops/matmul_tiled.rs:45-122: same contract as MatMul."""
+
+
+class BatchMatMul:
+    """ops/batch_matmul.rs:24-144: A[batch,m,k] . B[batch,k,n] -> [batch,m,n].
+
+    The reference reads batch/m/k from A and n from B without checking that
+    B agrees; here a disagreeing B is a ShapeMismatch instead of reading out
+    of bounds."""
+
+    def __init__(self, a: Tensor, b: Tensor):
+        self.a, self.b = a, b
+
+    def execute(self) -> Tensor:
+        as_, bs = self.a.shape(), self.b.shape()
+        if len(as_) != 3 or len(bs) != 3:
+            raise InvalidOperation("batch_matmul", f"requires 3D tensors, got shapes {as_} and {bs}")
+        batch, m, k = as_
+        if bs[0] != batch or bs[1] != k:
+            raise ShapeMismatch(as_, bs)
+        n = bs[2]
+        dev = _same_device(self.a, self.b)
+        out = Tensor.empty([batch, m, n], dev)
+        if batch * m * n == 0:
+            return out
+        with dev._lock:
+            dev.check(dev._lib.bch_sgemm_strided_batched(
+                dev.ctx, batch, m, n, k, C.c_void_p(self.a.ptr), m * k, C.c_void_p(self.b.ptr), k * n,
+                C.c_void_p(out.ptr), m * n), "batch_matmul")
+        return out
+
+
+class Softmax:
+    """ops/softmax.rs:31-133: softmax over ALL elements of the tensor."""
+
+    def __init__(self, t: Tensor):
+        if not t.shape():
+            raise InvalidOperation("Softmax", "Empty tensor not supported")
+        self.t = t
+
+    def execute(self) -> Tensor:
+        dev = self.t.device()
+        out = Tensor.empty(self.t.shape(), dev)
+        size = self.t.len()
+        if size == 0:
+            return out
+        with dev._lock:
+            dev.check(dev._lib.bch_softmax_rows(dev.ctx, 1, size, C.c_void_p(self.t.ptr),
+                                                C.c_void_p(out.ptr)), "softmax")
+        return out
+
+
+def _sdpa(dev: HipDevice, q: Tensor, k: Tensor, v: Tensor, causal: bool, op: str,
+          b: int, h: int, sq: int, skv: int, d: int) -> Tensor:
+    if d > 128:
+        raise UnsupportedOperation(op, f"{dev.name()} (head_dim {d} > 128)")
+    out = Tensor.empty(q.shape(), dev)
+    if b * h * sq * d == 0:
+        return out
+    if skv == 0:
+        raise InvalidOperation(op, "key sequence is empty (shape/dimension mismatch)")
+    scale = np.float32(1.0) / np.sqrt(np.float32(d))
+    with dev._lock:
+        dev.check(dev._lib.bch_sdpa_fwd(dev.ctx, b, h, sq, skv, d, float(scale), int(causal),
+                                        C.c_void_p(q.ptr), C.c_void_p(k.ptr), C.c_void_p(v.ptr),
+                                        C.c_void_p(out.ptr)), op)
+    return out
+
+
+class Attention:
+    """ops/attention/mod.rs:96-144 (validation) + compute.rs:21-111: softmax(QK^T/sqrt(D)) V,
+    Q [B,H,Sq,D], K/V [B,H,Skv,D] (cross-attention allowed)."""
+
+    def __init__(self, query: Tensor, key: Tensor, value: Tensor):
+        for name, t in (("query", query), ("key", key), ("value", value)):
+            if len(t.shape()) != 4:
+                raise InvalidOperation(
+                    "attention",
+                    f"{name} requires 4D tensor [batch, heads, seq_len, head_dim], got {len(t.shape())}D")
+        qs, ks, vs = query.shape(), key.shape(), value.shape()
+        if qs[0] != ks[0] or qs[1] != ks[1] or qs[3] != ks[3]:
+            raise ShapeMismatch(qs, ks)
+        if ks != vs:
+            raise ShapeMismatch(ks, vs)
+        self.q, self.k, self.v = query, key, value
+
+    def execute(self) -> Tensor:
+        b, h, sq, d = self.q.shape()
+        skv = self.k.shape()[2]
+        dev = _same_device(self.q, self.k, self.v)
+        return _sdpa(dev, self.q, self.k, self.v, False, "attention", b, h, sq, skv, d)
+
+
+class ScaledDotProductAttention:
+    """ops/scaled_dot_product_attention/mod.rs:101-149: self-attention, Q, K, V same shape."""
+
+    def __init__(self, query: Tensor, key: Tensor, value: Tensor):
+        qs, ks, vs = query.shape(), key.shape(), value.shape()
+        if len(qs) != 4 or len(ks) != 4 or len(vs) != 4:
+            raise InvalidInput("Q, K, V must be 4D tensors [batch, heads, seq_len, head_dim]")
+        if ks != qs or vs != qs:
+            raise ShapeMismatch(qs, vs if ks == qs else ks)
+        _same_device(query, key, value)
+        self.q, self.k, self.v = query, key, value
+
+    def execute(self) -> Tensor:
+        b, h, s, d = self.q.shape()
+        return _sdpa(self.q.device(), self.q, self.k, self.v, False, "scaled_dot_product_attention",
+                     b, h, s, s, d)
+
+
+class CausalAttention:
+    """ops/causal_attn/mod.rs:64-158: causal SDPA (key j <= query i), Q, K, V same shape.
+
+    The reference's GPU dispatch computes only rows i < 16 of head 0
+    (1-D grids for 2-D shaders, causal_attn/compute.rs:69-108); this
+    follows its CPU definition (ops/causal_attention.rs:52-134) for every
+    row and head."""
+
+    def __init__(self, query: Tensor, key: Tensor, value: Tensor):
+        qs, ks, vs = query.shape(), key.shape(), value.shape()
+        if len(qs) != 4 or len(ks) != 4 or len(vs) != 4:
+            raise ShapeMismatch(qs, ks)
+        if qs != ks or qs != vs:
+            raise ShapeMismatch(qs, ks)
+        self.q, self.k, self.v = query, key, value
+
+    def execute(self) -> Tensor:
+        b, h, s, d = self.q.shape()
+        dev = _same_device(self.q, self.k, self.v)
+        return _sdpa(dev, self.q, self.k, self.v, True, "causal_attention", b, h, s, s, d)
+
+
+class FlashAttention:
+    """ops/flash_attention.rs:45-146: 2-D [seq_len, head_dim] single-head attention,
+    scale 1/sqrt(head_dim).  The reference shader keeps at most 256 keys
+    (flash_attention_f64.wgsl:70-71); here every key is attended to, so the
+    two agree for seq_len <= 256."""
+
+    def __init__(self, query: Tensor, key: Tensor, value: Tensor, num_heads: int = 1):
+        if query.shape() != key.shape() or query.shape() != value.shape():
+            raise InvalidOperation(
+                "FlashAttention",
+                f"Q, K, V must have same shape, got Q: {query.shape()}, K: {key.shape()}, V: {value.shape()}")
+        if len(query.shape()) != 2:
+            raise InvalidOperation("FlashAttention",
+                                   f"Requires 2D tensors [seq_len, head_dim], got shape: {query.shape()}")
+        self.q, self.k, self.v = query, key, value
+        self.num_heads = num_heads
+
+    def execute(self) -> Tensor:
+        s, d = self.q.shape()
+        dev = _same_device(self.q, self.k, self.v)
+        return _sdpa(dev, self.q, self.k, self.v, False, "FlashAttention", 1, 1, s, s, d)

@@ -1,0 +1,266 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X hot path (one JSON line on stdout).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra]
+
+Headline (`value`): f32 GEMM M=N=K=4096 in TFLOP/s:
+one step = one bch_sgemm launch over inputs already resident in HBM (seeded
+U[-1,1) from the reference's LCG, seed 2, generated on the device).  The
+other configurations (row softmax, skinny GEMM, batched GEMM, fused
+attention) are measured in the same run and reported under "extra".
+
+Timing: HIP events recorded on the library's own stream (bch_event_*) give
+the average kernel duration used for `roofline`; the wall clock around
+exactly K launches, bracketed by bch_sync on both sides, gives ms_per_step.
+`cpu_baseline` is the reference's CPU matmul (execute_matmul_cpu, restated
+in oracle/) timed on this host on a bounded row sample.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, published
+FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense FP32 matrix, published
+PROFILES = ROOT / "profiles"
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+class Timer:
+    """HIP events on the context's stream + wall clock around K launches."""
+
+    def __init__(self, dev):
+        self.dev = dev
+        lib = dev._lib
+        self.e0, self.e1 = C.c_void_p(), C.c_void_p()
+        dev.check(lib.bch_event_create(dev.ctx, C.byref(self.e0)), "event")
+        dev.check(lib.bch_event_create(dev.ctx, C.byref(self.e1)), "event")
+
+    def run(self, fn, steps: int, warmup: int):
+        lib, dev = self.dev._lib, self.dev
+        for _ in range(warmup):
+            fn(0)
+        dev.sync()
+        t0 = time.perf_counter()
+        dev.check(lib.bch_event_record(dev.ctx, self.e0), "event")
+        for i in range(steps):
+            fn(i)
+        dev.check(lib.bch_event_record(dev.ctx, self.e1), "event")
+        dev.sync()
+        t1 = time.perf_counter()
+        ms = C.c_float()
+        dev.check(lib.bch_event_elapsed_ms(self.e0, self.e1, C.byref(ms)), "event")
+        return (t1 - t0) * 1e3 / steps, ms.value / steps  # wall ms/step, event ms/launch
+
+
+def load_traffic(key: str):
+    """HBM bytes per launch from the committed rocprofv3 --pmc summaries
+    (FETCH_SIZE + WRITE_SIZE, scaled by the copy-kernel calibration)."""
+    f = PROFILES / "traffic.json"
+    if not f.exists():
+        return None
+    try:
+        d = json.loads(f.read_text())
+        return d.get(key, {}).get("bytes_per_launch")
+    except Exception:
+        return None
+
+
+def bench_gemm(dev, steps, warmup):
+    from barracuda_amd import LcgStream
+    lib = dev._lib
+    n = 4096
+    s = LcgStream(2, dev)
+    a, b = s.uniform([n, n]), s.uniform([n, n])
+    from barracuda_amd import Tensor
+    c = Tensor.empty([n, n], dev)
+    ctx, pa, pb, pc = dev.ctx, C.c_void_p(a.ptr), C.c_void_p(b.ptr), C.c_void_p(c.ptr)
+
+    def step(_i):
+        st = lib.bch_sgemm(ctx, n, n, n, pa, n, pb, n, pc, n)
+        if st:
+            dev.check(st, "sgemm")
+
+    wall_ms, ev_ms = Timer(dev).run(step, steps, warmup)
+    flops = 2.0 * n ** 3
+    return {"wall_ms": wall_ms, "kernel_ms": ev_ms, "flops": flops,
+            "kernel": lib.bch_sgemm_kernel_name(n, n, n).decode()}, (a, b, c)
+
+
+def bench_extra(dev, reps: int = 20):
+    """The other BASELINE configs, each timed over `reps` launches."""
+    from barracuda_amd import LcgStream, Tensor
+    lib, ctx = dev._lib, dev.ctx
+    T = Timer(dev)
+    out = {}
+
+    # config 2: row softmax [65536 x 2048], N(0,3), seed 1
+    x = LcgStream(1, dev).normal([65536, 2048], 0.0, 3.0)
+    y = Tensor.empty([65536, 2048], dev)
+    px, py = C.c_void_p(x.ptr), C.c_void_p(y.ptr)
+    wall, ev = T.run(lambda i: lib.bch_softmax_rows(ctx, 65536, 2048, px, py), reps, 3)
+    nbytes = 2 * 4 * 65536 * 2048
+    out["softmax_65536x2048"] = {"GB/s": nbytes / (ev * 1e-3) / 1e9, "kernel_us": ev * 1e3,
+                                 "bytes_per_launch": nbytes,
+                                 "hbm_frac": nbytes / (ev * 1e-3) / 1e9 / HBM_PEAK_GBS}
+    del x, y
+
+    # config 4: skinny GEMM M in {1, 8, 32}, K 4096, N 11008; X ~ N(0,1), W ~ N(0,0.02), seed 3.
+    # Three weight copies (541 MB > the 256 MB Infinity Cache) are rotated.
+    K, N = 4096, 11008
+    for m in (1, 8, 32):
+        s = LcgStream(3, dev)
+        xs = s.normal([m, K])
+        ws = [s.normal([K, N], 0.0, 0.02) for _ in range(3)]
+        ys = Tensor.empty([m, N], dev)
+        pxs, pys = C.c_void_p(xs.ptr), C.c_void_p(ys.ptr)
+        pws = [C.c_void_p(w.ptr) for w in ws]
+        wall, ev = T.run(lambda i: lib.bch_sgemm(ctx, m, N, K, pxs, K, pws[i % 3], N, pys, N), reps, 3)
+        nbytes = 4 * (K * N + m * K + m * N)
+        out[f"skinny_m{m}"] = {"GB/s": nbytes / (ev * 1e-3) / 1e9, "us": ev * 1e3,
+                               "bytes_per_call": nbytes,
+                               "hbm_frac": nbytes / (ev * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                               "TFLOP/s": 2.0 * m * K * N / (ev * 1e-3) / 1e12}
+        del xs, ws, ys
+
+    # config 3b: batched 16 x 1024^3, U[-1,1), seed 2
+    s = LcgStream(2, dev)
+    a, b = s.uniform([16, 1024, 1024]), s.uniform([16, 1024, 1024])
+    c = Tensor.empty([16, 1024, 1024], dev)
+    pa, pb, pc = C.c_void_p(a.ptr), C.c_void_p(b.ptr), C.c_void_p(c.ptr)
+    mm = 1024 * 1024
+    wall, ev = T.run(lambda i: lib.bch_sgemm_strided_batched(ctx, 16, 1024, 1024, 1024, pa, mm, pb, mm,
+                                                              pc, mm), reps, 3)
+    fl = 2.0 * 16 * 1024 ** 3
+    out["batched_16x1024"] = {"TFLOP/s": fl / (ev * 1e-3) / 1e12, "ms": ev,
+                              "mfma_frac": fl / (ev * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS}
+    del a, b, c
+
+    # config 5: SDPA forward B=4, H=32, S=2048, D=128, N(0,1), seed 4, scale 1/sqrt(128)
+    Bb, H, S, D = 4, 32, 2048, 128
+    s = LcgStream(4, dev)
+    q, k, v = (s.normal([Bb, H, S, D]) for _ in range(3))
+    o = Tensor.empty([Bb, H, S, D], dev)
+    pq, pk, pv, po = (C.c_void_p(t.ptr) for t in (q, k, v, o))
+    scale = 1.0 / math.sqrt(D)
+    for causal in (0, 1):
+        wall, ev = T.run(lambda i: lib.bch_sdpa_fwd(ctx, Bb, H, S, S, D, scale, causal, pq, pk, pv, po),
+                         max(5, reps // 2), 2)
+        fl = 4.0 * Bb * H * S * S * D if not causal else 4.0 * Bb * H * (S * (S + 1) / 2) * D
+        key = "sdpa_causal" if causal else "sdpa_noncausal"
+        out[key] = {"ms": ev, "TFLOP/s": fl / (ev * 1e-3) / 1e12,
+                    "mfma_frac": fl / (ev * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS}
+    del q, k, v, o
+    return out
+
+
+def cpu_baselines(target_s: float = 12.0, extra: bool = True):
+    """The reference's CPU paths, restated in oracle/, on this host's cores."""
+    from oracle import bc_oracle as O
+    threads = O.num_threads()
+    n = 4096
+    rng = O.Lcg(2)
+    a, b = rng.uniform((n, n)), rng.uniform((n, n))
+    t0 = time.perf_counter()
+    O.matmul_cpu_exec_f32(a, b, 0, 16)
+    dt = time.perf_counter() - t0
+    rows = int(max(16, min(n, 16 * target_s / max(dt, 1e-3))))
+    rows = min(n, (rows // threads + 1) * threads)
+    t0 = time.perf_counter()
+    O.matmul_cpu_exec_f32(a, b, 0, rows)
+    dt = time.perf_counter() - t0
+    gemm = {"value": 2.0 * rows * n * n / dt / 1e12, "unit": "TFLOP/s", "cores": threads,
+            "kind": "port",
+            "sample": f"rows 0..{rows} of the 4096^3 GEMM (execute_matmul_cpu restated: "
+                      f"i-j-p f32 fma, OpenMP over rows as rayon), {dt:.1f} s; rate extrapolates linearly"}
+    ex = {}
+    if extra:
+        x = O.Lcg(1).normal((65536, 2048), 0.0, 3.0)
+        t0 = time.perf_counter()
+        O.softmax_dim_f32(x, 1, 0, 2048)
+        dt = time.perf_counter() - t0
+        ex["softmax_dim"] = {"GB/s": 2 * 4 * 2048 * 2048 / dt / 1e9, "cores": 1, "kind": "port",
+                             "sample": "rows 0..2048 of 65536x2048 (tensor_axis_ops.rs softmax_dim, serial)"}
+        s4 = O.Lcg(4)
+        shape = (1, 1, 2048, 128)
+        q, k, v = s4.normal(shape), s4.normal(shape), s4.normal(shape)
+        t0 = time.perf_counter()
+        O.causal_attention_cpu_f32(q, k, v)
+        dt = time.perf_counter() - t0
+        ex["causal_attention"] = {"ms_full_config_extrapolated": dt * 1e3 * 128, "cores": 1, "kind": "port",
+                                  "sample": "1 of 128 heads (causal_attention.rs, serial), x128 extrapolated"}
+    return gemm, ex
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-extra", action="store_true", help="only the headline GEMM")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one MI355X: the hot path here is single-GPU (no collectives); "
+              "run with --gpus 1", file=sys.stderr)
+        return 2
+
+    from barracuda_amd import get_device
+    dev = get_device()
+    log(f"gemm 4096^3: {args.warmup} warmup + {args.steps} timed launches")
+    g, keep = bench_gemm(dev, args.steps, args.warmup)
+    value = g["flops"] / (g["wall_ms"] * 1e-3) / 1e12
+    achieved = g["flops"] / (g["kernel_ms"] * 1e-3) / 1e12
+    log(f"  wall {g['wall_ms']:.3f} ms/step, kernel {g['kernel_ms']:.3f} ms -> {achieved:.1f} TFLOP/s")
+    del keep
+    extra = None
+    if not args.no_extra:
+        log("extra configs: softmax, skinny, batched, sdpa")
+        extra = bench_extra(dev)
+        for k_, v_ in extra.items():
+            log(f"  {k_}: {json.dumps({kk: round(vv, 4) if isinstance(vv, float) else vv for kk, vv in v_.items()})}")
+    cpu = None
+    if not args.no_cpu:
+        log("cpu baseline (oracle restatement of the reference CPU path)")
+        cpu, cpu_extra = cpu_baselines(extra=not args.no_extra)
+        if extra is not None:
+            extra["cpu"] = cpu_extra
+    rec = {
+        "metric": "f32 GEMM TFLOP/s @4096^3 (% FP32 MFMA peak); softmax GB/s; attention fwd ms",
+        "value": value,
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": g["wall_ms"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: U[-1,1) from the reference's rng.rs LCG, seed 2, generated in HBM",
+        "config": {"workload": "f32 GEMM C=A.B, M=N=K=4096, row-major (BASELINE configs[2])",
+                   "m": 4096, "n": 4096, "k": 4096, "kernel": g["kernel"]},
+        "roofline": {"bound": "mfma", "achieved": achieved, "peak": FP32_MFMA_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": achieved / FP32_MFMA_PEAK_TFLOPS,
+                     "traffic": load_traffic("sgemm_4096")},
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(rec), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

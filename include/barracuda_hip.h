@@ -1,0 +1,177 @@
+/*
+ * barracuda_hip.h -- C ABI of libbarracuda_hip.so, the MI355X (gfx950)
+ * implementation of barraCuda's dense ML-ops hot path: f32 matmul and
+ * batched matmul, row softmax, scaled-dot-product attention forward.
+ *
+ * Plain C: pointers, sizes, status codes.  No C++ or torch types cross this
+ * boundary.  Every call returns a bch_status (BCH_OK == 0) and never aborts;
+ * the message of the last failure is kept per context (bch_last_error) and
+ * per thread for calls that fail before a context exists.
+ *
+ * Conventions
+ *   - Matrices are row-major f32.  Device pointers come from bch_alloc (or
+ *     any hipMalloc'd memory of the same device).
+ *   - A context owns one HIP stream.  Compute calls enqueue on it and return
+ *     without waiting; bch_download and bch_sync wait.  A context is not
+ *     re-entrant: callers serialise use of one context (the Rust side holds
+ *     it behind a Mutex), or use one context per thread.
+ *   - Shapes are validated before anything touches the device, so a shape
+ *     error is reported identically with or without a GPU.
+ *
+ * Each entry point names the reference interface it replaces
+ * (ecoPrimals/barraCuda, paths relative to crates/barracuda/src/).
+ */
+#ifndef BARRACUDA_HIP_H
+#define BARRACUDA_HIP_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes.  Map 1:1 onto BarracudaError (error.rs:14-130). */
+typedef int bch_status;
+#define BCH_OK            0
+#define BCH_E_INVALID     1 /* null pointer / bad argument -> InvalidInput     (error.rs:187) */
+#define BCH_E_SHAPE       2 /* inconsistent dimensions     -> ShapeMismatch/InvalidOperation (error.rs:238,243) */
+#define BCH_E_NO_DEVICE   3 /* no HIP device               -> DeviceNotAvailable */
+#define BCH_E_OOM         4 /* device allocation failed    -> OutOfMemory */
+#define BCH_E_MODULE      5 /* code object missing/corrupt -> Device(String)   (error.rs:220) */
+#define BCH_E_LAUNCH      6 /* kernel launch failed        -> ExecutionError   (error.rs:230) */
+#define BCH_E_DEVICE      7 /* other HIP runtime failure   -> Device(String) / DeviceLost (error.rs:301) */
+#define BCH_E_UNSUPPORTED 8 /* op/entry not provided       -> UnsupportedOperation */
+
+typedef struct bch_ctx bch_ctx;
+typedef struct bch_event bch_event;
+
+/* ---- context and memory: replaces the WgpuDevice side of GpuBackend
+ *      (device/backend.rs:244-444; wgpu_backend.rs:122-155 download) ---- */
+
+/* Number of visible HIP devices; BCH_E_NO_DEVICE (and *count = 0) if none. */
+bch_status bch_device_count(int *count);
+
+/* Create a context on `device` (its own stream).  code_object_dir (nullable)
+ * is the directory bch_launch_code_object resolves relative names against;
+ * NULL means the directory of libbarracuda_hip.so.  Env
+ * BARRACUDA_HIP_DEVICE overrides device when device < 0. */
+bch_status bch_ctx_create(int device, const char *code_object_dir, bch_ctx **out);
+void bch_ctx_destroy(bch_ctx *ctx);
+
+/* Message of the last failed call on ctx; with ctx == NULL, the calling
+ * thread's last failure.  Never NULL ("" when none). */
+const char *bch_last_error(const bch_ctx *ctx);
+const char *bch_status_string(bch_status s);
+
+/* backend.rs alloc_buffer / alloc_buffer_init / upload / download.
+ * bch_alloc of 0 bytes returns a NULL pointer and BCH_OK.  Env
+ * BARRACUDA_HIP_FAIL_ALLOC=1 makes every bch_alloc fail with BCH_E_OOM
+ * (fault injection for OutOfMemory handling). */
+bch_status bch_alloc(bch_ctx *ctx, size_t bytes, void **dptr);
+bch_status bch_free(bch_ctx *ctx, void *dptr);
+bch_status bch_upload(bch_ctx *ctx, void *dst, const void *src, size_t bytes);
+bch_status bch_download(bch_ctx *ctx, void *dst, const void *src, size_t bytes);
+bch_status bch_memset(bch_ctx *ctx, void *dst, int value, size_t bytes);
+/* Wait for all work queued on ctx's stream (submit_and_poll, wgpu_device/
+ * submission.rs:143). */
+bch_status bch_sync(bch_ctx *ctx);
+
+/* ---- hot-path compute ---- */
+
+/* C[m,n] = A[m,k] . B[k,n], row-major, leading dimensions in elements
+ * (lda >= k, ldb >= n, ldc >= n).  m, n, k >= 0; k == 0 writes zeros.
+ * Replaces MatMul::execute (ops/matmul.rs:89-214: kernels K1
+ * matmul_gpu_evolved_f64.wgsl, K2 matmul_cpu_tiled_f64.wgsl, K3
+ * matmul_tiled_f64.wgsl) and MatmulTiled::execute (ops/matmul_tiled.rs:
+ * 62-122).  Routes m <= 32 (decode shapes) to the skinny HBM-streaming
+ * kernel and everything else to the FP32-MFMA tiled kernel. */
+bch_status bch_sgemm(bch_ctx *ctx, int m, int n, int k,
+                     const float *A, int lda, const float *B, int ldb,
+                     float *C, int ldc);
+
+/* C[b] = A[b] . B[b] for b < batch; A[b] starts at A + b*strideA (elements),
+ * leading dimensions k, n, n.  Replaces BatchMatMul::execute
+ * (ops/batch_matmul.rs:47-144, kernel K5 batch_matmul_f64.wgsl). */
+bch_status bch_sgemm_strided_batched(bch_ctx *ctx, int batch, int m, int n,
+                                     int k, const float *A, long long strideA,
+                                     const float *B, long long strideB,
+                                     float *C, long long strideC);
+
+/* Row-wise numerically stable softmax: out[r,:] = exp(x - max_r) / sum.
+ * rows, cols >= 1; in == out is allowed.  Replaces Tensor::softmax_dim
+ * (ops/tensor_axis_ops.rs:67-126) for the last axis, the attention row
+ * softmax K7 (shaders/activation/attention_softmax_f64.wgsl:24-58), and,
+ * with rows == 1, the global Softmax::execute (ops/softmax.rs:58-133, K11
+ * softmax_simple_f64.wgsl). */
+bch_status bch_softmax_rows(bch_ctx *ctx, long long rows, long long cols,
+                            const float *in, float *out);
+
+/* Softmax along a middle axis of a tensor viewed as [outer, axis, inner]
+ * (element (o,j,i) at (o*axis + j)*inner + i).  inner == 1 is the row case.
+ * Replaces Tensor::softmax_dim (ops/tensor_axis_ops.rs:67-126) for
+ * axis != last. */
+bch_status bch_softmax_axis(bch_ctx *ctx, long long outer, long long axis,
+                            long long inner, const float *in, float *out);
+
+/* Fused scaled-dot-product attention forward, [B,H,S,D] row-major:
+ *   o[b,h,i,:] = sum_j softmax_j(scale * q_i . k_j) v_j
+ * with j <= i when causal (causal requires Sq == Skv, as the reference's
+ * causal ops take one seq_len).  Non-causal Sq may differ from Skv
+ * (cross-attention).  1 <= D <= 128.  Never materialises the
+ * Sq x Skv score matrix.  Replaces Attention::execute (ops/attention/
+ * compute.rs:21-111: K6 attention_matmul_f64.wgsl -> K7 -> K9
+ * attention_apply_f64.wgsl), ScaledDotProductAttention (ops/
+ * scaled_dot_product_attention/compute.rs:19-108), CausalAttention (ops/
+ * causal_attn/compute.rs:24-115, K8 causal_attention_softmax_f64.wgsl),
+ * the CPU causal_attention (ops/causal_attention.rs:52-134) and
+ * FlashAttention::execute (ops/flash_attention.rs:96-145, K13). */
+bch_status bch_sdpa_fwd(bch_ctx *ctx, int B, int H, int Sq, int Skv, int D,
+                        float scale, int causal, const float *q,
+                        const float *k, const float *v, float *o);
+
+/* ---- seeded synthetic inputs, generated in HBM ---- */
+
+/* Fill dst[0..n) from the reference's seeded generators: uniform [lo, hi)
+ * from the Knuth LCG of rng.rs:20-70 (increment 1, u = (state >> 11) 2^-53,
+ * x = lo + (hi - lo) u), normal from ops/lattice/constants.rs:11-49 (MMIX
+ * increment, Box-Muller with u1 guarded by 1e-30, x = mu + sigma g, two
+ * draws per element).  Element i equals a sequential host fill.  *state is
+ * the generator state before the fill and is advanced past it (n steps, 2n
+ * for normal), so successive fills continue one stream, as the reference
+ * fills tensors in argument order.  Device counterpart of the seeded
+ * constructors Tensor::rand_with_rng / randn_with_rng (tensor/ops.rs:79-125). */
+bch_status bch_fill_uniform(bch_ctx *ctx, float *dst, size_t n,
+                            unsigned long long *state, double lo, double hi);
+bch_status bch_fill_normal(bch_ctx *ctx, float *dst, size_t n,
+                           unsigned long long *state, double mu, double sigma);
+
+/* ---- precompiled code objects: GpuBackend::dispatch_binary
+ *      (device/backend.rs:344-354) ---- */
+
+/* Load (and cache per context) a gfx950 code object and launch `entry` on
+ * grid[3] workgroups of block[3] threads.  args/nargs: kernelParams as in
+ * hipModuleLaunchKernel (args[i] points at the i-th argument's value).
+ * code_object is either an in-memory image (len > 0) or, with len == 0, a
+ * NUL-terminated path (relative paths resolve against code_object_dir). */
+bch_status bch_launch_code_object(bch_ctx *ctx, const void *code_object,
+                                  size_t len, const char *entry,
+                                  const unsigned grid[3],
+                                  const unsigned block[3], void **args,
+                                  size_t nargs, size_t shared_bytes);
+
+/* ---- timing on the context's stream (the hot path's own launches) ---- */
+bch_status bch_event_create(bch_ctx *ctx, bch_event **ev);
+bch_status bch_event_record(bch_ctx *ctx, bch_event *ev);
+/* Elapsed milliseconds between two recorded events (waits for `stop`). */
+bch_status bch_event_elapsed_ms(bch_event *start, bch_event *stop, float *ms);
+void bch_event_destroy(bch_event *ev);
+
+/* Name of the kernel a bch_sgemm / bch_softmax_rows / bch_sdpa_fwd call of
+ * this shape launches (for profilers and tests; NULL ctx allowed). */
+const char *bch_sgemm_kernel_name(int m, int n, int k);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* BARRACUDA_HIP_H */

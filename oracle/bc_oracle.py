@@ -1,0 +1,196 @@
+"""ctypes wrapper of oracle/libbc_oracle.so.
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py, as the checker or the timed CPU baseline.  The
+product (barracuda_amd/) never imports it.  See bc_oracle.c for what each
+function restates (reference file:line) and how it is pinned.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import math
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "libbc_oracle.so"
+
+_lib = None
+_fp = C.POINTER(C.c_float)
+_dp = C.POINTER(C.c_double)
+_ip = C.POINTER(C.c_int)
+_u64p = C.POINTER(C.c_uint64)
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(f"{LIB_PATH} missing: run `make -C oracle`")
+        L = C.CDLL(str(LIB_PATH))
+        L.bco_lcg_advance.restype = C.c_uint64
+        L.bco_lcg_advance.argtypes = [C.c_uint64, C.c_uint64, C.c_uint64]
+        L.bco_fill_uniform.argtypes = [_u64p, C.c_double, C.c_double, _fp, C.c_size_t]
+        L.bco_fill_normal.argtypes = [_u64p, C.c_double, C.c_double, _fp, C.c_size_t]
+        L.bco_matmul_f64.argtypes = [C.c_int, C.c_int, C.c_int, _fp, C.c_long, _fp, C.c_long, _dp,
+                                     C.c_long, _ip, C.c_int]
+        L.bco_softmax_rows_f64.argtypes = [C.c_long, C.c_long, _fp, _dp]
+        L.bco_sdpa_f64.argtypes = [C.c_int] * 5 + [C.c_double, C.c_int, _fp, _fp, _fp, _dp, _ip, C.c_int]
+        L.bco_matmul_cpu_exec_f32.argtypes = [C.c_int, C.c_int, C.c_int, _fp, _fp, _fp, C.c_int, C.c_int]
+        L.bco_matmul_k1_f32.argtypes = [C.c_int, C.c_int, C.c_int, _fp, _fp, _fp]
+        L.bco_batch_matmul_seq_f32.argtypes = [C.c_int, C.c_int, C.c_int, C.c_int, _fp, _fp, _fp]
+        L.bco_softmax_dim_f32.argtypes = [C.c_long, C.c_long, C.c_long, _fp, _fp, C.c_long, C.c_long]
+        L.bco_softmax_global_f32.argtypes = [C.c_long, _fp, _fp]
+        L.bco_attention_3pass_f32.argtypes = [C.c_int] * 6 + [_fp, _fp, _fp, _fp, _ip, C.c_int]
+        L.bco_causal_attention_cpu_f32.argtypes = [C.c_int] * 4 + [_fp, _fp, _fp, _fp, C.c_int, C.c_int]
+        L.bco_max_rel_err.restype = C.c_double
+        L.bco_max_rel_err.argtypes = [C.c_size_t, _fp, _dp]
+        L.bco_max_rel_err_f32ref.restype = C.c_double
+        L.bco_max_rel_err_f32ref.argtypes = [C.c_size_t, _fp, _fp]
+        L.bco_num_threads.restype = C.c_int
+        _lib = L
+    return _lib
+
+
+def _f(a: np.ndarray):
+    assert a.dtype == np.float32 and a.flags.c_contiguous
+    return a.ctypes.data_as(_fp)
+
+
+def _d(a: np.ndarray):
+    assert a.dtype == np.float64 and a.flags.c_contiguous
+    return a.ctypes.data_as(_dp)
+
+
+def _sel(sel):
+    if sel is None:
+        return None, 0, None
+    arr = np.ascontiguousarray(np.asarray(sel, dtype=np.int32))
+    return arr.ctypes.data_as(_ip), int(arr.size), arr
+
+
+# ---- generators (rng.rs:20-70, ops/lattice/constants.rs:11-49) -------------
+class Lcg:
+    """Sequential generator state; arrays are filled in argument order."""
+
+    def __init__(self, seed: int):
+        self.state = C.c_uint64(seed)
+
+    def uniform(self, shape, lo: float = -1.0, hi: float = 1.0) -> np.ndarray:
+        out = np.empty(shape, dtype=np.float32)
+        lib().bco_fill_uniform(C.byref(self.state), lo, hi, _f(out), out.size)
+        return out
+
+    def normal(self, shape, mu: float = 0.0, sigma: float = 1.0) -> np.ndarray:
+        out = np.empty(shape, dtype=np.float32)
+        lib().bco_fill_normal(C.byref(self.state), mu, sigma, _f(out), out.size)
+        return out
+
+
+def lcg_advance(state: int, inc: int, n: int) -> int:
+    return int(lib().bco_lcg_advance(state, inc, n))
+
+
+# ---- f64 oracles --------------------------------------------------------------
+def matmul_f64(a: np.ndarray, b: np.ndarray, rows=None) -> np.ndarray:
+    m, k = a.shape
+    k2, n = b.shape
+    assert k == k2
+    sp, ns, keep = _sel(rows)
+    c = np.empty((ns if rows is not None else m, n), dtype=np.float64)
+    lib().bco_matmul_f64(m, n, k, _f(a), k, _f(b), n, _d(c), n, sp, ns)
+    return c
+
+
+def softmax_rows_f64(x: np.ndarray) -> np.ndarray:
+    cols = x.shape[-1]
+    rows = x.size // cols
+    y = np.empty(x.shape, dtype=np.float64)
+    lib().bco_softmax_rows_f64(rows, cols, _f(x), _d(y))
+    return y
+
+
+def sdpa_f64(q, k, v, causal: bool, scale: float | None = None, heads=None) -> np.ndarray:
+    B, H, Sq, D = q.shape
+    Skv = k.shape[2]
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    sp, ns, keep = _sel(heads)
+    o = np.empty((ns, Sq, D) if heads is not None else (B, H, Sq, D), dtype=np.float64)
+    lib().bco_sdpa_f64(B, H, Sq, Skv, D, scale, int(causal), _f(q), _f(k), _f(v), _d(o), sp, ns)
+    return o
+
+
+# ---- f32 restatements ---------------------------------------------------------
+def matmul_cpu_exec_f32(a, b, row_begin: int = 0, row_end: int | None = None) -> np.ndarray:
+    m, k = a.shape
+    n = b.shape[1]
+    c = np.zeros((m, n), dtype=np.float32)
+    lib().bco_matmul_cpu_exec_f32(m, n, k, _f(a), _f(b), _f(c), row_begin, m if row_end is None else row_end)
+    return c
+
+
+def matmul_k1_f32(a, b) -> np.ndarray:
+    m, k = a.shape
+    n = b.shape[1]
+    c = np.empty((m, n), dtype=np.float32)
+    lib().bco_matmul_k1_f32(m, n, k, _f(a), _f(b), _f(c))
+    return c
+
+
+def batch_matmul_seq_f32(a, b) -> np.ndarray:
+    bt, m, k = a.shape
+    n = b.shape[2]
+    c = np.empty((bt, m, n), dtype=np.float32)
+    lib().bco_batch_matmul_seq_f32(bt, m, n, k, _f(a), _f(b), _f(c))
+    return c
+
+
+def softmax_dim_f32(x, axis: int = -1, slice_begin: int = 0, slice_end: int | None = None) -> np.ndarray:
+    shape = x.shape
+    axis = axis % len(shape)
+    outer = int(np.prod(shape[:axis], dtype=np.int64))
+    inner = int(np.prod(shape[axis + 1:], dtype=np.int64))
+    y = np.zeros_like(x)
+    end = outer * inner if slice_end is None else slice_end
+    lib().bco_softmax_dim_f32(outer, shape[axis], inner, _f(x), _f(y), slice_begin, end)
+    return y
+
+
+def softmax_global_f32(x) -> np.ndarray:
+    y = np.empty_like(x)
+    lib().bco_softmax_global_f32(x.size, _f(x), _f(y))
+    return y
+
+
+def attention_3pass_f32(q, k, v, causal: bool, heads=None) -> np.ndarray:
+    B, H, Sq, D = q.shape
+    Skv = k.shape[2]
+    sp, ns, keep = _sel(heads)
+    o = np.empty((ns, Sq, D) if heads is not None else (B, H, Sq, D), dtype=np.float32)
+    lib().bco_attention_3pass_f32(B, H, Sq, Skv, D, int(causal), _f(q), _f(k), _f(v), _f(o), sp, ns)
+    return o
+
+
+def causal_attention_cpu_f32(q, k, v, head_begin: int = 0, head_end: int | None = None) -> np.ndarray:
+    B, H, S, D = q.shape
+    o = np.zeros_like(q)
+    lib().bco_causal_attention_cpu_f32(B, H, S, D, _f(q), _f(k), _f(v), _f(o), head_begin,
+                                       B * H if head_end is None else head_end)
+    return o
+
+
+# ---- metric (tolerances/mod.rs:44-54 scale) ---------------------------------------
+def max_rel_err(x: np.ndarray, ref: np.ndarray) -> float:
+    """max |x - ref| / max(|ref|, 1); non-finite values must match exactly."""
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    if ref.dtype == np.float64:
+        ref = np.ascontiguousarray(ref).reshape(-1)
+        return float(lib().bco_max_rel_err(x.size, _f(x), _d(ref)))
+    ref = np.ascontiguousarray(ref, dtype=np.float32).reshape(-1)
+    return float(lib().bco_max_rel_err_f32ref(x.size, _f(x), _f(ref)))
+
+
+def num_threads() -> int:
+    return int(lib().bco_num_threads())

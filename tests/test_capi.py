@@ -1,0 +1,150 @@
+"""C-ABI checks that need no GPU: the library loads, exports every symbol the
+header declares, and validates arguments/shapes before touching a device
+(include/barracuda_hip.h conventions).  Also the host-side op API's shape
+validation, which mirrors the reference's error variants."""
+from __future__ import annotations
+
+import ctypes as C
+import subprocess
+
+import numpy as np
+import pytest
+
+from barracuda_amd import _native as N
+from barracuda_amd.error import (DeviceNotAvailable, InvalidOperation, OutOfMemory, ShapeMismatch,
+                                 UnsupportedOperation, from_status)
+
+
+def test_library_exports_every_header_symbol():
+    syms = N.header_symbols()
+    assert len(syms) >= 20
+    lib = N.load()
+    for s in syms:
+        assert hasattr(lib, s), s
+    # the binding declares a signature for each exported function
+    assert set(syms) == set(N.SIGNATURES)
+    out = subprocess.run(["nm", "-D", "--defined-only", str(N.LIB_PATH)], capture_output=True,
+                         text=True, check=True).stdout
+    exported = {l.split()[-1] for l in out.splitlines() if " T " in l}
+    assert set(syms) <= exported
+
+
+def test_library_carries_gfx950_code():
+    # the fat binary embedded in our own build names its target
+    assert b"amdgcn-amd-amdhsa--gfx950" in N.LIB_PATH.read_bytes()
+    hsaco = N.PKG / "lib" / "bch_softmax_rows.hsaco"
+    assert hsaco.exists() and hsaco.read_bytes()[:4] == b"\x7fELF"
+
+
+def test_status_strings_and_no_device_behaviour():
+    lib = N.load()
+    assert lib.bch_status_string(N.BCH_OK) == b"ok"
+    assert lib.bch_status_string(N.BCH_E_SHAPE) == b"shape mismatch"
+    assert lib.bch_status_string(99) == b"unknown status"
+    n = C.c_int(-1)
+    st = lib.bch_device_count(C.byref(n))
+    if st == N.BCH_E_NO_DEVICE:  # this container: no GPU
+        assert n.value == 0
+        ctx = C.c_void_p()
+        assert lib.bch_ctx_create(0, None, C.byref(ctx)) == N.BCH_E_NO_DEVICE
+        assert ctx.value is None
+        assert "no HIP device" in N.last_error(None)
+        with pytest.raises(DeviceNotAvailable):
+            from barracuda_amd import HipDevice
+            HipDevice(0)
+    else:
+        assert st == N.BCH_OK and n.value >= 1
+
+
+def test_null_and_shape_errors_before_device():
+    lib = N.load()
+    nul = C.c_void_p()
+    assert lib.bch_device_count(None) == N.BCH_E_INVALID
+    assert lib.bch_ctx_create(0, None, None) == N.BCH_E_INVALID
+    # shapes are validated first, identically with or without a GPU
+    assert lib.bch_sgemm(nul, -1, 4, 4, nul, 4, nul, 4, nul, 4) == N.BCH_E_SHAPE
+    assert "negative dimension" in N.last_error(None)
+    assert lib.bch_sgemm(nul, 4, 4, 8, nul, 4, nul, 4, nul, 4) == N.BCH_E_SHAPE  # lda < k
+    assert "leading dimension" in N.last_error(None)
+    assert lib.bch_sgemm(nul, 4, 4, 4, nul, 4, nul, 4, nul, 4) == N.BCH_E_INVALID  # ctx NULL
+    assert lib.bch_sgemm_strided_batched(nul, 2, 4, 4, 4, nul, 8, nul, 16, nul, 16) == N.BCH_E_SHAPE
+    assert lib.bch_softmax_rows(nul, 0, 5, nul, nul) == N.BCH_E_SHAPE
+    assert lib.bch_softmax_rows(nul, 2, 5, nul, nul) == N.BCH_E_INVALID
+    assert lib.bch_softmax_axis(nul, 1, 0, 1, nul, nul) == N.BCH_E_SHAPE
+    assert lib.bch_sdpa_fwd(nul, 1, 1, 4, 8, 16, 0.25, 1, nul, nul, nul, nul) == N.BCH_E_SHAPE
+    assert "causal" in N.last_error(None)
+    assert lib.bch_sdpa_fwd(nul, 1, 1, 4, 4, 256, 0.25, 0, nul, nul, nul, nul) == N.BCH_E_UNSUPPORTED
+    assert lib.bch_sdpa_fwd(nul, 0, 1, 4, 4, 16, 0.25, 0, nul, nul, nul, nul) == N.BCH_E_SHAPE
+    grid = (C.c_uint * 3)(1, 1, 1)
+    assert lib.bch_launch_code_object(nul, None, 0, b"x", grid, grid, None, 0, 0) == N.BCH_E_INVALID
+    ev = C.c_void_p()
+    assert lib.bch_event_create(nul, C.byref(ev)) == N.BCH_E_INVALID
+    f = C.c_float()
+    assert lib.bch_event_elapsed_ms(nul, nul, C.byref(f)) == N.BCH_E_INVALID
+    lib.bch_ctx_destroy(nul)  # NULL is a no-op
+    lib.bch_event_destroy(nul)
+
+
+def test_kernel_routing_names():
+    lib = N.load()
+    assert lib.bch_sgemm_kernel_name(4096, 4096, 4096) == b"sgemm_mfma_kernel<128,128,32,false>"
+    assert lib.bch_sgemm_kernel_name(1, 11008, 4096) == b"sgemm_skinny"
+    assert lib.bch_sgemm_kernel_name(32, 11008, 4096) == b"sgemm_skinny"
+    assert lib.bch_sgemm_kernel_name(100, 70, 33) == b"sgemm_mfma_kernel<128,128,32,true>"
+
+
+def test_status_to_error_variant_mapping():
+    assert isinstance(from_status(N.BCH_E_SHAPE, "x", "matmul"), InvalidOperation)
+    assert "mismatch" in str(from_status(N.BCH_E_SHAPE, "x", "matmul"))
+    assert isinstance(from_status(N.BCH_E_OOM, "x"), OutOfMemory)
+    assert isinstance(from_status(N.BCH_E_NO_DEVICE, "x"), DeviceNotAvailable)
+    assert isinstance(from_status(N.BCH_E_UNSUPPORTED, "x"), UnsupportedOperation)
+
+
+class _FakeTensor:
+    """Shape-only stand-in: the op constructors validate before any device work."""
+
+    def __init__(self, shape):
+        self._shape = list(shape)
+
+    def shape(self):
+        return list(self._shape)
+
+    def device(self):
+        return None
+
+
+def test_op_api_shape_validation_mirrors_reference():
+    from barracuda_amd import (Attention, CausalAttention, FlashAttention, InvalidInput, MatMul,
+                               ScaledDotProductAttention, Softmax)
+    T = _FakeTensor
+    # matmul.rs:92-114
+    with pytest.raises(InvalidOperation, match="2D"):
+        MatMul(T([4]), T([4, 4])).execute()
+    with pytest.raises(ShapeMismatch) as e:
+        MatMul(T([2, 3]), T([4, 2])).execute()
+    assert "mismatch" in str(e.value).lower()  # fault_injection.rs:46-55 wording
+    # softmax.rs:39-48
+    with pytest.raises(InvalidOperation, match="Empty tensor"):
+        Softmax(T([]))
+    # attention/mod.rs:96-144
+    with pytest.raises(InvalidOperation, match="4D"):
+        Attention(T([2, 4, 8]), T([1, 2, 4, 8]), T([1, 2, 4, 8]))
+    with pytest.raises(ShapeMismatch):
+        Attention(T([1, 2, 4, 8]), T([1, 3, 4, 8]), T([1, 3, 4, 8]))
+    with pytest.raises(ShapeMismatch):
+        Attention(T([1, 2, 4, 8]), T([1, 2, 6, 8]), T([1, 2, 5, 8]))
+    Attention(T([1, 2, 4, 8]), T([1, 2, 6, 8]), T([1, 2, 6, 8]))  # cross-attention is fine
+    # sdpa/mod.rs:101-149
+    with pytest.raises(InvalidInput):
+        ScaledDotProductAttention(T([4, 8]), T([4, 8]), T([4, 8]))
+    with pytest.raises(ShapeMismatch):
+        ScaledDotProductAttention(T([1, 1, 4, 8]), T([1, 1, 5, 8]), T([1, 1, 4, 8]))
+    # causal_attn/mod.rs:78-95
+    with pytest.raises(ShapeMismatch):
+        CausalAttention(T([1, 1, 4, 8]), T([1, 1, 4, 8]), T([1, 1, 4, 4]))
+    # flash_attention.rs:57-80
+    with pytest.raises(InvalidOperation, match="same shape"):
+        FlashAttention(T([4, 8]), T([4, 4]), T([4, 8]), 1)
+    with pytest.raises(InvalidOperation, match="2D"):
+        FlashAttention(T([1, 4, 8]), T([1, 4, 8]), T([1, 4, 8]), 1)

@@ -1,0 +1,80 @@
+"""Host API on the GPU: seeded device fills vs the oracle's generators, the
+reference tests' error paths, and allocation-failure injection."""
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+
+import numpy as np
+import pytest
+
+from barracuda_amd import LcgStream, Tensor
+from barracuda_amd.error import ShapeMismatch
+from oracle import bc_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+@pytest.mark.parametrize("seed", [0, 2, 12345])
+def test_device_uniform_fill_is_bit_exact(dev, seed):
+    _say(f"fill_uniform seed {seed}")
+    s = LcgStream(seed, dev)
+    a = s.uniform([1000, 37]).to_numpy()
+    b = s.uniform([3, 5], 0.0, 1.0).to_numpy()
+    r = O.Lcg(seed)
+    assert np.array_equal(a, r.uniform((1000, 37)))
+    assert np.array_equal(b, r.uniform((3, 5), 0.0, 1.0))
+    assert s.state.value == r.state.value
+
+
+@pytest.mark.parametrize("seed,sigma", [(1, 3.0), (3, 0.02), (4, 1.0)])
+def test_device_normal_fill_matches(dev, seed, sigma):
+    _say(f"fill_normal seed {seed} sigma {sigma}")
+    s = LcgStream(seed, dev)
+    x = s.normal([4099 * 3], 0.0, sigma).to_numpy()
+    y = s.normal([17]).to_numpy()
+    r = O.Lcg(seed)
+    rx, ry = r.normal(4099 * 3, 0.0, sigma), r.normal(17)
+    # device log/cos (f64) vs host libm: equal after rounding to f32, or 1 ulp apart
+    ulps = np.abs(x.view(np.int32).astype(np.int64) - rx.view(np.int32).astype(np.int64))
+    assert ulps.max() <= 1 and (ulps == 0).mean() > 0.999
+    assert np.array_equal(y.view(np.int32) // 2, ry.view(np.int32) // 2) or \
+        np.abs(y.view(np.int32).astype(np.int64) - ry.view(np.int32)).max() <= 1
+    assert s.state.value == r.state.value
+
+
+def test_fault_injection_shape_error_message(dev):
+    # T/fault_injection.rs:29-60: a mismatched matmul returns an error that
+    # names shape/dimension/mismatch, and the device stays usable
+    a = Tensor.from_data(np.ones(6, np.float32), [2, 3], dev)
+    b = Tensor.from_data(np.ones(8, np.float32), [4, 2], dev)
+    with pytest.raises(ShapeMismatch) as e:
+        a.matmul(b)
+    msg = str(e.value).lower()
+    assert any(w in msg for w in ("shape", "dimension", "mismatch"))
+    c = Tensor.from_data(np.ones(6, np.float32), [3, 2], dev)
+    assert np.array_equal(a.matmul(c).to_vec(), np.full(4, 3.0, np.float32))
+
+
+def test_alloc_failure_injection_maps_to_out_of_memory():
+    _say("alloc failure injection (child process)")
+    code = (
+        "import numpy as np\n"
+        "from barracuda_amd import Tensor, OutOfMemory, get_device\n"
+        "d = get_device()\n"
+        "try:\n"
+        "    Tensor.from_data(np.ones(4, np.float32), [4], d)\n"
+        "    print('NO-ERROR')\n"
+        "except OutOfMemory as e:\n"
+        "    print('OOM', e)\n")
+    env = dict(os.environ, BARRACUDA_HIP_FAIL_ALLOC="1")
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, "-c", code], env=env, cwd=root, capture_output=True, text=True,
+                       timeout=120)
+    assert "OOM" in r.stdout, r.stdout + r.stderr
+    assert "injected" in r.stdout

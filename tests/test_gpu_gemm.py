@@ -1,0 +1,157 @@
+"""f32 GEMM on the MI355X vs the oracle (bch_sgemm, bch_sgemm_strided_batched).
+
+Tolerance: max |x - ref| / max(|ref|, 1) <= 1e-4 against the f64 oracle
+(tolerances/mod.rs:44-54 scale).  The literal reference vectors are checked
+at the reference tests' own tolerances.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from barracuda_amd import Tensor
+from oracle import bc_oracle as O
+from tests.conftest import case_inputs
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-4
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+def _mm(dev, a, b):
+    ta = Tensor.from_data(a, list(a.shape), dev)
+    tb = Tensor.from_data(b, list(b.shape), dev)
+    return ta.matmul(tb).to_numpy()
+
+
+def test_golden_vectors(dev, golden):
+    for case in golden["matmul"]:
+        _say(f"matmul golden {case['name']}")
+        a, b = case_inputs(case)
+        got = _mm(dev, a, b).reshape(-1)
+        want = np.array(case["expected"])
+        if case["tol"] == 0.0:
+            assert np.array_equal(got, want.astype(np.float32)), case["name"]
+        else:
+            # the reference tests' absolute bound, widened to 1e-6 relative where
+            # |C| is so large (6875 in the ramps) that it is below 2 ulp of f32
+            bound = np.maximum(case["tol"], 1e-6 * np.abs(want))
+            assert np.all(np.abs(got - want) <= bound), case["name"]
+    for case in golden["batch_matmul"]:
+        a = np.array(case["a"], dtype=np.float32).reshape(case["a_shape"])
+        b = np.array(case["b"], dtype=np.float32).reshape(case["b_shape"])
+        ta, tb = Tensor.from_data(a, case["a_shape"], dev), Tensor.from_data(b, case["b_shape"], dev)
+        got = ta.batch_matmul(tb)
+        assert got.shape() == [2, 2, 2]
+        assert np.array_equal(got.to_vec(), np.array(case["expected"], dtype=np.float32))
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 1, 1), (2, 3, 1), (7, 5, 3), (33, 65, 17), (100, 70, 33),
+                                   (128, 128, 32), (256, 128, 64), (129, 257, 100), (512, 384, 160),
+                                   (40, 11008, 64), (300, 4, 4096), (64, 64, 0)])
+def test_shapes_vs_f64(dev, m, n, k):
+    _say(f"sgemm m={m} n={n} k={k}")
+    rng = O.Lcg(m * 7 + n * 13 + k)
+    a = rng.uniform((m, k))
+    b = rng.uniform((k, n))
+    got = _mm(dev, a, b) if k > 0 else None
+    if k == 0:
+        ta, tb = Tensor.empty([m, 0], dev), Tensor.empty([0, n], dev)
+        got = ta.matmul(tb).to_numpy()
+        assert not got.any()
+        return
+    ref = O.matmul_f64(a, b)
+    assert O.max_rel_err(got, ref) <= TOL
+    # integer-valued inputs: the MFMA path is exact
+    ai = np.round(a * 8).astype(np.float32)
+    bi = np.round(b * 8).astype(np.float32)
+    exact = (ai.astype(np.int64) @ bi.astype(np.int64)).astype(np.float32)
+    assert np.array_equal(_mm(dev, ai, bi), exact)
+
+
+@pytest.mark.parametrize("m", [1, 2, 8, 13, 32])
+def test_skinny_decode_shapes(dev, m):
+    """BASELINE config 4 shapes: M in {1, 8, 32}, K = 4096, N = 11008; X ~ N(0,1),
+    W ~ N(0, 0.02), seed 3 (plus M = 2, 13 for the routing edges)."""
+    _say(f"skinny m={m} k=4096 n=11008 seed 3")
+    rng = O.Lcg(3)
+    x = rng.normal((m, 4096))
+    w = rng.normal((4096, 11008), 0.0, 0.02)
+    got = _mm(dev, x, w)
+    ref = O.matmul_f64(x, w)
+    err = O.max_rel_err(got, ref)
+    _say(f"  max rel err = {err:.3e}")
+    assert err <= TOL
+
+
+def test_leading_dimensions_and_unaligned(dev):
+    _say("sgemm with lda/ldb/ldc > natural and an odd offset")
+    m, n, k = 96, 160, 72
+    rng = O.Lcg(77)
+    A = rng.uniform((m, k + 5))
+    B = rng.uniform((k, n + 3))
+    ta = Tensor.from_data(A, [m, k + 5], dev)
+    tb = Tensor.from_data(B, [k, n + 3], dev)
+    tc = Tensor.empty([m, n + 7], dev)
+    dev.check(dev._lib.bch_sgemm(dev.ctx, m, n, k, C.c_void_p(ta.ptr), k + 5, C.c_void_p(tb.ptr), n + 3,
+                                 C.c_void_p(tc.ptr), n + 7), "sgemm")
+    got = tc.to_numpy()[:, :n]
+    ref = O.matmul_f64(np.ascontiguousarray(A[:, :k]), np.ascontiguousarray(B[:, :n]))
+    assert O.max_rel_err(got, ref) <= TOL
+    # A starting 4 bytes into an allocation (not 16-byte aligned)
+    ta2 = Tensor.from_data(np.concatenate([[0.0], A.reshape(-1)]).astype(np.float32), [1 + A.size], dev)
+    tc2 = Tensor.empty([m, n], dev)
+    dev.check(dev._lib.bch_sgemm(dev.ctx, m, n, k, C.c_void_p(ta2.ptr + 4), k + 5, C.c_void_p(tb.ptr),
+                                 n + 3, C.c_void_p(tc2.ptr), n), "sgemm")
+    assert O.max_rel_err(tc2.to_numpy(), ref) <= TOL
+
+
+def test_config_4096_cubed(dev):
+    """BASELINE config 3a: 4096^3, U[-1,1), seed 2; f64 oracle on sampled rows."""
+    _say("sgemm 4096^3 seed 2")
+    rng = O.Lcg(2)
+    a = rng.uniform((4096, 4096))
+    b = rng.uniform((4096, 4096))
+    got = _mm(dev, a, b)
+    rows = [0, 1, 127, 128, 2047, 2048, 4095] + list(range(513, 4096, 257))
+    ref = O.matmul_f64(a, b, rows=rows)
+    err = O.max_rel_err(got[rows], ref)
+    _say(f"  max rel err (sampled rows) = {err:.3e}")
+    assert err <= TOL
+    # a column sample too: C[:, j] = A @ B[:, j]
+    cols = [0, 31, 32, 4000, 4095]
+    refc = a.astype(np.float64) @ b[:, cols].astype(np.float64)
+    assert O.max_rel_err(got[:, cols], refc) <= TOL
+
+
+def test_config_batched_16x1024(dev):
+    """BASELINE config 3b: batch 16 of 1024^3, U[-1,1), seed 2."""
+    _say("batched sgemm 16x1024^3 seed 2")
+    rng = O.Lcg(2)
+    a = rng.uniform((16, 1024, 1024))
+    b = rng.uniform((16, 1024, 1024))
+    ta, tb = Tensor.from_data(a, [16, 1024, 1024], dev), Tensor.from_data(b, [16, 1024, 1024], dev)
+    got = ta.batch_matmul(tb).to_numpy()
+    for bi in (0, 7, 15):
+        rows = [0, 5, 511, 1023]
+        ref = O.matmul_f64(np.ascontiguousarray(a[bi]), np.ascontiguousarray(b[bi]), rows=rows)
+        assert O.max_rel_err(got[bi][rows], ref) <= TOL
+    # batches are independent: batch 3 equals the single GEMM of batch 3
+    single = _mm(dev, np.ascontiguousarray(a[3]), np.ascontiguousarray(b[3]))
+    assert np.array_equal(single, got[3])
+
+
+def test_batched_ragged(dev):
+    _say("batched sgemm ragged 3x(37x45x29)")
+    rng = O.Lcg(5)
+    a = rng.uniform((3, 37, 29))
+    b = rng.uniform((3, 29, 45))
+    ta, tb = Tensor.from_data(a, [3, 37, 29], dev), Tensor.from_data(b, [3, 29, 45], dev)
+    got = ta.batch_matmul(tb).to_numpy()
+    for i in range(3):
+        assert O.max_rel_err(got[i], O.matmul_f64(np.ascontiguousarray(a[i]), np.ascontiguousarray(b[i]))) <= TOL

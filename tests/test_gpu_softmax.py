@@ -1,0 +1,132 @@
+"""Row softmax on the MI355X vs the oracle (bch_softmax_rows / bch_softmax_axis).
+
+Tolerance: max |x - ref| / max(|ref|, 1) <= 1e-4 against the f64 oracle
+(the north-star bar); in practice the kernel is within ~1e-6.  Elementwise
+relative error is also bounded where it is meaningful (outputs >= 1e-30).
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from barracuda_amd import Tensor
+from oracle import bc_oracle as O
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-4
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+def _softmax_gpu(dev, x: np.ndarray) -> np.ndarray:
+    t = Tensor.from_data(x, list(x.shape), dev)
+    return t.softmax_dim(len(x.shape) - 1).to_numpy()
+
+
+def test_golden_vectors(dev, golden):
+    for case in golden["softmax"]:
+        _say(f"softmax golden {case['name']}")
+        x = np.array(case["x"], dtype=np.float32).reshape(case["shape"])
+        axis = case.get("axis", len(case["shape"]) - 1)
+        t = Tensor.from_data(x, list(x.shape), dev)
+        got = (t.softmax() if len(case["shape"]) == 1 else t.softmax_dim(axis)).to_vec()
+        want = np.array(case["expected"])
+        assert O.max_rel_err(got, want) <= max(case.get("tol", 1e-5), 1e-6), case["name"]
+        if "sum_tol" in case:
+            assert np.all(np.abs(got.reshape(case["shape"]).sum(axis=axis) - 1.0) < case["sum_tol"])
+        if case.get("monotone"):
+            assert np.all(np.diff(got) > 0)
+        if "last_gt" in case:
+            assert got[-1] > case["last_gt"]
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 1), (3, 3), (5, 4), (7, 256), (9, 257), (4, 1000),
+                                       (33, 2048), (8, 4096), (3, 4100), (2, 10000), (1, 65536)])
+def test_shapes_vs_f64(dev, rows, cols):
+    _say(f"softmax rows={rows} cols={cols}")
+    x = O.Lcg(rows * 1000 + cols).normal((rows, cols), 0.0, 3.0)
+    got = _softmax_gpu(dev, x)
+    ref = O.softmax_rows_f64(x)
+    assert O.max_rel_err(got, ref) <= TOL
+    rel = np.abs(got - ref) / np.maximum(ref, 1e-30)
+    assert rel.max() < 1e-5
+    # the reference's own f32 algorithm agrees to the same bar
+    assert O.max_rel_err(got, O.softmax_dim_f32(x)) <= TOL
+
+
+def test_edge_values(dev):
+    _say("softmax edge values")
+    x = np.array([[-np.inf, 1.0, 2.0, -np.inf],
+                  [0.0, 0.0, 0.0, 0.0],
+                  [88.0, -88.0, 0.0, 1e-30],
+                  [1e30, 1e30, -1e30, 0.0]], dtype=np.float32)
+    got = _softmax_gpu(dev, x)
+    ref = O.softmax_rows_f64(x)
+    assert O.max_rel_err(got, ref) <= TOL
+    assert got[0, 0] == 0.0 and got[0, 3] == 0.0
+    assert np.all(got[1] == np.float32(0.25))
+    # block path (cols % 4 != 0) with -inf at the start of the row
+    x2 = np.full((2, 7), -np.inf, dtype=np.float32)
+    x2[:, 3:] = [1.0, 2.0, 3.0, 4.0]
+    got2 = _softmax_gpu(dev, x2)
+    assert O.max_rel_err(got2, O.softmax_rows_f64(x2)) <= TOL
+    assert np.all(got2[:, :3] == 0.0)
+
+
+def test_axis_and_inplace(dev):
+    _say("softmax axis / in-place")
+    x = O.Lcg(9).normal((4, 37, 12), 0.0, 2.0)
+    t = Tensor.from_data(x, list(x.shape), dev)
+    for axis in (0, 1, 2):
+        got = t.softmax_dim(axis).to_numpy()
+        want = O.softmax_rows_f64(np.ascontiguousarray(np.moveaxis(x, axis, -1)))
+        assert O.max_rel_err(got, np.ascontiguousarray(np.moveaxis(want, -1, axis))) <= TOL
+    # in == out through the C ABI
+    y = O.Lcg(10).normal((16, 2048), 0.0, 3.0)
+    ty = Tensor.from_data(y, [16, 2048], dev)
+    dev.check(dev._lib.bch_softmax_rows(dev.ctx, 16, 2048, C.c_void_p(ty.ptr), C.c_void_p(ty.ptr)), "sm")
+    assert O.max_rel_err(ty.to_numpy(), O.softmax_rows_f64(y)) <= TOL
+
+
+def test_code_object_dispatch(dev):
+    """dispatch_binary path: the same row softmax from the prebuilt .hsaco."""
+    _say("softmax via bch_launch_code_object")
+    from barracuda_amd import _native as N
+    rows = 64
+    x = O.Lcg(12).normal((rows, 2048), 0.0, 3.0)
+    tin = Tensor.from_data(x, [rows, 2048], dev)
+    tout = Tensor.empty([rows, 2048], dev)
+    args = [C.c_void_p(tin.ptr), C.c_void_p(tout.ptr), C.c_longlong(rows)]
+    dev.dispatch_binary("bch_softmax_rows.hsaco", "bch_softmax_rows_2048", (rows // 4, 1, 1), (256, 1, 1), args)
+    assert O.max_rel_err(tout.to_numpy(), O.softmax_rows_f64(x)) <= TOL
+    img = (N.PKG / "lib" / "bch_softmax_rows.hsaco").read_bytes()
+    tout2 = Tensor.empty([rows, 2048], dev)
+    args[1] = C.c_void_p(tout2.ptr)
+    dev.dispatch_binary(img, "bch_softmax_rows_2048", (rows // 4, 1, 1), (256, 1, 1), args)
+    assert np.array_equal(tout2.to_numpy(), tout.to_numpy())
+    from barracuda_amd import DeviceError
+    with pytest.raises(DeviceError):
+        dev.dispatch_binary(img, "no_such_kernel", (1, 1, 1), (64, 1, 1), args)
+    with pytest.raises(DeviceError):
+        dev.dispatch_binary(b"not a code object", "k", (1, 1, 1), (64, 1, 1), args)
+
+
+def test_config_65536x2048(dev):
+    """[65536 x 2048], N(0, 3), seed 1, max-subtracted."""
+    _say("softmax config 65536x2048 seed 1")
+    x = O.Lcg(1).normal((65536, 2048), 0.0, 3.0)
+    got = _softmax_gpu(dev, x)
+    ref = O.softmax_rows_f64(x)
+    err = O.max_rel_err(got, ref)
+    _say(f"  max rel err vs f64 = {err:.3e}")
+    assert err <= TOL
+    # size-independent properties: every row sums to 1, argmax preserved
+    assert np.abs(got.astype(np.float64).sum(axis=1) - 1.0).max() < 1e-5
+    assert np.array_equal(got[:1024].argmax(axis=1), x[:1024].argmax(axis=1))
+    # the reference's own f32 algorithm (softmax_dim) on a row sample
+    sub = O.softmax_dim_f32(x, 1, 0, 512)[:512]
+    assert O.max_rel_err(got[:512], sub) <= TOL

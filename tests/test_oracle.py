@@ -1,0 +1,272 @@
+"""Pin the CPU oracle (oracle/bc_oracle.c) before trusting it.
+
+Every oracle function is checked against something it does not compute
+itself: the reference tests' literal vectors (tests/golden/), exact integer
+arithmetic, closed forms, or brute force in numpy float64.  Planted-mistake
+tests show the checks catch a transposed operand, a wrong scale, a flipped
+mask and a changed summation order.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+
+from oracle import bc_oracle as O
+from tests.conftest import case_inputs, f32
+
+M64 = (1 << 64) - 1
+MUL = 6364136223846793005
+INC_MMIX = 1442695040888963407
+
+
+# ---------------------------------------------------------------- generators
+@pytest.mark.parametrize("seed", ["0", "1", "2", "3", "4", "42", "12345"])
+def test_uniform_matches_exact_lcg(golden, seed):
+    g = golden["lcg"][seed]
+    got = O.Lcg(int(seed)).uniform(8)
+    assert got.tolist() == g["uniform_pm1_f32"]
+    u01 = O.Lcg(int(seed)).uniform(8, 0.0, 1.0)
+    assert np.array_equal(u01, np.array(g["uniform_f64"], dtype=np.float32))
+
+
+@pytest.mark.parametrize("seed", ["0", "1", "3", "4", "42"])
+def test_normal_matches_box_muller(golden, seed):
+    g = golden["lcg"][seed]
+    got = O.Lcg(int(seed)).normal(8)
+    want = np.array(g["normal_f64"], dtype=np.float32)
+    # same f64 formula through the same libm: identical after rounding to f32
+    assert np.array_equal(got, want)
+    got3 = O.Lcg(int(seed)).normal(8, 0.0, 3.0)
+    assert np.allclose(got3, np.float32(3.0) * want, rtol=1e-6, atol=0)
+
+
+def test_jump_ahead_equals_stepping():
+    for inc in (1, INC_MMIX):
+        s = 987654321
+        for n in (0, 1, 2, 7, 1000, 12345):
+            x = s
+            for _ in range(n):
+                x = (x * MUL + inc) & M64
+            assert O.lcg_advance(s, inc, n) == x
+
+
+def test_parallel_fill_equals_sequential_stream():
+    # the threaded fill must produce the exact sequential stream, and
+    # filling A then B must continue the stream (argument order)
+    n = 300_001
+    rng = O.Lcg(7)
+    a = rng.uniform(n)
+    b = rng.uniform(5)
+    s = 7
+    idx = {0, 1, 2, n // 3, n // 2, n - 1}
+    for i in range(n + 5):
+        s = (s * MUL + 1) & M64
+        if i in idx:
+            assert a[i] == np.float32(2.0 * ((s >> 11) / float(1 << 53)) - 1.0)
+        if i >= n:
+            assert b[i - n] == np.float32(2.0 * ((s >> 11) / float(1 << 53)) - 1.0)
+    # normals consume two draws each
+    r2 = O.Lcg(11)
+    x = r2.normal(1001)
+    assert r2.state.value == O.lcg_advance(11, INC_MMIX, 2002)
+    assert np.array_equal(x[:10], O.Lcg(11).normal(10))
+
+
+def test_generator_moments():
+    # ops/lattice/constants.rs tests: U(0,1) mean 0.5; N(0,1) mean ~0, var ~1
+    u = O.Lcg(123).uniform(200_000, 0.0, 1.0).astype(np.float64)
+    assert abs(u.mean() - 0.5) < 0.005 and abs(u.var() - 1 / 12) < 0.002
+    z = O.Lcg(123).normal(200_000).astype(np.float64)
+    assert abs(z.mean()) < 0.02 and abs(z.var() - 1.0) < 0.05
+    assert u.min() >= 0.0 and u.max() < 1.0
+
+
+# ---------------------------------------------------------------- matmul
+def test_matmul_f64_golden(golden):
+    for case in golden["matmul"]:
+        a, b = case_inputs(case)
+        got = O.matmul_f64(a, b).reshape(-1)
+        want = np.array(case["expected"])
+        # exact rational expected values; f64 accumulation of f32 products
+        assert np.allclose(got, want, rtol=1e-12, atol=1e-12), case["name"]
+
+
+def test_matmul_f64_brute_force_and_row_selection():
+    rng = np.random.default_rng(0)
+    for (m, k, n) in [(1, 1, 1), (3, 5, 7), (17, 33, 9), (64, 3, 65)]:
+        a = rng.standard_normal((m, k)).astype(np.float32)
+        b = rng.standard_normal((k, n)).astype(np.float32)
+        want = a.astype(np.longdouble) @ b.astype(np.longdouble)
+        got = O.matmul_f64(a, b)
+        assert np.allclose(got, want.astype(np.float64), rtol=1e-13, atol=1e-13)
+        rows = [m - 1, 0]
+        assert np.array_equal(O.matmul_f64(a, b, rows=rows), got[rows])
+
+
+def test_matmul_f32_restatements_exact_on_integers():
+    rng = np.random.default_rng(1)
+    a = rng.integers(-8, 9, (37, 70)).astype(np.float32)
+    b = rng.integers(-8, 9, (70, 45)).astype(np.float32)
+    exact = a.astype(np.int64) @ b.astype(np.int64)
+    assert np.array_equal(O.matmul_cpu_exec_f32(a, b), exact.astype(np.float32))
+    assert np.array_equal(O.matmul_k1_f32(a, b), exact.astype(np.float32))
+    bt = np.stack([a[:, :40].copy(), a[:, 30:].copy()])
+    bb = np.stack([b[:40, :].copy(), b[30:, :].copy()])
+    want = np.stack([a[:, :40].astype(np.int64) @ b[:40].astype(np.int64),
+                     a[:, 30:].astype(np.int64) @ b[30:].astype(np.int64)])
+    assert np.array_equal(O.batch_matmul_seq_f32(bt, bb), want.astype(np.float32))
+
+
+def test_matmul_f32_restatements_within_tolerance_of_f64():
+    rng = O.Lcg(2)
+    a = rng.uniform((96, 512))
+    b = rng.uniform((512, 80))
+    ref = O.matmul_f64(a, b)
+    for got in (O.matmul_cpu_exec_f32(a, b), O.matmul_k1_f32(a, b)):
+        assert O.max_rel_err(got, ref) < 1e-5
+
+
+def test_k1_order_differs_from_sequential_order():
+    # pins the K1 grouping a0*b0 + (a1*b1 + (a2*b2 + (a3*b3 + acc))):
+    # on [1, 1, 1e8, -1e8] sequential f32 accumulation loses the ones
+    a = np.array([[1.0, 1.0, 1e8, -1e8]], dtype=np.float32)
+    b = np.ones((4, 1), dtype=np.float32)
+    assert O.matmul_cpu_exec_f32(a, b)[0, 0] == 0.0
+    assert O.matmul_k1_f32(a, b)[0, 0] == 2.0
+    assert O.matmul_f64(a, b)[0, 0] == 2.0
+
+
+def test_planted_transposed_operand_fails_golden(golden):
+    case = next(c for c in golden["matmul"] if c["name"] == "precision_2x3_3x2")
+    a, b = case_inputs(case)
+    wrong = O.matmul_f64(a, np.ascontiguousarray(b.reshape(2, 3).T))  # B read transposed
+    assert not np.allclose(wrong.reshape(-1), case["expected"], atol=1e-5)
+
+
+# ---------------------------------------------------------------- softmax
+def test_softmax_golden(golden):
+    for case in golden["softmax"]:
+        x = np.array(case["x"], dtype=np.float32).reshape(case["shape"])
+        axis = case.get("axis", len(case["shape"]) - 1)
+        got32 = O.softmax_dim_f32(x, axis).reshape(-1)
+        want = np.array(case["expected"])
+        assert O.max_rel_err(got32, want) < 2e-7, case["name"]
+        if axis == len(case["shape"]) - 1:
+            got64 = O.softmax_rows_f64(x).reshape(-1)
+            assert np.allclose(got64, want, rtol=1e-14, atol=1e-15), case["name"]
+        if "sum_tol" in case:
+            sums = got32.reshape(case["shape"]).sum(axis=axis)
+            assert np.all(np.abs(sums - 1.0) < case["sum_tol"])
+        if case.get("monotone"):
+            assert np.all(np.diff(got32) > 0)
+        if "last_gt" in case:
+            assert got32[-1] > case["last_gt"]
+
+
+def test_softmax_invariants_and_global():
+    x = O.Lcg(1).normal((64, 300), 0.0, 3.0)
+    y = O.softmax_rows_f64(x)
+    assert np.allclose(y.sum(axis=1), 1.0, atol=1e-14)
+    # shift invariance and the all-equal row
+    assert np.allclose(O.softmax_rows_f64(x + np.float32(5.0)), y, atol=1e-6)
+    eq = np.full((2, 7), 3.0, dtype=np.float32)
+    assert np.all(O.softmax_dim_f32(eq) == np.float32(1.0 / 7.0)) or \
+        np.allclose(O.softmax_dim_f32(eq), 1.0 / 7.0, rtol=1e-7)
+    g = O.softmax_global_f32(x)
+    assert abs(float(g.astype(np.float64).sum()) - 1.0) < 1e-4
+    # one sequential f32 sum over 19200 terms (the reference's order): its
+    # rounding sets the elementwise relative error, ~1e-4 here
+    ref = O.softmax_rows_f64(x.reshape(1, -1)).reshape(-1)
+    assert np.max(np.abs(g.reshape(-1) - ref) / ref) < 1e-3
+
+
+def test_softmax_axis_restatement_matches_transpose():
+    x = O.Lcg(5).normal((3, 11, 6))
+    got = O.softmax_dim_f32(x, 1)
+    want = O.softmax_rows_f64(np.ascontiguousarray(np.moveaxis(x, 1, 2)))
+    assert O.max_rel_err(got, np.ascontiguousarray(np.moveaxis(want, 2, 1))) < 1e-6
+
+
+# ---------------------------------------------------------------- attention
+def _np_sdpa(q, k, v, causal, scale):
+    q, k, v = (t.astype(np.float64) for t in (q, k, v))
+    s = np.einsum("bhid,bhjd->bhij", q, k) * scale
+    if causal:
+        i = np.arange(s.shape[2])[:, None]
+        j = np.arange(s.shape[3])[None, :]
+        s = np.where(j <= i, s, -np.inf)
+    s = s - s.max(axis=-1, keepdims=True)
+    p = np.exp(s)
+    p /= p.sum(axis=-1, keepdims=True)
+    return np.einsum("bhij,bhjd->bhid", p, v)
+
+
+def _att_inputs(case):
+    sq = case.get("shape_q", case.get("shape"))
+    skv = case.get("shape_kv", case.get("shape"))
+    q = np.array(case["q"], dtype=np.float32).reshape(sq)
+    k = np.array(case["k"], dtype=np.float32).reshape(skv)
+    v = np.array(case["v"], dtype=np.float32).reshape(skv)
+    return q, k, v
+
+
+def test_sdpa_f64_closed_forms(golden):
+    for case in golden["attention"]:
+        q, k, v = _att_inputs(case)
+        got = O.sdpa_f64(q, k, v, case["causal"]).reshape(-1)
+        assert np.allclose(got, case["expected"], rtol=1e-12, atol=1e-12), case["name"]
+
+
+def test_sdpa_f64_brute_force_cross_and_heads():
+    rng = O.Lcg(4)
+    for (B, H, Sq, Skv, D, causal) in [(1, 1, 5, 5, 3, True), (2, 3, 7, 7, 8, False),
+                                        (1, 2, 4, 9, 16, False), (2, 2, 33, 33, 32, True)]:
+        q = rng.normal((B, H, Sq, D))
+        k = rng.normal((B, H, Skv, D))
+        v = rng.normal((B, H, Skv, D))
+        scale = 1.0 / math.sqrt(D)
+        want = _np_sdpa(q, k, v, causal, scale)
+        got = O.sdpa_f64(q, k, v, causal)
+        assert np.allclose(got, want, rtol=1e-12, atol=1e-12)
+        heads = [B * H - 1, 0]
+        sel = O.sdpa_f64(q, k, v, causal, heads=heads)
+        assert np.array_equal(sel, got.reshape(B * H, Sq, D)[heads])
+        # causal row 0 is exactly V[0]
+        if causal:
+            assert np.array_equal(got[:, :, 0, :], v[:, :, 0, :].astype(np.float64))
+
+
+def test_attention_f32_restatements_within_tolerance():
+    rng = O.Lcg(4)
+    B, H, S, D = 1, 3, 64, 32
+    q, k, v = rng.normal((B, H, S, D)), rng.normal((B, H, S, D)), rng.normal((B, H, S, D))
+    for causal in (False, True):
+        ref = O.sdpa_f64(q, k, v, causal)
+        assert O.max_rel_err(O.attention_3pass_f32(q, k, v, causal), ref) < 1e-5
+    ref = O.sdpa_f64(q, k, v, True)
+    assert O.max_rel_err(O.causal_attention_cpu_f32(q, k, v), ref) < 1e-5
+    # the CPU causal path on a head subset writes only those heads
+    part = O.causal_attention_cpu_f32(q, k, v, 1, 2)
+    assert np.array_equal(part[0, 1], O.causal_attention_cpu_f32(q, k, v)[0, 1])
+    assert not part[0, 0].any() and not part[0, 2].any()
+
+
+def test_planted_attention_mistakes_fail_closed_forms(golden):
+    case = next(c for c in golden["attention"] if c["name"] == "causal_equal_scores_prefix_mean")
+    q, k, v = _att_inputs(case)
+    assert not np.allclose(O.sdpa_f64(q, k, v, False).reshape(-1), case["expected"], atol=1e-3)
+    case = next(c for c in golden["attention"] if c["name"] == "one_hot_2x2")
+    q, k, v = _att_inputs(case)
+    assert not np.allclose(O.sdpa_f64(q, k, v, False, scale=1.0).reshape(-1), case["expected"], atol=1e-3)
+
+
+# ---------------------------------------------------------------- metric
+def test_max_rel_err_metric():
+    ref = np.array([0.5, 10.0, -200.0], dtype=np.float64)
+    x = np.array([0.5 + 1e-3, 10.0 + 1e-3, -200.0 - 2e-2], dtype=np.float32)
+    # scale max(|ref|, 1): 1e-3/1, 1e-3/10, 2e-2/200
+    assert abs(O.max_rel_err(x, ref) - 1e-3) < 1e-6
+    assert O.max_rel_err(np.array([np.nan], np.float32), np.array([1.0])) == math.inf
+    assert O.max_rel_err(np.array([np.inf], np.float32), np.array([np.inf])) == 0.0
