@@ -42,6 +42,7 @@ SIGNATURES = {
     "bch_download": (_i, [_vp, _vp, _vp, _sz]),
     "bch_memset": (_i, [_vp, _vp, _i, _sz]),
     "bch_sync": (_i, [_vp]),
+    "bch_copy": (_i, [_vp, _vp, _vp, _sz]),
     "bch_sgemm": (_i, [_vp, _i, _i, _i, _vp, _i, _vp, _i, _vp, _i]),
     "bch_sgemm_strided_batched": (_i, [_vp, _i, _i, _i, _i, _vp, _ll, _vp, _ll, _vp, _ll]),
     "bch_softmax_rows": (_i, [_vp, _ll, _ll, _vp, _vp]),

@@ -35,7 +35,8 @@ DEVICE_FLAGS = [
     "-Wall", "-Wno-unused-function", "-Wno-unused-result",
 ]
 SOURCES = ["bch_runtime.hip", "softmax_rows.hip", "sgemm_mfma.hip",
-           "sgemm_skinny.hip", "sdpa_fwd.hip", "rng_fill.hip"]
+           "sgemm_skinny.hip", "sdpa_fwd.hip", "rng_fill.hip",
+           "copy.hip"]
 
 
 def _run(cmd: list[str]) -> None:

@@ -44,6 +44,7 @@ hipError_t launch_sgemm_skinny(hipStream_t s, int m, int n, int k,
                                int ldb, float* C, int ldc, void* ws,
                                size_t ws_bytes);
 size_t sgemm_skinny_workspace_bytes(int m, int n, int k);
+const char* sgemm_skinny_kernel_name(int m);
 bool sgemm_skinny_applies(int m, int n, int k, const float* A, int lda,
                           const float* B, int ldb);
 
@@ -53,6 +54,9 @@ hipError_t launch_fill_uniform(hipStream_t s, float* out, uint64_t n, uint64_t s
 hipError_t launch_fill_normal(hipStream_t s, float* out, uint64_t n, uint64_t state, double mu,
                               double sigma);
 uint64_t lcg_advance(uint64_t state, uint64_t inc, uint64_t n);
+
+// Device-to-device copy (16-byte path when aligned).
+hipError_t launch_copy(hipStream_t s, void* dst, const void* src, size_t bytes);
 
 // Fused attention forward over [B,H,S,D].
 hipError_t launch_sdpa(hipStream_t s, int B, int H, int Sq, int Skv, int D,

@@ -98,7 +98,9 @@ bch_status ensure_ws(bch_ctx* ctx, size_t bytes) {
     return from_hip(ctx, e, "workspace hipMalloc");
   }
   ctx->ws_bytes = want;
-  return BCH_OK;
+  // kernels that keep counters in the workspace expect them at zero and
+  // leave them at zero when they finish
+  return from_hip(ctx, hipMemsetAsync(ctx->ws, 0, want, ctx->stream), "workspace clear");
 }
 
 bool fail_alloc_injected() {
@@ -234,6 +236,14 @@ bch_status bch_memset(bch_ctx* ctx, void* dst, int value, size_t bytes) {
   bch_status st = use(ctx);
   if (st != BCH_OK) return st;
   return from_hip(ctx, hipMemsetAsync(dst, value, bytes, ctx->stream), "bch_memset");
+}
+
+bch_status bch_copy(bch_ctx* ctx, void* dst, const void* src, size_t bytes) {
+  if (!ctx || (bytes && (!dst || !src))) return fail(ctx, BCH_E_INVALID, "bch_copy: NULL argument");
+  if (!bytes) return BCH_OK;
+  bch_status st = use(ctx);
+  if (st != BCH_OK) return st;
+  return from_hip(ctx, bch::launch_copy(ctx->stream, dst, src, bytes), "bch_copy launch");
 }
 
 bch_status bch_sync(bch_ctx* ctx) {

@@ -277,7 +277,7 @@ namespace bch {
 
 const char* sgemm_kernel_name(int m, int n, int k) {
   if (m <= 32 && sgemm_skinny_applies(m, n, k, nullptr, k, nullptr, n))
-    return "sgemm_skinny";
+    return sgemm_skinny_kernel_name(m);
   if (m % kBM == 0 && n % kBN == 0 && k % kBK == 0)
     return "sgemm_mfma_kernel<128,128,32,false>";
   return "sgemm_mfma_kernel<128,128,32,true>";

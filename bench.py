@@ -99,13 +99,42 @@ def bench_gemm(dev, steps, warmup):
             "kernel": lib.bch_sgemm_kernel_name(n, n, n).decode()}, (a, b, c)
 
 
-def bench_extra(dev, reps: int = 20):
+WORKLOADS = ("softmax", "skinny", "batched", "sdpa", "copy")
+
+
+def bench_extra(dev, reps: int = 20, only=None):
     """The other BASELINE configs, each timed over `reps` launches."""
     from barracuda_amd import LcgStream, Tensor
     lib, ctx = dev._lib, dev.ctx
     T = Timer(dev)
     out = {}
+    want = set(only) if only else set(WORKLOADS) - {"copy"}
 
+    if "copy" in want:
+        # known-traffic reference: 512 MiB read + 512 MiB written
+        nb = 512 << 20
+        src = LcgStream(9, dev).uniform([nb // 4])
+        dst = Tensor.empty([nb // 4], dev)
+        ps, pd = C.c_void_p(src.ptr), C.c_void_p(dst.ptr)
+        wall, ev = T.run(lambda i: lib.bch_copy(ctx, pd, ps, nb), reps, 3)
+        out["copy_512MiB"] = {"GB/s": 2 * nb / (ev * 1e-3) / 1e9, "us": ev * 1e3, "bytes_per_launch": 2 * nb,
+                              "hbm_frac": 2 * nb / (ev * 1e-3) / 1e9 / HBM_PEAK_GBS}
+        del src, dst
+    if "softmax" in want:
+        out.update(_bench_softmax(dev, T, reps))
+    if "skinny" in want:
+        out.update(_bench_skinny(dev, T, reps))
+    if "batched" in want:
+        out.update(_bench_batched(dev, T, reps))
+    if "sdpa" in want:
+        out.update(_bench_sdpa(dev, T, reps))
+    return out
+
+
+def _bench_softmax(dev, T, reps):
+    from barracuda_amd import LcgStream, Tensor
+    lib, ctx = dev._lib, dev.ctx
+    out = {}
     # config 2: row softmax [65536 x 2048], N(0,3), seed 1
     x = LcgStream(1, dev).normal([65536, 2048], 0.0, 3.0)
     y = Tensor.empty([65536, 2048], dev)
@@ -115,8 +144,13 @@ def bench_extra(dev, reps: int = 20):
     out["softmax_65536x2048"] = {"GB/s": nbytes / (ev * 1e-3) / 1e9, "kernel_us": ev * 1e3,
                                  "bytes_per_launch": nbytes,
                                  "hbm_frac": nbytes / (ev * 1e-3) / 1e9 / HBM_PEAK_GBS}
-    del x, y
+    return out
 
+
+def _bench_skinny(dev, T, reps):
+    from barracuda_amd import LcgStream, Tensor
+    lib, ctx = dev._lib, dev.ctx
+    out = {}
     # config 4: skinny GEMM M in {1, 8, 32}, K 4096, N 11008; X ~ N(0,1), W ~ N(0,0.02), seed 3.
     # Three weight copies (541 MB > the 256 MB Infinity Cache) are rotated.
     K, N = 4096, 11008
@@ -134,7 +168,13 @@ def bench_extra(dev, reps: int = 20):
                                "hbm_frac": nbytes / (ev * 1e-3) / 1e9 / HBM_PEAK_GBS,
                                "TFLOP/s": 2.0 * m * K * N / (ev * 1e-3) / 1e12}
         del xs, ws, ys
+    return out
 
+
+def _bench_batched(dev, T, reps):
+    from barracuda_amd import LcgStream, Tensor
+    lib, ctx = dev._lib, dev.ctx
+    out = {}
     # config 3b: batched 16 x 1024^3, U[-1,1), seed 2
     s = LcgStream(2, dev)
     a, b = s.uniform([16, 1024, 1024]), s.uniform([16, 1024, 1024])
@@ -146,8 +186,13 @@ def bench_extra(dev, reps: int = 20):
     fl = 2.0 * 16 * 1024 ** 3
     out["batched_16x1024"] = {"TFLOP/s": fl / (ev * 1e-3) / 1e12, "ms": ev,
                               "mfma_frac": fl / (ev * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS}
-    del a, b, c
+    return out
 
+
+def _bench_sdpa(dev, T, reps):
+    from barracuda_amd import LcgStream, Tensor
+    lib, ctx = dev._lib, dev.ctx
+    out = {}
     # config 5: SDPA forward B=4, H=32, S=2048, D=128, N(0,1), seed 4, scale 1/sqrt(128)
     Bb, H, S, D = 4, 32, 2048, 128
     s = LcgStream(4, dev)
@@ -211,6 +256,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="only the headline GEMM")
+    ap.add_argument("--only", default=None,
+                    help="comma list of " + ",".join(("gemm",) + WORKLOADS) + ": time just these "
+                         "(profiling runs); prints their results as the JSON line")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: the hot path here is single-GPU (no collectives); "
@@ -219,6 +267,18 @@ def main() -> int:
 
     from barracuda_amd import get_device
     dev = get_device()
+    if args.only:
+        sel = [w.strip() for w in args.only.split(",") if w.strip()]
+        res = {}
+        if "gemm" in sel:
+            g, keep = bench_gemm(dev, args.steps, args.warmup)
+            res["gemm_4096"] = {"TFLOP/s": g["flops"] / (g["kernel_ms"] * 1e-3) / 1e12, "ms": g["kernel_ms"]}
+            del keep
+        rest = [w for w in sel if w != "gemm"]
+        if rest:
+            res.update(bench_extra(dev, only=rest))
+        print(json.dumps({"only": sel, "results": res}), flush=True)
+        return 0
     log(f"gemm 4096^3: {args.warmup} warmup + {args.steps} timed launches")
     g, keep = bench_gemm(dev, args.steps, args.warmup)
     value = g["flops"] / (g["wall_ms"] * 1e-3) / 1e12

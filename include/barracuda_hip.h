@@ -72,6 +72,10 @@ bch_status bch_free(bch_ctx *ctx, void *dptr);
 bch_status bch_upload(bch_ctx *ctx, void *dst, const void *src, size_t bytes);
 bch_status bch_download(bch_ctx *ctx, void *dst, const void *src, size_t bytes);
 bch_status bch_memset(bch_ctx *ctx, void *dst, int value, size_t bytes);
+/* Device-to-device copy on ctx's stream (no counterpart in GpuBackend, which
+ * copies through upload/download; here it is also the known-traffic kernel
+ * that calibrates the HBM byte counters used to profile the hot path). */
+bch_status bch_copy(bch_ctx *ctx, void *dst, const void *src, size_t bytes);
 /* Wait for all work queued on ctx's stream (submit_and_poll, wgpu_device/
  * submission.rs:143). */
 bch_status bch_sync(bch_ctx *ctx);

@@ -88,8 +88,9 @@ def test_null_and_shape_errors_before_device():
 def test_kernel_routing_names():
     lib = N.load()
     assert lib.bch_sgemm_kernel_name(4096, 4096, 4096) == b"sgemm_mfma_kernel<128,128,32,false>"
-    assert lib.bch_sgemm_kernel_name(1, 11008, 4096) == b"sgemm_skinny"
-    assert lib.bch_sgemm_kernel_name(32, 11008, 4096) == b"sgemm_skinny"
+    assert lib.bch_sgemm_kernel_name(1, 11008, 4096) == b"sgemm_skinny_fma"
+    assert lib.bch_sgemm_kernel_name(8, 11008, 4096) == b"sgemm_skinny_mfma<1>"
+    assert lib.bch_sgemm_kernel_name(32, 11008, 4096) == b"sgemm_skinny_mfma<2>"
     assert lib.bch_sgemm_kernel_name(100, 70, 33) == b"sgemm_mfma_kernel<128,128,32,true>"
 
 

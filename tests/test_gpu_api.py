@@ -78,3 +78,21 @@ def test_alloc_failure_injection_maps_to_out_of_memory():
                        timeout=120)
     assert "OOM" in r.stdout, r.stdout + r.stderr
     assert "injected" in r.stdout
+
+
+def test_device_copy(dev):
+    _say("bch_copy aligned / unaligned")
+    import ctypes as C
+    x = O.Lcg(8).uniform(100003)
+    src = Tensor.from_data(x, [100003], dev)
+    dst = Tensor.empty([100003], dev)
+    dev.check(dev._lib.bch_copy(dev.ctx, C.c_void_p(dst.ptr), C.c_void_p(src.ptr), 4 * 100000), "copy")
+    got = dst.to_vec()
+    assert np.array_equal(got[:100000], x[:100000])
+    dst2 = Tensor.empty([100003], dev)
+    dev.check(dev._lib.bch_copy(dev.ctx, C.c_void_p(dst2.ptr + 4), C.c_void_p(src.ptr + 8), 4 * 99990 + 3),
+              "copy")
+    got2 = dst2.to_vec()
+    assert np.array_equal(got2[1:99991], x[2:99992])
+    assert got2.view(np.uint8)[4 + 4 * 99990: 4 + 4 * 99990 + 3].tolist() == \
+        x.view(np.uint8)[8 + 4 * 99990: 8 + 4 * 99990 + 3].tolist()

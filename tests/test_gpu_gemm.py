@@ -89,6 +89,33 @@ def test_skinny_decode_shapes(dev, m):
     assert err <= TOL
 
 
+@pytest.mark.parametrize("m,n,k", [(1, 4, 1), (3, 12, 37), (4, 260, 1000), (5, 8, 3), (9, 1028, 333),
+                                   (16, 4096, 4100), (17, 300, 77), (31, 1024, 5000), (32, 11008, 129)])
+def test_skinny_ragged(dev, m, n, k):
+    _say(f"skinny ragged m={m} n={n} k={k}")
+    rng = O.Lcg(m * 100 + n + k)
+    a = rng.normal((m, k))
+    b = rng.normal((k, n), 0.0, 0.02)
+    assert O.max_rel_err(_mm(dev, a, b), O.matmul_f64(a, b)) <= TOL
+
+
+def test_skinny_repeated_calls_and_unaligned_a(dev):
+    _say("skinny repeated calls / unaligned A")
+    rng = O.Lcg(99)
+    a = rng.normal((9, 640))
+    b = rng.normal((640, 512))
+    ref = O.matmul_f64(a, b)
+    tb = Tensor.from_data(b, [640, 512], dev)
+    ta = Tensor.from_data(np.concatenate([[0.0], a.reshape(-1)]).astype(np.float32), [1 + a.size], dev)
+    for _ in range(3):  # workspace reuse across calls of different shapes
+        tc = Tensor.empty([9, 512], dev)
+        dev.check(dev._lib.bch_sgemm(dev.ctx, 9, 512, 640, C.c_void_p(ta.ptr + 4), 640, C.c_void_p(tb.ptr), 512,
+                                     C.c_void_p(tc.ptr), 512), "sgemm")
+        assert O.max_rel_err(tc.to_numpy(), ref) <= TOL
+        small = _mm(dev, a[:2, :100].copy(), b[:100, :8].copy())
+        assert O.max_rel_err(small, O.matmul_f64(a[:2, :100].copy(), b[:100, :8].copy())) <= TOL
+
+
 def test_leading_dimensions_and_unaligned(dev):
     _say("sgemm with lda/ldb/ldc > natural and an odd offset")
     m, n, k = 96, 160, 72
