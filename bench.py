@@ -143,7 +143,8 @@ def _bench_softmax(dev, T, reps):
     nbytes = 2 * 4 * 65536 * 2048
     out["softmax_65536x2048"] = {"GB/s": nbytes / (ev * 1e-3) / 1e9, "kernel_us": ev * 1e3,
                                  "bytes_per_launch": nbytes,
-                                 "hbm_frac": nbytes / (ev * 1e-3) / 1e9 / HBM_PEAK_GBS}
+                                 "hbm_frac": nbytes / (ev * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                                 "traffic": load_traffic("softmax_65536x2048")}
     return out
 
 
