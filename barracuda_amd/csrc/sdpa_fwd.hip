@@ -14,7 +14,8 @@
 // Design (FP32 MFMA for both products, v_mfma_f32_32x32x2_f32):
 //   * A workgroup = 4 wavefronts = 128 queries of one (b,h); wavefront w owns
 //     queries q0 + 32w .. +31, lane l's query is l % 32.  Key blocks of 32 are
-//     streamed through LDS, double-buffered, one barrier per block.
+//     streamed through LDS, double-buffered, one barrier per block; the next
+//     block's global loads are issued before the current block's MFMAs.
 //   * Scores are computed transposed, S^T = K Q^T (32 keys x 32 queries), so
 //     each lane holds 16 scores of ITS query: the row max and row sum are
 //     in-lane plus one exchange between the two lane halves.  The q operand
@@ -25,12 +26,16 @@
 //     is key 8(r/4) + 4(l/32) + r%4), so P never leaves registers.  V is
 //     stored transposed in LDS ([d][key]) so the A operand is one 128-bit
 //     LDS read per four MFMAs; K is stored [key][d] for the same reason.
-//   * Online softmax (running max m and sum l per query, O rescaled by
-//     2^(m_old - m_new)); the final O is divided by l.
+//   * Online softmax with a lazily moved reference max: exponentials are
+//     taken against a per-query reference m_ref, which only moves (and O and
+//     the running sum are only rescaled) when a block's max exceeds it by
+//     more than 2^8.  Every term stays <= 256 and the final O / l is exact
+//     algebra, so accuracy is unchanged while the rescale of the 64-value O
+//     accumulator -- the costliest vector work per block -- almost never runs.
 //   * Causal: key blocks past the workgroup's last query are not loaded;
 //     blocks entirely above a wavefront's diagonal are skipped by that
 //     wavefront; the diagonal block is masked per element.  Workgroups are
-//     issued longest-first.
+//     issued longest first across all heads (query block major).
 #include "bch_internal.h"
 
 #include <math.h>
@@ -43,10 +48,12 @@ constexpr int kBQ = 128;  // queries per workgroup
 constexpr int kBKV = 32;  // keys per block
 constexpr int kVLD = kBKV + 4;
 constexpr float kLog2E = 1.44269504088896340736f;
+constexpr float kLazy = 8.0f;  // log2 headroom before the reference max moves
 
 template <int DP>
 struct SdpaCfg {
   static constexpr int KLD = DP + 4;
+  static constexpr int KD4 = DP / 4;                   // float4 per K row
   static constexpr int K_F4 = kBKV * DP / 4 / 256;     // float4 of K per thread
   static constexpr int V_BLK = kBKV * DP / 16;          // 4x4 V blocks per tile
   static constexpr int LDS_FLOATS = 2 * (kBKV * KLD + DP * kVLD);
@@ -54,10 +61,69 @@ struct SdpaCfg {
 };
 
 template <int DP, bool FULL>
-__global__ __launch_bounds__(256) void sdpa_fwd_kernel(
-    int Sq, int Skv, int D, float qscale, int causal, const float* __restrict__ q,
-    const float* __restrict__ k, const float* __restrict__ v, float* __restrict__ o,
-    int qblocks) {
+__device__ __forceinline__ void load_k(const float* __restrict__ kh, int Skv, int D, int kb, int tid,
+                                       float4 (&rk)[SdpaCfg<DP>::K_F4]) {
+  using G = SdpaCfg<DP>;
+#pragma unroll
+  for (int f = 0; f < G::K_F4; ++f) {
+    const int idx = tid + f * 256;
+    const int key = idx / G::KD4, d0 = (idx % G::KD4) * 4;
+    const int gk = kb + key;
+    if (FULL) {
+      rk[f] = *reinterpret_cast<const float4*>(kh + (long long)gk * D + d0);
+    } else {
+      float t[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) t[e] = (gk < Skv && d0 + e < D) ? kh[(long long)gk * D + d0 + e] : 0.0f;
+      rk[f] = make_float4(t[0], t[1], t[2], t[3]);
+    }
+  }
+}
+
+template <int DP, bool FULL>
+__device__ __forceinline__ void load_v(const float* __restrict__ vh, int Skv, int D, int kb, int tid,
+                                       float4 (&rv)[4]) {
+  using G = SdpaCfg<DP>;
+  const int blk = tid < G::V_BLK ? tid : 0;  // threads past the tile reload block 0 (unused)
+  const int kq = blk / G::KD4, dq = blk % G::KD4;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int gk = kb + 4 * kq + e, d0 = 4 * dq;
+    if (FULL) {
+      rv[e] = *reinterpret_cast<const float4*>(vh + (long long)gk * D + d0);
+    } else {
+      float t[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) t[c] = (gk < Skv && d0 + c < D) ? vh[(long long)gk * D + d0 + c] : 0.0f;
+      rv[e] = make_float4(t[0], t[1], t[2], t[3]);
+    }
+  }
+}
+
+template <int DP>
+__device__ __forceinline__ void store_kv(float* __restrict__ ks, float* __restrict__ vt, int tid,
+                                         const float4 (&rk)[SdpaCfg<DP>::K_F4], const float4 (&rv)[4]) {
+  using G = SdpaCfg<DP>;
+#pragma unroll
+  for (int f = 0; f < G::K_F4; ++f) {
+    const int idx = tid + f * 256;
+    const int key = idx / G::KD4, d0 = (idx % G::KD4) * 4;
+    *reinterpret_cast<float4*>(ks + key * G::KLD + d0) = rk[f];
+  }
+  if (tid < G::V_BLK) {
+    const int kq = tid / G::KD4, dq = tid % G::KD4;
+    float* base = vt + (4 * dq) * kVLD + 4 * kq;
+    *reinterpret_cast<float4*>(base + 0 * kVLD) = make_float4(rv[0].x, rv[1].x, rv[2].x, rv[3].x);
+    *reinterpret_cast<float4*>(base + 1 * kVLD) = make_float4(rv[0].y, rv[1].y, rv[2].y, rv[3].y);
+    *reinterpret_cast<float4*>(base + 2 * kVLD) = make_float4(rv[0].z, rv[1].z, rv[2].z, rv[3].z);
+    *reinterpret_cast<float4*>(base + 3 * kVLD) = make_float4(rv[0].w, rv[1].w, rv[2].w, rv[3].w);
+  }
+}
+
+template <int DP, bool FULL>
+__global__ __launch_bounds__(256, 2) void sdpa_fwd_kernel(
+    int BH, int Sq, int Skv, int D, float qscale, int causal, const float* __restrict__ q,
+    const float* __restrict__ k, const float* __restrict__ v, float* __restrict__ o, int qblocks) {
   using G = SdpaCfg<DP>;
   constexpr int KLD = G::KLD;
   extern __shared__ float4 smem4[];
@@ -65,9 +131,10 @@ __global__ __launch_bounds__(256) void sdpa_fwd_kernel(
   float* Ks = smem;                        // [2][kBKV][KLD]
   float* Vt = smem + 2 * kBKV * KLD;       // [2][DP][kVLD]
 
-  int qb = blockIdx.x % qblocks;
-  const int bh = blockIdx.x / qblocks;
-  if (causal) qb = qblocks - 1 - qb;  // longest rows first
+  // query-block major: all heads' longest (causal) query blocks go first
+  const int qi = blockIdx.x / BH;
+  const int bh = blockIdx.x % BH;
+  const int qb = causal ? qblocks - 1 - qi : qi;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -91,87 +158,36 @@ __global__ __launch_bounds__(256) void sdpa_fwd_kernel(
       t[0] = x.x; t[1] = x.y; t[2] = x.z; t[3] = x.w;
     } else {
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        t[e] = (myq < Sq && d0 + e < D) ? qh[(long long)myq * D + d0 + e] : 0.0f;
+      for (int e = 0; e < 4; ++e) t[e] = (myq < Sq && d0 + e < D) ? qh[(long long)myq * D + d0 + e] : 0.0f;
     }
     qf[c] = make_float4(t[0] * qscale, t[1] * qscale, t[2] * qscale, t[3] * qscale);
   }
-
-  // ---- key/value tile staging ----
-  float4 rk[G::K_F4];
-  float4 rv[4];
-  constexpr int KD4 = DP / 4;  // float4 per K row
-  auto load_kv = [&](int kb) {
-#pragma unroll
-    for (int f = 0; f < G::K_F4; ++f) {
-      const int idx = tid + f * 256;
-      const int key = idx / KD4, d0 = (idx % KD4) * 4;
-      const int gk = kb + key;
-      if (FULL) {
-        rk[f] = *reinterpret_cast<const float4*>(kh + (long long)gk * D + d0);
-      } else {
-        float t[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) t[e] = (gk < Skv && d0 + e < D) ? kh[(long long)gk * D + d0 + e] : 0.0f;
-        rk[f] = make_float4(t[0], t[1], t[2], t[3]);
-      }
-    }
-    if (tid < G::V_BLK) {
-      const int kq = tid / KD4, dq = tid % KD4;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int gk = kb + 4 * kq + e, d0 = 4 * dq;
-        if (FULL) {
-          rv[e] = *reinterpret_cast<const float4*>(vh + (long long)gk * D + d0);
-        } else {
-          float t[4];
-#pragma unroll
-          for (int c = 0; c < 4; ++c) t[c] = (gk < Skv && d0 + c < D) ? vh[(long long)gk * D + d0 + c] : 0.0f;
-          rv[e] = make_float4(t[0], t[1], t[2], t[3]);
-        }
-      }
-    }
-  };
-  auto store_kv = [&](int buf) {
-    float* ks = Ks + buf * kBKV * KLD;
-    float* vt = Vt + buf * DP * kVLD;
-#pragma unroll
-    for (int f = 0; f < G::K_F4; ++f) {
-      const int idx = tid + f * 256;
-      const int key = idx / KD4, d0 = (idx % KD4) * 4;
-      *reinterpret_cast<float4*>(ks + key * KLD + d0) = rk[f];
-    }
-    if (tid < G::V_BLK) {
-      const int kq = tid / KD4, dq = tid % KD4;
-      float* base = vt + (4 * dq) * kVLD + 4 * kq;
-      *reinterpret_cast<float4*>(base + 0 * kVLD) = make_float4(rv[0].x, rv[1].x, rv[2].x, rv[3].x);
-      *reinterpret_cast<float4*>(base + 1 * kVLD) = make_float4(rv[0].y, rv[1].y, rv[2].y, rv[3].y);
-      *reinterpret_cast<float4*>(base + 2 * kVLD) = make_float4(rv[0].z, rv[1].z, rv[2].z, rv[3].z);
-      *reinterpret_cast<float4*>(base + 3 * kVLD) = make_float4(rv[0].w, rv[1].w, rv[2].w, rv[3].w);
-    }
-  };
 
   f32x16 oacc[DP / 32];
 #pragma unroll
   for (int b = 0; b < DP / 32; ++b)
 #pragma unroll
     for (int r = 0; r < 16; ++r) oacc[b][r] = 0.0f;
-  float m_run = -INFINITY, l_run = 0.0f;
+  float m_ref = -INFINITY, l_run = 0.0f;
 
   int kend = Skv;
   if (causal) kend = min(Skv, qb * kBQ + kBQ);
   const int nkb = (kend + kBKV - 1) / kBKV;
 
-  if (nkb > 0) {
-    load_kv(0);
-    store_kv(0);
-  }
+  float4 rk[G::K_F4];
+  float4 rv[4];
+  load_k<DP, FULL>(kh, Skv, D, 0, tid, rk);
+  load_v<DP, FULL>(vh, Skv, D, 0, tid, rv);
+  store_kv<DP>(Ks, Vt, tid, rk, rv);
   __syncthreads();
 
   for (int t = 0; t < nkb; ++t) {
     const int cur = t & 1;
     const int kb = t * kBKV;
-    if (t + 1 < nkb) load_kv(kb + kBKV);
+    // next block (the last iteration reloads the last block; never read)
+    const int kbn = min(t + 1, nkb - 1) * kBKV;
+    load_k<DP, FULL>(kh, Skv, D, kbn, tid, rk);
+    load_v<DP, FULL>(vh, Skv, D, kbn, tid, rv);
 
     // wave-uniform: skip blocks fully above this wavefront's diagonal and
     // wavefronts whose queries are all past Sq
@@ -202,9 +218,19 @@ __global__ __launch_bounds__(256) void sdpa_fwd_kernel(
 #pragma unroll
       for (int r = 1; r < 16; ++r) bm = fmaxf(bm, s[r]);
       bm = fmaxf(bm, __shfl_xor(bm, 32));
-      const float m_new = fmaxf(m_run, bm);
-      const float m_use = (m_new == -INFINITY) ? 0.0f : m_new;
-      const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+      // move the reference max only when this block exceeds it by > 2^kLazy
+      const bool move = bm > m_ref + kLazy;  // -inf reference: any finite block max moves it
+      if (__any(move)) {
+        const float m_new = move ? bm : m_ref;
+        const float alpha = (m_ref == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m_ref - m_new);
+        l_run *= alpha;
+#pragma unroll
+        for (int b = 0; b < DP / 32; ++b)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) oacc[b][r] *= alpha;
+        m_ref = m_new;
+      }
+      const float m_use = (m_ref == -INFINITY) ? 0.0f : m_ref;
       float rs = 0.0f;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
@@ -212,12 +238,7 @@ __global__ __launch_bounds__(256) void sdpa_fwd_kernel(
         rs += s[r];
       }
       rs += __shfl_xor(rs, 32);
-      l_run = l_run * alpha + rs;
-      m_run = m_new;
-#pragma unroll
-      for (int b = 0; b < DP / 32; ++b)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) oacc[b][r] *= alpha;
+      l_run += rs;
 
       const float* vs = Vt + cur * DP * kVLD + li * kVLD + 4 * lh;
 #pragma unroll
@@ -232,7 +253,7 @@ __global__ __launch_bounds__(256) void sdpa_fwd_kernel(
         }
       }
     }
-    if (t + 1 < nkb) store_kv(cur ^ 1);
+    store_kv<DP>(Ks + (cur ^ 1) * kBKV * KLD, Vt + (cur ^ 1) * DP * kVLD, tid, rk, rv);
     __syncthreads();
   }
 
@@ -265,7 +286,7 @@ hipError_t launch_dp(hipStream_t s, int B, int H, int Sq, int Skv, int D, float 
     if (e != hipSuccess) return e;
     attr_set = true;
   }
-  hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), lds, s, Sq, Skv, D, scale * kLog2E,
+  hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), lds, s, B * H, Sq, Skv, D, scale * kLog2E,
                      causal, q, k, v, o, qblocks);
   return hipGetLastError();
 }
