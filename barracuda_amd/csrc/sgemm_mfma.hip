@@ -19,8 +19,9 @@
 //     B as well, B tiles are stored k-contiguous ([n][k]) in LDS: each thread
 //     loads a 4(k) x 4(n) block with four 128-bit global loads and writes it
 //     transposed with four 128-bit LDS stores.
-//   * Block tile BM x BN x BK, four wavefronts in a 2x2 grid, each owning a
-//     (BM/2) x (BN/2) sub-tile of (BM/64) x (BN/64) MFMA blocks.  LDS rows
+//   * Block tile BM x BN x BK (256x256, 256x128 or 128x128 by shape, see
+//     pick_tile), four wavefronts in a 2x2 grid, each owning a (BM/2) x (BN/2)
+//     sub-tile of (BM/64) x (BN/64) MFMA blocks.  LDS rows
 //     are padded by 4 floats so the 128-bit reads of 32 consecutive rows do
 //     not collide on banks.  LDS is double-buffered: the global loads of
 //     tile t+1 are issued before the MFMAs of tile t and land in registers,
@@ -263,12 +264,51 @@ hipError_t launch_tiles(hipStream_t s, int batch, int m, int n, int k,
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
-constexpr int kBM = 128, kBN = 128, kBK = 32;
+constexpr int kBK = 32;
+constexpr int kNumCU = 256;  // MI355X
 
-bool fast_ok(int m, int n, int k, const float* A, int lda, long long sA,
-             const float* B, int ldb, long long sB) {
-  return m % kBM == 0 && n % kBN == 0 && k % kBK == 0 && lda % 4 == 0 &&
-         ldb % 4 == 0 && sA % 4 == 0 && sB % 4 == 0 && aligned16(A) && aligned16(B);
+// Tile choice: the largest block tile that still gives every CU at least
+// one tile.  Measured on MI355X (f32, TFLOP/s): 4096^3 -- 128x128 108,
+// 256x128 125, 256x256 132; 16 x 1024^3 -- 109 / 120 / 126; 2048^3 --
+// 113 / 62 / 33 (too few tiles for the larger shapes).
+enum class Tile { k256x256, k256x128, k128x128 };
+
+Tile pick_tile(int batch, int m, int n) {
+  const long long t256 = (long long)batch * ((m + 255) / 256) * ((n + 255) / 256);
+  if (t256 >= kNumCU) return Tile::k256x256;
+  const long long t256x128 = (long long)batch * ((m + 255) / 256) * ((n + 127) / 128);
+  if (t256x128 >= kNumCU) return Tile::k256x128;
+  return Tile::k128x128;
+}
+
+int tile_m(Tile t) { return t == Tile::k128x128 ? 128 : 256; }
+int tile_n(Tile t) { return t == Tile::k256x256 ? 256 : 128; }
+
+bool fast_ok(Tile t, int m, int n, int k, const float* A, int lda, long long sA, const float* B, int ldb,
+             long long sB) {
+  return m % tile_m(t) == 0 && n % tile_n(t) == 0 && k % kBK == 0 && lda % 4 == 0 && ldb % 4 == 0 &&
+         sA % 4 == 0 && sB % 4 == 0 && aligned16(A) && aligned16(B);
+}
+
+template <bool CHECK>
+hipError_t launch_tile(Tile t, hipStream_t s, int batch, int m, int n, int k, const float* A, int lda,
+                       long long sA, const float* B, int ldb, long long sB, float* C, int ldc, long long sC) {
+  switch (t) {
+    case Tile::k256x256:
+      return launch_tiles<256, 256, kBK, CHECK>(s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC);
+    case Tile::k256x128:
+      return launch_tiles<256, 128, kBK, CHECK>(s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC);
+    default:
+      return launch_tiles<128, 128, kBK, CHECK>(s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC);
+  }
+}
+
+const char* tile_name(Tile t, bool check) {
+  switch (t) {
+    case Tile::k256x256: return check ? "sgemm_mfma_kernel<256,256,32,true>" : "sgemm_mfma_kernel<256,256,32,false>";
+    case Tile::k256x128: return check ? "sgemm_mfma_kernel<256,128,32,true>" : "sgemm_mfma_kernel<256,128,32,false>";
+    default: return check ? "sgemm_mfma_kernel<128,128,32,true>" : "sgemm_mfma_kernel<128,128,32,false>";
+  }
 }
 
 }  // namespace
@@ -278,9 +318,9 @@ namespace bch {
 const char* sgemm_kernel_name(int m, int n, int k) {
   if (m <= 32 && sgemm_skinny_applies(m, n, k, nullptr, k, nullptr, n))
     return sgemm_skinny_kernel_name(m);
-  if (m % kBM == 0 && n % kBN == 0 && k % kBK == 0)
-    return "sgemm_mfma_kernel<128,128,32,false>";
-  return "sgemm_mfma_kernel<128,128,32,true>";
+  const Tile t = pick_tile(1, m, n);
+  const bool check = !(m % tile_m(t) == 0 && n % tile_n(t) == 0 && k % kBK == 0 && k % 4 == 0 && n % 4 == 0);
+  return tile_name(t, check);
 }
 
 size_t sgemm_workspace_bytes(int batch, int m, int n, int k) {
@@ -289,16 +329,16 @@ size_t sgemm_workspace_bytes(int batch, int m, int n, int k) {
   return 0;
 }
 
-hipError_t launch_sgemm(hipStream_t s, int batch, int m, int n, int k,
-                        const float* A, int lda, long long sA, const float* B,
-                        int ldb, long long sB, float* C, int ldc, long long sC,
-                        void* ws, size_t ws_bytes) {
+hipError_t launch_sgemm(hipStream_t s, int batch, int m, int n, int k, const float* A, int lda, long long sA,
+                        const float* B, int ldb, long long sB, float* C, int ldc, long long sC, void* ws,
+                        size_t ws_bytes) {
   if (batch <= 0 || m <= 0 || n <= 0) return hipSuccess;
   if (batch == 1 && sgemm_skinny_applies(m, n, k, A, lda, B, ldb))
     return launch_sgemm_skinny(s, m, n, k, A, lda, B, ldb, C, ldc, ws, ws_bytes);
-  if (fast_ok(m, n, k, A, lda, sA, B, ldb, sB))
-    return launch_tiles<kBM, kBN, kBK, false>(s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC);
-  return launch_tiles<kBM, kBN, kBK, true>(s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC);
+  const Tile t = pick_tile(batch, m, n);
+  if (fast_ok(t, m, n, k, A, lda, sA, B, ldb, sB))
+    return launch_tile<false>(t, s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC);
+  return launch_tile<true>(t, s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC);
 }
 
 }  // namespace bch

@@ -138,6 +138,20 @@ def test_leading_dimensions_and_unaligned(dev):
     assert O.max_rel_err(tc2.to_numpy(), ref) <= TOL
 
 
+@pytest.mark.parametrize("m,n,k", [(3072, 3072, 512), (4100, 4096, 300), (2048, 2048, 96), (4096, 3968, 64)])
+def test_large_tile_paths(dev, m, n, k):
+    """The 256x256 / 256x128 block tiles, aligned and ragged (sampled rows vs f64)."""
+    _say(f"sgemm large tiles m={m} n={n} k={k} ({dev._lib.bch_sgemm_kernel_name(m, n, k).decode()})")
+    rng = O.Lcg(m + n + k)
+    a = rng.uniform((m, k))
+    b = rng.uniform((k, n))
+    got = _mm(dev, a, b)
+    rows = [0, 1, 255, 256, m // 2, m - 2, m - 1]
+    assert O.max_rel_err(got[rows], O.matmul_f64(a, b, rows=rows)) <= TOL
+    cols = [0, 127, 128, 255, 256, n - 1]
+    assert O.max_rel_err(got[:, cols], a.astype(np.float64) @ b[:, cols].astype(np.float64)) <= TOL
+
+
 def test_config_4096_cubed(dev):
     """BASELINE config 3a: 4096^3, U[-1,1), seed 2; f64 oracle on sampled rows."""
     _say("sgemm 4096^3 seed 2")
