@@ -206,7 +206,9 @@ __global__ __launch_bounds__(256) void sgemm_skinny_mfma(int M, int N, int K, co
       }
 }
 
-// C[m][n] = sum over splits s, in order, of P[s][m][n]
+// C[m][n] = sum over splits s, in split order, of P[s][m][n]; one thread per
+// output element (measured faster than float4-per-thread variants here: the
+// partials were just written by other XCDs and the loads are latency-bound).
 __global__ __launch_bounds__(256) void sgemm_skinny_reduce(int M, int N, const float* __restrict__ P,
                                                            int splits, float* __restrict__ C, int ldc) {
   const long long t = (long long)blockIdx.x * 256 + threadIdx.x;

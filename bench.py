@@ -167,7 +167,8 @@ def _bench_skinny(dev, T, reps):
         out[f"skinny_m{m}"] = {"GB/s": nbytes / (ev * 1e-3) / 1e9, "us": ev * 1e3,
                                "bytes_per_call": nbytes,
                                "hbm_frac": nbytes / (ev * 1e-3) / 1e9 / HBM_PEAK_GBS,
-                               "TFLOP/s": 2.0 * m * K * N / (ev * 1e-3) / 1e12}
+                               "TFLOP/s": 2.0 * m * K * N / (ev * 1e-3) / 1e12,
+                               "traffic_main_kernel": load_traffic(f"skinny_m{m}")}
         del xs, ws, ys
     return out
 
@@ -186,7 +187,8 @@ def _bench_batched(dev, T, reps):
                                                               pc, mm), reps, 3)
     fl = 2.0 * 16 * 1024 ** 3
     out["batched_16x1024"] = {"TFLOP/s": fl / (ev * 1e-3) / 1e12, "ms": ev,
-                              "mfma_frac": fl / (ev * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS}
+                              "mfma_frac": fl / (ev * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS,
+                              "traffic": load_traffic("sgemm_batched_16x1024")}
     return out
 
 
@@ -207,7 +209,8 @@ def _bench_sdpa(dev, T, reps):
         fl = 4.0 * Bb * H * S * S * D if not causal else 4.0 * Bb * H * (S * (S + 1) / 2) * D
         key = "sdpa_causal" if causal else "sdpa_noncausal"
         out[key] = {"ms": ev, "TFLOP/s": fl / (ev * 1e-3) / 1e12,
-                    "mfma_frac": fl / (ev * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS}
+                    "mfma_frac": fl / (ev * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS,
+                    "traffic_avg_causal_and_not": load_traffic("sdpa_b4h32s2048d128")}
     del q, k, v, o
     return out
 
