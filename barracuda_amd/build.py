@@ -7,6 +7,7 @@ Outputs (git-ignored, shipped with the tree):
     barracuda_amd/lib/libbarracuda_hip.so
     barracuda_amd/lib/bch_softmax_rows.hsaco
     oracle/libbc_oracle.so                  (test infrastructure only)
+    tests/cpp/bch_host_tests                (C++ host-API tests)
 """
 from __future__ import annotations
 
@@ -76,6 +77,17 @@ def build_hip(verbose: bool = True) -> Path:
     return so
 
 
+def build_host_tests(verbose: bool = True) -> Path:
+    """The C++ host-API tests (tests/cpp/test_ops.cpp) against include/barracuda_hip_ops.hpp."""
+    exe = ROOT / "tests" / "cpp" / "bch_host_tests"
+    _run(["g++", "-std=c++17", "-O2", "-Wall", "-Wextra", f"-I{ROOT / 'include'}",
+          str(ROOT / "tests" / "cpp" / "test_ops.cpp"), f"-L{LIB}", "-lbarracuda_hip",
+          "-Wl,-rpath,$ORIGIN/../../barracuda_amd/lib", "-o", str(exe)])
+    if verbose:
+        print(f"built {exe.relative_to(ROOT)}")
+    return exe
+
+
 def build_oracle(verbose: bool = True) -> Path:
     odir = ROOT / "oracle"
     _run(["make", "-s", "-B", "-C", str(odir)])
@@ -88,6 +100,7 @@ def build_oracle(verbose: bool = True) -> Path:
 def build_all(verbose: bool = True) -> None:
     build_oracle(verbose)
     build_hip(verbose)
+    build_host_tests(verbose)
 
 
 if __name__ == "__main__":

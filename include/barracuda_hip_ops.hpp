@@ -1,0 +1,468 @@
+// barracuda_hip_ops.hpp -- C++17 host API over libbarracuda_hip (barracuda_hip.h).
+//
+// Mirrors the reference's Rust op surface for the dense ML-ops hot path
+// (ecoPrimals/barraCuda, paths relative to crates/barracuda/src/): the same
+// method names, argument meaning, validation order and error variants, so
+// that code and tests written against the reference read the same here.
+//
+//   Tensor::{from_data, from_vec_on, shape, len, to_vec}   tensor/mod.rs:185, 347, 409, 448
+//   Tensor::matmul / matmul_ref, MatMul                    ops/matmul.rs:49-243
+//   Tensor::matmul_tiled, MatmulTiled                      ops/matmul_tiled.rs:45-171
+//   Tensor::batch_matmul, BatchMatMul                      ops/batch_matmul.rs:24-163
+//   Tensor::softmax, Softmax (global)                      ops/softmax.rs:31-144
+//   Tensor::softmax_dim                                    ops/tensor_axis_ops.rs:67-126
+//   Tensor::attention, Attention                           ops/attention/mod.rs:84-206
+//   Tensor::scaled_dot_product_attention                   ops/scaled_dot_product_attention/mod.rs:81-226
+//   Tensor::causal_attention, CausalAttention              ops/causal_attn/mod.rs:64-158
+//   FlashAttention                                         ops/flash_attention.rs:45-146
+//   BarracudaError, Result<T>                              error.rs:14-130
+//
+// Every computation goes through the C ABI to the gfx950 kernels; there is
+// no host fallback.  Shape validation happens here, before any device call,
+// exactly where the reference does it.  Errors are values (Result<T>), as in
+// Rust; unwrap() on an error throws std::runtime_error with the message.
+#pragma once
+
+#include <cmath>
+#include <cstddef>
+#include <cstdint>
+#include <memory>
+#include <mutex>
+#include <optional>
+#include <sstream>
+#include <stdexcept>
+#include <string>
+#include <utility>
+#include <variant>
+#include <vector>
+
+#include "barracuda_hip.h"
+
+namespace barracuda {
+
+// ---------------------------------------------------------------- errors
+enum class ErrorKind {
+  Device,                // error.rs Device(String)
+  ShapeMismatch,         // ShapeMismatch{expected, actual}
+  InvalidOperation,      // InvalidOperation{op, reason}
+  InvalidInput,          // InvalidInput{message}
+  OutOfMemory,           // OutOfMemory(String)
+  ExecutionError,        // ExecutionError{message}
+  UnsupportedOperation,  // UnsupportedOperation{op, device}
+  DeviceLost,            // DeviceLost(String)
+};
+
+inline std::string shape_str(const std::vector<size_t>& s) {
+  std::ostringstream o;
+  o << '[';
+  for (size_t i = 0; i < s.size(); ++i) o << (i ? ", " : "") << s[i];
+  o << ']';
+  return o.str();
+}
+
+struct BarracudaError {
+  ErrorKind kind;
+  std::string message;  // rendered as the reference's #[error(...)] strings
+
+  static BarracudaError shape_mismatch(const std::vector<size_t>& expected, const std::vector<size_t>& actual) {
+    return {ErrorKind::ShapeMismatch,
+            "Shape mismatch: expected " + shape_str(expected) + ", got " + shape_str(actual)};
+  }
+  static BarracudaError invalid_op(const std::string& op, const std::string& reason) {
+    return {ErrorKind::InvalidOperation, "Invalid operation: " + op + " - " + reason};
+  }
+  static BarracudaError invalid_input(const std::string& msg) {
+    return {ErrorKind::InvalidInput, "Invalid input: " + msg};
+  }
+  static BarracudaError device(const std::string& msg) { return {ErrorKind::Device, "Device error: " + msg}; }
+  static BarracudaError unsupported(const std::string& op, const std::string& dev) {
+    return {ErrorKind::UnsupportedOperation, "Operation not supported on device: " + op + " on " + dev};
+  }
+  // bch_status -> variant (same table as INTEGRATION.md section 3)
+  static BarracudaError from_status(bch_status st, const std::string& detail, const std::string& op) {
+    switch (st) {
+      case BCH_E_INVALID: return invalid_input(detail);
+      case BCH_E_SHAPE: return invalid_op(op, "shape/dimension mismatch: " + detail);
+      case BCH_E_OOM: return {ErrorKind::OutOfMemory, "Out of memory: " + detail};
+      case BCH_E_LAUNCH: return {ErrorKind::ExecutionError, "Execution error: " + detail};
+      case BCH_E_UNSUPPORTED: return unsupported(op, "hip:gfx950 (" + detail + ")");
+      default: return device(detail);
+    }
+  }
+};
+
+template <class T>
+class Result {
+ public:
+  Result(T v) : v_(std::move(v)) {}                   // NOLINT: implicit like Ok(..)
+  Result(BarracudaError e) : v_(std::move(e)) {}      // NOLINT: implicit like Err(..)
+  bool is_ok() const { return v_.index() == 0; }
+  bool is_err() const { return v_.index() == 1; }
+  const BarracudaError& error() const { return std::get<1>(v_); }
+  T& value() { return std::get<0>(v_); }
+  T unwrap() && {
+    if (is_err()) throw std::runtime_error(error().message);
+    return std::move(std::get<0>(v_));
+  }
+  T unwrap() & {
+    if (is_err()) throw std::runtime_error(error().message);
+    return std::get<0>(v_);
+  }
+
+ private:
+  std::variant<T, BarracudaError> v_;
+};
+
+// ---------------------------------------------------------------- device
+// One bch_ctx (device + stream): the device half of GpuBackend
+// (device/backend.rs:244-444).  Calls are serialised: a context is not
+// re-entrant.
+class HipDevice {
+ public:
+  static Result<std::shared_ptr<HipDevice>> create(int ordinal = -1) {
+    bch_ctx* ctx = nullptr;
+    const bch_status st = bch_ctx_create(ordinal, nullptr, &ctx);
+    if (st != BCH_OK) return BarracudaError::from_status(st, bch_last_error(nullptr), "device");
+    return std::shared_ptr<HipDevice>(new HipDevice(ctx));
+  }
+  ~HipDevice() { bch_ctx_destroy(ctx_); }
+  HipDevice(const HipDevice&) = delete;
+  HipDevice& operator=(const HipDevice&) = delete;
+
+  std::string name() const { return "hip:gfx950"; }
+  bch_ctx* ctx() const { return ctx_; }
+  std::mutex& mutex() { return mu_; }
+  std::optional<BarracudaError> check(bch_status st, const std::string& op) const {
+    if (st == BCH_OK) return std::nullopt;
+    return BarracudaError::from_status(st, bch_last_error(ctx_), op);
+  }
+
+ private:
+  explicit HipDevice(bch_ctx* c) : ctx_(c) {}
+  bch_ctx* ctx_;
+  std::mutex mu_;
+};
+
+namespace detail {
+// Owned device allocation (RAII bch_free), shared between Tensor clones.
+struct DeviceBuffer {
+  std::shared_ptr<HipDevice> dev;
+  void* ptr = nullptr;
+  size_t bytes = 0;
+  ~DeviceBuffer() {
+    if (ptr) {
+      std::lock_guard<std::mutex> g(dev->mutex());
+      bch_free(dev->ctx(), ptr);
+    }
+  }
+};
+
+inline size_t numel(const std::vector<size_t>& s) {
+  size_t n = 1;
+  for (size_t d : s) n *= d;
+  return n;
+}
+}  // namespace detail
+
+// ---------------------------------------------------------------- tensor
+class Tensor {
+ public:
+  // tensor/mod.rs:185 from_data: upload f32 data with a shape
+  static Result<Tensor> from_data(const std::vector<float>& data, std::vector<size_t> shape,
+                                  const std::shared_ptr<HipDevice>& dev) {
+    if (data.size() != detail::numel(shape))
+      return BarracudaError::shape_mismatch({detail::numel(shape)}, {data.size()});
+    auto r = empty(std::move(shape), dev);
+    if (r.is_err()) return r;
+    Tensor t = std::move(r).unwrap();
+    if (!data.empty()) {
+      std::lock_guard<std::mutex> g(dev->mutex());
+      if (auto e = dev->check(bch_upload(dev->ctx(), t.buf_->ptr, data.data(), data.size() * sizeof(float)),
+                              "upload"))
+        return *e;
+    }
+    return t;
+  }
+  static Result<Tensor> from_vec_on(const std::vector<float>& data, std::vector<size_t> shape,
+                                    const std::shared_ptr<HipDevice>& dev) {
+    return from_data(data, std::move(shape), dev);
+  }
+  // an uninitialised output tensor (the reference's pooled output buffers)
+  static Result<Tensor> empty(std::vector<size_t> shape, const std::shared_ptr<HipDevice>& dev) {
+    auto buf = std::make_shared<detail::DeviceBuffer>();
+    buf->dev = dev;
+    buf->bytes = detail::numel(shape) * sizeof(float);
+    if (buf->bytes) {
+      std::lock_guard<std::mutex> g(dev->mutex());
+      if (auto e = dev->check(bch_alloc(dev->ctx(), buf->bytes, &buf->ptr), "alloc_buffer")) return *e;
+    }
+    return Tensor(std::move(buf), std::move(shape), dev);
+  }
+
+  const std::vector<size_t>& shape() const { return shape_; }
+  size_t len() const { return detail::numel(shape_); }
+  const std::shared_ptr<HipDevice>& device() const { return dev_; }
+  float* data_ptr() const { return static_cast<float*>(buf_->ptr); }
+
+  // tensor/mod.rs:448 to_vec: blocking readback
+  Result<std::vector<float>> to_vec() const {
+    std::vector<float> out(len());
+    if (!out.empty()) {
+      std::lock_guard<std::mutex> g(dev_->mutex());
+      if (auto e = dev_->check(bch_download(dev_->ctx(), out.data(), buf_->ptr, out.size() * sizeof(float)),
+                               "download"))
+        return *e;
+    }
+    return out;
+  }
+
+  inline Result<Tensor> matmul(const Tensor& other) const;
+  inline Result<Tensor> matmul_ref(const Tensor& other) const;
+  inline Result<Tensor> matmul_tiled(const Tensor& other) const;
+  inline Result<Tensor> batch_matmul(const Tensor& other) const;
+  inline Result<Tensor> softmax() const;
+  inline Result<Tensor> softmax_dim(size_t axis) const;
+  inline Result<Tensor> attention(const Tensor& key, const Tensor& value) const;
+  inline Result<Tensor> scaled_dot_product_attention(const Tensor& key, const Tensor& value) const;
+  inline Result<Tensor> causal_attention(const Tensor& key, const Tensor& value) const;
+
+ private:
+  Tensor(std::shared_ptr<detail::DeviceBuffer> b, std::vector<size_t> s, std::shared_ptr<HipDevice> d)
+      : buf_(std::move(b)), shape_(std::move(s)), dev_(std::move(d)) {}
+  std::shared_ptr<detail::DeviceBuffer> buf_;
+  std::vector<size_t> shape_;
+  std::shared_ptr<HipDevice> dev_;
+};
+
+// ---------------------------------------------------------------- ops
+// ops/matmul.rs:92-114: 2D+ inputs (>= 3-D use shape[0..2]), inner dims equal.
+struct MatMul {
+  const Tensor& lhs;
+  const Tensor& rhs;
+  static std::optional<BarracudaError> validate(const std::vector<size_t>& ls, const std::vector<size_t>& rs) {
+    if (ls.size() < 2 || rs.size() < 2)
+      return BarracudaError::invalid_op("matmul", "requires 2D+ tensors, got shapes " + shape_str(ls) + " and " +
+                                                      shape_str(rs));
+    if (ls[1] != rs[0]) return BarracudaError::shape_mismatch(ls, rs);
+    return std::nullopt;
+  }
+  Result<Tensor> execute() const {
+    if (auto e = validate(lhs.shape(), rhs.shape())) return *e;
+    const int m = (int)lhs.shape()[0], k = (int)lhs.shape()[1], n = (int)rhs.shape()[1];
+    auto dev = lhs.device();
+    auto r = Tensor::empty({(size_t)m, (size_t)n}, dev);
+    if (r.is_err() || m == 0 || n == 0) return r;
+    Tensor out = std::move(r).unwrap();
+    std::lock_guard<std::mutex> g(dev->mutex());
+    const int lk = k > 1 ? k : 1, ln = n > 1 ? n : 1;
+    if (auto e = dev->check(bch_sgemm(dev->ctx(), m, n, k, lhs.data_ptr(), lk, rhs.data_ptr(), ln, out.data_ptr(), ln),
+                            "matmul"))
+      return *e;
+    return out;
+  }
+};
+using MatmulTiled = MatMul;  // ops/matmul_tiled.rs: same contract
+
+// ops/batch_matmul.rs:47-144: A[batch,m,k] . B[batch,k,n].  The reference
+// does not check B against A; a disagreeing B is a ShapeMismatch here.
+struct BatchMatMul {
+  const Tensor& a;
+  const Tensor& b;
+  static std::optional<BarracudaError> validate(const std::vector<size_t>& as, const std::vector<size_t>& bs) {
+    if (as.size() != 3 || bs.size() != 3)
+      return BarracudaError::invalid_op("batch_matmul", "requires 3D tensors, got shapes " + shape_str(as) +
+                                                            " and " + shape_str(bs));
+    if (bs[0] != as[0] || bs[1] != as[2]) return BarracudaError::shape_mismatch(as, bs);
+    return std::nullopt;
+  }
+  Result<Tensor> execute() const {
+    if (auto e = validate(a.shape(), b.shape())) return *e;
+    const int batch = (int)a.shape()[0], m = (int)a.shape()[1], k = (int)a.shape()[2], n = (int)b.shape()[2];
+    auto dev = a.device();
+    auto r = Tensor::empty({(size_t)batch, (size_t)m, (size_t)n}, dev);
+    if (r.is_err() || batch * m * n == 0) return r;
+    Tensor out = std::move(r).unwrap();
+    std::lock_guard<std::mutex> g(dev->mutex());
+    if (auto e = dev->check(bch_sgemm_strided_batched(dev->ctx(), batch, m, n, k, a.data_ptr(), (long long)m * k,
+                                                      b.data_ptr(), (long long)k * n, out.data_ptr(),
+                                                      (long long)m * n),
+                            "batch_matmul"))
+      return *e;
+    return out;
+  }
+};
+
+// ops/softmax.rs:39-48 (non-empty shape), :58-133 (one softmax over all elements)
+struct Softmax {
+  const Tensor& input;
+  static std::optional<BarracudaError> validate(const std::vector<size_t>& s) {
+    if (s.empty()) return BarracudaError::invalid_op("Softmax", "Empty tensor not supported");
+    return std::nullopt;
+  }
+  Result<Tensor> execute() const {
+    if (auto e = validate(input.shape())) return *e;
+    auto dev = input.device();
+    auto r = Tensor::empty(input.shape(), dev);
+    if (r.is_err() || input.len() == 0) return r;
+    Tensor out = std::move(r).unwrap();
+    std::lock_guard<std::mutex> g(dev->mutex());
+    if (auto e = dev->check(bch_softmax_rows(dev->ctx(), 1, (long long)input.len(), input.data_ptr(), out.data_ptr()),
+                            "softmax"))
+      return *e;
+    return out;
+  }
+};
+
+// ops/tensor_axis_ops.rs:67-82: validation of softmax_dim
+inline std::optional<BarracudaError> validate_softmax_dim(const std::vector<size_t>& s, size_t axis) {
+  if (s.empty()) return BarracudaError::invalid_op("softmax_dim", "Empty tensor not supported");
+  if (axis >= s.size())
+    return BarracudaError::invalid_op("softmax_dim",
+                                      "Axis " + std::to_string(axis) + " out of bounds for shape " + shape_str(s));
+  return std::nullopt;
+}
+
+namespace detail {
+inline Result<Tensor> sdpa(const Tensor& q, const Tensor& k, const Tensor& v, bool causal, const char* op, int B,
+                           int H, int Sq, int Skv, int D) {
+  auto dev = q.device();
+  if (D > 128) return BarracudaError::unsupported(op, dev->name() + " (head_dim " + std::to_string(D) + " > 128)");
+  auto r = Tensor::empty(q.shape(), dev);
+  if (r.is_err() || (size_t)B * H * Sq * D == 0) return r;
+  if (Skv == 0) return BarracudaError::invalid_op(op, "key sequence is empty (shape/dimension mismatch)");
+  Tensor out = std::move(r).unwrap();
+  const float scale = 1.0f / std::sqrt((float)D);
+  std::lock_guard<std::mutex> g(dev->mutex());
+  if (auto e = dev->check(bch_sdpa_fwd(dev->ctx(), B, H, Sq, Skv, D, scale, causal ? 1 : 0, q.data_ptr(), k.data_ptr(),
+                                       v.data_ptr(), out.data_ptr()),
+                          op))
+    return *e;
+  return out;
+}
+}  // namespace detail
+
+// ops/attention/mod.rs:96-144: 4-D Q, K, V; batch, heads and head_dim of Q and
+// K equal (Sq may differ from Skv); K and V identical shapes.
+struct Attention {
+  const Tensor& q;
+  const Tensor& k;
+  const Tensor& v;
+  static std::optional<BarracudaError> validate(const std::vector<size_t>& qs, const std::vector<size_t>& ks,
+                                                const std::vector<size_t>& vs) {
+    const char* names[3] = {"query", "key", "value"};
+    const std::vector<size_t>* ss[3] = {&qs, &ks, &vs};
+    for (int i = 0; i < 3; ++i)
+      if (ss[i]->size() != 4)
+        return BarracudaError::invalid_op("attention", std::string(names[i]) +
+                                                           " requires 4D tensor [batch, heads, seq_len, head_dim], got " +
+                                                           std::to_string(ss[i]->size()) + "D");
+    if (qs[0] != ks[0] || qs[1] != ks[1] || qs[3] != ks[3]) return BarracudaError::shape_mismatch(qs, ks);
+    if (ks != vs) return BarracudaError::shape_mismatch(ks, vs);
+    return std::nullopt;
+  }
+  Result<Tensor> execute() const {
+    if (auto e = validate(q.shape(), k.shape(), v.shape())) return *e;
+    const auto& s = q.shape();
+    return detail::sdpa(q, k, v, false, "attention", (int)s[0], (int)s[1], (int)s[2], (int)k.shape()[2], (int)s[3]);
+  }
+};
+
+// ops/scaled_dot_product_attention/mod.rs:101-149: self-attention, equal shapes
+struct ScaledDotProductAttention {
+  const Tensor& q;
+  const Tensor& k;
+  const Tensor& v;
+  static std::optional<BarracudaError> validate(const std::vector<size_t>& qs, const std::vector<size_t>& ks,
+                                                const std::vector<size_t>& vs) {
+    if (qs.size() != 4 || ks.size() != 4 || vs.size() != 4)
+      return BarracudaError::invalid_input("Q, K, V must be 4D tensors [batch, heads, seq_len, head_dim]");
+    if (ks != qs || vs != qs) return BarracudaError::shape_mismatch(qs, ks == qs ? vs : ks);
+    return std::nullopt;
+  }
+  Result<Tensor> execute() const {
+    if (auto e = validate(q.shape(), k.shape(), v.shape())) return *e;
+    if (q.device() != k.device() || q.device() != v.device())
+      return BarracudaError::device("Q, K, V must be on the same device");
+    const auto& s = q.shape();
+    return detail::sdpa(q, k, v, false, "scaled_dot_product_attention", (int)s[0], (int)s[1], (int)s[2], (int)s[2],
+                        (int)s[3]);
+  }
+};
+
+// ops/causal_attn/mod.rs:78-95.  The reference's GPU dispatch computes only
+// rows < 16 of head 0; this follows its CPU definition
+// (ops/causal_attention.rs:52-134) for every row and head.
+struct CausalAttention {
+  const Tensor& q;
+  const Tensor& k;
+  const Tensor& v;
+  static std::optional<BarracudaError> validate(const std::vector<size_t>& qs, const std::vector<size_t>& ks,
+                                                const std::vector<size_t>& vs) {
+    if (qs.size() != 4 || ks.size() != 4 || vs.size() != 4) return BarracudaError::shape_mismatch(qs, ks);
+    if (qs != ks || qs != vs) return BarracudaError::shape_mismatch(qs, ks);
+    return std::nullopt;
+  }
+  Result<Tensor> execute() const {
+    if (auto e = validate(q.shape(), k.shape(), v.shape())) return *e;
+    const auto& s = q.shape();
+    return detail::sdpa(q, k, v, true, "causal_attention", (int)s[0], (int)s[1], (int)s[2], (int)s[2], (int)s[3]);
+  }
+};
+
+// ops/flash_attention.rs:57-80: 2-D [seq_len, head_dim], one head, scale
+// 1/sqrt(head_dim).  The reference shader keeps at most 256 keys; every key
+// is attended to here (the two agree for seq_len <= 256).
+struct FlashAttention {
+  const Tensor& q;
+  const Tensor& k;
+  const Tensor& v;
+  unsigned num_heads = 1;
+  static std::optional<BarracudaError> validate(const std::vector<size_t>& qs, const std::vector<size_t>& ks,
+                                                const std::vector<size_t>& vs) {
+    if (qs != ks || qs != vs)
+      return BarracudaError::invalid_op("FlashAttention", "Q, K, V must have same shape, got Q: " + shape_str(qs) +
+                                                               ", K: " + shape_str(ks) + ", V: " + shape_str(vs));
+    if (qs.size() != 2)
+      return BarracudaError::invalid_op("FlashAttention",
+                                        "Requires 2D tensors [seq_len, head_dim], got shape: " + shape_str(qs));
+    return std::nullopt;
+  }
+  Result<Tensor> execute() const {
+    if (auto e = validate(q.shape(), k.shape(), v.shape())) return *e;
+    const int S = (int)q.shape()[0], D = (int)q.shape()[1];
+    return detail::sdpa(q, k, v, false, "FlashAttention", 1, 1, S, S, D);
+  }
+};
+
+// ---------------------------------------------------------------- Tensor methods
+inline Result<Tensor> Tensor::matmul(const Tensor& other) const { return MatMul{*this, other}.execute(); }
+inline Result<Tensor> Tensor::matmul_ref(const Tensor& other) const { return MatMul{*this, other}.execute(); }
+inline Result<Tensor> Tensor::matmul_tiled(const Tensor& other) const { return MatmulTiled{*this, other}.execute(); }
+inline Result<Tensor> Tensor::batch_matmul(const Tensor& other) const { return BatchMatMul{*this, other}.execute(); }
+inline Result<Tensor> Tensor::softmax() const { return Softmax{*this}.execute(); }
+inline Result<Tensor> Tensor::softmax_dim(size_t axis) const {
+  if (auto e = validate_softmax_dim(shape_, axis)) return *e;
+  auto r = Tensor::empty(shape_, dev_);
+  if (r.is_err() || len() == 0) return r;
+  Tensor out = std::move(r).unwrap();
+  size_t outer = 1, inner = 1;
+  for (size_t i = 0; i < axis; ++i) outer *= shape_[i];
+  for (size_t i = axis + 1; i < shape_.size(); ++i) inner *= shape_[i];
+  std::lock_guard<std::mutex> g(dev_->mutex());
+  if (auto e = dev_->check(bch_softmax_axis(dev_->ctx(), (long long)outer, (long long)shape_[axis], (long long)inner,
+                                            data_ptr(), out.data_ptr()),
+                           "softmax_dim"))
+    return *e;
+  return out;
+}
+inline Result<Tensor> Tensor::attention(const Tensor& key, const Tensor& value) const {
+  return Attention{*this, key, value}.execute();
+}
+inline Result<Tensor> Tensor::scaled_dot_product_attention(const Tensor& key, const Tensor& value) const {
+  return ScaledDotProductAttention{*this, key, value}.execute();
+}
+inline Result<Tensor> Tensor::causal_attention(const Tensor& key, const Tensor& value) const {
+  return CausalAttention{*this, key, value}.execute();
+}
+
+}  // namespace barracuda

@@ -1,0 +1,296 @@
+// C++ host-API tests over libbarracuda_hip, written as the reference's own
+// Rust tests are (crates/barracuda/src/ops/*.rs #[cfg(test)] modules,
+// crates/barracuda/tests/fault_injection.rs), against include/barracuda_hip_ops.hpp.
+//
+//   bch_host_tests --cpu   validation and no-device behaviour (no GPU needed)
+//   bch_host_tests --gpu   everything, on device 0
+// Exit status 0 when every test passes; one line per test on stdout.
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <functional>
+#include <string>
+#include <vector>
+
+#include "barracuda_hip_ops.hpp"
+
+using namespace barracuda;
+
+namespace {
+
+int g_fail = 0, g_pass = 0;
+std::shared_ptr<HipDevice> g_dev;
+
+#define REQUIRE(cond)                                                                   \
+  do {                                                                                  \
+    if (!(cond)) throw std::runtime_error(std::string("requirement failed: ") + #cond + \
+                                          " (" + __FILE__ + ":" + std::to_string(__LINE__) + ")"); \
+  } while (0)
+
+void run(const char* name, const std::function<void()>& fn) {
+  try {
+    fn();
+    ++g_pass;
+    std::printf("PASS %s\n", name);
+  } catch (const std::exception& e) {
+    ++g_fail;
+    std::printf("FAIL %s: %s\n", name, e.what());
+  }
+  std::fflush(stdout);
+}
+
+Tensor T(const std::vector<float>& d, std::vector<size_t> s) { return Tensor::from_vec_on(d, std::move(s), g_dev).unwrap(); }
+
+// the reference tests' CPU matmul (ops/matmul.rs:250-262): i, j, p with mul_add
+std::vector<float> matmul_cpu(const std::vector<float>& a, const std::vector<float>& b, size_t m, size_t k, size_t n) {
+  std::vector<float> r(m * n, 0.0f);
+  for (size_t i = 0; i < m; ++i)
+    for (size_t j = 0; j < n; ++j) {
+      float sum = 0.0f;
+      for (size_t p = 0; p < k; ++p) sum = std::fma(a[i * k + p], b[p * n + j], sum);
+      r[i * n + j] = sum;
+    }
+  return r;
+}
+
+bool has_shape_words(const std::string& m) {
+  std::string s = m;
+  for (auto& c : s) c = (char)std::tolower(c);
+  return s.find("shape") != std::string::npos || s.find("dimension") != std::string::npos ||
+         s.find("mismatch") != std::string::npos;
+}
+
+// ---------------------------------------------------------------- CPU-only tests
+void cpu_tests() {
+  run("validate_matmul_requires_2d", [] {
+    auto e = MatMul::validate({4}, {4, 4});
+    REQUIRE(e && e->kind == ErrorKind::InvalidOperation && e->message.find("2D+") != std::string::npos);
+  });
+  run("validate_matmul_inner_dim_mismatch", [] {  // fault_injection.rs:29-60
+    auto e = MatMul::validate({2, 3}, {4, 2});
+    REQUIRE(e && e->kind == ErrorKind::ShapeMismatch && has_shape_words(e->message));
+    REQUIRE(e->message == "Shape mismatch: expected [2, 3], got [4, 2]");
+    REQUIRE(!MatMul::validate({2, 3}, {3, 5}));
+    REQUIRE(!MatMul::validate({2, 3, 7}, {3, 5}));  // >= 3-D uses shape[0..2] (matmul.rs:103-107)
+  });
+  run("validate_batch_matmul", [] {
+    REQUIRE(BatchMatMul::validate({2, 2, 3}, {2, 3, 2}) == std::nullopt);
+    REQUIRE(BatchMatMul::validate({2, 2, 3}, {3, 3, 2})->kind == ErrorKind::ShapeMismatch);
+    REQUIRE(BatchMatMul::validate({2, 3}, {2, 3, 2})->kind == ErrorKind::InvalidOperation);
+  });
+  run("validate_softmax_and_softmax_dim", [] {
+    REQUIRE(Softmax::validate({})->message == "Invalid operation: Softmax - Empty tensor not supported");
+    REQUIRE(!Softmax::validate({5}));
+    REQUIRE(validate_softmax_dim({2, 3}, 2)->message ==
+            "Invalid operation: softmax_dim - Axis 2 out of bounds for shape [2, 3]");
+    REQUIRE(!validate_softmax_dim({2, 3}, 1));
+  });
+  run("validate_attention", [] {  // attention/tests.rs:31-47
+    REQUIRE(Attention::validate({1, 1, 4, 8}, {1, 1, 2, 8}, {1, 1, 4, 8})->kind == ErrorKind::ShapeMismatch);
+    REQUIRE(Attention::validate({1, 4, 8}, {1, 1, 4, 8}, {1, 1, 4, 8})->kind == ErrorKind::InvalidOperation);
+    REQUIRE(!Attention::validate({1, 2, 4, 8}, {1, 2, 6, 8}, {1, 2, 6, 8}));  // cross-attention
+    REQUIRE(ScaledDotProductAttention::validate({4, 8}, {4, 8}, {4, 8})->kind == ErrorKind::InvalidInput);
+    REQUIRE(CausalAttention::validate({1, 1, 4, 8}, {1, 1, 4, 8}, {1, 1, 4, 4})->kind == ErrorKind::ShapeMismatch);
+    REQUIRE(FlashAttention::validate({4, 8}, {4, 4}, {4, 8})->kind == ErrorKind::InvalidOperation);
+    REQUIRE(FlashAttention::validate({1, 4, 8}, {1, 4, 8}, {1, 4, 8})->message.find("2D") != std::string::npos);
+  });
+  run("status_to_error_mapping", [] {
+    REQUIRE(BarracudaError::from_status(BCH_E_OOM, "x", "op").kind == ErrorKind::OutOfMemory);
+    REQUIRE(BarracudaError::from_status(BCH_E_SHAPE, "x", "matmul").kind == ErrorKind::InvalidOperation);
+    REQUIRE(has_shape_words(BarracudaError::from_status(BCH_E_SHAPE, "x", "matmul").message));
+    REQUIRE(BarracudaError::from_status(BCH_E_NO_DEVICE, "x", "op").kind == ErrorKind::Device);
+    REQUIRE(BarracudaError::from_status(BCH_E_UNSUPPORTED, "x", "op").kind == ErrorKind::UnsupportedOperation);
+  });
+}
+
+// ---------------------------------------------------------------- GPU tests
+void gpu_tests() {
+  // ops/matmul.rs tests
+  run("test_matmul_basic", [] {  // matmul.rs:264-290
+    std::vector<float> a = {1, 2, 3, 4, 5, 6}, b = {1, 2, 3, 4, 5, 6};
+    auto r = T(a, {2, 3}).matmul(T(b, {3, 2})).unwrap();
+    REQUIRE((r.shape() == std::vector<size_t>{2, 2}));
+    auto out = r.to_vec().unwrap(), exp = matmul_cpu(a, b, 2, 3, 2);
+    for (size_t i = 0; i < out.size(); ++i) REQUIRE(std::fabs(out[i] - exp[i]) < 1e-5f);
+  });
+  run("test_matmul_edge_cases", [] {  // matmul.rs:292-336: identity, zeros
+    auto r = T({1, 0, 0, 1}, {2, 2}).matmul(T({5, 6, 7, 8}, {2, 2})).unwrap().to_vec().unwrap();
+    std::vector<float> e = {5, 6, 7, 8};
+    for (size_t i = 0; i < 4; ++i) REQUIRE(std::fabs(r[i] - e[i]) < 1e-5f);
+    auto z = T({0, 0, 0, 0}, {2, 2}).matmul(T({1, 2, 3, 4}, {2, 2})).unwrap().to_vec().unwrap();
+    for (float v : z) REQUIRE(std::fabs(v) < 1e-6f);
+  });
+  run("test_matmul_single_element", [] {  // matmul.rs:338-356
+    auto r = T({5}, {1, 1}).matmul(T({3}, {1, 1})).unwrap().to_vec().unwrap();
+    REQUIRE(std::fabs(r[0] - 15.0f) < 1e-5f);
+  });
+  run("test_matmul_rectangular", [] {  // matmul.rs:358-377
+    std::vector<float> a = {1, 2, 3, 4, 5, 6, 7, 8}, b = {1, 0, 0, 0, 1, 0};
+    auto r = T(a, {4, 2}).matmul(T(b, {2, 3})).unwrap();
+    REQUIRE((r.shape() == std::vector<size_t>{4, 3}));
+    auto out = r.to_vec().unwrap(), exp = matmul_cpu(a, b, 4, 2, 3);
+    for (size_t i = 0; i < out.size(); ++i) REQUIRE(std::fabs(out[i] - exp[i]) < 1e-5f);
+  });
+  run("test_matmul_large_tensor", [] {  // matmul.rs:379-409 (bound widened to 1e-6 relative at |C| ~ 7e3)
+    const size_t m = 64, k = 32, n = 64;
+    std::vector<float> a(m * k), b(k * n);
+    for (size_t i = 0; i < a.size(); ++i) a[i] = (float)i * 0.01f;
+    for (size_t i = 0; i < b.size(); ++i) b[i] = (float)i * 0.01f;
+    auto out = T(a, {m, k}).matmul(T(b, {k, n})).unwrap().to_vec().unwrap();
+    auto exp = matmul_cpu(a, b, m, k, n);
+    for (size_t i = 0; i < out.size(); ++i)
+      REQUIRE(std::fabs(out[i] - exp[i]) < std::fmax(1e-3f, 2e-6f * std::fabs(exp[i])));
+  });
+  run("test_matmul_precision", [] {  // matmul.rs:411-443
+    std::vector<float> a = {1.234f, 2.345f, 3.456f, 4.567f, 5.678f, 6.789f};
+    std::vector<float> b = {0.111f, 0.222f, 0.333f, 0.444f, 0.555f, 0.666f};
+    auto out = T(a, {2, 3}).matmul_ref(T(b, {3, 2})).unwrap().to_vec().unwrap();
+    auto exp = matmul_cpu(a, b, 2, 3, 2);
+    for (size_t i = 0; i < 4; ++i) REQUIRE(std::fabs(out[i] - exp[i]) < 1e-5f);
+  });
+  run("test_matmul_tiled_and_decode_shape", [] {  // matmul_tiled.rs; skinny path m = 1
+    std::vector<float> a(300), b(300 * 64);
+    for (size_t i = 0; i < a.size(); ++i) a[i] = (float)((int)(i % 7) - 3);
+    for (size_t i = 0; i < b.size(); ++i) b[i] = (float)((int)(i % 5) - 2);
+    auto out = T(a, {1, 300}).matmul_tiled(T(b, {300, 64})).unwrap().to_vec().unwrap();
+    auto exp = matmul_cpu(a, b, 1, 300, 64);
+    for (size_t i = 0; i < out.size(); ++i) REQUIRE(out[i] == exp[i]);  // integers: exact
+  });
+  // ops/batch_matmul.rs:172-199
+  run("test_batch_matmul_basic", [] {
+    std::vector<float> a = {1, 2, 3, 4, 5, 6, 1, 1, 1, 2, 2, 2};
+    std::vector<float> b = {1, 0, 0, 1, 1, 1, 2, 0, 0, 2, 1, 1};
+    auto r = T(a, {2, 2, 3}).batch_matmul(T(b, {2, 3, 2})).unwrap();
+    REQUIRE((r.shape() == std::vector<size_t>{2, 2, 2}));
+    auto out = r.to_vec().unwrap();
+    std::vector<float> e = {4, 5, 10, 11, 3, 3, 6, 6};
+    for (size_t i = 0; i < 8; ++i) REQUIRE(out[i] == e[i]);
+  });
+  // ops/softmax.rs tests (global softmax)
+  run("test_softmax_basic", [] {  // softmax.rs:151-166
+    auto r = T({1, 2, 3}, {3}).softmax().unwrap().to_vec().unwrap();
+    float sum = r[0] + r[1] + r[2];
+    for (float v : r) REQUIRE(v > 0.0f && v < 1.0f);
+    REQUIRE(std::fabs(sum - 1.0f) < 1e-5f);
+    REQUIRE(r[2] > r[1] && r[1] > r[0]);
+  });
+  run("test_softmax_small_and_large_values", [] {  // softmax.rs:168-191
+    auto s = T({1e-6f, 2e-6f, 3e-6f}, {3}).softmax().unwrap().to_vec().unwrap();
+    REQUIRE(std::fabs(s[0] + s[1] + s[2] - 1.0f) < 1e-5f);
+    auto l = T({100, 200, 300}, {3}).softmax().unwrap().to_vec().unwrap();
+    REQUIRE(std::fabs(l[0] + l[1] + l[2] - 1.0f) < 1e-5f && l[2] > 0.99f);
+  });
+  run("test_softmax_large_input", [] {  // softmax.rs:193-206
+    std::vector<float> x(1000);
+    for (size_t i = 0; i < x.size(); ++i) x[i] = (float)i / 10.0f;
+    auto r = T(x, {1000}).softmax().unwrap().to_vec().unwrap();
+    double sum = 0;
+    for (float v : r) sum += v;
+    REQUIRE(std::fabs(sum - 1.0) < 1e-4);
+  });
+  run("test_softmax_vs_cpu", [] {  // softmax.rs:208-233
+    std::vector<float> x = {1, 2, 3, 4, 5};
+    auto r = T(x, {5}).softmax().unwrap().to_vec().unwrap();
+    float mx = 5, sum = 0;
+    std::vector<float> e(5);
+    for (int i = 0; i < 5; ++i) sum += e[i] = std::exp(x[i] - mx);
+    for (int i = 0; i < 5; ++i) REQUIRE(std::fabs(r[i] - e[i] / sum) < 1e-5f);
+  });
+  // ops/tensor_axis_ops.rs tests (softmax_dim)
+  run("test_softmax_dim_rows_and_columns", [] {  // tensor_axis_ops.rs:158-200
+    auto r = T({1, 2, 3, 4, 5, 6}, {2, 3}).softmax_dim(1).unwrap();
+    REQUIRE((r.shape() == std::vector<size_t>{2, 3}));
+    auto v = r.to_vec().unwrap();
+    REQUIRE(std::fabs(v[0] + v[1] + v[2] - 1.0f) < 1e-5f && std::fabs(v[3] + v[4] + v[5] - 1.0f) < 1e-5f);
+    auto c = T({1, 4, 2, 5, 3, 6}, {3, 2}).softmax_dim(0).unwrap().to_vec().unwrap();
+    REQUIRE(std::fabs(c[0] + c[2] + c[4] - 1.0f) < 1e-5f && std::fabs(c[1] + c[3] + c[5] - 1.0f) < 1e-5f);
+    auto one = T({1, 2, 3}, {3, 1}).softmax_dim(1).unwrap().to_vec().unwrap();
+    REQUIRE((one == std::vector<float>{1, 1, 1}));
+    REQUIRE(T({1, 2, 3}, {3}).softmax_dim(1).is_err());
+  });
+  // ops/attention/tests.rs
+  run("test_attention_basic", [] {  // attention/tests.rs:8-29
+    auto q = T(std::vector<float>(32, 1.0f), {1, 1, 4, 8});
+    auto k = T(std::vector<float>(32, 1.0f), {1, 1, 4, 8});
+    auto v = T(std::vector<float>(32, 2.0f), {1, 1, 4, 8});
+    auto o = q.attention(k, v).unwrap();
+    REQUIRE((o.shape() == std::vector<size_t>{1, 1, 4, 8}));
+    for (float x : o.to_vec().unwrap()) REQUIRE(std::fabs(x - 2.0f) < 0.1f);
+  });
+  run("test_attention_shape_validation", [] {  // attention/tests.rs:31-47
+    auto q = T(std::vector<float>(32, 1.0f), {1, 1, 4, 8});
+    auto k = T(std::vector<float>(16, 1.0f), {1, 1, 2, 8});
+    auto v = T(std::vector<float>(32, 1.0f), {1, 1, 4, 8});
+    REQUIRE(q.attention(k, v).is_err());
+  });
+  run("test_attention_multi_head", [] {  // attention/tests.rs:49-66
+    const size_t size = 2 * 4 * 8 * 16;
+    auto q = T(std::vector<float>(size, 0.5f), {2, 4, 8, 16});
+    auto v = T(std::vector<float>(size, 1.0f), {2, 4, 8, 16});
+    auto out = q.attention(q, v).unwrap().to_vec().unwrap();
+    REQUIRE(out.size() == size);
+    for (float x : out) REQUIRE(std::isfinite(x) && std::fabs(x - 1.0f) < 1e-6f);
+  });
+  run("test_sdpa_and_causal", [] {  // sdpa + causal: row 0 of causal attends to key 0 only
+    const size_t S = 5, D = 3;
+    std::vector<float> q(S * D, 0.0f), k(S * D, 1.0f), v(S * D);
+    for (size_t i = 0; i < v.size(); ++i) v[i] = (float)i;
+    auto tq = T(q, {1, 1, S, D}), tk = T(k, {1, 1, S, D}), tv = T(v, {1, 1, S, D});
+    auto c = tq.causal_attention(tk, tv).unwrap().to_vec().unwrap();
+    for (size_t i = 0; i < S; ++i)  // equal scores: row i = mean of V[0..=i]
+      for (size_t d = 0; d < D; ++d) {
+        float mean = 0;
+        for (size_t j = 0; j <= i; ++j) mean += v[j * D + d];
+        REQUIRE(std::fabs(c[i * D + d] - mean / (float)(i + 1)) < 1e-5f);
+      }
+    auto s = tq.scaled_dot_product_attention(tk, tv).unwrap().to_vec().unwrap();
+    for (size_t d = 0; d < D; ++d) {
+      float mean = 0;
+      for (size_t j = 0; j < S; ++j) mean += v[j * D + d];
+      REQUIRE(std::fabs(s[d] - mean / (float)S) < 1e-5f);
+    }
+  });
+  run("test_flash_attention_single_head", [] {  // flash_attention.rs:152-185
+    auto q = T(std::vector<float>(64, 0.3f), {16, 4});
+    auto v = T(std::vector<float>(64, 2.0f), {16, 4});
+    auto out = FlashAttention{q, q, v, 1}.execute().unwrap().to_vec().unwrap();
+    for (float x : out) REQUIRE(std::fabs(x - 2.0f) < 1e-5f);
+  });
+  // crates/barracuda/tests/fault_injection.rs:29-60
+  run("test_fault_injection_shape_mismatch", [] {
+    auto r = T({1, 2, 3, 4, 5, 6}, {2, 3}).matmul(T({1, 2, 3, 4, 5, 6, 7, 8}, {4, 2}));
+    REQUIRE(r.is_err() && has_shape_words(r.error().message));
+    // the device stays usable after the error
+    auto ok = T({1, 1, 1, 1, 1, 1}, {2, 3}).matmul(T({1, 1, 1, 1, 1, 1}, {3, 2})).unwrap().to_vec().unwrap();
+    for (float x : ok) REQUIRE(x == 3.0f);
+  });
+  run("test_tensor_from_data_size_mismatch", [] {
+    auto r = Tensor::from_data({1, 2, 3}, {2, 2}, g_dev);
+    REQUIRE(r.is_err() && r.error().kind == ErrorKind::ShapeMismatch);
+  });
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+  const bool gpu = argc > 1 && std::strcmp(argv[1], "--gpu") == 0;
+  cpu_tests();
+  auto dr = HipDevice::create(0);
+  if (!gpu) {
+    // without a GPU the device constructor returns Err(Device), never aborts
+    run("no_device_is_an_error_value", [&] {
+      if (dr.is_ok()) return;  // a GPU is present: nothing to check here
+      REQUIRE(dr.error().kind == ErrorKind::Device);
+      REQUIRE(dr.error().message.find("no HIP device") != std::string::npos);
+    });
+  } else {
+    if (dr.is_err()) {
+      std::printf("FAIL device: %s\n", dr.error().message.c_str());
+      return 1;
+    }
+    g_dev = dr.value();
+    gpu_tests();
+  }
+  std::printf("%d passed, %d failed\n", g_pass, g_fail);
+  return g_fail == 0 ? 0 : 1;
+}
