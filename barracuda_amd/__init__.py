@@ -4,15 +4,17 @@ hot path: f32 matmul / batched matmul, row softmax, fused attention forward.
 The compute lives in libbarracuda_hip.so (C ABI: include/barracuda_hip.h);
 this package is the host side that mirrors the reference's op API.
 """
-from .error import (BarracudaError, DeviceError, DeviceLost, DeviceNotAvailable, ExecutionError,
-                    InvalidInput, InvalidOperation, OutOfMemory, ShapeMismatch,
-                    UnsupportedOperation)
+from .error import (BarracudaError, CastOverflow, DeviceError, DeviceLost, DeviceNotAvailable,
+                    ExecutionError, InvalidInput, InvalidOperation, InvalidShape, OutOfMemory,
+                    ShapeMismatch, UnsupportedOperation)
+from .session import AttentionDims, SessionTensor, TensorSession
 from .tensor import (Attention, BatchMatMul, CausalAttention, FlashAttention, HipDevice, LcgStream,
                      MatMul, MatmulTiled, ScaledDotProductAttention, Softmax, Tensor, get_device)
 
 __all__ = [
-    "BarracudaError", "DeviceError", "DeviceLost", "DeviceNotAvailable", "ExecutionError",
-    "InvalidInput", "InvalidOperation", "OutOfMemory", "ShapeMismatch", "UnsupportedOperation",
+    "BarracudaError", "CastOverflow", "DeviceError", "DeviceLost", "DeviceNotAvailable",
+    "ExecutionError", "InvalidInput", "InvalidOperation", "InvalidShape", "OutOfMemory",
+    "ShapeMismatch", "UnsupportedOperation", "AttentionDims", "SessionTensor", "TensorSession",
     "Attention", "BatchMatMul", "CausalAttention", "FlashAttention", "HipDevice", "MatMul",
     "MatmulTiled", "ScaledDotProductAttention", "Softmax", "Tensor", "get_device", "LcgStream",
 ]

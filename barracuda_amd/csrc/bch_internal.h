@@ -21,11 +21,19 @@ __device__ __forceinline__ void store_nt(float4 r, float4* p) {
 }
 
 // Row softmax over a contiguous [rows, cols] f32 matrix (in may equal out).
+// ws/ws_bytes: device scratch of at least softmax_workspace_bytes(rows, cols)
+// bytes (zero when few long rows are not split across workgroups).
 hipError_t launch_softmax_rows(hipStream_t s, long long rows, long long cols,
-                               const float* in, float* out);
-// Softmax along the middle axis of [outer, axis, inner].
+                               const float* in, float* out, void* ws,
+                               size_t ws_bytes);
+size_t softmax_workspace_bytes(long long rows, long long cols);
+// Softmax along the middle axis of [outer, axis, inner]; the scratch rule of
+// launch_softmax_rows applies when inner == 1.
 hipError_t launch_softmax_axis(hipStream_t s, long long outer, long long axis,
-                               long long inner, const float* in, float* out);
+                               long long inner, const float* in, float* out,
+                               void* ws, size_t ws_bytes);
+size_t softmax_axis_workspace_bytes(long long outer, long long axis,
+                                    long long inner);
 const char* softmax_kernel_name(long long rows, long long cols);
 
 // C[b] = A[b] . B[b] (row-major), b < batch.  ws/ws_bytes: device scratch

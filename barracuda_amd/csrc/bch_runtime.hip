@@ -311,7 +311,13 @@ bch_status bch_softmax_rows(bch_ctx* ctx, long long rows, long long cols, const 
   if (!in || !out) return fail(ctx, BCH_E_INVALID, "softmax: NULL buffer");
   bch_status st = use(ctx);
   if (st != BCH_OK) return st;
-  return from_hip(ctx, bch::launch_softmax_rows(ctx->stream, rows, cols, in, out), "softmax launch");
+  size_t wsb = bch::softmax_workspace_bytes(rows, cols);
+  if (wsb) {
+    st = ensure_ws(ctx, wsb);
+    if (st != BCH_OK) return st;
+  }
+  return from_hip(ctx, bch::launch_softmax_rows(ctx->stream, rows, cols, in, out, ctx->ws, ctx->ws_bytes),
+                  "softmax launch");
 }
 
 bch_status bch_softmax_axis(bch_ctx* ctx, long long outer, long long axis, long long inner,
@@ -323,7 +329,13 @@ bch_status bch_softmax_axis(bch_ctx* ctx, long long outer, long long axis, long 
   if (!in || !out) return fail(ctx, BCH_E_INVALID, "softmax_dim: NULL buffer");
   bch_status st = use(ctx);
   if (st != BCH_OK) return st;
-  return from_hip(ctx, bch::launch_softmax_axis(ctx->stream, outer, axis, inner, in, out),
+  size_t wsb = bch::softmax_axis_workspace_bytes(outer, axis, inner);
+  if (wsb) {
+    st = ensure_ws(ctx, wsb);
+    if (st != BCH_OK) return st;
+  }
+  return from_hip(ctx, bch::launch_softmax_axis(ctx->stream, outer, axis, inner, in, out, ctx->ws,
+                                                ctx->ws_bytes),
                   "softmax_dim launch");
 }
 

@@ -12,6 +12,12 @@
 //     l, l+64, ...) and stays in registers; max and sum are wavefront
 //     all-reductions built from DPP row operations plus four v_readlane
 //     across the 16-lane rows; the output is written once.
+//   * a few long rows (the global softmax of Tensor::softmax and the session
+//     is one row of every element): each row is cut into chunks, one
+//     workgroup per chunk.  Pass 1 writes each chunk's online (max, sum)
+//     to scratch; pass 2 merges the row's chunk states in every workgroup
+//     and writes its chunk.  Read, read, write: 12 bytes per element, with
+//     the whole chip busy instead of one CU per row.
 //   * anything else: one workgroup per row, an online (max, sum) pass and a
 //     second read that writes; scalar loads, any cols.
 //   * axis != last: one thread per (outer, inner) slice, coalesced across
@@ -149,19 +155,13 @@ __device__ __forceinline__ void merge_state(float& m, float& s, float m2, float 
   m = mn;
 }
 
-// One workgroup (256 threads) per row, any cols.
-__global__ __launch_bounds__(256) void softmax_rows_block(
-    const float* __restrict__ in, float* __restrict__ out, long long rows,
-    long long cols) {
+// Merge the (max, sum) states of the 256 threads of a workgroup; every
+// thread gets the result.  Must be reached by all threads of the block.
+__device__ __forceinline__ void block_merge(float& m, float& s) {
   __shared__ float sm[4], ss[4];
-  const long long row = blockIdx.x;
-  const float* x = in + row * cols;
-  float* y = out + row * cols;
-  float m = -INFINITY, s = 0.0f;
-  for (long long j = threadIdx.x; j < cols; j += 256) online_push(m, s, x[j]);
   // wave-level merge: all-reduce the max, rescale, all-reduce the sum
-  float wm = wave_allreduce(m, OpMax());
-  float ws = wave_allreduce(m == -INFINITY ? 0.0f : s * exp_f32(m - wm), OpSum());
+  const float wm = wave_allreduce(m, OpMax());
+  const float ws = wave_allreduce(m == -INFINITY ? 0.0f : s * exp_f32(m - wm), OpSum());
   const int w = threadIdx.x >> 6;
   if ((threadIdx.x & 63) == 0) {
     sm[w] = wm;
@@ -171,8 +171,87 @@ __global__ __launch_bounds__(256) void softmax_rows_block(
   float M = sm[0], S = ss[0];
 #pragma unroll
   for (int i = 1; i < 4; ++i) merge_state(M, S, sm[i], ss[i]);
-  const float inv = 1.0f / S;
-  for (long long j = threadIdx.x; j < cols; j += 256) y[j] = exp_f32(x[j] - M) * inv;
+  m = M;
+  s = S;
+}
+
+// One workgroup (256 threads) per row, any cols.
+__global__ __launch_bounds__(256) void softmax_rows_block(
+    const float* __restrict__ in, float* __restrict__ out, long long rows,
+    long long cols) {
+  const long long row = blockIdx.x;
+  const float* x = in + row * cols;
+  float* y = out + row * cols;
+  float m = -INFINITY, s = 0.0f;
+  for (long long j = threadIdx.x; j < cols; j += 256) online_push(m, s, x[j]);
+  block_merge(m, s);
+  const float inv = 1.0f / s;
+  for (long long j = threadIdx.x; j < cols; j += 256) y[j] = exp_f32(x[j] - m) * inv;
+}
+
+// Online update with four elements at once: one rescale per float4.
+__device__ __forceinline__ void online_push4(float& m, float& s, float4 v) {
+  const float vm = fmaxf(fmaxf(v.x, v.y), fmaxf(v.z, v.w));
+  if (vm > m) {
+    s *= exp_f32(m - vm);  // m == -inf: exp_f32 clamps to 0, s was 0
+    m = vm;
+  }
+  if (m != -INFINITY)  // NaN elements make s NaN, as in online_push
+    s += (exp_f32(v.x - m) + exp_f32(v.y - m)) + (exp_f32(v.z - m) + exp_f32(v.w - m));
+}
+
+// Split rows, pass 1: block (c, r) reduces chunk c of row r to (max, sum)
+// and stores it at part[2 * (r * gridDim.x + c)].  VEC: float4 loads
+// (cols % 4 == 0, 16-byte aligned input, chunk % 1024 == 0).
+template <bool VEC>
+__global__ __launch_bounds__(256) void softmax_split_stats(
+    const float* __restrict__ in, long long cols, long long chunk,
+    float* __restrict__ part) {
+  const long long r = blockIdx.y;
+  const long long j0 = (long long)blockIdx.x * chunk;
+  const long long j1 = j0 + chunk < cols ? j0 + chunk : cols;
+  const float* x = in + r * cols;
+  float m = -INFINITY, s = 0.0f;
+  if (VEC) {
+    for (long long j = j0 + 4 * threadIdx.x; j < j1; j += 1024)
+      online_push4(m, s, *reinterpret_cast<const float4*>(x + j));
+  } else {
+    for (long long j = j0 + threadIdx.x; j < j1; j += 256) online_push(m, s, x[j]);
+  }
+  block_merge(m, s);
+  if (threadIdx.x == 0) {
+    const long long p = 2 * (r * gridDim.x + blockIdx.x);
+    part[p] = m;
+    part[p + 1] = s;
+  }
+}
+
+// Split rows, pass 2: block (c, r) merges the gridDim.x chunk states of row
+// r and writes chunk c.  VEC as in pass 1, plus a 16-byte aligned output.
+template <bool VEC>
+__global__ __launch_bounds__(256) void softmax_split_write(
+    const float* __restrict__ in, float* __restrict__ out, long long cols,
+    long long chunk, const float* __restrict__ part) {
+  const long long r = blockIdx.y;
+  const float* pr = part + 2 * r * gridDim.x;
+  float m = -INFINITY, s = 0.0f;
+  for (unsigned c = threadIdx.x; c < gridDim.x; c += 256) merge_state(m, s, pr[2 * c], pr[2 * c + 1]);
+  block_merge(m, s);
+  const float inv = 1.0f / s;
+  const long long j0 = (long long)blockIdx.x * chunk;
+  const long long j1 = j0 + chunk < cols ? j0 + chunk : cols;
+  const float* x = in + r * cols;
+  float* y = out + r * cols;
+  if (VEC) {
+    for (long long j = j0 + 4 * threadIdx.x; j < j1; j += 1024) {
+      const float4 v = *reinterpret_cast<const float4*>(x + j);
+      const float4 o = make_float4(exp_f32(v.x - m) * inv, exp_f32(v.y - m) * inv,
+                                   exp_f32(v.z - m) * inv, exp_f32(v.w - m) * inv);
+      bch::store_nt(o, reinterpret_cast<float4*>(y + j));
+    }
+  } else {
+    for (long long j = j0 + threadIdx.x; j < j1; j += 256) y[j] = exp_f32(x[j] - m) * inv;
+  }
 }
 
 // Softmax along the middle axis of [outer, axis, inner], thread per slice.
@@ -205,11 +284,49 @@ bool wave_path(long long cols, const float* in, const float* out) {
          (reinterpret_cast<uintptr_t>(out) % 16) == 0;
 }
 
+// Split-row plan: rows that alone would leave most of the 256 CUs idle are
+// cut into chunks of a multiple of 1024 elements (at least 16 Ki) so that
+// about kSplitTarget workgroups run; at most kMaxSplits chunks per row.
+constexpr long long kSplitTarget = 2048;
+constexpr long long kMinChunk = 16384;
+constexpr long long kMaxSplits = 4096;
+
+struct SplitPlan {
+  long long splits = 1, chunk = 0;
+};
+
+SplitPlan split_plan(long long rows, long long cols) {
+  SplitPlan p;
+  if (pick_nv(cols) > 0 && (cols % 4) == 0) return p;  // wave path is one pass
+  long long want = (kSplitTarget + rows - 1) / rows;
+  long long most = (cols + kMinChunk - 1) / kMinChunk;
+  long long sp = want < most ? want : most;
+  if (sp > kMaxSplits) sp = kMaxSplits;
+  if (sp < 2) return p;
+  long long chunk = (cols + sp - 1) / sp;
+  chunk = (chunk + 1023) / 1024 * 1024;
+  p.splits = (cols + chunk - 1) / chunk;
+  p.chunk = chunk;
+  if (p.splits < 2) p.splits = 1;
+  return p;
+}
+
 }  // namespace
 
 namespace bch {
 
+size_t softmax_workspace_bytes(long long rows, long long cols) {
+  if (rows <= 0 || cols <= 0) return 0;
+  const SplitPlan p = split_plan(rows, cols);
+  return p.splits > 1 ? (size_t)(2 * rows * p.splits) * sizeof(float) : 0;
+}
+
+size_t softmax_axis_workspace_bytes(long long outer, long long axis, long long inner) {
+  return inner == 1 ? softmax_workspace_bytes(outer, axis) : 0;
+}
+
 const char* softmax_kernel_name(long long rows, long long cols) {
+  if (split_plan(rows, cols).splits > 1) return "softmax_split_write";
   if ((cols % 4) == 0) {
     switch (pick_nv(cols)) {
       case 1: return "softmax_rows_wave<1>";
@@ -224,8 +341,26 @@ const char* softmax_kernel_name(long long rows, long long cols) {
 }
 
 hipError_t launch_softmax_rows(hipStream_t s, long long rows, long long cols,
-                               const float* in, float* out) {
+                               const float* in, float* out, void* ws,
+                               size_t ws_bytes) {
   if (rows <= 0 || cols <= 0) return hipSuccess;
+  const SplitPlan sp = split_plan(rows, cols);
+  if (sp.splits > 1) {
+    if (!ws || ws_bytes < softmax_workspace_bytes(rows, cols) || rows > 65535)
+      return hipErrorInvalidValue;
+    float* part = static_cast<float*>(ws);
+    const bool vec = (cols % 4) == 0 && (reinterpret_cast<uintptr_t>(in) % 16) == 0 &&
+                     (reinterpret_cast<uintptr_t>(out) % 16) == 0;
+    dim3 grid((unsigned)sp.splits, (unsigned)rows), block(256);
+    if (vec) {
+      hipLaunchKernelGGL(softmax_split_stats<true>, grid, block, 0, s, in, cols, sp.chunk, part);
+      hipLaunchKernelGGL(softmax_split_write<true>, grid, block, 0, s, in, out, cols, sp.chunk, part);
+    } else {
+      hipLaunchKernelGGL(softmax_split_stats<false>, grid, block, 0, s, in, cols, sp.chunk, part);
+      hipLaunchKernelGGL(softmax_split_write<false>, grid, block, 0, s, in, out, cols, sp.chunk, part);
+    }
+    return hipGetLastError();
+  }
   if (wave_path(cols, in, out)) {
     const long long blocks = (rows + 3) / 4;
     if (blocks > 0x7fffffffLL) return hipErrorInvalidValue;
@@ -245,9 +380,10 @@ hipError_t launch_softmax_rows(hipStream_t s, long long rows, long long cols,
 }
 
 hipError_t launch_softmax_axis(hipStream_t s, long long outer, long long axis,
-                               long long inner, const float* in, float* out) {
+                               long long inner, const float* in, float* out,
+                               void* ws, size_t ws_bytes) {
   if (outer <= 0 || axis <= 0 || inner <= 0) return hipSuccess;
-  if (inner == 1) return launch_softmax_rows(s, outer, axis, in, out);
+  if (inner == 1) return launch_softmax_rows(s, outer, axis, in, out, ws, ws_bytes);
   const long long slices = outer * inner;
   const long long blocks = (slices + 255) / 256;
   if (blocks > 0x7fffffffLL) return hipErrorInvalidValue;

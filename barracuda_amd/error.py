@@ -36,6 +36,15 @@ class ShapeMismatch(BarracudaError):
         super().__init__(f"Shape mismatch: expected {self.expected}, got {self.actual}")
 
 
+class InvalidShape(BarracudaError):
+    """error.rs InvalidShape{expected, actual} (:31-38, constructor :275)."""
+
+    def __init__(self, expected, actual):
+        self.expected = list(expected)
+        self.actual = list(actual)
+        super().__init__(f"Invalid shape: expected {self.expected}, got {self.actual}")
+
+
 class InvalidOperation(BarracudaError):
     """error.rs InvalidOperation{op, reason} (:243)."""
 
@@ -65,6 +74,16 @@ class ExecutionError(BarracudaError):
 
     def __init__(self, message: str):
         super().__init__(f"Execution error: {message}")
+
+
+class CastOverflow(BarracudaError):
+    """error.rs CastOverflow{from_type, to_type, value_description} (:143-152), raised by
+    cast.rs:31-37 usize_as_u32."""
+
+    def __init__(self, from_type: str, to_type: str, value_description: str):
+        self.from_type, self.to_type = from_type, to_type
+        self.value_description = value_description
+        super().__init__(f"Cast overflow: {from_type} → {to_type} ({value_description})")
 
 
 class UnsupportedOperation(BarracudaError):

@@ -299,7 +299,19 @@ def _same_device(*ts: Tensor) -> HipDevice:
     return dev
 
 
+_I32_MAX = 2**31 - 1
+
+
+def _check_i32(op: str, dev: HipDevice, **dims: int) -> None:
+    """The C ABI takes GEMM / attention dimensions as int; ctypes would wrap a
+    larger value silently, so refuse it here."""
+    for name, v in dims.items():
+        if v > _I32_MAX:
+            raise UnsupportedOperation(op, f"{dev.name()} ({name}={v} exceeds 2^31-1)")
+
+
 def _sgemm(dev: HipDevice, m: int, n: int, k: int, a: Tensor, b: Tensor, op: str) -> Tensor:
+    _check_i32(op, dev, m=m, n=n, k=k)
     out = Tensor.empty([m, n], dev)
     if m * n == 0:
         return out
@@ -351,6 +363,7 @@ class BatchMatMul:
             raise ShapeMismatch(as_, bs)
         n = bs[2]
         dev = _same_device(self.a, self.b)
+        _check_i32("batch_matmul", dev, batch=batch, m=m, n=n, k=k)
         out = Tensor.empty([batch, m, n], dev)
         if batch * m * n == 0:
             return out
@@ -385,6 +398,7 @@ def _sdpa(dev: HipDevice, q: Tensor, k: Tensor, v: Tensor, causal: bool, op: str
           b: int, h: int, sq: int, skv: int, d: int) -> Tensor:
     if d > 128:
         raise UnsupportedOperation(op, f"{dev.name()} (head_dim {d} > 128)")
+    _check_i32(op, dev, batch=b, heads=h, q_len=sq, kv_len=skv)
     out = Tensor.empty(q.shape(), dev)
     if b * h * sq * d == 0:
         return out

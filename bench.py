@@ -145,6 +145,14 @@ def _bench_softmax(dev, T, reps):
                                  "bytes_per_launch": nbytes,
                                  "hbm_frac": nbytes / (ev * 1e-3) / 1e9 / HBM_PEAK_GBS,
                                  "traffic": load_traffic("softmax_65536x2048")}
+    # Tensor::softmax (global) over the same 2^27 elements as one row: the
+    # split-row path, two passes (12 bytes per element of traffic at least)
+    n = 65536 * 2048
+    wall, ev = T.run(lambda i: lib.bch_softmax_rows(ctx, 1, n, px, py), reps, 3)
+    out["softmax_global_2^27"] = {"GB/s": nbytes / (ev * 1e-3) / 1e9, "us": ev * 1e3,
+                                  "bytes_per_call": nbytes,
+                                  "hbm_frac": nbytes / (ev * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                                  "hbm_frac_of_12B_floor": 1.5 * nbytes / (ev * 1e-3) / 1e9 / HBM_PEAK_GBS}
     return out
 
 

@@ -15,6 +15,7 @@
 //   Tensor::scaled_dot_product_attention                   ops/scaled_dot_product_attention/mod.rs:81-226
 //   Tensor::causal_attention, CausalAttention              ops/causal_attn/mod.rs:64-158
 //   FlashAttention                                         ops/flash_attention.rs:45-146
+//   TensorSession, SessionTensor, AttentionDims            session/mod.rs:60-540, session/tensor.rs:14-68
 //   BarracudaError, Result<T>                              error.rs:14-130
 //
 // Every computation goes through the C ABI to the gfx950 kernels; there is
@@ -23,6 +24,8 @@
 // Rust; unwrap() on an error throws std::runtime_error with the message.
 #pragma once
 
+#include <array>
+#include <climits>
 #include <cmath>
 #include <cstddef>
 #include <cstdint>
@@ -50,6 +53,8 @@ enum class ErrorKind {
   ExecutionError,        // ExecutionError{message}
   UnsupportedOperation,  // UnsupportedOperation{op, device}
   DeviceLost,            // DeviceLost(String)
+  InvalidShape,          // InvalidShape{expected, actual}
+  CastOverflow,          // CastOverflow{from_type, to_type, value_description}
 };
 
 inline std::string shape_str(const std::vector<size_t>& s) {
@@ -67,6 +72,12 @@ struct BarracudaError {
   static BarracudaError shape_mismatch(const std::vector<size_t>& expected, const std::vector<size_t>& actual) {
     return {ErrorKind::ShapeMismatch,
             "Shape mismatch: expected " + shape_str(expected) + ", got " + shape_str(actual)};
+  }
+  static BarracudaError invalid_shape(const std::vector<size_t>& expected, const std::vector<size_t>& actual) {
+    return {ErrorKind::InvalidShape, "Invalid shape: expected " + shape_str(expected) + ", got " + shape_str(actual)};
+  }
+  static BarracudaError cast_overflow(const std::string& from, const std::string& to, const std::string& value) {
+    return {ErrorKind::CastOverflow, "Cast overflow: " + from + " → " + to + " (" + value + ")"};
   }
   static BarracudaError invalid_op(const std::string& op, const std::string& reason) {
     return {ErrorKind::InvalidOperation, "Invalid operation: " + op + " - " + reason};
@@ -162,6 +173,14 @@ inline size_t numel(const std::vector<size_t>& s) {
   for (size_t d : s) n *= d;
   return n;
 }
+
+// The C ABI takes GEMM / attention dimensions as int.
+inline std::optional<BarracudaError> check_i32(const char* op, std::initializer_list<size_t> dims) {
+  for (size_t d : dims)
+    if (d > (size_t)INT_MAX)
+      return BarracudaError::unsupported(op, "hip:gfx950 (dimension " + std::to_string(d) + " exceeds 2^31-1)");
+  return std::nullopt;
+}
 }  // namespace detail
 
 // ---------------------------------------------------------------- tensor
@@ -248,6 +267,7 @@ struct MatMul {
   }
   Result<Tensor> execute() const {
     if (auto e = validate(lhs.shape(), rhs.shape())) return *e;
+    if (auto e = detail::check_i32("matmul", {lhs.shape()[0], lhs.shape()[1], rhs.shape()[1]})) return *e;
     const int m = (int)lhs.shape()[0], k = (int)lhs.shape()[1], n = (int)rhs.shape()[1];
     auto dev = lhs.device();
     auto r = Tensor::empty({(size_t)m, (size_t)n}, dev);
@@ -277,10 +297,11 @@ struct BatchMatMul {
   }
   Result<Tensor> execute() const {
     if (auto e = validate(a.shape(), b.shape())) return *e;
+    if (auto e = detail::check_i32("batch_matmul", {a.shape()[0], a.shape()[1], a.shape()[2], b.shape()[2]})) return *e;
     const int batch = (int)a.shape()[0], m = (int)a.shape()[1], k = (int)a.shape()[2], n = (int)b.shape()[2];
     auto dev = a.device();
     auto r = Tensor::empty({(size_t)batch, (size_t)m, (size_t)n}, dev);
-    if (r.is_err() || batch * m * n == 0) return r;
+    if (r.is_err() || (size_t)batch * m * n == 0) return r;
     Tensor out = std::move(r).unwrap();
     std::lock_guard<std::mutex> g(dev->mutex());
     if (auto e = dev->check(bch_sgemm_strided_batched(dev->ctx(), batch, m, n, k, a.data_ptr(), (long long)m * k,
@@ -323,17 +344,19 @@ inline std::optional<BarracudaError> validate_softmax_dim(const std::vector<size
 }
 
 namespace detail {
-inline Result<Tensor> sdpa(const Tensor& q, const Tensor& k, const Tensor& v, bool causal, const char* op, int B,
-                           int H, int Sq, int Skv, int D) {
+inline Result<Tensor> sdpa(const Tensor& q, const Tensor& k, const Tensor& v, bool causal, const char* op, size_t B,
+                           size_t H, size_t Sq, size_t Skv, size_t D) {
   auto dev = q.device();
   if (D > 128) return BarracudaError::unsupported(op, dev->name() + " (head_dim " + std::to_string(D) + " > 128)");
+  if (auto e = check_i32(op, {B, H, Sq, Skv})) return *e;
   auto r = Tensor::empty(q.shape(), dev);
   if (r.is_err() || (size_t)B * H * Sq * D == 0) return r;
   if (Skv == 0) return BarracudaError::invalid_op(op, "key sequence is empty (shape/dimension mismatch)");
   Tensor out = std::move(r).unwrap();
   const float scale = 1.0f / std::sqrt((float)D);
   std::lock_guard<std::mutex> g(dev->mutex());
-  if (auto e = dev->check(bch_sdpa_fwd(dev->ctx(), B, H, Sq, Skv, D, scale, causal ? 1 : 0, q.data_ptr(), k.data_ptr(),
+  if (auto e = dev->check(bch_sdpa_fwd(dev->ctx(), (int)B, (int)H, (int)Sq, (int)Skv, (int)D, scale, causal ? 1 : 0,
+                                       q.data_ptr(), k.data_ptr(),
                                        v.data_ptr(), out.data_ptr()),
                           op))
     return *e;
@@ -363,7 +386,7 @@ struct Attention {
   Result<Tensor> execute() const {
     if (auto e = validate(q.shape(), k.shape(), v.shape())) return *e;
     const auto& s = q.shape();
-    return detail::sdpa(q, k, v, false, "attention", (int)s[0], (int)s[1], (int)s[2], (int)k.shape()[2], (int)s[3]);
+    return detail::sdpa(q, k, v, false, "attention", s[0], s[1], s[2], k.shape()[2], s[3]);
   }
 };
 
@@ -384,8 +407,7 @@ struct ScaledDotProductAttention {
     if (q.device() != k.device() || q.device() != v.device())
       return BarracudaError::device("Q, K, V must be on the same device");
     const auto& s = q.shape();
-    return detail::sdpa(q, k, v, false, "scaled_dot_product_attention", (int)s[0], (int)s[1], (int)s[2], (int)s[2],
-                        (int)s[3]);
+    return detail::sdpa(q, k, v, false, "scaled_dot_product_attention", s[0], s[1], s[2], s[2], s[3]);
   }
 };
 
@@ -405,7 +427,7 @@ struct CausalAttention {
   Result<Tensor> execute() const {
     if (auto e = validate(q.shape(), k.shape(), v.shape())) return *e;
     const auto& s = q.shape();
-    return detail::sdpa(q, k, v, true, "causal_attention", (int)s[0], (int)s[1], (int)s[2], (int)s[2], (int)s[3]);
+    return detail::sdpa(q, k, v, true, "causal_attention", s[0], s[1], s[2], s[2], s[3]);
   }
 };
 
@@ -429,7 +451,7 @@ struct FlashAttention {
   }
   Result<Tensor> execute() const {
     if (auto e = validate(q.shape(), k.shape(), v.shape())) return *e;
-    const int S = (int)q.shape()[0], D = (int)q.shape()[1];
+    const size_t S = q.shape()[0], D = q.shape()[1];
     return detail::sdpa(q, k, v, false, "FlashAttention", 1, 1, S, S, D);
   }
 };
@@ -464,5 +486,247 @@ inline Result<Tensor> Tensor::scaled_dot_product_attention(const Tensor& key, co
 inline Result<Tensor> Tensor::causal_attention(const Tensor& key, const Tensor& value) const {
   return CausalAttention{*this, key, value}.execute();
 }
+
+// ---------------------------------------------------------------- session
+// The unit value of Result<()>.
+struct Unit {};
+
+// session/mod.rs:60-99: the [B, H, S, D] dimensions of an attention op.
+struct AttentionDims {
+  size_t batch_size = 0;
+  size_t n_heads = 0;
+  size_t seq_len = 0;
+  size_t head_dim = 0;
+  size_t total_elements() const { return batch_size * n_heads * seq_len * head_dim; }
+  // (batch_size, seq_len, n_heads, head_dim), each checked to fit u32
+  // (cast.rs:31-37 usize_as_u32)
+  Result<std::array<uint32_t, 4>> as_u32() const {
+    const size_t v[4] = {batch_size, seq_len, n_heads, head_dim};
+    std::array<uint32_t, 4> out{};
+    for (int i = 0; i < 4; ++i) {
+      if (v[i] > (size_t)UINT32_MAX) return BarracudaError::cast_overflow("usize", "u32", std::to_string(v[i]));
+      out[i] = (uint32_t)v[i];
+    }
+    return out;
+  }
+};
+
+class TensorSession;
+
+// session/tensor.rs:14-68: a buffer owned by a session, with its shape.  The
+// buffer exists from creation; an op's output reads as zeros until
+// TensorSession::run() has executed the op.
+class SessionTensor {
+ public:
+  const std::vector<size_t>& shape() const { return shape_; }
+  size_t len() const { return detail::numel(shape_); }
+  bool is_empty() const { return len() == 0; }
+  size_t buffer_id() const { return id_; }
+  Result<std::vector<float>> to_vec() const {
+    std::vector<float> out(len());
+    if (!out.empty()) {
+      std::lock_guard<std::mutex> g(buf_->dev->mutex());
+      if (auto e = buf_->dev->check(
+              bch_download(buf_->dev->ctx(), out.data(), buf_->ptr, out.size() * sizeof(float)), "download"))
+        return *e;
+    }
+    return out;
+  }
+  // a standalone Tensor holding a copy (tensor.rs:64-67)
+  Result<Tensor> to_tensor() const {
+    auto v = to_vec();
+    if (v.is_err()) return v.error();
+    return Tensor::from_data(v.value(), shape_, buf_->dev);
+  }
+
+ private:
+  friend class TensorSession;
+  SessionTensor(const void* owner, size_t id, std::shared_ptr<detail::DeviceBuffer> b, std::vector<size_t> s)
+      : owner_(owner), id_(id), buf_(std::move(b)), shape_(std::move(s)) {}
+  const void* owner_;
+  size_t id_;
+  std::shared_ptr<detail::DeviceBuffer> buf_;
+  std::vector<size_t> shape_;
+};
+
+// session/mod.rs:118-540: ops are recorded, then run() enqueues them all, in
+// order, on the device's one stream and waits once.  Outputs are allocated
+// (zero-filled) when an op is recorded.  Routed to this library's kernels
+// with grids that cover the whole problem, so the reference session's
+// dispatch defects (partial non-square matmul tiers, session/types.rs:53-58;
+// a one-workgroup softmax, dispatch.rs:217; an attention grid over the
+// 65,535 limit, dispatch.rs:289-295) are not reproduced.  softmax is the
+// global softmax over every element, what the reference session's shader
+// computes for each output it writes; attention is non-causal.
+class TensorSession {
+ public:
+  explicit TensorSession(std::shared_ptr<HipDevice> dev) : dev_(std::move(dev)) {}
+  static TensorSession with_device(std::shared_ptr<HipDevice> dev) { return TensorSession(std::move(dev)); }
+  TensorSession(const TensorSession&) = delete;
+  TensorSession& operator=(const TensorSession&) = delete;
+  TensorSession(TensorSession&&) = delete;
+
+  // session/mod.rs:155-165
+  void reset() {
+    ops_.clear();
+    executed_ = false;
+  }
+  size_t num_ops() const { return ops_.size(); }
+  bool executed() const { return executed_; }
+
+  // session/mod.rs:172-198
+  Result<SessionTensor> tensor(const std::vector<float>& data) { return tensor_with_shape(data, {data.size()}); }
+  Result<SessionTensor> tensor_with_shape(const std::vector<float>& data, const std::vector<size_t>& shape) {
+    if (data.size() != detail::numel(shape)) return BarracudaError::invalid_shape(shape, {data.size()});
+    auto b = alloc(shape, false);
+    if (b.is_err()) return b.error();
+    if (!data.empty()) {
+      std::lock_guard<std::mutex> g(dev_->mutex());
+      if (auto e = dev_->check(bch_upload(dev_->ctx(), b.value()->ptr, data.data(), data.size() * sizeof(float)),
+                               "upload"))
+        return *e;
+    }
+    return reg(std::move(b).unwrap(), shape);
+  }
+  // session/mod.rs:204-207: the copy stays in HBM (device to device) instead
+  // of the reference's read-back and re-upload; the result is the same.
+  Result<SessionTensor> import(const Tensor& t) {
+    if (t.device() != dev_) {
+      auto v = t.to_vec();
+      if (v.is_err()) return v.error();
+      return tensor_with_shape(v.value(), t.shape());
+    }
+    auto b = alloc(t.shape(), false);
+    if (b.is_err()) return b.error();
+    if (b.value()->bytes) {
+      std::lock_guard<std::mutex> g(dev_->mutex());
+      if (auto e = dev_->check(bch_copy(dev_->ctx(), b.value()->ptr, t.data_ptr(), b.value()->bytes), "import"))
+        return *e;
+    }
+    return reg(std::move(b).unwrap(), t.shape());
+  }
+
+  // session/mod.rs:305-333: output[m x n] = a[m x k] b[k x n]
+  Result<SessionTensor> matmul(const SessionTensor& a, const SessionTensor& b) {
+    if (auto e = own({&a, &b})) return *e;
+    if (a.shape().size() != 2 || b.shape().size() != 2) return BarracudaError::invalid_shape(a.shape(), b.shape());
+    const size_t m = a.shape()[0], k = a.shape()[1];
+    if (b.shape()[0] != k) return BarracudaError::shape_mismatch({m, k}, b.shape());
+    const size_t n = b.shape()[1];
+    for (size_t d : {m, k, n})  // session/mod.rs:327-329 usize_as_u32
+      if (d > (size_t)UINT32_MAX) return BarracudaError::cast_overflow("usize", "u32", std::to_string(d));
+    if (auto e = detail::check_i32("matmul", {m, k, n})) return *e;
+    auto out = alloc_output({m, n});
+    if (out.is_ok()) ops_.push_back({Op::MatMul, {a.id_, b.id_, out.value().id_, 0}, {m, k, n, 0}});
+    return out;
+  }
+
+  // session/mod.rs:364-371, over every element (dispatch.rs:211)
+  Result<SessionTensor> softmax(const SessionTensor& a) {
+    if (auto e = own({&a})) return *e;
+    auto out = alloc_output(a.shape());
+    if (out.is_ok()) ops_.push_back({Op::Softmax, {a.id_, out.value().id_, 0, 0}, {a.len(), 0, 0, 0}});
+    return out;
+  }
+
+  // session/mod.rs:481-518: softmax(Q K^T / sqrt(D)) V over [B, H, S, D]
+  Result<SessionTensor> attention(const SessionTensor& q, const SessionTensor& k, const SessionTensor& v,
+                                  const AttentionDims& dims) {
+    if (auto e = own({&q, &k, &v})) return *e;
+    const size_t expected = dims.total_elements();
+    const std::pair<const char*, const SessionTensor*> qkv[3] = {{"q", &q}, {"k", &k}, {"v", &v}};
+    for (const auto& [name, t] : qkv)
+      if (t->len() != expected)
+        return BarracudaError::invalid_input(std::string("attention: ") + name + " len " + std::to_string(t->len()) +
+                                             " ≠ B×H×S×D=" + std::to_string(expected));
+    if (auto e = dims.as_u32(); e.is_err()) return e.error();
+    if (dims.head_dim > 128)
+      return BarracudaError::unsupported("attention",
+                                         dev_->name() + " (head_dim " + std::to_string(dims.head_dim) + " > 128)");
+    if (auto e = detail::check_i32("attention", {dims.batch_size, dims.n_heads, dims.seq_len})) return *e;
+    auto out = alloc_output({dims.batch_size, dims.n_heads, dims.seq_len, dims.head_dim});
+    if (out.is_ok())
+      ops_.push_back({Op::Attention, {q.id_, k.id_, v.id_, out.value().id_},
+                      {dims.batch_size, dims.n_heads, dims.seq_len, dims.head_dim}});
+    return out;
+  }
+
+  // session/mod.rs:521-540: every recorded op, in order, one wait.  A launch
+  // error stops the batch; ops enqueued before it have been submitted.
+  Result<Unit> run() {
+    if (ops_.empty()) return Unit{};
+    std::lock_guard<std::mutex> g(dev_->mutex());
+    bch_ctx* c = dev_->ctx();
+    auto p = [this](size_t id) { return static_cast<float*>(bufs_[id]->ptr); };
+    for (const Op& op : ops_) {
+      bch_status st = BCH_OK;
+      const char* name = "run";
+      switch (op.kind) {
+        case Op::MatMul: {
+          const int m = (int)op.dim[0], k = (int)op.dim[1], n = (int)op.dim[2];
+          const int lk = k > 1 ? k : 1, ln = n > 1 ? n : 1;
+          name = "matmul";
+          if (m && n) st = bch_sgemm(c, m, n, k, p(op.buf[0]), lk, p(op.buf[1]), ln, p(op.buf[2]), ln);
+          break;
+        }
+        case Op::Softmax:
+          name = "softmax";
+          if (op.dim[0]) st = bch_softmax_rows(c, 1, (long long)op.dim[0], p(op.buf[0]), p(op.buf[1]));
+          break;
+        case Op::Attention: {
+          const size_t B = op.dim[0], H = op.dim[1], S = op.dim[2], D = op.dim[3];
+          name = "attention";
+          if (B * H * S * D != 0)
+            st = bch_sdpa_fwd(c, (int)B, (int)H, (int)S, (int)S, (int)D, 1.0f / std::sqrt((float)D), 0,
+                              p(op.buf[0]), p(op.buf[1]), p(op.buf[2]), p(op.buf[3]));
+          break;
+        }
+      }
+      if (auto e = dev_->check(st, name)) return *e;
+    }
+    if (auto e = dev_->check(bch_sync(c), "run")) return *e;
+    executed_ = true;
+    return Unit{};
+  }
+
+ private:
+  struct Op {
+    enum Kind { MatMul, Softmax, Attention } kind;
+    size_t buf[4];
+    size_t dim[4];
+  };
+
+  Result<std::shared_ptr<detail::DeviceBuffer>> alloc(const std::vector<size_t>& shape, bool zero) {
+    auto buf = std::make_shared<detail::DeviceBuffer>();
+    buf->dev = dev_;
+    buf->bytes = detail::numel(shape) * sizeof(float);
+    if (buf->bytes) {
+      std::lock_guard<std::mutex> g(dev_->mutex());
+      if (auto e = dev_->check(bch_alloc(dev_->ctx(), buf->bytes, &buf->ptr), "alloc_buffer")) return *e;
+      if (zero)
+        if (auto e = dev_->check(bch_memset(dev_->ctx(), buf->ptr, 0, buf->bytes), "alloc_output")) return *e;
+    }
+    return buf;
+  }
+  SessionTensor reg(std::shared_ptr<detail::DeviceBuffer> b, const std::vector<size_t>& shape) {
+    bufs_.push_back(b);
+    return SessionTensor(this, bufs_.size() - 1, std::move(b), shape);
+  }
+  Result<SessionTensor> alloc_output(const std::vector<size_t>& shape) {
+    auto b = alloc(shape, true);
+    if (b.is_err()) return b.error();
+    return reg(std::move(b).unwrap(), shape);
+  }
+  std::optional<BarracudaError> own(std::initializer_list<const SessionTensor*> ts) const {
+    for (const SessionTensor* t : ts)
+      if (t->owner_ != this) return BarracudaError::invalid_input("session tensor belongs to another TensorSession");
+    return std::nullopt;
+  }
+
+  std::shared_ptr<HipDevice> dev_;
+  std::vector<std::shared_ptr<detail::DeviceBuffer>> bufs_;
+  std::vector<Op> ops_;
+  bool executed_ = false;
+};
 
 }  // namespace barracuda

@@ -101,6 +101,16 @@ void cpu_tests() {
     REQUIRE(BarracudaError::from_status(BCH_E_NO_DEVICE, "x", "op").kind == ErrorKind::Device);
     REQUIRE(BarracudaError::from_status(BCH_E_UNSUPPORTED, "x", "op").kind == ErrorKind::UnsupportedOperation);
   });
+  run("attention_dims_and_session_errors", [] {  // session/mod.rs:78-98, error.rs:436-445
+    AttentionDims d{4, 32, 2048, 128};
+    REQUIRE(d.total_elements() == 4ull * 32 * 2048 * 128);
+    auto u = d.as_u32().unwrap();
+    REQUIRE(u[0] == 4 && u[1] == 2048 && u[2] == 32 && u[3] == 128);  // (batch, seq, heads, dim)
+    auto big = AttentionDims{1, 1, (size_t)UINT32_MAX + 1, 1}.as_u32();
+    REQUIRE(big.is_err() && big.error().kind == ErrorKind::CastOverflow);
+    REQUIRE(big.error().message == "Cast overflow: usize → u32 (4294967296)");
+    REQUIRE(BarracudaError::invalid_shape({1, 2, 3}, {1, 2}).message == "Invalid shape: expected [1, 2, 3], got [1, 2]");
+  });
 }
 
 // ---------------------------------------------------------------- GPU tests
@@ -267,6 +277,80 @@ void gpu_tests() {
   run("test_tensor_from_data_size_mismatch", [] {
     auto r = Tensor::from_data({1, 2, 3}, {2, 2}, g_dev);
     REQUIRE(r.is_err() && r.error().kind == ErrorKind::ShapeMismatch);
+  });
+
+  // session/mod.rs tests
+  run("test_session_matmul_2x2", [] {  // session/mod.rs:678-694
+    TensorSession s(g_dev);
+    auto a = s.tensor_with_shape({1, 2, 3, 4}, {2, 2}).unwrap();
+    auto b = s.tensor_with_shape({5, 6, 7, 8}, {2, 2}).unwrap();
+    auto c = s.matmul(a, b).unwrap();
+    REQUIRE((c.shape() == std::vector<size_t>{2, 2}));
+    s.run().unwrap();
+    auto r = c.to_vec().unwrap();
+    const float e[4] = {19, 22, 43, 50};
+    for (int i = 0; i < 4; ++i) REQUIRE(std::fabs(r[i] - e[i]) < 0.01f);
+  });
+  run("test_session_reset_and_reuse", [] {  // session/mod.rs:710-723, with matmul for add
+    TensorSession s(g_dev);
+    auto a = s.tensor_with_shape({1, 2}, {1, 2}).unwrap();
+    auto b = s.tensor_with_shape({3, 4}, {2, 1}).unwrap();
+    auto c = s.matmul(a, b).unwrap();
+    REQUIRE(c.to_vec().unwrap()[0] == 0.0f);  // allocated, not yet computed
+    s.run().unwrap();
+    REQUIRE(c.to_vec().unwrap()[0] == 11.0f);
+    s.reset();
+    REQUIRE(s.num_ops() == 0 && !s.executed());
+    auto z = s.softmax(s.tensor({0, 0, 0, 0}).unwrap()).unwrap();
+    s.run().unwrap();
+    for (float x : z.to_vec().unwrap()) REQUIRE(x == 0.25f);
+    REQUIRE(c.to_tensor().unwrap().to_vec().unwrap()[0] == 11.0f);
+  });
+  run("test_session_ops_match_tensor_ops", [] {
+    // non-square matmul, softmax over > 256 elements, attention: the session
+    // runs the same kernels as the Tensor ops, so results are bit-identical
+    const size_t m = 37, k = 300, n = 129;
+    std::vector<float> a(m * k), b(k * n);
+    for (size_t i = 0; i < a.size(); ++i) a[i] = (float)((i * 7919) % 23) / 11.0f - 1.0f;
+    for (size_t i = 0; i < b.size(); ++i) b[i] = (float)((i * 104729) % 19) / 9.0f - 1.0f;
+    TensorSession s(g_dev);
+    auto sc = s.matmul(s.tensor_with_shape(a, {m, k}).unwrap(), s.tensor_with_shape(b, {k, n}).unwrap()).unwrap();
+    auto sp = s.softmax(sc).unwrap();
+    const size_t B = 2, H = 3, S = 40, D = 16;
+    std::vector<float> q(B * H * S * D);
+    for (size_t i = 0; i < q.size(); ++i) q[i] = (float)((i * 31) % 17) / 8.0f - 1.0f;
+    auto tq = s.tensor(q).unwrap();
+    auto so = s.attention(tq, tq, tq, AttentionDims{B, H, S, D}).unwrap();
+    REQUIRE(s.num_ops() == 3);
+    REQUIRE((so.shape() == std::vector<size_t>{B, H, S, D}));
+    s.run().unwrap();
+    auto c = T(a, {m, k}).matmul(T(b, {k, n})).unwrap();
+    REQUIRE(sc.to_vec().unwrap() == c.to_vec().unwrap());
+    REQUIRE(sp.to_vec().unwrap() == c.softmax().unwrap().to_vec().unwrap());
+    auto qt = T(q, {B, H, S, D});
+    REQUIRE(so.to_vec().unwrap() == qt.attention(qt, qt).unwrap().to_vec().unwrap());
+    auto ref = matmul_cpu(a, b, m, k, n);
+    auto got = sc.to_vec().unwrap();
+    for (size_t i = 0; i < ref.size(); ++i) REQUIRE(std::fabs(got[i] - ref[i]) <= 1e-4f * std::fmax(1.0f, std::fabs(ref[i])));
+  });
+  run("test_session_validation", [] {
+    TensorSession s(g_dev);
+    auto r = s.tensor_with_shape({0, 0, 0, 0, 0}, {2, 3});
+    REQUIRE(r.is_err() && r.error().message == "Invalid shape: expected [2, 3], got [5]");
+    auto a3 = s.tensor_with_shape(std::vector<float>(8), {2, 2, 2}).unwrap();
+    auto a2 = s.tensor_with_shape(std::vector<float>(6), {2, 3}).unwrap();
+    auto b2 = s.tensor_with_shape(std::vector<float>(8), {2, 4}).unwrap();
+    REQUIRE(s.matmul(a3, b2).error().kind == ErrorKind::InvalidShape);
+    REQUIRE(s.matmul(a2, b2).error().message == "Shape mismatch: expected [2, 3], got [2, 4]");
+    auto q = s.tensor(std::vector<float>(16)).unwrap();
+    auto bad = s.tensor(std::vector<float>(15)).unwrap();
+    auto e = s.attention(q, bad, q, AttentionDims{1, 2, 4, 2});
+    REQUIRE(e.is_err() && e.error().message == "Invalid input: attention: k len 15 ≠ B×H×S×D=16");
+    TensorSession other(g_dev);
+    auto foreign = other.tensor({1}).unwrap();
+    REQUIRE(s.softmax(foreign).error().kind == ErrorKind::InvalidInput);
+    REQUIRE(s.num_ops() == 0);
+    s.run().unwrap();  // nothing recorded: no-op
   });
 }
 
