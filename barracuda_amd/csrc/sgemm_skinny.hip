@@ -6,26 +6,32 @@
 // small m.  Contract unchanged: C[m,n] = sum_p A[m,p] B[p,n], f32.
 //
 // The job is streaming B ([k, n] row-major, k*n*4 bytes) from HBM once.
-// Two kernels write split-k partials; a third sums them in split order, so
-// the result is deterministic:
+// The main kernels write split-k partials; a second kernel sums each
+// output's partials in a fixed order, so results are deterministic.
 //   * m <= 4, sgemm_skinny_fma: a wavefront owns 256 columns (lane l holds
 //     columns 4l..4l+3, one 1 KB row segment per load); the four wavefronts
 //     of a workgroup take interleaved rows with 8 row loads in flight; A[i][k]
-//     is wave-uniform and comes through the scalar cache.
-//   * 4 < m <= 32, sgemm_skinny_mfma: at 2m multiply-adds per B element the
+//     is wave-uniform and comes through the scalar cache.  k is split 16 ways.
+//   * 4 < m <= 32, sgemm_skinny_sk: at 2m multiply-adds per B element the
 //     non-packed FP32 VALU cannot keep up with HBM, so v_mfma_f32_16x16x4_f32
-//     computes C^T = B^T A^T (m padded to 16 or 32).  Lane l = 16q + i loads
-//     float4 B[k][n0 + 4i .. +3] and feeds component c to MFMA block c; in a
-//     16-row chunk lane quarter q takes rows 4q + s in step s.  The four
-//     wavefronts of a workgroup cover 4 x 64 adjacent columns of the same
-//     rows (1 KB per row per workgroup).  The workgroup's A^T slice is staged
-//     once in LDS (zero past m and past the k range), so every chunk is
-//     branch-free: B rows past the range are clamped to the last valid row
-//     (an L2 hit) and meet zeros in A.  B loads run PF chunks ahead.
+//     computes C^T = B^T A^T (m padded to 16 or 32).  The work is cut into
+//     units of 16 rows x 256 columns (4 wavefronts x 64 columns), ordered
+//     column group by column group, and every workgroup takes an equal
+//     contiguous run of units (stream-K): with one workgroup per CU every
+//     CU streams the same number of bytes.  A run crosses at most a few
+//     column-group boundaries; each run segment leaves one partial block.
+//     In a unit, lane l = 16q + i loads float4 B[k][n0 + 4i .. +3] and feeds
+//     component c to MFMA block c; lane quarter q takes rows 4q + s in step s.
+//     The workgroup's A^T slice (all of its units) is staged in LDS once,
+//     with direct-to-LDS 16-byte loads in a rolled loop; B loads run PF
+//     units ahead of the MFMAs.
 //   * Measured on MI355X (K 4096, N 11008, weights rotated past the 256 MB
-//     Infinity Cache): cross-XCD release/acquire fences for an in-kernel
-//     "last workgroup reduces" cost ~75 us per call, so the split reduction
-//     is a separate launch (~3 us).
+//     Infinity Cache): the stream-K layout removes the tail of an uneven
+//     grid (516 workgroups on 256 CUs); kernel code is kept small (one
+//     unrolled pipeline step, rolled staging), as every CU fetches the whole
+//     kernel from L2 once per launch; cross-XCD release/acquire fences for
+//     an in-kernel "last workgroup reduces" cost ~75 us per call, so the
+//     reduction is a separate launch.
 #include "bch_internal.h"
 
 #include <stdint.h>
@@ -33,12 +39,16 @@
 namespace {
 
 typedef float f32x4v __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void;
 
-constexpr int kFmaCols = 256;   // columns per workgroup, FMA kernel
+constexpr int kFmaCols = 256;  // columns per workgroup, FMA kernel
 constexpr int kFmaUnroll = 8;
-constexpr int kMmaCols = 256;   // columns per workgroup, MFMA kernel (4 x 64)
-constexpr int kStageF4 = 16;    // float4 of A staged per thread (MFMA kernel)
-constexpr int kPF = 2;          // chunks of B in flight ahead of the MFMAs
+constexpr int kFmaSplits = 16;
+constexpr int kSkCols = 256;   // columns per unit / column group (4 x 64)
+constexpr int kSkRows = 16;    // rows per unit
+constexpr int kSkPF = 4;       // units of B in flight ahead of the MFMAs
+constexpr int kSkWGs = 256;    // one workgroup per CU
+constexpr int kLdsBytes = 160 * 1024;
 
 // ---------------------------------------------------------------- m <= 4
 template <int MT>
@@ -101,46 +111,114 @@ __global__ __launch_bounds__(256) void sgemm_skinny_fma(int M, int N, int K, con
   }
 }
 
+// C[m][n] = sum over splits s < splits, in split order, of P[s][m][n].  The
+// loads of a batch of 16 partials are all in flight before the adds.
+__global__ __launch_bounds__(256) void sgemm_skinny_reduce(int M, int N, const float* __restrict__ P, int splits,
+                                                           float* __restrict__ C, int ldc) {
+  const long long t = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (t >= (long long)M * N) return;
+  const long long ps = (long long)M * N;
+  float s = 0.f;
+  for (int i = 0; i < splits; i += 16) {
+    float v[16];
+#pragma unroll
+    for (int q = 0; q < 16; ++q) v[q] = P[(long long)min(i + q, splits - 1) * ps + t];
+#pragma unroll
+    for (int q = 0; q < 16; ++q)
+      if (i + q < splits) s += v[q];
+  }
+  C[(t / N) * ldc + t % N] = s;
+}
+
 // ---------------------------------------------------------------- 4 < m <= 32
-template <int MB>  // m blocks of 16
-__global__ __launch_bounds__(256) void sgemm_skinny_mfma(int M, int N, int K, const float* __restrict__ A,
-                                                         int lda, const float* __restrict__ B, int ldb,
-                                                         float* __restrict__ P, int kchunk, int avec) {
+// Stream-K unit bookkeeping: U units, G workgroups, workgroup w owns units
+// [w U / G, (w + 1) U / G).  The workgroup holding unit u:
+__host__ __device__ inline int wg_of_unit(long long u, long long U, int G) { return (int)(((u + 1) * G - 1) / U); }
+
+constexpr int vmcnt_imm(int n) { return (n & 0xF) | (0x7 << 4) | (0xF << 8) | ((n >> 4) << 14); }
+
+// Partial block of (column group g, slot s): P[((g * smax + s) * M + m) * 256 + column - 256 g], the slot
+// being the workgroup's position among those covering g.  DMA: A^T staged
+// with direct-to-LDS 16-byte loads (lda % 4 == 0, K % 4 == 0, A 16-byte
+// aligned); otherwise with scalar loads.
+template <int MB, bool DMA>
+__global__ __launch_bounds__(256, 1) void sgemm_skinny_sk(int M, int N, int K, const float* __restrict__ A,
+                                                          int lda, const float* __restrict__ B, int ldb,
+                                                          float* __restrict__ P, long long U, int G, int kb,
+                                                          int smax) {
   extern __shared__ float4 smem4[];
-  float* xs = reinterpret_cast<float*>(smem4);  // [16 MB][nch*16 + 4]
+  float* xs = reinterpret_cast<float*>(smem4);  // A^T: [16 MB][16 nu + 4]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int lq = lane >> 4, li = lane & 15;
-  const int n0 = blockIdx.x * kMmaCols + 64 * wave;
-  const int nl = min(n0 + 4 * li, N - 4);  // columns past N are computed and dropped
-  const int kbeg = blockIdx.y * kchunk, kend = min(K, kbeg + kchunk);
-  const int nch = kend > kbeg ? (kend - kbeg + 15) / 16 : 0;
-  const int ld = nch * 16 + 4;
+  const int w = blockIdx.x;
+  const long long ub = (long long)w * U / G, ue = (long long)(w + 1) * U / G;
+  const int nu = (int)(ue - ub);
+  const int g0 = (int)(ub / kb), t0 = (int)(ub - (long long)g0 * kb);
+  const int q4 = 4 * nu;  // float4 per staged row
+  const int ldu = 4 * q4 + 4;
+  constexpr int PF = kSkPF, NB = kSkPF + 1;
 
-  // stage A^T: all loads issued before the LDS writes
-  {
-    const int q4 = nch * 4;
-    const int total = MB * 16 * q4;
-    float4 r[kStageF4];
+  // B cursor: unit (lg, lt); advanced once per load, held at the last unit.
+  float4 wv[NB][4];
+  int lg = g0, lt = t0, lcount = 0;
+  auto load = [&](int sb) {
+    const float* bp = B + min(lg * kSkCols + 64 * wave + 4 * li, N - 4);
+    const int r0 = kSkRows * lt + 4 * lq;
 #pragma unroll
-    for (int u = 0; u < kStageF4; ++u) {
-      const int e = tid + u * 256;
-      const int m = q4 ? e / q4 : 0, kq = q4 ? e % q4 : 0;
-      const int kk = kbeg + 4 * kq;
-      const float* ar = A + (long long)m * lda + kk;
-      if (e < total && m < M && kk + 3 < kend && avec) {
-        r[u] = *reinterpret_cast<const float4*>(ar);
-      } else {
-        float t[4];
+    for (int s = 0; s < 4; ++s)
+      wv[sb][s] = bch::load_nt(reinterpret_cast<const float4*>(bp + (long long)min(r0 + s, K - 1) * ldb));
+    ++lcount;  // uniform arithmetic, no branch between the loads
+    lt += lcount < nu ? 1 : 0;
+    const int wrap = lt == kb ? 1 : 0;
+    lt -= wrap * kb;
+    lg += wrap;
+  };
+  // k of staged float4 q (its unit is t0 + q / 4, wrapped into the next column group)
+  auto k_of = [&](int q) {
+    int t = t0 + (q >> 2);
+    while (t >= kb) t -= kb;
+    return kSkRows * t + 4 * (q & 3);
+  };
+
+  // padding rows M .. 16 MB - 1 first: LDS stores after the direct loads would wait for them
+  for (int e = M * q4 + tid; e < 16 * MB * q4; e += 256) {
+    const int m = e / q4, q = e - m * q4;
+    *reinterpret_cast<float4*>(xs + m * ldu + 4 * q) = make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  if (DMA) {
+    // one (row, 64-float4 block) per wavefront instruction, lanes past the row masked
+    const int nq = (q4 + 63) >> 6;
+    for (int pr = wave; pr < M * nq; pr += 4) {
+      const int m = pr / nq, qb = (pr - m * nq) << 6;
+      const int k = k_of(qb + lane);
+      if (qb + lane < q4)
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(A + (long long)m * lda + min(k, K - 4)),
+                                         (lds_void*)(xs + m * ldu + 4 * qb), 16, 0, 0);
+    }
 #pragma unroll
-        for (int q = 0; q < 4; ++q) t[q] = (e < total && m < M && kk + q < kend) ? ar[q] : 0.f;
-        r[u] = make_float4(t[0], t[1], t[2], t[3]);
+    for (int p = 0; p < PF; ++p) load(p);
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(4 * PF));  // the direct loads have landed; B stays in flight
+    if (K % kSkRows != 0) {
+      // rows past K in the last unit were loaded from clamped addresses: zero them once all waves' loads landed
+      __syncthreads();
+      for (int e = tid; e < M * q4; e += 256) {
+        const int m = e / q4, q = e - m * q4;
+        const int k = k_of(q);
+        if (k >= K) *reinterpret_cast<float4*>(xs + m * ldu + 4 * q) = make_float4(0.f, 0.f, 0.f, 0.f);
       }
     }
+  } else {
+    for (int e = tid; e < M * q4; e += 256) {
+      const int m = e / q4, q = e - m * q4;
+      const int k = k_of(q);
+      const float* ar = A + (long long)m * lda;
+      float v[4];
 #pragma unroll
-    for (int u = 0; u < kStageF4; ++u) {
-      const int e = tid + u * 256;
-      if (e < total) *reinterpret_cast<float4*>(xs + (e / q4) * ld + 4 * (e % q4)) = r[u];
+      for (int c = 0; c < 4; ++c) v[c] = k + c < K ? ar[k + c] : 0.f;
+      *reinterpret_cast<float4*>(xs + m * ldu + 4 * q) = make_float4(v[0], v[1], v[2], v[3]);
     }
+#pragma unroll
+    for (int p = 0; p < PF; ++p) load(p);
   }
   __syncthreads();
 
@@ -149,103 +227,138 @@ __global__ __launch_bounds__(256) void sgemm_skinny_mfma(int M, int N, int K, co
   for (int c = 0; c < 4; ++c)
 #pragma unroll
     for (int b = 0; b < MB; ++b) acc[c][b] = (f32x4v){0.f, 0.f, 0.f, 0.f};
-  if (nch > 0) {
-    const int klast = kend - 1;
-    const float* Bl = B + nl;
-    constexpr int NB = kPF + 1;
-    float4 w[NB][4];
-    auto load = [&](int slot, int j) {
-      const int k16 = kbeg + 16 * j + 4 * lq;
+  int gcur = g0, tcur = t0;
+  int slot = w - wg_of_unit((long long)g0 * kb, U, G);  // later groups start in this workgroup: slot 0
+  // value r of block (c, b) is column 64 wave + 16 lq + 4 r + c, row 16 b + li: a float4 over c
+  auto flush = [&]() {
+    float* pt = P + (long long)(gcur * smax + slot) * M * kSkCols + 64 * wave + 16 * lq;
+    const int nrem = N - gcur * kSkCols - 64 * wave - 16 * lq;
 #pragma unroll
-      for (int s = 0; s < 4; ++s)
-        w[slot][s] = bch::load_nt(reinterpret_cast<const float4*>(Bl + (long long)min(k16 + s, klast) * ldb));
-    };
-    auto mma = [&](int slot, int j) {
-      float4 x[MB];
+    for (int b = 0; b < MB; ++b) {
+      const int m = 16 * b + li;
 #pragma unroll
-      for (int b = 0; b < MB; ++b) x[b] = *reinterpret_cast<const float4*>(xs + (16 * b + li) * ld + 16 * j + 4 * lq);
+      for (int r = 0; r < 4; ++r)
+        if (m < M && 4 * r < nrem)
+          *reinterpret_cast<float4*>(pt + m * kSkCols + 4 * r) =
+              make_float4(acc[0][b][r], acc[1][b][r], acc[2][b][r], acc[3][b][r]);
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const float ws[4] = {w[slot][s].x, w[slot][s].y, w[slot][s].z, w[slot][s].w};
+      for (int c = 0; c < 4; ++c) acc[c][b] = (f32x4v){0.f, 0.f, 0.f, 0.f};
+    }
+  };
+  auto mma = [&](int sb, int i) {
+    float4 x[MB];
 #pragma unroll
-        for (int b = 0; b < MB; ++b) {
-          const float xv = s == 0 ? x[b].x : s == 1 ? x[b].y : s == 2 ? x[b].z : x[b].w;
+    for (int b = 0; b < MB; ++b) x[b] = *reinterpret_cast<const float4*>(xs + (16 * b + li) * ldu + 16 * i + 4 * lq);
 #pragma unroll
-          for (int c = 0; c < 4; ++c) acc[c][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(ws[c], xv, acc[c][b], 0, 0, 0);
-        }
-      }
-    };
+    for (int s = 0; s < 4; ++s) {
+      const float ws[4] = {wv[sb][s].x, wv[sb][s].y, wv[sb][s].z, wv[sb][s].w};
 #pragma unroll
-    for (int p = 0; p < kPF; ++p) load(p, p);
-    int j = 0;
-    for (; j + NB <= nch; j += NB) {
+      for (int b = 0; b < MB; ++b) {
+        const float xv = s == 0 ? x[b].x : s == 1 ? x[b].y : s == 2 ? x[b].z : x[b].w;
 #pragma unroll
-      for (int p = 0; p < NB; ++p) {
-        load((p + kPF) % NB, j + p + kPF);
-        mma(p, j + p);
+        for (int c = 0; c < 4; ++c) acc[c][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(ws[c], xv, acc[c][b], 0, 0, 0);
       }
     }
+  };
+  // one unrolled copy of the pipeline step: loads are unconditional (the
+  // cursor holds at the last unit), the MFMAs are guarded by i < nu
+  for (int i = 0; i < nu; i += NB) {
 #pragma unroll
     for (int p = 0; p < NB; ++p) {
-      if (j + p < nch) {
-        load((p + kPF) % NB, j + p + kPF);
-        mma(p, j + p);
+      load((p + PF) % NB);
+      if (i + p < nu) {
+        mma(p, i + p);
+        if (++tcur == kb && i + p + 1 < nu) {
+          flush();
+          tcur = 0;
+          ++gcur;
+          slot = 0;
+        }
       }
     }
   }
-  // value r of block (c, b): column n0 + 4(4 lq + r) + c, row m = 16 b + li
-  float* pt = P + (long long)blockIdx.y * M * N;
-#pragma unroll
-  for (int c = 0; c < 4; ++c)
-#pragma unroll
-    for (int b = 0; b < MB; ++b)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int m = 16 * b + li, n = n0 + 4 * (4 * lq + r) + c;
-        if (m < M && n < N) pt[(long long)m * N + n] = acc[c][b][r];
-      }
+  flush();
 }
 
-// C[m][n] = sum over splits s, in split order, of P[s][m][n]; one thread per
-// output element (measured faster than float4-per-thread variants here: the
-// partials were just written by other XCDs and the loads are latency-bound).
-__global__ __launch_bounds__(256) void sgemm_skinny_reduce(int M, int N, const float* __restrict__ P,
-                                                           int splits, float* __restrict__ C, int ldc) {
+// C[m][n] = sum of the partial blocks of n's column group, in slot order
+// (the k order); loads in batches of 8, all in flight before the adds.
+__global__ __launch_bounds__(256) void sgemm_skinny_sk_reduce(int M, int N, const float* __restrict__ P, long long U,
+                                                              int G, int kb, int smax, float* __restrict__ C,
+                                                              int ldc) {
   const long long t = (long long)blockIdx.x * 256 + threadIdx.x;
   if (t >= (long long)M * N) return;
-  const long long ps = (long long)M * N;
+  const int m = (int)(t / N), n = (int)(t - (long long)m * N), g = n / kSkCols;
+  const int wf = wg_of_unit((long long)g * kb, U, G);
+  const int ns = wg_of_unit((long long)g * kb + kb - 1, U, G) - wf + 1;
+  const float* p = P + ((long long)g * smax * M + m) * kSkCols + (n - g * kSkCols);
+  const long long st = (long long)M * kSkCols;
   float s = 0.f;
-  for (int sp = 0; sp < splits; ++sp) s += P[sp * ps + t];
-  C[(t / N) * ldc + t % N] = s;
+  for (int i = 0; i < ns; i += 8) {
+    float v[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) v[q] = p[(long long)min(i + q, ns - 1) * st];
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+      if (i + q < ns) s += v[q];
+  }
+  C[(long long)m * ldc + n] = s;
 }
 
 bool use_fma(int m) { return m <= 4; }
 
-int mma_mb(int m) { return m <= 16 ? 1 : 2; }
+int sk_mb(int m) { return m <= 16 ? 1 : 2; }
 
-// k rows per split and split count.  The FMA path splits k 16 ways
-// (measured best at K 4096 / N 11008); the MFMA path stages its A slice in
-// LDS, which bounds the rows per split by the staging registers, and keeps
-// ~2 workgroups per CU.
-void plan(int m, int n, int k, int* kchunk, int* splits) {
-  if (use_fma(m)) {
-    int s = 16;
-    if (k < 16 * 4 * kFmaUnroll) s = (k + 4 * kFmaUnroll - 1) / (4 * kFmaUnroll);
-    if (s < 1) s = 1;
-    int kc = (k + s - 1) / s;
-    *kchunk = kc;
-    *splits = (k + kc - 1) / kc;
-    return;
-  }
-  const int mb = mma_mb(m);
-  const int max_rows = kStageF4 * 256 * 4 / (16 * mb);  // staged A^T fits the unrolled loads
-  const int colgroups = (n + kMmaCols - 1) / kMmaCols;
-  int s = (512 + colgroups - 1) / colgroups;
-  int kc = (k + s - 1) / s;
-  kc = (kc + 15) / 16 * 16;
-  if (kc > max_rows) kc = max_rows;
+// FMA path: k rows per split and split count.
+void fma_plan(int k, int* kchunk, int* splits) {
+  int s = kFmaSplits;
+  if (k < kFmaSplits * 4 * kFmaUnroll) s = (k + 4 * kFmaUnroll - 1) / (4 * kFmaUnroll);
+  if (s < 1) s = 1;
+  const int kc = (k + s - 1) / s;
   *kchunk = kc;
   *splits = (k + kc - 1) / kc;
+}
+
+// Stream-K path: units, workgroups (one per CU, more when a run's A^T slice
+// would not fit in LDS), units per workgroup, and partial slots per group.
+struct SkPlan {
+  long long U = 0;
+  int cg = 0, kb = 0, G = 0, upw = 0, smax = 0, mb = 1;
+  size_t lds = 0;
+};
+
+SkPlan sk_plan(int m, int n, int k) {
+  SkPlan p;
+  p.mb = sk_mb(m);
+  p.cg = (n + kSkCols - 1) / kSkCols;
+  p.kb = (k + kSkRows - 1) / kSkRows;
+  p.U = (long long)p.cg * p.kb;
+  const int cap = (kLdsBytes / (4 * 16 * p.mb) - 4) / kSkRows;  // units whose A^T fits in LDS
+  long long g = kSkWGs;
+  if ((p.U + g - 1) / g > cap) g = (p.U + cap - 1) / cap;
+  if (g > p.U) g = p.U;
+  p.G = (int)g;
+  p.upw = (int)((p.U + p.G - 1) / p.G);
+  for (int c = 0; c < p.cg; ++c) {
+    const int ns = wg_of_unit((long long)c * p.kb + p.kb - 1, p.U, p.G) - wg_of_unit((long long)c * p.kb, p.U, p.G) + 1;
+    if (ns > p.smax) p.smax = ns;
+  }
+  p.lds = sizeof(float) * 16 * p.mb * (size_t)(16 * p.upw + 4);
+  return p;
+}
+
+template <int MB, bool DMA>
+hipError_t launch_sk(hipStream_t s, const SkPlan& p, int m, int n, int k, const float* A, int lda, const float* B,
+                     int ldb, float* P) {
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(sgemm_skinny_sk<MB, DMA>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  hipLaunchKernelGGL((sgemm_skinny_sk<MB, DMA>), dim3(p.G), dim3(256), p.lds, s, m, n, k, A, lda, B, ldb, P, p.U,
+                     p.G, p.kb, p.smax);
+  return hipGetLastError();
 }
 
 }  // namespace
@@ -253,9 +366,13 @@ void plan(int m, int n, int k, int* kchunk, int* splits) {
 namespace bch {
 
 size_t sgemm_skinny_workspace_bytes(int m, int n, int k) {
-  int kc, s;
-  plan(m, n, k, &kc, &s);
-  return sizeof(float) * (size_t)s * (size_t)m * (size_t)n;
+  if (use_fma(m)) {
+    int kc, s;
+    fma_plan(k, &kc, &s);
+    return sizeof(float) * (size_t)s * (size_t)m * (size_t)n;
+  }
+  const SkPlan p = sk_plan(m, n, k);
+  return sizeof(float) * (size_t)p.cg * (size_t)p.smax * (size_t)m * kSkCols;
 }
 
 bool sgemm_skinny_applies(int m, int n, int k, const float* A, int lda, const float* B, int ldb) {
@@ -269,16 +386,18 @@ bool sgemm_skinny_applies(int m, int n, int k, const float* A, int lda, const fl
 
 const char* sgemm_skinny_kernel_name(int m) {
   if (use_fma(m)) return "sgemm_skinny_fma";
-  return mma_mb(m) == 1 ? "sgemm_skinny_mfma<1>" : "sgemm_skinny_mfma<2>";
+  return sk_mb(m) == 1 ? "sgemm_skinny_sk<1>" : "sgemm_skinny_sk<2>";
 }
 
 hipError_t launch_sgemm_skinny(hipStream_t s, int m, int n, int k, const float* A, int lda,
                                const float* B, int ldb, float* C, int ldc, void* ws, size_t ws_bytes) {
-  int kchunk, splits;
-  plan(m, n, k, &kchunk, &splits);
   if (ws == nullptr || ws_bytes < sgemm_skinny_workspace_bytes(m, n, k)) return hipErrorInvalidValue;
   float* P = static_cast<float*>(ws);
+  const long long total = (long long)m * n;
+  const dim3 rgrid((unsigned)((total + 255) / 256));
   if (use_fma(m)) {
+    int kchunk, splits;
+    fma_plan(k, &kchunk, &splits);
     dim3 grid((n + kFmaCols - 1) / kFmaCols, splits), block(256);
     if (m == 1)
       hipLaunchKernelGGL(sgemm_skinny_fma<1>, grid, block, 0, s, m, n, k, A, lda, B, ldb, P, kchunk);
@@ -286,38 +405,20 @@ hipError_t launch_sgemm_skinny(hipStream_t s, int m, int n, int k, const float* 
       hipLaunchKernelGGL(sgemm_skinny_fma<2>, grid, block, 0, s, m, n, k, A, lda, B, ldb, P, kchunk);
     else
       hipLaunchKernelGGL(sgemm_skinny_fma<4>, grid, block, 0, s, m, n, k, A, lda, B, ldb, P, kchunk);
-  } else {
-    dim3 grid((n + kMmaCols - 1) / kMmaCols, splits), block(256);
-    const int mb = mma_mb(m);
-    const size_t lds = sizeof(float) * 16 * mb * (size_t)(kchunk + 4);
-    const int avec = (lda % 4 == 0) && (reinterpret_cast<uintptr_t>(A) & 15) == 0;
-    if (mb == 1) {
-      static bool set1 = false;
-      if (!set1) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(sgemm_skinny_mfma<1>),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize,
-                                           (int)(sizeof(float) * 16 * 1 * (kStageF4 * 256 * 4 / (16 * 1) + 4)));
-        if (e != hipSuccess) return e;
-        set1 = true;
-      }
-      hipLaunchKernelGGL(sgemm_skinny_mfma<1>, grid, block, lds, s, m, n, k, A, lda, B, ldb, P, kchunk, avec);
-    } else {
-      static bool set2 = false;
-      if (!set2) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(sgemm_skinny_mfma<2>),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize,
-                                           (int)(sizeof(float) * 16 * 2 * (kStageF4 * 256 * 4 / (16 * 2) + 4)));
-        if (e != hipSuccess) return e;
-        set2 = true;
-      }
-      hipLaunchKernelGGL(sgemm_skinny_mfma<2>, grid, block, lds, s, m, n, k, A, lda, B, ldb, P, kchunk, avec);
-    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(sgemm_skinny_reduce, rgrid, dim3(256), 0, s, m, n, P, splits, C, ldc);
+    return hipGetLastError();
   }
-  hipError_t e = hipGetLastError();
+  const SkPlan p = sk_plan(m, n, k);
+  const bool dma = lda % 4 == 0 && k % 4 == 0 && (reinterpret_cast<uintptr_t>(A) & 15) == 0;
+  hipError_t e;
+  if (p.mb == 1)
+    e = dma ? launch_sk<1, true>(s, p, m, n, k, A, lda, B, ldb, P) : launch_sk<1, false>(s, p, m, n, k, A, lda, B, ldb, P);
+  else
+    e = dma ? launch_sk<2, true>(s, p, m, n, k, A, lda, B, ldb, P) : launch_sk<2, false>(s, p, m, n, k, A, lda, B, ldb, P);
   if (e != hipSuccess) return e;
-  const long long total = (long long)m * n;
-  hipLaunchKernelGGL(sgemm_skinny_reduce, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, m, n, P,
-                     splits, C, ldc);
+  hipLaunchKernelGGL(sgemm_skinny_sk_reduce, rgrid, dim3(256), 0, s, m, n, P, p.U, p.G, p.kb, p.smax, C, ldc);
   return hipGetLastError();
 }
 

@@ -99,6 +99,29 @@ def test_skinny_ragged(dev, m, n, k):
     assert O.max_rel_err(_mm(dev, a, b), O.matmul_f64(a, b)) <= TOL
 
 
+@pytest.mark.parametrize("m", [5, 8, 16, 17, 32])
+def test_skinny_exact_integers(dev, m):
+    """Small-integer inputs make every partial sum exact in f32, so the split-k
+    stream-K path must match the int64 product bit for bit (K 4096, N 11008)."""
+    _say(f"skinny exact integers m={m}")
+    rng = O.Lcg(m + 7)
+    a = np.round(rng.uniform((m, 4096)) * 3).astype(np.float32)
+    b = np.round(rng.uniform((4096, 11008)) * 7).astype(np.float32)
+    exact = (a.astype(np.int64) @ b.astype(np.int64)).astype(np.float32)
+    assert np.array_equal(_mm(dev, a, b), exact)
+
+
+def test_skinny_long_k_more_workgroups_than_cus(dev):
+    """K = 400000: a workgroup's A^T run would overflow LDS at one workgroup
+    per CU, so the plan uses more workgroups (several rounds)."""
+    m, n, k = 32, 256, 400000
+    _say(f"skinny long k m={m} n={n} k={k}")
+    rng = O.Lcg(4)
+    a = rng.normal((m, k))
+    b = rng.normal((k, n), 0.0, 0.02)
+    assert O.max_rel_err(_mm(dev, a, b), O.matmul_f64(a, b)) <= TOL
+
+
 def test_skinny_repeated_calls_and_unaligned_a(dev):
     _say("skinny repeated calls / unaligned A")
     rng = O.Lcg(99)
