@@ -12,7 +12,11 @@
 //     columns 4l..4l+3, one 1 KB row segment per load); the four wavefronts
 //     of a workgroup take interleaved rows with 8 row loads in flight; A[i][k]
 //     is wave-uniform and comes through the scalar cache.  k is split 16 ways.
-//   * 4 < m <= 32, sgemm_skinny_sk: at 2m multiply-adds per B element the
+//   * 16 < m <= 32 (K % 4 == 0, aligned A), sgemm_skinny_w32: the same
+//     stream-K layout with v_mfma_f32_32x32x2_f32 over all 32 rows at once,
+//     512-byte row segments per load and one wave per SIMD (described at
+//     the kernel).
+//   * 4 < m <= 32 otherwise, sgemm_skinny_sk: at 2m multiply-adds per B element the
 //     non-packed FP32 VALU cannot keep up with HBM, so v_mfma_f32_16x16x4_f32
 //     computes C^T = B^T A^T (m padded to 16 or 32).  The work is cut into
 //     units of 16 rows x 256 columns (4 wavefronts x 64 columns), ordered
@@ -280,6 +284,143 @@ __global__ __launch_bounds__(256, 1) void sgemm_skinny_sk(int M, int N, int K, c
   flush();
 }
 
+// ---------------------------------------------------------------- 16 < m <= 32
+// v_mfma_f32_32x32x2_f32 computes C^T = B^T A^T with all 32 rows of A in one
+// tile, so each B element feeds exactly one MFMA.  A workgroup is 4 waves:
+// column half ch = wave & 1 (128 of the group's 256 columns) and row stream
+// rs = wave >> 1.  A unit is 32 rows x 256 columns; stream rs takes rows
+// 16 rs .. 16 rs + 15 of it as 8 row pairs (p, p + 8), lane half lh holding
+// row 8 lh + p.  One float4 load per pair gives lane (lh, j) the columns
+// 4j .. 4j + 3 of its row, i.e. the MFMA A-operand of column block c = 0..3
+// (columns {4j + c}): no shuffles, 512 contiguous bytes per row per load.
+// A is read as two float4 per lane per unit (A[m][r0 .. r0 + 7], m = lane
+// & 31), straight from L2.  The loads are branch-free (a fixed 10 per unit)
+// so the compiler's wait on a unit's data leaves the PF later units in
+// flight.  With the MFMA accumulators in VGPRs (this file is built with
+// -mllvm -amdgpu-mfma-vgpr-form) nothing is copied to AGPRs in the loop.
+// At a flush the two row streams are summed through LDS, in stream order.
+// The dynamic LDS request (kW32Lds) keeps one workgroup per CU, so every
+// SIMD runs exactly one wave: two waves on one SIMD would share its matrix
+// core, and with 64 MACs per B element the MFMA time is close to the HBM
+// time.  Requires K % 4 == 0, lda % 4 == 0 and 16-byte aligned A (the
+// clamped float4 A loads stay inside the row).
+constexpr int kW32Rows = 32;
+constexpr int kW32PF = 2;
+constexpr int kW32Lds = 96 * 1024;  // > half of the CU's 160 KB: one workgroup per CU
+
+template <int PF, bool EDGE>
+__global__ __launch_bounds__(256, 1) void sgemm_skinny_w32(int M, int N, int K, const float* __restrict__ A, int lda,
+                                                           const float* __restrict__ B, int ldb,
+                                                           float* __restrict__ P, long long U, int G, int nblk,
+                                                           int smax) {
+  typedef float f32x16v __attribute__((ext_vector_type(16)));
+  extern __shared__ float4 smem4[];
+  constexpr int LDR = 128 + 4;
+  float* red = reinterpret_cast<float*>(smem4);  // [2 column halves][32 m][LDR]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int ch = wave & 1, rs = wave >> 1;
+  const int lh = lane >> 5, lm = lane & 31;
+  const int w = blockIdx.x;
+  const long long ub = (long long)w * U / G, ue = (long long)(w + 1) * U / G;
+  const int nu = (int)(ue - ub);
+  const int g0 = (int)(ub / nblk), t0 = (int)(ub - (long long)g0 * nblk);
+  constexpr int NB = PF + 1;
+  const float* arow = A + (long long)(lm < M ? lm : M - 1) * lda;  // rows m >= M compute columns never stored
+
+  float4 bv[NB][8];
+  float4 av[NB][2];
+  int lg = g0, lt = t0, lcount = 0;  // load cursor: advanced once per load, held at the last unit
+  auto load = [&](int sb) {
+    const int col = min(lg * kSkCols + 128 * ch + 4 * lm, N - 4);
+    const int r0 = kW32Rows * lt + 16 * rs + 8 * lh;
+#pragma unroll
+    for (int p = 0; p < 8; ++p)
+      bv[sb][p] = bch::load_nt(reinterpret_cast<const float4*>(B + (long long)min(r0 + p, K - 1) * ldb + col));
+    av[sb][0] = *reinterpret_cast<const float4*>(arow + min(r0, K - 4));
+    av[sb][1] = *reinterpret_cast<const float4*>(arow + min(r0 + 4, K - 4));
+    if (EDGE) {  // rows past K (last unit when K % 32 != 0): zero both operands
+#pragma unroll
+      for (int p = 0; p < 8; ++p)
+        if (r0 + p >= K) bv[sb][p] = make_float4(0.f, 0.f, 0.f, 0.f);
+      float* a = reinterpret_cast<float*>(&av[sb][0]);
+#pragma unroll
+      for (int c = 0; c < 8; ++c)
+        if (r0 + c >= K) a[c] = 0.f;
+    }
+    ++lcount;
+    lt += lcount < nu ? 1 : 0;
+    const int wrap = lt == nblk ? 1 : 0;
+    lt -= wrap * nblk;
+    lg += wrap;
+  };
+#pragma unroll
+  for (int p = 0; p < PF; ++p) load(p);
+
+  f32x16v acc[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[c][r] = 0.f;
+
+  int gcur = g0, tcur = t0;
+  int slot = w - wg_of_unit((long long)g0 * nblk, U, G);
+  // value r of block c: row m = lm, column 4 i + c of the wave's half, i = 8 (r / 4) + 4 lh + r % 4
+  auto flush = [&]() {
+    float* rb = red + ch * 32 * LDR;
+    if (rs == 1) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int i = 8 * (r >> 2) + 4 * lh + (r & 3);
+        *reinterpret_cast<float4*>(rb + lm * LDR + 4 * i) = make_float4(acc[0][r], acc[1][r], acc[2][r], acc[3][r]);
+      }
+    }
+    __syncthreads();
+    if (rs == 0 && lm < M) {
+      float* pt = P + (long long)(gcur * smax + slot) * M * kSkCols + 128 * ch + lm * kSkCols;
+      const int nrem = N - gcur * kSkCols - 128 * ch;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int i = 8 * (r >> 2) + 4 * lh + (r & 3);
+        const float4 o = *reinterpret_cast<const float4*>(rb + lm * LDR + 4 * i);
+        if (4 * i < nrem)
+          *reinterpret_cast<float4*>(pt + 4 * i) =
+              make_float4(acc[0][r] + o.x, acc[1][r] + o.y, acc[2][r] + o.z, acc[3][r] + o.w);
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[c][r] = 0.f;
+  };
+  auto mma = [&](int sb) {
+    const float a8[8] = {av[sb][0].x, av[sb][0].y, av[sb][0].z, av[sb][0].w,
+                         av[sb][1].x, av[sb][1].y, av[sb][1].z, av[sb][1].w};
+#pragma unroll
+    for (int p = 0; p < 8; ++p) {
+      const float b4[4] = {bv[sb][p].x, bv[sb][p].y, bv[sb][p].z, bv[sb][p].w};
+#pragma unroll
+      for (int c = 0; c < 4; ++c) acc[c] = __builtin_amdgcn_mfma_f32_32x32x2f32(b4[c], a8[p], acc[c], 0, 0, 0);
+    }
+  };
+  for (int i = 0; i < nu; i += NB) {
+#pragma unroll
+    for (int p = 0; p < NB; ++p) {
+      load((p + PF) % NB);
+      if (i + p < nu) {
+        mma(p);
+        if (++tcur == nblk && i + p + 1 < nu) {
+          flush();
+          tcur = 0;
+          ++gcur;
+          slot = 0;
+        }
+      }
+    }
+  }
+  flush();
+}
+
 // C[m][n] = sum of the partial blocks of n's column group, in slot order
 // (the k order); loads in batches of 8, all in flight before the adds.
 __global__ __launch_bounds__(256) void sgemm_skinny_sk_reduce(int M, int N, const float* __restrict__ P, long long U,
@@ -308,6 +449,27 @@ bool use_fma(int m) { return m <= 4; }
 
 int sk_mb(int m) { return m <= 16 ? 1 : 2; }
 
+// The 32x32x2 kernel: m > 16 (below that the 16x16x4 kernel, with half the
+// padded MFMA work, measured faster) and the alignment its clamped float4 A
+// loads need.
+bool use_w32(int m, int k, const float* A, int lda) {
+  return m > 16 && k >= 4 && k % 4 == 0 && lda % 4 == 0 && (reinterpret_cast<uintptr_t>(A) & 15) == 0;
+}
+
+// Compute units of the current device (the stream-K grids take one
+// workgroup per CU); cached per device.
+int cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  if (cached[dev] <= 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = kSkWGs;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
 // FMA path: k rows per split and split count.
 void fma_plan(int k, int* kchunk, int* splits) {
   int s = kFmaSplits;
@@ -333,7 +495,7 @@ SkPlan sk_plan(int m, int n, int k) {
   p.kb = (k + kSkRows - 1) / kSkRows;
   p.U = (long long)p.cg * p.kb;
   const int cap = (kLdsBytes / (4 * 16 * p.mb) - 4) / kSkRows;  // units whose A^T fits in LDS
-  long long g = kSkWGs;
+  long long g = cu_count();
   if ((p.U + g - 1) / g > cap) g = (p.U + cap - 1) / cap;
   if (g > p.U) g = p.U;
   p.G = (int)g;
@@ -344,6 +506,43 @@ SkPlan sk_plan(int m, int n, int k) {
   }
   p.lds = sizeof(float) * 16 * p.mb * (size_t)(16 * p.upw + 4);
   return p;
+}
+
+// 32x32x2 path: 32-row units, one workgroup per CU.
+struct W32Plan {
+  long long U = 0;
+  int cg = 0, nblk = 0, G = 0, smax = 0;
+};
+
+W32Plan w32_plan(int n, int k) {
+  W32Plan p;
+  p.cg = (n + kSkCols - 1) / kSkCols;
+  p.nblk = (k + kW32Rows - 1) / kW32Rows;
+  p.U = (long long)p.cg * p.nblk;
+  long long g = cu_count();
+  if (g > p.U) g = p.U;
+  p.G = (int)g;
+  for (int c = 0; c < p.cg; ++c) {
+    const int ns = wg_of_unit((long long)c * p.nblk + p.nblk - 1, p.U, p.G) -
+                   wg_of_unit((long long)c * p.nblk, p.U, p.G) + 1;
+    if (ns > p.smax) p.smax = ns;
+  }
+  return p;
+}
+
+template <bool EDGE>
+hipError_t launch_w32(hipStream_t s, const W32Plan& p, int m, int n, int k, const float* A, int lda, const float* B,
+                      int ldb, float* P) {
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(sgemm_skinny_w32<kW32PF, EDGE>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, kW32Lds);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  hipLaunchKernelGGL((sgemm_skinny_w32<kW32PF, EDGE>), dim3(p.G), dim3(256), kW32Lds, s, m, n, k, A, lda, B, ldb, P,
+                     p.U, p.G, p.nblk, p.smax);
+  return hipGetLastError();
 }
 
 template <int MB, bool DMA>
@@ -371,8 +570,15 @@ size_t sgemm_skinny_workspace_bytes(int m, int n, int k) {
     fma_plan(k, &kc, &s);
     return sizeof(float) * (size_t)s * (size_t)m * (size_t)n;
   }
+  // the larger of the two MFMA paths' needs (which one runs depends on A's alignment)
   const SkPlan p = sk_plan(m, n, k);
-  return sizeof(float) * (size_t)p.cg * (size_t)p.smax * (size_t)m * kSkCols;
+  size_t bytes = sizeof(float) * (size_t)p.cg * (size_t)p.smax * (size_t)m * kSkCols;
+  if (m > 16) {
+    const W32Plan q = w32_plan(n, k);
+    const size_t b2 = sizeof(float) * (size_t)q.cg * (size_t)q.smax * (size_t)m * kSkCols;
+    if (b2 > bytes) bytes = b2;
+  }
+  return bytes;
 }
 
 bool sgemm_skinny_applies(int m, int n, int k, const float* A, int lda, const float* B, int ldb) {
@@ -386,6 +592,7 @@ bool sgemm_skinny_applies(int m, int n, int k, const float* A, int lda, const fl
 
 const char* sgemm_skinny_kernel_name(int m) {
   if (use_fma(m)) return "sgemm_skinny_fma";
+  if (m > 16) return "sgemm_skinny_w32";  // with K % 4 == 0 and aligned A, as at the configs
   return sk_mb(m) == 1 ? "sgemm_skinny_sk<1>" : "sgemm_skinny_sk<2>";
 }
 
@@ -408,6 +615,14 @@ hipError_t launch_sgemm_skinny(hipStream_t s, int m, int n, int k, const float* 
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(sgemm_skinny_reduce, rgrid, dim3(256), 0, s, m, n, P, splits, C, ldc);
+    return hipGetLastError();
+  }
+  if (use_w32(m, k, A, lda)) {
+    const W32Plan q = w32_plan(n, k);
+    hipError_t e = k % kW32Rows == 0 ? launch_w32<false>(s, q, m, n, k, A, lda, B, ldb, P)
+                                     : launch_w32<true>(s, q, m, n, k, A, lda, B, ldb, P);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(sgemm_skinny_sk_reduce, rgrid, dim3(256), 0, s, m, n, P, q.U, q.G, q.nblk, q.smax, C, ldc);
     return hipGetLastError();
   }
   const SkPlan p = sk_plan(m, n, k);

@@ -93,7 +93,8 @@ def test_kernel_routing_names():
     assert lib.bch_sgemm_kernel_name(4100, 4096, 300) == b"sgemm_mfma_kernel<256,256,32,true>"
     assert lib.bch_sgemm_kernel_name(1, 11008, 4096) == b"sgemm_skinny_fma"
     assert lib.bch_sgemm_kernel_name(8, 11008, 4096) == b"sgemm_skinny_sk<1>"
-    assert lib.bch_sgemm_kernel_name(32, 11008, 4096) == b"sgemm_skinny_sk<2>"
+    assert lib.bch_sgemm_kernel_name(16, 11008, 4096) == b"sgemm_skinny_sk<1>"
+    assert lib.bch_sgemm_kernel_name(32, 11008, 4096) == b"sgemm_skinny_w32"
     assert lib.bch_sgemm_kernel_name(100, 70, 33) == b"sgemm_mfma_kernel<128,128,32,true>"
 
 

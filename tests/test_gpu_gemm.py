@@ -122,6 +122,32 @@ def test_skinny_long_k_more_workgroups_than_cus(dev):
     assert O.max_rel_err(_mm(dev, a, b), O.matmul_f64(a, b)) <= TOL
 
 
+@pytest.mark.parametrize("m,n,k,lda_pad,a_off", [
+    (20, 4, 4, 0, 0),        # one 32-row unit, K < 32 (tail rows zeroed)
+    (24, 100, 36, 0, 0),     # ragged last column group, K % 32 != 0
+    (32, 8, 4096, 0, 0),     # fewer units than CUs
+    (17, 520, 68, 4, 0),     # lda = k + 4 (still a multiple of 4)
+    (32, 512, 640, 1, 0),    # lda % 4 != 0: the 16x16x4 fallback
+    (18, 256, 64, 0, 1),     # A misaligned by one float: the fallback
+])
+def test_skinny_m_over_16_routes(dev, m, n, k, lda_pad, a_off):
+    """16 < m <= 32: the 32x32x2 kernel (aligned A, K % 4 == 0) and its
+    fallbacks, called through the C ABI with an explicit lda."""
+    _say(f"skinny m={m} n={n} k={k} lda=k+{lda_pad} a_off={a_off}")
+    rng = O.Lcg(m + n + k)
+    a = rng.normal((m, k))
+    b = rng.normal((k, n), 0.0, 0.02)
+    lda = k + lda_pad
+    a_buf = np.zeros(a_off + m * lda, dtype=np.float32)
+    a_buf[a_off:].reshape(m, lda)[:, :k] = a
+    ta = Tensor.from_data(a_buf, [a_buf.size], dev)
+    tb = Tensor.from_data(b, [k, n], dev)
+    tc = Tensor.empty([m, n], dev)
+    dev.check(dev._lib.bch_sgemm(dev.ctx, m, n, k, C.c_void_p(ta.ptr + 4 * a_off), lda, C.c_void_p(tb.ptr), n,
+                                 C.c_void_p(tc.ptr), n), "sgemm")
+    assert O.max_rel_err(tc.to_numpy(), O.matmul_f64(a, b)) <= TOL
+
+
 def test_skinny_repeated_calls_and_unaligned_a(dev):
     _say("skinny repeated calls / unaligned A")
     rng = O.Lcg(99)
