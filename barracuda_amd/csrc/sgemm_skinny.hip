@@ -33,9 +33,12 @@
 //     Infinity Cache): the stream-K layout removes the tail of an uneven
 //     grid (516 workgroups on 256 CUs); kernel code is kept small (one
 //     unrolled pipeline step, rolled staging), as every CU fetches the whole
-//     kernel from L2 once per launch; cross-XCD release/acquire fences for
-//     an in-kernel "last workgroup reduces" cost ~75 us per call, so the
-//     reduction is a separate launch.
+//     kernel from L2 once per launch.  An in-kernel "last workgroup reduces"
+//     (256 workgroups, 43 column groups, 32 KB partial blocks) measured 3-9 us
+//     per call for the agent-scope release/acquire alone, and the last
+//     workgroup of a group then reads every slot by itself, so the reduction
+//     stays a separate launch.  A full-K column-strip layout (no partials,
+//     one launch) uses only N / 64 = 172 CUs and streamed at 5.2 TB/s.
 #include "bch_internal.h"
 
 #include <stdint.h>
@@ -302,10 +305,13 @@ __global__ __launch_bounds__(256, 1) void sgemm_skinny_sk(int M, int N, int K, c
 // The dynamic LDS request (kW32Lds) keeps one workgroup per CU, so every
 // SIMD runs exactly one wave: two waves on one SIMD would share its matrix
 // core, and with 64 MACs per B element the MFMA time is close to the HBM
-// time.  Requires K % 4 == 0, lda % 4 == 0 and 16-byte aligned A (the
-// clamped float4 A loads stay inside the row).
+// time.  One unit of loads in flight ahead of the MFMAs (PF = 1) measured
+// fastest at K 4096, N 11008 (PF 1 / 2 / 3: 37.7 / 38.7 / 40 us per launch):
+// deeper prefetch buys no bandwidth and costs registers.  Requires K % 4 == 0,
+// lda % 4 == 0 and 16-byte aligned A (the clamped float4 A loads stay inside
+// the row).
 constexpr int kW32Rows = 32;
-constexpr int kW32PF = 2;
+constexpr int kW32PF = 1;
 constexpr int kW32Lds = 96 * 1024;  // > half of the CU's 160 KB: one workgroup per CU
 
 template <int PF, bool EDGE>
@@ -353,8 +359,15 @@ __global__ __launch_bounds__(256, 1) void sgemm_skinny_w32(int M, int N, int K, 
     lt -= wrap * nblk;
     lg += wrap;
   };
+  // The prologue units are issued in order (no interleaving across units):
+  // the loop header's wait then only has to cover the oldest unit, as on the
+  // back edge; interleaved, the last-issued load belongs to unit 0 and the
+  // header's single wait becomes vmcnt(0) on every iteration.
 #pragma unroll
-  for (int p = 0; p < PF; ++p) load(p);
+  for (int p = 0; p < PF; ++p) {
+    load(p);
+    __builtin_amdgcn_sched_barrier(0);
+  }
 
   f32x16v acc[4];
 #pragma unroll

@@ -150,7 +150,7 @@ def _bench_softmax(dev, T, reps):
     n = 65536 * 2048
     wall, ev = T.run(lambda i: lib.bch_softmax_rows(ctx, 1, n, px, py), reps, 3)
     out["softmax_global_2^27"] = {"GB/s": nbytes / (ev * 1e-3) / 1e9, "us": ev * 1e3,
-                                  "bytes_per_call": nbytes,
+                                  "bytes_per_call": nbytes, "traffic": load_traffic("softmax_global_2^27"),
                                   "hbm_frac": nbytes / (ev * 1e-3) / 1e9 / HBM_PEAK_GBS,
                                   "hbm_frac_of_12B_floor": 1.5 * nbytes / (ev * 1e-3) / 1e9 / HBM_PEAK_GBS}
     return out
@@ -176,7 +176,7 @@ def _bench_skinny(dev, T, reps):
                                "bytes_per_call": nbytes,
                                "hbm_frac": nbytes / (ev * 1e-3) / 1e9 / HBM_PEAK_GBS,
                                "TFLOP/s": 2.0 * m * K * N / (ev * 1e-3) / 1e12,
-                               "traffic_main_kernel": load_traffic(f"skinny_m{m}")}
+                               "traffic": load_traffic(f"skinny_m{m}")}
         del xs, ws, ys
     return out
 
@@ -218,7 +218,7 @@ def _bench_sdpa(dev, T, reps):
         key = "sdpa_causal" if causal else "sdpa_noncausal"
         out[key] = {"ms": ev, "TFLOP/s": fl / (ev * 1e-3) / 1e12,
                     "mfma_frac": fl / (ev * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS,
-                    "traffic_avg_causal_and_not": load_traffic("sdpa_b4h32s2048d128")}
+                    "traffic": load_traffic(key)}
     del q, k, v, o
     return out
 
