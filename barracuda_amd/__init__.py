@@ -8,13 +8,15 @@ from .error import (BarracudaError, CastOverflow, DeviceError, DeviceLost, Devic
                     ExecutionError, InvalidInput, InvalidOperation, InvalidShape, OutOfMemory,
                     ShapeMismatch, UnsupportedOperation)
 from .session import AttentionDims, SessionTensor, TensorSession
-from .tensor import (Attention, BatchMatMul, CausalAttention, FlashAttention, HipDevice, LcgStream,
-                     MatMul, MatmulTiled, ScaledDotProductAttention, Softmax, Tensor, get_device)
+from .tensor import (Attention, BatchMatMul, CausalAttention, FlashAttention, GroupedQueryAttention, HipDevice,
+                     LcgStream, MatMul, MatmulTiled, MultiHeadAttention, ScaledDotProductAttention, Softmax,
+                     Tensor, get_device)
 
 __all__ = [
     "BarracudaError", "CastOverflow", "DeviceError", "DeviceLost", "DeviceNotAvailable",
     "ExecutionError", "InvalidInput", "InvalidOperation", "InvalidShape", "OutOfMemory",
     "ShapeMismatch", "UnsupportedOperation", "AttentionDims", "SessionTensor", "TensorSession",
-    "Attention", "BatchMatMul", "CausalAttention", "FlashAttention", "HipDevice", "MatMul",
+    "Attention", "BatchMatMul", "CausalAttention", "FlashAttention", "GroupedQueryAttention", "HipDevice",
+    "MatMul", "MultiHeadAttention",
     "MatmulTiled", "ScaledDotProductAttention", "Softmax", "Tensor", "get_device", "LcgStream",
 ]

@@ -29,6 +29,13 @@ _ll = C.c_longlong
 _sz = C.c_size_t
 _f = C.c_float
 
+
+
+class AttnLayout(C.Structure):
+    """bch_attn_layout: element (b, h, i, d) at b*batch + h*head + i*row + d."""
+    _fields_ = [("batch_stride", C.c_longlong), ("head_stride", C.c_longlong), ("row_stride", C.c_longlong)]
+
+
 # name -> (restype, argtypes)
 SIGNATURES = {
     "bch_device_count": (_i, [C.POINTER(_i)]),
@@ -48,6 +55,8 @@ SIGNATURES = {
     "bch_softmax_rows": (_i, [_vp, _ll, _ll, _vp, _vp]),
     "bch_softmax_axis": (_i, [_vp, _ll, _ll, _ll, _vp, _vp]),
     "bch_sdpa_fwd": (_i, [_vp, _i, _i, _i, _i, _i, _f, _i, _vp, _vp, _vp, _vp]),
+    "bch_sdpa_fwd_ex": (_i, [_vp, _i, _i, _i, _i, _i, _i, _f, _i, _vp, AttnLayout, _vp, AttnLayout, _vp,
+                             AttnLayout, _vp, AttnLayout]),
     "bch_launch_code_object": (_i, [_vp, _vp, _sz, C.c_char_p, C.POINTER(C.c_uint),
                                     C.POINTER(C.c_uint), C.POINTER(_vp), _sz, _sz]),
     "bch_event_create": (_i, [_vp, C.POINTER(_vp)]),

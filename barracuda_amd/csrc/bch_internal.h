@@ -70,5 +70,18 @@ hipError_t launch_copy(hipStream_t s, void* dst, const void* src, size_t bytes);
 hipError_t launch_sdpa(hipStream_t s, int B, int H, int Sq, int Skv, int D,
                        float scale, int causal, const float* q,
                        const float* k, const float* v, float* o);
+// Strided form: per tensor (batch, head, row) strides in elements, the head
+// dimension contiguous; key/value head of query head h is h / (H / Hkv).
+struct SdpaLayout {
+  long long batch, head, row;
+};
+struct SdpaStrides {
+  SdpaLayout q, k, v, o;
+};
+hipError_t launch_sdpa_strided(hipStream_t s, int B, int H, int Hkv, int Sq,
+                               int Skv, int D, float scale, int causal,
+                               const float* q, const float* k,
+                               const float* v, float* o,
+                               const SdpaStrides& st);
 
 }  // namespace bch

@@ -355,6 +355,37 @@ bch_status bch_sdpa_fwd(bch_ctx* ctx, int B, int H, int Sq, int Skv, int D, floa
                   "attention launch");
 }
 
+bch_status bch_sdpa_fwd_ex(bch_ctx* ctx, int B, int H, int Hkv, int Sq, int Skv, int D, float scale, int causal,
+                           const float* q, bch_attn_layout ql, const float* k, bch_attn_layout kl, const float* v,
+                           bch_attn_layout vl, float* o, bch_attn_layout ol) {
+  if (B < 1 || H < 1 || Hkv < 1 || Sq < 1 || Skv < 1 || D < 1)
+    return fail(ctx, BCH_E_SHAPE, "attention: empty dimension (B=%d, H=%d, Hkv=%d, Sq=%d, Skv=%d, D=%d)", B, H,
+                Hkv, Sq, Skv, D);
+  if (H % Hkv != 0)
+    return fail(ctx, BCH_E_INVALID, "num_q_heads (%d) must be divisible by num_kv_heads (%d)", H, Hkv);
+  if (causal && Sq != Skv)
+    return fail(ctx, BCH_E_SHAPE, "attention: causal mask needs Sq == Skv (shape mismatch %d vs %d)", Sq, Skv);
+  if (D > 128) return fail(ctx, BCH_E_UNSUPPORTED, "attention: head dimension %d > 128", D);
+  const bch_attn_layout* ls[4] = {&ql, &kl, &vl, &ol};
+  for (int i = 0; i < 4; ++i)
+    if (ls[i]->batch_stride < 0 || ls[i]->head_stride < 0 || ls[i]->row_stride < D)
+      return fail(ctx, BCH_E_INVALID,
+                  "attention: %c layout (batch %lld, head %lld, row %lld) needs non-negative strides and "
+                  "row stride >= D = %d",
+                  "qkvo"[i], ls[i]->batch_stride, ls[i]->head_stride, ls[i]->row_stride, D);
+  if (!ctx) return fail(ctx, BCH_E_INVALID, "attention: ctx is NULL");
+  if (!q || !k || !v || !o) return fail(ctx, BCH_E_INVALID, "attention: NULL buffer");
+  bch_status st = use(ctx);
+  if (st != BCH_OK) return st;
+  bch::SdpaStrides s;
+  s.q = {ql.batch_stride, ql.head_stride, ql.row_stride};
+  s.k = {kl.batch_stride, kl.head_stride, kl.row_stride};
+  s.v = {vl.batch_stride, vl.head_stride, vl.row_stride};
+  s.o = {ol.batch_stride, ol.head_stride, ol.row_stride};
+  return from_hip(ctx, bch::launch_sdpa_strided(ctx->stream, B, H, Hkv, Sq, Skv, D, scale, causal, q, k, v, o, s),
+                  "attention launch");
+}
+
 bch_status bch_fill_uniform(bch_ctx* ctx, float* dst, size_t n, unsigned long long* state, double lo,
                             double hi) {
   if (!ctx || !state || (n && !dst)) return fail(ctx, BCH_E_INVALID, "fill_uniform: NULL argument");

@@ -9,7 +9,14 @@
 // :96-145, K13).  Contract: o[b,h,i,:] = sum_j softmax_j(scale q_i . k_j) v_j,
 // j <= i when causal.  The score matrix is never written to memory.
 //
-// Layout: q [B,H,Sq,D], k and v [B,H,Skv,D], o [B,H,Sq,D], f32 row-major.
+// Layout: per tensor a (batch, head, row) stride in elements with the head
+// dimension contiguous; [B,H,S,D] row-major is the dense case.  K and V may
+// have fewer heads than Q (grouped-query attention, ops/
+// grouped_query_attention/compute.rs:27-121): query head h reads key/value
+// head h / (H / Hkv).  Strided views also give multi-head attention its
+// head split and concat for free (ops/mha/projections.rs:18-58 copy
+// [B,S,H*D] <-> [B,H,S,D] through head_split_f64.wgsl / head_concat_f64.wgsl;
+// here the kernel reads and writes the [B,S,H,D] projections in place).
 //
 // Design (FP32 MFMA for both products, v_mfma_f32_32x32x2_f32):
 //   * A workgroup = 4 wavefronts = 128 queries of one (b,h); wavefront w owns
@@ -61,7 +68,7 @@ struct SdpaCfg {
 };
 
 template <int DP, bool FULL>
-__device__ __forceinline__ void load_k(const float* __restrict__ kh, int Skv, int D, int kb, int tid,
+__device__ __forceinline__ void load_k(const float* __restrict__ kh, long long ldk, int Skv, int D, int kb, int tid,
                                        float4 (&rk)[SdpaCfg<DP>::K_F4]) {
   using G = SdpaCfg<DP>;
 #pragma unroll
@@ -70,18 +77,18 @@ __device__ __forceinline__ void load_k(const float* __restrict__ kh, int Skv, in
     const int key = idx / G::KD4, d0 = (idx % G::KD4) * 4;
     const int gk = kb + key;
     if (FULL) {
-      rk[f] = *reinterpret_cast<const float4*>(kh + (long long)gk * D + d0);
+      rk[f] = *reinterpret_cast<const float4*>(kh + gk * ldk + d0);
     } else {
       float t[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) t[e] = (gk < Skv && d0 + e < D) ? kh[(long long)gk * D + d0 + e] : 0.0f;
+      for (int e = 0; e < 4; ++e) t[e] = (gk < Skv && d0 + e < D) ? kh[gk * ldk + d0 + e] : 0.0f;
       rk[f] = make_float4(t[0], t[1], t[2], t[3]);
     }
   }
 }
 
 template <int DP, bool FULL>
-__device__ __forceinline__ void load_v(const float* __restrict__ vh, int Skv, int D, int kb, int tid,
+__device__ __forceinline__ void load_v(const float* __restrict__ vh, long long ldv, int Skv, int D, int kb, int tid,
                                        float4 (&rv)[4]) {
   using G = SdpaCfg<DP>;
   const int blk = tid < G::V_BLK ? tid : 0;  // threads past the tile reload block 0 (unused)
@@ -90,11 +97,11 @@ __device__ __forceinline__ void load_v(const float* __restrict__ vh, int Skv, in
   for (int e = 0; e < 4; ++e) {
     const int gk = kb + 4 * kq + e, d0 = 4 * dq;
     if (FULL) {
-      rv[e] = *reinterpret_cast<const float4*>(vh + (long long)gk * D + d0);
+      rv[e] = *reinterpret_cast<const float4*>(vh + gk * ldv + d0);
     } else {
       float t[4];
 #pragma unroll
-      for (int c = 0; c < 4; ++c) t[c] = (gk < Skv && d0 + c < D) ? vh[(long long)gk * D + d0 + c] : 0.0f;
+      for (int c = 0; c < 4; ++c) t[c] = (gk < Skv && d0 + c < D) ? vh[gk * ldv + d0 + c] : 0.0f;
       rv[e] = make_float4(t[0], t[1], t[2], t[3]);
     }
   }
@@ -122,8 +129,9 @@ __device__ __forceinline__ void store_kv(float* __restrict__ ks, float* __restri
 
 template <int DP, bool FULL>
 __global__ __launch_bounds__(256, 2) void sdpa_fwd_kernel(
-    int BH, int Sq, int Skv, int D, float qscale, int causal, const float* __restrict__ q,
-    const float* __restrict__ k, const float* __restrict__ v, float* __restrict__ o, int qblocks) {
+    int H, int group, int BH, int Sq, int Skv, int D, float qscale, int causal, const float* __restrict__ q,
+    const float* __restrict__ k, const float* __restrict__ v, float* __restrict__ o, bch::SdpaStrides st,
+    int qblocks) {
   using G = SdpaCfg<DP>;
   constexpr int KLD = G::KLD;
   extern __shared__ float4 smem4[];
@@ -142,10 +150,11 @@ __global__ __launch_bounds__(256, 2) void sdpa_fwd_kernel(
   const int q0w = qb * kBQ + wave * 32;  // first query of this wavefront
   const int myq = q0w + li;
 
-  const float* qh = q + (long long)bh * Sq * D;
-  const float* kh = k + (long long)bh * Skv * D;
-  const float* vh = v + (long long)bh * Skv * D;
-  float* oh = o + (long long)bh * Sq * D;
+  const int bi = bh / H, hq = bh - bi * H, hk = hq / group;
+  const float* qh = q + bi * st.q.batch + hq * st.q.head;
+  const float* kh = k + bi * st.k.batch + hk * st.k.head;
+  const float* vh = v + bi * st.v.batch + hk * st.v.head;
+  float* oh = o + bi * st.o.batch + hq * st.o.head;
 
   // ---- q operand: qf[c] = q[myq][8c + 4lh .. +3] * scale * log2(e) ----
   float4 qf[DP / 8];
@@ -154,11 +163,11 @@ __global__ __launch_bounds__(256, 2) void sdpa_fwd_kernel(
     const int d0 = 8 * c + 4 * lh;
     float t[4];
     if (FULL) {
-      const float4 x = *reinterpret_cast<const float4*>(qh + (long long)myq * D + d0);
+      const float4 x = *reinterpret_cast<const float4*>(qh + myq * st.q.row + d0);
       t[0] = x.x; t[1] = x.y; t[2] = x.z; t[3] = x.w;
     } else {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) t[e] = (myq < Sq && d0 + e < D) ? qh[(long long)myq * D + d0 + e] : 0.0f;
+      for (int e = 0; e < 4; ++e) t[e] = (myq < Sq && d0 + e < D) ? qh[myq * st.q.row + d0 + e] : 0.0f;
     }
     qf[c] = make_float4(t[0] * qscale, t[1] * qscale, t[2] * qscale, t[3] * qscale);
   }
@@ -176,8 +185,8 @@ __global__ __launch_bounds__(256, 2) void sdpa_fwd_kernel(
 
   float4 rk[G::K_F4];
   float4 rv[4];
-  load_k<DP, FULL>(kh, Skv, D, 0, tid, rk);
-  load_v<DP, FULL>(vh, Skv, D, 0, tid, rv);
+  load_k<DP, FULL>(kh, st.k.row, Skv, D, 0, tid, rk);
+  load_v<DP, FULL>(vh, st.v.row, Skv, D, 0, tid, rv);
   store_kv<DP>(Ks, Vt, tid, rk, rv);
   __syncthreads();
 
@@ -186,8 +195,8 @@ __global__ __launch_bounds__(256, 2) void sdpa_fwd_kernel(
     const int kb = t * kBKV;
     // next block (the last iteration reloads the last block; never read)
     const int kbn = min(t + 1, nkb - 1) * kBKV;
-    load_k<DP, FULL>(kh, Skv, D, kbn, tid, rk);
-    load_v<DP, FULL>(vh, Skv, D, kbn, tid, rv);
+    load_k<DP, FULL>(kh, st.k.row, Skv, D, kbn, tid, rk);
+    load_v<DP, FULL>(vh, st.v.row, Skv, D, kbn, tid, rv);
 
     // wave-uniform: skip blocks fully above this wavefront's diagonal and
     // wavefronts whose queries are all past Sq
@@ -265,15 +274,15 @@ __global__ __launch_bounds__(256, 2) void sdpa_fwd_kernel(
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int d = 32 * b + 8 * (r >> 2) + 4 * lh + (r & 3);
-        if (FULL || d < D) oh[(long long)myq * D + d] = oacc[b][r] * inv;
+        if (FULL || d < D) oh[myq * st.o.row + d] = oacc[b][r] * inv;
       }
     }
   }
 }
 
 template <int DP, bool FULL>
-hipError_t launch_dp(hipStream_t s, int B, int H, int Sq, int Skv, int D, float scale, int causal,
-                     const float* q, const float* k, const float* v, float* o) {
+hipError_t launch_dp(hipStream_t s, int B, int H, int Hkv, int Sq, int Skv, int D, float scale, int causal,
+                     const float* q, const float* k, const float* v, float* o, const bch::SdpaStrides& st) {
   const int qblocks = (Sq + kBQ - 1) / kBQ;
   const long long blocks = (long long)B * H * qblocks;
   if (blocks > 0x7fffffffLL) return hipErrorInvalidValue;
@@ -286,32 +295,44 @@ hipError_t launch_dp(hipStream_t s, int B, int H, int Sq, int Skv, int D, float 
     if (e != hipSuccess) return e;
     attr_set = true;
   }
-  hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), lds, s, B * H, Sq, Skv, D, scale * kLog2E,
-                     causal, q, k, v, o, qblocks);
+  hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), lds, s, H, H / Hkv, B * H, Sq, Skv, D,
+                     scale * kLog2E, causal, q, k, v, o, st, qblocks);
   return hipGetLastError();
 }
 
+bool aligned16(const float* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+bool mult4(const bch::SdpaLayout& l) { return l.batch % 4 == 0 && l.head % 4 == 0 && l.row % 4 == 0; }
+
 template <int DP>
-hipError_t launch_d(hipStream_t s, int B, int H, int Sq, int Skv, int D, float scale, int causal,
-                    const float* q, const float* k, const float* v, float* o) {
-  const bool full = D == DP && Sq % kBQ == 0 && Skv % kBKV == 0 &&
-                    (reinterpret_cast<uintptr_t>(q) & 15) == 0 &&
-                    (reinterpret_cast<uintptr_t>(k) & 15) == 0 &&
-                    (reinterpret_cast<uintptr_t>(v) & 15) == 0;
-  if (full) return launch_dp<DP, true>(s, B, H, Sq, Skv, D, scale, causal, q, k, v, o);
-  return launch_dp<DP, false>(s, B, H, Sq, Skv, D, scale, causal, q, k, v, o);
+hipError_t launch_d(hipStream_t s, int B, int H, int Hkv, int Sq, int Skv, int D, float scale, int causal,
+                    const float* q, const float* k, const float* v, float* o, const bch::SdpaStrides& st) {
+  // full tiles, 128-bit loads: every row start 16-byte aligned
+  const bool full = D == DP && Sq % kBQ == 0 && Skv % kBKV == 0 && aligned16(q) && aligned16(k) &&
+                    aligned16(v) && mult4(st.q) && mult4(st.k) && mult4(st.v);
+  if (full) return launch_dp<DP, true>(s, B, H, Hkv, Sq, Skv, D, scale, causal, q, k, v, o, st);
+  return launch_dp<DP, false>(s, B, H, Hkv, Sq, Skv, D, scale, causal, q, k, v, o, st);
 }
 
 }  // namespace
 
 namespace bch {
 
+hipError_t launch_sdpa_strided(hipStream_t s, int B, int H, int Hkv, int Sq, int Skv, int D, float scale,
+                               int causal, const float* q, const float* k, const float* v, float* o,
+                               const SdpaStrides& st) {
+  if (Hkv < 1 || H % Hkv != 0) return hipErrorInvalidValue;
+  if (D <= 32) return launch_d<32>(s, B, H, Hkv, Sq, Skv, D, scale, causal, q, k, v, o, st);
+  if (D <= 64) return launch_d<64>(s, B, H, Hkv, Sq, Skv, D, scale, causal, q, k, v, o, st);
+  if (D <= 128) return launch_d<128>(s, B, H, Hkv, Sq, Skv, D, scale, causal, q, k, v, o, st);
+  return hipErrorInvalidValue;
+}
+
 hipError_t launch_sdpa(hipStream_t s, int B, int H, int Sq, int Skv, int D, float scale, int causal,
                        const float* q, const float* k, const float* v, float* o) {
-  if (D <= 32) return launch_d<32>(s, B, H, Sq, Skv, D, scale, causal, q, k, v, o);
-  if (D <= 64) return launch_d<64>(s, B, H, Sq, Skv, D, scale, causal, q, k, v, o);
-  if (D <= 128) return launch_d<128>(s, B, H, Sq, Skv, D, scale, causal, q, k, v, o);
-  return hipErrorInvalidValue;
+  SdpaStrides st;
+  st.q = st.o = SdpaLayout{(long long)H * Sq * D, (long long)Sq * D, D};
+  st.k = st.v = SdpaLayout{(long long)H * Skv * D, (long long)Skv * D, D};
+  return launch_sdpa_strided(s, B, H, H, Sq, Skv, D, scale, causal, q, k, v, o, st);
 }
 
 }  // namespace bch

@@ -16,6 +16,9 @@ Reference (crates/barracuda/src/):
   Tensor::scaled_dot_product_attention           ops/scaled_dot_product_attention/mod.rs:81-226
   Tensor::causal_attention, CausalAttention      ops/causal_attn/mod.rs:64-158
   FlashAttention                                 ops/flash_attention.rs:45-146
+  Tensor::grouped_query_attention                ops/grouped_query_attention/mod.rs:52-226
+  Tensor::multi_head_attention                   ops/mha/mod.rs:48-263, projections.rs:18-58
+  Tensor::reshape                                tensor/mod.rs (shape-only view)
 """
 from __future__ import annotations
 
@@ -34,7 +37,7 @@ from .error import (BarracudaError, DeviceError, DeviceNotAvailable, InvalidInpu
 __all__ = [
     "HipDevice", "get_device", "Tensor", "MatMul", "MatmulTiled", "BatchMatMul",
     "Softmax", "Attention", "ScaledDotProductAttention", "CausalAttention",
-    "FlashAttention", "LcgStream",
+    "FlashAttention", "GroupedQueryAttention", "MultiHeadAttention", "LcgStream",
 ]
 
 
@@ -219,6 +222,14 @@ class Tensor:
         """Shares the buffer, as Tensor::clone bumps a refcount (tensor/mod.rs:267-278)."""
         return Tensor(self._buf, self._shape, self._device)
 
+    def reshape(self, shape: Sequence[int]) -> "Tensor":
+        """Same buffer, new shape with the same element count (the reference's
+        reshape, used by MultiHeadAttention at ops/mha/projections.rs:32-35)."""
+        shape = [int(x) for x in shape]
+        if _numel(shape) != self.len():
+            raise ShapeMismatch(shape, self._shape)
+        return Tensor(self._buf, shape, self._device)
+
     # -- ops (same names as the reference) -----------------------------------
     def matmul(self, other: "Tensor") -> "Tensor":
         return MatMul(self, other).execute()
@@ -262,6 +273,13 @@ class Tensor:
 
     def causal_attention(self, key: "Tensor", value: "Tensor") -> "Tensor":
         return CausalAttention(self, key, value).execute()
+
+    def grouped_query_attention(self, key: "Tensor", value: "Tensor") -> "Tensor":
+        return GroupedQueryAttention(self, key, value).execute()
+
+    def multi_head_attention(self, key: "Tensor", value: "Tensor", w_q: "Tensor", w_k: "Tensor",
+                             w_v: "Tensor", w_o: "Tensor", num_heads: int) -> "Tensor":
+        return MultiHeadAttention(self, key, value, w_q, w_k, w_v, w_o, num_heads).execute()
 
 
 class LcgStream:
@@ -497,3 +515,114 @@ class FlashAttention:
         s, d = self.q.shape()
         dev = _same_device(self.q, self.k, self.v)
         return _sdpa(dev, self.q, self.k, self.v, False, "FlashAttention", 1, 1, s, s, d)
+
+
+def _dense(h: int, s: int, d: int) -> N.AttnLayout:
+    """[B, H, S, D] row-major."""
+    return N.AttnLayout(h * s * d, s * d, d)
+
+
+def _sdpa_ex(dev: HipDevice, op: str, b: int, h: int, hkv: int, sq: int, skv: int, d: int, causal: bool,
+             q: Tensor, ql: N.AttnLayout, k: Tensor, kl: N.AttnLayout, v: Tensor, vl: N.AttnLayout,
+             o: Tensor, ol: N.AttnLayout) -> None:
+    """bch_sdpa_fwd_ex: strided operands, hkv key/value heads, scale 1/sqrt(d)."""
+    if d > 128:
+        raise UnsupportedOperation(op, f"{dev.name()} (head_dim {d} > 128)")
+    _check_i32(op, dev, batch=b, heads=h, kv_heads=hkv, q_len=sq, kv_len=skv)
+    if b * h * sq * d == 0:
+        return
+    if skv == 0:
+        raise InvalidOperation(op, "key sequence is empty (shape/dimension mismatch)")
+    scale = np.float32(1.0) / np.sqrt(np.float32(d))
+    with dev._lock:
+        dev.check(dev._lib.bch_sdpa_fwd_ex(dev.ctx, b, h, hkv, sq, skv, d, float(scale), int(causal),
+                                           C.c_void_p(q.ptr), ql, C.c_void_p(k.ptr), kl, C.c_void_p(v.ptr), vl,
+                                           C.c_void_p(o.ptr), ol), op)
+
+
+class GroupedQueryAttention:
+    """ops/grouped_query_attention/mod.rs:52-147 (validation) + compute.rs:27-121:
+    Q [B, Hq, S, D], K/V [B, Hkv, S, D], query head h attends with key/value
+    head h / (Hq / Hkv); softmax(Q K^T / sqrt(D)) V, non-causal.  One fused
+    launch replaces the reference's three passes and its two [B, Hq, S, S]
+    intermediates."""
+
+    def __init__(self, query: Tensor, key: Tensor, value: Tensor):
+        qs, ks, vs = query.shape(), key.shape(), value.shape()
+        if len(qs) != 4 or len(ks) != 4 or len(vs) != 4:
+            raise InvalidInput("All inputs must be 4D tensors [batch, heads, seq_len, head_dim]")
+        b, hq, s, d = qs
+        if ks[0] != b or ks[2] != s or ks[3] != d:
+            raise ShapeMismatch([b, hq, s, d], ks)
+        if vs != ks:
+            raise ShapeMismatch(ks, vs)
+        hkv = ks[1]
+        if hkv == 0 or hq % hkv != 0:
+            raise InvalidInput(f"num_q_heads ({hq}) must be divisible by num_kv_heads ({hkv})")
+        if query.device() is not key.device() or query.device() is not value.device():
+            raise DeviceError("All tensors must be on the same device")
+        self.q, self.k, self.v = query, key, value
+
+    def execute(self) -> Tensor:
+        b, hq, s, d = self.q.shape()
+        hkv = self.k.shape()[1]
+        dev = self.q.device()
+        out = Tensor.empty([b, hq, s, d], dev)
+        _sdpa_ex(dev, "grouped_query_attention", b, hq, hkv, s, s, d, False,
+                 self.q, _dense(hq, s, d), self.k, _dense(hkv, s, d), self.v, _dense(hkv, s, d),
+                 out, _dense(hq, s, d))
+        return out
+
+
+class MultiHeadAttention:
+    """ops/mha/mod.rs:48-187 + projections.rs:18-58: query [B, Sq, D], key /
+    value [B, Skv, D], weights [D, D]; heads = D / num_heads wide.
+
+        Q' = query W_q, K' = key W_k, V' = value W_v      (three GEMMs)
+        O[b, i, h] = attention(Q'[b, :, h], K'[b, :, h], V'[b, :, h])
+        out = O W_o                                        (one GEMM)
+
+    The reference copies each projection into [B, H, S, D/H] (head_split) and
+    the attention output back into [B, S, D] (head_concat); here the fused
+    attention reads the [B, S, H, D/H] projections and writes the [B, S, H,
+    D/H] output through strides, so neither copy exists."""
+
+    def __init__(self, query: Tensor, key: Tensor, value: Tensor, w_q: Tensor, w_k: Tensor, w_v: Tensor,
+                 w_o: Tensor, num_heads: int):
+        qs, ks, vs = query.shape(), key.shape(), value.shape()
+        if len(qs) != 3 or len(ks) != 3 or len(vs) != 3:
+            raise ShapeMismatch(qs, [0, 0, 0])
+        if qs[0] != ks[0] or qs[0] != vs[0]:
+            raise ShapeMismatch(qs, ks)
+        if qs[2] != ks[2] or ks[2] != vs[2]:
+            raise ShapeMismatch(qs, ks)
+        if ks != vs:
+            raise ShapeMismatch(ks, vs)
+        ws = [w.shape() for w in (w_q, w_k, w_v, w_o)]
+        if any(len(w) != 2 for w in ws):
+            raise ShapeMismatch(ws[0], [0, 0])
+        d = qs[2]
+        if any(w != [d, d] for w in ws):
+            raise ShapeMismatch(ws[0], [d, d])
+        if num_heads == 0 or d % num_heads != 0:
+            raise InvalidOperation("multi_head_attention",
+                                   f"d_model ({d}) must be divisible by num_heads ({num_heads})")
+        self.q, self.k, self.v = query, key, value
+        self.w_q, self.w_k, self.w_v, self.w_o = w_q, w_k, w_v, w_o
+        self.num_heads = num_heads
+
+    def execute(self) -> Tensor:
+        b, sq, d = self.q.shape()
+        skv = self.k.shape()[1]
+        h = self.num_heads
+        hd = d // h
+        dev = _same_device(self.q, self.k, self.v, self.w_q, self.w_k, self.w_v, self.w_o)
+        qp = _sgemm(dev, b * sq, d, d, self.q, self.w_q, "multi_head_attention")
+        kp = _sgemm(dev, b * skv, d, d, self.k, self.w_k, "multi_head_attention")
+        vp = _sgemm(dev, b * skv, d, d, self.v, self.w_v, "multi_head_attention")
+        o = Tensor.empty([b * sq, d], dev)
+        # head h of row i of batch b is at b*S*d + i*d + h*hd: the [B, S, H, hd] view
+        _sdpa_ex(dev, "multi_head_attention", b, h, h, sq, skv, hd, False,
+                 qp, N.AttnLayout(sq * d, hd, d), kp, N.AttnLayout(skv * d, hd, d),
+                 vp, N.AttnLayout(skv * d, hd, d), o, N.AttnLayout(sq * d, hd, d))
+        return _sgemm(dev, b * sq, d, d, o, self.w_o, "multi_head_attention").reshape([b, sq, d])

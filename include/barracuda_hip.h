@@ -133,6 +133,35 @@ bch_status bch_sdpa_fwd(bch_ctx *ctx, int B, int H, int Sq, int Skv, int D,
                         float scale, int causal, const float *q,
                         const float *k, const float *v, float *o);
 
+/* Layout of one attention operand: element (b, h, i, d) is at
+ * b*batch_stride + h*head_stride + i*row_stride + d (elements; the head
+ * dimension is contiguous).  Dense [B,H,S,D] is {H*S*D, S*D, D}; the
+ * [B,S,H*D] output of a projection GEMM viewed per head is {S*H*D, D, H*D}. */
+typedef struct bch_attn_layout {
+  long long batch_stride;
+  long long head_stride;
+  long long row_stride;
+} bch_attn_layout;
+
+/* bch_sdpa_fwd over strided operands, with Hkv key/value heads shared by
+ * the H query heads (query head h reads key/value head h / (H / Hkv);
+ * H % Hkv == 0, else BCH_E_INVALID "num_q_heads (H) must be divisible by
+ * num_kv_heads (Hkv)").  q, o have H heads and Sq rows; k, v have Hkv heads
+ * and Skv rows.  Strides >= 0, row_stride >= D.  Replaces
+ * GroupedQueryAttention::execute (ops/grouped_query_attention/compute.rs:
+ * 27-121: gqa_matmul_f64.wgsl -> gqa_softmax_f64.wgsl -> gqa_apply_f64.wgsl;
+ * validation mod.rs:84-147) with Hkv < H, and the attention core of
+ * MultiHeadAttention::execute (ops/mha/mod.rs:152-187) together with its
+ * head_split / head_concat copies (ops/mha/projections.rs:18-58,
+ * shaders/tensor/head_split_f64.wgsl, head_concat_f64.wgsl), which become
+ * the strides of the [B,S,H*D] projection buffers. */
+bch_status bch_sdpa_fwd_ex(bch_ctx *ctx, int B, int H, int Hkv, int Sq,
+                           int Skv, int D, float scale, int causal,
+                           const float *q, bch_attn_layout q_layout,
+                           const float *k, bch_attn_layout k_layout,
+                           const float *v, bch_attn_layout v_layout,
+                           float *o, bch_attn_layout o_layout);
+
 /* ---- seeded synthetic inputs, generated in HBM ---- */
 
 /* Fill dst[0..n) from the reference's seeded generators: uniform [lo, hi)

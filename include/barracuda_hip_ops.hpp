@@ -15,6 +15,9 @@
 //   Tensor::scaled_dot_product_attention                   ops/scaled_dot_product_attention/mod.rs:81-226
 //   Tensor::causal_attention, CausalAttention              ops/causal_attn/mod.rs:64-158
 //   FlashAttention                                         ops/flash_attention.rs:45-146
+//   Tensor::grouped_query_attention, GroupedQueryAttention ops/grouped_query_attention/mod.rs:52-226
+//   Tensor::multi_head_attention, MultiHeadAttention       ops/mha/mod.rs:48-263, projections.rs:18-58
+//   Tensor::reshape                                        tensor/mod.rs (shape-only view)
 //   TensorSession, SessionTensor, AttentionDims            session/mod.rs:60-540, session/tensor.rs:14-68
 //   BarracudaError, Result<T>                              error.rs:14-130
 //
@@ -244,6 +247,17 @@ class Tensor {
   inline Result<Tensor> attention(const Tensor& key, const Tensor& value) const;
   inline Result<Tensor> scaled_dot_product_attention(const Tensor& key, const Tensor& value) const;
   inline Result<Tensor> causal_attention(const Tensor& key, const Tensor& value) const;
+  inline Result<Tensor> grouped_query_attention(const Tensor& key, const Tensor& value) const;
+  inline Result<Tensor> multi_head_attention(const Tensor& key, const Tensor& value, const Tensor& w_q,
+                                             const Tensor& w_k, const Tensor& w_v, const Tensor& w_o,
+                                             size_t num_heads) const;
+
+  // Same buffer under a new shape with the same element count (used by
+  // MultiHeadAttention, ops/mha/projections.rs:32-35).
+  Result<Tensor> reshape(std::vector<size_t> shape) const {
+    if (detail::numel(shape) != len()) return BarracudaError::shape_mismatch(shape, shape_);
+    return Tensor(buf_, std::move(shape), dev_);
+  }
 
  private:
   Tensor(std::shared_ptr<detail::DeviceBuffer> b, std::vector<size_t> s, std::shared_ptr<HipDevice> d)
@@ -456,6 +470,128 @@ struct FlashAttention {
   }
 };
 
+namespace detail {
+// bch_sdpa_fwd_ex with scale 1/sqrt(D): strided operands, Hkv key/value heads.
+inline std::optional<BarracudaError> sdpa_ex(const std::shared_ptr<HipDevice>& dev, const char* op, size_t B,
+                                             size_t H, size_t Hkv, size_t Sq, size_t Skv, size_t D, bool causal,
+                                             const Tensor& q, bch_attn_layout ql, const Tensor& k,
+                                             bch_attn_layout kl, const Tensor& v, bch_attn_layout vl,
+                                             const Tensor& o, bch_attn_layout ol) {
+  if (D > 128) return BarracudaError::unsupported(op, dev->name() + " (head_dim " + std::to_string(D) + " > 128)");
+  if (auto e = check_i32(op, {B, H, Hkv, Sq, Skv})) return *e;
+  if (B * H * Sq * D == 0) return std::nullopt;
+  if (Skv == 0) return BarracudaError::invalid_op(op, "key sequence is empty (shape/dimension mismatch)");
+  const float scale = 1.0f / std::sqrt((float)D);
+  std::lock_guard<std::mutex> g(dev->mutex());
+  return dev->check(bch_sdpa_fwd_ex(dev->ctx(), (int)B, (int)H, (int)Hkv, (int)Sq, (int)Skv, (int)D, scale,
+                                    causal ? 1 : 0, q.data_ptr(), ql, k.data_ptr(), kl, v.data_ptr(), vl,
+                                    o.data_ptr(), ol),
+                    op);
+}
+inline bch_attn_layout dense_layout(size_t H, size_t S, size_t D) {
+  return bch_attn_layout{(long long)(H * S * D), (long long)(S * D), (long long)D};
+}
+}  // namespace detail
+
+// ops/grouped_query_attention/mod.rs:84-147: Q [B, Hq, S, D], K = V [B, Hkv, S, D],
+// Hq a multiple of Hkv; query head h attends with key/value head h / (Hq / Hkv).
+// One fused launch replaces the three passes of compute.rs:27-121.
+struct GroupedQueryAttention {
+  const Tensor& q;
+  const Tensor& k;
+  const Tensor& v;
+  static std::optional<BarracudaError> validate(const std::vector<size_t>& qs, const std::vector<size_t>& ks,
+                                                const std::vector<size_t>& vs) {
+    if (qs.size() != 4 || ks.size() != 4 || vs.size() != 4)
+      return BarracudaError::invalid_input("All inputs must be 4D tensors [batch, heads, seq_len, head_dim]");
+    if (ks[0] != qs[0] || ks[2] != qs[2] || ks[3] != qs[3]) return BarracudaError::shape_mismatch(qs, ks);
+    if (vs != ks) return BarracudaError::shape_mismatch(ks, vs);
+    if (ks[1] == 0 || qs[1] % ks[1] != 0)
+      return BarracudaError::invalid_input("num_q_heads (" + std::to_string(qs[1]) +
+                                           ") must be divisible by num_kv_heads (" + std::to_string(ks[1]) + ")");
+    return std::nullopt;
+  }
+  Result<Tensor> execute() const {
+    if (auto e = validate(q.shape(), k.shape(), v.shape())) return *e;
+    if (q.device() != k.device() || q.device() != v.device())
+      return BarracudaError::device("All tensors must be on the same device");
+    const auto& s = q.shape();
+    const size_t B = s[0], Hq = s[1], S = s[2], D = s[3], Hkv = k.shape()[1];
+    auto r = Tensor::empty(s, q.device());
+    if (r.is_err()) return r;
+    Tensor out = std::move(r).unwrap();
+    if (auto e = detail::sdpa_ex(q.device(), "grouped_query_attention", B, Hq, Hkv, S, S, D, false, q,
+                                 detail::dense_layout(Hq, S, D), k, detail::dense_layout(Hkv, S, D), v,
+                                 detail::dense_layout(Hkv, S, D), out, detail::dense_layout(Hq, S, D)))
+      return *e;
+    return out;
+  }
+};
+
+// ops/mha/mod.rs:48-187: query [B, Sq, D], key = value [B, Skv, D], four
+// [D, D] weights, num_heads dividing D.  Q' = query W_q etc. (three GEMMs),
+// attention per head over the [B, S, H, D/H] views of the projections (the
+// reference's head_split / head_concat copies, projections.rs:18-58, become
+// strides), then out = O W_o.
+struct MultiHeadAttention {
+  const Tensor& q;
+  const Tensor& k;
+  const Tensor& v;
+  const Tensor& w_q;
+  const Tensor& w_k;
+  const Tensor& w_v;
+  const Tensor& w_o;
+  size_t num_heads;
+  static std::optional<BarracudaError> validate(const std::vector<size_t>& qs, const std::vector<size_t>& ks,
+                                                const std::vector<size_t>& vs,
+                                                const std::array<std::vector<size_t>, 4>& ws, size_t heads) {
+    if (qs.size() != 3 || ks.size() != 3 || vs.size() != 3) return BarracudaError::shape_mismatch(qs, {0, 0, 0});
+    if (qs[0] != ks[0] || qs[0] != vs[0]) return BarracudaError::shape_mismatch(qs, ks);
+    if (qs[2] != ks[2] || ks[2] != vs[2]) return BarracudaError::shape_mismatch(qs, ks);
+    if (ks != vs) return BarracudaError::shape_mismatch(ks, vs);
+    for (const auto& w : ws)
+      if (w.size() != 2) return BarracudaError::shape_mismatch(ws[0], {0, 0});
+    const size_t d = qs[2];
+    for (const auto& w : ws)
+      if (w != std::vector<size_t>{d, d}) return BarracudaError::shape_mismatch(ws[0], {d, d});
+    if (heads == 0 || d % heads != 0)
+      return BarracudaError::invalid_op("multi_head_attention", "d_model (" + std::to_string(d) +
+                                                                    ") must be divisible by num_heads (" +
+                                                                    std::to_string(heads) + ")");
+    return std::nullopt;
+  }
+  Result<Tensor> execute() const {
+    if (auto e = validate(q.shape(), k.shape(), v.shape(), {w_q.shape(), w_k.shape(), w_v.shape(), w_o.shape()},
+                          num_heads))
+      return *e;
+    const size_t B = q.shape()[0], Sq = q.shape()[1], D = q.shape()[2], Skv = k.shape()[1];
+    const size_t H = num_heads, hd = D / H;
+    auto project = [&](const Tensor& x, size_t S, const Tensor& w) -> Result<Tensor> {
+      auto x2 = x.reshape({B * S, D});
+      if (x2.is_err()) return x2;
+      return MatMul{x2.unwrap(), w}.execute();
+    };
+    auto qp = project(q, Sq, w_q);
+    if (qp.is_err()) return qp;
+    auto kp = project(k, Skv, w_k);
+    if (kp.is_err()) return kp;
+    auto vp = project(v, Skv, w_v);
+    if (vp.is_err()) return vp;
+    auto ro = Tensor::empty({B * Sq, D}, q.device());
+    if (ro.is_err()) return ro;
+    Tensor o = std::move(ro).unwrap();
+    // head h of row i of batch b starts at b*S*D + i*D + h*hd
+    const bch_attn_layout lq{(long long)(Sq * D), (long long)hd, (long long)D};
+    const bch_attn_layout lkv{(long long)(Skv * D), (long long)hd, (long long)D};
+    if (auto e = detail::sdpa_ex(q.device(), "multi_head_attention", B, H, H, Sq, Skv, hd, false, qp.unwrap(), lq,
+                                 kp.unwrap(), lkv, vp.unwrap(), lkv, o, lq))
+      return *e;
+    auto out = MatMul{o, w_o}.execute();
+    if (out.is_err()) return out;
+    return out.unwrap().reshape({B, Sq, D});
+  }
+};
+
 // ---------------------------------------------------------------- Tensor methods
 inline Result<Tensor> Tensor::matmul(const Tensor& other) const { return MatMul{*this, other}.execute(); }
 inline Result<Tensor> Tensor::matmul_ref(const Tensor& other) const { return MatMul{*this, other}.execute(); }
@@ -485,6 +621,14 @@ inline Result<Tensor> Tensor::scaled_dot_product_attention(const Tensor& key, co
 }
 inline Result<Tensor> Tensor::causal_attention(const Tensor& key, const Tensor& value) const {
   return CausalAttention{*this, key, value}.execute();
+}
+inline Result<Tensor> Tensor::grouped_query_attention(const Tensor& key, const Tensor& value) const {
+  return GroupedQueryAttention{*this, key, value}.execute();
+}
+inline Result<Tensor> Tensor::multi_head_attention(const Tensor& key, const Tensor& value, const Tensor& w_q,
+                                                   const Tensor& w_k, const Tensor& w_v, const Tensor& w_o,
+                                                   size_t num_heads) const {
+  return MultiHeadAttention{*this, key, value, w_q, w_k, w_v, w_o, num_heads}.execute();
 }
 
 // ---------------------------------------------------------------- session

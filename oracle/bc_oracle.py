@@ -181,6 +181,54 @@ def causal_attention_cpu_f32(q, k, v, head_begin: int = 0, head_end: int | None 
     return o
 
 
+# ---- callers of the attention core ------------------------------------------------
+def gqa_f64(q, k, v, causal: bool = False, scale: float | None = None) -> np.ndarray:
+    """Grouped-query attention in f64 (ops/grouped_query_attention/compute.rs:27-121;
+    gqa_matmul_f64.wgsl:44-47 maps query head h to key/value head
+    h / heads_per_group, gqa_softmax_f64.wgsl and gqa_apply_f64.wgsl are the
+    row softmax and the P.V product of the plain attention).  The K/V heads
+    are repeated group-wise (head h of the result reads h // group) and the
+    f64 SDPA oracle does the rest.  The reference op is non-causal; causal is
+    the same mask as sdpa_f64's."""
+    hq, hkv = q.shape[1], k.shape[1]
+    g = hq // hkv
+    return sdpa_f64(q, np.repeat(k, g, axis=1), np.repeat(v, g, axis=1), causal, scale)
+
+
+def gqa_3pass_f32(q, k, v) -> np.ndarray:
+    """f32 restatement of the three GQA passes: the same arithmetic as the
+    plain attention's K6 -> K7 -> K9 (score = sequential dot / sqrt(D), max
+    initialised to -1e9, exp, sum, divide; sequential P.V), with the
+    key/value head of query head h being h // (Hq / Hkv)."""
+    hq, hkv = q.shape[1], k.shape[1]
+    g = hq // hkv
+    return attention_3pass_f32(q, np.ascontiguousarray(np.repeat(k, g, axis=1)),
+                               np.ascontiguousarray(np.repeat(v, g, axis=1)), False)
+
+
+def mha_f64(query, key, value, w_q, w_k, w_v, w_o, num_heads: int) -> np.ndarray:
+    """Multi-head attention in float64 throughout (ops/mha/mod.rs:152-187,
+    projections.rs:18-58): project with [D, D] weights, split heads
+    ([B,S,H*hd] -> [B,H,S,hd] as head_split_f64.wgsl indexes it: element
+    (b,h,s,d) <- (b,s,h*hd+d)), non-causal attention with scale 1/sqrt(hd)
+    (the Attention op), concatenate heads (head_concat_f64.wgsl, the inverse
+    map) and project with W_o."""
+    B, Sq, D = query.shape
+    Skv = key.shape[1]
+    H = num_heads
+    hd = D // H
+    f = lambda a: np.asarray(a, dtype=np.float64)
+    split = lambda x, S: x.reshape(B, S, H, hd).transpose(0, 2, 1, 3)
+    qp = split(f(query).reshape(B * Sq, D) @ f(w_q), Sq)
+    kp = split(f(key).reshape(B * Skv, D) @ f(w_k), Skv)
+    vp = split(f(value).reshape(B * Skv, D) @ f(w_v), Skv)
+    s = qp @ kp.transpose(0, 1, 3, 2) / math.sqrt(hd)
+    s = np.exp(s - s.max(axis=-1, keepdims=True))
+    p = s / s.sum(axis=-1, keepdims=True)
+    o = (p @ vp).transpose(0, 2, 1, 3).reshape(B * Sq, D)
+    return (o @ f(w_o)).reshape(B, Sq, D)
+
+
 # ---- metric (tolerances/mod.rs:44-54 scale) ---------------------------------------
 def max_rel_err(x: np.ndarray, ref: np.ndarray) -> float:
     """max |x - ref| / max(|ref|, 1); non-finite values must match exactly."""

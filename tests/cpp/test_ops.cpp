@@ -94,6 +94,23 @@ void cpu_tests() {
     REQUIRE(FlashAttention::validate({4, 8}, {4, 4}, {4, 8})->kind == ErrorKind::InvalidOperation);
     REQUIRE(FlashAttention::validate({1, 4, 8}, {1, 4, 8}, {1, 4, 8})->message.find("2D") != std::string::npos);
   });
+  run("validate_gqa_and_mha", [] {  // grouped_query_attention/mod.rs:84-147, mha/mod.rs:62-126
+    REQUIRE(GroupedQueryAttention::validate({1, 8, 4}, {1, 2, 4, 4}, {1, 2, 4, 4})->kind == ErrorKind::InvalidInput);
+    REQUIRE(GroupedQueryAttention::validate({1, 8, 4, 4}, {1, 2, 5, 4}, {1, 2, 5, 4})->kind ==
+            ErrorKind::ShapeMismatch);
+    REQUIRE(GroupedQueryAttention::validate({1, 8, 4, 4}, {1, 3, 4, 4}, {1, 3, 4, 4})->message ==
+            "Invalid input: num_q_heads (8) must be divisible by num_kv_heads (3)");
+    REQUIRE(!GroupedQueryAttention::validate({1, 8, 4, 4}, {1, 2, 4, 4}, {1, 2, 4, 4}));
+    const std::vector<size_t> x{2, 8, 64}, w{64, 64};
+    const std::array<std::vector<size_t>, 4> ws{w, w, w, w};
+    REQUIRE(MultiHeadAttention::validate({16, 64}, x, x, ws, 8)->kind == ErrorKind::ShapeMismatch);
+    REQUIRE(MultiHeadAttention::validate(x, {2, 16, 64}, {2, 8, 64}, ws, 8)->kind == ErrorKind::ShapeMismatch);
+    REQUIRE(MultiHeadAttention::validate(x, x, x, {w, w, std::vector<size_t>{64, 32}, w}, 8)->kind ==
+            ErrorKind::ShapeMismatch);
+    REQUIRE(MultiHeadAttention::validate(x, x, x, ws, 7)->message ==
+            "Invalid operation: multi_head_attention - d_model (64) must be divisible by num_heads (7)");
+    REQUIRE(!MultiHeadAttention::validate(x, {2, 16, 64}, {2, 16, 64}, ws, 8));  // cross-attention
+  });
   run("status_to_error_mapping", [] {
     REQUIRE(BarracudaError::from_status(BCH_E_OOM, "x", "op").kind == ErrorKind::OutOfMemory);
     REQUIRE(BarracudaError::from_status(BCH_E_SHAPE, "x", "matmul").kind == ErrorKind::InvalidOperation);
@@ -267,6 +284,29 @@ void gpu_tests() {
     for (float x : out) REQUIRE(std::fabs(x - 2.0f) < 1e-5f);
   });
   // crates/barracuda/tests/fault_injection.rs:29-60
+  run("test_grouped_query_attention_basic", [] {  // grouped_query_attention/tests.rs:21-38
+    auto q = T(std::vector<float>(8 * 16, 0.5f), {1, 8, 4, 4});
+    auto kv = T(std::vector<float>(2 * 16, 0.5f), {1, 2, 4, 4});
+    auto out = q.grouped_query_attention(kv, kv).unwrap();
+    REQUIRE(out.shape() == (std::vector<size_t>{1, 8, 4, 4}));
+    for (float x : out.to_vec().unwrap()) REQUIRE(std::fabs(x - 0.5f) <= 1e-6f);
+  });
+  run("test_mha_basic_and_cross_attention", [] {  // mha/tests.rs:9-56, :98-149
+    // q = k = 0.5, v = 1, all weights 0.01, d_model 64, 8 heads: 0.64 per head, out = 0.64 * 0.01 * 64
+    for (size_t skv : {8, 16}) {
+      auto q = T(std::vector<float>(2 * 8 * 64, 0.5f), {2, 8, 64});
+      auto k = T(std::vector<float>(2 * skv * 64, 0.5f), {2, skv, 64});
+      auto v = T(std::vector<float>(2 * skv * 64, 1.0f), {2, skv, 64});
+      auto w = T(std::vector<float>(64 * 64, 0.01f), {64, 64});
+      auto out = q.multi_head_attention(k, v, w, w, w, w, 8).unwrap();
+      REQUIRE(out.shape() == (std::vector<size_t>{2, 8, 64}));
+      const double w64 = (double)0.01f, want = 64 * w64 * 64 * w64;
+      for (float x : out.to_vec().unwrap()) REQUIRE(std::fabs(x - want) <= 1e-5 * want);
+    }
+    auto q = T(std::vector<float>(2 * 8 * 64, 0.5f), {2, 8, 64});
+    auto w = T(std::vector<float>(64 * 64, 0.01f), {64, 64});
+    REQUIRE(q.multi_head_attention(q, q, w, w, w, w, 7).is_err());  // mha/tests.rs:59-96
+  });
   run("test_fault_injection_shape_mismatch", [] {
     auto r = T({1, 2, 3, 4, 5, 6}, {2, 3}).matmul(T({1, 2, 3, 4, 5, 6, 7, 8}, {4, 2}));
     REQUIRE(r.is_err() && has_shape_words(r.error().message));

@@ -153,3 +153,23 @@ def test_op_api_shape_validation_mirrors_reference():
         FlashAttention(T([4, 8]), T([4, 4]), T([4, 8]), 1)
     with pytest.raises(InvalidOperation, match="2D"):
         FlashAttention(T([1, 4, 8]), T([1, 4, 8]), T([1, 4, 8]), 1)
+
+
+def test_sdpa_ex_validation_before_device():
+    lib = N.load()
+    nul = C.c_void_p()
+    dense = N.AttnLayout(8 * 16 * 32, 16 * 32, 32)
+    # num_q_heads must be a multiple of num_kv_heads (grouped_query_attention/mod.rs:118-123)
+    assert lib.bch_sdpa_fwd_ex(nul, 1, 8, 3, 16, 16, 32, 0.25, 0, nul, dense, nul, dense, nul, dense, nul,
+                               dense) == N.BCH_E_INVALID
+    assert "num_q_heads (8) must be divisible by num_kv_heads (3)" in N.last_error(None)
+    assert lib.bch_sdpa_fwd_ex(nul, 1, 8, 0, 16, 16, 32, 0.25, 0, nul, dense, nul, dense, nul, dense, nul,
+                               dense) == N.BCH_E_SHAPE
+    bad = N.AttnLayout(0, 0, 16)  # row stride < D
+    assert lib.bch_sdpa_fwd_ex(nul, 1, 8, 2, 16, 16, 32, 0.25, 0, nul, dense, nul, bad, nul, dense, nul,
+                               dense) == N.BCH_E_INVALID
+    assert "k layout" in N.last_error(None)
+    assert lib.bch_sdpa_fwd_ex(nul, 1, 8, 2, 16, 8, 32, 0.25, 1, nul, dense, nul, dense, nul, dense, nul,
+                               dense) == N.BCH_E_SHAPE
+    assert lib.bch_sdpa_fwd_ex(nul, 1, 8, 2, 16, 16, 32, 0.25, 0, nul, dense, nul, dense, nul, dense, nul,
+                               dense) == N.BCH_E_INVALID  # ctx NULL
