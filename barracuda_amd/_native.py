@@ -22,6 +22,8 @@ BCH_E_MODULE = 5
 BCH_E_LAUNCH = 6
 BCH_E_DEVICE = 7
 BCH_E_UNSUPPORTED = 8
+BCH_ACT_NONE = 0
+BCH_ACT_RELU = 1
 
 _vp = C.c_void_p
 _i = C.c_int
@@ -51,6 +53,7 @@ SIGNATURES = {
     "bch_sync": (_i, [_vp]),
     "bch_copy": (_i, [_vp, _vp, _vp, _sz]),
     "bch_sgemm": (_i, [_vp, _i, _i, _i, _vp, _i, _vp, _i, _vp, _i]),
+    "bch_sgemm_ex": (_i, [_vp, _i, _i, _i, _i, _vp, _i, _vp, _i, _vp, _i, _vp, _i]),
     "bch_sgemm_strided_batched": (_i, [_vp, _i, _i, _i, _i, _vp, _ll, _vp, _ll, _vp, _ll]),
     "bch_softmax_rows": (_i, [_vp, _ll, _ll, _vp, _vp]),
     "bch_softmax_axis": (_i, [_vp, _ll, _ll, _ll, _vp, _vp]),

@@ -45,12 +45,21 @@ hipError_t launch_sgemm(hipStream_t s, int batch, int m, int n, int k,
                         size_t ws_bytes);
 size_t sgemm_workspace_bytes(int batch, int m, int n, int k);
 const char* sgemm_kernel_name(int m, int n, int k);
+// With B given as [n][k] when transb (C = A B^T), and the linear layer's
+// epilogue C = max(acc + bias[col], 0): bias nullable, relu 0/1.
+hipError_t launch_sgemm_ex(hipStream_t s, bool transb, int batch, int m,
+                           int n, int k, const float* A, int lda,
+                           long long sA, const float* B, int ldb,
+                           long long sB, const float* bias, int relu,
+                           float* C, int ldc, long long sC, void* ws,
+                           size_t ws_bytes);
 
-// Skinny (m <= 32) GEMM: streams B once; split-k partials go to ws.
+// Skinny (m <= 32) GEMM: streams B once; split-k partials go to ws; the
+// reduce applies the epilogue (bias nullable, relu 0/1).
 hipError_t launch_sgemm_skinny(hipStream_t s, int m, int n, int k,
                                const float* A, int lda, const float* B,
                                int ldb, float* C, int ldc, void* ws,
-                               size_t ws_bytes);
+                               size_t ws_bytes, const float* bias, int relu);
 size_t sgemm_skinny_workspace_bytes(int m, int n, int k);
 const char* sgemm_skinny_kernel_name(int m);
 bool sgemm_skinny_applies(int m, int n, int k, const float* A, int lda,

@@ -253,6 +253,32 @@ bch_status bch_sync(bch_ctx* ctx) {
   return from_hip(ctx, hipStreamSynchronize(ctx->stream), "bch_sync");
 }
 
+bch_status bch_sgemm_ex(bch_ctx* ctx, int transb, int m, int n, int k, const float* A, int lda, const float* B,
+                        int ldb, const float* bias, int act, float* C, int ldc) {
+  if (transb != 0 && transb != 1) return fail(ctx, BCH_E_INVALID, "linear: transb must be 0 or 1 (got %d)", transb);
+  if (act != BCH_ACT_NONE && act != BCH_ACT_RELU)
+    return fail(ctx, BCH_E_INVALID, "linear: unknown activation %d", act);
+  if (m < 0 || n < 0 || k < 0)
+    return fail(ctx, BCH_E_SHAPE, "linear: negative dimension (m=%d, n=%d, k=%d)", m, n, k);
+  const int kmin = k > 1 ? k : 1, nmin = n > 1 ? n : 1;
+  if (lda < kmin || ldb < (transb ? kmin : nmin) || ldc < nmin)
+    return fail(ctx, BCH_E_SHAPE, "linear: leading dimension too small (lda=%d k=%d, ldb=%d %s=%d, ldc=%d n=%d)",
+                lda, k, ldb, transb ? "k" : "n", transb ? k : n, ldc, n);
+  if (!ctx) return fail(ctx, BCH_E_INVALID, "linear: ctx is NULL");
+  if (m == 0 || n == 0) return BCH_OK;
+  if (!C || (k > 0 && (!A || !B))) return fail(ctx, BCH_E_INVALID, "linear: NULL buffer");
+  bch_status st = use(ctx);
+  if (st != BCH_OK) return st;
+  size_t wsb = transb ? 0 : bch::sgemm_workspace_bytes(1, m, n, k);
+  if (wsb) {
+    st = ensure_ws(ctx, wsb);
+    if (st != BCH_OK) return st;
+  }
+  hipError_t e = bch::launch_sgemm_ex(ctx->stream, transb != 0, 1, m, n, k, A, lda, 0, B, ldb, 0, bias,
+                                      act == BCH_ACT_RELU, C, ldc, 0, ctx->ws, ctx->ws_bytes);
+  return from_hip(ctx, e, "linear launch");
+}
+
 bch_status bch_sgemm_strided_batched(bch_ctx* ctx, int batch, int m, int n, int k,
                                      const float* A, long long strideA, const float* B,
                                      long long strideB, float* C, long long strideC);

@@ -18,7 +18,8 @@
 //     ds_read_b128 per 32-row block feeds four MFMAs.  To make that true for
 //     B as well, B tiles are stored k-contiguous ([n][k]) in LDS: each thread
 //     loads a 4(k) x 4(n) block with four 128-bit global loads and writes it
-//     transposed with four 128-bit LDS stores.
+//     transposed with four 128-bit LDS stores, the lanes of a store phase
+//     covering one LDS row.
 //   * Block tile BM x BN x BK (256x256, 256x128 or 128x128 by shape, see
 //     pick_tile), four wavefronts in a 2x2 grid, each owning a (BM/2) x (BN/2)
 //     sub-tile of (BM/64) x (BN/64) MFMA blocks.  LDS rows
@@ -34,6 +35,13 @@
 //   * CHECK=false needs m % BM == 0, n % BN == 0, k % BK == 0, lda/ldb/
 //     strides multiples of 4 and 16-byte aligned A/B; CHECK=true guards
 //     every load (zero fill) and store and handles any shape and alignment.
+//   * TB: B is given as [n][k] (ldb >= k), C = A B^T -- the linear layer's
+//     y = x W^T with W [out, in] (shaders/misc/linear_f64.wgsl, the layers of
+//     nn/fused_mlp.rs:38-168).  Its tile is already k-contiguous, so it is
+//     loaded like the A tile (128-bit rows straight into LDS [n][k]).
+//   * Epilogue: C = acc (+ bias[col]) (then max(., 0)), fused into the store
+//     -- linear_f64.wgsl adds the bias after the dot product, and fused_mlp
+//     runs relu_f64.wgsl as a separate pass over the output.
 #include "bch_internal.h"
 
 #include <stdint.h>
@@ -62,11 +70,11 @@ __device__ __forceinline__ float4 ld4(const float* p) {
   return *reinterpret_cast<const float4*>(p);
 }
 
-template <int BM, int BN, int BK, bool CHECK>
+template <int BM, int BN, int BK, bool CHECK, bool TB>
 __global__ __launch_bounds__(kThreads) void sgemm_mfma_kernel(
     int M, int N, int K, const float* __restrict__ A, int lda, long long sA,
     const float* __restrict__ B, int ldb, long long sB, float* __restrict__ C,
-    int ldc, long long sC, int tiles_m, int tiles_n) {
+    int ldc, long long sC, int tiles_m, int tiles_n, const float* __restrict__ bias, int relu) {
   using G = Cfg<BM, BN, BK>;
   constexpr int LDK = G::LDK;
   extern __shared__ float4 smem4[];
@@ -108,11 +116,15 @@ __global__ __launch_bounds__(kThreads) void sgemm_mfma_kernel(
   constexpr int A_RSTEP = kThreads / A_TPR;     // rows per float4 round
   const int a_r = tid / A_TPR, a_c = (tid % A_TPR) * 4;
   // B: 4x4 block q covers k rows 4*kq .. +3 and n cols 4*nq .. +3 where
-  //    blk = tid + q*kThreads, nq = blk % (BN/4), kq = blk / (BN/4).
-  constexpr int B_NQ = BN / 4;
+  //    blk = tid + q*kThreads, kq = blk % (BK/4), nq = blk / (BK/4).  The 8
+  //    lanes of an LDS store phase then write one row's 8 consecutive float4
+  //    (128 contiguous bytes, no bank conflict); with nq varying fastest
+  //    they wrote rows 4 apart, 16-way conflicted (measured: 130.5 vs 134.3
+  //    TFLOP/s at 4096^3).  A global load still covers whole 128-byte lines.
+  constexpr int B_KQ = BK / 4;
 
   float4 ra[G::A_F4];
-  float4 rb[G::B_BLK][4];
+  float4 rb[G::B_BLK][4];  // TB: rb[q][e] is float4 number 4q + e of the [n][k] tile rows
 
   auto load_tile = [&](int k0) {
 #pragma unroll
@@ -129,21 +141,39 @@ __global__ __launch_bounds__(kThreads) void sgemm_mfma_kernel(
         ra[f] = make_float4(t[0], t[1], t[2], t[3]);
       }
     }
+    if constexpr (TB) {
+      // rows of B^T are rows of the [n][k] input: same pattern as A
 #pragma unroll
-    for (int q = 0; q < G::B_BLK; ++q) {
-      const int blk = tid + q * kThreads;
-      const int nq = blk % B_NQ, kq = blk / B_NQ;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int gk = k0 + 4 * kq + e, gn = n0 + 4 * nq;
+      for (int f = 0; f < 4 * G::B_BLK; ++f) {
+        const int r = a_r + f * A_RSTEP;
+        const int gr = n0 + r, gc = k0 + a_c;
         if (!CHECK) {
-          rb[q][e] = ld4(B + (long long)gk * ldb + gn);
+          rb[f >> 2][f & 3] = ld4(B + (long long)gr * ldb + gc);
         } else {
           float t[4];
 #pragma unroll
-          for (int c = 0; c < 4; ++c)
-            t[c] = (gk < K && gn + c < N) ? B[(long long)gk * ldb + gn + c] : 0.0f;
-          rb[q][e] = make_float4(t[0], t[1], t[2], t[3]);
+          for (int e = 0; e < 4; ++e)
+            t[e] = (gr < N && gc + e < K) ? B[(long long)gr * ldb + gc + e] : 0.0f;
+          rb[f >> 2][f & 3] = make_float4(t[0], t[1], t[2], t[3]);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < G::B_BLK; ++q) {
+        const int blk = tid + q * kThreads;
+        const int kq = blk % B_KQ, nq = blk / B_KQ;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int gk = k0 + 4 * kq + e, gn = n0 + 4 * nq;
+          if (!CHECK) {
+            rb[q][e] = ld4(B + (long long)gk * ldb + gn);
+          } else {
+            float t[4];
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+              t[c] = (gk < K && gn + c < N) ? B[(long long)gk * ldb + gn + c] : 0.0f;
+            rb[q][e] = make_float4(t[0], t[1], t[2], t[3]);
+          }
         }
       }
     }
@@ -157,10 +187,18 @@ __global__ __launch_bounds__(kThreads) void sgemm_mfma_kernel(
       const int r = a_r + f * A_RSTEP;
       *reinterpret_cast<float4*>(as + r * LDK + a_c) = ra[f];
     }
+    if constexpr (TB) {
+#pragma unroll
+      for (int f = 0; f < 4 * G::B_BLK; ++f) {
+        const int r = a_r + f * A_RSTEP;
+        *reinterpret_cast<float4*>(bs + r * LDK + a_c) = rb[f >> 2][f & 3];
+      }
+      return;
+    }
 #pragma unroll
     for (int q = 0; q < G::B_BLK; ++q) {
       const int blk = tid + q * kThreads;
-      const int nq = blk % B_NQ, kq = blk / B_NQ;
+      const int kq = blk % B_KQ, nq = blk / B_KQ;
       // transpose the 4(k) x 4(n) block: column c of rb -> LDS row n
       float* base = bs + (4 * nq) * LDK + 4 * kq;
       *reinterpret_cast<float4*>(base + 0 * LDK) =
@@ -228,27 +266,33 @@ __global__ __launch_bounds__(kThreads) void sgemm_mfma_kernel(
 
   // ---- epilogue: value r of lane l is row 8*(r/4) + 4*lh + r%4, col li ----
 #pragma unroll
-  for (int i = 0; i < G::TM; ++i) {
+  for (int j = 0; j < G::TN; ++j) {
+    const int col = n0 + wn + j * 32 + li;
+    // bias and relu are uniform over the launch: the branches do not diverge
+    const float bj = bias ? (!CHECK || col < N ? bias[col] : 0.0f) : 0.0f;
 #pragma unroll
-    for (int j = 0; j < G::TN; ++j) {
-      const int col = n0 + wn + j * 32 + li;
+    for (int i = 0; i < G::TM; ++i) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int row = m0 + wm + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-        if (!CHECK || (row < M && col < N)) C[(long long)row * ldc + col] = acc[i][j][r];
+        float v = acc[i][j][r];
+        if (bias) v += bj;
+        if (relu) v = fmaxf(v, 0.0f);
+        if (!CHECK || (row < M && col < N)) C[(long long)row * ldc + col] = v;
       }
     }
   }
 }
 
-template <int BM, int BN, int BK, bool CHECK>
+template <int BM, int BN, int BK, bool CHECK, bool TB>
 hipError_t launch_tiles(hipStream_t s, int batch, int m, int n, int k,
                         const float* A, int lda, long long sA, const float* B,
-                        int ldb, long long sB, float* C, int ldc, long long sC) {
+                        int ldb, long long sB, float* C, int ldc, long long sC,
+                        const float* bias, int relu) {
   using G = Cfg<BM, BN, BK>;
   const int tm = (m + BM - 1) / BM, tn = (n + BN - 1) / BN;
   const size_t lds = sizeof(float) * G::LDS_FLOATS;
-  auto kern = sgemm_mfma_kernel<BM, BN, BK, CHECK>;
+  auto kern = sgemm_mfma_kernel<BM, BN, BK, CHECK, TB>;
   static bool attr_set = false;  // per instantiation
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
@@ -258,7 +302,7 @@ hipError_t launch_tiles(hipStream_t s, int batch, int m, int n, int k,
   }
   if (batch > 65535) return hipErrorInvalidValue;
   hipLaunchKernelGGL(kern, dim3(tm * tn, batch), dim3(kThreads), lds, s, m, n, k,
-                     A, lda, sA, B, ldb, sB, C, ldc, sC, tm, tn);
+                     A, lda, sA, B, ldb, sB, C, ldc, sC, tm, tn, bias, relu);
   return hipGetLastError();
 }
 
@@ -290,16 +334,20 @@ bool fast_ok(Tile t, int m, int n, int k, const float* A, int lda, long long sA,
          sA % 4 == 0 && sB % 4 == 0 && aligned16(A) && aligned16(B);
 }
 
-template <bool CHECK>
+template <bool CHECK, bool TB>
 hipError_t launch_tile(Tile t, hipStream_t s, int batch, int m, int n, int k, const float* A, int lda,
-                       long long sA, const float* B, int ldb, long long sB, float* C, int ldc, long long sC) {
+                       long long sA, const float* B, int ldb, long long sB, float* C, int ldc, long long sC,
+                       const float* bias, int relu) {
   switch (t) {
     case Tile::k256x256:
-      return launch_tiles<256, 256, kBK, CHECK>(s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC);
+      return launch_tiles<256, 256, kBK, CHECK, TB>(s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC, bias,
+                                                    relu);
     case Tile::k256x128:
-      return launch_tiles<256, 128, kBK, CHECK>(s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC);
+      return launch_tiles<256, 128, kBK, CHECK, TB>(s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC, bias,
+                                                    relu);
     default:
-      return launch_tiles<128, 128, kBK, CHECK>(s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC);
+      return launch_tiles<128, 128, kBK, CHECK, TB>(s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC, bias,
+                                                    relu);
   }
 }
 
@@ -332,13 +380,23 @@ size_t sgemm_workspace_bytes(int batch, int m, int n, int k) {
 hipError_t launch_sgemm(hipStream_t s, int batch, int m, int n, int k, const float* A, int lda, long long sA,
                         const float* B, int ldb, long long sB, float* C, int ldc, long long sC, void* ws,
                         size_t ws_bytes) {
+  return launch_sgemm_ex(s, false, batch, m, n, k, A, lda, sA, B, ldb, sB, nullptr, 0, C, ldc, sC, ws, ws_bytes);
+}
+
+hipError_t launch_sgemm_ex(hipStream_t s, bool transb, int batch, int m, int n, int k, const float* A, int lda,
+                           long long sA, const float* B, int ldb, long long sB, const float* bias, int relu,
+                           float* C, int ldc, long long sC, void* ws, size_t ws_bytes) {
   if (batch <= 0 || m <= 0 || n <= 0) return hipSuccess;
-  if (batch == 1 && sgemm_skinny_applies(m, n, k, A, lda, B, ldb))
-    return launch_sgemm_skinny(s, m, n, k, A, lda, B, ldb, C, ldc, ws, ws_bytes);
+  if (!transb && batch == 1 && sgemm_skinny_applies(m, n, k, A, lda, B, ldb))
+    return launch_sgemm_skinny(s, m, n, k, A, lda, B, ldb, C, ldc, ws, ws_bytes, bias, relu);
   const Tile t = pick_tile(batch, m, n);
-  if (fast_ok(t, m, n, k, A, lda, sA, B, ldb, sB))
-    return launch_tile<false>(t, s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC);
-  return launch_tile<true>(t, s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC);
+  // the [n][k] tile loads need the same alignment as the [k][n] ones (ldb, sB multiples of 4)
+  const bool fast = fast_ok(t, m, n, k, A, lda, sA, B, ldb, sB);
+  if (transb)
+    return fast ? launch_tile<false, true>(t, s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC, bias, relu)
+                : launch_tile<true, true>(t, s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC, bias, relu);
+  return fast ? launch_tile<false, false>(t, s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC, bias, relu)
+              : launch_tile<true, false>(t, s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC, bias, relu);
 }
 
 }  // namespace bch

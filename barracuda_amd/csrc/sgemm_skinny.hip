@@ -119,9 +119,16 @@ __global__ __launch_bounds__(256) void sgemm_skinny_fma(int M, int N, int K, con
 }
 
 // C[m][n] = sum over splits s < splits, in split order, of P[s][m][n].  The
-// loads of a batch of 16 partials are all in flight before the adds.
+// loads of a batch of 16 partials are all in flight before the adds.  Then
+// the linear layer's epilogue: + bias[n], max(., 0) (both optional).
+__device__ __forceinline__ float epilogue(float s, const float* __restrict__ bias, int n, int relu) {
+  if (bias) s += bias[n];
+  return relu ? fmaxf(s, 0.0f) : s;
+}
+
 __global__ __launch_bounds__(256) void sgemm_skinny_reduce(int M, int N, const float* __restrict__ P, int splits,
-                                                           float* __restrict__ C, int ldc) {
+                                                           float* __restrict__ C, int ldc,
+                                                           const float* __restrict__ bias, int relu) {
   const long long t = (long long)blockIdx.x * 256 + threadIdx.x;
   if (t >= (long long)M * N) return;
   const long long ps = (long long)M * N;
@@ -134,7 +141,7 @@ __global__ __launch_bounds__(256) void sgemm_skinny_reduce(int M, int N, const f
     for (int q = 0; q < 16; ++q)
       if (i + q < splits) s += v[q];
   }
-  C[(t / N) * ldc + t % N] = s;
+  C[(t / N) * ldc + t % N] = epilogue(s, bias, (int)(t % N), relu);
 }
 
 // ---------------------------------------------------------------- 4 < m <= 32
@@ -438,7 +445,7 @@ __global__ __launch_bounds__(256, 1) void sgemm_skinny_w32(int M, int N, int K, 
 // (the k order); loads in batches of 8, all in flight before the adds.
 __global__ __launch_bounds__(256) void sgemm_skinny_sk_reduce(int M, int N, const float* __restrict__ P, long long U,
                                                               int G, int kb, int smax, float* __restrict__ C,
-                                                              int ldc) {
+                                                              int ldc, const float* __restrict__ bias, int relu) {
   const long long t = (long long)blockIdx.x * 256 + threadIdx.x;
   if (t >= (long long)M * N) return;
   const int m = (int)(t / N), n = (int)(t - (long long)m * N), g = n / kSkCols;
@@ -455,7 +462,7 @@ __global__ __launch_bounds__(256) void sgemm_skinny_sk_reduce(int M, int N, cons
     for (int q = 0; q < 8; ++q)
       if (i + q < ns) s += v[q];
   }
-  C[(long long)m * ldc + n] = s;
+  C[(long long)m * ldc + n] = epilogue(s, bias, n, relu);
 }
 
 bool use_fma(int m) { return m <= 4; }
@@ -610,7 +617,8 @@ const char* sgemm_skinny_kernel_name(int m) {
 }
 
 hipError_t launch_sgemm_skinny(hipStream_t s, int m, int n, int k, const float* A, int lda,
-                               const float* B, int ldb, float* C, int ldc, void* ws, size_t ws_bytes) {
+                               const float* B, int ldb, float* C, int ldc, void* ws, size_t ws_bytes,
+                               const float* bias, int relu) {
   if (ws == nullptr || ws_bytes < sgemm_skinny_workspace_bytes(m, n, k)) return hipErrorInvalidValue;
   float* P = static_cast<float*>(ws);
   const long long total = (long long)m * n;
@@ -627,7 +635,7 @@ hipError_t launch_sgemm_skinny(hipStream_t s, int m, int n, int k, const float* 
       hipLaunchKernelGGL(sgemm_skinny_fma<4>, grid, block, 0, s, m, n, k, A, lda, B, ldb, P, kchunk);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(sgemm_skinny_reduce, rgrid, dim3(256), 0, s, m, n, P, splits, C, ldc);
+    hipLaunchKernelGGL(sgemm_skinny_reduce, rgrid, dim3(256), 0, s, m, n, P, splits, C, ldc, bias, relu);
     return hipGetLastError();
   }
   if (use_w32(m, k, A, lda)) {
@@ -635,7 +643,8 @@ hipError_t launch_sgemm_skinny(hipStream_t s, int m, int n, int k, const float* 
     hipError_t e = k % kW32Rows == 0 ? launch_w32<false>(s, q, m, n, k, A, lda, B, ldb, P)
                                      : launch_w32<true>(s, q, m, n, k, A, lda, B, ldb, P);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(sgemm_skinny_sk_reduce, rgrid, dim3(256), 0, s, m, n, P, q.U, q.G, q.nblk, q.smax, C, ldc);
+    hipLaunchKernelGGL(sgemm_skinny_sk_reduce, rgrid, dim3(256), 0, s, m, n, P, q.U, q.G, q.nblk, q.smax, C, ldc,
+                       bias, relu);
     return hipGetLastError();
   }
   const SkPlan p = sk_plan(m, n, k);
@@ -646,7 +655,8 @@ hipError_t launch_sgemm_skinny(hipStream_t s, int m, int n, int k, const float* 
   else
     e = dma ? launch_sk<2, true>(s, p, m, n, k, A, lda, B, ldb, P) : launch_sk<2, false>(s, p, m, n, k, A, lda, B, ldb, P);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(sgemm_skinny_sk_reduce, rgrid, dim3(256), 0, s, m, n, P, p.U, p.G, p.kb, p.smax, C, ldc);
+  hipLaunchKernelGGL(sgemm_skinny_sk_reduce, rgrid, dim3(256), 0, s, m, n, P, p.U, p.G, p.kb, p.smax, C, ldc, bias,
+                     relu);
   return hipGetLastError();
 }
 

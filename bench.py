@@ -99,7 +99,7 @@ def bench_gemm(dev, steps, warmup):
             "kernel": lib.bch_sgemm_kernel_name(n, n, n).decode()}, (a, b, c)
 
 
-WORKLOADS = ("softmax", "skinny", "batched", "sdpa", "copy")
+WORKLOADS = ("softmax", "skinny", "batched", "sdpa", "linear", "copy")
 
 
 def bench_extra(dev, reps: int = 20, only=None):
@@ -128,7 +128,27 @@ def bench_extra(dev, reps: int = 20, only=None):
         out.update(_bench_batched(dev, T, reps))
     if "sdpa" in want:
         out.update(_bench_sdpa(dev, T, reps))
+    if "linear" in want:
+        out.update(_bench_linear(dev, T, reps))
     return out
+
+
+def _bench_linear(dev, T, reps):
+    """The linear layer of nn::fused_mlp at the GEMM config's size: y =
+    relu(x W^T + b), W [out, in] = [4096, 4096], one launch (bias and ReLU in
+    the GEMM epilogue)."""
+    from barracuda_amd import LcgStream, Tensor
+    from barracuda_amd import _native as N
+    lib, ctx = dev._lib, dev.ctx
+    n = 4096
+    s = LcgStream(5, dev)
+    x, w, b = s.uniform([n, n]), s.uniform([n, n]), s.uniform([n])
+    y = Tensor.empty([n, n], dev)
+    px, pw, pb, py = (C.c_void_p(t.ptr) for t in (x, w, b, y))
+    wall, ev = T.run(lambda i: lib.bch_sgemm_ex(ctx, 1, n, n, n, px, n, pw, n, pb, N.BCH_ACT_RELU, py, n), reps, 3)
+    fl = 2.0 * n ** 3
+    return {"linear_4096_wT_bias_relu": {"TFLOP/s": fl / (ev * 1e-3) / 1e12, "ms": ev,
+                                         "mfma_frac": fl / (ev * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS}}
 
 
 def _bench_softmax(dev, T, reps):
@@ -299,7 +319,7 @@ def main() -> int:
     del keep
     extra = None
     if not args.no_extra:
-        log("extra configs: softmax, skinny, batched, sdpa")
+        log("extra configs: softmax, skinny, batched, sdpa, linear")
         extra = bench_extra(dev)
         for k_, v_ in extra.items():
             log(f"  {k_}: {json.dumps({kk: round(vv, 4) if isinstance(vv, float) else vv for kk, vv in v_.items()})}")

@@ -93,6 +93,24 @@ bch_status bch_sgemm(bch_ctx *ctx, int m, int n, int k,
                      const float *A, int lda, const float *B, int ldb,
                      float *C, int ldc);
 
+/* Activation of bch_sgemm_ex's epilogue. */
+#define BCH_ACT_NONE 0
+#define BCH_ACT_RELU 1 /* max(x, 0): shaders/activation/relu_f64.wgsl */
+
+/* The linear layer: C = act(A . op(B) + bias), row-major, where op(B) = B
+ * for transb == 0 (B [k, n], ldb >= n) and B^T for transb == 1 (B [n, k],
+ * ldb >= k: the weight layout [out_features, in_features] of
+ * shaders/misc/linear_f64.wgsl, y = x W^T + b).  bias (nullable) has n
+ * entries and is added after the dot product, as linear_f64.wgsl does; act
+ * is BCH_ACT_NONE or BCH_ACT_RELU.  Everything happens in the GEMM's own
+ * epilogue: one launch per layer where the reference's nn::fused_mlp
+ * (nn/fused_mlp.rs:38-168) dispatches linear_f64.wgsl and then
+ * relu_f64.wgsl over the output.  transb == 0, act == NONE, bias == NULL is
+ * bch_sgemm. */
+bch_status bch_sgemm_ex(bch_ctx *ctx, int transb, int m, int n, int k,
+                        const float *A, int lda, const float *B, int ldb,
+                        const float *bias, int act, float *C, int ldc);
+
 /* C[b] = A[b] . B[b] for b < batch; A[b] starts at A + b*strideA (elements),
  * leading dimensions k, n, n.  Replaces BatchMatMul::execute
  * (ops/batch_matmul.rs:47-144, kernel K5 batch_matmul_f64.wgsl). */

@@ -18,6 +18,7 @@
 //   Tensor::grouped_query_attention, GroupedQueryAttention ops/grouped_query_attention/mod.rs:52-226
 //   Tensor::multi_head_attention, MultiHeadAttention       ops/mha/mod.rs:48-263, projections.rs:18-58
 //   Tensor::reshape                                        tensor/mod.rs (shape-only view)
+//   nn::fused_mlp, nn::Activation                          nn/fused_mlp.rs:25-168
 //   TensorSession, SessionTensor, AttentionDims            session/mod.rs:60-540, session/tensor.rs:14-68
 //   BarracudaError, Result<T>                              error.rs:14-130
 //
@@ -251,6 +252,10 @@ class Tensor {
   inline Result<Tensor> multi_head_attention(const Tensor& key, const Tensor& value, const Tensor& w_q,
                                              const Tensor& w_k, const Tensor& w_v, const Tensor& w_o,
                                              size_t num_heads) const;
+
+  // A tensor with a shape and no buffer or device: for validation-only
+  // tests of the op structs (nothing may read its data).
+  static Tensor null_for_tests(std::vector<size_t> shape) { return Tensor(nullptr, std::move(shape), nullptr); }
 
   // Same buffer under a new shape with the same element count (used by
   // MultiHeadAttention, ops/mha/projections.rs:32-35).
@@ -630,6 +635,74 @@ inline Result<Tensor> Tensor::multi_head_attention(const Tensor& key, const Tens
                                                    size_t num_heads) const {
   return MultiHeadAttention{*this, key, value, w_q, w_k, w_v, w_o, num_heads}.execute();
 }
+
+// ---------------------------------------------------------------- nn
+namespace nn {
+// nn/fused_mlp.rs:25-31
+enum class Activation { ReLU };
+
+// nn/fused_mlp.rs:38-168: per layer y = relu(x W^T + b) (W [out, in]) or
+// relu(x W + b) (W [in, out]); the reference dispatches linear_f64.wgsl and
+// relu_f64.wgsl per layer, here each layer is one GEMM whose epilogue adds
+// the bias and applies ReLU (bch_sgemm_ex).  Same validation order and
+// messages.  Non-square [in, out] weights: the reference's shader still
+// indexes them as [out, in] (linear_f64.wgsl:35); this computes x W.
+inline Result<Tensor> fused_mlp(const Tensor& input, const std::vector<Tensor>& weights,
+                                const std::vector<Tensor>& biases, Activation activation = Activation::ReLU) {
+  if (weights.size() != biases.size())
+    return BarracudaError::invalid_input("fused_mlp: weights len " + std::to_string(weights.size()) +
+                                         " != biases len " + std::to_string(biases.size()));
+  if (weights.empty()) return BarracudaError::invalid_input("fused_mlp: at least one layer required");
+  const auto& shape = input.shape();
+  if (shape.size() != 2)
+    return BarracudaError::invalid_input("fused_mlp: input must be 2D, got " + shape_str(shape));
+  const size_t batch = shape[0];
+  size_t in_features = shape[1];
+  struct Layer {
+    size_t in, out;
+    int transb;
+  };
+  std::vector<Layer> layers;
+  for (size_t i = 0; i < weights.size(); ++i) {
+    const auto& ws = weights[i].shape();
+    Layer L{};
+    if (ws.size() != 2)
+      return BarracudaError::invalid_input("fused_mlp: weight[" + std::to_string(i) + "] must be 2D");
+    if (ws[1] == in_features)
+      L = {ws[1], ws[0], 1};
+    else if (ws[0] == in_features)
+      L = {ws[0], ws[1], 0};
+    else
+      return BarracudaError::invalid_input("fused_mlp: weight[" + std::to_string(i) + "] shape " + shape_str(ws) +
+                                           " incompatible");
+    if (biases[i].shape() != std::vector<size_t>{L.out})
+      return BarracudaError::invalid_input("fused_mlp: bias[" + std::to_string(i) + "] shape mismatch");
+    layers.push_back(L);
+    in_features = L.out;
+  }
+  auto dev = input.device();
+  const int act = activation == Activation::ReLU ? BCH_ACT_RELU : BCH_ACT_NONE;
+  Tensor x = input;
+  for (size_t i = 0; i < layers.size(); ++i) {
+    const Layer& L = layers[i];
+    if (auto e = detail::check_i32("fused_mlp", {batch, L.in, L.out})) return *e;
+    auto r = Tensor::empty({batch, L.out}, dev);
+    if (r.is_err()) return r;
+    Tensor y = std::move(r).unwrap();
+    if (batch != 0 && L.out != 0) {
+      const int lin = L.in > 1 ? (int)L.in : 1, lout = L.out > 1 ? (int)L.out : 1;
+      std::lock_guard<std::mutex> g(dev->mutex());
+      if (auto e = dev->check(bch_sgemm_ex(dev->ctx(), L.transb, (int)batch, (int)L.out, (int)L.in, x.data_ptr(),
+                                           lin, weights[i].data_ptr(), L.transb ? lin : lout,
+                                           biases[i].data_ptr(), act, y.data_ptr(), lout),
+                              "fused_mlp"))
+        return *e;
+    }
+    x = y;
+  }
+  return x;
+}
+}  // namespace nn
 
 // ---------------------------------------------------------------- session
 // The unit value of Result<()>.

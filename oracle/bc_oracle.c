@@ -260,6 +260,29 @@ BCO_API void bco_matmul_cpu_exec_f32(int m, int n, int k, const float *A,
     }
 }
 
+/* shaders/misc/linear_f64.wgsl:21-44 in f32: y[b][o] = sum over in_f, in
+ * order, of x[b][in_f] * W[o][in_f] (:34-38, sum += x * w, contracted), then
+ * + bias[o] when bias != NULL (:41-43).  W is [out, in] (:17).  relu != 0
+ * then applies relu_f64.wgsl (max(x, 0)) in place, as nn/fused_mlp.rs:
+ * 139-151 dispatches it after every linear layer. */
+BCO_API void bco_linear_f32(int batch, int in_f, int out_f, const float *X,
+                            const float *W, const float *bias, int relu,
+                            float *Y)
+{
+    #pragma omp parallel for collapse(2) schedule(static)
+    for (int b = 0; b < batch; ++b) {
+        for (int o = 0; o < out_f; ++o) {
+            const float *x = X + (long)b * in_f;
+            const float *w = W + (long)o * in_f;
+            float sum = 0.0f;
+            for (int i = 0; i < in_f; ++i) sum = fmaf(x[i], w[i], sum);
+            if (bias) sum += bias[o];
+            if (relu) sum = sum > 0.0f ? sum : 0.0f;
+            Y[(long)b * out_f + o] = sum;
+        }
+    }
+}
+
 /* shaders/math/matmul_gpu_evolved_f64.wgsl:73-152 (K1) in f32: per 32-wide
  * k-tile, groups of four evaluated as a0*b0 + (a1*b1 + (a2*b2 + (a3*b3 +
  * acc))) (:124-127), then the remainder sequentially (:129-138).  The

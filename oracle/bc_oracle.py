@@ -44,6 +44,7 @@ def lib() -> C.CDLL:
         L.bco_softmax_global_f32.argtypes = [C.c_long, _fp, _fp]
         L.bco_attention_3pass_f32.argtypes = [C.c_int] * 6 + [_fp, _fp, _fp, _fp, _ip, C.c_int]
         L.bco_causal_attention_cpu_f32.argtypes = [C.c_int] * 4 + [_fp, _fp, _fp, _fp, C.c_int, C.c_int]
+        L.bco_linear_f32.argtypes = [C.c_int] * 3 + [_fp, _fp, _fp, C.c_int, _fp]
         L.bco_max_rel_err.restype = C.c_double
         L.bco_max_rel_err.argtypes = [C.c_size_t, _fp, _dp]
         L.bco_max_rel_err_f32ref.restype = C.c_double
@@ -227,6 +228,34 @@ def mha_f64(query, key, value, w_q, w_k, w_v, w_o, num_heads: int) -> np.ndarray
     p = s / s.sum(axis=-1, keepdims=True)
     o = (p @ vp).transpose(0, 2, 1, 3).reshape(B * Sq, D)
     return (o @ f(w_o)).reshape(B, Sq, D)
+
+
+def linear_f32(x, w_out_in, bias=None, relu: bool = False) -> np.ndarray:
+    """linear_f64.wgsl in f32 (see bco_linear_f32): x [batch, in], W [out, in]."""
+    batch, in_f = x.shape
+    out_f = w_out_in.shape[0]
+    y = np.empty((batch, out_f), dtype=np.float32)
+    bp = _f(bias) if bias is not None else None
+    lib().bco_linear_f32(batch, in_f, out_f, _f(x), _f(w_out_in), bp, int(relu), _f(y))
+    return y
+
+
+def fused_mlp_f32(x, weights, biases) -> np.ndarray:
+    """nn/fused_mlp.rs:38-168 in f32 on [out, in] weights: every layer is
+    linear_f64.wgsl followed by relu_f64.wgsl, the last one included."""
+    for w, b in zip(weights, biases):
+        x = linear_f32(np.ascontiguousarray(x), np.ascontiguousarray(w), np.ascontiguousarray(b), True)
+    return x
+
+
+def fused_mlp_f64(x, weights, biases) -> np.ndarray:
+    """The fused MLP's mathematical contract in float64: per layer
+    y = max(x W^T + b, 0) with W [out, in] (linear_f64.wgsl:33-43 then
+    relu_f64.wgsl), ReLU after every layer (fused_mlp.rs:139-151)."""
+    y = np.asarray(x, dtype=np.float64)
+    for w, b in zip(weights, biases):
+        y = np.maximum(y @ np.asarray(w, dtype=np.float64).T + np.asarray(b, dtype=np.float64), 0.0)
+    return y
 
 
 # ---- metric (tolerances/mod.rs:44-54 scale) ---------------------------------------

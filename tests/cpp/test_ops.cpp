@@ -111,6 +111,19 @@ void cpu_tests() {
             "Invalid operation: multi_head_attention - d_model (64) must be divisible by num_heads (7)");
     REQUIRE(!MultiHeadAttention::validate(x, {2, 16, 64}, {2, 16, 64}, ws, 8));  // cross-attention
   });
+  run("validate_fused_mlp", [] {  // nn/fused_mlp.rs:44-97 (runs before any device use)
+    auto r = nn::fused_mlp(Tensor::null_for_tests({4, 8}), {}, {});
+    REQUIRE(r.is_err() && r.error().message == "Invalid input: fused_mlp: at least one layer required");
+    auto r2 = nn::fused_mlp(Tensor::null_for_tests({4, 8, 1}), {Tensor::null_for_tests({16, 8})},
+                            {Tensor::null_for_tests({16})});
+    REQUIRE(r2.is_err() && r2.error().message == "Invalid input: fused_mlp: input must be 2D, got [4, 8, 1]");
+    auto r3 = nn::fused_mlp(Tensor::null_for_tests({4, 8}), {Tensor::null_for_tests({5, 7})},
+                            {Tensor::null_for_tests({5})});
+    REQUIRE(r3.is_err() && r3.error().message == "Invalid input: fused_mlp: weight[0] shape [5, 7] incompatible");
+    auto r4 = nn::fused_mlp(Tensor::null_for_tests({4, 8}), {Tensor::null_for_tests({16, 8})},
+                            {Tensor::null_for_tests({8})});
+    REQUIRE(r4.is_err() && r4.error().message == "Invalid input: fused_mlp: bias[0] shape mismatch");
+  });
   run("status_to_error_mapping", [] {
     REQUIRE(BarracudaError::from_status(BCH_E_OOM, "x", "op").kind == ErrorKind::OutOfMemory);
     REQUIRE(BarracudaError::from_status(BCH_E_SHAPE, "x", "matmul").kind == ErrorKind::InvalidOperation);
@@ -306,6 +319,34 @@ void gpu_tests() {
     auto q = T(std::vector<float>(2 * 8 * 64, 0.5f), {2, 8, 64});
     auto w = T(std::vector<float>(64 * 64, 0.01f), {64, 64});
     REQUIRE(q.multi_head_attention(q, q, w, w, w, w, 7).is_err());  // mha/tests.rs:59-96
+  });
+  run("test_fused_mlp_two_layers", [] {  // nn/fused_mlp.rs: linear + relu per layer, W [out, in]
+    const size_t batch = 3, d0 = 4, d1 = 5, d2 = 2;
+    std::vector<float> x(batch * d0), w0(d1 * d0), b0(d1), w1(d2 * d1), b1(d2);
+    for (size_t i = 0; i < x.size(); ++i) x[i] = (float)((int)(i % 7) - 3);
+    for (size_t i = 0; i < w0.size(); ++i) w0[i] = (float)((int)(i % 5) - 2);
+    for (size_t i = 0; i < w1.size(); ++i) w1[i] = (float)((int)(i % 3) - 1);
+    for (size_t i = 0; i < d1; ++i) b0[i] = (float)i - 2.0f;
+    for (size_t i = 0; i < d2; ++i) b1[i] = 0.5f;
+    auto out = nn::fused_mlp(T(x, {batch, d0}), {T(w0, {d1, d0}), T(w1, {d2, d1})}, {T(b0, {d1}), T(b1, {d2})},
+                             nn::Activation::ReLU)
+                   .unwrap();
+    REQUIRE(out.shape() == (std::vector<size_t>{batch, d2}));
+    // integer-valued: exact
+    std::vector<float> h(batch * d1), y(batch * d2);
+    for (size_t b = 0; b < batch; ++b) {
+      for (size_t o = 0; o < d1; ++o) {
+        float s = 0;
+        for (size_t i = 0; i < d0; ++i) s += x[b * d0 + i] * w0[o * d0 + i];
+        h[b * d1 + o] = std::fmax(s + b0[o], 0.0f);
+      }
+      for (size_t o = 0; o < d2; ++o) {
+        float s = 0;
+        for (size_t i = 0; i < d1; ++i) s += h[b * d1 + i] * w1[o * d1 + i];
+        y[b * d2 + o] = std::fmax(s + b1[o], 0.0f);
+      }
+    }
+    REQUIRE(out.to_vec().unwrap() == y);
   });
   run("test_fault_injection_shape_mismatch", [] {
     auto r = T({1, 2, 3, 4, 5, 6}, {2, 3}).matmul(T({1, 2, 3, 4, 5, 6, 7, 8}, {4, 2}));

@@ -173,3 +173,17 @@ def test_sdpa_ex_validation_before_device():
                                dense) == N.BCH_E_SHAPE
     assert lib.bch_sdpa_fwd_ex(nul, 1, 8, 2, 16, 16, 32, 0.25, 0, nul, dense, nul, dense, nul, dense, nul,
                                dense) == N.BCH_E_INVALID  # ctx NULL
+
+
+def test_sgemm_ex_validation_before_device():
+    lib = N.load()
+    nul = C.c_void_p()
+    assert lib.bch_sgemm_ex(nul, 2, 4, 4, 4, nul, 4, nul, 4, nul, 0, nul, 4) == N.BCH_E_INVALID
+    assert "transb" in N.last_error(None)
+    assert lib.bch_sgemm_ex(nul, 0, 4, 4, 4, nul, 4, nul, 4, nul, 7, nul, 4) == N.BCH_E_INVALID
+    assert "activation" in N.last_error(None)
+    # transb: B is [n, k], so ldb >= k
+    assert lib.bch_sgemm_ex(nul, 1, 4, 16, 8, nul, 8, nul, 4, nul, N.BCH_ACT_RELU, nul, 16) == N.BCH_E_SHAPE
+    assert "leading dimension" in N.last_error(None)
+    assert lib.bch_sgemm_ex(nul, 0, 4, 16, 8, nul, 8, nul, 8, nul, N.BCH_ACT_RELU, nul, 16) == N.BCH_E_SHAPE
+    assert lib.bch_sgemm_ex(nul, 1, 4, 16, 8, nul, 8, nul, 8, nul, N.BCH_ACT_RELU, nul, 16) == N.BCH_E_INVALID

@@ -23,6 +23,7 @@ def _run(mode: str) -> str:
 def test_cpp_host_validation_without_device():
     out = _run("--cpu")
     assert "PASS validate_matmul_inner_dim_mismatch" in out
+    assert "PASS validate_fused_mlp" in out
     assert "PASS no_device_is_an_error_value" in out
 
 
@@ -32,5 +33,5 @@ def test_cpp_host_ops_on_gpu():
     for name in ("test_matmul_basic", "test_batch_matmul_basic", "test_softmax_vs_cpu",
                  "test_softmax_dim_rows_and_columns", "test_attention_basic", "test_sdpa_and_causal",
                  "test_fault_injection_shape_mismatch", "test_grouped_query_attention_basic",
-                 "test_mha_basic_and_cross_attention"):
+                 "test_mha_basic_and_cross_attention", "test_fused_mlp_two_layers"):
         assert f"PASS {name}" in out

@@ -1,0 +1,108 @@
+"""The linear layer (bch_sgemm_ex: transposed weights, fused bias + ReLU)
+and nn::fused_mlp on the MI355X vs the oracle.
+
+Tolerance: max |x - ref| / max(|ref|, 1) <= 1e-4 against the f64 oracle
+(oracle.fused_mlp_f64 / numpy float64); the reference's own f32 algorithm
+(linear_f64.wgsl + relu_f64.wgsl, oracle.linear_f32) is held to the same
+bar on the same inputs.  Integer-valued inputs are bit-exact.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from barracuda_amd import Activation, Tensor, fused_mlp
+from barracuda_amd import _native as N
+from oracle import bc_oracle as O
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-4
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+def _up(dev, a):
+    return Tensor.from_data(a, list(a.shape), dev)
+
+
+def _sgemm_ex(dev, transb, x, w, bias, act):
+    m, k = x.shape
+    n = w.shape[0] if transb else w.shape[1]
+    tx, tw = _up(dev, x), _up(dev, w)
+    tb = _up(dev, bias) if bias is not None else None
+    ty = Tensor.empty([m, n], dev)
+    with dev._lock:
+        dev.check(dev._lib.bch_sgemm_ex(dev.ctx, transb, m, n, k, C.c_void_p(tx.ptr), k, C.c_void_p(tw.ptr),
+                                        k if transb else n, C.c_void_p(tb.ptr) if tb else None, act,
+                                        C.c_void_p(ty.ptr), n), "sgemm_ex")
+    return ty.to_numpy()
+
+
+def _ref(x, w, bias, transb, relu):
+    y = x.astype(np.float64) @ (w.astype(np.float64).T if transb else w.astype(np.float64))
+    if bias is not None:
+        y = y + bias.astype(np.float64)
+    return np.maximum(y, 0.0) if relu else y
+
+
+@pytest.mark.parametrize("m,n,k", [(256, 256, 256), (512, 768, 1024), (100, 77, 33), (1, 1024, 512),
+                                   (8, 11008, 256), (32, 512, 4096), (300, 129, 64)])
+@pytest.mark.parametrize("transb", [0, 1])
+def test_sgemm_ex_vs_f64(dev, m, n, k, transb):
+    _say(f"sgemm_ex m={m} n={n} k={k} transb={transb}")
+    rng = O.Lcg(m + 3 * n + 7 * k + transb)
+    x = rng.uniform((m, k))
+    w = rng.uniform((n, k) if transb else (k, n))
+    bias = rng.uniform((n,))
+    for act, b in ((N.BCH_ACT_RELU, bias), (N.BCH_ACT_NONE, bias), (N.BCH_ACT_RELU, None)):
+        got = _sgemm_ex(dev, transb, x, w, b, act)
+        assert O.max_rel_err(got, _ref(x, w, b, transb, act == N.BCH_ACT_RELU)) <= TOL, (act, b is None)
+
+
+@pytest.mark.parametrize("transb", [0, 1])
+def test_sgemm_ex_exact_on_integers(dev, transb):
+    _say(f"sgemm_ex integers transb={transb}")
+    rng = np.random.default_rng(17)
+    for m, n, k in ((256, 256, 64), (4, 64, 96), (50, 70, 90)):
+        x = rng.integers(-8, 9, (m, k)).astype(np.float32)
+        w = rng.integers(-8, 9, (n, k) if transb else (k, n)).astype(np.float32)
+        b = rng.integers(-100, 101, n).astype(np.float32)
+        want = x.astype(np.int64) @ (w.astype(np.int64).T if transb else w.astype(np.int64)) + b
+        got = _sgemm_ex(dev, transb, x, w, b, N.BCH_ACT_RELU)
+        assert np.array_equal(got, np.maximum(want, 0).astype(np.float32))
+        if transb:  # the reference's own f32 algorithm, bit for bit on integers
+            assert np.array_equal(got, O.linear_f32(x, w, b, relu=True))
+
+
+@pytest.mark.parametrize("batch,dims", [(256, [512, 1024, 256, 64]), (7, [33, 65, 17]), (1, [4096, 1024, 4096]),
+                                        (1024, [256, 256, 256])])
+def test_fused_mlp_vs_f64(dev, batch, dims):
+    _say(f"fused_mlp batch={batch} dims={dims}")
+    rng = O.Lcg(batch + sum(dims))
+    x = rng.normal((batch, dims[0]))
+    ws = [rng.normal((dims[i + 1], dims[i]), 0.0, 1.0 / np.sqrt(dims[i])) for i in range(len(dims) - 1)]
+    bs = [rng.normal((dims[i + 1],), 0.0, 0.1) for i in range(len(dims) - 1)]
+    got = fused_mlp(_up(dev, x), [_up(dev, w) for w in ws], [_up(dev, b) for b in bs], Activation.ReLU)
+    assert got.shape() == [batch, dims[-1]]
+    ref = O.fused_mlp_f64(x, ws, bs)
+    assert O.max_rel_err(got.to_numpy(), ref) <= TOL
+    if batch * max(dims) <= 1 << 20:
+        assert O.max_rel_err(got.to_numpy(), O.fused_mlp_f32(x, ws, bs)) <= TOL
+
+
+def test_fused_mlp_in_out_weights_and_square_layers(dev):
+    """[in, out] weights are used as x W; square weights take the [out, in] reading (x W^T)."""
+    _say("fused_mlp mixed weight orientation")
+    rng = O.Lcg(23)
+    x = rng.normal((64, 48))
+    w0 = rng.normal((48, 80), 0.0, 0.15)   # [in, out] (48 != 80): x W
+    w1 = rng.normal((80, 80), 0.0, 0.1)    # square: [out, in], x W^T
+    w2 = rng.normal((10, 80), 0.0, 0.1)    # [out, in]
+    bs = [rng.normal((80,)), rng.normal((80,)), rng.normal((10,))]
+    got = fused_mlp(_up(dev, x), [_up(dev, w0), _up(dev, w1), _up(dev, w2)], [_up(dev, b) for b in bs])
+    ref = O.fused_mlp_f64(x, [w0.T, w1, w2], bs)
+    assert O.max_rel_err(got.to_numpy(), ref) <= TOL

@@ -164,3 +164,52 @@ def test_reshape_is_a_view_with_the_same_element_count():
     assert t.reshape([16, 64]).shape() == [16, 64]
     with pytest.raises(ShapeMismatch):
         t.reshape([15, 64])
+
+
+# ------------------------------------------------------------------ linear / fused MLP
+def test_linear_f32_exact_on_integers():
+    rng = np.random.default_rng(5)
+    x = rng.integers(-8, 9, (6, 13)).astype(np.float32)
+    w = rng.integers(-8, 9, (9, 13)).astype(np.float32)  # [out, in]
+    b = rng.integers(-50, 51, 9).astype(np.float32)
+    want = x.astype(np.int64) @ w.astype(np.int64).T + b.astype(np.int64)
+    assert np.array_equal(O.linear_f32(x, w, b), want.astype(np.float32))
+    assert np.array_equal(O.linear_f32(x, w, b, relu=True), np.maximum(want, 0).astype(np.float32))
+    assert np.array_equal(O.linear_f32(x, w), (x.astype(np.int64) @ w.astype(np.int64).T).astype(np.float32))
+
+
+def test_fused_mlp_oracles_agree_and_closed_forms():
+    rng = np.random.default_rng(8)
+    x = rng.standard_normal((5, 12)).astype(np.float32)
+    ws = [rng.standard_normal((16, 12)).astype(np.float32) / 3, rng.standard_normal((7, 16)).astype(np.float32) / 4]
+    bs = [rng.standard_normal(16).astype(np.float32), rng.standard_normal(7).astype(np.float32)]
+    ref = O.fused_mlp_f64(x, ws, bs)
+    assert O.max_rel_err(O.fused_mlp_f32(x, ws, bs), ref) < 1e-5
+    assert np.all(ref >= 0)  # ReLU after the last layer too
+    # identity weights and zero bias: relu(x)
+    eye = np.eye(12, dtype=np.float32)
+    assert np.array_equal(O.fused_mlp_f64(x, [eye], [np.zeros(12, np.float32)]), np.maximum(x, 0))
+    # planted mistakes: W instead of W^T (non-square), and no ReLU on the last layer
+    wrong = np.maximum(np.maximum(x @ ws[0].T + bs[0], 0) @ ws[1].T + bs[1], -np.inf)
+    assert np.max(np.abs(wrong - ref)) > 1e-2
+    w_sq = rng.standard_normal((12, 12)).astype(np.float32)
+    assert np.max(np.abs(O.fused_mlp_f64(x, [w_sq], [bs[0][:12]]) - np.maximum(x @ w_sq + bs[0][:12], 0))) > 1e-2
+
+
+def test_fused_mlp_validation_mirrors_reference():
+    from barracuda_amd import fused_mlp
+    dev = object()
+    x = _t([4, 8], dev)
+    w1, b1 = _t([16, 8], dev), _t([16], dev)
+    with pytest.raises(InvalidInput, match=r"fused_mlp: weights len 1 != biases len 0"):
+        fused_mlp(x, [w1], [])
+    with pytest.raises(InvalidInput, match="at least one layer required"):
+        fused_mlp(x, [], [])
+    with pytest.raises(InvalidInput, match=r"fused_mlp: input must be 2D, got \[4, 8, 1\]"):
+        fused_mlp(_t([4, 8, 1], dev), [w1], [b1])
+    with pytest.raises(InvalidInput, match=r"fused_mlp: weight\[0\] must be 2D"):
+        fused_mlp(x, [_t([16, 8, 1], dev)], [b1])
+    with pytest.raises(InvalidInput, match=r"fused_mlp: weight\[1\] shape \[5, 7\] incompatible"):
+        fused_mlp(x, [w1, _t([5, 7], dev)], [b1, _t([5], dev)])
+    with pytest.raises(InvalidInput, match=r"fused_mlp: bias\[0\] shape mismatch"):
+        fused_mlp(x, [w1], [_t([8], dev)])
