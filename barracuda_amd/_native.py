@@ -55,6 +55,8 @@ SIGNATURES = {
     "bch_sgemm": (_i, [_vp, _i, _i, _i, _vp, _i, _vp, _i, _vp, _i]),
     "bch_sgemm_ex": (_i, [_vp, _i, _i, _i, _i, _vp, _i, _vp, _i, _vp, _i, _vp, _i]),
     "bch_sgemm_strided_batched": (_i, [_vp, _i, _i, _i, _i, _vp, _ll, _vp, _ll, _vp, _ll]),
+    "bch_dgemm": (_i, [_vp, _i, _i, _i, _i, _i, _i, C.c_double, _vp, _i, _ll, _vp, _i, _ll, C.c_double, _vp,
+                       _i, _ll]),
     "bch_softmax_rows": (_i, [_vp, _ll, _ll, _vp, _vp]),
     "bch_softmax_axis": (_i, [_vp, _ll, _ll, _ll, _vp, _vp]),
     "bch_sdpa_fwd": (_i, [_vp, _i, _i, _i, _i, _i, _f, _i, _vp, _vp, _vp, _vp]),

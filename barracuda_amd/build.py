@@ -36,8 +36,8 @@ DEVICE_FLAGS = [
     "-Wall", "-Wno-unused-function", "-Wno-unused-result",
 ]
 SOURCES = ["bch_runtime.hip", "softmax_rows.hip", "sgemm_mfma.hip",
-           "sgemm_skinny.hip", "sdpa_fwd.hip", "rng_fill.hip",
-           "copy.hip"]
+           "sgemm_skinny.hip", "sdpa_fwd.hip", "dgemm_mfma.hip",
+           "rng_fill.hip", "copy.hip"]
 # Per-file code-generation flags.  The skinny GEMM keeps its MFMA
 # accumulators in VGPRs: with the default heuristics the compiler parks them
 # in AGPRs and copies them back and forth inside the k loop (measured: 716

@@ -65,6 +65,14 @@ const char* sgemm_skinny_kernel_name(int m);
 bool sgemm_skinny_applies(int m, int n, int k, const float* A, int lda,
                           const float* B, int ldb);
 
+// f64 GEMM on the FP64 matrix cores: C[b] = alpha op(A[b]) op(B[b]) (+ beta
+// C[b] when beta != 0); transa: A stored [k][m]; transb: B stored [n][k].
+hipError_t launch_dgemm(hipStream_t s, bool transa, bool transb, int batch,
+                        int m, int n, int k, double alpha, const double* A,
+                        int lda, long long sA, const double* B, int ldb,
+                        long long sB, double beta, double* C, int ldc,
+                        long long sC);
+
 // Seeded fills (rng.rs LCG / lattice Box-Muller); state is the value before.
 hipError_t launch_fill_uniform(hipStream_t s, float* out, uint64_t n, uint64_t state, double lo,
                                double hi);

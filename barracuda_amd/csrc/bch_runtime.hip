@@ -330,6 +330,32 @@ bch_status bch_sgemm_strided_batched(bch_ctx* ctx, int batch, int m, int n, int 
   return from_hip(ctx, e, "batch_matmul launch");
 }
 
+bch_status bch_dgemm(bch_ctx* ctx, int transa, int transb, int batch, int m, int n, int k, double alpha,
+                     const double* A, int lda, long long strideA, const double* B, int ldb, long long strideB,
+                     double beta, double* C, int ldc, long long strideC) {
+  if ((transa != 0 && transa != 1) || (transb != 0 && transb != 1))
+    return fail(ctx, BCH_E_INVALID, "gemm_f64: transpose flags must be 0 or 1 (got %d, %d)", transa, transb);
+  if (batch < 0 || m < 0 || n < 0 || k < 0)
+    return fail(ctx, BCH_E_SHAPE, "gemm_f64: negative dimension (batch=%d, m=%d, n=%d, k=%d)", batch, m, n, k);
+  const int ar = transa ? m : k, br = transb ? k : n;  // stored row lengths of A and B
+  if (lda < (ar > 1 ? ar : 1) || ldb < (br > 1 ? br : 1) || ldc < (n > 1 ? n : 1))
+    return fail(ctx, BCH_E_SHAPE, "gemm_f64: leading dimension too small (lda=%d needs %d, ldb=%d needs %d, "
+                "ldc=%d needs %d)", lda, ar, ldb, br, ldc, n);
+  const long long asz = (long long)(transa ? k : m) * lda, bsz = (long long)(transb ? n : k) * ldb;
+  if (batch > 1 && (strideA < asz || strideB < bsz || strideC < (long long)m * ldc))
+    return fail(ctx, BCH_E_SHAPE, "gemm_f64: batch stride smaller than one matrix (sA=%lld, sB=%lld, sC=%lld)",
+                strideA, strideB, strideC);
+  if (!ctx) return fail(ctx, BCH_E_INVALID, "gemm_f64: ctx is NULL");
+  if (batch == 0 || m == 0 || n == 0) return BCH_OK;
+  if (!C || (k > 0 && (!A || !B))) return fail(ctx, BCH_E_INVALID, "gemm_f64: NULL buffer");
+  bch_status st = use(ctx);
+  if (st != BCH_OK) return st;
+  return from_hip(ctx,
+                  bch::launch_dgemm(ctx->stream, transa != 0, transb != 0, batch, m, n, k, alpha, A, lda, strideA,
+                                    B, ldb, strideB, beta, C, ldc, strideC),
+                  "gemm_f64 launch");
+}
+
 bch_status bch_softmax_rows(bch_ctx* ctx, long long rows, long long cols, const float* in, float* out) {
   if (rows < 1 || cols < 1)
     return fail(ctx, BCH_E_SHAPE, "softmax: empty dimension (rows=%lld, cols=%lld)", rows, cols);

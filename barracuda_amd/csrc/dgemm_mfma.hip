@@ -1,0 +1,253 @@
+// dgemm_mfma.hip -- f64 GEMM on the gfx950 FP64 matrix cores.
+//
+// Replaces GemmF64::{execute, execute_gemm, execute_gemm_ex} and
+// GemmCachedF64 (crates/barracuda/src/ops/linalg/gemm_f64.rs:77-456;
+// shaders/linalg/gemm_f64.wgsl, a 16x16 scalar tile).  Contract, batched:
+//   C[b] = alpha op(A[b]) op(B[b]) (+ beta C[b] when beta != 0),
+// op(A) = A ([m][k]) or A^T (A stored [k][m]), op(B) = B ([k][n]) or B^T
+// (B stored [n][k]), f64 throughout.  With beta == 0, C is not read (the
+// shader's `if (params.beta != 0.0)`, gemm_f64.wgsl:84-89).
+//
+// Design:
+//   * v_mfma_f64_16x16x4_f64: a wavefront multiplies a 16x4 A block by a
+//     4x16 B block into a 16x16 f64 accumulator (4 values per lane).  Lane l
+//     supplies A[l%16][l/16] and B[l/16][l%16]; value r of lane l is
+//     C[l/16 + 4*r][l%16] (rows interleave across the lane quarters, unlike
+//     the f32 16x16 MFMAs' 4*(l/16) + r; checked by the 2 x 2 and ragged
+//     GEMM tests, which a row permutation fails).  The k index a lane quarter feeds is free, so
+//     quarter q takes k = 4q + s in step s of a 16-wide k-tile: four
+//     consecutive k per lane, two 128-bit LDS reads per operand block.
+//   * Block tile 128 x 128 x 16, four wavefronts in a 2x2 grid, each owning
+//     64 x 64 as 4 x 4 MFMA blocks (128 accumulator registers).  LDS holds
+//     both tiles k-contiguous ([m][k], [n][k]), rows padded to 18 doubles so
+//     the 16 rows a read phase touches fall in distinct banks; double
+//     buffered (2 x 36 KB), so two workgroups fit on a CU.
+//   * Tile loads: an operand whose rows are k-contiguous (A, or B^T stored
+//     [n][k]) is copied row by row (8 lanes x 16 bytes per 128-byte row);
+//     one whose rows run along m or n (B [k][n], or A^T stored [k][m]) is
+//     loaded as 2 x 2 blocks and written transposed, the 8 lanes of a store
+//     phase covering one LDS row (no bank conflicts).
+//   * Workgroup -> tile mapping is XCD-aware and grouped, as in the f32 GEMM.
+//   * CHECK=false needs m % 128 == 0, n % 128 == 0, k % 16 == 0, even
+//     leading dimensions and batch strides, 16-byte aligned A and B; CHECK
+//     guards every load (zero fill) and store.
+#include "bch_internal.h"
+
+#include <stdint.h>
+
+namespace {
+
+typedef double f64x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kDT = 256;  // threads
+constexpr int kDBM = 128, kDBN = 128, kDBK = 16;
+constexpr int kDLDK = kDBK + 2;  // padded LDS row, doubles
+
+struct d2 {
+  double x, y;
+};
+
+__device__ __forceinline__ d2 ld2(const double* p) { return *reinterpret_cast<const d2*>(p); }
+
+// Global -> registers for one 128-row x 16-k operand tile of op(X).
+// KCONT: row r, element k of op(X) is X[r * ld + k] (rows k-contiguous);
+// otherwise it is X[k * ld + r] (the stored matrix is [k][rows]).
+// Registers: 4 pairs of doubles per thread either way.
+template <bool KCONT, bool CHECK>
+__device__ __forceinline__ void load_dtile(const double* __restrict__ X, int ld, int rows, int K, int r0, int k0,
+                                           int tid, d2 (&reg)[4]) {
+  if (KCONT) {
+    // pair f: row tid / 8 + 32 f, k 2 * (tid % 8)
+#pragma unroll
+    for (int f = 0; f < 4; ++f) {
+      const int r = r0 + tid / 8 + 32 * f, k = k0 + 2 * (tid % 8);
+      if (!CHECK) {
+        reg[f] = ld2(X + (long long)r * ld + k);
+      } else {
+        reg[f].x = (r < rows && k < K) ? X[(long long)r * ld + k] : 0.0;
+        reg[f].y = (r < rows && k + 1 < K) ? X[(long long)r * ld + k + 1] : 0.0;
+      }
+    }
+  } else {
+    // 2 x 2 block q (q = 0, 1): blk = tid + 256 q, kq = blk % 8, rq = blk / 8;
+    // reg[2q + e] = X[k0 + 2 kq + e][r0 + 2 rq .. +1]
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int blk = tid + kDT * q, kq = blk % 8, rq = blk / 8;
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int k = k0 + 2 * kq + e, r = r0 + 2 * rq;
+        if (!CHECK) {
+          reg[2 * q + e] = ld2(X + (long long)k * ld + r);
+        } else {
+          reg[2 * q + e].x = (k < K && r < rows) ? X[(long long)k * ld + r] : 0.0;
+          reg[2 * q + e].y = (k < K && r + 1 < rows) ? X[(long long)k * ld + r + 1] : 0.0;
+        }
+      }
+    }
+  }
+}
+
+// registers -> LDS tile [128][kDLDK] (k-contiguous)
+template <bool KCONT>
+__device__ __forceinline__ void store_dtile(double* __restrict__ s, int tid, const d2 (&reg)[4]) {
+  if (KCONT) {
+#pragma unroll
+    for (int f = 0; f < 4; ++f) {
+      const int r = tid / 8 + 32 * f, k = 2 * (tid % 8);
+      *reinterpret_cast<d2*>(s + r * kDLDK + k) = reg[f];
+    }
+  } else {
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int blk = tid + kDT * q, kq = blk % 8, rq = blk / 8;
+      // reg[2q + e] holds (k = 2kq + e; rows 2rq, 2rq + 1): row 2rq + c gets (k, k + 1)
+      *reinterpret_cast<d2*>(s + (2 * rq) * kDLDK + 2 * kq) = d2{reg[2 * q].x, reg[2 * q + 1].x};
+      *reinterpret_cast<d2*>(s + (2 * rq + 1) * kDLDK + 2 * kq) = d2{reg[2 * q].y, reg[2 * q + 1].y};
+    }
+  }
+}
+
+template <bool TA, bool TB, bool CHECK>
+__global__ __launch_bounds__(kDT, 2) void dgemm_mfma_kernel(
+    int M, int N, int K, double alpha, const double* __restrict__ A, int lda, long long sA,
+    const double* __restrict__ B, int ldb, long long sB, double beta, double* __restrict__ C, int ldc,
+    long long sC, int tiles_m, int tiles_n) {
+  __shared__ double As[2][kDBM * kDLDK];
+  __shared__ double Bs[2][kDBN * kDLDK];
+
+  // ---- tile mapping (XCD-aware, grouped; as sgemm_mfma_kernel) ----
+  const int ntiles = tiles_m * tiles_n;
+  const int p = blockIdx.x;
+  int lt = p;
+  if ((ntiles & 7) == 0) lt = (p & 7) * (ntiles >> 3) + (p >> 3);
+  constexpr int GROUP = 8;
+  const int group_size = GROUP * tiles_n;
+  const int g = lt / group_size;
+  const int first_m = g * GROUP;
+  const int gm = min(tiles_m - first_m, GROUP);
+  const int within = lt - g * group_size;
+  const int m0 = (first_m + within % gm) * kDBM, n0 = (within / gm) * kDBN;
+
+  const long long bz = blockIdx.y;
+  A += bz * sA;
+  B += bz * sB;
+  C += bz * sC;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int li = lane & 15, lq = lane >> 4;
+  const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+
+  d2 ra[4], rb[4];
+  f64x4 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = (f64x4){0.0, 0.0, 0.0, 0.0};
+
+  const int nk = (K + kDBK - 1) / kDBK;
+  if (nk > 0) {
+    load_dtile<!TA, CHECK>(A, lda, M, K, m0, 0, tid, ra);
+    load_dtile<TB, CHECK>(B, ldb, N, K, n0, 0, tid, rb);
+    store_dtile<!TA>(As[0], tid, ra);
+    store_dtile<TB>(Bs[0], tid, rb);
+  }
+  __syncthreads();
+
+  for (int t = 0; t < nk; ++t) {
+    const int cur = t & 1;
+    if (t + 1 < nk) {
+      load_dtile<!TA, CHECK>(A, lda, M, K, m0, (t + 1) * kDBK, tid, ra);
+      load_dtile<TB, CHECK>(B, ldb, N, K, n0, (t + 1) * kDBK, tid, rb);
+    }
+    const double* as = As[cur] + (wm + li) * kDLDK + 4 * lq;
+    const double* bs = Bs[cur] + (wn + li) * kDLDK + 4 * lq;
+    d2 a[4][2], b[4][2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      a[i][0] = *reinterpret_cast<const d2*>(as + i * 16 * kDLDK);
+      a[i][1] = *reinterpret_cast<const d2*>(as + i * 16 * kDLDK + 2);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      b[j][0] = *reinterpret_cast<const d2*>(bs + j * 16 * kDLDK);
+      b[j][1] = *reinterpret_cast<const d2*>(bs + j * 16 * kDLDK + 2);
+    }
+    // step s uses k = 4 lq + s
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const double av = (s & 1) ? a[i][s >> 1].y : a[i][s >> 1].x;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const double bv = (s & 1) ? b[j][s >> 1].y : b[j][s >> 1].x;
+          acc[i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64(av, bv, acc[i][j], 0, 0, 0);
+        }
+      }
+    }
+    if (t + 1 < nk) {
+      store_dtile<!TA>(As[cur ^ 1], tid, ra);
+      store_dtile<TB>(Bs[cur ^ 1], tid, rb);
+    }
+    __syncthreads();
+  }
+
+  // ---- epilogue: value r of lane (lq, li) is row lq + 4 r, col li of the block ----
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int col = n0 + wn + 16 * j + li;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = m0 + wm + 16 * i + lq + 4 * r;
+        if (!CHECK || (row < M && col < N)) {
+          double* c = C + (long long)row * ldc + col;
+          const double v = alpha * acc[i][j][r];
+          *c = beta != 0.0 ? v + beta * *c : v;
+        }
+      }
+    }
+  }
+}
+
+template <bool TA, bool TB, bool CHECK>
+hipError_t launch_d(hipStream_t s, int batch, int m, int n, int k, double alpha, const double* A, int lda,
+                    long long sA, const double* B, int ldb, long long sB, double beta, double* C, int ldc,
+                    long long sC) {
+  const int tm = (m + kDBM - 1) / kDBM, tn = (n + kDBN - 1) / kDBN;
+  if ((long long)tm * tn > 0x7fffffffLL || batch > 65535) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((dgemm_mfma_kernel<TA, TB, CHECK>), dim3(tm * tn, batch), dim3(kDT), 0, s, m, n, k, alpha, A,
+                     lda, sA, B, ldb, sB, beta, C, ldc, sC, tm, tn);
+  return hipGetLastError();
+}
+
+template <bool TA, bool TB>
+hipError_t launch_ab(hipStream_t s, int batch, int m, int n, int k, double alpha, const double* A, int lda,
+                     long long sA, const double* B, int ldb, long long sB, double beta, double* C, int ldc,
+                     long long sC) {
+  const bool fast = m % kDBM == 0 && n % kDBN == 0 && k % kDBK == 0 && lda % 2 == 0 && ldb % 2 == 0 &&
+                    sA % 2 == 0 && sB % 2 == 0 && (reinterpret_cast<uintptr_t>(A) & 15) == 0 &&
+                    (reinterpret_cast<uintptr_t>(B) & 15) == 0;
+  if (fast) return launch_d<TA, TB, false>(s, batch, m, n, k, alpha, A, lda, sA, B, ldb, sB, beta, C, ldc, sC);
+  return launch_d<TA, TB, true>(s, batch, m, n, k, alpha, A, lda, sA, B, ldb, sB, beta, C, ldc, sC);
+}
+
+}  // namespace
+
+namespace bch {
+
+hipError_t launch_dgemm(hipStream_t s, bool transa, bool transb, int batch, int m, int n, int k, double alpha,
+                        const double* A, int lda, long long sA, const double* B, int ldb, long long sB,
+                        double beta, double* C, int ldc, long long sC) {
+  if (batch <= 0 || m <= 0 || n <= 0) return hipSuccess;
+  if (transa) {
+    if (transb) return launch_ab<true, true>(s, batch, m, n, k, alpha, A, lda, sA, B, ldb, sB, beta, C, ldc, sC);
+    return launch_ab<true, false>(s, batch, m, n, k, alpha, A, lda, sA, B, ldb, sB, beta, C, ldc, sC);
+  }
+  if (transb) return launch_ab<false, true>(s, batch, m, n, k, alpha, A, lda, sA, B, ldb, sB, beta, C, ldc, sC);
+  return launch_ab<false, false>(s, batch, m, n, k, alpha, A, lda, sA, B, ldb, sB, beta, C, ldc, sC);
+}
+
+}  // namespace bch

@@ -19,6 +19,8 @@ from __future__ import annotations
 
 import argparse
 import ctypes as C
+
+import numpy as np
 import json
 import math
 import os
@@ -31,6 +33,7 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, published
 FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense FP32 matrix, published
+FP64_MFMA_PEAK_TFLOPS = 78.6   # MI355X dense FP64 matrix, published
 PROFILES = ROOT / "profiles"
 
 
@@ -99,7 +102,7 @@ def bench_gemm(dev, steps, warmup):
             "kernel": lib.bch_sgemm_kernel_name(n, n, n).decode()}, (a, b, c)
 
 
-WORKLOADS = ("softmax", "skinny", "batched", "sdpa", "linear", "copy")
+WORKLOADS = ("softmax", "skinny", "batched", "sdpa", "linear", "dgemm", "copy")
 
 
 def bench_extra(dev, reps: int = 20, only=None):
@@ -130,7 +133,27 @@ def bench_extra(dev, reps: int = 20, only=None):
         out.update(_bench_sdpa(dev, T, reps))
     if "linear" in want:
         out.update(_bench_linear(dev, T, reps))
+    if "dgemm" in want:
+        out.update(_bench_dgemm(dev, T, reps))
     return out
+
+
+def _bench_dgemm(dev, T, reps):
+    """GemmF64 (ops/linalg/gemm_f64.rs) at 4096^3 on the FP64 matrix cores,
+    operands resident in HBM."""
+    from barracuda_amd import F64Buffer
+    lib, ctx = dev._lib, dev.ctx
+    n = 4096
+    rng = np.random.default_rng(2)
+    a = F64Buffer(dev, n * n).upload(rng.uniform(-1, 1, n * n))
+    b = F64Buffer(dev, n * n).upload(rng.uniform(-1, 1, n * n))
+    c = F64Buffer(dev, n * n)
+    pa, pb, pc = C.c_void_p(a.ptr), C.c_void_p(b.ptr), C.c_void_p(c.ptr)
+    wall, ev = T.run(lambda i: lib.bch_dgemm(ctx, 0, 0, 1, n, n, n, 1.0, pa, n, n * n, pb, n, n * n, 0.0, pc, n,
+                                             n * n), max(5, reps // 2), 2)
+    fl = 2.0 * n ** 3
+    return {"dgemm_4096": {"TFLOP/s": fl / (ev * 1e-3) / 1e12, "ms": ev,
+                           "fp64_mfma_frac": fl / (ev * 1e-3) / 1e12 / FP64_MFMA_PEAK_TFLOPS}}
 
 
 def _bench_linear(dev, T, reps):
@@ -319,7 +342,7 @@ def main() -> int:
     del keep
     extra = None
     if not args.no_extra:
-        log("extra configs: softmax, skinny, batched, sdpa, linear")
+        log("extra configs: softmax, skinny, batched, sdpa, linear, dgemm")
         extra = bench_extra(dev)
         for k_, v_ in extra.items():
             log(f"  {k_}: {json.dumps({kk: round(vv, 4) if isinstance(vv, float) else vv for kk, vv in v_.items()})}")

@@ -119,6 +119,23 @@ bch_status bch_sgemm_strided_batched(bch_ctx *ctx, int batch, int m, int n,
                                      const float *B, long long strideB,
                                      float *C, long long strideC);
 
+/* f64 GEMM on the FP64 matrix cores, batched:
+ *   C[b] = alpha * op(A[b]) * op(B[b])          (beta == 0: C is not read)
+ *   C[b] = alpha * op(A[b]) * op(B[b]) + beta * C[b]   (beta != 0)
+ * op(A) = A stored [m][k] (lda >= k) when transa == 0, A^T of A stored
+ * [k][m] (lda >= m) when transa == 1; op(B) = B [k][n] (ldb >= n) or B^T
+ * of B stored [n][k] (ldb >= k).  C [m][n], ldc >= n.  Batch b's matrices
+ * start at A + b*strideA, B + b*strideB, C + b*strideC (elements).
+ * Replaces GemmF64::execute / execute_gemm / execute_gemm_ex and
+ * GemmCachedF64::{multiply, execute_to_buffer} (ops/linalg/gemm_f64.rs:
+ * 77-456, shaders/linalg/gemm_f64.wgsl), whose buffers are packed:
+ * strides m*k, k*n, m*n. */
+bch_status bch_dgemm(bch_ctx *ctx, int transa, int transb, int batch, int m,
+                     int n, int k, double alpha, const double *A, int lda,
+                     long long strideA, const double *B, int ldb,
+                     long long strideB, double beta, double *C, int ldc,
+                     long long strideC);
+
 /* Row-wise numerically stable softmax: out[r,:] = exp(x - max_r) / sum.
  * rows, cols >= 1; in == out is allowed.  Replaces Tensor::softmax_dim
  * (ops/tensor_axis_ops.rs:67-126) for the last axis, the attention row

@@ -19,6 +19,7 @@
 //   Tensor::multi_head_attention, MultiHeadAttention       ops/mha/mod.rs:48-263, projections.rs:18-58
 //   Tensor::reshape                                        tensor/mod.rs (shape-only view)
 //   nn::fused_mlp, nn::Activation                          nn/fused_mlp.rs:25-168
+//   GemmF64, GemmCachedF64                                 ops/linalg/gemm_f64.rs:77-456
 //   TensorSession, SessionTensor, AttentionDims            session/mod.rs:60-540, session/tensor.rs:14-68
 //   BarracudaError, Result<T>                              error.rs:14-130
 //
@@ -28,6 +29,7 @@
 // Rust; unwrap() on an error throws std::runtime_error with the message.
 #pragma once
 
+#include <algorithm>
 #include <array>
 #include <climits>
 #include <cmath>
@@ -703,6 +705,99 @@ inline Result<Tensor> fused_mlp(const Tensor& input, const std::vector<Tensor>& 
   return x;
 }
 }  // namespace nn
+
+// ---------------------------------------------------------------- f64 GEMM
+// ops/linalg/gemm_f64.rs:77-249: batched C = alpha op(A) op(B) + beta C over
+// packed row-major f64 host data (the reference's C buffer starts zeroed, so
+// beta multiplies zero).  One bch_dgemm on the FP64 matrix cores.
+struct GemmF64 {
+  static Result<std::vector<double>> execute(const std::shared_ptr<HipDevice>& dev, const std::vector<double>& a,
+                                             const std::vector<double>& b, size_t m, size_t k, size_t n,
+                                             size_t batch_size) {
+    return execute_gemm(dev, a, b, m, k, n, batch_size, 1.0, 0.0);
+  }
+  static Result<std::vector<double>> execute_gemm(const std::shared_ptr<HipDevice>& dev,
+                                                  const std::vector<double>& a, const std::vector<double>& b,
+                                                  size_t m, size_t k, size_t n, size_t batch_size, double alpha,
+                                                  double beta) {
+    return execute_gemm_ex(dev, a, b, m, k, n, batch_size, alpha, beta, false, false);
+  }
+  static Result<std::vector<double>> execute_gemm_ex(const std::shared_ptr<HipDevice>& dev,
+                                                     const std::vector<double>& a, const std::vector<double>& b,
+                                                     size_t m, size_t k, size_t n, size_t batch_size, double alpha,
+                                                     double beta, bool trans_a, bool trans_b) {
+    const size_t ea = batch_size * m * k, eb = batch_size * k * n;
+    if (a.size() != ea)
+      return BarracudaError::invalid_input("A: expected " + std::to_string(ea) + " elements, got " +
+                                           std::to_string(a.size()));
+    if (b.size() != eb)
+      return BarracudaError::invalid_input("B: expected " + std::to_string(eb) + " elements, got " +
+                                           std::to_string(b.size()));
+    std::vector<double> c(batch_size * m * n, 0.0);
+    if (auto e = run(dev, a, b, c, m, k, n, batch_size, alpha, beta, trans_a, trans_b)) return *e;
+    return c;
+  }
+
+  // upload a and b, run bch_dgemm with c as the initial C, read C back into c
+  static std::optional<BarracudaError> run(const std::shared_ptr<HipDevice>& dev, const std::vector<double>& a,
+                                           const std::vector<double>& b, std::vector<double>& c, size_t m, size_t k,
+                                           size_t n, size_t batch, double alpha, double beta, bool ta, bool tb) {
+    if (auto e = detail::check_i32("gemm_f64", {batch, m, n, k})) return e;
+    if (c.empty()) return std::nullopt;
+    std::lock_guard<std::mutex> g(dev->mutex());
+    void *pa = nullptr, *pb = nullptr, *pc = nullptr;
+    std::optional<BarracudaError> err;
+    auto chk = [&](bch_status st, const char* op) {
+      if (!err) err = dev->check(st, op);
+      return !err;
+    };
+    if (chk(bch_alloc(dev->ctx(), a.size() * 8, &pa), "alloc_buffer") &&
+        chk(bch_alloc(dev->ctx(), b.size() * 8, &pb), "alloc_buffer") &&
+        chk(bch_alloc(dev->ctx(), c.size() * 8, &pc), "alloc_buffer") &&
+        (a.empty() || chk(bch_upload(dev->ctx(), pa, a.data(), a.size() * 8), "upload")) &&
+        (b.empty() || chk(bch_upload(dev->ctx(), pb, b.data(), b.size() * 8), "upload")) &&
+        chk(bch_upload(dev->ctx(), pc, c.data(), c.size() * 8), "upload")) {
+      const int lda = (int)std::max<size_t>(ta ? m : k, 1), ldb = (int)std::max<size_t>(tb ? k : n, 1);
+      if (chk(bch_dgemm(dev->ctx(), ta, tb, (int)batch, (int)m, (int)n, (int)k, alpha, static_cast<double*>(pa), lda,
+                        (long long)(m * k), static_cast<double*>(pb), ldb, (long long)(k * n), beta,
+                        static_cast<double*>(pc), (int)std::max<size_t>(n, 1), (long long)(m * n)),
+              "gemm_f64"))
+        chk(bch_download(dev->ctx(), c.data(), pc, c.size() * 8), "download");
+    }
+    for (void* p : {pa, pb, pc})
+      if (p) bch_free(dev->ctx(), p);
+    return err;
+  }
+};
+
+// ops/linalg/gemm_f64.rs:252-456: B held on the device, C = A B for many A
+// (the reference's dispatch swaps its m and n grid dimensions; here every
+// element is computed whatever m and n are).
+class GemmCachedF64 {
+ public:
+  static Result<GemmCachedF64> create(std::shared_ptr<HipDevice> dev, const std::vector<double>& b, size_t k,
+                                      size_t n, size_t batch_size) {
+    if (b.size() != batch_size * k * n)
+      return BarracudaError::invalid_input("GemmCachedF64: B has " + std::to_string(b.size()) +
+                                           " elements, expected batch×K×N=" + std::to_string(batch_size * k * n));
+    return GemmCachedF64(std::move(dev), b, k, n, batch_size);
+  }
+  Result<std::vector<double>> multiply(const std::vector<double>& a, size_t m) const {
+    if (a.size() != batch_size * m * k)
+      return BarracudaError::invalid_input("GemmCachedF64::execute_to_buffer: A has " + std::to_string(a.size()) +
+                                           " elements, expected batch×M×K=" + std::to_string(batch_size * m * k));
+    std::vector<double> c(batch_size * m * n, 0.0);
+    if (auto e = GemmF64::run(dev_, a, b_, c, m, k, n, batch_size, 1.0, 0.0, false, false)) return *e;
+    return c;
+  }
+  size_t k, n, batch_size;
+
+ private:
+  GemmCachedF64(std::shared_ptr<HipDevice> dev, std::vector<double> b, size_t k_, size_t n_, size_t batch)
+      : k(k_), n(n_), batch_size(batch), dev_(std::move(dev)), b_(std::move(b)) {}
+  std::shared_ptr<HipDevice> dev_;
+  std::vector<double> b_;
+};
 
 // ---------------------------------------------------------------- session
 // The unit value of Result<()>.

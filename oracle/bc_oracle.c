@@ -260,6 +260,37 @@ BCO_API void bco_matmul_cpu_exec_f32(int m, int n, int k, const float *A,
     }
 }
 
+/* shaders/linalg/gemm_f64.wgsl:33-91 (GemmF64, ops/linalg/gemm_f64.rs:
+ * 153-249): per batch b (packed strides m*k, k*n, m*n), per (row, col),
+ * acc = acc + A(row, kk) * B(kk, col) over kk in order (16-wide tiles
+ * walked in order, :63-80; contracted), A(row, kk) = A[row*k + kk] or, with
+ * trans_a, A[kk*m + row] (:51-56), likewise B; then C = alpha * acc, plus
+ * beta * C_in when beta != 0 (:84-89).  cin may be NULL (read as zero). */
+BCO_API void bco_gemm_f64_wgsl(int trans_a, int trans_b, int batch, int m,
+                               int n, int k, double alpha, const double *A,
+                               const double *B, double beta,
+                               const double *cin, double *C)
+{
+    #pragma omp parallel for collapse(2) schedule(static)
+    for (int b = 0; b < batch; ++b) {
+        for (int row = 0; row < m; ++row) {
+            const double *a = A + (long)b * m * k;
+            const double *bb = B + (long)b * k * n;
+            for (int col = 0; col < n; ++col) {
+                double acc = 0.0;
+                for (int kk = 0; kk < k; ++kk) {
+                    const double av = trans_a ? a[(long)kk * m + row] : a[(long)row * k + kk];
+                    const double bv = trans_b ? bb[(long)col * k + kk] : bb[(long)kk * n + col];
+                    acc = fma(av, bv, acc);
+                }
+                const long ci = (long)b * m * n + (long)row * n + col;
+                const double c0 = cin ? cin[ci] : 0.0;
+                C[ci] = beta != 0.0 ? alpha * acc + beta * c0 : alpha * acc;
+            }
+        }
+    }
+}
+
 /* shaders/misc/linear_f64.wgsl:21-44 in f32: y[b][o] = sum over in_f, in
  * order, of x[b][in_f] * W[o][in_f] (:34-38, sum += x * w, contracted), then
  * + bias[o] when bias != NULL (:41-43).  W is [out, in] (:17).  relu != 0

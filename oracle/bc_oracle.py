@@ -45,6 +45,7 @@ def lib() -> C.CDLL:
         L.bco_attention_3pass_f32.argtypes = [C.c_int] * 6 + [_fp, _fp, _fp, _fp, _ip, C.c_int]
         L.bco_causal_attention_cpu_f32.argtypes = [C.c_int] * 4 + [_fp, _fp, _fp, _fp, C.c_int, C.c_int]
         L.bco_linear_f32.argtypes = [C.c_int] * 3 + [_fp, _fp, _fp, C.c_int, _fp]
+        L.bco_gemm_f64_wgsl.argtypes = [C.c_int] * 6 + [C.c_double, _dp, _dp, C.c_double, _dp, _dp]
         L.bco_max_rel_err.restype = C.c_double
         L.bco_max_rel_err.argtypes = [C.c_size_t, _fp, _dp]
         L.bco_max_rel_err_f32ref.restype = C.c_double
@@ -256,6 +257,32 @@ def fused_mlp_f64(x, weights, biases) -> np.ndarray:
     for w, b in zip(weights, biases):
         y = np.maximum(y @ np.asarray(w, dtype=np.float64).T + np.asarray(b, dtype=np.float64), 0.0)
     return y
+
+
+def gemm_f64_wgsl(a, b, m: int, k: int, n: int, batch: int, alpha: float = 1.0, beta: float = 0.0,
+                  trans_a: bool = False, trans_b: bool = False, c_in=None) -> np.ndarray:
+    """gemm_f64.wgsl restated in C (bco_gemm_f64_wgsl): packed f64 inputs, flat f64 output."""
+    a = np.ascontiguousarray(a, dtype=np.float64).reshape(-1)
+    b = np.ascontiguousarray(b, dtype=np.float64).reshape(-1)
+    c = np.empty(batch * m * n, dtype=np.float64)
+    ci = None if c_in is None else _d(np.ascontiguousarray(c_in, dtype=np.float64).reshape(-1))
+    lib().bco_gemm_f64_wgsl(int(trans_a), int(trans_b), batch, m, n, k, alpha, _d(a), _d(b), beta, ci, _d(c))
+    return c
+
+
+def gemm_longdouble(a, b, m: int, k: int, n: int, batch: int, trans_a: bool = False,
+                    trans_b: bool = False) -> np.ndarray:
+    """op(A) op(B) per batch in numpy longdouble (x87 80-bit here): the
+    accuracy yardstick for the f64 GEMM, flat output."""
+    A = np.asarray(a, dtype=np.longdouble).reshape(batch, k, m) if trans_a else \
+        np.asarray(a, dtype=np.longdouble).reshape(batch, m, k)
+    B = np.asarray(b, dtype=np.longdouble).reshape(batch, n, k) if trans_b else \
+        np.asarray(b, dtype=np.longdouble).reshape(batch, k, n)
+    if trans_a:
+        A = A.transpose(0, 2, 1)
+    if trans_b:
+        B = B.transpose(0, 2, 1)
+    return np.matmul(A, B).reshape(-1)
 
 
 # ---- metric (tolerances/mod.rs:44-54 scale) ---------------------------------------

@@ -348,6 +348,23 @@ void gpu_tests() {
     }
     REQUIRE(out.to_vec().unwrap() == y);
   });
+  run("test_gemm_f64_basic_transpose_batched", [] {  // ops/linalg/gemm_f64.rs tests
+    const std::vector<double> want{19, 22, 43, 50};
+    REQUIRE(GemmF64::execute(g_dev, {1, 2, 3, 4}, {5, 6, 7, 8}, 2, 2, 2, 1).unwrap() == want);
+    REQUIRE(GemmF64::execute_gemm_ex(g_dev, {1, 3, 2, 4}, {5, 6, 7, 8}, 2, 2, 2, 1, 1.0, 0.0, true, false).unwrap() ==
+            want);
+    REQUIRE(GemmF64::execute_gemm_ex(g_dev, {1, 2, 3, 4}, {5, 7, 6, 8}, 2, 2, 2, 1, 1.0, 0.0, false, true).unwrap() ==
+            want);
+    std::vector<double> a{1, 0, 0, 0, 1, 0, 0, 0, 1, 2, 0, 0, 0, 2, 0, 0, 0, 2}, b;
+    for (int r = 0; r < 2; ++r)
+      for (int i = 1; i <= 9; ++i) b.push_back(i);
+    auto c = GemmF64::execute(g_dev, a, b, 3, 3, 3, 2).unwrap();
+    REQUIRE(c[0] == 1.0 && c[4] == 5.0 && c[9] == 2.0 && c[13] == 10.0);
+    REQUIRE(GemmF64::execute(g_dev, {1, 2, 3}, {1, 2, 3, 4}, 2, 2, 2, 1).error().message ==
+            "Invalid input: A: expected 4 elements, got 3");
+    auto cached = GemmCachedF64::create(g_dev, {5, 6, 7, 8, 9, 10}, 2, 3, 1).unwrap();
+    REQUIRE(cached.multiply({1, 2}, 1).unwrap() == (std::vector<double>{21, 24, 27}));  // [1 2] [[5 6 7] [8 9 10]]
+  });
   run("test_fault_injection_shape_mismatch", [] {
     auto r = T({1, 2, 3, 4, 5, 6}, {2, 3}).matmul(T({1, 2, 3, 4, 5, 6, 7, 8}, {4, 2}));
     REQUIRE(r.is_err() && has_shape_words(r.error().message));

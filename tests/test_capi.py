@@ -187,3 +187,16 @@ def test_sgemm_ex_validation_before_device():
     assert "leading dimension" in N.last_error(None)
     assert lib.bch_sgemm_ex(nul, 0, 4, 16, 8, nul, 8, nul, 8, nul, N.BCH_ACT_RELU, nul, 16) == N.BCH_E_SHAPE
     assert lib.bch_sgemm_ex(nul, 1, 4, 16, 8, nul, 8, nul, 8, nul, N.BCH_ACT_RELU, nul, 16) == N.BCH_E_INVALID
+
+
+def test_dgemm_validation_before_device():
+    lib = N.load()
+    nul = C.c_void_p()
+    assert lib.bch_dgemm(nul, 2, 0, 1, 4, 4, 4, 1.0, nul, 4, 16, nul, 4, 16, 0.0, nul, 4, 16) == N.BCH_E_INVALID
+    assert lib.bch_dgemm(nul, 0, 0, 1, -1, 4, 4, 1.0, nul, 4, 16, nul, 4, 16, 0.0, nul, 4, 16) == N.BCH_E_SHAPE
+    # transa: A stored [k][m], lda >= m
+    assert lib.bch_dgemm(nul, 1, 0, 1, 8, 4, 2, 1.0, nul, 2, 16, nul, 4, 8, 0.0, nul, 4, 32) == N.BCH_E_SHAPE
+    assert "leading dimension" in N.last_error(None)
+    assert lib.bch_dgemm(nul, 0, 0, 2, 4, 4, 4, 1.0, nul, 4, 8, nul, 4, 16, 0.0, nul, 4, 16) == N.BCH_E_SHAPE
+    assert "batch stride" in N.last_error(None)
+    assert lib.bch_dgemm(nul, 1, 1, 2, 4, 4, 4, 1.0, nul, 4, 16, nul, 4, 16, 0.0, nul, 4, 16) == N.BCH_E_INVALID

@@ -33,5 +33,6 @@ def test_cpp_host_ops_on_gpu():
     for name in ("test_matmul_basic", "test_batch_matmul_basic", "test_softmax_vs_cpu",
                  "test_softmax_dim_rows_and_columns", "test_attention_basic", "test_sdpa_and_causal",
                  "test_fault_injection_shape_mismatch", "test_grouped_query_attention_basic",
-                 "test_mha_basic_and_cross_attention", "test_fused_mlp_two_layers"):
+                 "test_mha_basic_and_cross_attention", "test_fused_mlp_two_layers",
+                 "test_gemm_f64_basic_transpose_batched"):
         assert f"PASS {name}" in out

@@ -1,0 +1,108 @@
+"""f64 GEMM on the MI355X FP64 matrix cores (bch_dgemm, GemmF64,
+GemmCachedF64) vs the oracle.
+
+Tolerance: max |x - ref| / max(|ref|, 1) <= 1e-12 against a longdouble
+product (oracle.gemm_longdouble); the reference's own algorithm restated in
+f64 (oracle.gemm_f64_wgsl) is held to the same bar.  The reference tests'
+vectors and integer-valued inputs are bit-exact.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from barracuda_amd import F64Buffer, GemmCachedF64, GemmF64
+from oracle import bc_oracle as O
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-12
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+def _rel(x, ref) -> float:
+    ref = np.asarray(ref, dtype=np.float64)
+    return float(np.max(np.abs(np.asarray(x) - ref) / np.maximum(np.abs(ref), 1.0)))
+
+
+def test_reference_vectors(dev):
+    _say("dgemm reference vectors")
+    assert GemmF64.execute(dev, [1, 2, 3, 4], [5, 6, 7, 8], 2, 2, 2, 1).tolist() == [19, 22, 43, 50]
+    assert GemmF64.execute_gemm_ex(dev, [1, 3, 2, 4], [5, 6, 7, 8], 2, 2, 2, 1, 1.0, 0.0, True, False).tolist() == \
+        [19, 22, 43, 50]
+    assert GemmF64.execute_gemm_ex(dev, [1, 2, 3, 4], [5, 7, 6, 8], 2, 2, 2, 1, 1.0, 0.0, False, True).tolist() == \
+        [19, 22, 43, 50]
+    b9 = list(range(1, 10))
+    got = GemmF64.execute(dev, [1, 0, 0, 0, 1, 0, 0, 0, 1, 2, 0, 0, 0, 2, 0, 0, 0, 2], b9 + b9, 3, 3, 3, 2)
+    assert got.tolist() == b9 + [2 * x for x in b9]
+
+
+@pytest.mark.parametrize("batch,m,k,n", [(1, 128, 128, 128), (1, 256, 512, 384), (1, 100, 33, 77), (1, 1, 1, 1),
+                                         (1, 3, 17, 129), (4, 64, 80, 96), (2, 256, 64, 128)])
+@pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True), (True, True)])
+def test_dgemm_vs_longdouble(dev, batch, m, k, n, ta, tb):
+    _say(f"dgemm batch={batch} m={m} k={k} n={n} ta={ta} tb={tb}")
+    rng = O.Lcg(batch + m * 3 + k * 5 + n * 7 + 2 * ta + tb)
+    a = rng.uniform((batch * m * k,)).astype(np.float64) + rng.uniform((batch * m * k,)).astype(np.float64) * 1e-7
+    b = rng.uniform((batch * k * n,)).astype(np.float64) + rng.uniform((batch * k * n,)).astype(np.float64) * 1e-7
+    got = GemmF64.execute_gemm_ex(dev, a, b, m, k, n, batch, 1.0, 0.0, ta, tb)
+    assert _rel(got, O.gemm_longdouble(a, b, m, k, n, batch, ta, tb)) <= TOL
+    assert _rel(got, O.gemm_f64_wgsl(a, b, m, k, n, batch, trans_a=ta, trans_b=tb)) <= TOL
+
+
+def test_dgemm_exact_on_integers(dev):
+    _say("dgemm integers")
+    rng = np.random.default_rng(4)
+    for (m, k, n) in ((128, 256, 128), (50, 70, 90)):
+        a = rng.integers(-64, 65, m * k).astype(np.float64)
+        b = rng.integers(-64, 65, k * n).astype(np.float64)
+        want = (a.astype(np.int64).reshape(m, k) @ b.astype(np.int64).reshape(k, n)).reshape(-1)
+        assert np.array_equal(GemmF64.execute(dev, a, b, m, k, n, 1), want.astype(np.float64))
+
+
+def test_alpha_beta_reads_c_only_when_beta_nonzero(dev):
+    _say("dgemm alpha/beta")
+    m = k = n = 128
+    rng = O.Lcg(77)
+    a = rng.uniform((m * k,)).astype(np.float64)
+    b = rng.uniform((k * n,)).astype(np.float64)
+    cin = rng.uniform((m * n,)).astype(np.float64)
+    lib = dev._lib
+    for alpha, beta, c0 in ((0.5, -2.0, cin), (3.0, 0.0, np.full(m * n, np.nan))):
+        da, db = F64Buffer(dev, a.size).upload(a), F64Buffer(dev, b.size).upload(b)
+        dc = F64Buffer(dev, m * n).upload(c0)
+        with dev._lock:
+            dev.check(lib.bch_dgemm(dev.ctx, 0, 0, 1, m, n, k, alpha, C.c_void_p(da.ptr), k, m * k,
+                                    C.c_void_p(db.ptr), n, k * n, beta, C.c_void_p(dc.ptr), n, m * n), "dgemm")
+        want = O.gemm_f64_wgsl(a, b, m, k, n, 1, alpha=alpha, beta=beta, c_in=c0)
+        assert _rel(dc.to_vec(), want) <= TOL
+
+
+def test_gemm_cached_non_square(dev):
+    """GemmCachedF64 with m != n: every output element is computed."""
+    _say("GemmCachedF64 m=40 k=64 n=200 batch=2")
+    rng = O.Lcg(5)
+    k, n, batch, m = 64, 200, 2, 40
+    b = rng.uniform((batch * k * n,)).astype(np.float64)
+    g = GemmCachedF64.new(dev, b, k, n, batch)
+    for mm in (m, 7):
+        a = rng.uniform((batch * mm * k,)).astype(np.float64)
+        assert _rel(g.multiply(a, mm), O.gemm_longdouble(a, b, mm, k, n, batch)) <= TOL
+
+
+def test_dgemm_2048_sampled_rows(dev):
+    """A full-tile size with every CU busy; rows sampled against longdouble."""
+    _say("dgemm 2048^3 sampled rows")
+    n = 2048
+    rng = O.Lcg(2)
+    a = rng.uniform((n * n,)).astype(np.float64)
+    b = rng.uniform((n * n,)).astype(np.float64)
+    got = GemmF64.execute(dev, a, b, n, n, n, 1).reshape(n, n)
+    B = b.astype(np.longdouble).reshape(n, n)
+    for r in (0, 1, 777, 2047):
+        ref = (a[r * n:(r + 1) * n].astype(np.longdouble) @ B).astype(np.float64)
+        assert _rel(got[r], ref) <= TOL

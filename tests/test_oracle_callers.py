@@ -213,3 +213,53 @@ def test_fused_mlp_validation_mirrors_reference():
         fused_mlp(x, [w1, _t([5, 7], dev)], [b1, _t([5], dev)])
     with pytest.raises(InvalidInput, match=r"fused_mlp: bias\[0\] shape mismatch"):
         fused_mlp(x, [w1], [_t([8], dev)])
+
+
+# ------------------------------------------------------------------ f64 GEMM
+def _gemm_cases():
+    # ops/linalg/gemm_f64.rs tests: 2x2 basic, transpose A, transpose B, batched identities
+    yield dict(a=[1, 2, 3, 4], b=[5, 6, 7, 8], mkn=(2, 2, 2), batch=1, ta=False, tb=False, want=[19, 22, 43, 50])
+    yield dict(a=[1, 3, 2, 4], b=[5, 6, 7, 8], mkn=(2, 2, 2), batch=1, ta=True, tb=False, want=[19, 22, 43, 50])
+    yield dict(a=[1, 2, 3, 4], b=[5, 7, 6, 8], mkn=(2, 2, 2), batch=1, ta=False, tb=True, want=[19, 22, 43, 50])
+    b9 = list(range(1, 10))
+    yield dict(a=[1, 0, 0, 0, 1, 0, 0, 0, 1, 2, 0, 0, 0, 2, 0, 0, 0, 2], b=b9 + b9, mkn=(3, 3, 3), batch=2,
+               ta=False, tb=False, want=b9 + [2 * x for x in b9])
+
+
+@pytest.mark.parametrize("case", list(_gemm_cases()), ids=["basic", "trans_a", "trans_b", "batched"])
+def test_gemm_f64_oracle_reference_vectors(case):
+    m, k, n = case["mkn"]
+    got = O.gemm_f64_wgsl(case["a"], case["b"], m, k, n, case["batch"], trans_a=case["ta"], trans_b=case["tb"])
+    assert got.tolist() == [float(x) for x in case["want"]]
+
+
+@pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True), (True, True)])
+def test_gemm_f64_oracle_vs_longdouble_and_planted_transpose(ta, tb):
+    rng = np.random.default_rng(13)
+    batch, m, k, n = 2, 7, 19, 5
+    a = rng.uniform(-1, 1, batch * m * k)
+    b = rng.uniform(-1, 1, batch * k * n)
+    got = O.gemm_f64_wgsl(a, b, m, k, n, batch, trans_a=ta, trans_b=tb)
+    ref = O.gemm_longdouble(a, b, m, k, n, batch, ta, tb)
+    assert np.max(np.abs(got - ref.astype(np.float64))) < 1e-14
+    flipped = O.gemm_f64_wgsl(a, b, m, k, n, batch, trans_a=ta, trans_b=not tb)
+    assert np.max(np.abs(flipped - got)) > 1e-3  # reading B with the wrong orientation is caught
+
+
+def test_gemm_f64_oracle_alpha_beta():
+    a, b = [1.0, 2.0, 3.0, 4.0], [5.0, 6.0, 7.0, 8.0]
+    cin = np.array([1.0, -1.0, 0.5, 2.0])
+    got = O.gemm_f64_wgsl(a, b, 2, 2, 2, 1, alpha=2.0, beta=3.0, c_in=cin)
+    assert got.tolist() == [2 * 19 + 3 * 1.0, 2 * 22 - 3.0, 2 * 43 + 1.5, 2 * 50 + 6.0]
+    nan_in = np.full(4, np.nan)
+    assert O.gemm_f64_wgsl(a, b, 2, 2, 2, 1, alpha=1.0, beta=0.0, c_in=nan_in).tolist() == [19, 22, 43, 50]
+
+
+def test_gemm_f64_validation_mirrors_reference():
+    from barracuda_amd import GemmCachedF64, GemmF64
+    with pytest.raises(InvalidInput, match="A: expected 4 elements, got 3"):
+        GemmF64.execute(None, [1, 2, 3], [1, 2, 3, 4], 2, 2, 2, 1)
+    with pytest.raises(InvalidInput, match="B: expected 8 elements, got 4"):
+        GemmF64.execute_gemm_ex(None, [1] * 8, [1] * 4, 2, 2, 2, 2, 1.0, 0.0, True, False)
+    with pytest.raises(InvalidInput, match=r"GemmCachedF64: B has 5 elements, expected batch×K×N=6"):
+        GemmCachedF64(None, [1] * 5, 2, 3, 1)
