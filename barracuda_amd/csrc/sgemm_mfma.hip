@@ -41,7 +41,12 @@
 //     loaded like the A tile (128-bit rows straight into LDS [n][k]).
 //   * Epilogue: C = acc (+ bias[col]) (then max(., 0)), fused into the store
 //     -- linear_f64.wgsl adds the bias after the dot product, and fused_mlp
-//     runs relu_f64.wgsl as a separate pass over the output.
+//     runs relu_f64.wgsl as a separate pass over the output.  EPI is a
+//     template flag so the plain GEMM stores straight from the accumulators
+//     (400 VGPRs, no spill at 256x256); the bias/ReLU variant of that tile
+//     parks 8 accumulators in scratch for the epilogue only (36 bytes per
+//     lane, no AGPR copies in the k-loop; measured at the plain kernel's
+//     rate).
 #include "bch_internal.h"
 
 #include <stdint.h>
@@ -70,7 +75,7 @@ __device__ __forceinline__ float4 ld4(const float* p) {
   return *reinterpret_cast<const float4*>(p);
 }
 
-template <int BM, int BN, int BK, bool CHECK, bool TB>
+template <int BM, int BN, int BK, bool CHECK, bool TB, bool EPI>
 __global__ __launch_bounds__(kThreads) void sgemm_mfma_kernel(
     int M, int N, int K, const float* __restrict__ A, int lda, long long sA,
     const float* __restrict__ B, int ldb, long long sB, float* __restrict__ C,
@@ -265,26 +270,42 @@ __global__ __launch_bounds__(kThreads) void sgemm_mfma_kernel(
   }
 
   // ---- epilogue: value r of lane l is row 8*(r/4) + 4*lh + r%4, col li ----
-#pragma unroll
-  for (int j = 0; j < G::TN; ++j) {
-    const int col = n0 + wn + j * 32 + li;
-    // bias and relu are uniform over the launch: the branches do not diverge
-    const float bj = bias ? (!CHECK || col < N ? bias[col] : 0.0f) : 0.0f;
+  if constexpr (!EPI) {
 #pragma unroll
     for (int i = 0; i < G::TM; ++i) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = m0 + wm + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-        float v = acc[i][j][r];
-        if (bias) v += bj;
-        if (relu) v = fmaxf(v, 0.0f);
-        if (!CHECK || (row < M && col < N)) C[(long long)row * ldc + col] = v;
+      for (int j = 0; j < G::TN; ++j) {
+        const int col = n0 + wn + j * 32 + li;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = m0 + wm + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+          if (!CHECK || (row < M && col < N)) C[(long long)row * ldc + col] = acc[i][j][r];
+        }
+      }
+    }
+  } else {
+    // bias and relu are uniform over the launch (no divergence); one 32 x 32
+    // block at a time, so only 16 accumulators are out of the AGPRs at once
+#pragma unroll
+    for (int j = 0; j < G::TN; ++j) {
+      const int col = n0 + wn + j * 32 + li;
+      const float bj = bias ? (!CHECK || col < N ? bias[col] : 0.0f) : 0.0f;
+#pragma unroll
+      for (int i = 0; i < G::TM; ++i) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = m0 + wm + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+          float v = acc[i][j][r] + bj;
+          if (relu) v = fmaxf(v, 0.0f);
+          if (!CHECK || (row < M && col < N)) C[(long long)row * ldc + col] = v;
+        }
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
   }
 }
 
-template <int BM, int BN, int BK, bool CHECK, bool TB>
+template <int BM, int BN, int BK, bool CHECK, bool TB, bool EPI>
 hipError_t launch_tiles(hipStream_t s, int batch, int m, int n, int k,
                         const float* A, int lda, long long sA, const float* B,
                         int ldb, long long sB, float* C, int ldc, long long sC,
@@ -292,7 +313,7 @@ hipError_t launch_tiles(hipStream_t s, int batch, int m, int n, int k,
   using G = Cfg<BM, BN, BK>;
   const int tm = (m + BM - 1) / BM, tn = (n + BN - 1) / BN;
   const size_t lds = sizeof(float) * G::LDS_FLOATS;
-  auto kern = sgemm_mfma_kernel<BM, BN, BK, CHECK, TB>;
+  auto kern = sgemm_mfma_kernel<BM, BN, BK, CHECK, TB, EPI>;
   static bool attr_set = false;  // per instantiation
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
@@ -334,21 +355,29 @@ bool fast_ok(Tile t, int m, int n, int k, const float* A, int lda, long long sA,
          sA % 4 == 0 && sB % 4 == 0 && aligned16(A) && aligned16(B);
 }
 
-template <bool CHECK, bool TB>
+template <bool CHECK, bool TB, bool EPI>
 hipError_t launch_tile(Tile t, hipStream_t s, int batch, int m, int n, int k, const float* A, int lda,
                        long long sA, const float* B, int ldb, long long sB, float* C, int ldc, long long sC,
                        const float* bias, int relu) {
   switch (t) {
     case Tile::k256x256:
-      return launch_tiles<256, 256, kBK, CHECK, TB>(s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC, bias,
-                                                    relu);
+      return launch_tiles<256, 256, kBK, CHECK, TB, EPI>(s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC,
+                                                         bias, relu);
     case Tile::k256x128:
-      return launch_tiles<256, 128, kBK, CHECK, TB>(s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC, bias,
-                                                    relu);
+      return launch_tiles<256, 128, kBK, CHECK, TB, EPI>(s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC,
+                                                         bias, relu);
     default:
-      return launch_tiles<128, 128, kBK, CHECK, TB>(s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC, bias,
-                                                    relu);
+      return launch_tiles<128, 128, kBK, CHECK, TB, EPI>(s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC,
+                                                         bias, relu);
   }
+}
+
+template <bool TB, bool EPI>
+hipError_t launch_tile_any(bool fast, Tile t, hipStream_t s, int batch, int m, int n, int k, const float* A,
+                           int lda, long long sA, const float* B, int ldb, long long sB, float* C, int ldc,
+                           long long sC, const float* bias, int relu) {
+  return fast ? launch_tile<false, TB, EPI>(t, s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC, bias, relu)
+              : launch_tile<true, TB, EPI>(t, s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC, bias, relu);
 }
 
 const char* tile_name(Tile t, bool check) {
@@ -392,11 +421,14 @@ hipError_t launch_sgemm_ex(hipStream_t s, bool transb, int batch, int m, int n, 
   const Tile t = pick_tile(batch, m, n);
   // the [n][k] tile loads need the same alignment as the [k][n] ones (ldb, sB multiples of 4)
   const bool fast = fast_ok(t, m, n, k, A, lda, sA, B, ldb, sB);
+  const bool epi = bias != nullptr || relu != 0;
   if (transb)
-    return fast ? launch_tile<false, true>(t, s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC, bias, relu)
-                : launch_tile<true, true>(t, s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC, bias, relu);
-  return fast ? launch_tile<false, false>(t, s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC, bias, relu)
-              : launch_tile<true, false>(t, s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC, bias, relu);
+    return epi ? launch_tile_any<true, true>(fast, t, s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC, bias, relu)
+               : launch_tile_any<true, false>(fast, t, s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC, bias,
+                                              relu);
+  return epi ? launch_tile_any<false, true>(fast, t, s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC, bias, relu)
+             : launch_tile_any<false, false>(fast, t, s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC, bias,
+                                             relu);
 }
 
 }  // namespace bch
