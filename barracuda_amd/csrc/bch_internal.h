@@ -61,6 +61,14 @@ hipError_t launch_sgemm_skinny(hipStream_t s, int m, int n, int k,
                                int ldb, float* C, int ldc, void* ws,
                                size_t ws_bytes, const float* bias, int relu);
 size_t sgemm_skinny_workspace_bytes(int m, int n, int k);
+// Skinny (m <= 32) GEMM with W given as [n][k] (C = A W^T), same epilogue.
+hipError_t launch_sgemm_skinny_nt(hipStream_t s, int m, int n, int k,
+                                  const float* A, int lda, const float* W,
+                                  int ldw, float* C, int ldc, void* ws,
+                                  size_t ws_bytes, const float* bias, int relu);
+size_t sgemm_skinny_nt_workspace_bytes(int m, int n, int k);
+bool sgemm_skinny_nt_applies(int m, int n, int k, const float* A, int lda,
+                             const float* W, int ldw);
 const char* sgemm_skinny_kernel_name(int m);
 bool sgemm_skinny_applies(int m, int n, int k, const float* A, int lda,
                           const float* B, int ldb);

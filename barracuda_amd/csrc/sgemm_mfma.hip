@@ -418,6 +418,8 @@ hipError_t launch_sgemm_ex(hipStream_t s, bool transb, int batch, int m, int n, 
   if (batch <= 0 || m <= 0 || n <= 0) return hipSuccess;
   if (!transb && batch == 1 && sgemm_skinny_applies(m, n, k, A, lda, B, ldb))
     return launch_sgemm_skinny(s, m, n, k, A, lda, B, ldb, C, ldc, ws, ws_bytes, bias, relu);
+  if (transb && batch == 1 && sgemm_skinny_nt_applies(m, n, k, A, lda, B, ldb))
+    return launch_sgemm_skinny_nt(s, m, n, k, A, lda, B, ldb, C, ldc, ws, ws_bytes, bias, relu);
   const Tile t = pick_tile(batch, m, n);
   // the [n][k] tile loads need the same alignment as the [k][n] ones (ldb, sB multiples of 4)
   const bool fast = fast_ok(t, m, n, k, A, lda, sA, B, ldb, sB);

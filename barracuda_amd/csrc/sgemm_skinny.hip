@@ -443,16 +443,18 @@ __global__ __launch_bounds__(256, 1) void sgemm_skinny_w32(int M, int N, int K, 
 
 // C[m][n] = sum of the partial blocks of n's column group, in slot order
 // (the k order); loads in batches of 8, all in flight before the adds.
+// cols: columns per group (the partial block width).
 __global__ __launch_bounds__(256) void sgemm_skinny_sk_reduce(int M, int N, const float* __restrict__ P, long long U,
                                                               int G, int kb, int smax, float* __restrict__ C,
-                                                              int ldc, const float* __restrict__ bias, int relu) {
+                                                              int ldc, const float* __restrict__ bias, int relu,
+                                                              int cols) {
   const long long t = (long long)blockIdx.x * 256 + threadIdx.x;
   if (t >= (long long)M * N) return;
-  const int m = (int)(t / N), n = (int)(t - (long long)m * N), g = n / kSkCols;
+  const int m = (int)(t / N), n = (int)(t - (long long)m * N), g = n / cols;
   const int wf = wg_of_unit((long long)g * kb, U, G);
   const int ns = wg_of_unit((long long)g * kb + kb - 1, U, G) - wf + 1;
-  const float* p = P + ((long long)g * smax * M + m) * kSkCols + (n - g * kSkCols);
-  const long long st = (long long)M * kSkCols;
+  const float* p = P + ((long long)g * smax * M + m) * cols + (n - g * cols);
+  const long long st = (long long)M * cols;
   float s = 0.f;
   for (int i = 0; i < ns; i += 8) {
     float v[8];
@@ -463,6 +465,150 @@ __global__ __launch_bounds__(256) void sgemm_skinny_sk_reduce(int M, int N, cons
       if (i + q < ns) s += v[q];
   }
   C[(long long)m * ldc + n] = epilogue(s, bias, n, relu);
+}
+
+// ---------------------------------------------------------------- transposed weights, m <= 32
+// C[m][n] = sum_k A[m][k] W[n][k]: the linear layer with W [out, in]
+// (shaders/misc/linear_f64.wgsl) at decode sizes.  v_mfma_f32_16x16x4_f32
+// computes C^T = W A^T on 16 (n) x 16 (m) blocks, m padded to 16 or 32.
+// A unit is 128 rows of W (output columns) x 64 k; wave w owns rows 32w ..
+// 32w + 31.  Its tile is loaded as 4 rows x 256 contiguous bytes per
+// instruction (whole 128-byte lines) and re-laid through the wave's own LDS
+// rows (padded to 68 floats: conflict-free both ways, no workgroup barrier)
+// into the MFMA operand order: lane l = 16q + i holds row i of a 16-row
+// block at k = 16f + 4q .. +3 and feeds k = 16f + 4q + c in step (f, c).
+// The A operand is the same four float4 of A row 16b + i, through L2 (A is
+// tiny and shared by every workgroup).  Measured at K 4096, N 11008 (M = 1 /
+// 8 / 32): the first layout (16 rows x four separated 16-byte pieces per
+// load) 63 / 68 / 92 us, contiguous 64-byte row pieces 43 / 47 / 76 us, the
+// LDS re-layout 35 / 35 / 58 us.  Stream-K over units ordered row group by
+// row group, one partial block (M x 128) per run segment, reduced by
+// sgemm_skinny_sk_reduce with 128 columns per group.  Requires K % 4 == 0,
+// lda % 4 == 0, ldw % 4 == 0 and 16-byte aligned A, W.
+constexpr int kNtRows = 128;
+constexpr int kNtK = 64;
+constexpr int kNtPF = 1;
+
+template <int MB, bool EDGE>
+__global__ __launch_bounds__(256, 2) void sgemm_skinny_nt(int M, int N, int K, const float* __restrict__ A, int lda,
+                                                          const float* __restrict__ W, int ldw,
+                                                          float* __restrict__ P, long long U, int G, int nkb,
+                                                          int smax) {
+  constexpr int LDW = kNtK + 4;  // padded LDS row (floats)
+  __shared__ float wl[4][32 * LDW];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int q = lane >> 4, i = lane & 15;
+  const int w = blockIdx.x;
+  const long long ub = (long long)w * U / G, ue = (long long)(w + 1) * U / G;
+  const int nu = (int)(ue - ub);
+  const int g0 = (int)(ub / nkb), t0 = (int)(ub - (long long)g0 * nkb);
+  constexpr int PF = kNtPF, NB = kNtPF + 1;
+  float* ws = wl[wave];
+
+  const float* arow[MB];
+#pragma unroll
+  for (int b = 0; b < MB; ++b) arow[b] = A + (long long)min(16 * b + i, M - 1) * lda;
+
+  // W: instruction f loads rows 4 f + q of the wave's 32, k chunk 4 i (4 rows x 256 contiguous bytes)
+  float4 wv[NB][8];
+  float4 av[NB][MB][4];
+  int lg = g0, lt = t0, lcount = 0;
+  auto load = [&](int sb) {
+    const int kw = kNtK * lt + 4 * i;
+#pragma unroll
+    for (int f = 0; f < 8; ++f) {
+      const float* wr = W + (long long)min(kNtRows * lg + 32 * wave + 4 * f + q, N - 1) * ldw;
+      wv[sb][f] = bch::load_nt(reinterpret_cast<const float4*>(wr + min(kw, K - 4)));
+      if (EDGE && kw >= K) wv[sb][f] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    const int k0 = kNtK * lt + 4 * q;
+#pragma unroll
+    for (int b = 0; b < MB; ++b)
+#pragma unroll
+      for (int f = 0; f < 4; ++f) {
+        av[sb][b][f] = *reinterpret_cast<const float4*>(arow[b] + min(k0 + 16 * f, K - 4));
+        if (EDGE && k0 + 16 * f >= K) av[sb][b][f] = make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    ++lcount;
+    lt += lcount < nu ? 1 : 0;
+    const int wrap = lt == nkb ? 1 : 0;
+    lt -= wrap * nkb;
+    lg += wrap;
+  };
+#pragma unroll
+  for (int p = 0; p < PF; ++p) {
+    load(p);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
+  f32x4v acc[2][MB];
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+    for (int b = 0; b < MB; ++b) acc[rb][b] = (f32x4v){0.f, 0.f, 0.f, 0.f};
+  int gcur = g0, tcur = t0;
+  int slot = w - wg_of_unit((long long)g0 * nkb, U, G);
+  auto flush = [&]() {
+    float* pt = P + (long long)(gcur * smax + slot) * M * kNtRows;
+    const int nrem = N - gcur * kNtRows;
+#pragma unroll
+    for (int b = 0; b < MB; ++b) {
+      const int m = 16 * b + i;
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb) {
+        const int c = 32 * wave + 16 * rb + 4 * q;
+        if (m < M && c < nrem)
+          *reinterpret_cast<float4*>(pt + (long long)m * kNtRows + c) =
+              make_float4(acc[rb][b][0], acc[rb][b][1], acc[rb][b][2], acc[rb][b][3]);
+        acc[rb][b] = (f32x4v){0.f, 0.f, 0.f, 0.f};
+      }
+    }
+  };
+  auto mma = [&](int sb) {
+    // re-layout the wave's 32 x 64 tile through its own LDS rows
+#pragma unroll
+    for (int f = 0; f < 8; ++f) *reinterpret_cast<float4*>(ws + (4 * f + q) * LDW + 4 * i) = wv[sb][f];
+    __builtin_amdgcn_wave_barrier();
+    float4 wt[2][4];
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+      for (int f = 0; f < 4; ++f) wt[rb][f] = *reinterpret_cast<const float4*>(ws + (16 * rb + i) * LDW + 16 * f + 4 * q);
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int f = 0; f < 4; ++f) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+#pragma unroll
+        for (int b = 0; b < MB; ++b) {
+          const float4 a4 = av[sb][b][f];
+          const float x = c == 0 ? a4.x : c == 1 ? a4.y : c == 2 ? a4.z : a4.w;
+#pragma unroll
+          for (int rb = 0; rb < 2; ++rb) {
+            const float4 w4 = wt[rb][f];
+            const float y = c == 0 ? w4.x : c == 1 ? w4.y : c == 2 ? w4.z : w4.w;
+            acc[rb][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(y, x, acc[rb][b], 0, 0, 0);
+          }
+        }
+      }
+    }
+  };
+  for (int it = 0; it < nu; it += NB) {
+#pragma unroll
+    for (int p = 0; p < NB; ++p) {
+      load((p + PF) % NB);
+      if (it + p < nu) {
+        mma(p);
+        if (++tcur == nkb && it + p + 1 < nu) {
+          flush();
+          tcur = 0;
+          ++gcur;
+          slot = 0;
+        }
+      }
+    }
+  }
+  flush();
 }
 
 bool use_fma(int m) { return m <= 4; }
@@ -550,6 +696,27 @@ W32Plan w32_plan(int n, int k) {
   return p;
 }
 
+// transposed-weight path: 128-row x 64-k units, two workgroups per CU
+struct NtPlan {
+  long long U = 0;
+  int ng = 0, nkb = 0, G = 0, smax = 0;
+};
+
+NtPlan nt_plan(int n, int k) {
+  NtPlan p;
+  p.ng = (n + kNtRows - 1) / kNtRows;
+  p.nkb = (k + kNtK - 1) / kNtK;
+  p.U = (long long)p.ng * p.nkb;
+  long long g = 2LL * cu_count();
+  if (g > p.U) g = p.U;
+  p.G = (int)g;
+  for (int c = 0; c < p.ng; ++c) {
+    const int ns = wg_of_unit((long long)c * p.nkb + p.nkb - 1, p.U, p.G) - wg_of_unit((long long)c * p.nkb, p.U, p.G) + 1;
+    if (ns > p.smax) p.smax = ns;
+  }
+  return p;
+}
+
 template <bool EDGE>
 hipError_t launch_w32(hipStream_t s, const W32Plan& p, int m, int n, int k, const float* A, int lda, const float* B,
                       int ldb, float* P) {
@@ -583,6 +750,49 @@ hipError_t launch_sk(hipStream_t s, const SkPlan& p, int m, int n, int k, const 
 }  // namespace
 
 namespace bch {
+
+bool sgemm_skinny_nt_applies(int m, int n, int k, const float* A, int lda, const float* W, int ldw) {
+  if (m < 1 || m > 32 || n < 1 || k < 4 || k % 4 != 0 || lda % 4 != 0 || ldw % 4 != 0) return false;
+  if (A && (reinterpret_cast<uintptr_t>(A) & 15) != 0) return false;
+  if (W && (reinterpret_cast<uintptr_t>(W) & 15) != 0) return false;
+  return true;
+}
+
+size_t sgemm_skinny_nt_workspace_bytes(int m, int n, int k) {
+  const NtPlan p = nt_plan(n, k);
+  return sizeof(float) * (size_t)p.ng * (size_t)p.smax * (size_t)m * kNtRows;
+}
+
+hipError_t launch_sgemm_skinny_nt(hipStream_t s, int m, int n, int k, const float* A, int lda, const float* W,
+                                  int ldw, float* C, int ldc, void* ws, size_t ws_bytes, const float* bias,
+                                  int relu) {
+  if (ws == nullptr || ws_bytes < sgemm_skinny_nt_workspace_bytes(m, n, k)) return hipErrorInvalidValue;
+  float* P = static_cast<float*>(ws);
+  const NtPlan p = nt_plan(n, k);
+  const bool edge = k % kNtK != 0;
+  const dim3 grid(p.G), block(256);
+  if (m <= 16) {
+    if (edge)
+      hipLaunchKernelGGL((sgemm_skinny_nt<1, true>), grid, block, 0, s, m, n, k, A, lda, W, ldw, P, p.U, p.G, p.nkb,
+                         p.smax);
+    else
+      hipLaunchKernelGGL((sgemm_skinny_nt<1, false>), grid, block, 0, s, m, n, k, A, lda, W, ldw, P, p.U, p.G, p.nkb,
+                         p.smax);
+  } else {
+    if (edge)
+      hipLaunchKernelGGL((sgemm_skinny_nt<2, true>), grid, block, 0, s, m, n, k, A, lda, W, ldw, P, p.U, p.G, p.nkb,
+                         p.smax);
+    else
+      hipLaunchKernelGGL((sgemm_skinny_nt<2, false>), grid, block, 0, s, m, n, k, A, lda, W, ldw, P, p.U, p.G, p.nkb,
+                         p.smax);
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const long long total = (long long)m * n;
+  hipLaunchKernelGGL(sgemm_skinny_sk_reduce, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, m, n, P, p.U, p.G,
+                     p.nkb, p.smax, C, ldc, bias, relu, kNtRows);
+  return hipGetLastError();
+}
 
 size_t sgemm_skinny_workspace_bytes(int m, int n, int k) {
   if (use_fma(m)) {
@@ -644,7 +854,7 @@ hipError_t launch_sgemm_skinny(hipStream_t s, int m, int n, int k, const float* 
                                      : launch_w32<true>(s, q, m, n, k, A, lda, B, ldb, P);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(sgemm_skinny_sk_reduce, rgrid, dim3(256), 0, s, m, n, P, q.U, q.G, q.nblk, q.smax, C, ldc,
-                       bias, relu);
+                       bias, relu, kSkCols);
     return hipGetLastError();
   }
   const SkPlan p = sk_plan(m, n, k);
@@ -656,7 +866,7 @@ hipError_t launch_sgemm_skinny(hipStream_t s, int m, int n, int k, const float* 
     e = dma ? launch_sk<2, true>(s, p, m, n, k, A, lda, B, ldb, P) : launch_sk<2, false>(s, p, m, n, k, A, lda, B, ldb, P);
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(sgemm_skinny_sk_reduce, rgrid, dim3(256), 0, s, m, n, P, p.U, p.G, p.kb, p.smax, C, ldc, bias,
-                     relu);
+                     relu, kSkCols);
   return hipGetLastError();
 }
 

@@ -170,8 +170,23 @@ def _bench_linear(dev, T, reps):
     px, pw, pb, py = (C.c_void_p(t.ptr) for t in (x, w, b, y))
     wall, ev = T.run(lambda i: lib.bch_sgemm_ex(ctx, 1, n, n, n, px, n, pw, n, pb, N.BCH_ACT_RELU, py, n), reps, 3)
     fl = 2.0 * n ** 3
-    return {"linear_4096_wT_bias_relu": {"TFLOP/s": fl / (ev * 1e-3) / 1e12, "ms": ev,
-                                         "mfma_frac": fl / (ev * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS}}
+    out = {"linear_4096_wT_bias_relu": {"TFLOP/s": fl / (ev * 1e-3) / 1e12, "ms": ev,
+                                        "mfma_frac": fl / (ev * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS}}
+    del x, w, b, y
+    # decode-sized layers with [out, in] weights (the skinny config's shape, W^T): HBM-bound
+    K, Nn = 4096, 11008
+    ws = [s.normal([Nn, K], 0.0, 0.02) for _ in range(3)]
+    bias = s.normal([Nn])
+    pws, pbias = [C.c_void_p(t.ptr) for t in ws], C.c_void_p(bias.ptr)
+    for m in (1, 8, 32):
+        xs, ys = s.normal([m, K]), Tensor.empty([m, Nn], dev)
+        pxs, pys = C.c_void_p(xs.ptr), C.c_void_p(ys.ptr)
+        wall, ev = T.run(lambda i: lib.bch_sgemm_ex(ctx, 1, m, Nn, K, pxs, K, pws[i % 3], K, pbias, N.BCH_ACT_RELU,
+                                                    pys, Nn), reps, 3)
+        nbytes = 4 * (K * Nn + m * K + m * Nn + Nn)
+        out[f"linear_decode_wT_m{m}"] = {"GB/s": nbytes / (ev * 1e-3) / 1e9, "us": ev * 1e3,
+                                         "hbm_frac": nbytes / (ev * 1e-3) / 1e9 / HBM_PEAK_GBS}
+    return out
 
 
 def _bench_softmax(dev, T, reps):

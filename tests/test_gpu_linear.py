@@ -63,6 +63,35 @@ def test_sgemm_ex_vs_f64(dev, m, n, k, transb):
         assert O.max_rel_err(got, _ref(x, w, b, transb, act == N.BCH_ACT_RELU)) <= TOL, (act, b is None)
 
 
+@pytest.mark.parametrize("m,n,k", [(1, 11008, 4096), (8, 4096, 4096), (32, 1024, 4096), (5, 300, 100), (17, 77, 36),
+                                   (16, 129, 68), (32, 4, 4), (2, 200, 1028)])
+def test_sgemm_ex_transposed_decode_shapes(dev, m, n, k):
+    """m <= 32 with [n][k] weights: the weight-row-streaming kernel, bias + ReLU in its reduce."""
+    _say(f"sgemm_ex transposed decode m={m} n={n} k={k}")
+    rng = O.Lcg(m * 11 + n + k)
+    x = rng.normal((m, k))
+    w = rng.normal((n, k), 0.0, 0.05)
+    bias = rng.normal((n,))
+    for act, b in ((N.BCH_ACT_RELU, bias), (N.BCH_ACT_NONE, None)):
+        got = _sgemm_ex(dev, 1, x, w, b, act)
+        assert O.max_rel_err(got, _ref(x, w, b, True, act == N.BCH_ACT_RELU)) <= TOL, act
+
+
+def test_sgemm_ex_transposed_unaligned_falls_back(dev):
+    """lda not a multiple of 4: the tiled kernel's guarded path."""
+    _say("sgemm_ex transposed unaligned lda")
+    m, n, k = 8, 256, 130
+    rng = O.Lcg(99)
+    xp = rng.normal((m, k + 1))  # rows of k + 1 floats: lda = 131
+    w = rng.normal((n, k), 0.0, 0.05)
+    tx, tw = _up(dev, xp), _up(dev, w)
+    ty = Tensor.empty([m, n], dev)
+    with dev._lock:
+        dev.check(dev._lib.bch_sgemm_ex(dev.ctx, 1, m, n, k, C.c_void_p(tx.ptr), k + 1, C.c_void_p(tw.ptr), k, None,
+                                        0, C.c_void_p(ty.ptr), n), "sgemm_ex")
+    assert O.max_rel_err(ty.to_numpy(), _ref(np.ascontiguousarray(xp[:, :k]), w, None, True, False)) <= TOL
+
+
 @pytest.mark.parametrize("transb", [0, 1])
 def test_sgemm_ex_exact_on_integers(dev, transb):
     _say(f"sgemm_ex integers transb={transb}")
