@@ -88,6 +88,11 @@ hipError_t launch_fill_normal(hipStream_t s, float* out, uint64_t n, uint64_t st
                               double sigma);
 uint64_t lcg_advance(uint64_t state, uint64_t inc, uint64_t n);
 
+// Raise `func`'s dynamic LDS limit to `bytes` on the current device, once per
+// (function, device); thread-safe.  Kernels asking for more than 64 KB of
+// dynamic LDS need it before their first launch on each device.
+hipError_t ensure_dynamic_lds(const void* func, int bytes);
+
 // Device-to-device copy (16-byte path when aligned).
 hipError_t launch_copy(hipStream_t s, void* dst, const void* src, size_t bytes);
 

@@ -17,6 +17,8 @@
 
 #include <map>
 #include <mutex>
+#include <set>
+#include <tuple>
 #include <string>
 
 #include "../../include/barracuda_hip.h"
@@ -564,3 +566,21 @@ void bch_event_destroy(bch_event* ev) {
 const char* bch_sgemm_kernel_name(int m, int n, int k) { return bch::sgemm_kernel_name(m, n, k); }
 
 }  // extern "C"
+
+namespace bch {
+
+hipError_t ensure_dynamic_lds(const void* func, int bytes) {
+  static std::mutex mu;
+  static std::set<std::tuple<const void*, int, int>> done;  // (function, device, bytes)
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  std::lock_guard<std::mutex> g(mu);
+  const auto key = std::make_tuple(func, dev, bytes);
+  if (done.count(key)) return hipSuccess;
+  e = hipFuncSetAttribute(func, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  if (e == hipSuccess) done.insert(key);
+  return e;
+}
+
+}  // namespace bch

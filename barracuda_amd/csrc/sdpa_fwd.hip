@@ -288,13 +288,8 @@ hipError_t launch_dp(hipStream_t s, int B, int H, int Hkv, int Sq, int Skv, int 
   if (blocks > 0x7fffffffLL) return hipErrorInvalidValue;
   const size_t lds = sizeof(float) * SdpaCfg<DP>::LDS_FLOATS;
   auto kern = sdpa_fwd_kernel<DP, FULL>;
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return e;
-    attr_set = true;
-  }
+  hipError_t e = bch::ensure_dynamic_lds(reinterpret_cast<const void*>(kern), (int)lds);
+  if (e != hipSuccess) return e;
   hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), lds, s, H, H / Hkv, B * H, Sq, Skv, D,
                      scale * kLog2E, causal, q, k, v, o, st, qblocks);
   return hipGetLastError();

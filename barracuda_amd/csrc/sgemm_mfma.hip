@@ -314,13 +314,8 @@ hipError_t launch_tiles(hipStream_t s, int batch, int m, int n, int k,
   const int tm = (m + BM - 1) / BM, tn = (n + BN - 1) / BN;
   const size_t lds = sizeof(float) * G::LDS_FLOATS;
   auto kern = sgemm_mfma_kernel<BM, BN, BK, CHECK, TB, EPI>;
-  static bool attr_set = false;  // per instantiation
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return e;
-    attr_set = true;
-  }
+  hipError_t e = bch::ensure_dynamic_lds(reinterpret_cast<const void*>(kern), (int)lds);
+  if (e != hipSuccess) return e;
   if (batch > 65535) return hipErrorInvalidValue;
   hipLaunchKernelGGL(kern, dim3(tm * tn, batch), dim3(kThreads), lds, s, m, n, k,
                      A, lda, sA, B, ldb, sB, C, ldc, sC, tm, tn, bias, relu);

@@ -43,6 +43,8 @@
 
 #include <stdint.h>
 
+#include <atomic>
+
 namespace {
 
 typedef float f32x4v __attribute__((ext_vector_type(4)));
@@ -625,15 +627,15 @@ bool use_w32(int m, int k, const float* A, int lda) {
 // Compute units of the current device (the stream-K grids take one
 // workgroup per CU); cached per device.
 int cu_count() {
-  static int cached[64] = {0};
+  static std::atomic<int> cached[64];  // zero-initialised (static storage)
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
-  if (cached[dev] <= 0) {
-    int n = 0;
+  int n = cached[dev].load(std::memory_order_relaxed);
+  if (n <= 0) {
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = kSkWGs;
-    cached[dev] = n;
+    cached[dev].store(n, std::memory_order_relaxed);
   }
-  return cached[dev];
+  return n;
 }
 
 // FMA path: k rows per split and split count.
@@ -720,13 +722,8 @@ NtPlan nt_plan(int n, int k) {
 template <bool EDGE>
 hipError_t launch_w32(hipStream_t s, const W32Plan& p, int m, int n, int k, const float* A, int lda, const float* B,
                       int ldb, float* P) {
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(sgemm_skinny_w32<kW32PF, EDGE>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, kW32Lds);
-    if (e != hipSuccess) return e;
-    attr_set = true;
-  }
+  hipError_t e = bch::ensure_dynamic_lds(reinterpret_cast<const void*>(sgemm_skinny_w32<kW32PF, EDGE>), kW32Lds);
+  if (e != hipSuccess) return e;
   hipLaunchKernelGGL((sgemm_skinny_w32<kW32PF, EDGE>), dim3(p.G), dim3(256), kW32Lds, s, m, n, k, A, lda, B, ldb, P,
                      p.U, p.G, p.nblk, p.smax);
   return hipGetLastError();
@@ -735,13 +732,8 @@ hipError_t launch_w32(hipStream_t s, const W32Plan& p, int m, int n, int k, cons
 template <int MB, bool DMA>
 hipError_t launch_sk(hipStream_t s, const SkPlan& p, int m, int n, int k, const float* A, int lda, const float* B,
                      int ldb, float* P) {
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(sgemm_skinny_sk<MB, DMA>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
-    if (e != hipSuccess) return e;
-    attr_set = true;
-  }
+  hipError_t e = bch::ensure_dynamic_lds(reinterpret_cast<const void*>(sgemm_skinny_sk<MB, DMA>), kLdsBytes);
+  if (e != hipSuccess) return e;
   hipLaunchKernelGGL((sgemm_skinny_sk<MB, DMA>), dim3(p.G), dim3(256), p.lds, s, m, n, k, A, lda, B, ldb, P, p.U,
                      p.G, p.kb, p.smax);
   return hipGetLastError();

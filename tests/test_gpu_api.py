@@ -96,3 +96,41 @@ def test_device_copy(dev):
     assert np.array_equal(got2[1:99991], x[2:99992])
     assert got2.view(np.uint8)[4 + 4 * 99990: 4 + 4 * 99990 + 3].tolist() == \
         x.view(np.uint8)[8 + 4 * 99990: 8 + 4 * 99990 + 3].tolist()
+
+
+def test_two_contexts_from_two_threads():
+    """Two contexts on the device, driven from two threads at once: the
+    per-device launch set-up (dynamic-LDS limits) is shared and locked, and
+    each context's results stay its own."""
+    import threading
+    from barracuda_amd import HipDevice
+    from oracle import bc_oracle as O
+    print("two contexts, two threads", flush=True)
+    rng = O.Lcg(31)
+    a, b = rng.uniform((512, 512)), rng.uniform((512, 512))
+    x, w = rng.normal((8, 1024)), rng.normal((1024, 2048), 0.0, 0.02)
+    q = rng.normal((1, 4, 256, 128))
+    want_mm, want_sk = O.matmul_f64(a, b), O.matmul_f64(x, w)
+    want_at = O.sdpa_f64(q, q, q, True)
+    errs = []
+
+    def work(seed):
+        try:
+            d = HipDevice(0)
+            for _ in range(3):
+                c = Tensor.from_data(a, [512, 512], d).matmul(Tensor.from_data(b, [512, 512], d)).to_numpy()
+                y = Tensor.from_data(x, [8, 1024], d).matmul(Tensor.from_data(w, [1024, 2048], d)).to_numpy()
+                tq = Tensor.from_data(q, list(q.shape), d)
+                o = tq.causal_attention(tq, tq).to_numpy()
+                errs.append(max(O.max_rel_err(c, want_mm), O.max_rel_err(y, want_sk), O.max_rel_err(o, want_at)))
+            d.close()
+        except Exception as e:  # reported below
+            errs.append(e)
+
+    ts = [threading.Thread(target=work, args=(s,)) for s in (1, 2)]
+    for t in ts:
+        t.start()
+    for t in ts:
+        t.join(timeout=120)
+    assert len(errs) == 6, errs
+    assert all(isinstance(e, float) and e <= 1e-4 for e in errs), errs
