@@ -40,7 +40,7 @@ namespace {
 typedef double f64x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kDT = 256;  // threads
-constexpr int kDBM = 128, kDBN = 128, kDBK = 16;
+constexpr int kDBK = 16;
 constexpr int kDLDK = kDBK + 2;  // padded LDS row, doubles
 
 struct d2 {
@@ -49,17 +49,17 @@ struct d2 {
 
 __device__ __forceinline__ d2 ld2(const double* p) { return *reinterpret_cast<const d2*>(p); }
 
-// Global -> registers for one 128-row x 16-k operand tile of op(X).
+// Global -> registers for one ROWS-row x 16-k operand tile of op(X).
 // KCONT: row r, element k of op(X) is X[r * ld + k] (rows k-contiguous);
 // otherwise it is X[k * ld + r] (the stored matrix is [k][rows]).
-// Registers: 4 pairs of doubles per thread either way.
-template <bool KCONT, bool CHECK>
+// Registers: ROWS / 32 pairs of doubles per thread either way.
+template <int ROWS, bool KCONT, bool CHECK>
 __device__ __forceinline__ void load_dtile(const double* __restrict__ X, int ld, int rows, int K, int r0, int k0,
-                                           int tid, d2 (&reg)[4]) {
+                                           int tid, d2 (&reg)[ROWS / 32]) {
   if (KCONT) {
     // pair f: row tid / 8 + 32 f, k 2 * (tid % 8)
 #pragma unroll
-    for (int f = 0; f < 4; ++f) {
+    for (int f = 0; f < ROWS / 32; ++f) {
       const int r = r0 + tid / 8 + 32 * f, k = k0 + 2 * (tid % 8);
       if (!CHECK) {
         reg[f] = ld2(X + (long long)r * ld + k);
@@ -69,10 +69,10 @@ __device__ __forceinline__ void load_dtile(const double* __restrict__ X, int ld,
       }
     }
   } else {
-    // 2 x 2 block q (q = 0, 1): blk = tid + 256 q, kq = blk % 8, rq = blk / 8;
+    // 2 x 2 block q (q < ROWS / 64): blk = tid + 256 q, kq = blk % 8, rq = blk / 8;
     // reg[2q + e] = X[k0 + 2 kq + e][r0 + 2 rq .. +1]
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
+    for (int q = 0; q < ROWS / 64; ++q) {
       const int blk = tid + kDT * q, kq = blk % 8, rq = blk / 8;
 #pragma unroll
       for (int e = 0; e < 2; ++e) {
@@ -88,18 +88,18 @@ __device__ __forceinline__ void load_dtile(const double* __restrict__ X, int ld,
   }
 }
 
-// registers -> LDS tile [128][kDLDK] (k-contiguous)
-template <bool KCONT>
-__device__ __forceinline__ void store_dtile(double* __restrict__ s, int tid, const d2 (&reg)[4]) {
+// registers -> LDS tile [ROWS][kDLDK] (k-contiguous)
+template <int ROWS, bool KCONT>
+__device__ __forceinline__ void store_dtile(double* __restrict__ s, int tid, const d2 (&reg)[ROWS / 32]) {
   if (KCONT) {
 #pragma unroll
-    for (int f = 0; f < 4; ++f) {
+    for (int f = 0; f < ROWS / 32; ++f) {
       const int r = tid / 8 + 32 * f, k = 2 * (tid % 8);
       *reinterpret_cast<d2*>(s + r * kDLDK + k) = reg[f];
     }
   } else {
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
+    for (int q = 0; q < ROWS / 64; ++q) {
       const int blk = tid + kDT * q, kq = blk % 8, rq = blk / 8;
       // reg[2q + e] holds (k = 2kq + e; rows 2rq, 2rq + 1): row 2rq + c gets (k, k + 1)
       *reinterpret_cast<d2*>(s + (2 * rq) * kDLDK + 2 * kq) = d2{reg[2 * q].x, reg[2 * q + 1].x};
@@ -108,11 +108,14 @@ __device__ __forceinline__ void store_dtile(double* __restrict__ s, int tid, con
   }
 }
 
-template <bool TA, bool TB, bool CHECK>
-__global__ __launch_bounds__(kDT, 2) void dgemm_mfma_kernel(
+// BM x BN block tile (2 x 2 waves of (BM/2) x (BN/2), TM x TN MFMA blocks each);
+// OCC workgroups per CU.
+template <int BM, int BN, int OCC, bool TA, bool TB, bool CHECK>
+__global__ __launch_bounds__(kDT, OCC) void dgemm_mfma_kernel(
     int M, int N, int K, double alpha, const double* __restrict__ A, int lda, long long sA,
     const double* __restrict__ B, int ldb, long long sB, double beta, double* __restrict__ C, int ldc,
     long long sC, int tiles_m, int tiles_n) {
+  constexpr int kDBM = BM, kDBN = BN, TM = BM / 32, TN = BN / 32;
   __shared__ double As[2][kDBM * kDLDK];
   __shared__ double Bs[2][kDBN * kDLDK];
 
@@ -136,40 +139,40 @@ __global__ __launch_bounds__(kDT, 2) void dgemm_mfma_kernel(
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int li = lane & 15, lq = lane >> 4;
-  const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+  const int wm = (wave >> 1) * (BM / 2), wn = (wave & 1) * (BN / 2);
 
-  d2 ra[4], rb[4];
-  f64x4 acc[4][4];
+  d2 ra[BM / 32], rb[BN / 32];
+  f64x4 acc[TM][TN];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = (f64x4){0.0, 0.0, 0.0, 0.0};
+    for (int j = 0; j < TN; ++j) acc[i][j] = (f64x4){0.0, 0.0, 0.0, 0.0};
 
   const int nk = (K + kDBK - 1) / kDBK;
   if (nk > 0) {
-    load_dtile<!TA, CHECK>(A, lda, M, K, m0, 0, tid, ra);
-    load_dtile<TB, CHECK>(B, ldb, N, K, n0, 0, tid, rb);
-    store_dtile<!TA>(As[0], tid, ra);
-    store_dtile<TB>(Bs[0], tid, rb);
+    load_dtile<BM, !TA, CHECK>(A, lda, M, K, m0, 0, tid, ra);
+    load_dtile<BN, TB, CHECK>(B, ldb, N, K, n0, 0, tid, rb);
+    store_dtile<BM, !TA>(As[0], tid, ra);
+    store_dtile<BN, TB>(Bs[0], tid, rb);
   }
   __syncthreads();
 
   for (int t = 0; t < nk; ++t) {
     const int cur = t & 1;
     if (t + 1 < nk) {
-      load_dtile<!TA, CHECK>(A, lda, M, K, m0, (t + 1) * kDBK, tid, ra);
-      load_dtile<TB, CHECK>(B, ldb, N, K, n0, (t + 1) * kDBK, tid, rb);
+      load_dtile<BM, !TA, CHECK>(A, lda, M, K, m0, (t + 1) * kDBK, tid, ra);
+      load_dtile<BN, TB, CHECK>(B, ldb, N, K, n0, (t + 1) * kDBK, tid, rb);
     }
     const double* as = As[cur] + (wm + li) * kDLDK + 4 * lq;
     const double* bs = Bs[cur] + (wn + li) * kDLDK + 4 * lq;
-    d2 a[4][2], b[4][2];
+    d2 a[TM][2], b[TN][2];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < TM; ++i) {
       a[i][0] = *reinterpret_cast<const d2*>(as + i * 16 * kDLDK);
       a[i][1] = *reinterpret_cast<const d2*>(as + i * 16 * kDLDK + 2);
     }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < TN; ++j) {
       b[j][0] = *reinterpret_cast<const d2*>(bs + j * 16 * kDLDK);
       b[j][1] = *reinterpret_cast<const d2*>(bs + j * 16 * kDLDK + 2);
     }
@@ -177,27 +180,27 @@ __global__ __launch_bounds__(kDT, 2) void dgemm_mfma_kernel(
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < TM; ++i) {
         const double av = (s & 1) ? a[i][s >> 1].y : a[i][s >> 1].x;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < TN; ++j) {
           const double bv = (s & 1) ? b[j][s >> 1].y : b[j][s >> 1].x;
           acc[i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64(av, bv, acc[i][j], 0, 0, 0);
         }
       }
     }
     if (t + 1 < nk) {
-      store_dtile<!TA>(As[cur ^ 1], tid, ra);
-      store_dtile<TB>(Bs[cur ^ 1], tid, rb);
+      store_dtile<BM, !TA>(As[cur ^ 1], tid, ra);
+      store_dtile<BN, TB>(Bs[cur ^ 1], tid, rb);
     }
     __syncthreads();
   }
 
   // ---- epilogue: value r of lane (lq, li) is row lq + 4 r, col li of the block ----
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < TM; ++i) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < TN; ++j) {
       const int col = n0 + wn + 16 * j + li;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
@@ -212,26 +215,35 @@ __global__ __launch_bounds__(kDT, 2) void dgemm_mfma_kernel(
   }
 }
 
-template <bool TA, bool TB, bool CHECK>
+template <int BM, int BN, int OCC, bool TA, bool TB, bool CHECK>
 hipError_t launch_d(hipStream_t s, int batch, int m, int n, int k, double alpha, const double* A, int lda,
                     long long sA, const double* B, int ldb, long long sB, double beta, double* C, int ldc,
                     long long sC) {
-  const int tm = (m + kDBM - 1) / kDBM, tn = (n + kDBN - 1) / kDBN;
+  const int tm = (m + BM - 1) / BM, tn = (n + BN - 1) / BN;
   if ((long long)tm * tn > 0x7fffffffLL || batch > 65535) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((dgemm_mfma_kernel<TA, TB, CHECK>), dim3(tm * tn, batch), dim3(kDT), 0, s, m, n, k, alpha, A,
-                     lda, sA, B, ldb, sB, beta, C, ldc, sC, tm, tn);
+  hipLaunchKernelGGL((dgemm_mfma_kernel<BM, BN, OCC, TA, TB, CHECK>), dim3(tm * tn, batch), dim3(kDT), 0, s, m, n, k,
+                     alpha, A, lda, sA, B, ldb, sB, beta, C, ldc, sC, tm, tn);
   return hipGetLastError();
 }
+
+#ifndef BCH_DGEMM_TILE_M  // tile choice (a build-time knob for tuning sweeps)
+#define BCH_DGEMM_TILE_M 128
+#define BCH_DGEMM_TILE_N 128
+#define BCH_DGEMM_OCC 2
+#endif
+constexpr int kDTileM = BCH_DGEMM_TILE_M, kDTileN = BCH_DGEMM_TILE_N, kDOcc = BCH_DGEMM_OCC;
 
 template <bool TA, bool TB>
 hipError_t launch_ab(hipStream_t s, int batch, int m, int n, int k, double alpha, const double* A, int lda,
                      long long sA, const double* B, int ldb, long long sB, double beta, double* C, int ldc,
                      long long sC) {
-  const bool fast = m % kDBM == 0 && n % kDBN == 0 && k % kDBK == 0 && lda % 2 == 0 && ldb % 2 == 0 &&
+  constexpr int BM = kDTileM, BN = kDTileN, OCC = kDOcc;
+  const bool fast = m % BM == 0 && n % BN == 0 && k % kDBK == 0 && lda % 2 == 0 && ldb % 2 == 0 &&
                     sA % 2 == 0 && sB % 2 == 0 && (reinterpret_cast<uintptr_t>(A) & 15) == 0 &&
                     (reinterpret_cast<uintptr_t>(B) & 15) == 0;
-  if (fast) return launch_d<TA, TB, false>(s, batch, m, n, k, alpha, A, lda, sA, B, ldb, sB, beta, C, ldc, sC);
-  return launch_d<TA, TB, true>(s, batch, m, n, k, alpha, A, lda, sA, B, ldb, sB, beta, C, ldc, sC);
+  if (fast)
+    return launch_d<BM, BN, OCC, TA, TB, false>(s, batch, m, n, k, alpha, A, lda, sA, B, ldb, sB, beta, C, ldc, sC);
+  return launch_d<BM, BN, OCC, TA, TB, true>(s, batch, m, n, k, alpha, A, lda, sA, B, ldb, sB, beta, C, ldc, sC);
 }
 
 }  // namespace
