@@ -51,29 +51,30 @@ namespace {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int kBQ = 128;  // queries per workgroup
 constexpr int kBKV = 32;  // keys per block
 constexpr int kVLD = kBKV + 4;
 constexpr float kLog2E = 1.44269504088896340736f;
 constexpr float kLazy = 8.0f;  // log2 headroom before the reference max moves
 
-template <int DP>
+// NT threads per workgroup: NT / 64 wavefronts of 32 queries each.
+template <int DP, int NT>
 struct SdpaCfg {
+  static constexpr int BQ = NT / 2;                    // queries per workgroup
   static constexpr int KLD = DP + 4;
   static constexpr int KD4 = DP / 4;                   // float4 per K row
-  static constexpr int K_F4 = kBKV * DP / 4 / 256;     // float4 of K per thread
+  static constexpr int K_F4 = kBKV * DP / 4 / NT;      // float4 of K per thread
   static constexpr int V_BLK = kBKV * DP / 16;          // 4x4 V blocks per tile
   static constexpr int LDS_FLOATS = 2 * (kBKV * KLD + DP * kVLD);
   static_assert(K_F4 >= 1, "K tile must cover the workgroup");
 };
 
-template <int DP, bool FULL>
+template <int DP, int NT, bool FULL>
 __device__ __forceinline__ void load_k(const float* __restrict__ kh, long long ldk, int Skv, int D, int kb, int tid,
-                                       float4 (&rk)[SdpaCfg<DP>::K_F4]) {
-  using G = SdpaCfg<DP>;
+                                       float4 (&rk)[SdpaCfg<DP, NT>::K_F4]) {
+  using G = SdpaCfg<DP, NT>;
 #pragma unroll
   for (int f = 0; f < G::K_F4; ++f) {
-    const int idx = tid + f * 256;
+    const int idx = tid + f * NT;
     const int key = idx / G::KD4, d0 = (idx % G::KD4) * 4;
     const int gk = kb + key;
     if (FULL) {
@@ -87,10 +88,10 @@ __device__ __forceinline__ void load_k(const float* __restrict__ kh, long long l
   }
 }
 
-template <int DP, bool FULL>
+template <int DP, int NT, bool FULL>
 __device__ __forceinline__ void load_v(const float* __restrict__ vh, long long ldv, int Skv, int D, int kb, int tid,
                                        float4 (&rv)[4]) {
-  using G = SdpaCfg<DP>;
+  using G = SdpaCfg<DP, NT>;
   const int blk = tid < G::V_BLK ? tid : 0;  // threads past the tile reload block 0 (unused)
   const int kq = blk / G::KD4, dq = blk % G::KD4;
 #pragma unroll
@@ -107,13 +108,13 @@ __device__ __forceinline__ void load_v(const float* __restrict__ vh, long long l
   }
 }
 
-template <int DP>
+template <int DP, int NT>
 __device__ __forceinline__ void store_kv(float* __restrict__ ks, float* __restrict__ vt, int tid,
-                                         const float4 (&rk)[SdpaCfg<DP>::K_F4], const float4 (&rv)[4]) {
-  using G = SdpaCfg<DP>;
+                                         const float4 (&rk)[SdpaCfg<DP, NT>::K_F4], const float4 (&rv)[4]) {
+  using G = SdpaCfg<DP, NT>;
 #pragma unroll
   for (int f = 0; f < G::K_F4; ++f) {
-    const int idx = tid + f * 256;
+    const int idx = tid + f * NT;
     const int key = idx / G::KD4, d0 = (idx % G::KD4) * 4;
     *reinterpret_cast<float4*>(ks + key * G::KLD + d0) = rk[f];
   }
@@ -127,13 +128,13 @@ __device__ __forceinline__ void store_kv(float* __restrict__ ks, float* __restri
   }
 }
 
-template <int DP, bool FULL>
-__global__ __launch_bounds__(256, 2) void sdpa_fwd_kernel(
+template <int DP, bool FULL, int NT>
+__global__ __launch_bounds__(NT, 2) void sdpa_fwd_kernel(
     int H, int group, int BH, int Sq, int Skv, int D, float qscale, int causal, const float* __restrict__ q,
     const float* __restrict__ k, const float* __restrict__ v, float* __restrict__ o, bch::SdpaStrides st,
     int qblocks) {
-  using G = SdpaCfg<DP>;
-  constexpr int KLD = G::KLD;
+  using G = SdpaCfg<DP, NT>;
+  constexpr int KLD = G::KLD, kBQ = G::BQ;
   extern __shared__ float4 smem4[];
   float* smem = reinterpret_cast<float*>(smem4);
   float* Ks = smem;                        // [2][kBKV][KLD]
@@ -185,9 +186,9 @@ __global__ __launch_bounds__(256, 2) void sdpa_fwd_kernel(
 
   float4 rk[G::K_F4];
   float4 rv[4];
-  load_k<DP, FULL>(kh, st.k.row, Skv, D, 0, tid, rk);
-  load_v<DP, FULL>(vh, st.v.row, Skv, D, 0, tid, rv);
-  store_kv<DP>(Ks, Vt, tid, rk, rv);
+  load_k<DP, NT, FULL>(kh, st.k.row, Skv, D, 0, tid, rk);
+  load_v<DP, NT, FULL>(vh, st.v.row, Skv, D, 0, tid, rv);
+  store_kv<DP, NT>(Ks, Vt, tid, rk, rv);
   __syncthreads();
 
   for (int t = 0; t < nkb; ++t) {
@@ -195,8 +196,8 @@ __global__ __launch_bounds__(256, 2) void sdpa_fwd_kernel(
     const int kb = t * kBKV;
     // next block (the last iteration reloads the last block; never read)
     const int kbn = min(t + 1, nkb - 1) * kBKV;
-    load_k<DP, FULL>(kh, st.k.row, Skv, D, kbn, tid, rk);
-    load_v<DP, FULL>(vh, st.v.row, Skv, D, kbn, tid, rv);
+    load_k<DP, NT, FULL>(kh, st.k.row, Skv, D, kbn, tid, rk);
+    load_v<DP, NT, FULL>(vh, st.v.row, Skv, D, kbn, tid, rv);
 
     // wave-uniform: skip blocks fully above this wavefront's diagonal and
     // wavefronts whose queries are all past Sq
@@ -262,7 +263,7 @@ __global__ __launch_bounds__(256, 2) void sdpa_fwd_kernel(
         }
       }
     }
-    store_kv<DP>(Ks + (cur ^ 1) * kBKV * KLD, Vt + (cur ^ 1) * DP * kVLD, tid, rk, rv);
+    store_kv<DP, NT>(Ks + (cur ^ 1) * kBKV * KLD, Vt + (cur ^ 1) * DP * kVLD, tid, rk, rv);
     __syncthreads();
   }
 
@@ -280,17 +281,18 @@ __global__ __launch_bounds__(256, 2) void sdpa_fwd_kernel(
   }
 }
 
-template <int DP, bool FULL>
+template <int DP, bool FULL, int NT>
 hipError_t launch_dp(hipStream_t s, int B, int H, int Hkv, int Sq, int Skv, int D, float scale, int causal,
                      const float* q, const float* k, const float* v, float* o, const bch::SdpaStrides& st) {
-  const int qblocks = (Sq + kBQ - 1) / kBQ;
+  using G = SdpaCfg<DP, NT>;
+  const int qblocks = (Sq + G::BQ - 1) / G::BQ;
   const long long blocks = (long long)B * H * qblocks;
   if (blocks > 0x7fffffffLL) return hipErrorInvalidValue;
-  const size_t lds = sizeof(float) * SdpaCfg<DP>::LDS_FLOATS;
-  auto kern = sdpa_fwd_kernel<DP, FULL>;
+  const size_t lds = sizeof(float) * G::LDS_FLOATS;
+  auto kern = sdpa_fwd_kernel<DP, FULL, NT>;
   hipError_t e = bch::ensure_dynamic_lds(reinterpret_cast<const void*>(kern), (int)lds);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), lds, s, H, H / Hkv, B * H, Sq, Skv, D,
+  hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(NT), lds, s, H, H / Hkv, B * H, Sq, Skv, D,
                      scale * kLog2E, causal, q, k, v, o, st, qblocks);
   return hipGetLastError();
 }
@@ -298,14 +300,19 @@ hipError_t launch_dp(hipStream_t s, int B, int H, int Hkv, int Sq, int Skv, int 
 bool aligned16(const float* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 bool mult4(const bch::SdpaLayout& l) { return l.batch % 4 == 0 && l.head % 4 == 0 && l.row % 4 == 0; }
 
+#ifndef BCH_SDPA_WIDE_NT  // threads per workgroup for head dims 64 and 128 (a build-time knob for sweeps)
+#define BCH_SDPA_WIDE_NT 256
+#endif
+
 template <int DP>
 hipError_t launch_d(hipStream_t s, int B, int H, int Hkv, int Sq, int Skv, int D, float scale, int causal,
                     const float* q, const float* k, const float* v, float* o, const bch::SdpaStrides& st) {
+  constexpr int NT = DP >= 64 ? BCH_SDPA_WIDE_NT : 256;
   // full tiles, 128-bit loads: every row start 16-byte aligned
-  const bool full = D == DP && Sq % kBQ == 0 && Skv % kBKV == 0 && aligned16(q) && aligned16(k) &&
+  const bool full = D == DP && Sq % SdpaCfg<DP, NT>::BQ == 0 && Skv % kBKV == 0 && aligned16(q) && aligned16(k) &&
                     aligned16(v) && mult4(st.q) && mult4(st.k) && mult4(st.v);
-  if (full) return launch_dp<DP, true>(s, B, H, Hkv, Sq, Skv, D, scale, causal, q, k, v, o, st);
-  return launch_dp<DP, false>(s, B, H, Hkv, Sq, Skv, D, scale, causal, q, k, v, o, st);
+  if (full) return launch_dp<DP, true, NT>(s, B, H, Hkv, Sq, Skv, D, scale, causal, q, k, v, o, st);
+  return launch_dp<DP, false, NT>(s, B, H, Hkv, Sq, Skv, D, scale, causal, q, k, v, o, st);
 }
 
 }  // namespace
