@@ -21,8 +21,19 @@
 // Design (FP32 MFMA for both products, v_mfma_f32_32x32x2_f32):
 //   * A workgroup = 4 wavefronts = 128 queries of one (b,h); wavefront w owns
 //     queries q0 + 32w .. +31, lane l's query is l % 32.  Key blocks of 32 are
-//     streamed through LDS, double-buffered, one barrier per block; the next
-//     block's global loads are issued before the current block's MFMAs.
+//     streamed through LDS, double-buffered, one barrier per block; blocks are
+//     loaded two ahead (the top of iteration t stores block t + 1 and issues
+//     the loads of block t + 2), which took causal 1.14 -> 1.10 ms at
+//     config 5: one block ahead, the compiler sank half of the loads down to
+//     their LDS stores and every block waited out a load latency.
+//   * Measured and not kept (config 5, same box, A/B): 512-thread
+//     workgroups of 256 queries (half the K/V traffic per FLOP; -1% /
+//     +2%); fragment reads pinned two chunks ahead; independent
+//     accumulators for the QK^T and PV chains (no change: dependent MFMA
+//     chains issue back to back); software-pipelining QK^T of block t + 1
+//     against the softmax of block t with branch-free masking and rescale
+//     (+2% / +4% time: the compiler kept the two phases apart and the
+//     unconditional rescale added work).
 //   * Scores are computed transposed, S^T = K Q^T (32 keys x 32 queries), so
 //     each lane holds 16 scores of ITS query: the row max and row sum are
 //     in-lane plus one exchange between the two lane halves.  The q operand
@@ -68,63 +79,81 @@ struct SdpaCfg {
   static_assert(K_F4 >= 1, "K tile must cover the workgroup");
 };
 
+// Staging registers for one key/value block, as vector values rather than
+// float4 arrays: carried across the loop back-edge, the arrays were left in
+// scratch memory.  Element 4f + e is component e of float4 number f.
+template <int N>
+using f32v = float __attribute__((ext_vector_type(N)));
+template <int DP, int NT>
+struct KvRegs {
+  f32v<4 * SdpaCfg<DP, NT>::K_F4> k;
+  f32v<16> v;
+};
+
+__device__ __forceinline__ float4 get4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+
 template <int DP, int NT, bool FULL>
 __device__ __forceinline__ void load_k(const float* __restrict__ kh, long long ldk, int Skv, int D, int kb, int tid,
-                                       float4 (&rk)[SdpaCfg<DP, NT>::K_F4]) {
+                                       KvRegs<DP, NT>& r) {
   using G = SdpaCfg<DP, NT>;
 #pragma unroll
   for (int f = 0; f < G::K_F4; ++f) {
     const int idx = tid + f * NT;
     const int key = idx / G::KD4, d0 = (idx % G::KD4) * 4;
     const int gk = kb + key;
+    float t[4];
     if (FULL) {
-      rk[f] = *reinterpret_cast<const float4*>(kh + gk * ldk + d0);
+      const float4 x = get4(kh + gk * ldk + d0);
+      t[0] = x.x; t[1] = x.y; t[2] = x.z; t[3] = x.w;
     } else {
-      float t[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) t[e] = (gk < Skv && d0 + e < D) ? kh[gk * ldk + d0 + e] : 0.0f;
-      rk[f] = make_float4(t[0], t[1], t[2], t[3]);
     }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) r.k[4 * f + e] = t[e];
   }
 }
 
 template <int DP, int NT, bool FULL>
 __device__ __forceinline__ void load_v(const float* __restrict__ vh, long long ldv, int Skv, int D, int kb, int tid,
-                                       float4 (&rv)[4]) {
+                                       KvRegs<DP, NT>& r) {
   using G = SdpaCfg<DP, NT>;
   const int blk = tid < G::V_BLK ? tid : 0;  // threads past the tile reload block 0 (unused)
   const int kq = blk / G::KD4, dq = blk % G::KD4;
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     const int gk = kb + 4 * kq + e, d0 = 4 * dq;
+    float t[4];
     if (FULL) {
-      rv[e] = *reinterpret_cast<const float4*>(vh + gk * ldv + d0);
+      const float4 x = get4(vh + gk * ldv + d0);
+      t[0] = x.x; t[1] = x.y; t[2] = x.z; t[3] = x.w;
     } else {
-      float t[4];
 #pragma unroll
       for (int c = 0; c < 4; ++c) t[c] = (gk < Skv && d0 + c < D) ? vh[gk * ldv + d0 + c] : 0.0f;
-      rv[e] = make_float4(t[0], t[1], t[2], t[3]);
     }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) r.v[4 * e + c] = t[c];
   }
 }
 
 template <int DP, int NT>
 __device__ __forceinline__ void store_kv(float* __restrict__ ks, float* __restrict__ vt, int tid,
-                                         const float4 (&rk)[SdpaCfg<DP, NT>::K_F4], const float4 (&rv)[4]) {
+                                         const KvRegs<DP, NT>& r) {
   using G = SdpaCfg<DP, NT>;
 #pragma unroll
   for (int f = 0; f < G::K_F4; ++f) {
     const int idx = tid + f * NT;
     const int key = idx / G::KD4, d0 = (idx % G::KD4) * 4;
-    *reinterpret_cast<float4*>(ks + key * G::KLD + d0) = rk[f];
+    *reinterpret_cast<float4*>(ks + key * G::KLD + d0) =
+        make_float4(r.k[4 * f], r.k[4 * f + 1], r.k[4 * f + 2], r.k[4 * f + 3]);
   }
   if (tid < G::V_BLK) {
+    // transpose the 4(key) x 4(d) block: row d of Vt gets keys 4kq .. 4kq + 3
     const int kq = tid / G::KD4, dq = tid % G::KD4;
     float* base = vt + (4 * dq) * kVLD + 4 * kq;
-    *reinterpret_cast<float4*>(base + 0 * kVLD) = make_float4(rv[0].x, rv[1].x, rv[2].x, rv[3].x);
-    *reinterpret_cast<float4*>(base + 1 * kVLD) = make_float4(rv[0].y, rv[1].y, rv[2].y, rv[3].y);
-    *reinterpret_cast<float4*>(base + 2 * kVLD) = make_float4(rv[0].z, rv[1].z, rv[2].z, rv[3].z);
-    *reinterpret_cast<float4*>(base + 3 * kVLD) = make_float4(rv[0].w, rv[1].w, rv[2].w, rv[3].w);
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      *reinterpret_cast<float4*>(base + c * kVLD) = make_float4(r.v[c], r.v[4 + c], r.v[8 + c], r.v[12 + c]);
   }
 }
 
@@ -184,20 +213,28 @@ __global__ __launch_bounds__(NT, 2) void sdpa_fwd_kernel(
   if (causal) kend = min(Skv, qb * kBQ + kBQ);
   const int nkb = (kend + kBKV - 1) / kBKV;
 
-  float4 rk[G::K_F4];
-  float4 rv[4];
-  load_k<DP, NT, FULL>(kh, st.k.row, Skv, D, 0, tid, rk);
-  load_v<DP, NT, FULL>(vh, st.v.row, Skv, D, 0, tid, rv);
-  store_kv<DP, NT>(Ks, Vt, tid, rk, rv);
+  // Key/value blocks are loaded two ahead: the top of iteration t stores
+  // block t + 1 (loaded during iteration t - 1) into the buffer the previous
+  // barrier released, then issues the loads of block t + 2.  With the loads
+  // one block ahead and stored at the bottom, the compiler moved half of them
+  // down to their stores, exposing a full load latency per block.
+  // Blocks past the end are clamped to the last one (reloaded, never read).
+  // (nkb >= 1: Skv >= 1 is validated, and a causal block row has >= 1 key)
+  KvRegs<DP, NT> kv;
+  load_k<DP, NT, FULL>(kh, st.k.row, Skv, D, 0, tid, kv);
+  load_v<DP, NT, FULL>(vh, st.v.row, Skv, D, 0, tid, kv);
+  store_kv<DP, NT>(Ks, Vt, tid, kv);
+  load_k<DP, NT, FULL>(kh, st.k.row, Skv, D, min(1, nkb - 1) * kBKV, tid, kv);
+  load_v<DP, NT, FULL>(vh, st.v.row, Skv, D, min(1, nkb - 1) * kBKV, tid, kv);
   __syncthreads();
 
   for (int t = 0; t < nkb; ++t) {
     const int cur = t & 1;
     const int kb = t * kBKV;
-    // next block (the last iteration reloads the last block; never read)
-    const int kbn = min(t + 1, nkb - 1) * kBKV;
-    load_k<DP, NT, FULL>(kh, st.k.row, Skv, D, kbn, tid, rk);
-    load_v<DP, NT, FULL>(vh, st.v.row, Skv, D, kbn, tid, rv);
+    store_kv<DP, NT>(Ks + (cur ^ 1) * kBKV * KLD, Vt + (cur ^ 1) * DP * kVLD, tid, kv);
+    const int kbn = min(t + 2, nkb - 1) * kBKV;
+    load_k<DP, NT, FULL>(kh, st.k.row, Skv, D, kbn, tid, kv);
+    load_v<DP, NT, FULL>(vh, st.v.row, Skv, D, kbn, tid, kv);
 
     // wave-uniform: skip blocks fully above this wavefront's diagonal and
     // wavefronts whose queries are all past Sq
@@ -263,7 +300,6 @@ __global__ __launch_bounds__(NT, 2) void sdpa_fwd_kernel(
         }
       }
     }
-    store_kv<DP, NT>(Ks + (cur ^ 1) * kBKV * KLD, Vt + (cur ^ 1) * DP * kVLD, tid, rk, rv);
     __syncthreads();
   }
 
