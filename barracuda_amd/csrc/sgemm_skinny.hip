@@ -26,9 +26,9 @@
 //     column-group boundaries; each run segment leaves one partial block.
 //     In a unit, lane l = 16q + i loads float4 B[k][n0 + 4i .. +3] and feeds
 //     component c to MFMA block c; lane quarter q takes rows 4q + s in step s.
-//     The workgroup's A^T slice (all of its units) is staged in LDS once,
-//     with direct-to-LDS 16-byte loads in a rolled loop; B loads run PF
-//     units ahead of the MFMAs.
+//     The A^T operand of a unit is one float4 of A per lane, loaded from
+//     L2 with the unit's B (A aligned; otherwise the workgroup's A^T slice
+//     is staged in LDS once); B loads run PF units ahead of the MFMAs.
 //   * Measured on MI355X (K 4096, N 11008, weights rotated past the 256 MB
 //     Infinity Cache): the stream-K layout removes the tail of an uneven
 //     grid (516 workgroups on 256 CUs); kernel code is kept small (one
@@ -48,14 +48,13 @@
 namespace {
 
 typedef float f32x4v __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) void lds_void;
 
 constexpr int kFmaCols = 256;  // columns per workgroup, FMA kernel
 constexpr int kFmaUnroll = 8;
 constexpr int kFmaSplits = 16;
 constexpr int kSkCols = 256;   // columns per unit / column group (4 x 64)
 constexpr int kSkRows = 16;    // rows per unit
-constexpr int kSkPF = 4;       // units of B in flight ahead of the MFMAs
+constexpr int kSkPF = 3;       // units of B in flight ahead of the MFMAs
 constexpr int kSkWGs = 256;    // one workgroup per CU
 constexpr int kLdsBytes = 160 * 1024;
 
@@ -128,11 +127,14 @@ __device__ __forceinline__ float epilogue(float s, const float* __restrict__ bia
   return relu ? fmaxf(s, 0.0f) : s;
 }
 
+// Block (x, m) covers columns 256 x .. 256 x + 255 of row m.
 __global__ __launch_bounds__(256) void sgemm_skinny_reduce(int M, int N, const float* __restrict__ P, int splits,
                                                            float* __restrict__ C, int ldc,
                                                            const float* __restrict__ bias, int relu) {
-  const long long t = (long long)blockIdx.x * 256 + threadIdx.x;
-  if (t >= (long long)M * N) return;
+  const int n = blockIdx.x * 256 + threadIdx.x;
+  const int m = blockIdx.y;
+  if (n >= N) return;
+  const long long t = (long long)m * N + n;
   const long long ps = (long long)M * N;
   float s = 0.f;
   for (int i = 0; i < splits; i += 16) {
@@ -143,7 +145,7 @@ __global__ __launch_bounds__(256) void sgemm_skinny_reduce(int M, int N, const f
     for (int q = 0; q < 16; ++q)
       if (i + q < splits) s += v[q];
   }
-  C[(t / N) * ldc + t % N] = epilogue(s, bias, (int)(t % N), relu);
+  C[(long long)m * ldc + n] = epilogue(s, bias, n, relu);
 }
 
 // ---------------------------------------------------------------- 4 < m <= 32
@@ -151,19 +153,21 @@ __global__ __launch_bounds__(256) void sgemm_skinny_reduce(int M, int N, const f
 // [w U / G, (w + 1) U / G).  The workgroup holding unit u:
 __host__ __device__ inline int wg_of_unit(long long u, long long U, int G) { return (int)(((u + 1) * G - 1) / U); }
 
-constexpr int vmcnt_imm(int n) { return (n & 0xF) | (0x7 << 4) | (0xF << 8) | ((n >> 4) << 14); }
-
 // Partial block of (column group g, slot s): P[((g * smax + s) * M + m) * 256 + column - 256 g], the slot
-// being the workgroup's position among those covering g.  DMA: A^T staged
-// with direct-to-LDS 16-byte loads (lda % 4 == 0, K % 4 == 0, A 16-byte
-// aligned); otherwise with scalar loads.
-template <int MB, bool DMA>
+// being the workgroup's position among those covering g.  AREG (lda % 4 == 0,
+// K % 4 == 0, A 16-byte aligned): the MFMA's A^T operand is one float4 of A
+// per lane per unit and block, loaded with that unit's B and from L2 (A is
+// small and shared by every workgroup), PF units ahead like B.  Otherwise the
+// workgroup's A^T slice is staged in LDS once with scalar loads.  Measured at
+// K 4096, N 11008, M 8: staging the slice with direct-to-LDS loads before the
+// first MFMA cost 1.7 us per call over the register operand.
+template <int MB, bool AREG>
 __global__ __launch_bounds__(256, 1) void sgemm_skinny_sk(int M, int N, int K, const float* __restrict__ A,
                                                           int lda, const float* __restrict__ B, int ldb,
                                                           float* __restrict__ P, long long U, int G, int kb,
                                                           int smax) {
   extern __shared__ float4 smem4[];
-  float* xs = reinterpret_cast<float*>(smem4);  // A^T: [16 MB][16 nu + 4]
+  float* xs = reinterpret_cast<float*>(smem4);  // A^T (staged path): [16 MB][16 nu + 4]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int lq = lane >> 4, li = lane & 15;
   const int w = blockIdx.x;
@@ -174,8 +178,13 @@ __global__ __launch_bounds__(256, 1) void sgemm_skinny_sk(int M, int N, int K, c
   const int ldu = 4 * q4 + 4;
   constexpr int PF = kSkPF, NB = kSkPF + 1;
 
+  const float* arow[MB];
+#pragma unroll
+  for (int b = 0; b < MB; ++b) arow[b] = A + (long long)min(16 * b + li, M - 1) * lda;
+
   // B cursor: unit (lg, lt); advanced once per load, held at the last unit.
   float4 wv[NB][4];
+  float4 av[NB][MB];
   int lg = g0, lt = t0, lcount = 0;
   auto load = [&](int sb) {
     const float* bp = B + min(lg * kSkCols + 64 * wave + 4 * li, N - 4);
@@ -183,60 +192,44 @@ __global__ __launch_bounds__(256, 1) void sgemm_skinny_sk(int M, int N, int K, c
 #pragma unroll
     for (int s = 0; s < 4; ++s)
       wv[sb][s] = bch::load_nt(reinterpret_cast<const float4*>(bp + (long long)min(r0 + s, K - 1) * ldb));
+    if (AREG) {
+      // A[16 b + li][r0 .. r0 + 3]: K % 4 == 0, so the float4 lies wholly below K or wholly past it
+#pragma unroll
+      for (int b = 0; b < MB; ++b) {
+        av[sb][b] = *reinterpret_cast<const float4*>(arow[b] + min(r0, K - 4));
+        if (r0 >= K) av[sb][b] = make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    }
     ++lcount;  // uniform arithmetic, no branch between the loads
     lt += lcount < nu ? 1 : 0;
     const int wrap = lt == kb ? 1 : 0;
     lt -= wrap * kb;
     lg += wrap;
   };
-  // k of staged float4 q (its unit is t0 + q / 4, wrapped into the next column group)
-  auto k_of = [&](int q) {
-    int t = t0 + (q >> 2);
-    while (t >= kb) t -= kb;
-    return kSkRows * t + 4 * (q & 3);
-  };
 
-  // padding rows M .. 16 MB - 1 first: LDS stores after the direct loads would wait for them
-  for (int e = M * q4 + tid; e < 16 * MB * q4; e += 256) {
-    const int m = e / q4, q = e - m * q4;
-    *reinterpret_cast<float4*>(xs + m * ldu + 4 * q) = make_float4(0.f, 0.f, 0.f, 0.f);
-  }
-  if (DMA) {
-    // one (row, 64-float4 block) per wavefront instruction, lanes past the row masked
-    const int nq = (q4 + 63) >> 6;
-    for (int pr = wave; pr < M * nq; pr += 4) {
-      const int m = pr / nq, qb = (pr - m * nq) << 6;
-      const int k = k_of(qb + lane);
-      if (qb + lane < q4)
-        __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(A + (long long)m * lda + min(k, K - 4)),
-                                         (lds_void*)(xs + m * ldu + 4 * qb), 16, 0, 0);
-    }
+  if (AREG) {
 #pragma unroll
     for (int p = 0; p < PF; ++p) load(p);
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm(4 * PF));  // the direct loads have landed; B stays in flight
-    if (K % kSkRows != 0) {
-      // rows past K in the last unit were loaded from clamped addresses: zero them once all waves' loads landed
-      __syncthreads();
-      for (int e = tid; e < M * q4; e += 256) {
-        const int m = e / q4, q = e - m * q4;
-        const int k = k_of(q);
-        if (k >= K) *reinterpret_cast<float4*>(xs + m * ldu + 4 * q) = make_float4(0.f, 0.f, 0.f, 0.f);
-      }
-    }
   } else {
-    for (int e = tid; e < M * q4; e += 256) {
+    // k of staged float4 q (its unit is t0 + q / 4, wrapped into the next column group)
+    auto k_of = [&](int q) {
+      int t = t0 + (q >> 2);
+      while (t >= kb) t -= kb;
+      return kSkRows * t + 4 * (q & 3);
+    };
+    for (int e = tid; e < 16 * MB * q4; e += 256) {
       const int m = e / q4, q = e - m * q4;
       const int k = k_of(q);
-      const float* ar = A + (long long)m * lda;
+      const float* ar = A + (long long)min(m, M - 1) * lda;
       float v[4];
 #pragma unroll
-      for (int c = 0; c < 4; ++c) v[c] = k + c < K ? ar[k + c] : 0.f;
+      for (int c = 0; c < 4; ++c) v[c] = m < M && k + c < K ? ar[k + c] : 0.f;
       *reinterpret_cast<float4*>(xs + m * ldu + 4 * q) = make_float4(v[0], v[1], v[2], v[3]);
     }
 #pragma unroll
     for (int p = 0; p < PF; ++p) load(p);
+    __syncthreads();
   }
-  __syncthreads();
 
   f32x4v acc[4][MB];
 #pragma unroll
@@ -264,7 +257,8 @@ __global__ __launch_bounds__(256, 1) void sgemm_skinny_sk(int M, int N, int K, c
   auto mma = [&](int sb, int i) {
     float4 x[MB];
 #pragma unroll
-    for (int b = 0; b < MB; ++b) x[b] = *reinterpret_cast<const float4*>(xs + (16 * b + li) * ldu + 16 * i + 4 * lq);
+    for (int b = 0; b < MB; ++b)
+      x[b] = AREG ? av[sb][b] : *reinterpret_cast<const float4*>(xs + (16 * b + li) * ldu + 16 * i + 4 * lq);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       const float ws[4] = {wv[sb][s].x, wv[sb][s].y, wv[sb][s].z, wv[sb][s].w};
@@ -445,18 +439,28 @@ __global__ __launch_bounds__(256, 1) void sgemm_skinny_w32(int M, int N, int K, 
 
 // C[m][n] = sum of the partial blocks of n's column group, in slot order
 // (the k order); loads in batches of 8, all in flight before the adds.
-// cols: columns per group (the partial block width).
+// Block (x, m) covers columns 256 x .. 256 x + 255 of row m; the partial
+// block width is 1 << cshift columns.  The group's slot count comes from the
+// stream-K bookkeeping in 32-bit arithmetic when U G < 2^32 (WIDE: 64-bit);
+// 64-bit divisions per thread measured as most of the kernel's instructions.
+template <bool WIDE>
 __global__ __launch_bounds__(256) void sgemm_skinny_sk_reduce(int M, int N, const float* __restrict__ P, long long U,
                                                               int G, int kb, int smax, float* __restrict__ C,
                                                               int ldc, const float* __restrict__ bias, int relu,
-                                                              int cols) {
-  const long long t = (long long)blockIdx.x * 256 + threadIdx.x;
-  if (t >= (long long)M * N) return;
-  const int m = (int)(t / N), n = (int)(t - (long long)m * N), g = n / cols;
-  const int wf = wg_of_unit((long long)g * kb, U, G);
-  const int ns = wg_of_unit((long long)g * kb + kb - 1, U, G) - wf + 1;
-  const float* p = P + ((long long)g * smax * M + m) * cols + (n - g * cols);
-  const long long st = (long long)M * cols;
+                                                              int cshift) {
+  const int n = blockIdx.x * 256 + threadIdx.x;
+  const int m = blockIdx.y;
+  if (n >= N) return;
+  const int g = n >> cshift;
+  int ns;
+  if (WIDE) {
+    ns = wg_of_unit((long long)g * kb + kb - 1, U, G) - wg_of_unit((long long)g * kb, U, G) + 1;
+  } else {
+    const unsigned u0 = (unsigned)g * (unsigned)kb, uu = (unsigned)U, gg = (unsigned)G;
+    ns = (int)(((u0 + (unsigned)kb) * gg - 1u) / uu) - (int)(((u0 + 1u) * gg - 1u) / uu) + 1;
+  }
+  const float* p = P + ((long long)g * smax * M + m) * (1 << cshift) + (n - (g << cshift));
+  const long long st = (long long)M << cshift;
   float s = 0.f;
   for (int i = 0; i < ns; i += 8) {
     float v[8];
@@ -467,6 +471,20 @@ __global__ __launch_bounds__(256) void sgemm_skinny_sk_reduce(int M, int N, cons
       if (i + q < ns) s += v[q];
   }
   C[(long long)m * ldc + n] = epilogue(s, bias, n, relu);
+}
+
+// Launch the split-k reduce of a stream-K plan (cols: partial block width, 256 or 128).
+hipError_t launch_sk_reduce(hipStream_t s, int m, int n, const float* P, long long U, int G, int kb, int smax,
+                            float* C, int ldc, const float* bias, int relu, int cols) {
+  const dim3 grid((unsigned)((n + 255) / 256), (unsigned)m);
+  const int cshift = cols == 256 ? 8 : 7;
+  if ((unsigned long long)U * (unsigned long long)G < (1ULL << 32))
+    hipLaunchKernelGGL(sgemm_skinny_sk_reduce<false>, grid, dim3(256), 0, s, m, n, P, U, G, kb, smax, C, ldc, bias,
+                       relu, cshift);
+  else
+    hipLaunchKernelGGL(sgemm_skinny_sk_reduce<true>, grid, dim3(256), 0, s, m, n, P, U, G, kb, smax, C, ldc, bias,
+                       relu, cshift);
+  return hipGetLastError();
 }
 
 // ---------------------------------------------------------------- transposed weights, m <= 32
@@ -648,23 +666,31 @@ void fma_plan(int k, int* kchunk, int* splits) {
   *splits = (k + kc - 1) / kc;
 }
 
-// Stream-K path: units, workgroups (one per CU, more when a run's A^T slice
-// would not fit in LDS), units per workgroup, and partial slots per group.
+// Stream-K path: units, workgroups (one per CU; on the staged-A path more
+// when a run's A^T slice would not fit in LDS), units per workgroup, and
+// partial slots per group.
 struct SkPlan {
   long long U = 0;
   int cg = 0, kb = 0, G = 0, upw = 0, smax = 0, mb = 1;
   size_t lds = 0;
 };
 
-SkPlan sk_plan(int m, int n, int k) {
+// A operand per unit in registers: needs whole, aligned float4 rows of A.
+bool sk_areg(int k, const float* A, int lda) {
+  return k % 4 == 0 && lda % 4 == 0 && (reinterpret_cast<uintptr_t>(A) & 15) == 0;
+}
+
+SkPlan sk_plan(int m, int n, int k, bool areg) {
   SkPlan p;
   p.mb = sk_mb(m);
   p.cg = (n + kSkCols - 1) / kSkCols;
   p.kb = (k + kSkRows - 1) / kSkRows;
   p.U = (long long)p.cg * p.kb;
-  const int cap = (kLdsBytes / (4 * 16 * p.mb) - 4) / kSkRows;  // units whose A^T fits in LDS
   long long g = cu_count();
-  if ((p.U + g - 1) / g > cap) g = (p.U + cap - 1) / cap;
+  if (!areg) {
+    const int cap = (kLdsBytes / (4 * 16 * p.mb) - 4) / kSkRows;  // units whose A^T fits in LDS
+    if ((p.U + g - 1) / g > cap) g = (p.U + cap - 1) / cap;
+  }
   if (g > p.U) g = p.U;
   p.G = (int)g;
   p.upw = (int)((p.U + p.G - 1) / p.G);
@@ -672,7 +698,7 @@ SkPlan sk_plan(int m, int n, int k) {
     const int ns = wg_of_unit((long long)c * p.kb + p.kb - 1, p.U, p.G) - wg_of_unit((long long)c * p.kb, p.U, p.G) + 1;
     if (ns > p.smax) p.smax = ns;
   }
-  p.lds = sizeof(float) * 16 * p.mb * (size_t)(16 * p.upw + 4);
+  p.lds = areg ? 0 : sizeof(float) * 16 * p.mb * (size_t)(16 * p.upw + 4);
   return p;
 }
 
@@ -729,12 +755,14 @@ hipError_t launch_w32(hipStream_t s, const W32Plan& p, int m, int n, int k, cons
   return hipGetLastError();
 }
 
-template <int MB, bool DMA>
+template <int MB, bool AREG>
 hipError_t launch_sk(hipStream_t s, const SkPlan& p, int m, int n, int k, const float* A, int lda, const float* B,
                      int ldb, float* P) {
-  hipError_t e = bch::ensure_dynamic_lds(reinterpret_cast<const void*>(sgemm_skinny_sk<MB, DMA>), kLdsBytes);
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((sgemm_skinny_sk<MB, DMA>), dim3(p.G), dim3(256), p.lds, s, m, n, k, A, lda, B, ldb, P, p.U,
+  if (!AREG) {
+    hipError_t e = bch::ensure_dynamic_lds(reinterpret_cast<const void*>(sgemm_skinny_sk<MB, AREG>), kLdsBytes);
+    if (e != hipSuccess) return e;
+  }
+  hipLaunchKernelGGL((sgemm_skinny_sk<MB, AREG>), dim3(p.G), dim3(256), p.lds, s, m, n, k, A, lda, B, ldb, P, p.U,
                      p.G, p.kb, p.smax);
   return hipGetLastError();
 }
@@ -780,10 +808,7 @@ hipError_t launch_sgemm_skinny_nt(hipStream_t s, int m, int n, int k, const floa
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  const long long total = (long long)m * n;
-  hipLaunchKernelGGL(sgemm_skinny_sk_reduce, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, m, n, P, p.U, p.G,
-                     p.nkb, p.smax, C, ldc, bias, relu, kNtRows);
-  return hipGetLastError();
+  return launch_sk_reduce(s, m, n, P, p.U, p.G, p.nkb, p.smax, C, ldc, bias, relu, kNtRows);
 }
 
 size_t sgemm_skinny_workspace_bytes(int m, int n, int k) {
@@ -792,9 +817,13 @@ size_t sgemm_skinny_workspace_bytes(int m, int n, int k) {
     fma_plan(k, &kc, &s);
     return sizeof(float) * (size_t)s * (size_t)m * (size_t)n;
   }
-  // the larger of the two MFMA paths' needs (which one runs depends on A's alignment)
-  const SkPlan p = sk_plan(m, n, k);
-  size_t bytes = sizeof(float) * (size_t)p.cg * (size_t)p.smax * (size_t)m * kSkCols;
+  // the largest of the MFMA paths' needs (which one runs depends on A's alignment)
+  size_t bytes = 0;
+  for (const bool areg : {false, true}) {
+    const SkPlan p = sk_plan(m, n, k, areg);
+    const size_t b1 = sizeof(float) * (size_t)p.cg * (size_t)p.smax * (size_t)m * kSkCols;
+    if (b1 > bytes) bytes = b1;
+  }
   if (m > 16) {
     const W32Plan q = w32_plan(n, k);
     const size_t b2 = sizeof(float) * (size_t)q.cg * (size_t)q.smax * (size_t)m * kSkCols;
@@ -823,8 +852,7 @@ hipError_t launch_sgemm_skinny(hipStream_t s, int m, int n, int k, const float* 
                                const float* bias, int relu) {
   if (ws == nullptr || ws_bytes < sgemm_skinny_workspace_bytes(m, n, k)) return hipErrorInvalidValue;
   float* P = static_cast<float*>(ws);
-  const long long total = (long long)m * n;
-  const dim3 rgrid((unsigned)((total + 255) / 256));
+  const dim3 rgrid((unsigned)((n + 255) / 256), (unsigned)m);
   if (use_fma(m)) {
     int kchunk, splits;
     fma_plan(k, &kchunk, &splits);
@@ -845,21 +873,17 @@ hipError_t launch_sgemm_skinny(hipStream_t s, int m, int n, int k, const float* 
     hipError_t e = k % kW32Rows == 0 ? launch_w32<false>(s, q, m, n, k, A, lda, B, ldb, P)
                                      : launch_w32<true>(s, q, m, n, k, A, lda, B, ldb, P);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(sgemm_skinny_sk_reduce, rgrid, dim3(256), 0, s, m, n, P, q.U, q.G, q.nblk, q.smax, C, ldc,
-                       bias, relu, kSkCols);
-    return hipGetLastError();
+    return launch_sk_reduce(s, m, n, P, q.U, q.G, q.nblk, q.smax, C, ldc, bias, relu, kSkCols);
   }
-  const SkPlan p = sk_plan(m, n, k);
-  const bool dma = lda % 4 == 0 && k % 4 == 0 && (reinterpret_cast<uintptr_t>(A) & 15) == 0;
+  const bool areg = sk_mb(m) == 1 && sk_areg(k, A, lda);
+  const SkPlan p = sk_plan(m, n, k, areg);
   hipError_t e;
   if (p.mb == 1)
-    e = dma ? launch_sk<1, true>(s, p, m, n, k, A, lda, B, ldb, P) : launch_sk<1, false>(s, p, m, n, k, A, lda, B, ldb, P);
-  else
-    e = dma ? launch_sk<2, true>(s, p, m, n, k, A, lda, B, ldb, P) : launch_sk<2, false>(s, p, m, n, k, A, lda, B, ldb, P);
+    e = areg ? launch_sk<1, true>(s, p, m, n, k, A, lda, B, ldb, P) : launch_sk<1, false>(s, p, m, n, k, A, lda, B, ldb, P);
+  else  // m > 16 with aligned A takes the 32x32x2 kernel above
+    e = launch_sk<2, false>(s, p, m, n, k, A, lda, B, ldb, P);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(sgemm_skinny_sk_reduce, rgrid, dim3(256), 0, s, m, n, P, p.U, p.G, p.kb, p.smax, C, ldc, bias,
-                     relu, kSkCols);
-  return hipGetLastError();
+  return launch_sk_reduce(s, m, n, P, p.U, p.G, p.kb, p.smax, C, ldc, bias, relu, kSkCols);
 }
 
 }  // namespace bch
