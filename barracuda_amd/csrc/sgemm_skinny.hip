@@ -631,6 +631,125 @@ __global__ __launch_bounds__(256, 2) void sgemm_skinny_nt(int M, int N, int K, c
   flush();
 }
 
+// ---------------------------------------------------------------- transposed weights, m <= 4, whole rows
+// C[m][n] = sum_k A[m][k] W[n][k] with every workgroup owning whole rows of W
+// (a contiguous run of output columns) over all of K: one launch, no split-k
+// partials, no reduce kernel.  Rows of W are contiguous, so workgroup g
+// streams rows [g N / G, (g + 1) N / G) as one contiguous block of memory.
+// Wave w of the workgroup takes rows w, w + 8, ... of the block; a row is
+// cut into chunks of 1024 k, four 1 KB row loads each (lane l holds
+// k = 256 j + 4 l .. + 3 of load j), streamed one chunk ahead.  A is staged
+// in LDS once ([MT][nk * 1024], zero past M and K), so the FMA operand of a
+// load is one ds_read_b128 per row of A.  Each lane keeps four
+// partial sums per row of A (one per float4 component); at the end of a row
+// they are added, summed over the wavefront (DPP all-reduce, fixed order),
+// and the epilogue (+ bias[n], ReLU) is applied before the store.  The row
+// count per wave differs by at most one across the workgroup.  EDGE: K is
+// not a multiple of 1024, so loads past K are clamped and zeroed.  Requires
+// K % 4 == 0, lda % 4 == 0, ldw % 4 == 0 and 16-byte aligned A and W.
+// Measured at K 4096, N 11008 (per call, M = 1 / 2 / 4 / 8): chunks of 2048
+// k two ahead 32.7 / 33.9 / 37.9 / 40.5 us, one ahead 30.2 / 32.0 / 33.2 /
+// 38.6 us; chunks of 1024 k one ahead 30.4 / 31.1 / 32.4 / 38.7 us (two or
+// three ahead slower); 4 or 16 waves per workgroup slower.  At M = 8 the LDS
+// reads of A (one 16-byte read per W float4 per row of A) and the FMAs make
+// it slower than the MFMA split-k kernel (35.8 us), so M = 5..8 stay there.
+constexpr int kRowK = 1024;                 // k per chunk
+constexpr int kRowLoads = kRowK / 256;      // 1 KB row loads per chunk
+constexpr int kRowPF = 1;                   // chunks in flight ahead of the FMAs
+constexpr int kRowWaves = 8;                // wavefronts per workgroup (one workgroup per CU)
+
+template <int MT, bool EDGE>
+__global__ __launch_bounds__(64 * kRowWaves, 1) void sgemm_skinny_nt_rows(int M, int N, int K,
+                                                                         const float* __restrict__ A, int lda,
+                                                                         const float* __restrict__ W, int ldw,
+                                                                         float* __restrict__ C, int ldc,
+                                                                         const float* __restrict__ bias,
+                                                                         int relu) {
+  extern __shared__ float4 smem4[];
+  float* as = reinterpret_cast<float*>(smem4);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nk = (K + kRowK - 1) / kRowK;
+  const int KP = nk * kRowK;  // staged row length
+  for (int e = tid; e < MT * (KP / 4); e += 64 * kRowWaves) {
+    const int m = e / (KP / 4), k = 4 * (e - m * (KP / 4));
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (m < M && k < K) v = *reinterpret_cast<const float4*>(A + (long long)m * lda + k);
+    *reinterpret_cast<float4*>(as + m * KP + k) = v;
+  }
+  __syncthreads();
+
+  const int r0 = (int)((long long)blockIdx.x * N / gridDim.x);
+  const int r1 = (int)((long long)(blockIdx.x + 1) * N / gridDim.x);
+  const int nrows = r1 - r0 > wave ? (r1 - r0 - wave + kRowWaves - 1) / kRowWaves : 0;
+  const int nu = nrows * nk;  // chunks of this wave, row-major
+  if (nu == 0) return;        // no barrier follows
+  constexpr int PF = kRowPF, NB = kRowPF + 1;
+
+  float4 wv[NB][kRowLoads];
+  int lrow = 0, lchunk = 0, lcount = 0;  // load cursor: advanced once per load, held at the last chunk
+  auto load = [&](int sb) {
+    const float* wr = W + (long long)(r0 + wave + kRowWaves * lrow) * ldw;
+#pragma unroll
+    for (int j = 0; j < kRowLoads; ++j) {
+      const int k = kRowK * lchunk + 256 * j + 4 * lane;
+      wv[sb][j] = bch::load_nt(reinterpret_cast<const float4*>(wr + (EDGE ? min(k, K - 4) : k)));
+      if (EDGE && k >= K) wv[sb][j] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    ++lcount;
+    const int adv = lcount < nu ? 1 : 0;
+    lchunk += adv;
+    const int wrap = lchunk == nk ? 1 : 0;
+    lchunk -= wrap * nk;
+    lrow += wrap;
+  };
+#pragma unroll
+  for (int p = 0; p < PF; ++p) load(p);
+
+  float4 acc[MT];
+#pragma unroll
+  for (int m = 0; m < MT; ++m) acc[m] = make_float4(0.f, 0.f, 0.f, 0.f);
+  int crow = 0, cchunk = 0;
+  auto fma_chunk = [&](int sb) {
+#pragma unroll
+    for (int j = 0; j < kRowLoads; ++j) {
+      const int k = kRowK * cchunk + 256 * j + 4 * lane;
+      const float4 w = wv[sb][j];
+#pragma unroll
+      for (int m = 0; m < MT; ++m) {
+        const float4 a = *reinterpret_cast<const float4*>(as + m * KP + k);
+        acc[m].x = fmaf(a.x, w.x, acc[m].x);
+        acc[m].y = fmaf(a.y, w.y, acc[m].y);
+        acc[m].z = fmaf(a.z, w.z, acc[m].z);
+        acc[m].w = fmaf(a.w, w.w, acc[m].w);
+      }
+    }
+  };
+  auto finish_row = [&]() {
+    const int n = r0 + wave + kRowWaves * crow;
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      const float v = bch::wave_allreduce((acc[m].x + acc[m].y) + (acc[m].z + acc[m].w), bch::OpSum());
+      if (m < M && lane == 0) C[(long long)m * ldc + n] = epilogue(v, bias, n, relu);
+      acc[m] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  };
+  for (int i = 0; i < nu; i += NB) {
+#pragma unroll
+    for (int p = 0; p < NB; ++p) {
+      load((p + PF) % NB);
+      if (i + p < nu) {
+        fma_chunk(p);
+        if (++cchunk == nk) {
+          finish_row();
+          cchunk = 0;
+          ++crow;
+        }
+      }
+    }
+  }
+}
+
 bool use_fma(int m) { return m <= 4; }
 
 int sk_mb(int m) { return m <= 16 ? 1 : 2; }
@@ -745,6 +864,36 @@ NtPlan nt_plan(int n, int k) {
   return p;
 }
 
+// Whole-row path for transposed weights: m <= 4, the staged A fits in LDS,
+// and every wave of every CU gets at least one row.
+int rows_mt(int m) { return m <= 1 ? 1 : m <= 2 ? 2 : 4; }
+
+bool use_rows(int m, int n, int k) {
+  if (m > 4) return false;
+  const long long kp = (long long)((k + kRowK - 1) / kRowK) * kRowK;
+  if ((long long)rows_mt(m) * kp * (long long)sizeof(float) > kLdsBytes) return false;
+  return n >= kRowWaves * cu_count();
+}
+
+template <int MT>
+hipError_t launch_rows(hipStream_t s, int m, int n, int k, const float* A, int lda, const float* W, int ldw, float* C,
+                       int ldc, const float* bias, int relu) {
+  const bool edge = k % kRowK != 0;
+  const void* f = edge ? reinterpret_cast<const void*>(sgemm_skinny_nt_rows<MT, true>)
+                       : reinterpret_cast<const void*>(sgemm_skinny_nt_rows<MT, false>);
+  hipError_t e = bch::ensure_dynamic_lds(f, kLdsBytes);
+  if (e != hipSuccess) return e;
+  const int lds = (int)(sizeof(float) * MT * (size_t)((k + kRowK - 1) / kRowK) * kRowK);
+  const dim3 grid(cu_count()), block(64 * kRowWaves);
+  if (edge)
+    hipLaunchKernelGGL((sgemm_skinny_nt_rows<MT, true>), grid, block, lds, s, m, n, k, A, lda, W, ldw, C, ldc, bias,
+                       relu);
+  else
+    hipLaunchKernelGGL((sgemm_skinny_nt_rows<MT, false>), grid, block, lds, s, m, n, k, A, lda, W, ldw, C, ldc, bias,
+                       relu);
+  return hipGetLastError();
+}
+
 template <bool EDGE>
 hipError_t launch_w32(hipStream_t s, const W32Plan& p, int m, int n, int k, const float* A, int lda, const float* B,
                       int ldb, float* P) {
@@ -779,6 +928,7 @@ bool sgemm_skinny_nt_applies(int m, int n, int k, const float* A, int lda, const
 }
 
 size_t sgemm_skinny_nt_workspace_bytes(int m, int n, int k) {
+  if (use_rows(m, n, k)) return 0;
   const NtPlan p = nt_plan(n, k);
   return sizeof(float) * (size_t)p.ng * (size_t)p.smax * (size_t)m * kNtRows;
 }
@@ -786,6 +936,12 @@ size_t sgemm_skinny_nt_workspace_bytes(int m, int n, int k) {
 hipError_t launch_sgemm_skinny_nt(hipStream_t s, int m, int n, int k, const float* A, int lda, const float* W,
                                   int ldw, float* C, int ldc, void* ws, size_t ws_bytes, const float* bias,
                                   int relu) {
+  if (use_rows(m, n, k)) {
+    const int mt = rows_mt(m);
+    if (mt == 1) return launch_rows<1>(s, m, n, k, A, lda, W, ldw, C, ldc, bias, relu);
+    if (mt == 2) return launch_rows<2>(s, m, n, k, A, lda, W, ldw, C, ldc, bias, relu);
+    return launch_rows<4>(s, m, n, k, A, lda, W, ldw, C, ldc, bias, relu);
+  }
   if (ws == nullptr || ws_bytes < sgemm_skinny_nt_workspace_bytes(m, n, k)) return hipErrorInvalidValue;
   float* P = static_cast<float*>(ws);
   const NtPlan p = nt_plan(n, k);

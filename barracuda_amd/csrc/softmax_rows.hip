@@ -48,40 +48,9 @@ __device__ __forceinline__ float exp_f32(float x) {
   return fmaf(r, e * kLn2, r);    // 2^p * (1 + e ln 2)
 }
 
-template <int CTRL>
-__device__ __forceinline__ float dpp(float v) {
-  return __builtin_bit_cast(
-      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
-                                         0xF, 0xF, true));
-}
-
-__device__ __forceinline__ float readlane(float v, int lane) {
-  return __builtin_bit_cast(
-      float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
-}
-
-struct OpMax {
-  __device__ float operator()(float a, float b) const { return fmaxf(a, b); }
-};
-struct OpSum {
-  __device__ float operator()(float a, float b) const { return a + b; }
-};
-
-// All-reduce over the 64 lanes of a wavefront; every lane gets the result.
-//   quad_perm[1,0,3,2] (0xB1): lane ^ 1      quad_perm[2,3,0,1] (0x4E): lane ^ 2
-//   row_half_mirror (0x141): lane i <-> 7-i within 8, joins the two quads
-//   row_mirror      (0x140): lane i <-> 15-i within 16, joins the two halves
-// then the four 16-lane rows are combined through v_readlane (uniform).
-template <typename Op>
-__device__ __forceinline__ float wave_allreduce(float v, Op op) {
-  v = op(v, dpp<0xB1>(v));
-  v = op(v, dpp<0x4E>(v));
-  v = op(v, dpp<0x141>(v));
-  v = op(v, dpp<0x140>(v));
-  float r0 = readlane(v, 0), r1 = readlane(v, 16);
-  float r2 = readlane(v, 32), r3 = readlane(v, 48);
-  return op(op(r0, r1), op(r2, r3));
-}
+using bch::OpMax;
+using bch::OpSum;
+using bch::wave_allreduce;
 
 // One wavefront per row, NV float4 per lane (cols <= 256 * NV, cols % 4 == 0).
 template <int NV>

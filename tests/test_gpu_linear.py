@@ -77,6 +77,35 @@ def test_sgemm_ex_transposed_decode_shapes(dev, m, n, k):
         assert O.max_rel_err(got, _ref(x, w, b, True, act == N.BCH_ACT_RELU)) <= TOL, act
 
 
+@pytest.mark.parametrize("m,n,k", [(1, 2048, 4096), (2, 2053, 2052), (3, 5000, 1024), (4, 4100, 6144),
+                                   (4, 2304, 4100), (1, 3000, 44000), (6, 3000, 2048)])
+def test_sgemm_ex_transposed_whole_rows(dev, m, n, k):
+    """m <= 4, n >= 8 waves x CUs: each workgroup owns whole weight rows (one launch, no partials).
+    Covers every row-block width (m = 1, 2, 3-4), rows per workgroup not a multiple of the wave
+    count, K past a 1024 chunk boundary (4100, 2052), a staged A too large for LDS (m = 1,
+    k = 44000: 176 KB), which takes the split-k kernel, and m = 6 next to it (split-k)."""
+    _say(f"sgemm_ex transposed whole rows m={m} n={n} k={k}")
+    rng = O.Lcg(m * 101 + n + 3 * k)
+    x = rng.normal((m, k))
+    w = rng.normal((n, k), 0.0, 0.05)
+    bias = rng.normal((n,))
+    for act, b in ((N.BCH_ACT_RELU, bias), (N.BCH_ACT_NONE, None)):
+        got = _sgemm_ex(dev, 1, x, w, b, act)
+        assert O.max_rel_err(got, _ref(x, w, b, True, act == N.BCH_ACT_RELU)) <= TOL, act
+        assert np.array_equal(got, _sgemm_ex(dev, 1, x, w, b, act)), "not deterministic"
+
+
+def test_sgemm_ex_transposed_whole_rows_exact_on_integers(dev):
+    _say("sgemm_ex transposed whole rows, integers")
+    rng = np.random.default_rng(23)
+    for m, n, k in ((1, 2048, 96), (4, 2100, 2056), (2, 2048, 1024)):
+        x = rng.integers(-8, 9, (m, k)).astype(np.float32)
+        w = rng.integers(-8, 9, (n, k)).astype(np.float32)
+        b = rng.integers(-100, 101, n).astype(np.float32)
+        want = x.astype(np.int64) @ w.astype(np.int64).T + b
+        assert np.array_equal(_sgemm_ex(dev, 1, x, w, b, N.BCH_ACT_NONE), want.astype(np.float32))
+
+
 def test_sgemm_ex_transposed_unaligned_falls_back(dev):
     """lda not a multiple of 4: the tiled kernel's guarded path."""
     _say("sgemm_ex transposed unaligned lda")
