@@ -260,6 +260,7 @@ def _bench_batched(dev, T, reps):
 
 def _bench_sdpa(dev, T, reps):
     from barracuda_amd import LcgStream, Tensor
+    from barracuda_amd import _native as N
     lib, ctx = dev._lib, dev.ctx
     out = {}
     # config 5: SDPA forward B=4, H=32, S=2048, D=128, N(0,1), seed 4, scale 1/sqrt(128)
@@ -277,7 +278,20 @@ def _bench_sdpa(dev, T, reps):
         out[key] = {"ms": ev, "TFLOP/s": fl / (ev * 1e-3) / 1e12,
                     "mfma_frac": fl / (ev * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS,
                     "traffic": load_traffic(key)}
-    del q, k, v, o
+    del k, v
+    # grouped-query attention (ops/grouped_query_attention): the same queries, 8 key/value
+    # heads shared by 4 query heads each, through bch_sdpa_fwd_ex (dense [B,H,S,D] layouts)
+    Hkv = 8
+    kg, vg = s.normal([Bb, Hkv, S, D]), s.normal([Bb, Hkv, S, D])
+    lq = N.AttnLayout(H * S * D, S * D, D)
+    lkv = N.AttnLayout(Hkv * S * D, S * D, D)
+    pkg, pvg = C.c_void_p(kg.ptr), C.c_void_p(vg.ptr)
+    wall, ev = T.run(lambda i: lib.bch_sdpa_fwd_ex(ctx, Bb, H, Hkv, S, S, D, scale, 0, pq, lq, pkg, lkv, pvg, lkv,
+                                                   po, lq), max(5, reps // 2), 2)
+    fl = 4.0 * Bb * H * S * S * D
+    out["gqa_hkv8_noncausal"] = {"ms": ev, "TFLOP/s": fl / (ev * 1e-3) / 1e12,
+                                 "mfma_frac": fl / (ev * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS}
+    del q, kg, vg, o
     return out
 
 
