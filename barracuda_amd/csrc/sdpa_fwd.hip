@@ -53,7 +53,27 @@
 //   * Causal: key blocks past the workgroup's last query are not loaded;
 //     blocks entirely above a wavefront's diagonal are skipped by that
 //     wavefront; the diagonal block is masked per element.  Workgroups are
-//     issued longest first across all heads (query block major).
+//     issued longest first across all heads (query block major); with
+//     B*H % 8 == 0 every query block of a head then lands on one XCD.
+//   * Non-causal: workgroups are issued head-major and remapped so that each
+//     XCD (dispatch is round-robin over the 8 XCDs) runs a contiguous range
+//     of heads, all query blocks of a head together.  The co-resident
+//     workgroups of an XCD then cover 4 heads instead of 16, and each head's
+//     K/V blocks are fetched into that XCD's L2 once for up to 16 readers:
+//     at config 5, L2 misses 18.6 M -> 4.2 M and HBM fetch 2.2 -> 0.4 GB per
+//     launch.  Query heads sharing a key/value head (grouped-query) are
+//     adjacent, so they share it in the same L2.
+//   * The max and sum exchanges between the two lane halves are
+//     v_permlane32_swap (a VALU op) rather than an LDS-routed shuffle, which
+//     sat on the path from the last QK^T MFMA to the first PV MFMA.
+//     Together with the order above, against the previous kernel on one
+//     box: non-causal 2.22 -> 2.20 ms, causal 1.11 -> 1.10, grouped-query
+//     2.08 -> 2.06 (on another box the order alone: 2.23 -> 2.18).
+//   * Measured and not kept: s_setprio 1 over each wave's MFMA phases
+//     (non-causal 0-2% faster, causal 1-2% slower); head-major order for
+//     causal too (1.10 -> 1.45 ms: a head's long query blocks then run
+//     together, unbalanced); causal in groups of 4 heads per XCD, longest
+//     first within a group (1.18 ms).
 #include "bch_internal.h"
 
 #include <math.h>
@@ -89,6 +109,17 @@ struct KvRegs {
   f32v<4 * SdpaCfg<DP, NT>::K_F4> k;
   f32v<16> v;
 };
+
+// x combined with x from lane l ^ 32, the same value in both halves.
+// v_permlane32_swap of (x, x) returns, per lane, {x[l & 31], x[(l & 31) + 32]}.
+__device__ __forceinline__ float half_swap_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float half_swap_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 
 __device__ __forceinline__ float4 get4(const float* p) { return *reinterpret_cast<const float4*>(p); }
 
@@ -169,9 +200,19 @@ __global__ __launch_bounds__(NT, 2) void sdpa_fwd_kernel(
   float* Ks = smem;                        // [2][kBKV][KLD]
   float* Vt = smem + 2 * kBKV * KLD;       // [2][DP][kVLD]
 
-  // query-block major: all heads' longest (causal) query blocks go first
-  const int qi = blockIdx.x / BH;
-  const int bh = blockIdx.x % BH;
+  // causal: query-block major, all heads' longest query blocks first.
+  // non-causal: head-major over an XCD-contiguous remap of the grid.
+  int qi, bh;
+  if (causal) {
+    qi = blockIdx.x / BH;
+    bh = blockIdx.x % BH;
+  } else {
+    const int nb = gridDim.x;
+    int L = blockIdx.x;
+    if ((nb & 7) == 0) L = (L & 7) * (nb >> 3) + (L >> 3);
+    bh = L / qblocks;
+    qi = L - bh * qblocks;
+  }
   const int qb = causal ? qblocks - 1 - qi : qi;
 
   const int tid = threadIdx.x;
@@ -264,7 +305,7 @@ __global__ __launch_bounds__(NT, 2) void sdpa_fwd_kernel(
       float bm = s[0];
 #pragma unroll
       for (int r = 1; r < 16; ++r) bm = fmaxf(bm, s[r]);
-      bm = fmaxf(bm, __shfl_xor(bm, 32));
+      bm = half_swap_max(bm);
       // move the reference max only when this block exceeds it by > 2^kLazy
       const bool move = bm > m_ref + kLazy;  // -inf reference: any finite block max moves it
       if (__any(move)) {
@@ -284,7 +325,7 @@ __global__ __launch_bounds__(NT, 2) void sdpa_fwd_kernel(
         s[r] = __builtin_amdgcn_exp2f(s[r] - m_use);
         rs += s[r];
       }
-      rs += __shfl_xor(rs, 32);
+      rs = half_swap_sum(rs);
       l_run += rs;
 
       const float* vs = Vt + cur * DP * kVLD + li * kVLD + 4 * lh;

@@ -42,10 +42,19 @@ def log(msg: str) -> None:
 
 
 class Timer:
-    """HIP events on the context's stream + wall clock around K launches."""
+    """HIP events on the context's stream + wall clock around K launches.
 
-    def __init__(self, dev):
+    `warm_ms`: after the warmup launches, keep launching (untimed) until that
+    much wall time has passed.  Measured on the box: from idle, the clocks
+    take ~25 ms of full load to settle (GEMM 4096^3 launches go 1100-1190 us
+    -> 940-945 us over the first ~25 launches; the first 12 attention
+    launches of a process average 2.19 ms against 2.06 ms afterwards), and
+    each extra workload starts after host-side input generation has left
+    the GPU idle."""
+
+    def __init__(self, dev, warm_ms: float = 0.0):
         self.dev = dev
+        self.warm_ms = warm_ms
         lib = dev._lib
         self.e0, self.e1 = C.c_void_p(), C.c_void_p()
         dev.check(lib.bch_event_create(dev.ctx, C.byref(self.e0)), "event")
@@ -53,9 +62,14 @@ class Timer:
 
     def run(self, fn, steps: int, warmup: int):
         lib, dev = self.dev._lib, self.dev
+        tw = time.perf_counter()
         for _ in range(warmup):
             fn(0)
         dev.sync()
+        while (time.perf_counter() - tw) * 1e3 < self.warm_ms:
+            for _ in range(max(1, warmup)):
+                fn(0)
+            dev.sync()
         t0 = time.perf_counter()
         dev.check(lib.bch_event_record(dev.ctx, self.e0), "event")
         for i in range(steps):
@@ -109,7 +123,7 @@ def bench_extra(dev, reps: int = 20, only=None):
     """The other BASELINE configs, each timed over `reps` launches."""
     from barracuda_amd import LcgStream, Tensor
     lib, ctx = dev._lib, dev.ctx
-    T = Timer(dev)
+    T = Timer(dev, warm_ms=40.0)
     out = {}
     want = set(only) if only else set(WORKLOADS) - {"copy"}
 
@@ -337,7 +351,7 @@ def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=30)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="only the headline GEMM")
     ap.add_argument("--only", default=None,
