@@ -47,7 +47,9 @@ def test_closed_forms(dev, golden):
     (1, 1, 1, 1, 1, False), (1, 1, 5, 5, 3, True), (2, 3, 7, 7, 8, False), (1, 2, 4, 9, 16, False),
     (1, 1, 33, 33, 32, True), (2, 2, 100, 100, 64, True), (1, 2, 128, 128, 128, False),
     (1, 2, 256, 256, 128, True), (1, 1, 130, 70, 128, False), (1, 1, 64, 300, 100, False),
-    (2, 1, 257, 257, 128, True)])
+    (2, 1, 257, 257, 128, True),
+    # grids that are a multiple of 8 take the XCD-contiguous head-major order (non-causal)
+    (2, 4, 256, 256, 64, False), (1, 8, 384, 384, 32, False), (1, 8, 384, 320, 128, False)])
 def test_shapes_vs_f64(dev, B, H, Sq, Skv, D, causal):
     _say(f"sdpa B={B} H={H} Sq={Sq} Skv={Skv} D={D} causal={causal}")
     rng = O.Lcg(B * 131 + H * 17 + Sq * 3 + Skv + D)
