@@ -269,6 +269,15 @@ def _bench_batched(dev, T, reps):
     out["batched_16x1024"] = {"TFLOP/s": fl / (ev * 1e-3) / 1e12, "ms": ev,
                               "mfma_frac": fl / (ev * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS,
                               "traffic": load_traffic("sgemm_batched_16x1024")}
+    del a, b, c
+    # config 1's shape on the GPU, beside its CPU-path time in extra.cpu.matmul_256
+    s0 = LcgStream(0, dev)
+    a, b = s0.uniform([256, 256]), s0.uniform([256, 256])
+    c = Tensor.empty([256, 256], dev)
+    pa, pb, pc = C.c_void_p(a.ptr), C.c_void_p(b.ptr), C.c_void_p(c.ptr)
+    wall, ev = T.run(lambda i: lib.bch_sgemm(ctx, 256, 256, 256, pa, 256, pb, 256, pc, 256), reps, 3)
+    out["matmul_256"] = {"us": ev * 1e3, "GFLOP/s": 2.0 * 256 ** 3 / (ev * 1e-3) / 1e9,
+                         "kernel": lib.bch_sgemm_kernel_name(256, 256, 256).decode()}
     return out
 
 
@@ -330,6 +339,17 @@ def cpu_baselines(target_s: float = 12.0, extra: bool = True):
                       f"i-j-p f32 fma, OpenMP over rows as rayon), {dt:.1f} s; rate extrapolates linearly"}
     ex = {}
     if extra:
+        # the 256^3 matmul on the reference's CPU path, whole
+        a2, b2 = O.Lcg(0).uniform((256, 256)), O.Lcg(0).uniform((256, 256))
+        O.matmul_cpu_exec_f32(a2, b2, 0, 256)
+        reps, t0 = 0, time.perf_counter()
+        while reps < 5 or time.perf_counter() - t0 < 0.5:
+            O.matmul_cpu_exec_f32(a2, b2, 0, 256)
+            reps += 1
+        dt = (time.perf_counter() - t0) / reps
+        ex["matmul_256"] = {"ms": dt * 1e3, "GFLOP/s": 2.0 * 256 ** 3 / dt / 1e9, "cores": threads, "kind": "port",
+                            "sample": f"whole 256^3 matmul (execute_matmul_cpu restated, OpenMP over rows), "
+                                      f"mean of {reps} calls; NagaExecutor not run: no Rust toolchain"}
         x = O.Lcg(1).normal((65536, 2048), 0.0, 3.0)
         t0 = time.perf_counter()
         O.softmax_dim_f32(x, 1, 0, 2048)
