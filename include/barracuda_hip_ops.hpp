@@ -95,7 +95,7 @@ struct BarracudaError {
   static BarracudaError unsupported(const std::string& op, const std::string& dev) {
     return {ErrorKind::UnsupportedOperation, "Operation not supported on device: " + op + " on " + dev};
   }
-  // bch_status -> variant (same table as INTEGRATION.md section 3)
+  // bch_status -> BarracudaError variant (error.rs:14-130)
   static BarracudaError from_status(bch_status st, const std::string& detail, const std::string& op) {
     switch (st) {
       case BCH_E_INVALID: return invalid_input(detail);
