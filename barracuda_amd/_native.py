@@ -22,6 +22,7 @@ BCH_E_MODULE = 5
 BCH_E_LAUNCH = 6
 BCH_E_DEVICE = 7
 BCH_E_UNSUPPORTED = 8
+BCH_E_DEVICE_LOST = 9
 BCH_ACT_NONE = 0
 BCH_ACT_RELU = 1
 
@@ -43,6 +44,7 @@ SIGNATURES = {
     "bch_device_count": (_i, [C.POINTER(_i)]),
     "bch_ctx_create": (_i, [_i, C.c_char_p, C.POINTER(_vp)]),
     "bch_ctx_destroy": (None, [_vp]),
+    "bch_ctx_is_lost": (_i, [_vp, C.POINTER(_i)]),
     "bch_last_error": (C.c_char_p, [_vp]),
     "bch_status_string": (C.c_char_p, [_i]),
     "bch_alloc": (_i, [_vp, _sz, C.POINTER(_vp)]),

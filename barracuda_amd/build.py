@@ -106,10 +106,52 @@ def build_oracle(verbose: bool = True) -> Path:
     return so
 
 
+SAN = LIB / "sanitize"
+# Host-code sanitizers for the C ABI's runtime: every flag applies to the
+# host pass only (each -fsanitize= right after -Xarch_host); device code is
+# built exactly as in build_hip.
+HOST_SAN = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
+            "-Xarch_host", "-fno-sanitize-recover=undefined", "-Xarch_host", "-fno-omit-frame-pointer"]
+CLANGXX = "/opt/rocm/llvm/bin/clang++"
+
+
+def build_sanitized(verbose: bool = True) -> Path:
+    """AddressSanitizer + UndefinedBehaviorSanitizer builds of the host code,
+    run on the CPU by tests/test_sanitizers.py:
+      oracle/_asan/libbc_oracle.so              (gcc; `make -C oracle asan`)
+      barracuda_amd/lib/sanitize/libbarracuda_hip.so   (bch_runtime.hip's host
+          pass sanitized, linked against the clang ASan runtime; the kernels'
+          objects are build_hip's)
+      barracuda_amd/lib/sanitize/bch_host_tests (tests/cpp/test_ops.cpp,
+          clang++, same runtime)
+    Needs build_hip's objects."""
+    _run(["make", "-s", "-C", str(ROOT / "oracle"), "asan"])
+    SAN.mkdir(parents=True, exist_ok=True)
+    rt = SAN / "bch_runtime.o"
+    _run([HIPCC, f"--offload-arch={ARCH}", "-O1", "-g", "-std=c++17", "-fPIC",
+          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", *HOST_SAN,
+          "-c", str(CSRC / "bch_runtime.hip"), "-o", str(rt)])
+    objs = [str(OBJ / (Path(s).stem + ".o")) for s in SOURCES if s != "bch_runtime.hip"]
+    so = SAN / "libbarracuda_hip.so"
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-shared-libasan", *HOST_SAN[:4],
+          "-o", str(so), str(rt), *objs, "-Wl,-rpath,/opt/rocm/lib", "-ldl"])
+    asan_rt = subprocess.run([CLANGXX, "-print-file-name=libclang_rt.asan-x86_64.so"], capture_output=True,
+                             text=True).stdout.strip()
+    exe = SAN / "bch_host_tests"
+    _run([CLANGXX, "-std=c++17", "-O1", "-g", "-fno-omit-frame-pointer", "-fsanitize=address,undefined",
+          "-fno-sanitize-recover=undefined", "-shared-libasan", f"-I{ROOT / 'include'}",
+          str(ROOT / "tests" / "cpp" / "test_ops.cpp"), f"-L{SAN}", "-lbarracuda_hip",
+          f"-Wl,-rpath,{SAN}", f"-Wl,-rpath,{Path(asan_rt).parent}", "-o", str(exe)])
+    if verbose:
+        print(f"built sanitized host builds under {SAN.relative_to(ROOT)} and oracle/_asan")
+    return SAN
+
+
 def build_all(verbose: bool = True) -> None:
     build_oracle(verbose)
     build_hip(verbose)
     build_host_tests(verbose)
+    build_sanitized(verbose)
 
 
 if __name__ == "__main__":

@@ -32,6 +32,18 @@ struct bch_ctx {
   std::map<std::string, hipModule_t> modules;
   void* ws = nullptr;
   size_t ws_bytes = 0;
+  // Sticky: set by the first HIP error that leaves the device context
+  // unusable (a kernel fault, an ECC error); every later call that would
+  // touch the device fails with BCH_E_DEVICE_LOST.  The reference flags its
+  // device the same way (device/wgpu_device/submission.rs:23-71, lost.store)
+  // and GpuBackend::is_lost reports it (device/backend.rs:256).
+  bool lost = false;
+  std::string lost_reason;
+  // Host-side fault injection (BARRACUDA_HIP_INJECT_HIP_ERROR, read once at
+  // bch_ctx_create): the next device call reports this HIP error as if the
+  // runtime had returned it, so the error translation and the lost flag can
+  // be tested without making the GPU fault.
+  int inject_hip_error = 0;
 };
 
 struct bch_event {
@@ -54,8 +66,35 @@ bch_status fail(bch_ctx* ctx, bch_status st, const char* fmt, ...) {
   return st;
 }
 
+// HIP errors after which the context cannot run further work: the device
+// raised an exception while executing a kernel (memory fault, trap, assert,
+// watchdog), an uncorrectable ECC error, or the context is gone.  HIP keeps
+// reporting them on every later call; the reference's equivalent is a wgpu
+// device-lost panic.
+bool context_fatal(hipError_t e) {
+  switch (e) {
+    case hipErrorIllegalAddress:
+    case hipErrorLaunchFailure:
+    case hipErrorAssert:
+    case hipErrorLaunchTimeOut:
+    case hipErrorECCNotCorrectable:
+    case hipErrorContextIsDestroyed:
+      return true;
+    default:
+      return false;
+  }
+}
+
 bch_status from_hip(bch_ctx* ctx, hipError_t e, const char* what) {
   if (e == hipSuccess) return BCH_OK;
+  if (context_fatal(e)) {
+    bch_status st = fail(ctx, BCH_E_DEVICE_LOST, "%s: %s (%d)", what, hipGetErrorString(e), (int)e);
+    if (ctx && !ctx->lost) {
+      ctx->lost = true;
+      ctx->lost_reason = ctx->last_error;
+    }
+    return st;
+  }
   bch_status st = BCH_E_DEVICE;
   if (e == hipErrorOutOfMemory) st = BCH_E_OOM;
   else if (e == hipErrorNoDevice || e == hipErrorInvalidDevice) st = BCH_E_NO_DEVICE;
@@ -63,13 +102,19 @@ bch_status from_hip(bch_ctx* ctx, hipError_t e, const char* what) {
            e == hipErrorNotFound || e == hipErrorSharedObjectInitFailed ||
            e == hipErrorNoBinaryForGpu || e == hipErrorFileNotFound)
     st = BCH_E_MODULE;
-  else if (e == hipErrorLaunchFailure || e == hipErrorLaunchOutOfResources ||
-           e == hipErrorInvalidConfiguration)
+  else if (e == hipErrorLaunchOutOfResources || e == hipErrorInvalidConfiguration)
     st = BCH_E_LAUNCH;
   return fail(ctx, st, "%s: %s (%d)", what, hipGetErrorString(e), (int)e);
 }
 
+// Every call that touches the device starts here.
 bch_status use(bch_ctx* ctx) {
+  if (ctx->lost) return fail(ctx, BCH_E_DEVICE_LOST, "device lost: %s", ctx->lost_reason.c_str());
+  if (ctx->inject_hip_error) {
+    const hipError_t e = static_cast<hipError_t>(ctx->inject_hip_error);
+    ctx->inject_hip_error = 0;
+    return from_hip(ctx, e, "injected by BARRACUDA_HIP_INJECT_HIP_ERROR");
+  }
   hipError_t e = hipSetDevice(ctx->device);
   return from_hip(ctx, e, "hipSetDevice");
 }
@@ -126,6 +171,7 @@ const char* bch_status_string(bch_status s) {
     case BCH_E_LAUNCH: return "kernel launch failed";
     case BCH_E_DEVICE: return "device error";
     case BCH_E_UNSUPPORTED: return "unsupported operation";
+    case BCH_E_DEVICE_LOST: return "device lost";
     default: return "unknown status";
   }
 }
@@ -163,6 +209,7 @@ bch_status bch_ctx_create(int device, const char* code_object_dir, bch_ctx** out
     return fail(nullptr, BCH_E_NO_DEVICE, "bch_ctx_create: device %d not present (%d visible)", device, n);
   bch_ctx* ctx = new bch_ctx();
   ctx->device = device;
+  if (const char* inj = getenv("BARRACUDA_HIP_INJECT_HIP_ERROR")) ctx->inject_hip_error = atoi(inj);
   ctx->co_dir = code_object_dir ? code_object_dir : lib_dir();
   hipError_t e = hipSetDevice(device);
   if (e == hipSuccess) e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
@@ -172,6 +219,12 @@ bch_status bch_ctx_create(int device, const char* code_object_dir, bch_ctx** out
     return st;
   }
   *out = ctx;
+  return BCH_OK;
+}
+
+bch_status bch_ctx_is_lost(const bch_ctx* ctx, int* lost) {
+  if (!ctx || !lost) return fail(nullptr, BCH_E_INVALID, "bch_ctx_is_lost: NULL argument");
+  *lost = ctx->lost ? 1 : 0;
   return BCH_OK;
 }
 
@@ -348,8 +401,13 @@ bch_status bch_dgemm(bch_ctx* ctx, int transa, int transb, int batch, int m, int
   if (lda < (ar > 1 ? ar : 1) || ldb < (br > 1 ? br : 1) || ldc < (n > 1 ? n : 1))
     return fail(ctx, BCH_E_SHAPE, "gemm_f64: leading dimension too small (lda=%d needs %d, ldb=%d needs %d, "
                 "ldc=%d needs %d)", lda, ar, ldb, br, ldc, n);
-  const long long asz = (long long)(transa ? k : m) * lda, bsz = (long long)(transb ? n : k) * ldb;
-  if (batch > 1 && (strideA < asz || strideB < bsz || strideC < (long long)m * ldc))
+  // Extent of one stored matrix: (rows - 1) * ld + row length, 0 when empty
+  // (k == 0 leaves A and B empty whatever lda and ldb are).
+  auto extent = [](long long rows, long long cols, long long ld) {
+    return rows > 0 && cols > 0 ? (rows - 1) * ld + cols : 0LL;
+  };
+  const long long asz = extent(transa ? k : m, ar, lda), bsz = extent(transb ? n : k, br, ldb);
+  if (batch > 1 && (strideA < asz || strideB < bsz || strideC < extent(m, n, ldc)))
     return fail(ctx, BCH_E_SHAPE, "gemm_f64: batch stride smaller than one matrix (sA=%lld, sB=%lld, sC=%lld)",
                 strideA, strideB, strideC);
   if (!ctx) return fail(ctx, BCH_E_INVALID, "gemm_f64: ctx is NULL");

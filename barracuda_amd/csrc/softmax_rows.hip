@@ -55,7 +55,7 @@ using bch::wave_allreduce;
 // One wavefront per row, NV float4 per lane (cols <= 256 * NV, cols % 4 == 0).
 template <int NV>
 __device__ __forceinline__ void softmax_rows_wave_body(
-    const float* __restrict__ in, float* __restrict__ out, long long rows,
+    const float* in, float* out, long long rows,
     int cols) {
   const int lane = threadIdx.x & 63;
   const long long row = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -101,7 +101,7 @@ __device__ __forceinline__ void softmax_rows_wave_body(
 
 template <int NV>
 __global__ __launch_bounds__(256) void softmax_rows_wave(
-    const float* __restrict__ in, float* __restrict__ out, long long rows,
+    const float* in, float* out, long long rows,
     int cols) {
   softmax_rows_wave_body<NV>(in, out, rows, cols);
 }
@@ -146,7 +146,7 @@ __device__ __forceinline__ void block_merge(float& m, float& s) {
 
 // One workgroup (256 threads) per row, any cols.
 __global__ __launch_bounds__(256) void softmax_rows_block(
-    const float* __restrict__ in, float* __restrict__ out, long long rows,
+    const float* in, float* out, long long rows,
     long long cols) {
   const long long row = blockIdx.x;
   const float* x = in + row * cols;
@@ -212,7 +212,7 @@ __global__ __launch_bounds__(256) void softmax_split_stats(
 // r and writes chunk c.  VEC as in pass 1, plus a 16-byte aligned output.
 template <bool VEC>
 __global__ __launch_bounds__(256) void softmax_split_write(
-    const float* __restrict__ in, float* __restrict__ out, long long cols,
+    const float* in, float* out, long long cols,
     long long chunk, const float* __restrict__ part) {
   const long long r = blockIdx.y;
   const float* pr = part + 2 * r * gridDim.x;
@@ -247,7 +247,7 @@ __global__ __launch_bounds__(256) void softmax_split_write(
 
 // Softmax along the middle axis of [outer, axis, inner], thread per slice.
 __global__ __launch_bounds__(256) void softmax_axis_strided(
-    const float* __restrict__ in, float* __restrict__ out, long long outer,
+    const float* in, float* out, long long outer,
     long long axis, long long inner) {
   const long long t = (long long)blockIdx.x * 256 + threadIdx.x;
   if (t >= outer * inner) return;
@@ -390,6 +390,6 @@ hipError_t launch_softmax_axis(hipStream_t s, long long outer, long long axis,
 // Unmangled entry for the code-object path (bch_launch_code_object): the
 // cols == 2048 register-resident row softmax, 4 rows per 256-thread block.
 extern "C" __global__ __launch_bounds__(256) void bch_softmax_rows_2048(
-    const float* __restrict__ in, float* __restrict__ out, long long rows) {
+    const float* in, float* out, long long rows) {
   softmax_rows_wave_body<8>(in, out, rows, 2048);
 }

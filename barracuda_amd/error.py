@@ -16,12 +16,20 @@ class DeviceError(BarracudaError):
         super().__init__(f"Device error: {msg}")
 
 
-class DeviceNotAvailable(DeviceError):
-    """No HIP device (error.rs:225 device_not_found maps to Device)."""
+class DeviceNotAvailable(BarracudaError):
+    """error.rs DeviceNotAvailable{device, reason} (:92-99): no HIP device, or
+    the requested ordinal is not present."""
+
+    def __init__(self, device: str, reason: str):
+        self.device = device
+        self.reason = reason
+        super().__init__(f"Device not available: {device} - {reason}")
 
 
 class DeviceLost(BarracudaError):
-    """error.rs DeviceLost(String) (:301)."""
+    """error.rs DeviceLost(String) (:52-59): the context can run no more work
+    (a kernel fault, an uncorrectable ECC error).  Retriable on a fresh
+    device, as the reference documents."""
 
     def __init__(self, msg: str):
         super().__init__(f"GPU device lost: {msg}")
@@ -102,7 +110,9 @@ def from_status(status: int, msg: str, op: str = "op", device: str = "hip"):
     if status == N.BCH_E_SHAPE:
         return InvalidOperation(op, f"shape/dimension mismatch: {msg}")
     if status == N.BCH_E_NO_DEVICE:
-        return DeviceNotAvailable(msg)
+        return DeviceNotAvailable(device, msg)
+    if status == N.BCH_E_DEVICE_LOST:
+        return DeviceLost(msg)
     if status == N.BCH_E_OOM:
         return OutOfMemory(msg)
     if status == N.BCH_E_LAUNCH:

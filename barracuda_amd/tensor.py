@@ -65,6 +65,15 @@ class HipDevice:
     def name(self) -> str:
         return "hip:gfx950"
 
+    def is_lost(self) -> bool:
+        """GpuBackend::is_lost (device/backend.rs:256): whether a call on this
+        context has reported a lost device (a kernel fault, an uncorrectable
+        ECC error).  Sticky: every later device call raises DeviceLost."""
+        flag = C.c_int(0)
+        with self._lock:
+            self.check(self._lib.bch_ctx_is_lost(self._ctx, C.byref(flag)), "is_lost")
+        return bool(flag.value)
+
     def check(self, status: int, op: str) -> None:
         if status != N.BCH_OK:
             raise from_status(status, N.last_error(self._ctx), op, self.name())

@@ -35,6 +35,9 @@ HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, published
 FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense FP32 matrix, published
 FP64_MFMA_PEAK_TFLOPS = 78.6   # MI355X dense FP64 matrix, published
 PROFILES = ROOT / "profiles"
+# Untimed launches before every timed region continue until this much wall
+# time has passed since the first warmup launch (the clock settle).
+SETTLE_MS = 60.0
 
 
 def log(msg: str) -> None:
@@ -110,7 +113,10 @@ def bench_gemm(dev, steps, warmup):
         if st:
             dev.check(st, "sgemm")
 
-    wall_ms, ev_ms = Timer(dev).run(step, steps, warmup)
+    # The same clock settle as every other workload: from idle, the clocks
+    # take ~25 ms of full load to reach steady state, so W warmup launches
+    # alone (the driver passes W = 5) would time the ramp.
+    wall_ms, ev_ms = Timer(dev, warm_ms=SETTLE_MS).run(step, steps, warmup)
     flops = 2.0 * n ** 3
     return {"wall_ms": wall_ms, "kernel_ms": ev_ms, "flops": flops,
             "kernel": lib.bch_sgemm_kernel_name(n, n, n).decode()}, (a, b, c)
@@ -123,7 +129,7 @@ def bench_extra(dev, reps: int = 20, only=None):
     """The other BASELINE configs, each timed over `reps` launches."""
     from barracuda_amd import LcgStream, Tensor
     lib, ctx = dev._lib, dev.ctx
-    T = Timer(dev, warm_ms=40.0)
+    T = Timer(dev, warm_ms=SETTLE_MS)
     out = {}
     want = set(only) if only else set(WORKLOADS) - {"copy"}
 
@@ -318,9 +324,36 @@ def _bench_sdpa(dev, T, reps):
     return out
 
 
+def host_cpu() -> dict:
+    """What the CPU baselines ran on: the model name from /proc/cpuinfo (what
+    lscpu prints as "Model name") and the logical CPU count."""
+    model = "unknown"
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"cpu_model": model, "nproc": os.cpu_count()}
+
+
+def _timed(fn, min_s: float = 0.0, min_reps: int = 1):
+    """Mean seconds per call of fn() over at least min_reps calls and min_s."""
+    reps, t0 = 0, time.perf_counter()
+    while reps < min_reps or time.perf_counter() - t0 < min_s:
+        fn()
+        reps += 1
+    return (time.perf_counter() - t0) / reps, reps
+
+
 def cpu_baselines(target_s: float = 12.0, extra: bool = True):
-    """The reference's CPU paths, restated in oracle/, on this host's cores."""
+    """The reference's CPU paths, restated in oracle/, on this host's cores:
+    one entry per BASELINE config (configs 3a/3b/4 on execute_matmul_cpu,
+    cpu_executor/executor.rs:241-260, with all cores as rayon uses them;
+    softmax_dim and both attention paths serial, as in the reference)."""
     from oracle import bc_oracle as O
+    host = host_cpu()
     threads = O.num_threads()
     n = 4096
     rng = O.Lcg(2)
@@ -334,36 +367,78 @@ def cpu_baselines(target_s: float = 12.0, extra: bool = True):
     O.matmul_cpu_exec_f32(a, b, 0, rows)
     dt = time.perf_counter() - t0
     gemm = {"value": 2.0 * rows * n * n / dt / 1e12, "unit": "TFLOP/s", "cores": threads,
-            "kind": "port",
+            "kind": "port", **host,
             "sample": f"rows 0..{rows} of the 4096^3 GEMM (execute_matmul_cpu restated: "
                       f"i-j-p f32 fma, OpenMP over rows as rayon), {dt:.1f} s; rate extrapolates linearly"}
+    del a, b
     ex = {}
-    if extra:
-        # the 256^3 matmul on the reference's CPU path, whole
-        a2, b2 = O.Lcg(0).uniform((256, 256)), O.Lcg(0).uniform((256, 256))
-        O.matmul_cpu_exec_f32(a2, b2, 0, 256)
-        reps, t0 = 0, time.perf_counter()
-        while reps < 5 or time.perf_counter() - t0 < 0.5:
-            O.matmul_cpu_exec_f32(a2, b2, 0, 256)
-            reps += 1
-        dt = (time.perf_counter() - t0) / reps
-        ex["matmul_256"] = {"ms": dt * 1e3, "GFLOP/s": 2.0 * 256 ** 3 / dt / 1e9, "cores": threads, "kind": "port",
-                            "sample": f"whole 256^3 matmul (execute_matmul_cpu restated, OpenMP over rows), "
-                                      f"mean of {reps} calls; NagaExecutor not run: no Rust toolchain"}
-        x = O.Lcg(1).normal((65536, 2048), 0.0, 3.0)
+    if not extra:
+        return gemm, ex
+    # config 1: the 256^3 matmul on the reference's CPU path, whole
+    a2, b2 = O.Lcg(0).uniform((256, 256)), O.Lcg(0).uniform((256, 256))
+    O.matmul_cpu_exec_f32(a2, b2, 0, 256)
+    dt, reps = _timed(lambda: O.matmul_cpu_exec_f32(a2, b2, 0, 256), 0.5, 5)
+    ex["matmul_256"] = {"ms": dt * 1e3, "GFLOP/s": 2.0 * 256 ** 3 / dt / 1e9, "cores": threads, "kind": "port",
+                        **host, "sample": f"whole 256^3 matmul (execute_matmul_cpu restated, OpenMP over rows), "
+                                          f"mean of {reps} calls; NagaExecutor not run: no Rust toolchain"}
+    # config 2: softmax_dim, serial (tensor_axis_ops.rs:67-126 runs on the host thread)
+    x = O.Lcg(1).normal((65536, 2048), 0.0, 3.0)
+    t0 = time.perf_counter()
+    O.softmax_dim_f32(x, 1, 0, 2048)
+    dt = time.perf_counter() - t0
+    ex["softmax_dim"] = {"GB/s": 2 * 4 * 2048 * 2048 / dt / 1e9, "cores": 1, "kind": "port", **host,
+                         "us_full_config_extrapolated": dt * 32 * 1e6,
+                         "sample": "rows 0..2048 of 65536x2048 (tensor_axis_ops.rs softmax_dim, serial), "
+                                   "x32 extrapolated"}
+    del x
+    # config 3b: batched 16 x 1024^3, execute_matmul_cpu per batch on a row sample of every batch
+    s2 = O.Lcg(2)
+    ab, bb = s2.uniform((16, 1024, 1024)), s2.uniform((16, 1024, 1024))
+    rb = threads  # rows per batch in the sample: one per thread
+    t0 = time.perf_counter()
+    for i in range(16):
+        O.matmul_cpu_exec_f32(ab[i], bb[i], 0, rb)
+    dt = time.perf_counter() - t0
+    fl = 2.0 * 16 * rb * 1024 * 1024
+    ex["batched_16x1024"] = {"TFLOP/s": fl / dt / 1e12, "ms_full_config_extrapolated": dt * 1024 / rb * 1e3,
+                             "cores": threads, "kind": "port", **host,
+                             "sample": f"rows 0..{rb} of each of the 16 batches (execute_matmul_cpu restated, "
+                                       f"OpenMP over rows), {dt:.2f} s; x{1024 // rb} extrapolated"}
+    del ab, bb
+    # config 4: skinny M in {1, 8, 32} x K 4096 x N 11008, whole op (rayon over M rows:
+    # at M = 1 only one core has work, as in the reference)
+    K, N = 4096, 11008
+    for m in (1, 8, 32):
+        s3 = O.Lcg(3)
+        xs, w = s3.normal((m, K)), s3.normal((K, N), 0.0, 0.02)
+        dt, reps = _timed(lambda: O.matmul_cpu_exec_f32(xs, w), 0.3, 2)
+        nbytes = 4 * (K * N + m * K + m * N)
+        ex[f"skinny_m{m}"] = {"us": dt * 1e6, "GB/s": nbytes / dt / 1e9, "GFLOP/s": 2.0 * m * K * N / dt / 1e9,
+                              "cores": min(threads, m), "kind": "port", **host,
+                              "sample": f"whole op, mean of {reps} calls (execute_matmul_cpu restated, "
+                                        f"OpenMP over the {m} rows)"}
+        del xs, w
+    # config 5: one (b,h) head of S=2048, D=128 on each attention path, serial, x128
+    s4 = O.Lcg(4)
+    shape = (1, 1, 2048, 128)
+    q, k, v = s4.normal(shape), s4.normal(shape), s4.normal(shape)
+    t0 = time.perf_counter()
+    O.causal_attention_cpu_f32(q, k, v)
+    dt = time.perf_counter() - t0
+    ex["causal_attention"] = {"ms_full_config_extrapolated": dt * 1e3 * 128, "cores": 1, "kind": "port", **host,
+                              "sample": "1 of 128 heads (causal_attention.rs:52-134, serial), x128 extrapolated"}
+    O.set_num_threads(1)
+    try:
         t0 = time.perf_counter()
-        O.softmax_dim_f32(x, 1, 0, 2048)
+        O.attention_3pass_f32(q, k, v, False)
         dt = time.perf_counter() - t0
-        ex["softmax_dim"] = {"GB/s": 2 * 4 * 2048 * 2048 / dt / 1e9, "cores": 1, "kind": "port",
-                             "sample": "rows 0..2048 of 65536x2048 (tensor_axis_ops.rs softmax_dim, serial)"}
-        s4 = O.Lcg(4)
-        shape = (1, 1, 2048, 128)
-        q, k, v = s4.normal(shape), s4.normal(shape), s4.normal(shape)
-        t0 = time.perf_counter()
-        O.causal_attention_cpu_f32(q, k, v)
-        dt = time.perf_counter() - t0
-        ex["causal_attention"] = {"ms_full_config_extrapolated": dt * 1e3 * 128, "cores": 1, "kind": "port",
-                                  "sample": "1 of 128 heads (causal_attention.rs, serial), x128 extrapolated"}
+    finally:
+        O.set_num_threads(threads)
+    ex["attention_noncausal"] = {"ms_full_config_extrapolated": dt * 1e3 * 128, "cores": 1, "kind": "port",
+                                 **host,
+                                 "sample": "1 of 128 heads, the three passes of Attention::execute (K6 scores / "
+                                           "sqrt(D), K7 row softmax, K9 P.V; ops/attention/compute.rs:21-111) "
+                                           "on the host, serial, x128 extrapolated"}
     return gemm, ex
 
 

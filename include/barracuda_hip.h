@@ -38,9 +38,15 @@ typedef int bch_status;
 #define BCH_E_NO_DEVICE   3 /* no HIP device               -> DeviceNotAvailable */
 #define BCH_E_OOM         4 /* device allocation failed    -> OutOfMemory */
 #define BCH_E_MODULE      5 /* code object missing/corrupt -> Device(String)   (error.rs:220) */
-#define BCH_E_LAUNCH      6 /* kernel launch failed        -> ExecutionError   (error.rs:230) */
-#define BCH_E_DEVICE      7 /* other HIP runtime failure   -> Device(String) / DeviceLost (error.rs:301) */
+#define BCH_E_LAUNCH      6 /* launch rejected (resources, configuration) -> ExecutionError (error.rs:230) */
+#define BCH_E_DEVICE      7 /* other HIP runtime failure   -> Device(String)   (error.rs:220) */
 #define BCH_E_UNSUPPORTED 8 /* op/entry not provided       -> UnsupportedOperation */
+#define BCH_E_DEVICE_LOST 9 /* the context can run no more work: a kernel
+                             * faulted (memory fault, trap, assert, watchdog),
+                             * an uncorrectable ECC error, or the context is
+                             * gone.  Sticky: every later call on the context
+                             * that touches the device returns it too.
+                             *                             -> DeviceLost(String) (error.rs:59) */
 
 typedef struct bch_ctx bch_ctx;
 typedef struct bch_event bch_event;
@@ -57,6 +63,16 @@ bch_status bch_device_count(int *count);
  * BARRACUDA_HIP_DEVICE overrides device when device < 0. */
 bch_status bch_ctx_create(int device, const char *code_object_dir, bch_ctx **out);
 void bch_ctx_destroy(bch_ctx *ctx);
+
+/* *lost = 1 once a call on ctx has returned BCH_E_DEVICE_LOST, else 0.
+ * Replaces GpuBackend::is_lost (device/backend.rs:256), which reads the flag
+ * that WgpuDevice::poll_safe sets on a device-lost panic
+ * (device/wgpu_device/submission.rs:23-71).  The caller recovers with a fresh
+ * context (the reference retries on a fresh device, error.rs:52-58).
+ * Env BARRACUDA_HIP_INJECT_HIP_ERROR=<hipError_t value>, read by
+ * bch_ctx_create, makes the context's first device call report that HIP
+ * error (fault injection for this mapping; no kernel runs). */
+bch_status bch_ctx_is_lost(const bch_ctx *ctx, int *lost);
 
 /* Message of the last failed call on ctx; with ctx == NULL, the calling
  * thread's last failure.  Never NULL ("" when none). */

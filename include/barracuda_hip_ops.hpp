@@ -59,6 +59,7 @@ enum class ErrorKind {
   ExecutionError,        // ExecutionError{message}
   UnsupportedOperation,  // UnsupportedOperation{op, device}
   DeviceLost,            // DeviceLost(String)
+  DeviceNotAvailable,    // DeviceNotAvailable{device, reason}
   InvalidShape,          // InvalidShape{expected, actual}
   CastOverflow,          // CastOverflow{from_type, to_type, value_description}
 };
@@ -95,15 +96,23 @@ struct BarracudaError {
   static BarracudaError unsupported(const std::string& op, const std::string& dev) {
     return {ErrorKind::UnsupportedOperation, "Operation not supported on device: " + op + " on " + dev};
   }
+  static BarracudaError device_lost(const std::string& msg) {
+    return {ErrorKind::DeviceLost, "GPU device lost: " + msg};
+  }
+  static BarracudaError device_not_available(const std::string& dev, const std::string& reason) {
+    return {ErrorKind::DeviceNotAvailable, "Device not available: " + dev + " - " + reason};
+  }
   // bch_status -> BarracudaError variant (error.rs:14-130)
   static BarracudaError from_status(bch_status st, const std::string& detail, const std::string& op) {
     switch (st) {
       case BCH_E_INVALID: return invalid_input(detail);
       case BCH_E_SHAPE: return invalid_op(op, "shape/dimension mismatch: " + detail);
+      case BCH_E_NO_DEVICE: return device_not_available("hip", detail);
       case BCH_E_OOM: return {ErrorKind::OutOfMemory, "Out of memory: " + detail};
       case BCH_E_LAUNCH: return {ErrorKind::ExecutionError, "Execution error: " + detail};
       case BCH_E_UNSUPPORTED: return unsupported(op, "hip:gfx950 (" + detail + ")");
-      default: return device(detail);
+      case BCH_E_DEVICE_LOST: return device_lost(detail);
+      default: return device(detail);  // BCH_E_MODULE, BCH_E_DEVICE
     }
   }
 };
@@ -147,6 +156,11 @@ class HipDevice {
   HipDevice& operator=(const HipDevice&) = delete;
 
   std::string name() const { return "hip:gfx950"; }
+  // GpuBackend::is_lost (device/backend.rs:256)
+  bool is_lost() const {
+    int lost = 0;
+    return bch_ctx_is_lost(ctx_, &lost) == BCH_OK && lost != 0;
+  }
   bch_ctx* ctx() const { return ctx_; }
   std::mutex& mutex() { return mu_; }
   std::optional<BarracudaError> check(bch_status st, const std::string& op) const {

@@ -197,6 +197,33 @@ BCO_API void bco_softmax_rows_f64(long rows, long cols, const float *x, double *
  * from Skv) and ops/causal_attention.rs:52-134 (causal, Sq == Skv).
  * heads_sel (nullable) restricts the (b*H + h) heads computed; O then holds
  * n_sel heads of [Sq, D] each, in that order.  Parallel over (head, row). */
+/* One query row i of head bh: o_i = sum_j softmax_j(scale q_i.k_j) v_j over
+ * j < Skv (j <= i when causal), all in double.  p: Skv doubles of scratch. */
+static void sdpa_row_f64(int Sq, int Skv, int D, double scale, int causal,
+                         const float *q, const float *k, const float *v,
+                         int bh, int i, double *oi, double *p)
+{
+    const float *qi = q + ((long)bh * Sq + i) * D;
+    const float *kh = k + (long)bh * Skv * D;
+    const float *vh = v + (long)bh * Skv * D;
+    int jend = causal ? (i + 1 < Skv ? i + 1 : Skv) : Skv;
+    double mx = -INFINITY;
+    for (int j = 0; j < jend; ++j) {
+        double s = 0.0;
+        for (int d = 0; d < D; ++d) s += (double)qi[d] * (double)kh[(long)j * D + d];
+        p[j] = s * scale;
+        if (p[j] > mx) mx = p[j];
+    }
+    double sum = 0.0;
+    for (int j = 0; j < jend; ++j) { p[j] = exp(p[j] - mx); sum += p[j]; }
+    for (int d = 0; d < D; ++d) oi[d] = 0.0;
+    for (int j = 0; j < jend; ++j) {
+        double w = p[j] / sum;
+        const float *vj = vh + (long)j * D;
+        for (int d = 0; d < D; ++d) oi[d] += w * (double)vj[d];
+    }
+}
+
 BCO_API void bco_sdpa_f64(int B, int H, int Sq, int Skv, int D, double scale,
                           int causal, const float *q, const float *k,
                           const float *v, double *o, const int *heads_sel,
@@ -210,26 +237,31 @@ BCO_API void bco_sdpa_f64(int B, int H, int Sq, int Skv, int D, double scale,
         for (int hh = 0; hh < nheads; ++hh) {
             for (int i = 0; i < Sq; ++i) {
                 int bh = heads_sel ? heads_sel[hh] : hh;
-                const float *qi = q + ((long)bh * Sq + i) * D;
-                const float *kh = k + (long)bh * Skv * D;
-                const float *vh = v + (long)bh * Skv * D;
-                double *oi = o + ((long)hh * Sq + i) * D;
-                int jend = causal ? (i + 1 < Skv ? i + 1 : Skv) : Skv;
-                double mx = -INFINITY;
-                for (int j = 0; j < jend; ++j) {
-                    double s = 0.0;
-                    for (int d = 0; d < D; ++d) s += (double)qi[d] * (double)kh[(long)j * D + d];
-                    p[j] = s * scale;
-                    if (p[j] > mx) mx = p[j];
-                }
-                double sum = 0.0;
-                for (int j = 0; j < jend; ++j) { p[j] = exp(p[j] - mx); sum += p[j]; }
-                for (int d = 0; d < D; ++d) oi[d] = 0.0;
-                for (int j = 0; j < jend; ++j) {
-                    double w = p[j] / sum;
-                    const float *vj = vh + (long)j * D;
-                    for (int d = 0; d < D; ++d) oi[d] += w * (double)vj[d];
-                }
+                sdpa_row_f64(Sq, Skv, D, scale, causal, q, k, v, bh, i,
+                             o + ((long)hh * Sq + i) * D, p);
+            }
+        }
+        free(p);
+    }
+}
+
+/* The same oracle on a row sample of every head: rows[bh * n_rows + r] is
+ * the r-th query row taken from head bh (of all B*H), written to
+ * o[(bh * n_rows + r) * D ..]. */
+BCO_API void bco_sdpa_f64_rows(int B, int H, int Sq, int Skv, int D,
+                               double scale, int causal, const float *q,
+                               const float *k, const float *v, double *o,
+                               const int *rows, int n_rows)
+{
+    int nheads = B * H;
+    #pragma omp parallel
+    {
+        double *p = (double *)malloc(sizeof(double) * (size_t)Skv);
+        #pragma omp for schedule(dynamic, 4) collapse(2)
+        for (int bh = 0; bh < nheads; ++bh) {
+            for (int r = 0; r < n_rows; ++r) {
+                long idx = (long)bh * n_rows + r;
+                sdpa_row_f64(Sq, Skv, D, scale, causal, q, k, v, bh, rows[idx], o + idx * D, p);
             }
         }
         free(p);
@@ -551,5 +583,16 @@ BCO_API int bco_num_threads(void)
     return omp_get_max_threads();
 #else
     return 1;
+#endif
+}
+
+/* Thread count of the OpenMP loops above (the CPU baselines time the
+ * reference's serial paths with 1 and its rayon paths with all cores). */
+BCO_API void bco_set_num_threads(int n)
+{
+#ifdef _OPENMP
+    if (n > 0) omp_set_num_threads(n);
+#else
+    (void)n;
 #endif
 }

@@ -9,12 +9,13 @@ from __future__ import annotations
 
 import ctypes as C
 import math
+import os
 from pathlib import Path
 
 import numpy as np
 
 HERE = Path(__file__).resolve().parent
-LIB_PATH = HERE / "libbc_oracle.so"
+LIB_PATH = Path(os.environ.get("BC_ORACLE_LIB", HERE / "libbc_oracle.so"))
 
 _lib = None
 _fp = C.POINTER(C.c_float)
@@ -37,6 +38,7 @@ def lib() -> C.CDLL:
                                      C.c_long, _ip, C.c_int]
         L.bco_softmax_rows_f64.argtypes = [C.c_long, C.c_long, _fp, _dp]
         L.bco_sdpa_f64.argtypes = [C.c_int] * 5 + [C.c_double, C.c_int, _fp, _fp, _fp, _dp, _ip, C.c_int]
+        L.bco_sdpa_f64_rows.argtypes = [C.c_int] * 5 + [C.c_double, C.c_int, _fp, _fp, _fp, _dp, _ip, C.c_int]
         L.bco_matmul_cpu_exec_f32.argtypes = [C.c_int, C.c_int, C.c_int, _fp, _fp, _fp, C.c_int, C.c_int]
         L.bco_matmul_k1_f32.argtypes = [C.c_int, C.c_int, C.c_int, _fp, _fp, _fp]
         L.bco_batch_matmul_seq_f32.argtypes = [C.c_int, C.c_int, C.c_int, C.c_int, _fp, _fp, _fp]
@@ -51,6 +53,7 @@ def lib() -> C.CDLL:
         L.bco_max_rel_err_f32ref.restype = C.c_double
         L.bco_max_rel_err_f32ref.argtypes = [C.c_size_t, _fp, _fp]
         L.bco_num_threads.restype = C.c_int
+        L.bco_set_num_threads.argtypes = [C.c_int]
         _lib = L
     return _lib
 
@@ -121,6 +124,21 @@ def sdpa_f64(q, k, v, causal: bool, scale: float | None = None, heads=None) -> n
     sp, ns, keep = _sel(heads)
     o = np.empty((ns, Sq, D) if heads is not None else (B, H, Sq, D), dtype=np.float64)
     lib().bco_sdpa_f64(B, H, Sq, Skv, D, scale, int(causal), _f(q), _f(k), _f(v), _d(o), sp, ns)
+    return o
+
+
+def sdpa_f64_rows(q, k, v, causal: bool, rows, scale: float | None = None) -> np.ndarray:
+    """sdpa_f64 on a row sample of every head: rows is [B*H, n] query-row
+    indices (per head); returns [B*H, n, D] float64."""
+    B, H, Sq, D = q.shape
+    Skv = k.shape[2]
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    r = np.ascontiguousarray(np.asarray(rows, dtype=np.int32))
+    assert r.ndim == 2 and r.shape[0] == B * H and r.min() >= 0 and r.max() < Sq
+    o = np.empty((B * H, r.shape[1], D), dtype=np.float64)
+    lib().bco_sdpa_f64_rows(B, H, Sq, Skv, D, scale, int(causal), _f(q), _f(k), _f(v), _d(o),
+                            r.ctypes.data_as(_ip), r.shape[1])
     return o
 
 
@@ -298,3 +316,8 @@ def max_rel_err(x: np.ndarray, ref: np.ndarray) -> float:
 
 def num_threads() -> int:
     return int(lib().bco_num_threads())
+
+
+def set_num_threads(n: int) -> None:
+    """Threads of the OpenMP loops from now on (n >= 1)."""
+    lib().bco_set_num_threads(int(n))

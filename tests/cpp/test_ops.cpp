@@ -128,8 +128,19 @@ void cpu_tests() {
     REQUIRE(BarracudaError::from_status(BCH_E_OOM, "x", "op").kind == ErrorKind::OutOfMemory);
     REQUIRE(BarracudaError::from_status(BCH_E_SHAPE, "x", "matmul").kind == ErrorKind::InvalidOperation);
     REQUIRE(has_shape_words(BarracudaError::from_status(BCH_E_SHAPE, "x", "matmul").message));
-    REQUIRE(BarracudaError::from_status(BCH_E_NO_DEVICE, "x", "op").kind == ErrorKind::Device);
+    REQUIRE(BarracudaError::from_status(BCH_E_NO_DEVICE, "x", "op").kind == ErrorKind::DeviceNotAvailable);
+    REQUIRE(BarracudaError::from_status(BCH_E_NO_DEVICE, "no GPU", "op").message ==
+            "Device not available: hip - no GPU");  // error.rs:92-99 #[error] form
     REQUIRE(BarracudaError::from_status(BCH_E_UNSUPPORTED, "x", "op").kind == ErrorKind::UnsupportedOperation);
+    REQUIRE(BarracudaError::from_status(BCH_E_LAUNCH, "x", "op").kind == ErrorKind::ExecutionError);
+    REQUIRE(BarracudaError::from_status(BCH_E_INVALID, "x", "op").kind == ErrorKind::InvalidInput);
+    REQUIRE(BarracudaError::from_status(BCH_E_MODULE, "x", "op").kind == ErrorKind::Device);
+    REQUIRE(BarracudaError::from_status(BCH_E_DEVICE, "x", "op").kind == ErrorKind::Device);
+    const auto lost = BarracudaError::from_status(BCH_E_DEVICE_LOST, "fault", "op");
+    REQUIRE(lost.kind == ErrorKind::DeviceLost && lost.message == "GPU device lost: fault");  // error.rs:59
+    REQUIRE(std::string(bch_status_string(BCH_E_DEVICE_LOST)) == "device lost");
+    int flag = 7;
+    REQUIRE(bch_ctx_is_lost(nullptr, &flag) == BCH_E_INVALID);
   });
   run("attention_dims_and_session_errors", [] {  // session/mod.rs:78-98, error.rs:436-445
     AttentionDims d{4, 32, 2048, 128};
@@ -462,7 +473,7 @@ int main(int argc, char** argv) {
     // without a GPU the device constructor returns Err(Device), never aborts
     run("no_device_is_an_error_value", [&] {
       if (dr.is_ok()) return;  // a GPU is present: nothing to check here
-      REQUIRE(dr.error().kind == ErrorKind::Device);
+      REQUIRE(dr.error().kind == ErrorKind::DeviceNotAvailable);
       REQUIRE(dr.error().message.find("no HIP device") != std::string::npos);
     });
   } else {

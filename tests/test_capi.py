@@ -103,7 +103,24 @@ def test_status_to_error_variant_mapping():
     assert "mismatch" in str(from_status(N.BCH_E_SHAPE, "x", "matmul"))
     assert isinstance(from_status(N.BCH_E_OOM, "x"), OutOfMemory)
     assert isinstance(from_status(N.BCH_E_NO_DEVICE, "x"), DeviceNotAvailable)
+    assert str(from_status(N.BCH_E_NO_DEVICE, "no GPU", device="hip")) == "Device not available: hip - no GPU"
     assert isinstance(from_status(N.BCH_E_UNSUPPORTED, "x"), UnsupportedOperation)
+    from barracuda_amd.error import DeviceError, DeviceLost, ExecutionError, InvalidInput
+    assert isinstance(from_status(N.BCH_E_LAUNCH, "x"), ExecutionError)
+    assert isinstance(from_status(N.BCH_E_INVALID, "x"), InvalidInput)
+    for st in (N.BCH_E_MODULE, N.BCH_E_DEVICE):
+        e = from_status(st, "x")
+        assert isinstance(e, DeviceError) and not isinstance(e, DeviceLost)
+    lost = from_status(N.BCH_E_DEVICE_LOST, "fault")
+    assert isinstance(lost, DeviceLost) and str(lost) == "GPU device lost: fault"  # error.rs:59
+
+
+def test_device_lost_status_string_and_null_query():
+    import ctypes as C
+    lib = N.load()
+    assert lib.bch_status_string(N.BCH_E_DEVICE_LOST) == b"device lost"
+    flag = C.c_int(5)
+    assert lib.bch_ctx_is_lost(None, C.byref(flag)) == N.BCH_E_INVALID
 
 
 class _FakeTensor:
@@ -200,3 +217,24 @@ def test_dgemm_validation_before_device():
     assert lib.bch_dgemm(nul, 0, 0, 2, 4, 4, 4, 1.0, nul, 4, 8, nul, 4, 16, 0.0, nul, 4, 16) == N.BCH_E_SHAPE
     assert "batch stride" in N.last_error(None)
     assert lib.bch_dgemm(nul, 1, 1, 2, 4, 4, 4, 1.0, nul, 4, 16, nul, 4, 16, 0.0, nul, 4, 16) == N.BCH_E_INVALID
+
+
+def test_dgemm_empty_k_batched_passes_validation():
+    """Batched GemmF64 with k == 0 (packed strides m*k = 0, k*n = 0, lda =
+    ldb-of-B^T = 1): A and B are empty, so only C's stride is checked and
+    validation reaches the ctx check (BCH_E_INVALID with ctx = NULL), as the
+    reference only rejects length mismatches (ops/linalg/gemm_f64.rs)."""
+    lib = N.load()
+    nul = C.c_void_p()
+    # transa = transb = 0: lda = max(k, 1), strideA = m*k = 0, strideB = k*n = 0
+    assert lib.bch_dgemm(nul, 0, 0, 3, 4, 5, 0, 1.0, nul, 1, 0, nul, 5, 0, 0.5, nul, 5, 20) == N.BCH_E_INVALID
+    assert "ctx" in N.last_error(None)
+    # trans_b with k == 0: B stored [n][k], ldb = 1
+    assert lib.bch_dgemm(nul, 0, 1, 3, 4, 5, 0, 1.0, nul, 1, 0, nul, 1, 0, 0.5, nul, 5, 20) == N.BCH_E_INVALID
+    # transa with k == 0: A stored [k][m] is empty
+    assert lib.bch_dgemm(nul, 1, 0, 3, 4, 5, 0, 1.0, nul, 4, 0, nul, 5, 0, 0.5, nul, 5, 20) == N.BCH_E_INVALID
+    # C's stride is still checked
+    assert lib.bch_dgemm(nul, 0, 0, 3, 4, 5, 0, 1.0, nul, 1, 0, nul, 5, 0, 0.5, nul, 5, 19) == N.BCH_E_SHAPE
+    # padded leading dimensions: the extent is (rows - 1) * ld + row length
+    assert lib.bch_dgemm(nul, 0, 0, 2, 4, 4, 4, 1.0, nul, 6, 22, nul, 4, 16, 0.0, nul, 4, 16) == N.BCH_E_INVALID
+    assert lib.bch_dgemm(nul, 0, 0, 2, 4, 4, 4, 1.0, nul, 6, 21, nul, 4, 16, 0.0, nul, 4, 16) == N.BCH_E_SHAPE

@@ -134,3 +134,52 @@ def test_two_contexts_from_two_threads():
         t.join(timeout=120)
     assert len(errs) == 6, errs
     assert all(isinstance(e, float) and e <= 1e-4 for e in errs), errs
+
+
+@pytest.mark.parametrize("hip_error", [700, 719])  # hipErrorIllegalAddress, hipErrorLaunchFailure
+def test_device_lost_injection_is_sticky(monkeypatch, hip_error):
+    """A context-fatal HIP error (injected on the host: no kernel runs)
+    becomes DeviceLost, is_lost() turns true, and every later device call on
+    that context fails the same way (WgpuDevice::poll_safe's lost flag,
+    device/wgpu_device/submission.rs:23-71; GpuBackend::is_lost, device/
+    backend.rs:256).  A fresh context works."""
+    _say(f"device-lost injection, hipError {hip_error}")
+    from barracuda_amd import DeviceLost, HipDevice
+    monkeypatch.setenv("BARRACUDA_HIP_INJECT_HIP_ERROR", str(hip_error))
+    d = HipDevice(0)
+    monkeypatch.delenv("BARRACUDA_HIP_INJECT_HIP_ERROR")
+    assert not d.is_lost()
+    with pytest.raises(DeviceLost, match=str(hip_error)):
+        d.alloc(1024)
+    assert d.is_lost()
+    with pytest.raises(DeviceLost, match="device lost"):
+        d.sync()
+    with pytest.raises(DeviceLost):
+        Tensor.from_data(np.ones(4, np.float32), [4], d)
+    assert d.is_lost()
+    d.close()
+    d2 = HipDevice(0)
+    assert not d2.is_lost()
+    t = Tensor.from_data(np.arange(4, dtype=np.float32), [4], d2)
+    assert np.array_equal(t.to_vec(), np.arange(4, dtype=np.float32))
+    d2.close()
+
+
+@pytest.mark.parametrize("hip_error,kind", [(2, "OutOfMemory"), (701, "ExecutionError"), (1, "DeviceError")])
+def test_injected_recoverable_errors_keep_the_context(monkeypatch, hip_error, kind):
+    """hipErrorOutOfMemory, hipErrorLaunchOutOfResources and
+    hipErrorInvalidValue map to OutOfMemory, ExecutionError and Device; none
+    marks the context lost, and the next call succeeds."""
+    _say(f"recoverable injection, hipError {hip_error}")
+    import barracuda_amd as B
+    monkeypatch.setenv("BARRACUDA_HIP_INJECT_HIP_ERROR", str(hip_error))
+    d = B.HipDevice(0)
+    monkeypatch.delenv("BARRACUDA_HIP_INJECT_HIP_ERROR")
+    with pytest.raises(getattr(B, kind)) as e:
+        d.sync()
+    assert not isinstance(e.value, B.DeviceLost)
+    assert not d.is_lost()
+    d.sync()
+    t = Tensor.from_data(np.ones(8, np.float32), [2, 4], d)
+    assert np.array_equal(t.to_vec(), np.ones(8, np.float32))
+    d.close()

@@ -106,3 +106,12 @@ def test_dgemm_2048_sampled_rows(dev):
     for r in (0, 1, 777, 2047):
         ref = (a[r * n:(r + 1) * n].astype(np.longdouble) @ B).astype(np.float64)
         assert _rel(got[r], ref) <= TOL
+
+
+@pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True), (True, True)])
+def test_dgemm_empty_k_batched(dev, ta, tb):
+    """k == 0 with batch > 1: op(A) op(B) is the zero matrix, so C = 0
+    (the reference's fresh C buffer scaled by beta); no shape error."""
+    _say(f"dgemm batch=3 m=4 k=0 n=5 ta={ta} tb={tb}")
+    got = GemmF64.execute_gemm_ex(dev, [], [], 4, 0, 5, 3, 1.0, 0.5, ta, tb)
+    assert got.shape == (60,) and not np.any(got)

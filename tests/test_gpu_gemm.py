@@ -227,10 +227,17 @@ def test_config_batched_16x1024(dev):
     b = rng.uniform((16, 1024, 1024))
     ta, tb = Tensor.from_data(a, [16, 1024, 1024], dev), Tensor.from_data(b, [16, 1024, 1024], dev)
     got = ta.batch_matmul(tb).to_numpy()
-    for bi in (0, 7, 15):
-        rows = [0, 5, 511, 1023]
-        ref = O.matmul_f64(np.ascontiguousarray(a[bi]), np.ascontiguousarray(b[bi]), rows=rows)
-        assert O.max_rel_err(got[bi][rows], ref) <= TOL
+    # every batch, one row from each 256-row tile (the position inside the
+    # tile moves with the batch) plus the first and last rows; and a column
+    # from each 256-column tile
+    for bi in range(16):
+        rows = sorted({0, 1023} | {t * 256 + (bi * 37 + t * 101) % 256 for t in range(4)})
+        ab, bb = np.ascontiguousarray(a[bi]), np.ascontiguousarray(b[bi])
+        ref = O.matmul_f64(ab, bb, rows=rows)
+        err = O.max_rel_err(got[bi][rows], ref)
+        cols = [t * 256 + (bi * 53 + t * 29) % 256 for t in range(4)]
+        errc = O.max_rel_err(got[bi][:, cols], ab.astype(np.float64) @ bb[:, cols].astype(np.float64))
+        assert err <= TOL and errc <= TOL, (bi, rows, cols, err, errc)
     # batches are independent: batch 3 equals the single GEMM of batch 3
     single = _mm(dev, np.ascontiguousarray(a[3]), np.ascontiguousarray(b[3]))
     assert np.array_equal(single, got[3])

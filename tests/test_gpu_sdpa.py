@@ -97,3 +97,14 @@ def test_config_b4_h32_s2048_d128(dev):
         ref32 = O.attention_3pass_f32(q, k, v, causal, heads=[37])
         assert O.max_rel_err(got[1], ref32[0]) <= TOL
         assert np.isfinite(out).all()
+        # every one of the 128 heads on a row sample that touches each of its
+        # 16 query blocks of 128 (the row inside the block moves with the
+        # head and the block) and the last row: a head or block mapping slip
+        # anywhere in the grid fails here
+        rows = np.array([[blk * 128 + (h * 37 + blk * 11) % 128 for blk in range(16)] + [2047]
+                         for h in range(128)], dtype=np.int32)
+        refr = O.sdpa_f64_rows(q, k, v, causal, rows)
+        gotr = np.take_along_axis(out.reshape(128, 2048, 128), rows[:, :, None].astype(np.int64), axis=1)
+        err_all = O.max_rel_err(gotr, refr)
+        _say(f"  all 128 heads x 17 rows: max rel err vs f64 = {err_all:.3e}")
+        assert err_all <= TOL

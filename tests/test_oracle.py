@@ -270,3 +270,15 @@ def test_max_rel_err_metric():
     assert abs(O.max_rel_err(x, ref) - 1e-3) < 1e-6
     assert O.max_rel_err(np.array([np.nan], np.float32), np.array([1.0])) == math.inf
     assert O.max_rel_err(np.array([np.inf], np.float32), np.array([np.inf])) == 0.0
+
+
+def test_sdpa_f64_rows_equals_full_oracle_rows():
+    """The row-sampled f64 attention oracle (used on all heads at config
+    size) returns exactly the rows of the full oracle."""
+    r = O.Lcg(5)
+    q, k, v = (r.normal((2, 3, 40, 16)) for _ in range(3))
+    rows = np.array([[0, 5, 39], [1, 2, 3], [39, 38, 0], [7, 7, 7], [10, 20, 30], [0, 1, 2]], dtype=np.int32)
+    for causal in (False, True):
+        full = O.sdpa_f64(q, k, v, causal).reshape(6, 40, 16)
+        got = O.sdpa_f64_rows(q, k, v, causal, rows)
+        assert np.array_equal(got, np.take_along_axis(full, rows[:, :, None].astype(np.int64), axis=1))
