@@ -55,6 +55,7 @@ SIGNATURES = {
     "bch_sync": (_i, [_vp]),
     "bch_copy": (_i, [_vp, _vp, _vp, _sz]),
     "bch_sgemm": (_i, [_vp, _i, _i, _i, _vp, _i, _vp, _i, _vp, _i]),
+    "bch_sgemm_noalloc": (_i, [_vp, _i, _i, _i, _vp, _i, _vp, _i, _vp, _i]),
     "bch_sgemm_ex": (_i, [_vp, _i, _i, _i, _i, _vp, _i, _vp, _i, _vp, _i, _vp, _i]),
     "bch_sgemm_strided_batched": (_i, [_vp, _i, _i, _i, _i, _vp, _ll, _vp, _ll, _vp, _ll]),
     "bch_dgemm": (_i, [_vp, _i, _i, _i, _i, _i, _i, C.c_double, _vp, _i, _ll, _vp, _i, _ll, C.c_double, _vp,

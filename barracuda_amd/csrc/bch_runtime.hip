@@ -24,6 +24,14 @@
 #include "../../include/barracuda_hip.h"
 #include "bch_internal.h"
 
+// Fixed scratch of bch_sgemm_noalloc (no hipMalloc on that path): the
+// skinny GEMM's split-k partials.  Each device that loads the library holds
+// its own copy until the process ends.  In host code `scratch` names a
+// host-side stand-in, never device memory: the device address is resolved
+// once per device with hipGetSymbolAddress and only that address is used.
+constexpr size_t kNoAllocScratchBytes = (size_t)16 << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
 struct bch_ctx {
   int device = -1;
   hipStream_t stream = nullptr;
@@ -44,6 +52,10 @@ struct bch_ctx {
   // runtime had returned it, so the error translation and the lost flag can
   // be tested without making the GPU fault.
   int inject_hip_error = 0;
+  // This device's copy of `scratch` (resolved at bch_ctx_create), or null
+  // with the reason in scratch_error.
+  void* scratch = nullptr;
+  std::string scratch_error;
 };
 
 struct bch_event {
@@ -156,6 +168,31 @@ bool fail_alloc_injected() {
   return v && v[0] == '1';
 }
 
+// Device address of `scratch` on the current device, resolved once per
+// device (hipGetSymbolAddress with that device current) and kept.
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];
+
+void resolve_scratch(bch_ctx* ctx) {
+  if (ctx->device < 0 || ctx->device >= kMaxDevices) {
+    ctx->scratch_error = "device ordinal beyond the scratch table";
+    return;
+  }
+  std::lock_guard<std::mutex> g(g_scratch_mu);
+  if (!g_scratch_ptr[ctx->device]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      (void)hipGetLastError();
+      ctx->scratch_error = std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e);
+      return;
+    }
+    g_scratch_ptr[ctx->device] = p;
+  }
+  ctx->scratch = g_scratch_ptr[ctx->device];
+}
+
 }  // namespace
 
 extern "C" {
@@ -218,6 +255,7 @@ bch_status bch_ctx_create(int device, const char* code_object_dir, bch_ctx** out
     delete ctx;
     return st;
   }
+  resolve_scratch(ctx);
   *out = ctx;
   return BCH_OK;
 }
@@ -363,6 +401,31 @@ bch_status bch_sgemm(bch_ctx* ctx, int m, int n, int k, const float* A, int lda,
   hipError_t e = bch::launch_sgemm(ctx->stream, 1, m, n, k, A, lda, 0, B, ldb, 0, C, ldc, 0,
                                    ctx->ws, ctx->ws_bytes);
   return from_hip(ctx, e, "matmul launch");
+}
+
+bch_status bch_sgemm_noalloc(bch_ctx* ctx, int m, int n, int k, const float* A, int lda,
+                             const float* B, int ldb, float* C, int ldc) {
+  if (m < 0 || n < 0 || k < 0)
+    return fail(ctx, BCH_E_SHAPE, "matmul: negative dimension (m=%d, n=%d, k=%d)", m, n, k);
+  if (lda < (k > 1 ? k : 1) || ldb < (n > 1 ? n : 1) || ldc < (n > 1 ? n : 1))
+    return fail(ctx, BCH_E_SHAPE, "matmul: leading dimension too small (lda=%d k=%d, ldb=%d n=%d, ldc=%d n=%d)",
+                lda, k, ldb, n, ldc, n);
+  if (!ctx) return fail(ctx, BCH_E_INVALID, "matmul: ctx is NULL");
+  if (m == 0 || n == 0) return BCH_OK;
+  if (!C || (k > 0 && (!A || !B))) return fail(ctx, BCH_E_INVALID, "matmul: NULL buffer");
+  bch_status st = use(ctx);
+  if (st != BCH_OK) return st;
+  // sized with this device current (the stream-K plans take one workgroup per CU)
+  const size_t wsb = bch::sgemm_workspace_bytes(1, m, n, k);
+  if (wsb > kNoAllocScratchBytes)
+    return fail(ctx, BCH_E_UNSUPPORTED,
+                "matmul (no-alloc): m=%d n=%d k=%d needs %zu bytes of scratch, more than the fixed %zu",
+                m, n, k, wsb, kNoAllocScratchBytes);
+  if (wsb && !ctx->scratch)
+    return fail(ctx, BCH_E_DEVICE, "matmul (no-alloc): fixed scratch unavailable (%s)", ctx->scratch_error.c_str());
+  hipError_t e = bch::launch_sgemm(ctx->stream, 1, m, n, k, A, lda, 0, B, ldb, 0, C, ldc, 0,
+                                   wsb ? ctx->scratch : nullptr, wsb ? kNoAllocScratchBytes : 0);
+  return from_hip(ctx, e, "matmul (no-alloc) launch");
 }
 
 bch_status bch_sgemm_strided_batched(bch_ctx* ctx, int batch, int m, int n, int k,

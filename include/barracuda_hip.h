@@ -109,6 +109,21 @@ bch_status bch_sgemm(bch_ctx *ctx, int m, int n, int k,
                      const float *A, int lda, const float *B, int ldb,
                      float *C, int ldc);
 
+/* bch_sgemm without any device allocation: no hipMalloc, hipFree or
+ * allocating library call on any path.  No counterpart in the reference; it
+ * is for callers that cannot allocate (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid allocation).  The decode-shaped
+ * (m <= 32) path's split-k partials go to a fixed 16 MiB device array
+ * (one per GPU, held until the process ends) instead of the context's
+ * workspace; shapes needing more return BCH_E_UNSUPPORTED (e.g. m = 32 with
+ * n above ~65000).  No kernel relies on the array's earlier contents.
+ * Every call on one GPU shares that GPU's array, so calls that overlap in
+ * time on one GPU (two contexts or streams) race: serialise them.  Results
+ * are bit-identical to bch_sgemm's. */
+bch_status bch_sgemm_noalloc(bch_ctx *ctx, int m, int n, int k,
+                             const float *A, int lda, const float *B, int ldb,
+                             float *C, int ldc);
+
 /* Activation of bch_sgemm_ex's epilogue. */
 #define BCH_ACT_NONE 0
 #define BCH_ACT_RELU 1 /* max(x, 0): shaders/activation/relu_f64.wgsl */

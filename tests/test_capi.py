@@ -238,3 +238,15 @@ def test_dgemm_empty_k_batched_passes_validation():
     # padded leading dimensions: the extent is (rows - 1) * ld + row length
     assert lib.bch_dgemm(nul, 0, 0, 2, 4, 4, 4, 1.0, nul, 6, 22, nul, 4, 16, 0.0, nul, 4, 16) == N.BCH_E_INVALID
     assert lib.bch_dgemm(nul, 0, 0, 2, 4, 4, 4, 1.0, nul, 6, 21, nul, 4, 16, 0.0, nul, 4, 16) == N.BCH_E_SHAPE
+
+
+def test_sgemm_noalloc_validation_before_device():
+    """The no-allocation matmul validates like bch_sgemm before the context
+    is needed."""
+    lib = N.load()
+    nul = C.c_void_p()
+    assert lib.bch_sgemm_noalloc(nul, -1, 4, 4, nul, 4, nul, 4, nul, 4) == N.BCH_E_SHAPE
+    assert lib.bch_sgemm_noalloc(nul, 4, 4, 4, nul, 3, nul, 4, nul, 4) == N.BCH_E_SHAPE
+    assert "leading dimension" in N.last_error(None)
+    assert lib.bch_sgemm_noalloc(nul, 4, 4, 4, nul, 4, nul, 4, nul, 4) == N.BCH_E_INVALID
+    assert "ctx" in N.last_error(None)

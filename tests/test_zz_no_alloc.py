@@ -1,0 +1,68 @@
+"""bch_sgemm_noalloc (the matmul entry point that allocates nothing; its
+scratch is a fixed per-GPU device array) against bch_sgemm, called through
+the C ABI: bit-identical outputs, on two calls in a row with the second
+smaller, on each kernel family (decode-shaped split-k paths that use the
+scratch, and the MFMA tile path that needs none), and a clear rejection of a
+shape whose partials would not fit."""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from barracuda_amd import Tensor
+from barracuda_amd import _native as N
+from oracle import bc_oracle as O
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-4
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+def _both(dev, m, n, k, seed):
+    rng = O.Lcg(seed)
+    a, b = rng.normal((m, k)), rng.normal((k, n), 0.0, 0.02)
+    ta, tb = Tensor.from_data(a, [m, k], dev), Tensor.from_data(b, [k, n], dev)
+    c_ref, c_na = Tensor.empty([m, n], dev), Tensor.empty([m, n], dev)
+    lib, ctx = dev._lib, dev.ctx
+    pa, pb = C.c_void_p(ta.ptr), C.c_void_p(tb.ptr)
+    dev.check(lib.bch_sgemm(ctx, m, n, k, pa, k, pb, n, C.c_void_p(c_ref.ptr), n), "sgemm")
+    dev.check(lib.bch_sgemm_noalloc(ctx, m, n, k, pa, k, pb, n, C.c_void_p(c_na.ptr), n), "sgemm_noalloc")
+    got, want = c_na.to_numpy(), c_ref.to_numpy()
+    return got, want, a, b
+
+
+@pytest.mark.parametrize("shapes", [
+    # (m, n, k) pairs: a call, then a smaller one; decode paths use the scratch
+    [(32, 11008, 4096), (8, 3000, 1024)],
+    [(8, 11008, 4096), (1, 4096, 512)],
+    [(1, 11008, 4096), (20, 1000, 300)],
+    [(256, 512, 384), (32, 256, 64)],
+])
+def test_noalloc_matches_sgemm_twice(dev, shapes):
+    for i, (m, n, k) in enumerate(shapes):
+        _say(f"sgemm_noalloc call {i}: m={m} n={n} k={k} kernel={dev._lib.bch_sgemm_kernel_name(m, n, k).decode()}")
+        got, want, a, b = _both(dev, m, n, k, 1000 * i + m + n + k)
+        assert np.array_equal(got, want), (m, n, k)
+        rows = list(range(min(m, 4))) + [m - 1]
+        assert O.max_rel_err(got[rows], O.matmul_f64(a, b, rows=rows)) <= TOL
+
+
+def test_noalloc_rejects_what_does_not_fit(dev):
+    """m = 32, n = 262144: the split-k partials exceed the fixed 16 MiB, so
+    the call fails before any launch, with the sizes in the message."""
+    m, n, k = 32, 262144, 64
+    _say(f"sgemm_noalloc rejection m={m} n={n} k={k}")
+    ta, tb, tc = Tensor.empty([m, k], dev), Tensor.empty([k, n], dev), Tensor.empty([m, n], dev)
+    lib = dev._lib
+    st = lib.bch_sgemm_noalloc(dev.ctx, m, n, k, C.c_void_p(ta.ptr), k, C.c_void_p(tb.ptr), n,
+                               C.c_void_p(tc.ptr), n)
+    assert st == N.BCH_E_UNSUPPORTED
+    msg = N.last_error(dev.ctx)
+    assert "scratch" in msg and str(16 << 20) in msg
+    # the context stays usable
+    dev.sync()
