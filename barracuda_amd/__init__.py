@@ -11,9 +11,9 @@ from . import linalg, nn
 from .linalg import F64Buffer, GemmCachedF64, GemmF64
 from .nn import Activation, fused_mlp
 from .session import AttentionDims, SessionTensor, TensorSession
-from .tensor import (Attention, BatchMatMul, CausalAttention, FlashAttention, GroupedQueryAttention, HipDevice,
-                     LcgStream, MatMul, MatmulTiled, MultiHeadAttention, ScaledDotProductAttention, Softmax,
-                     Tensor, get_device)
+from .tensor import (GELU, Attention, BatchMatMul, CausalAttention, FlashAttention, GroupedQueryAttention,
+                     HipDevice, LayerNorm, LcgStream, MatMul, MatmulTiled, MultiHeadAttention, ReLU,
+                     ScaledDotProductAttention, Softmax, Tensor, get_device)
 
 __all__ = [
     "BarracudaError", "CastOverflow", "DeviceError", "DeviceLost", "DeviceNotAvailable",
@@ -23,4 +23,5 @@ __all__ = [
     "Attention", "BatchMatMul", "CausalAttention", "FlashAttention", "GroupedQueryAttention", "HipDevice",
     "MatMul", "MultiHeadAttention",
     "MatmulTiled", "ScaledDotProductAttention", "Softmax", "Tensor", "get_device", "LcgStream",
+    "ReLU", "GELU", "LayerNorm",
 ]

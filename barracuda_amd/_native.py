@@ -25,6 +25,8 @@ BCH_E_UNSUPPORTED = 8
 BCH_E_DEVICE_LOST = 9
 BCH_ACT_NONE = 0
 BCH_ACT_RELU = 1
+BCH_ACT_GELU = 2
+BCH_EW_ADD, BCH_EW_SUB, BCH_EW_MUL, BCH_EW_NEG, BCH_EW_FMA, BCH_EW_SCALE, BCH_EW_RELU, BCH_EW_GELU = range(8)
 
 _vp = C.c_void_p
 _i = C.c_int
@@ -61,6 +63,9 @@ SIGNATURES = {
     "bch_dgemm": (_i, [_vp, _i, _i, _i, _i, _i, _i, C.c_double, _vp, _i, _ll, _vp, _i, _ll, C.c_double, _vp,
                        _i, _ll]),
     "bch_softmax_rows": (_i, [_vp, _ll, _ll, _vp, _vp]),
+    "bch_elementwise": (_i, [_vp, _i, _ll, _vp, _vp, _vp, _f, _vp]),
+    "bch_layer_norm": (_i, [_vp, _ll, _ll, _f, _vp, _vp]),
+    "bch_layer_norm_kernel_name": (C.c_char_p, [_ll, _ll]),
     "bch_softmax_axis": (_i, [_vp, _ll, _ll, _ll, _vp, _vp]),
     "bch_sdpa_fwd": (_i, [_vp, _i, _i, _i, _i, _i, _f, _i, _vp, _vp, _vp, _vp]),
     "bch_sdpa_fwd_ex": (_i, [_vp, _i, _i, _i, _i, _i, _i, _f, _i, _vp, AttnLayout, _vp, AttnLayout, _vp,

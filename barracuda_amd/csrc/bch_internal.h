@@ -32,6 +32,39 @@ __device__ __forceinline__ float readlane(float v, int lane) {
       float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
 }
 
+// Activation of the linear layer's epilogue and of the element-wise ops
+// (the values of BCH_ACT_*).
+constexpr int kActNone = 0, kActRelu = 1, kActGelu = 2;
+
+// GELU, tanh form (shaders/activation/gelu_f64.wgsl: 0.5 x (1 + tanh(y)),
+// y = 0.7978845608 (x + 0.044715 x^3)), evaluated as the identical
+// x / (1 + e^z), z = -2y, which stays finite for every finite x (an
+// exp-ratio tanh such as the f64 shader's tanh_f64, math_f64.wgsl:718-722,
+// overflows to inf/inf).  z > 88 (x below about -9.6): the quotient is below
+// 1e-37 in magnitude and the result is -0 (also for x = -inf, where the
+// formula itself is inf * 0).  z is floored at -126, where e^z already
+// underflows to 0, so y = +inf (x^3 overflowing for |x| > 1.8e19) gives x.
+// e^z is 2^(z log2 e) on v_exp_f32 with the product's rounding error carried
+// by one fma (within a few ulp of a correctly rounded expf).  NaN propagates.
+__device__ __forceinline__ float gelu_tanh(float x) {
+  const float y = 0.7978845608f * fmaf(0.044715f * x, x * x, x);
+  float z = -2.0f * y;
+  if (z > 88.0f) return -0.0f;
+  z = z < -126.0f ? -126.0f : z;
+  const float p = z * 1.44269502162933349609375f;
+  float e = fmaf(z, 1.44269502162933349609375f, -p);
+  e = fmaf(z, 1.925963033500011829e-8f, e);
+  const float r = __builtin_amdgcn_exp2f(p);
+  const float ez = fmaf(r, e * 0.693147180559945309f, r);
+  return x / (1.0f + ez);
+}
+
+__device__ __forceinline__ float activate(float v, int act) {
+  if (act == kActRelu) return fmaxf(v, 0.0f);
+  if (act == kActGelu) return gelu_tanh(v);
+  return v;
+}
+
 struct OpMax {
   __device__ float operator()(float a, float b) const { return fmaxf(a, b); }
 };
@@ -81,26 +114,27 @@ hipError_t launch_sgemm(hipStream_t s, int batch, int m, int n, int k,
 size_t sgemm_workspace_bytes(int batch, int m, int n, int k);
 const char* sgemm_kernel_name(int m, int n, int k);
 // With B given as [n][k] when transb (C = A B^T), and the linear layer's
-// epilogue C = max(acc + bias[col], 0): bias nullable, relu 0/1.
+// epilogue C = act(acc + bias[col]): bias nullable, act kActNone / kActRelu /
+// kActGelu.
 hipError_t launch_sgemm_ex(hipStream_t s, bool transb, int batch, int m,
                            int n, int k, const float* A, int lda,
                            long long sA, const float* B, int ldb,
-                           long long sB, const float* bias, int relu,
+                           long long sB, const float* bias, int act,
                            float* C, int ldc, long long sC, void* ws,
                            size_t ws_bytes);
 
 // Skinny (m <= 32) GEMM: streams B once; split-k partials go to ws; the
-// reduce applies the epilogue (bias nullable, relu 0/1).
+// reduce applies the epilogue (bias nullable, act as above).
 hipError_t launch_sgemm_skinny(hipStream_t s, int m, int n, int k,
                                const float* A, int lda, const float* B,
                                int ldb, float* C, int ldc, void* ws,
-                               size_t ws_bytes, const float* bias, int relu);
+                               size_t ws_bytes, const float* bias, int act);
 size_t sgemm_skinny_workspace_bytes(int m, int n, int k);
 // Skinny (m <= 32) GEMM with W given as [n][k] (C = A W^T), same epilogue.
 hipError_t launch_sgemm_skinny_nt(hipStream_t s, int m, int n, int k,
                                   const float* A, int lda, const float* W,
                                   int ldw, float* C, int ldc, void* ws,
-                                  size_t ws_bytes, const float* bias, int relu);
+                                  size_t ws_bytes, const float* bias, int act);
 size_t sgemm_skinny_nt_workspace_bytes(int m, int n, int k);
 bool sgemm_skinny_nt_applies(int m, int n, int k, const float* A, int lda,
                              const float* W, int ldw);
@@ -127,6 +161,14 @@ uint64_t lcg_advance(uint64_t state, uint64_t inc, uint64_t n);
 // (function, device); thread-safe.  Kernels asking for more than 64 KB of
 // dynamic LDS need it before their first launch on each device.
 hipError_t ensure_dynamic_lds(const void* func, int bytes);
+
+// Element-wise ops of the session (op: BCH_EW_*), HBM-streaming.
+hipError_t launch_elementwise(hipStream_t s, int op, long long n, const float* a, const float* b,
+                              const float* c, float scalar, float* out);
+// Layer norm over the last axis of [rows, cols]: (x - mean) / sqrt(var + eps).
+hipError_t launch_layer_norm(hipStream_t s, long long rows, long long cols, float eps, const float* in,
+                             float* out);
+const char* layer_norm_kernel_name(long long rows, long long cols);
 
 // Device-to-device copy (16-byte path when aligned).
 hipError_t launch_copy(hipStream_t s, void* dst, const void* src, size_t bytes);

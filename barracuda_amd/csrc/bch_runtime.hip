@@ -350,7 +350,7 @@ bch_status bch_sync(bch_ctx* ctx) {
 bch_status bch_sgemm_ex(bch_ctx* ctx, int transb, int m, int n, int k, const float* A, int lda, const float* B,
                         int ldb, const float* bias, int act, float* C, int ldc) {
   if (transb != 0 && transb != 1) return fail(ctx, BCH_E_INVALID, "linear: transb must be 0 or 1 (got %d)", transb);
-  if (act != BCH_ACT_NONE && act != BCH_ACT_RELU)
+  if (act != BCH_ACT_NONE && act != BCH_ACT_RELU && act != BCH_ACT_GELU)
     return fail(ctx, BCH_E_INVALID, "linear: unknown activation %d", act);
   if (m < 0 || n < 0 || k < 0)
     return fail(ctx, BCH_E_SHAPE, "linear: negative dimension (m=%d, n=%d, k=%d)", m, n, k);
@@ -372,8 +372,8 @@ bch_status bch_sgemm_ex(bch_ctx* ctx, int transb, int m, int n, int k, const flo
     st = ensure_ws(ctx, wsb);
     if (st != BCH_OK) return st;
   }
-  hipError_t e = bch::launch_sgemm_ex(ctx->stream, transb != 0, 1, m, n, k, A, lda, 0, B, ldb, 0, bias,
-                                      act == BCH_ACT_RELU, C, ldc, 0, ctx->ws, ctx->ws_bytes);
+  hipError_t e = bch::launch_sgemm_ex(ctx->stream, transb != 0, 1, m, n, k, A, lda, 0, B, ldb, 0, bias, act, C,
+                                      ldc, 0, ctx->ws, ctx->ws_bytes);
   return from_hip(ctx, e, "linear launch");
 }
 
@@ -498,6 +498,32 @@ bch_status bch_softmax_rows(bch_ctx* ctx, long long rows, long long cols, const 
   }
   return from_hip(ctx, bch::launch_softmax_rows(ctx->stream, rows, cols, in, out, ctx->ws, ctx->ws_bytes),
                   "softmax launch");
+}
+
+bch_status bch_elementwise(bch_ctx* ctx, int op, long long n, const float* a, const float* b, const float* c,
+                           float scalar, float* out) {
+  if (op < BCH_EW_ADD || op > BCH_EW_GELU) return fail(ctx, BCH_E_INVALID, "elementwise: unknown op %d", op);
+  if (n < 0) return fail(ctx, BCH_E_SHAPE, "elementwise: negative element count %lld", n);
+  if (!ctx) return fail(ctx, BCH_E_INVALID, "elementwise: ctx is NULL");
+  if (n == 0) return BCH_OK;
+  const bool needs_b = op == BCH_EW_ADD || op == BCH_EW_SUB || op == BCH_EW_MUL || op == BCH_EW_FMA;
+  if (!a || !out || (needs_b && !b) || (op == BCH_EW_FMA && !c))
+    return fail(ctx, BCH_E_INVALID, "elementwise: NULL buffer");
+  bch_status st = use(ctx);
+  if (st != BCH_OK) return st;
+  return from_hip(ctx, bch::launch_elementwise(ctx->stream, op, n, a, b, c, scalar, out), "elementwise launch");
+}
+
+bch_status bch_layer_norm(bch_ctx* ctx, long long rows, long long cols, float eps, const float* in, float* out) {
+  if (rows < 1 || cols < 1)
+    return fail(ctx, BCH_E_SHAPE, "layer_norm: empty dimension (rows=%lld, cols=%lld)", rows, cols);
+  if (!(eps >= 0.0f)) return fail(ctx, BCH_E_INVALID, "layer_norm: epsilon must be >= 0 (got %g)", (double)eps);
+  if (rows > 0x7fffffffLL) return fail(ctx, BCH_E_UNSUPPORTED, "layer_norm: %lld rows > 2^31 - 1", rows);
+  if (!ctx) return fail(ctx, BCH_E_INVALID, "layer_norm: ctx is NULL");
+  if (!in || !out) return fail(ctx, BCH_E_INVALID, "layer_norm: NULL buffer");
+  bch_status st = use(ctx);
+  if (st != BCH_OK) return st;
+  return from_hip(ctx, bch::launch_layer_norm(ctx->stream, rows, cols, eps, in, out), "layer_norm launch");
 }
 
 bch_status bch_softmax_axis(bch_ctx* ctx, long long outer, long long axis, long long inner,
@@ -686,6 +712,10 @@ void bch_event_destroy(bch_event* ev) {
 }
 
 const char* bch_sgemm_kernel_name(int m, int n, int k) { return bch::sgemm_kernel_name(m, n, k); }
+
+const char* bch_layer_norm_kernel_name(long long rows, long long cols) {
+  return bch::layer_norm_kernel_name(rows, cols);
+}
 
 }  // extern "C"
 

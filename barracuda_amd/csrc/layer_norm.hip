@@ -1,0 +1,147 @@
+// layer_norm.hip -- layer normalisation over the last axis for gfx950.
+//
+// Replaces TensorSession::layer_norm (crates/barracuda/src/session/mod.rs:
+// 379-398, dispatched at session/dispatch.rs:221-240 with epsilon 1e-5) and
+// the op it binds, LayerNorm (ops/layer_norm_wgsl.rs, shaders/norm/
+// layer_norm_f64.wgsl: one thread per row, three sweeps).  Same contract per
+// row of `cols` features, no affine parameters:
+//   mean = sum(x) / cols
+//   var  = sum((x - mean)^2) / cols          (two-pass, biased)
+//   y    = (x - mean) / sqrt(var + eps)
+//
+// HBM-bound: one read and one write of the matrix (8 bytes per element).
+//   * cols % 4 == 0, cols <= 4096, 16-byte aligned rows: one wavefront per
+//     row; the row is loaded once with 128-bit coalesced loads and stays in
+//     registers; the sum and the sum of squared deviations are wavefront
+//     all-reductions (DPP row ops + v_readlane), so the two passes of the
+//     reference cost no second read; the output is written once.
+//   * anything else: one 256-thread workgroup per row, the same two passes
+//     with block reductions over a second read of the row (from cache).
+#include "bch_internal.h"
+
+#include <math.h>
+
+namespace {
+
+using bch::OpSum;
+using bch::wave_allreduce;
+
+template <int NV>
+__global__ __launch_bounds__(256) void layer_norm_wave(const float* in, float* out, long long rows, int cols,
+                                                       float eps) {
+  const int lane = threadIdx.x & 63;
+  const long long row = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;  // wave-uniform
+  const int nvec = cols >> 2;
+  const float4* src = reinterpret_cast<const float4*>(in + row * (long long)cols);
+  float4* dst = reinterpret_cast<float4*>(out + row * (long long)cols);
+  float4 v[NV];
+  float s = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int idx = i * 64 + lane;
+    v[i] = idx < nvec ? bch::load_nt(src + idx) : make_float4(0.f, 0.f, 0.f, 0.f);
+    s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
+  }
+  const float mean = wave_allreduce(s, OpSum()) / (float)cols;
+  float q = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    if (i * 64 + lane < nvec) {
+      const float dx = v[i].x - mean, dy = v[i].y - mean, dz = v[i].z - mean, dw = v[i].w - mean;
+      q += fmaf(dx, dx, dy * dy) + fmaf(dz, dz, dw * dw);
+    }
+  }
+  const float var = wave_allreduce(q, OpSum()) / (float)cols;
+  const float rstd = 1.0f / sqrtf(var + eps);
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int idx = i * 64 + lane;
+    if (idx < nvec)
+      bch::store_nt(make_float4((v[i].x - mean) * rstd, (v[i].y - mean) * rstd, (v[i].z - mean) * rstd,
+                                (v[i].w - mean) * rstd),
+                    dst + idx);
+  }
+}
+
+// Sum over the 256 threads of a workgroup; every thread gets it.  Must be
+// reached by all threads of the block.
+__device__ __forceinline__ float block_sum(float v, float* sh) {
+  v = wave_allreduce(v, OpSum());
+  const int w = threadIdx.x >> 6;
+  __syncthreads();  // sh may still be read from the previous call
+  if ((threadIdx.x & 63) == 0) sh[w] = v;
+  __syncthreads();
+  return (sh[0] + sh[1]) + (sh[2] + sh[3]);
+}
+
+__global__ __launch_bounds__(256) void layer_norm_block(const float* in, float* out, long long cols, float eps) {
+  __shared__ float sh[4];
+  const long long row = blockIdx.x;
+  const float* x = in + row * cols;
+  float* y = out + row * cols;
+  float s = 0.0f;
+  for (long long j = threadIdx.x; j < cols; j += 256) s += x[j];
+  const float mean = block_sum(s, sh) / (float)cols;
+  float q = 0.0f;
+  for (long long j = threadIdx.x; j < cols; j += 256) {
+    const float d = x[j] - mean;
+    q = fmaf(d, d, q);
+  }
+  const float var = block_sum(q, sh) / (float)cols;
+  const float rstd = 1.0f / sqrtf(var + eps);
+  for (long long j = threadIdx.x; j < cols; j += 256) y[j] = (x[j] - mean) * rstd;
+}
+
+int pick_nv(long long cols) {
+  if (cols <= 256) return 1;
+  if (cols <= 512) return 2;
+  if (cols <= 1024) return 4;
+  if (cols <= 2048) return 8;
+  if (cols <= 4096) return 16;
+  return 0;
+}
+
+bool wave_path(long long cols, const float* in, const float* out) {
+  return cols % 4 == 0 && pick_nv(cols) > 0 && (reinterpret_cast<uintptr_t>(in) & 15) == 0 &&
+         (reinterpret_cast<uintptr_t>(out) & 15) == 0;
+}
+
+}  // namespace
+
+namespace bch {
+
+const char* layer_norm_kernel_name(long long rows, long long cols) {
+  (void)rows;
+  if (cols % 4 == 0) {
+    switch (pick_nv(cols)) {
+      case 1: return "layer_norm_wave<1>";
+      case 2: return "layer_norm_wave<2>";
+      case 4: return "layer_norm_wave<4>";
+      case 8: return "layer_norm_wave<8>";
+      case 16: return "layer_norm_wave<16>";
+      default: break;
+    }
+  }
+  return "layer_norm_block";
+}
+
+hipError_t launch_layer_norm(hipStream_t s, long long rows, long long cols, float eps, const float* in, float* out) {
+  if (rows <= 0 || cols <= 0) return hipSuccess;
+  if (wave_path(cols, in, out)) {
+    const dim3 grid((unsigned)((rows + 3) / 4)), block(256);
+    const int c = (int)cols;
+    switch (pick_nv(cols)) {
+      case 1: hipLaunchKernelGGL(layer_norm_wave<1>, grid, block, 0, s, in, out, rows, c, eps); break;
+      case 2: hipLaunchKernelGGL(layer_norm_wave<2>, grid, block, 0, s, in, out, rows, c, eps); break;
+      case 4: hipLaunchKernelGGL(layer_norm_wave<4>, grid, block, 0, s, in, out, rows, c, eps); break;
+      case 8: hipLaunchKernelGGL(layer_norm_wave<8>, grid, block, 0, s, in, out, rows, c, eps); break;
+      default: hipLaunchKernelGGL(layer_norm_wave<16>, grid, block, 0, s, in, out, rows, c, eps); break;
+    }
+    return hipGetLastError();
+  }
+  hipLaunchKernelGGL(layer_norm_block, dim3((unsigned)rows), dim3(256), 0, s, in, out, cols, eps);
+  return hipGetLastError();
+}
+
+}  // namespace bch

@@ -55,11 +55,12 @@
 //     y = x W^T with W [out, in] (shaders/misc/linear_f64.wgsl, the layers of
 //     nn/fused_mlp.rs:38-168).  Its tile is already k-contiguous, so it is
 //     loaded like the A tile (128-bit rows straight into LDS [n][k]).
-//   * Epilogue: C = acc (+ bias[col]) (then max(., 0)), fused into the store
-//     -- linear_f64.wgsl adds the bias after the dot product, and fused_mlp
-//     runs relu_f64.wgsl as a separate pass over the output.  EPI is a
+//   * Epilogue: C = act(acc (+ bias[col])) with act none, ReLU or GELU (tanh
+//     form), fused into the store -- linear_f64.wgsl adds the bias after the
+//     dot product, and fused_mlp runs relu_f64.wgsl (gelu_f64.wgsl for a GELU
+//     layer) as a separate pass over the output.  EPI is a
 //     template flag so the plain GEMM stores straight from the accumulators
-//     (420 VGPRs, no spill at 256x256); the bias/ReLU variant of that tile
+//     (420 VGPRs, no spill at 256x256); the bias/activation variant of that tile
 //     parks 8 accumulators in scratch for the epilogue only (36 bytes per
 //     lane, no AGPR copies in the k-loop; measured at the plain kernel's
 //     rate).
@@ -95,7 +96,7 @@ template <int BM, int BN, int BK, bool CHECK, bool TB, bool EPI>
 __global__ __launch_bounds__(kThreads) void sgemm_mfma_kernel(
     int M, int N, int K, const float* __restrict__ A, int lda, long long sA,
     const float* __restrict__ B, int ldb, long long sB, float* __restrict__ C,
-    int ldc, long long sC, int tiles_m, int tiles_n, const float* __restrict__ bias, int relu) {
+    int ldc, long long sC, int tiles_m, int tiles_n, const float* __restrict__ bias, int act) {
   using G = Cfg<BM, BN, BK>;
   constexpr int LDK = G::LDK;
   extern __shared__ float4 smem4[];
@@ -343,7 +344,7 @@ __global__ __launch_bounds__(kThreads) void sgemm_mfma_kernel(
       }
     }
   } else {
-    // bias and relu are uniform over the launch (no divergence); one 32 x 32
+    // bias and the activation are uniform over the launch (no divergence); one 32 x 32
     // block at a time, so only 16 accumulators are out of the AGPRs at once
 #pragma unroll
     for (int j = 0; j < G::TN; ++j) {
@@ -355,7 +356,7 @@ __global__ __launch_bounds__(kThreads) void sgemm_mfma_kernel(
         for (int r = 0; r < 16; ++r) {
           const int row = m0 + wm + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
           float v = acc[i][j][r] + bj;
-          if (relu) v = fmaxf(v, 0.0f);
+          v = bch::activate(v, act);
           if (!CHECK || (row < M && col < N)) C[(long long)row * ldc + col] = v;
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -368,7 +369,7 @@ template <int BM, int BN, int BK, bool CHECK, bool TB, bool EPI>
 hipError_t launch_tiles(hipStream_t s, int batch, int m, int n, int k,
                         const float* A, int lda, long long sA, const float* B,
                         int ldb, long long sB, float* C, int ldc, long long sC,
-                        const float* bias, int relu) {
+                        const float* bias, int act) {
   using G = Cfg<BM, BN, BK>;
   const int tm = (m + BM - 1) / BM, tn = (n + BN - 1) / BN;
   const size_t lds = sizeof(float) * G::LDS_FLOATS;
@@ -377,7 +378,7 @@ hipError_t launch_tiles(hipStream_t s, int batch, int m, int n, int k,
   if (e != hipSuccess) return e;
   if (batch > 65535) return hipErrorInvalidValue;
   hipLaunchKernelGGL(kern, dim3(tm * tn, batch), dim3(kThreads), lds, s, m, n, k,
-                     A, lda, sA, B, ldb, sB, C, ldc, sC, tm, tn, bias, relu);
+                     A, lda, sA, B, ldb, sB, C, ldc, sC, tm, tn, bias, act);
   return hipGetLastError();
 }
 
@@ -412,26 +413,26 @@ bool fast_ok(Tile t, int m, int n, int k, const float* A, int lda, long long sA,
 template <bool CHECK, bool TB, bool EPI>
 hipError_t launch_tile(Tile t, hipStream_t s, int batch, int m, int n, int k, const float* A, int lda,
                        long long sA, const float* B, int ldb, long long sB, float* C, int ldc, long long sC,
-                       const float* bias, int relu) {
+                       const float* bias, int act) {
   switch (t) {
     case Tile::k256x256:
       return launch_tiles<256, 256, kBK, CHECK, TB, EPI>(s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC,
-                                                         bias, relu);
+                                                         bias, act);
     case Tile::k256x128:
       return launch_tiles<256, 128, kBK, CHECK, TB, EPI>(s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC,
-                                                         bias, relu);
+                                                         bias, act);
     default:
       return launch_tiles<128, 128, kBK, CHECK, TB, EPI>(s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC,
-                                                         bias, relu);
+                                                         bias, act);
   }
 }
 
 template <bool TB, bool EPI>
 hipError_t launch_tile_any(bool fast, Tile t, hipStream_t s, int batch, int m, int n, int k, const float* A,
                            int lda, long long sA, const float* B, int ldb, long long sB, float* C, int ldc,
-                           long long sC, const float* bias, int relu) {
-  return fast ? launch_tile<false, TB, EPI>(t, s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC, bias, relu)
-              : launch_tile<true, TB, EPI>(t, s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC, bias, relu);
+                           long long sC, const float* bias, int act) {
+  return fast ? launch_tile<false, TB, EPI>(t, s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC, bias, act)
+              : launch_tile<true, TB, EPI>(t, s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC, bias, act);
 }
 
 const char* tile_name(Tile t, bool check) {
@@ -467,24 +468,24 @@ hipError_t launch_sgemm(hipStream_t s, int batch, int m, int n, int k, const flo
 }
 
 hipError_t launch_sgemm_ex(hipStream_t s, bool transb, int batch, int m, int n, int k, const float* A, int lda,
-                           long long sA, const float* B, int ldb, long long sB, const float* bias, int relu,
+                           long long sA, const float* B, int ldb, long long sB, const float* bias, int act,
                            float* C, int ldc, long long sC, void* ws, size_t ws_bytes) {
   if (batch <= 0 || m <= 0 || n <= 0) return hipSuccess;
   if (!transb && batch == 1 && sgemm_skinny_applies(m, n, k, A, lda, B, ldb))
-    return launch_sgemm_skinny(s, m, n, k, A, lda, B, ldb, C, ldc, ws, ws_bytes, bias, relu);
+    return launch_sgemm_skinny(s, m, n, k, A, lda, B, ldb, C, ldc, ws, ws_bytes, bias, act);
   if (transb && batch == 1 && sgemm_skinny_nt_applies(m, n, k, A, lda, B, ldb))
-    return launch_sgemm_skinny_nt(s, m, n, k, A, lda, B, ldb, C, ldc, ws, ws_bytes, bias, relu);
+    return launch_sgemm_skinny_nt(s, m, n, k, A, lda, B, ldb, C, ldc, ws, ws_bytes, bias, act);
   const Tile t = pick_tile(batch, m, n);
   // the [n][k] tile loads need the same alignment as the [k][n] ones (ldb, sB multiples of 4)
   const bool fast = fast_ok(t, m, n, k, A, lda, sA, B, ldb, sB);
-  const bool epi = bias != nullptr || relu != 0;
+  const bool epi = bias != nullptr || act != 0;
   if (transb)
-    return epi ? launch_tile_any<true, true>(fast, t, s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC, bias, relu)
+    return epi ? launch_tile_any<true, true>(fast, t, s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC, bias, act)
                : launch_tile_any<true, false>(fast, t, s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC, bias,
-                                              relu);
-  return epi ? launch_tile_any<false, true>(fast, t, s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC, bias, relu)
+                                              act);
+  return epi ? launch_tile_any<false, true>(fast, t, s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC, bias, act)
              : launch_tile_any<false, false>(fast, t, s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC, bias,
-                                             relu);
+                                             act);
 }
 
 }  // namespace bch

@@ -121,16 +121,16 @@ __global__ __launch_bounds__(256) void sgemm_skinny_fma(int M, int N, int K, con
 
 // C[m][n] = sum over splits s < splits, in split order, of P[s][m][n].  The
 // loads of a batch of 16 partials are all in flight before the adds.  Then
-// the linear layer's epilogue: + bias[n], max(., 0) (both optional).
-__device__ __forceinline__ float epilogue(float s, const float* __restrict__ bias, int n, int relu) {
+// the linear layer's epilogue: + bias[n], then the activation (both optional).
+__device__ __forceinline__ float epilogue(float s, const float* __restrict__ bias, int n, int act) {
   if (bias) s += bias[n];
-  return relu ? fmaxf(s, 0.0f) : s;
+  return bch::activate(s, act);
 }
 
 // Block (x, m) covers columns 256 x .. 256 x + 255 of row m.
 __global__ __launch_bounds__(256) void sgemm_skinny_reduce(int M, int N, const float* __restrict__ P, int splits,
                                                            float* __restrict__ C, int ldc,
-                                                           const float* __restrict__ bias, int relu) {
+                                                           const float* __restrict__ bias, int act) {
   const int n = blockIdx.x * 256 + threadIdx.x;
   const int m = blockIdx.y;
   if (n >= N) return;
@@ -145,7 +145,7 @@ __global__ __launch_bounds__(256) void sgemm_skinny_reduce(int M, int N, const f
     for (int q = 0; q < 16; ++q)
       if (i + q < splits) s += v[q];
   }
-  C[(long long)m * ldc + n] = epilogue(s, bias, n, relu);
+  C[(long long)m * ldc + n] = epilogue(s, bias, n, act);
 }
 
 // ---------------------------------------------------------------- 4 < m <= 32
@@ -446,7 +446,7 @@ __global__ __launch_bounds__(256, 1) void sgemm_skinny_w32(int M, int N, int K, 
 template <bool WIDE>
 __global__ __launch_bounds__(256) void sgemm_skinny_sk_reduce(int M, int N, const float* __restrict__ P, long long U,
                                                               int G, int kb, int smax, float* __restrict__ C,
-                                                              int ldc, const float* __restrict__ bias, int relu,
+                                                              int ldc, const float* __restrict__ bias, int act,
                                                               int cshift) {
   const int n = blockIdx.x * 256 + threadIdx.x;
   const int m = blockIdx.y;
@@ -470,20 +470,20 @@ __global__ __launch_bounds__(256) void sgemm_skinny_sk_reduce(int M, int N, cons
     for (int q = 0; q < 8; ++q)
       if (i + q < ns) s += v[q];
   }
-  C[(long long)m * ldc + n] = epilogue(s, bias, n, relu);
+  C[(long long)m * ldc + n] = epilogue(s, bias, n, act);
 }
 
 // Launch the split-k reduce of a stream-K plan (cols: partial block width, 256 or 128).
 hipError_t launch_sk_reduce(hipStream_t s, int m, int n, const float* P, long long U, int G, int kb, int smax,
-                            float* C, int ldc, const float* bias, int relu, int cols) {
+                            float* C, int ldc, const float* bias, int act, int cols) {
   const dim3 grid((unsigned)((n + 255) / 256), (unsigned)m);
   const int cshift = cols == 256 ? 8 : 7;
   if ((unsigned long long)U * (unsigned long long)G < (1ULL << 32))
     hipLaunchKernelGGL(sgemm_skinny_sk_reduce<false>, grid, dim3(256), 0, s, m, n, P, U, G, kb, smax, C, ldc, bias,
-                       relu, cshift);
+                       act, cshift);
   else
     hipLaunchKernelGGL(sgemm_skinny_sk_reduce<true>, grid, dim3(256), 0, s, m, n, P, U, G, kb, smax, C, ldc, bias,
-                       relu, cshift);
+                       act, cshift);
   return hipGetLastError();
 }
 
@@ -643,7 +643,7 @@ __global__ __launch_bounds__(256, 2) void sgemm_skinny_nt(int M, int N, int K, c
 // load is one ds_read_b128 per row of A.  Each lane keeps four
 // partial sums per row of A (one per float4 component); at the end of a row
 // they are added, summed over the wavefront (DPP all-reduce, fixed order),
-// and the epilogue (+ bias[n], ReLU) is applied before the store.  The row
+// and the epilogue (+ bias[n], activation) is applied before the store.  The row
 // count per wave differs by at most one across the workgroup.  EDGE: K is
 // not a multiple of 1024, so loads past K are clamped and zeroed.  Requires
 // K % 4 == 0, lda % 4 == 0, ldw % 4 == 0 and 16-byte aligned A and W.
@@ -664,7 +664,7 @@ __global__ __launch_bounds__(64 * kRowWaves, 1) void sgemm_skinny_nt_rows(int M,
                                                                          const float* __restrict__ W, int ldw,
                                                                          float* __restrict__ C, int ldc,
                                                                          const float* __restrict__ bias,
-                                                                         int relu) {
+                                                                         int act) {
   extern __shared__ float4 smem4[];
   float* as = reinterpret_cast<float*>(smem4);
   const int tid = threadIdx.x, lane = tid & 63;
@@ -730,7 +730,7 @@ __global__ __launch_bounds__(64 * kRowWaves, 1) void sgemm_skinny_nt_rows(int M,
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
       const float v = bch::wave_allreduce((acc[m].x + acc[m].y) + (acc[m].z + acc[m].w), bch::OpSum());
-      if (m < M && lane == 0) C[(long long)m * ldc + n] = epilogue(v, bias, n, relu);
+      if (m < M && lane == 0) C[(long long)m * ldc + n] = epilogue(v, bias, n, act);
       acc[m] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
   };
@@ -877,7 +877,7 @@ bool use_rows(int m, int n, int k) {
 
 template <int MT>
 hipError_t launch_rows(hipStream_t s, int m, int n, int k, const float* A, int lda, const float* W, int ldw, float* C,
-                       int ldc, const float* bias, int relu) {
+                       int ldc, const float* bias, int act) {
   const bool edge = k % kRowK != 0;
   const void* f = edge ? reinterpret_cast<const void*>(sgemm_skinny_nt_rows<MT, true>)
                        : reinterpret_cast<const void*>(sgemm_skinny_nt_rows<MT, false>);
@@ -887,10 +887,10 @@ hipError_t launch_rows(hipStream_t s, int m, int n, int k, const float* A, int l
   const dim3 grid(cu_count()), block(64 * kRowWaves);
   if (edge)
     hipLaunchKernelGGL((sgemm_skinny_nt_rows<MT, true>), grid, block, lds, s, m, n, k, A, lda, W, ldw, C, ldc, bias,
-                       relu);
+                       act);
   else
     hipLaunchKernelGGL((sgemm_skinny_nt_rows<MT, false>), grid, block, lds, s, m, n, k, A, lda, W, ldw, C, ldc, bias,
-                       relu);
+                       act);
   return hipGetLastError();
 }
 
@@ -935,12 +935,12 @@ size_t sgemm_skinny_nt_workspace_bytes(int m, int n, int k) {
 
 hipError_t launch_sgemm_skinny_nt(hipStream_t s, int m, int n, int k, const float* A, int lda, const float* W,
                                   int ldw, float* C, int ldc, void* ws, size_t ws_bytes, const float* bias,
-                                  int relu) {
+                                  int act) {
   if (use_rows(m, n, k)) {
     const int mt = rows_mt(m);
-    if (mt == 1) return launch_rows<1>(s, m, n, k, A, lda, W, ldw, C, ldc, bias, relu);
-    if (mt == 2) return launch_rows<2>(s, m, n, k, A, lda, W, ldw, C, ldc, bias, relu);
-    return launch_rows<4>(s, m, n, k, A, lda, W, ldw, C, ldc, bias, relu);
+    if (mt == 1) return launch_rows<1>(s, m, n, k, A, lda, W, ldw, C, ldc, bias, act);
+    if (mt == 2) return launch_rows<2>(s, m, n, k, A, lda, W, ldw, C, ldc, bias, act);
+    return launch_rows<4>(s, m, n, k, A, lda, W, ldw, C, ldc, bias, act);
   }
   if (ws == nullptr || ws_bytes < sgemm_skinny_nt_workspace_bytes(m, n, k)) return hipErrorInvalidValue;
   float* P = static_cast<float*>(ws);
@@ -964,7 +964,7 @@ hipError_t launch_sgemm_skinny_nt(hipStream_t s, int m, int n, int k, const floa
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  return launch_sk_reduce(s, m, n, P, p.U, p.G, p.nkb, p.smax, C, ldc, bias, relu, kNtRows);
+  return launch_sk_reduce(s, m, n, P, p.U, p.G, p.nkb, p.smax, C, ldc, bias, act, kNtRows);
 }
 
 size_t sgemm_skinny_workspace_bytes(int m, int n, int k) {
@@ -1005,7 +1005,7 @@ const char* sgemm_skinny_kernel_name(int m) {
 
 hipError_t launch_sgemm_skinny(hipStream_t s, int m, int n, int k, const float* A, int lda,
                                const float* B, int ldb, float* C, int ldc, void* ws, size_t ws_bytes,
-                               const float* bias, int relu) {
+                               const float* bias, int act) {
   if (ws == nullptr || ws_bytes < sgemm_skinny_workspace_bytes(m, n, k)) return hipErrorInvalidValue;
   float* P = static_cast<float*>(ws);
   const dim3 rgrid((unsigned)((n + 255) / 256), (unsigned)m);
@@ -1021,7 +1021,7 @@ hipError_t launch_sgemm_skinny(hipStream_t s, int m, int n, int k, const float* 
       hipLaunchKernelGGL(sgemm_skinny_fma<4>, grid, block, 0, s, m, n, k, A, lda, B, ldb, P, kchunk);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(sgemm_skinny_reduce, rgrid, dim3(256), 0, s, m, n, P, splits, C, ldc, bias, relu);
+    hipLaunchKernelGGL(sgemm_skinny_reduce, rgrid, dim3(256), 0, s, m, n, P, splits, C, ldc, bias, act);
     return hipGetLastError();
   }
   if (use_w32(m, k, A, lda)) {
@@ -1029,7 +1029,7 @@ hipError_t launch_sgemm_skinny(hipStream_t s, int m, int n, int k, const float* 
     hipError_t e = k % kW32Rows == 0 ? launch_w32<false>(s, q, m, n, k, A, lda, B, ldb, P)
                                      : launch_w32<true>(s, q, m, n, k, A, lda, B, ldb, P);
     if (e != hipSuccess) return e;
-    return launch_sk_reduce(s, m, n, P, q.U, q.G, q.nblk, q.smax, C, ldc, bias, relu, kSkCols);
+    return launch_sk_reduce(s, m, n, P, q.U, q.G, q.nblk, q.smax, C, ldc, bias, act, kSkCols);
   }
   const bool areg = sk_mb(m) == 1 && sk_areg(k, A, lda);
   const SkPlan p = sk_plan(m, n, k, areg);
@@ -1039,7 +1039,7 @@ hipError_t launch_sgemm_skinny(hipStream_t s, int m, int n, int k, const float* 
   else  // m > 16 with aligned A takes the 32x32x2 kernel above
     e = launch_sk<2, false>(s, p, m, n, k, A, lda, B, ldb, P);
   if (e != hipSuccess) return e;
-  return launch_sk_reduce(s, m, n, P, p.U, p.G, p.kb, p.smax, C, ldc, bias, relu, kSkCols);
+  return launch_sk_reduce(s, m, n, P, p.U, p.G, p.kb, p.smax, C, ldc, bias, act, kSkCols);
 }
 
 }  // namespace bch

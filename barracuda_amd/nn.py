@@ -25,12 +25,16 @@ from . import _native as N
 from .error import InvalidInput
 from .tensor import Tensor, _check_i32, _same_device
 
-__all__ = ["Activation", "fused_mlp"]
+__all__ = ["Activation", "fused_mlp", "linear"]
 
 
 class Activation(enum.Enum):
-    """fused_mlp.rs:25-31: the MLP's activation (only ReLU exists)."""
+    """fused_mlp.rs:25-31: the MLP's activation.  The reference has ReLU
+    only; GELU (the tanh form of shaders/activation/gelu_f64.wgsl, the
+    activation of transformer MLP blocks) is the same fused epilogue with
+    BCH_ACT_GELU."""
     ReLU = "ReLU"
+    GELU = "GELU"
 
 
 def fused_mlp(input: Tensor, weights: Sequence[Tensor], biases: Sequence[Tensor],
@@ -59,7 +63,7 @@ def fused_mlp(input: Tensor, weights: Sequence[Tensor], biases: Sequence[Tensor]
         layers.append((in_f, out_f, transb))
         in_features = out_f
     dev = _same_device(input, *weights, *biases)
-    act = N.BCH_ACT_RELU if activation is Activation.ReLU else N.BCH_ACT_NONE
+    act = {Activation.ReLU: N.BCH_ACT_RELU, Activation.GELU: N.BCH_ACT_GELU}[activation]
     x = input
     for (in_f, out_f, transb), w, b in zip(layers, weights, biases):
         _check_i32("fused_mlp", dev, batch=batch, in_features=in_f, out_features=out_f)
@@ -72,3 +76,27 @@ def fused_mlp(input: Tensor, weights: Sequence[Tensor], biases: Sequence[Tensor]
                                                 C.c_void_p(y.ptr), max(out_f, 1)), "fused_mlp")
         x = y
     return x
+
+
+def linear(input: Tensor, weight: Tensor, bias: Tensor | None = None, activation: Activation | None = None) -> Tensor:
+    """One layer of linear_f64.wgsl (y = x W^T + b, W [out, in]) with the
+    activation that follows it fused into the GEMM's epilogue: one launch,
+    the output written once.  input [batch, in]."""
+    shape, ws = input.shape(), weight.shape()
+    if len(shape) != 2 or len(ws) != 2 or ws[1] != shape[1]:
+        raise InvalidInput(f"linear: input {shape} and weight {ws} (expected [out, {shape[-1] if shape else '?'}])")
+    batch, in_f = shape
+    out_f = ws[0]
+    if bias is not None and bias.shape() != [out_f]:
+        raise InvalidInput("linear: bias shape mismatch")
+    dev = _same_device(input, weight, *([bias] if bias is not None else []))
+    _check_i32("linear", dev, batch=batch, in_features=in_f, out_features=out_f)
+    act = {None: N.BCH_ACT_NONE, Activation.ReLU: N.BCH_ACT_RELU, Activation.GELU: N.BCH_ACT_GELU}[activation]
+    y = Tensor.empty([batch, out_f], dev)
+    if batch * out_f:
+        with dev._lock:
+            dev.check(dev._lib.bch_sgemm_ex(dev.ctx, 1, batch, out_f, in_f, C.c_void_p(input.ptr), max(in_f, 1),
+                                            C.c_void_p(weight.ptr), max(in_f, 1),
+                                            C.c_void_p(bias.ptr) if bias is not None else None, act,
+                                            C.c_void_p(y.ptr), max(out_f, 1)), "linear")
+    return y

@@ -1,11 +1,15 @@
-"""TensorSession: record matmul / softmax / attention, then run them in one batch.
+"""TensorSession: record ops, then run them in one batch.
 
-Mirrors crates/barracuda/src/session/ for the ops of this path:
+Mirrors crates/barracuda/src/session/:
   AttentionDims {batch_size, n_heads, seq_len, head_dim}   session/mod.rs:60-99
   TensorSession::{new, with_device, reset, num_ops}        session/mod.rs:134-165
   TensorSession::{tensor, tensor_with_shape, import}       session/mod.rs:172-207
+  TensorSession::{add, sub, mul, negate, fma, scale}       session/mod.rs:214-300
   TensorSession::matmul                                    session/mod.rs:305-333
+  TensorSession::{relu, gelu}                              session/mod.rs:340-360
   TensorSession::softmax                                   session/mod.rs:364-371
+  TensorSession::layer_norm                                session/mod.rs:379-398
+  TensorSession::reshape                                   session/mod.rs:403-415
   TensorSession::attention                                 session/mod.rs:481-518
   TensorSession::run                                       session/mod.rs:521-540
   SessionTensor::{shape, len, is_empty, to_vec, to_tensor} session/tensor.rs:14-68
@@ -31,8 +35,10 @@ what the shader the reference session binds (softmax_simple_f64.wgsl)
 computes for each output it writes; attention is the non-causal
 softmax(Q K^T / sqrt(D)) V over [B, H, S, D].
 
-Element-wise ops, activations, layer_norm, reshape and head_split/concat of
-the reference session are not part of this path and are not provided.
+The element-wise ops, ReLU and GELU run on bch_elementwise; layer_norm on
+bch_layer_norm with the epsilon the reference session passes (1e-5,
+dispatch.rs:221-240).  head_split / head_concat are not provided: the fused
+attention reads projection outputs through strides instead.
 """
 from __future__ import annotations
 
@@ -43,11 +49,18 @@ from typing import Sequence
 import numpy as np
 
 from .error import CastOverflow, ExecutionError, InvalidInput, InvalidShape, ShapeMismatch, UnsupportedOperation
+from . import _native as N
 from .tensor import HipDevice, Tensor, _Buffer, _check_i32, _numel, get_device
 
 __all__ = ["AttentionDims", "SessionTensor", "TensorSession"]
 
 _U32_MAX = 2**32 - 1
+LAYER_NORM_EPS = 1e-5  # session/dispatch.rs:221-240
+
+# session op name -> (BCH_EW_* code, operands read)
+_ELEMENTWISE = {"add": (N.BCH_EW_ADD, 2), "sub": (N.BCH_EW_SUB, 2), "mul": (N.BCH_EW_MUL, 2),
+                "negate": (N.BCH_EW_NEG, 1), "fma": (N.BCH_EW_FMA, 3), "scale": (N.BCH_EW_SCALE, 1),
+                "relu": (N.BCH_EW_RELU, 1), "gelu": (N.BCH_EW_GELU, 1)}
 
 
 def _usize_as_u32(v: int) -> int:
@@ -175,6 +188,76 @@ class TensorSession:
         return self._register(buf, shape)
 
     # -- ops ---------------------------------------------------------------
+    def _same_shape(self, a: SessionTensor, b: SessionTensor) -> None:
+        """session/mod.rs:571-580 check_same_shape."""
+        if a._shape != b._shape:
+            raise ShapeMismatch(a._shape, b._shape)
+
+    def _elementwise(self, kind: str, *ins: SessionTensor, scalar: float = 0.0) -> SessionTensor:
+        self._own(*ins)
+        for t in ins[1:]:
+            self._same_shape(ins[0], t)
+        out = self._alloc_output(ins[0]._shape)
+        ids = [t.buffer_id for t in ins] + [None] * (3 - len(ins))
+        self._ops.append(("elementwise", kind, *ids, out.buffer_id, float(np.float32(scalar)), ins[0].len()))
+        return out
+
+    def add(self, a: SessionTensor, b: SessionTensor) -> SessionTensor:
+        """a + b element-wise (session/mod.rs:214-226)."""
+        return self._elementwise("add", a, b)
+
+    def sub(self, a: SessionTensor, b: SessionTensor) -> SessionTensor:
+        """a - b element-wise (session/mod.rs:228-240)."""
+        return self._elementwise("sub", a, b)
+
+    def mul(self, a: SessionTensor, b: SessionTensor) -> SessionTensor:
+        """a * b element-wise (session/mod.rs:242-254)."""
+        return self._elementwise("mul", a, b)
+
+    def negate(self, a: SessionTensor) -> SessionTensor:
+        """-a (session/mod.rs:256-264)."""
+        return self._elementwise("negate", a)
+
+    def fma(self, a: SessionTensor, b: SessionTensor, c: SessionTensor) -> SessionTensor:
+        """fma(a, b, c) element-wise; a, b and c share one shape (session/mod.rs:268-287)."""
+        return self._elementwise("fma", a, b, c)
+
+    def scale(self, a: SessionTensor, scalar: float) -> SessionTensor:
+        """a * scalar, the scalar as f32 (session/mod.rs:289-300)."""
+        return self._elementwise("scale", a, scalar=scalar)
+
+    def relu(self, a: SessionTensor) -> SessionTensor:
+        """max(0, a) (session/mod.rs:340-347)."""
+        return self._elementwise("relu", a)
+
+    def gelu(self, a: SessionTensor) -> SessionTensor:
+        """Tanh-form GELU, gelu_f64.wgsl (session/mod.rs:352-359)."""
+        return self._elementwise("gelu", a)
+
+    def layer_norm(self, a: SessionTensor, feature_size: int) -> SessionTensor:
+        """Layer norm over consecutive groups of `feature_size` elements
+        (session/mod.rs:379-398): InvalidInput when the element count is not
+        a multiple of feature_size; epsilon 1e-5."""
+        self._own(a)
+        total = a.len()
+        feature_size = int(feature_size)
+        if feature_size == 0 or total % feature_size:
+            raise InvalidInput(f"layer_norm: total {total} not divisible by feature_size {feature_size}")
+        _usize_as_u32(feature_size)
+        out = self._alloc_output(a._shape)
+        self._ops.append(("layer_norm", a.buffer_id, out.buffer_id, total // feature_size, feature_size))
+        return out
+
+    def reshape(self, a: SessionTensor, new_shape: Sequence[int]) -> SessionTensor:
+        """Metadata only: the same buffer with a new shape of the same element
+        count, ShapeMismatch(new, old) otherwise (session/mod.rs:403-415)."""
+        self._own(a)
+        new_shape = [int(x) for x in new_shape]
+        if _numel(new_shape) != a.len():
+            raise ShapeMismatch(new_shape, a._shape)
+        return SessionTensor(self, a.buffer_id, new_shape)
+
+    # -- ops ---------------------------------------------------------------
     def matmul(self, a: SessionTensor, b: SessionTensor) -> SessionTensor:
         """output[m x n] = a[m x k] b[k x n] (session/mod.rs:305-333)."""
         self._own(a, b)
@@ -235,6 +318,18 @@ class TensorSession:
                     if m and n:
                         dev.check(lib.bch_sgemm(ctx, m, n, k, ptr[a], max(k, 1), ptr[b], max(n, 1), ptr[o],
                                                 max(n, 1)), "matmul")
+                elif kind == "elementwise":
+                    _, name, a, b, c, o, scalar, n = op
+                    if n:
+                        code = _ELEMENTWISE[name][0]
+                        pb = ptr[b] if b is not None else None
+                        pc = ptr[c] if c is not None else None
+                        dev.check(lib.bch_elementwise(ctx, code, n, ptr[a], pb, pc, scalar, ptr[o]), name)
+                elif kind == "layer_norm":
+                    _, a, o, rows, cols = op
+                    if rows * cols:
+                        dev.check(lib.bch_layer_norm(ctx, rows, cols, LAYER_NORM_EPS, ptr[a], ptr[o]),
+                                  "layer_norm")
                 elif kind == "softmax":
                     _, a, o, size = op
                     if size:

@@ -38,6 +38,7 @@ __all__ = [
     "HipDevice", "get_device", "Tensor", "MatMul", "MatmulTiled", "BatchMatMul",
     "Softmax", "Attention", "ScaledDotProductAttention", "CausalAttention",
     "FlashAttention", "GroupedQueryAttention", "MultiHeadAttention", "LcgStream",
+    "ReLU", "GELU", "LayerNorm",
 ]
 
 
@@ -274,6 +275,18 @@ class Tensor:
                       "softmax_dim")
         return out
 
+    def relu(self) -> "Tensor":
+        """ops/relu.rs:106: max(x, 0) element-wise."""
+        return ReLU(self).execute()
+
+    def gelu_wgsl(self) -> "Tensor":
+        """ops/gelu_wgsl.rs:147: tanh-form GELU element-wise."""
+        return GELU(self).execute()
+
+    def layer_norm_wgsl(self, epsilon: float) -> "Tensor":
+        """ops/layer_norm_wgsl.rs:160-165: layer norm over the last axis."""
+        return LayerNorm(self, epsilon).execute()
+
     def attention(self, key: "Tensor", value: "Tensor") -> "Tensor":
         return Attention(self, key, value).execute()
 
@@ -418,6 +431,63 @@ class Softmax:
         with dev._lock:
             dev.check(dev._lib.bch_softmax_rows(dev.ctx, 1, size, C.c_void_p(self.t.ptr),
                                                 C.c_void_p(out.ptr)), "softmax")
+        return out
+
+
+def _elementwise(dev: HipDevice, op: int, out: Tensor, a: Tensor, b: Tensor | None = None,
+                 c: Tensor | None = None, scalar: float = 0.0, name: str = "elementwise") -> Tensor:
+    n = out.len()
+    if n:
+        p = lambda t: C.c_void_p(t.ptr) if t is not None else None
+        with dev._lock:
+            dev.check(dev._lib.bch_elementwise(dev.ctx, op, n, p(a), p(b), p(c), float(scalar), p(out)), name)
+    return out
+
+
+class ReLU:
+    """ops/relu.rs: max(x, 0) over every element (relu_f64.wgsl)."""
+
+    def __init__(self, input: Tensor):
+        self.input = input
+
+    def execute(self) -> Tensor:
+        dev = self.input.device()
+        return _elementwise(dev, N.BCH_EW_RELU, Tensor.empty(self.input.shape(), dev), self.input, name="relu")
+
+
+class GELU:
+    """ops/gelu_wgsl.rs:33-141: x Phi(x) in the tanh form of gelu_f64.wgsl,
+    0.5 x (1 + tanh(0.7978845608 (x + 0.044715 x^3))), over every element."""
+
+    def __init__(self, input: Tensor):
+        self.input = input
+
+    def execute(self) -> Tensor:
+        dev = self.input.device()
+        return _elementwise(dev, N.BCH_EW_GELU, Tensor.empty(self.input.shape(), dev), self.input, name="gelu")
+
+
+class LayerNorm:
+    """ops/layer_norm_wgsl.rs:47-157: normalise each row along the last
+    dimension, (x - mean) / sqrt(var + epsilon), biased variance, no affine
+    parameters (layer_norm_f64.wgsl)."""
+
+    def __init__(self, input: Tensor, epsilon: float):
+        self.input = input
+        self.epsilon = float(epsilon)
+
+    def execute(self) -> Tensor:
+        shape = self.input.shape()
+        if not shape:
+            raise InvalidOperation("LayerNorm", "Empty tensor not supported")
+        dev = self.input.device()
+        out = Tensor.empty(shape, dev)
+        cols = shape[-1]
+        rows = _numel(shape[:-1])
+        if rows * cols:
+            with dev._lock:
+                dev.check(dev._lib.bch_layer_norm(dev.ctx, rows, cols, self.epsilon, C.c_void_p(self.input.ptr),
+                                                  C.c_void_p(out.ptr)), "layer_norm")
         return out
 
 

@@ -35,8 +35,8 @@ HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, published
 FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense FP32 matrix, published
 FP64_MFMA_PEAK_TFLOPS = 78.6   # MI355X dense FP64 matrix, published
 PROFILES = ROOT / "profiles"
-# Untimed launches before every timed region continue until this much wall
-# time has passed since the first warmup launch (the clock settle).
+# Before every timed region's warmup launches, another kernel keeps the GPU
+# busy for this long (the clock settle, ClockWarmer).
 SETTLE_MS = 60.0
 
 
@@ -44,20 +44,47 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
+class ClockWarmer:
+    """Brings the clocks to steady state before a timed region with a kernel
+    other than the one about to be timed: the 4096^3 GEMM with B given as
+    [n][k] (bch_sgemm_ex, transb, no epilogue), a different kernel
+    instantiation from every workload here.  From idle the clocks take ~25
+    ms of full load to settle (measured on the box: 4096^3 launches go
+    1100-1190 us -> 940-945 us over the first ~25 launches), and each
+    workload starts after host-side set-up has left the GPU idle.  Warming
+    with another kernel keeps the timed kernel's own launches (W warmup + K
+    timed) all at steady clocks, so a profiler's per-kernel average over the
+    run agrees with the HIP-event average of the timed launches."""
+
+    N = 4096
+
+    def __init__(self, dev):
+        from barracuda_amd import LcgStream, Tensor
+        self.dev = dev
+        s = LcgStream(17, dev)
+        self._a, self._b = s.uniform([self.N, self.N]), s.uniform([self.N, self.N])
+        self._c = Tensor.empty([self.N, self.N], dev)
+
+    def run(self, ms: float) -> None:
+        dev, lib, n = self.dev, self.dev._lib, self.N
+        pa, pb, pc = C.c_void_p(self._a.ptr), C.c_void_p(self._b.ptr), C.c_void_p(self._c.ptr)
+        t0 = time.perf_counter()
+        while (time.perf_counter() - t0) * 1e3 < ms:
+            for _ in range(4):
+                dev.check(lib.bch_sgemm_ex(dev.ctx, 1, n, n, n, pa, n, pb, n, None, 0, pc, n), "clock warm-up")
+            dev.sync()
+
+
 class Timer:
     """HIP events on the context's stream + wall clock around K launches.
 
-    `warm_ms`: after the warmup launches, keep launching (untimed) until that
-    much wall time has passed.  Measured on the box: from idle, the clocks
-    take ~25 ms of full load to settle (GEMM 4096^3 launches go 1100-1190 us
-    -> 940-945 us over the first ~25 launches; the first 12 attention
-    launches of a process average 2.19 ms against 2.06 ms afterwards), and
-    each extra workload starts after host-side input generation has left
-    the GPU idle."""
+    Before the W warmup launches, the ClockWarmer keeps the GPU busy with
+    another kernel for `warm_ms` (the clock settle)."""
 
-    def __init__(self, dev, warm_ms: float = 0.0):
+    def __init__(self, dev, warm_ms: float = 0.0, warmer: ClockWarmer | None = None):
         self.dev = dev
         self.warm_ms = warm_ms
+        self.warmer = warmer if warmer is not None or warm_ms <= 0 else ClockWarmer(dev)
         lib = dev._lib
         self.e0, self.e1 = C.c_void_p(), C.c_void_p()
         dev.check(lib.bch_event_create(dev.ctx, C.byref(self.e0)), "event")
@@ -65,14 +92,11 @@ class Timer:
 
     def run(self, fn, steps: int, warmup: int):
         lib, dev = self.dev._lib, self.dev
-        tw = time.perf_counter()
+        if self.warmer is not None:
+            self.warmer.run(self.warm_ms)
         for _ in range(warmup):
             fn(0)
         dev.sync()
-        while (time.perf_counter() - tw) * 1e3 < self.warm_ms:
-            for _ in range(max(1, warmup)):
-                fn(0)
-            dev.sync()
         t0 = time.perf_counter()
         dev.check(lib.bch_event_record(dev.ctx, self.e0), "event")
         for i in range(steps):
@@ -98,7 +122,7 @@ def load_traffic(key: str):
         return None
 
 
-def bench_gemm(dev, steps, warmup):
+def bench_gemm(dev, steps, warmup, warmer=None):
     from barracuda_amd import LcgStream
     lib = dev._lib
     n = 4096
@@ -116,20 +140,20 @@ def bench_gemm(dev, steps, warmup):
     # The same clock settle as every other workload: from idle, the clocks
     # take ~25 ms of full load to reach steady state, so W warmup launches
     # alone (the driver passes W = 5) would time the ramp.
-    wall_ms, ev_ms = Timer(dev, warm_ms=SETTLE_MS).run(step, steps, warmup)
+    wall_ms, ev_ms = Timer(dev, warm_ms=SETTLE_MS, warmer=warmer).run(step, steps, warmup)
     flops = 2.0 * n ** 3
     return {"wall_ms": wall_ms, "kernel_ms": ev_ms, "flops": flops,
             "kernel": lib.bch_sgemm_kernel_name(n, n, n).decode()}, (a, b, c)
 
 
-WORKLOADS = ("softmax", "skinny", "batched", "sdpa", "linear", "dgemm", "copy")
+WORKLOADS = ("softmax", "skinny", "batched", "sdpa", "linear", "dgemm", "norm", "copy")
 
 
-def bench_extra(dev, reps: int = 20, only=None):
+def bench_extra(dev, reps: int = 20, only=None, warmer=None):
     """The other BASELINE configs, each timed over `reps` launches."""
     from barracuda_amd import LcgStream, Tensor
     lib, ctx = dev._lib, dev.ctx
-    T = Timer(dev, warm_ms=SETTLE_MS)
+    T = Timer(dev, warm_ms=SETTLE_MS, warmer=warmer)
     out = {}
     want = set(only) if only else set(WORKLOADS) - {"copy"}
 
@@ -155,6 +179,33 @@ def bench_extra(dev, reps: int = 20, only=None):
         out.update(_bench_linear(dev, T, reps))
     if "dgemm" in want:
         out.update(_bench_dgemm(dev, T, reps))
+    if "norm" in want:
+        out.update(_bench_norm(dev, T, reps))
+    return out
+
+
+def _bench_norm(dev, T, reps):
+    """The steps either side of the path (TensorSession::layer_norm and
+    ::gelu, session/mod.rs:349-398) at the softmax config's size: layer norm
+    of [65536 x 2048] (one read + one write, 8 B per element) and GELU over
+    the same 2^27 elements, both HBM-bound."""
+    from barracuda_amd import LcgStream, Tensor
+    from barracuda_amd import _native as N
+    lib, ctx = dev._lib, dev.ctx
+    out = {}
+    rows, cols = 65536, 2048
+    x = LcgStream(1, dev).normal([rows, cols], 0.0, 3.0)
+    y = Tensor.empty([rows, cols], dev)
+    px, py = C.c_void_p(x.ptr), C.c_void_p(y.ptr)
+    nbytes = 2 * 4 * rows * cols
+    wall, ev = T.run(lambda i: lib.bch_layer_norm(ctx, rows, cols, 1e-5, px, py), reps, 3)
+    out["layer_norm_65536x2048"] = {"GB/s": nbytes / (ev * 1e-3) / 1e9, "us": ev * 1e3, "bytes_per_launch": nbytes,
+                                    "hbm_frac": nbytes / (ev * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                                    "kernel": lib.bch_layer_norm_kernel_name(rows, cols).decode()}
+    n = rows * cols
+    wall, ev = T.run(lambda i: lib.bch_elementwise(ctx, N.BCH_EW_GELU, n, px, None, None, 0.0, py), reps, 3)
+    out["gelu_2^27"] = {"GB/s": nbytes / (ev * 1e-3) / 1e9, "us": ev * 1e3, "bytes_per_launch": nbytes,
+                        "hbm_frac": nbytes / (ev * 1e-3) / 1e9 / HBM_PEAK_GBS}
     return out
 
 
@@ -192,6 +243,9 @@ def _bench_linear(dev, T, reps):
     fl = 2.0 * n ** 3
     out = {"linear_4096_wT_bias_relu": {"TFLOP/s": fl / (ev * 1e-3) / 1e12, "ms": ev,
                                         "mfma_frac": fl / (ev * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS}}
+    wall, ev = T.run(lambda i: lib.bch_sgemm_ex(ctx, 1, n, n, n, px, n, pw, n, pb, N.BCH_ACT_GELU, py, n), reps, 3)
+    out["linear_4096_wT_bias_gelu"] = {"TFLOP/s": fl / (ev * 1e-3) / 1e12, "ms": ev,
+                                       "mfma_frac": fl / (ev * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS}
     del x, w, b, y
     # decode-sized layers with [out, in] weights (the skinny config's shape, W^T): HBM-bound
     K, Nn = 4096, 11008
@@ -394,7 +448,7 @@ def cpu_baselines(target_s: float = 12.0, extra: bool = True):
     # config 3b: batched 16 x 1024^3, execute_matmul_cpu per batch on a row sample of every batch
     s2 = O.Lcg(2)
     ab, bb = s2.uniform((16, 1024, 1024)), s2.uniform((16, 1024, 1024))
-    rb = threads  # rows per batch in the sample: one per thread
+    rb = 4 * threads  # rows per batch in the sample: four per thread
     t0 = time.perf_counter()
     for i in range(16):
         O.matmul_cpu_exec_f32(ab[i], bb[i], 0, rb)
@@ -460,28 +514,29 @@ def main() -> int:
 
     from barracuda_amd import get_device
     dev = get_device()
+    warmer = ClockWarmer(dev)
     if args.only:
         sel = [w.strip() for w in args.only.split(",") if w.strip()]
         res = {}
         if "gemm" in sel:
-            g, keep = bench_gemm(dev, args.steps, args.warmup)
+            g, keep = bench_gemm(dev, args.steps, args.warmup, warmer)
             res["gemm_4096"] = {"TFLOP/s": g["flops"] / (g["kernel_ms"] * 1e-3) / 1e12, "ms": g["kernel_ms"]}
             del keep
         rest = [w for w in sel if w != "gemm"]
         if rest:
-            res.update(bench_extra(dev, only=rest))
+            res.update(bench_extra(dev, only=rest, warmer=warmer))
         print(json.dumps({"only": sel, "results": res}), flush=True)
         return 0
     log(f"gemm 4096^3: {args.warmup} warmup + {args.steps} timed launches")
-    g, keep = bench_gemm(dev, args.steps, args.warmup)
+    g, keep = bench_gemm(dev, args.steps, args.warmup, warmer)
     value = g["flops"] / (g["wall_ms"] * 1e-3) / 1e12
     achieved = g["flops"] / (g["kernel_ms"] * 1e-3) / 1e12
     log(f"  wall {g['wall_ms']:.3f} ms/step, kernel {g['kernel_ms']:.3f} ms -> {achieved:.1f} TFLOP/s")
     del keep
     extra = None
     if not args.no_extra:
-        log("extra configs: softmax, skinny, batched, sdpa, linear, dgemm")
-        extra = bench_extra(dev)
+        log("extra configs: softmax, skinny, batched, sdpa, linear, dgemm, norm")
+        extra = bench_extra(dev, warmer=warmer)
         for k_, v_ in extra.items():
             log(f"  {k_}: {json.dumps({kk: round(vv, 4) if isinstance(vv, float) else vv for kk, vv in v_.items()})}")
     cpu = None

@@ -127,16 +127,19 @@ bch_status bch_sgemm_noalloc(bch_ctx *ctx, int m, int n, int k,
 /* Activation of bch_sgemm_ex's epilogue. */
 #define BCH_ACT_NONE 0
 #define BCH_ACT_RELU 1 /* max(x, 0): shaders/activation/relu_f64.wgsl */
+#define BCH_ACT_GELU 2 /* 0.5 x (1 + tanh(0.7978845608 (x + 0.044715 x^3))):
+                        * shaders/activation/gelu_f64.wgsl (run in f32 with
+                        * WGSL's tanh); large |x| gives x (or -0) */
 
 /* The linear layer: C = act(A . op(B) + bias), row-major, where op(B) = B
  * for transb == 0 (B [k, n], ldb >= n) and B^T for transb == 1 (B [n, k],
  * ldb >= k: the weight layout [out_features, in_features] of
  * shaders/misc/linear_f64.wgsl, y = x W^T + b).  bias (nullable) has n
  * entries and is added after the dot product, as linear_f64.wgsl does; act
- * is BCH_ACT_NONE or BCH_ACT_RELU.  Everything happens in the GEMM's own
- * epilogue: one launch per layer where the reference's nn::fused_mlp
- * (nn/fused_mlp.rs:38-168) dispatches linear_f64.wgsl and then
- * relu_f64.wgsl over the output.  transb == 0, act == NONE, bias == NULL is
+ * is BCH_ACT_NONE, BCH_ACT_RELU or BCH_ACT_GELU.  Everything happens in the
+ * GEMM's own epilogue: one launch per layer where the reference's
+ * nn::fused_mlp (nn/fused_mlp.rs:38-168) dispatches linear_f64.wgsl and
+ * then relu_f64.wgsl (gelu_f64.wgsl, ops/gelu_wgsl.rs) over the output.  transb == 0, act == NONE, bias == NULL is
  * bch_sgemm. */
 bch_status bch_sgemm_ex(bch_ctx *ctx, int transb, int m, int n, int k,
                         const float *A, int lda, const float *B, int ldb,
@@ -175,6 +178,36 @@ bch_status bch_dgemm(bch_ctx *ctx, int transa, int transb, int batch, int m,
  * softmax_simple_f64.wgsl). */
 bch_status bch_softmax_rows(bch_ctx *ctx, long long rows, long long cols,
                             const float *in, float *out);
+
+/* Element-wise ops of TensorSession over n f32 elements:
+ *   BCH_EW_ADD out = a + b      BCH_EW_SUB out = a - b     BCH_EW_MUL out = a * b
+ *   BCH_EW_NEG out = -a         BCH_EW_FMA out = fma(a, b, c)
+ *   BCH_EW_SCALE out = a * scalar
+ *   BCH_EW_RELU out = max(a, 0) BCH_EW_GELU out = GELU(a) (as BCH_ACT_GELU)
+ * b is read by add/sub/mul/fma, c by fma only (others may be NULL); out may
+ * equal a, b or c.  Replaces the session's inline add/sub/mul/negate/fma/
+ * scale shaders (session/pipelines.rs:76-145, dispatch.rs) and its ReLU and
+ * GELU ops (session/mod.rs:340-359: ops/relu.rs, ops/gelu_wgsl.rs). */
+#define BCH_EW_ADD 0
+#define BCH_EW_SUB 1
+#define BCH_EW_MUL 2
+#define BCH_EW_NEG 3
+#define BCH_EW_FMA 4
+#define BCH_EW_SCALE 5
+#define BCH_EW_RELU 6
+#define BCH_EW_GELU 7
+bch_status bch_elementwise(bch_ctx *ctx, int op, long long n, const float *a,
+                           const float *b, const float *c, float scalar,
+                           float *out);
+
+/* Layer normalisation of each row of a [rows, cols] f32 matrix:
+ *   out = (x - mean) / sqrt(var + eps), mean and (biased) var over the row.
+ * No affine parameters; in == out is allowed.  Replaces
+ * TensorSession::layer_norm (session/mod.rs:379-398, epsilon 1e-5 at
+ * dispatch.rs:221-240) and LayerNorm::execute / Tensor::layer_norm_wgsl
+ * (ops/layer_norm_wgsl.rs, shaders/norm/layer_norm_f64.wgsl). */
+bch_status bch_layer_norm(bch_ctx *ctx, long long rows, long long cols,
+                          float eps, const float *in, float *out);
 
 /* Softmax along a middle axis of a tensor viewed as [outer, axis, inner]
  * (element (o,j,i) at (o*axis + j)*inner + i).  inner == 1 is the row case.
@@ -268,6 +301,7 @@ void bch_event_destroy(bch_event *ev);
 /* Name of the kernel a bch_sgemm / bch_softmax_rows / bch_sdpa_fwd call of
  * this shape launches (for profilers and tests; NULL ctx allowed). */
 const char *bch_sgemm_kernel_name(int m, int n, int k);
+const char *bch_layer_norm_kernel_name(long long rows, long long cols);
 
 #ifdef __cplusplus
 }

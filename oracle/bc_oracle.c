@@ -596,3 +596,78 @@ BCO_API void bco_set_num_threads(int n)
     (void)n;
 #endif
 }
+
+/* ------------------------------------------------------------------------
+ * 4. The steps either side of the path: GELU and layer norm (TensorSession
+ *    session/mod.rs:349-398, dispatch.rs:196-240; the GEMM epilogue)
+ * ---------------------------------------------------------------------- */
+
+/* shaders/activation/gelu_f64.wgsl:17-31 in double:
+ * 0.5 x (1 + tanh(0.7978845608 (x + 0.044715 x^3))), libm tanh. */
+BCO_API void bco_gelu_f64(size_t n, const float *x, double *y)
+{
+    for (size_t i = 0; i < n; ++i) {
+        double v = (double)x[i];
+        double x3 = v * v * v;
+        double inner = 0.7978845608 * (v + 0.044715 * x3);
+        y[i] = 0.5 * v * (1.0 + tanh(inner));
+    }
+}
+
+/* gelu_f64.wgsl as the session runs it: downcast to f32 with tanh_f64 ->
+ * the WGSL tanh builtin (shaders/precision/compiler.rs:91-109, bound at
+ * session/pipelines.rs:54-62,154), same operation order. */
+BCO_API void bco_gelu_wgsl_f32(size_t n, const float *x, float *y)
+{
+    for (size_t i = 0; i < n; ++i) {
+        float v = x[i];
+        float x3 = v * v * v;
+        float inner = 0.7978845608f * (v + 0.044715f * x3);
+        y[i] = 0.5f * v * (1.0f + tanhf(inner));
+    }
+}
+
+/* shaders/norm/layer_norm_f64.wgsl:20-50 in double: per row, sequential
+ * mean, two-pass biased variance, (x - mean) / sqrt(var + eps). */
+BCO_API void bco_layer_norm_f64(long rows, long cols, double eps,
+                                const float *x, double *y)
+{
+    #pragma omp parallel for schedule(static)
+    for (long r = 0; r < rows; ++r) {
+        const float *xr = x + r * cols;
+        double *yr = y + r * cols;
+        double sum = 0.0;
+        for (long i = 0; i < cols; ++i) sum += (double)xr[i];
+        double mean = sum / (double)cols;
+        double var_sum = 0.0;
+        for (long i = 0; i < cols; ++i) {
+            double d = (double)xr[i] - mean;
+            var_sum += d * d;
+        }
+        double sd = sqrt(var_sum / (double)cols + eps);
+        for (long i = 0; i < cols; ++i) yr[i] = ((double)xr[i] - mean) / sd;
+    }
+}
+
+/* layer_norm_f64.wgsl downcast to f32 (sqrt_f64 -> sqrt): the same steps
+ * in f32 with sequential sums, one thread per row as the shader runs. */
+BCO_API void bco_layer_norm_f32(long rows, long cols, float eps,
+                                const float *x, float *y)
+{
+    #pragma omp parallel for schedule(static)
+    for (long r = 0; r < rows; ++r) {
+        const float *xr = x + r * cols;
+        float *yr = y + r * cols;
+        float sum = 0.0f;
+        for (long i = 0; i < cols; ++i) sum = sum + xr[i];
+        float mean = sum / (float)cols;
+        float var_sum = 0.0f;
+        for (long i = 0; i < cols; ++i) {
+            float d = xr[i] - mean;
+            var_sum = var_sum + d * d;
+        }
+        float variance = var_sum / (float)cols;
+        float sd = sqrtf(variance + eps);
+        for (long i = 0; i < cols; ++i) yr[i] = (xr[i] - mean) / sd;
+    }
+}

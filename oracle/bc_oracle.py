@@ -54,6 +54,10 @@ def lib() -> C.CDLL:
         L.bco_max_rel_err_f32ref.argtypes = [C.c_size_t, _fp, _fp]
         L.bco_num_threads.restype = C.c_int
         L.bco_set_num_threads.argtypes = [C.c_int]
+        L.bco_gelu_f64.argtypes = [C.c_size_t, _fp, _dp]
+        L.bco_gelu_wgsl_f32.argtypes = [C.c_size_t, _fp, _fp]
+        L.bco_layer_norm_f64.argtypes = [C.c_long, C.c_long, C.c_double, _fp, _dp]
+        L.bco_layer_norm_f32.argtypes = [C.c_long, C.c_long, C.c_float, _fp, _fp]
         _lib = L
     return _lib
 
@@ -301,6 +305,41 @@ def gemm_longdouble(a, b, m: int, k: int, n: int, batch: int, trans_a: bool = Fa
     if trans_b:
         B = B.transpose(0, 2, 1)
     return np.matmul(A, B).reshape(-1)
+
+
+# ---- GELU and layer norm (session/mod.rs:349-398) -----------------------------------
+def gelu_f64(x) -> np.ndarray:
+    """gelu_f64.wgsl:17-31 in float64 (libm tanh)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty(x.shape, dtype=np.float64)
+    lib().bco_gelu_f64(x.size, _f(x), _d(y))
+    return y
+
+
+def gelu_wgsl_f32(x) -> np.ndarray:
+    """gelu_f64.wgsl downcast to f32 with the tanh builtin (compiler.rs:91-109)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty_like(x)
+    lib().bco_gelu_wgsl_f32(x.size, _f(x), _f(y))
+    return y
+
+
+def layer_norm_f64(x, eps: float = 1e-5) -> np.ndarray:
+    """layer_norm_f64.wgsl:20-50 in float64 over the last axis."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    cols = x.shape[-1]
+    y = np.empty(x.shape, dtype=np.float64)
+    lib().bco_layer_norm_f64(x.size // cols, cols, eps, _f(x), _d(y))
+    return y
+
+
+def layer_norm_f32(x, eps: float = 1e-5) -> np.ndarray:
+    """layer_norm_f64.wgsl downcast to f32: sequential sums, one row per thread."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    cols = x.shape[-1]
+    y = np.empty_like(x)
+    lib().bco_layer_norm_f32(x.size // cols, cols, eps, _f(x), _f(y))
+    return y
 
 
 # ---- metric (tolerances/mod.rs:44-54 scale) ---------------------------------------

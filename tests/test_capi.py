@@ -250,3 +250,23 @@ def test_sgemm_noalloc_validation_before_device():
     assert "leading dimension" in N.last_error(None)
     assert lib.bch_sgemm_noalloc(nul, 4, 4, 4, nul, 4, nul, 4, nul, 4) == N.BCH_E_INVALID
     assert "ctx" in N.last_error(None)
+
+
+def test_elementwise_and_layer_norm_validation_before_device():
+    lib = N.load()
+    nul = C.c_void_p()
+    assert lib.bch_elementwise(nul, 8, 4, nul, nul, nul, 0.0, nul) == N.BCH_E_INVALID
+    assert "unknown op" in N.last_error(None)
+    assert lib.bch_elementwise(nul, N.BCH_EW_ADD, -1, nul, nul, nul, 0.0, nul) == N.BCH_E_SHAPE
+    assert lib.bch_elementwise(nul, N.BCH_EW_GELU, 4, nul, nul, nul, 0.0, nul) == N.BCH_E_INVALID
+    assert lib.bch_layer_norm(nul, 0, 4, 1e-5, nul, nul) == N.BCH_E_SHAPE
+    assert lib.bch_layer_norm(nul, 4, 4, -1.0, nul, nul) == N.BCH_E_INVALID
+    assert lib.bch_layer_norm(nul, 4, 4, float("nan"), nul, nul) == N.BCH_E_INVALID
+    assert lib.bch_layer_norm(nul, 1 << 31, 4, 1e-5, nul, nul) == N.BCH_E_UNSUPPORTED
+    assert lib.bch_layer_norm(nul, 4, 4, 1e-5, nul, nul) == N.BCH_E_INVALID
+    assert "ctx" in N.last_error(None)
+    assert lib.bch_sgemm_ex(nul, 0, 4, 4, 4, nul, 4, nul, 4, nul, 3, nul, 4) == N.BCH_E_INVALID
+    assert lib.bch_sgemm_ex(nul, 1, 4, 4, 4, nul, 4, nul, 4, nul, N.BCH_ACT_GELU, nul, 4) == N.BCH_E_INVALID
+    assert "ctx" in N.last_error(None)
+    assert lib.bch_layer_norm_kernel_name(65536, 2048) == b"layer_norm_wave<8>"
+    assert lib.bch_layer_norm_kernel_name(3, 4100) == b"layer_norm_block"

@@ -282,3 +282,72 @@ def test_sdpa_f64_rows_equals_full_oracle_rows():
         full = O.sdpa_f64(q, k, v, causal).reshape(6, 40, 16)
         got = O.sdpa_f64_rows(q, k, v, causal, rows)
         assert np.array_equal(got, np.take_along_axis(full, rows[:, :, None].astype(np.int64), axis=1))
+
+
+# ---- GELU and layer norm (session/mod.rs:349-398) --------------------------------
+def test_gelu_oracle_reference_assertions_and_identities():
+    """activations.rs:237-242 (GELU(0) = 0, GELU(10) > 9.99, |GELU(-10)| <
+    0.01); the odd-part identity GELU(x) - GELU(-x) = x of the tanh form; the
+    erf form x Phi(x) it approximates (tanh-form error below 5e-4 over
+    [-8, 8]: a dropped cubic term is 0.034 off, a 0.04 coefficient 0.003)."""
+    from scipy.special import erf
+    g = O.gelu_f64(np.array([0.0, 10.0, -10.0], np.float32))
+    assert g[0] == 0.0 and g[1] > 9.99 and abs(g[2]) < 0.01
+    x = np.linspace(-8, 8, 40001).astype(np.float32)
+    gx, gn = O.gelu_f64(x), O.gelu_f64(-x)
+    xd = x.astype(np.float64)
+    assert np.max(np.abs((gx - gn) - xd)) < 1e-12
+    exact = 0.5 * xd * (1.0 + erf(xd / np.sqrt(2.0)))
+    assert np.max(np.abs(gx - exact)) < 5e-4
+    # large |x|: x and 0
+    big = np.array([30.0, 1e4, -30.0, -1e4], np.float32)
+    assert np.array_equal(O.gelu_f64(big), np.array([30.0, 1e4, -0.0, -0.0]))
+
+
+def test_gelu_planted_mistakes_fail():
+    from scipy.special import erf
+    x = np.linspace(-8, 8, 4001)
+    exact = 0.5 * x * (1.0 + erf(x / np.sqrt(2.0)))
+    no_cubic = 0.5 * x * (1.0 + np.tanh(0.7978845608 * x))
+    wrong_sign = 0.5 * x * (1.0 - np.tanh(0.7978845608 * (x + 0.044715 * x ** 3)))
+    assert np.max(np.abs(no_cubic - exact)) > 5e-4
+    assert np.max(np.abs(wrong_sign - exact)) > 5e-4
+
+
+def test_gelu_f32_restatement_tracks_f64():
+    x = O.Lcg(11).normal((100000,), 0.0, 4.0)
+    assert O.max_rel_err(O.gelu_wgsl_f32(x), O.gelu_f64(x)) < 1e-6
+
+
+def test_layer_norm_oracle_closed_forms():
+    """layer_norm_f64.wgsl on [1,2,3,4]: mean 2.5, biased var 1.25 (an
+    unbiased n-1 variance would be 5/3); the reference tests' vectors
+    (ops/layer_norm_wgsl.rs:166-192: row means below 1e-5); output mean 0
+    and biased variance var / (var + eps) on random rows; a constant row is
+    0 (eps keeps 0 / sqrt(eps) finite); shift/scale invariance."""
+    y = O.layer_norm_f64(np.array([[1, 2, 3, 4]], np.float32))
+    want = (np.array([1, 2, 3, 4]) - 2.5) / np.sqrt(1.25 + 1e-5)
+    assert np.max(np.abs(y[0] - want)) < 1e-12
+    wrong = (np.array([1, 2, 3, 4]) - 2.5) / np.sqrt(5.0 / 3.0 + 1e-5)
+    assert np.max(np.abs(y[0] - wrong)) > 1e-2
+    y2 = O.layer_norm_f64(np.array([[1, 2, 3], [4, 5, 6]], np.float32))
+    assert np.all(np.abs(y2.mean(axis=1)) < 1e-5)
+    x = O.Lcg(12).normal((64, 777), 2.0, 3.0)
+    y = O.layer_norm_f64(x, 1e-5)
+    xd = x.astype(np.float64)
+    v = xd.var(axis=1)
+    assert np.max(np.abs(y.mean(axis=1))) < 1e-12
+    assert np.max(np.abs(y.var(axis=1) - v / (v + 1e-5))) < 1e-12
+    z = O.layer_norm_f64(np.full((2, 2048), 3.0, np.float32))
+    assert np.array_equal(z, np.zeros((2, 2048)))
+    # LN(a x) with eps a^2 equals LN(x) with eps (a = 4 is exact in f32), and
+    # LN(x + b) = LN(x) on integer-valued rows (exact shifts)
+    y_s = O.layer_norm_f64((x * np.float32(4.0)).astype(np.float32), 16e-5)
+    assert np.max(np.abs(y_s - y)) < 1e-12
+    xi = np.floor(O.Lcg(14).normal((8, 300), 0.0, 50.0)).astype(np.float32)
+    assert np.max(np.abs(O.layer_norm_f64(xi + np.float32(1000.0)) - O.layer_norm_f64(xi))) < 1e-9
+
+
+def test_layer_norm_f32_restatement_tracks_f64():
+    x = O.Lcg(13).normal((256, 2048), 0.0, 3.0)
+    assert O.max_rel_err(O.layer_norm_f32(x), O.layer_norm_f64(x)) < 1e-5
