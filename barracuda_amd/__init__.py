@@ -7,7 +7,7 @@ this package is the host side that mirrors the reference's op API.
 from .error import (BarracudaError, CastOverflow, DeviceError, DeviceLost, DeviceNotAvailable,
                     ExecutionError, InvalidInput, InvalidOperation, InvalidShape, OutOfMemory,
                     ShapeMismatch, UnsupportedOperation)
-from . import linalg, nn
+from . import ipc, linalg, nn
 from .linalg import F64Buffer, GemmCachedF64, GemmF64
 from .nn import Activation, fused_mlp
 from .session import AttentionDims, SessionTensor, TensorSession
@@ -19,7 +19,7 @@ __all__ = [
     "BarracudaError", "CastOverflow", "DeviceError", "DeviceLost", "DeviceNotAvailable",
     "ExecutionError", "InvalidInput", "InvalidOperation", "InvalidShape", "OutOfMemory",
     "ShapeMismatch", "UnsupportedOperation", "AttentionDims", "SessionTensor", "TensorSession",
-    "Activation", "fused_mlp", "nn", "linalg", "F64Buffer", "GemmCachedF64", "GemmF64",
+    "Activation", "fused_mlp", "nn", "linalg", "ipc", "F64Buffer", "GemmCachedF64", "GemmF64",
     "Attention", "BatchMatMul", "CausalAttention", "FlashAttention", "GroupedQueryAttention", "HipDevice",
     "MatMul", "MultiHeadAttention",
     "MatmulTiled", "ScaledDotProductAttention", "Softmax", "Tensor", "get_device", "LcgStream",
