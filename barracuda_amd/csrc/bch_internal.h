@@ -157,6 +157,12 @@ hipError_t launch_fill_normal(hipStream_t s, float* out, uint64_t n, uint64_t st
                               double sigma);
 uint64_t lcg_advance(uint64_t state, uint64_t inc, uint64_t n);
 
+// Compute units of the current device, cached per device; kDefaultCUs
+// (MI355X) when no device is visible, so launch plans and kernel names can
+// be computed without a GPU.
+constexpr int kDefaultCUs = 256;
+int device_cu_count();
+
 // Raise `func`'s dynamic LDS limit to `bytes` on the current device, once per
 // (function, device); thread-safe.  Kernels asking for more than 64 KB of
 // dynamic LDS need it before their first launch on each device.

@@ -15,6 +15,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <atomic>
 #include <map>
 #include <mutex>
 #include <set>
@@ -720,6 +721,24 @@ const char* bch_layer_norm_kernel_name(long long rows, long long cols) {
 }  // extern "C"
 
 namespace bch {
+
+int device_cu_count() {
+  static std::atomic<int> cached[64];  // zero-initialised (static storage)
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    (void)hipGetLastError();
+    dev = 0;
+  }
+  int n = cached[dev].load(std::memory_order_relaxed);
+  if (n <= 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) {
+      (void)hipGetLastError();
+      return kDefaultCUs;  // no device visible (validation-only calls): not cached
+    }
+    cached[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
 
 hipError_t ensure_dynamic_lds(const void* func, int bytes) {
   static std::mutex mu;

@@ -377,14 +377,10 @@ hipError_t launch_dp(hipStream_t s, int B, int H, int Hkv, int Sq, int Skv, int 
 bool aligned16(const float* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 bool mult4(const bch::SdpaLayout& l) { return l.batch % 4 == 0 && l.head % 4 == 0 && l.row % 4 == 0; }
 
-#ifndef BCH_SDPA_WIDE_NT  // threads per workgroup for head dims 64 and 128 (a build-time knob for sweeps)
-#define BCH_SDPA_WIDE_NT 256
-#endif
-
 template <int DP>
 hipError_t launch_d(hipStream_t s, int B, int H, int Hkv, int Sq, int Skv, int D, float scale, int causal,
                     const float* q, const float* k, const float* v, float* o, const bch::SdpaStrides& st) {
-  constexpr int NT = DP >= 64 ? BCH_SDPA_WIDE_NT : 256;
+  constexpr int NT = 256;  // four wavefronts of 32 queries each
   // full tiles, 128-bit loads: every row start 16-byte aligned
   const bool full = D == DP && Sq % SdpaCfg<DP, NT>::BQ == 0 && Skv % kBKV == 0 && aligned16(q) && aligned16(k) &&
                     aligned16(v) && mult4(st.q) && mult4(st.k) && mult4(st.v);

@@ -385,15 +385,15 @@ hipError_t launch_tiles(hipStream_t s, int batch, int m, int n, int k,
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 constexpr int kBK = 32;
-constexpr int kNumCU = 256;  // MI355X
 
-// Tile choice: the largest block tile that still gives every CU at least
-// one tile.  Measured on MI355X (f32, TFLOP/s): 4096^3 -- 128x128 108,
+// Tile choice: the largest block tile that still gives every CU of the
+// device at least one tile.  Measured on MI355X (f32, TFLOP/s): 4096^3 -- 128x128 108,
 // 256x128 125, 256x256 132; 16 x 1024^3 -- 109 / 120 / 126; 2048^3 --
 // 113 / 62 / 33 (too few tiles for the larger shapes).
 enum class Tile { k256x256, k256x128, k128x128 };
 
 Tile pick_tile(int batch, int m, int n) {
+  const int kNumCU = bch::device_cu_count();
   const long long t256 = (long long)batch * ((m + 255) / 256) * ((n + 255) / 256);
   if (t256 >= kNumCU) return Tile::k256x256;
   const long long t256x128 = (long long)batch * ((m + 255) / 256) * ((n + 127) / 128);

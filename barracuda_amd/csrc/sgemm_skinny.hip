@@ -43,7 +43,6 @@
 
 #include <stdint.h>
 
-#include <atomic>
 
 namespace {
 
@@ -55,7 +54,6 @@ constexpr int kFmaSplits = 16;
 constexpr int kSkCols = 256;   // columns per unit / column group (4 x 64)
 constexpr int kSkRows = 16;    // rows per unit
 constexpr int kSkPF = 3;       // units of B in flight ahead of the MFMAs
-constexpr int kSkWGs = 256;    // one workgroup per CU
 constexpr int kLdsBytes = 160 * 1024;
 
 // ---------------------------------------------------------------- m <= 4
@@ -761,19 +759,9 @@ bool use_w32(int m, int k, const float* A, int lda) {
   return m > 16 && k >= 4 && k % 4 == 0 && lda % 4 == 0 && (reinterpret_cast<uintptr_t>(A) & 15) == 0;
 }
 
-// Compute units of the current device (the stream-K grids take one
-// workgroup per CU); cached per device.
-int cu_count() {
-  static std::atomic<int> cached[64];  // zero-initialised (static storage)
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
-  int n = cached[dev].load(std::memory_order_relaxed);
-  if (n <= 0) {
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = kSkWGs;
-    cached[dev].store(n, std::memory_order_relaxed);
-  }
-  return n;
-}
+// Compute units of the current device: the stream-K grids take one
+// workgroup per CU.
+int cu_count() { return bch::device_cu_count(); }
 
 // FMA path: k rows per split and split count.
 void fma_plan(int k, int* kchunk, int* splits) {
