@@ -471,11 +471,11 @@ __global__ __launch_bounds__(256) void sgemm_skinny_sk_reduce(int M, int N, cons
   C[(long long)m * ldc + n] = epilogue(s, bias, n, act);
 }
 
-// Launch the split-k reduce of a stream-K plan (cols: partial block width, 256 or 128).
+// Launch the split-k reduce of a stream-K plan (cols: partial block width, 256 or 32).
 hipError_t launch_sk_reduce(hipStream_t s, int m, int n, const float* P, long long U, int G, int kb, int smax,
                             float* C, int ldc, const float* bias, int act, int cols) {
   const dim3 grid((unsigned)((n + 255) / 256), (unsigned)m);
-  const int cshift = cols == 256 ? 8 : 7;
+  const int cshift = __builtin_ctz((unsigned)cols);  // cols: a power of two
   if ((unsigned long long)U * (unsigned long long)G < (1ULL << 32))
     hipLaunchKernelGGL(sgemm_skinny_sk_reduce<false>, grid, dim3(256), 0, s, m, n, P, U, G, kb, smax, C, ldc, bias,
                        act, cshift);
@@ -485,148 +485,234 @@ hipError_t launch_sk_reduce(hipStream_t s, int m, int n, const float* P, long lo
   return hipGetLastError();
 }
 
-// ---------------------------------------------------------------- transposed weights, m <= 32
+// ---------------------------------------------------------------- transposed weights, 4 < m <= 32
 // C[m][n] = sum_k A[m][k] W[n][k]: the linear layer with W [out, in]
-// (shaders/misc/linear_f64.wgsl) at decode sizes.  v_mfma_f32_16x16x4_f32
-// computes C^T = W A^T on 16 (n) x 16 (m) blocks, m padded to 16 or 32.
-// A unit is 128 rows of W (output columns) x 64 k; wave w owns rows 32w ..
-// 32w + 31.  Its tile is loaded as 4 rows x 256 contiguous bytes per
-// instruction (whole 128-byte lines) and re-laid through the wave's own LDS
-// rows (padded to 68 floats: conflict-free both ways, no workgroup barrier)
-// into the MFMA operand order: lane l = 16q + i holds row i of a 16-row
-// block at k = 16f + 4q .. +3 and feeds k = 16f + 4q + c in step (f, c).
-// The A operand is the same four float4 of A row 16b + i, through L2 (A is
-// tiny and shared by every workgroup).  Measured at K 4096, N 11008 (M = 1 /
-// 8 / 32): the first layout (16 rows x four separated 16-byte pieces per
-// load) 63 / 68 / 92 us, contiguous 64-byte row pieces 43 / 47 / 76 us, the
-// LDS re-layout 35 / 35 / 58 us.  Stream-K over units ordered row group by
-// row group, one partial block (M x 128) per run segment, reduced by
-// sgemm_skinny_sk_reduce with 128 columns per group.  Requires K % 4 == 0,
-// lda % 4 == 0, ldw % 4 == 0 and 16-byte aligned A, W.
-constexpr int kNtRows = 128;
-constexpr int kNtK = 64;
-constexpr int kNtPF = 1;
+// (shaders/misc/linear_f64.wgsl) at decode sizes.  Stream-K over units of
+// 32 rows of W (output columns n) x 256 k, ordered row group by row group:
+// every row of a unit is one 1 KB contiguous piece of W.  Workgroups of 8
+// wavefronts, one per CU:
+//   * waves 4..7 copy units into a 3-slot LDS ring with direct-to-LDS loads
+//     (global_load_lds_dwordx4: 8 rows per wave, rows padded to 260 floats
+//     so that the operand reads below are free of bank conflicts), and wait
+//     for a unit with s_waitcnt on their own load count;
+//   * waves 0..3 run v_mfma_f32_16x16x4_f32 (C^T = W A^T on 16 n x 16 m
+//     blocks, m padded to 16 or 32) over k quarters of each unit: lane
+//     l = 16 q + i reads row i of a 16-row block at k = 16 t + 4 q .. + 3
+//     from the ring and the same four k of A row 16 b + i from L2 (two units
+//     ahead), and feeds k = 16 t + 4 q + c in step (t, c).
+// One workgroup barrier per unit hands the ring over: the loaders wait for
+// unit i + 1 before it, the MFMA waves read unit i + 1 after it, between the
+// two halves of unit i's MFMAs (so the reads overlap MFMAs).  At the end of a
+// run segment (the units of one row group in this workgroup) one more
+// barrier hands the four waves' sums to LDS, where they are added in wave
+// order and written as a partial block (M x 32) for sgemm_skinny_sk_reduce,
+// which adds the blocks of a group in slot (k) order and applies the
+// epilogue.  EDGE (K % 256 != 0): loads past K read from K - 4 and both MFMA
+// operands of such k are zeroed where they are used; rows past N read row
+// N - 1 and are never stored.  Requires K % 4 == 0, lda % 4 == 0,
+// ldw % 4 == 0 and 16-byte aligned A and W.
+// Measured on one MI355X at K 4096, N 11008 (per call, M = 8 / 32, reduce
+// included): 34.5 / 48.8 us, against 35.8 / 51.9 us for the kernel before
+// it (units of 128 rows x 64 k loaded as 4 rows x 256 B per instruction and
+// re-laid per wave through LDS).  A pure read of the weights in this
+// schedule takes 30.2 us; whole-row ownership (each workgroup its own 43
+// rows over all K, no partials) measured 37.7 us at M = 8: the row blocks
+// left per workgroup are short and keep too few bytes in flight.
+constexpr int kRgRows = 32;                    // rows of W (output columns) per unit
+constexpr int kRgK = 256;                      // k per unit
+constexpr int kRgLdr = kRgK + 4;               // padded LDS row (floats)
+constexpr int kRgSlot = kRgRows * kRgLdr * 4;  // bytes per ring slot
+constexpr int kRgD = 3;                        // ring slots
+
+template <int MB>
+constexpr int rg_lds_bytes() {
+  return kRgD * kRgSlot + 4 * 2 * MB * 4 * 64 * 4;  // ring, then the segment-end sums of 4 waves
+}
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// loader: wait until at most n of this wave's units (8 loads each) are in flight
+__device__ __forceinline__ void rg_wait_units(int n) {
+  if (n <= 0)
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  else if (n == 1)
+    asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+  else
+    asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+}
+
+// workgroup barrier that no memory access or instruction is moved across
+__device__ __forceinline__ void rg_barrier() {
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// s_waitcnt lgkmcnt(0) (vmcnt and expcnt left at their maximum)
+constexpr int kLgkmZero = 0xC07F;
 
 template <int MB, bool EDGE>
-__global__ __launch_bounds__(256, 2) void sgemm_skinny_nt(int M, int N, int K, const float* __restrict__ A, int lda,
-                                                          const float* __restrict__ W, int ldw,
-                                                          float* __restrict__ P, long long U, int G, int nkb,
-                                                          int smax) {
-  constexpr int LDW = kNtK + 4;  // padded LDS row (floats)
-  __shared__ float wl[4][32 * LDW];
+__global__ __launch_bounds__(512, 1) void sgemm_skinny_nt_ring(int M, int N, int K, const float* __restrict__ A,
+                                                               int lda, const float* __restrict__ W, int ldw,
+                                                               float* __restrict__ P, long long U, int G, int nkb,
+                                                               int smax) {
+  extern __shared__ float4 smem4[];
+  char* ring = reinterpret_cast<char*>(smem4);
+  float* red = reinterpret_cast<float*>(ring + kRgD * kRgSlot);  // [4 waves][2 rb][MB][4 r][64 lanes]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int q = lane >> 4, i = lane & 15;
   const int w = blockIdx.x;
   const long long ub = (long long)w * U / G, ue = (long long)(w + 1) * U / G;
-  const int nu = (int)(ue - ub);
+  const int nu = (int)(ue - ub);  // >= 1: G <= U
   const int g0 = (int)(ub / nkb), t0 = (int)(ub - (long long)g0 * nkb);
-  constexpr int PF = kNtPF, NB = kNtPF + 1;
-  float* ws = wl[wave];
 
+  if (wave >= 4) {
+    // ---- loader wave lw: rows 8 lw .. 8 lw + 7 of every unit
+    const int lw = wave - 4;
+    int lg = g0, lt = t0;
+    auto issue = [&](int i) {
+      int kk = kRgK * lt + 4 * lane;
+      if (EDGE) kk = min(kk, K - 4);
+      char* dst = ring + (i % kRgD) * kRgSlot + 8 * lw * (kRgLdr * 4);
+#pragma unroll
+      for (int r = 0; r < 8; ++r) {
+        const int row = min(kRgRows * lg + 8 * lw + r, N - 1);
+        __builtin_amdgcn_global_load_lds(W + (long long)row * ldw + kk, (lds_void*)(dst + r * kRgLdr * 4), 16, 0,
+                                         2 /* nt */);
+      }
+      if (++lt == nkb) {
+        lt = 0;
+        ++lg;
+      }
+    };
+    const int n0 = nu < kRgD - 1 ? nu : kRgD - 1;
+    for (int i = 0; i < n0; ++i) issue(i);
+    rg_wait_units(n0 - 1);
+    __builtin_amdgcn_s_barrier();
+    int st = t0;
+    for (int i = 0; i < nu; ++i) {
+      if (i + kRgD - 1 < nu) issue(i + kRgD - 1);
+      const int last = i + kRgD - 1 < nu ? i + kRgD - 1 : nu - 1;
+      rg_wait_units(last - (i + 1));  // unit i + 1 has landed
+      __builtin_amdgcn_s_barrier();
+      const bool group_end = ++st == nkb;
+      if (group_end) st = 0;
+      if (group_end || i + 1 == nu) __builtin_amdgcn_s_barrier();  // the segment-end sums
+    }
+    return;
+  }
+
+  // ---- MFMA wave cw: k quarter [64 cw, 64 cw + 64) of every unit
+  const int cw = wave, q = lane >> 4, i16 = lane & 15;
   const float* arow[MB];
 #pragma unroll
-  for (int b = 0; b < MB; ++b) arow[b] = A + (long long)min(16 * b + i, M - 1) * lda;
-
-  // W: instruction f loads rows 4 f + q of the wave's 32, k chunk 4 i (4 rows x 256 contiguous bytes)
-  float4 wv[NB][8];
-  float4 av[NB][MB][4];
-  int lg = g0, lt = t0, lcount = 0;
-  auto load = [&](int sb) {
-    const int kw = kNtK * lt + 4 * i;
-#pragma unroll
-    for (int f = 0; f < 8; ++f) {
-      const float* wr = W + (long long)min(kNtRows * lg + 32 * wave + 4 * f + q, N - 1) * ldw;
-      wv[sb][f] = bch::load_nt(reinterpret_cast<const float4*>(wr + min(kw, K - 4)));
-      if (EDGE && kw >= K) wv[sb][f] = make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-    const int k0 = kNtK * lt + 4 * q;
+  for (int b = 0; b < MB; ++b) arow[b] = A + (long long)min(16 * b + i16, M - 1) * lda;
+  constexpr int PX = 2, NX = PX + 1;  // units of A in flight ahead of the MFMAs
+  float4 av[NX][MB][4];
+  int xt = t0, xn = 0;  // A cursor: advanced once per load, held at the last unit
+  auto load_a = [&](int sb) {
 #pragma unroll
     for (int b = 0; b < MB; ++b)
 #pragma unroll
-      for (int f = 0; f < 4; ++f) {
-        av[sb][b][f] = *reinterpret_cast<const float4*>(arow[b] + min(k0 + 16 * f, K - 4));
-        if (EDGE && k0 + 16 * f >= K) av[sb][b][f] = make_float4(0.f, 0.f, 0.f, 0.f);
+      for (int tt = 0; tt < 4; ++tt) {
+        int k = kRgK * xt + 64 * cw + 16 * tt + 4 * q;
+        if (EDGE) k = min(k, K - 4);  // zeroed where used
+        av[sb][b][tt] = *reinterpret_cast<const float4*>(arow[b] + k);
       }
-    ++lcount;
-    lt += lcount < nu ? 1 : 0;
-    const int wrap = lt == nkb ? 1 : 0;
-    lt -= wrap * nkb;
-    lg += wrap;
+    if (++xn < nu && ++xt == nkb) xt = 0;
   };
 #pragma unroll
-  for (int p = 0; p < PF; ++p) {
-    load(p);
-    __builtin_amdgcn_sched_barrier(0);
-  }
-
+  for (int p = 0; p < PX; ++p) load_a(p);
+  float4 wv[2][2][4];
+  auto read_w = [&](int sb, int i) {
+    const char* sl = ring + (i % kRgD) * kRgSlot + (64 * cw + 4 * q) * 4;
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt)
+        wv[sb][rb][tt] = *reinterpret_cast<const float4*>(sl + (16 * rb + i16) * (kRgLdr * 4) + 64 * tt);
+  };
   f32x4v acc[2][MB];
 #pragma unroll
   for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
     for (int b = 0; b < MB; ++b) acc[rb][b] = (f32x4v){0.f, 0.f, 0.f, 0.f};
-  int gcur = g0, tcur = t0;
-  int slot = w - wg_of_unit((long long)g0 * nkb, U, G);
-  auto flush = [&]() {
-    float* pt = P + (long long)(gcur * smax + slot) * M * kNtRows;
-    const int nrem = N - gcur * kNtRows;
+  // steps t0_, t0_ + 1 of the unit whose k starts at kbase
+  auto mma = [&](int sw, int sx, int t0_, int kbase) {
 #pragma unroll
-    for (int b = 0; b < MB; ++b) {
-      const int m = 16 * b + i;
+    for (int tt = t0_; tt < t0_ + 2; ++tt) {
+      const bool live = !EDGE || kbase + 64 * cw + 16 * tt + 4 * q < K;
 #pragma unroll
-      for (int rb = 0; rb < 2; ++rb) {
-        const int c = 32 * wave + 16 * rb + 4 * q;
-        if (m < M && c < nrem)
-          *reinterpret_cast<float4*>(pt + (long long)m * kNtRows + c) =
-              make_float4(acc[rb][b][0], acc[rb][b][1], acc[rb][b][2], acc[rb][b][3]);
-        acc[rb][b] = (f32x4v){0.f, 0.f, 0.f, 0.f};
-      }
-    }
-  };
-  auto mma = [&](int sb) {
-    // re-layout the wave's 32 x 64 tile through its own LDS rows
-#pragma unroll
-    for (int f = 0; f < 8; ++f) *reinterpret_cast<float4*>(ws + (4 * f + q) * LDW + 4 * i) = wv[sb][f];
-    __builtin_amdgcn_wave_barrier();
-    float4 wt[2][4];
-#pragma unroll
-    for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-      for (int f = 0; f < 4; ++f) wt[rb][f] = *reinterpret_cast<const float4*>(ws + (16 * rb + i) * LDW + 16 * f + 4 * q);
-    __builtin_amdgcn_wave_barrier();
-#pragma unroll
-    for (int f = 0; f < 4; ++f) {
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
+      for (int c = 0; c < 4; ++c)
 #pragma unroll
         for (int b = 0; b < MB; ++b) {
-          const float4 a4 = av[sb][b][f];
-          const float x = c == 0 ? a4.x : c == 1 ? a4.y : c == 2 ? a4.z : a4.w;
+          const float4 a4 = av[sx][b][tt];
+          float x = c == 0 ? a4.x : c == 1 ? a4.y : c == 2 ? a4.z : a4.w;
+          if (EDGE) x = live ? x : 0.f;
 #pragma unroll
           for (int rb = 0; rb < 2; ++rb) {
-            const float4 w4 = wt[rb][f];
-            const float y = c == 0 ? w4.x : c == 1 ? w4.y : c == 2 ? w4.z : w4.w;
+            const float4 w4 = wv[sw][rb][tt];
+            float y = c == 0 ? w4.x : c == 1 ? w4.y : c == 2 ? w4.z : w4.w;
+            if (EDGE) y = live ? y : 0.f;
             acc[rb][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(y, x, acc[rb][b], 0, 0, 0);
           }
         }
-      }
     }
   };
-  for (int it = 0; it < nu; it += NB) {
+  // Segment end: value r of block (rb, b) at lane (q, i) is n = 16 rb + 4 q + r,
+  // m = 16 b + i.  After the exchange wave cw adds the four waves' values of
+  // rows m = cw + 4 (2 u + lane / 32), n = lane % 32, and stores them.
+  auto seg_end = [&](int g) {
 #pragma unroll
-    for (int p = 0; p < NB; ++p) {
-      load((p + PF) % NB);
-      if (it + p < nu) {
-        mma(p);
-        if (++tcur == nkb && it + p + 1 < nu) {
-          flush();
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+      for (int b = 0; b < MB; ++b)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) red[(((cw * 2 + rb) * MB + b) * 4 + r) * 64 + lane] = acc[rb][b][r];
+    __builtin_amdgcn_s_waitcnt(kLgkmZero);
+    rg_barrier();
+    const int slot = w - wg_of_unit((long long)g * nkb, U, G);
+    const int n = lane & 31;
+    const int rb = n >> 4, qq = (n >> 2) & 3, r = n & 3;
+    constexpr int kWave = 2 * MB * 4 * 64;  // one wave's values
+#pragma unroll
+    for (int u = 0; u < 2 * MB; ++u) {
+      const int m = cw + 4 * (2 * u + (lane >> 5));
+      const int e = ((rb * MB + (m >> 4)) * 4 + r) * 64 + 16 * qq + (m & 15);
+      const float s = ((red[e] + red[kWave + e]) + red[2 * kWave + e]) + red[3 * kWave + e];
+      if (m < M) P[((long long)(g * smax + slot) * M + m) * kRgRows + n] = s;
+    }
+#pragma unroll
+    for (int rb2 = 0; rb2 < 2; ++rb2)
+#pragma unroll
+      for (int b = 0; b < MB; ++b) acc[rb2][b] = (f32x4v){0.f, 0.f, 0.f, 0.f};
+  };
+  __builtin_amdgcn_s_barrier();  // unit 0 has landed
+  asm volatile("" ::: "memory");
+  read_w(0, 0);
+  int gcur = g0, tcur = t0;
+  // unrolled 2 NX times so that both register rings are indexed statically
+  for (int i0 = 0; i0 < nu; i0 += 2 * NX) {
+#pragma unroll
+    for (int p = 0; p < 2 * NX; ++p) {
+      const int i = i0 + p;
+      if (i < nu) {
+        load_a((p + PX) % NX);
+        mma(p & 1, p % NX, 0, kRgK * tcur);
+        __builtin_amdgcn_s_waitcnt(kLgkmZero);  // this unit's ring reads are complete
+        rg_barrier();
+        if (i + 1 < nu) read_w((p + 1) & 1, i + 1);
+        mma(p & 1, p % NX, 2, kRgK * tcur);
+        const bool group_end = ++tcur == nkb;
+        if (group_end || i + 1 == nu) seg_end(gcur);
+        if (group_end) {
           tcur = 0;
           ++gcur;
-          slot = 0;
         }
       }
     }
   }
-  flush();
 }
 
 // ---------------------------------------------------------------- transposed weights, m <= 4, whole rows
@@ -831,7 +917,7 @@ W32Plan w32_plan(int n, int k) {
   return p;
 }
 
-// transposed-weight path: 128-row x 64-k units, two workgroups per CU
+// transposed-weight path: 32-row x 256-k units, one workgroup per CU
 struct NtPlan {
   long long U = 0;
   int ng = 0, nkb = 0, G = 0, smax = 0;
@@ -839,10 +925,10 @@ struct NtPlan {
 
 NtPlan nt_plan(int n, int k) {
   NtPlan p;
-  p.ng = (n + kNtRows - 1) / kNtRows;
-  p.nkb = (k + kNtK - 1) / kNtK;
+  p.ng = (n + kRgRows - 1) / kRgRows;
+  p.nkb = (k + kRgK - 1) / kRgK;
   p.U = (long long)p.ng * p.nkb;
-  long long g = 2LL * cu_count();
+  long long g = cu_count();
   if (g > p.U) g = p.U;
   p.G = (int)g;
   for (int c = 0; c < p.ng; ++c) {
@@ -904,6 +990,17 @@ hipError_t launch_sk(hipStream_t s, const SkPlan& p, int m, int n, int k, const 
   return hipGetLastError();
 }
 
+template <int MB, bool EDGE>
+hipError_t launch_nt_ring(hipStream_t s, const NtPlan& p, int m, int n, int k, const float* A, int lda,
+                          const float* W, int ldw, float* P) {
+  const void* f = reinterpret_cast<const void*>(sgemm_skinny_nt_ring<MB, EDGE>);
+  hipError_t e = bch::ensure_dynamic_lds(f, rg_lds_bytes<MB>());
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((sgemm_skinny_nt_ring<MB, EDGE>), dim3(p.G), dim3(512), rg_lds_bytes<MB>(), s, m, n, k, A, lda,
+                     W, ldw, P, p.U, p.G, p.nkb, p.smax);
+  return hipGetLastError();
+}
+
 }  // namespace
 
 namespace bch {
@@ -918,7 +1015,7 @@ bool sgemm_skinny_nt_applies(int m, int n, int k, const float* A, int lda, const
 size_t sgemm_skinny_nt_workspace_bytes(int m, int n, int k) {
   if (use_rows(m, n, k)) return 0;
   const NtPlan p = nt_plan(n, k);
-  return sizeof(float) * (size_t)p.ng * (size_t)p.smax * (size_t)m * kNtRows;
+  return sizeof(float) * (size_t)p.ng * (size_t)p.smax * (size_t)m * kRgRows;
 }
 
 hipError_t launch_sgemm_skinny_nt(hipStream_t s, int m, int n, int k, const float* A, int lda, const float* W,
@@ -933,26 +1030,13 @@ hipError_t launch_sgemm_skinny_nt(hipStream_t s, int m, int n, int k, const floa
   if (ws == nullptr || ws_bytes < sgemm_skinny_nt_workspace_bytes(m, n, k)) return hipErrorInvalidValue;
   float* P = static_cast<float*>(ws);
   const NtPlan p = nt_plan(n, k);
-  const bool edge = k % kNtK != 0;
-  const dim3 grid(p.G), block(256);
-  if (m <= 16) {
-    if (edge)
-      hipLaunchKernelGGL((sgemm_skinny_nt<1, true>), grid, block, 0, s, m, n, k, A, lda, W, ldw, P, p.U, p.G, p.nkb,
-                         p.smax);
-    else
-      hipLaunchKernelGGL((sgemm_skinny_nt<1, false>), grid, block, 0, s, m, n, k, A, lda, W, ldw, P, p.U, p.G, p.nkb,
-                         p.smax);
-  } else {
-    if (edge)
-      hipLaunchKernelGGL((sgemm_skinny_nt<2, true>), grid, block, 0, s, m, n, k, A, lda, W, ldw, P, p.U, p.G, p.nkb,
-                         p.smax);
-    else
-      hipLaunchKernelGGL((sgemm_skinny_nt<2, false>), grid, block, 0, s, m, n, k, A, lda, W, ldw, P, p.U, p.G, p.nkb,
-                         p.smax);
-  }
-  hipError_t e = hipGetLastError();
+  const bool edge = k % kRgK != 0;
+  hipError_t e = m <= 16 ? (edge ? launch_nt_ring<1, true>(s, p, m, n, k, A, lda, W, ldw, P)
+                                 : launch_nt_ring<1, false>(s, p, m, n, k, A, lda, W, ldw, P))
+                         : (edge ? launch_nt_ring<2, true>(s, p, m, n, k, A, lda, W, ldw, P)
+                                 : launch_nt_ring<2, false>(s, p, m, n, k, A, lda, W, ldw, P));
   if (e != hipSuccess) return e;
-  return launch_sk_reduce(s, m, n, P, p.U, p.G, p.nkb, p.smax, C, ldc, bias, act, kNtRows);
+  return launch_sk_reduce(s, m, n, P, p.U, p.G, p.nkb, p.smax, C, ldc, bias, act, kRgRows);
 }
 
 size_t sgemm_skinny_workspace_bytes(int m, int n, int k) {
