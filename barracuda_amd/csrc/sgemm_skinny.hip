@@ -43,6 +43,8 @@
 
 #include <stdint.h>
 
+#include <atomic>
+
 
 namespace {
 
@@ -505,15 +507,29 @@ hipError_t launch_sk_reduce(hipStream_t s, int m, int n, const float* P, long lo
 // two halves of unit i's MFMAs (so the reads overlap MFMAs).  At the end of a
 // run segment (the units of one row group in this workgroup) one more
 // barrier hands the four waves' sums to LDS, where they are added in wave
-// order and written as a partial block (M x 32) for sgemm_skinny_sk_reduce,
-// which adds the blocks of a group in slot (k) order and applies the
-// epilogue.  EDGE (K % 256 != 0): loads past K read from K - 4 and both MFMA
+// order.  A segment that covers its whole row group is stored to C with the
+// epilogue.  Otherwise the group is split over consecutive workgroups and
+// combined in this kernel, with no second launch:
+//   * its owner is the last of them, whose first segment is the group's
+//     tail; it keeps that block in registers until the end of its run;
+//   * every other one (a contributor, whose last segment it is) stores its
+//     block with agent-scope (sc1) stores, waits for their completion
+//     (s_waitcnt vmcnt(0)) and then sets its flag to the launch's epoch;
+//   * at the end of its run the owner waits for the flags of its
+//     contributors, loads their blocks (sc1), adds them in k order followed
+//     by its own, applies the epilogue, stores C and resets the flags.
+// An owner waits only on lower-numbered workgroups, which are dispatched
+// before it and never wait before storing their block, so the wait always
+// ends; it is bounded anyway (a block that never arrives turns the outputs
+// NaN).  The epoch (64-bit, one per launch) keeps stale flags from matching;
+// the reset keeps a replay of a captured launch, which reuses its epoch,
+// from matching the previous replay's flags.  EDGE (K % 256 != 0): loads past K read from K - 4 and both MFMA
 // operands of such k are zeroed where they are used; rows past N read row
 // N - 1 and are never stored.  Requires K % 4 == 0, lda % 4 == 0,
 // ldw % 4 == 0 and 16-byte aligned A and W.
-// Measured on one MI355X at K 4096, N 11008 (per call, M = 8 / 32, reduce
-// included): 34.5 / 48.8 us, against 35.8 / 51.9 us for the kernel before
-// it (units of 128 rows x 64 k loaded as 4 rows x 256 B per instruction and
+// Measured on one MI355X at K 4096, N 11008 (per call, M = 8 / 32): with a
+// separate reduce launch 34.6 / 48.5 us, against 35.8 / 51.9 us for the
+// kernel before it (units of 128 rows x 64 k loaded as 4 rows x 256 B per instruction and
 // re-laid per wave through LDS).  A pure read of the weights in this
 // schedule takes 30.2 us; whole-row ownership (each workgroup its own 43
 // rows over all K, no partials) measured 37.7 us at M = 8: the row blocks
@@ -553,11 +569,13 @@ __device__ __forceinline__ void rg_barrier() {
 // s_waitcnt lgkmcnt(0) (vmcnt and expcnt left at their maximum)
 constexpr int kLgkmZero = 0xC07F;
 
+constexpr unsigned kRgSpin = 1u << 22;  // owner's polls of one flag (about 0.1 s) before giving up
+
 template <int MB, bool EDGE>
-__global__ __launch_bounds__(512, 1) void sgemm_skinny_nt_ring(int M, int N, int K, const float* __restrict__ A,
-                                                               int lda, const float* __restrict__ W, int ldw,
-                                                               float* __restrict__ P, long long U, int G, int nkb,
-                                                               int smax) {
+__global__ __launch_bounds__(512, 1) void sgemm_skinny_nt_ring(
+    int M, int N, int K, const float* __restrict__ A, int lda, const float* __restrict__ W, int ldw,
+    float* __restrict__ C, int ldc, const float* __restrict__ bias, int act, float* __restrict__ P,
+    unsigned long long* __restrict__ F, unsigned long long epoch, long long U, int G, int nkb, int smax) {
   extern __shared__ float4 smem4[];
   char* ring = reinterpret_cast<char*>(smem4);
   float* red = reinterpret_cast<float*>(ring + kRgD * kRgSlot);  // [4 waves][2 rb][MB][4 r][64 lanes]
@@ -661,37 +679,67 @@ __global__ __launch_bounds__(512, 1) void sgemm_skinny_nt_ring(int M, int N, int
     }
   };
   // Segment end: value r of block (rb, b) at lane (q, i) is n = 16 rb + 4 q + r,
-  // m = 16 b + i.  After the exchange wave cw adds the four waves' values of
-  // rows m = cw + 4 (2 u + lane / 32), n = lane % 32, and stores them.
-  auto seg_end = [&](int g) {
+  // m = 16 b + i.  After the exchange wave cw holds the sums of rows
+  // m = cw + 4 (2 u + lane / 32), n = lane % 32, u < 2 MB.
+  // Partial block of (group g, slot sl): [sl][wave][u][lane] floats, lane-major.
+  __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(P, 0, 0x7fffffff, 0x00020000);
+  auto pofs = [&](int g, int sl, int u) { return ((((g * smax + sl) * 4 + cw) * 2 * MB + u) * 64 + lane) * 4; };
+  const int ncol = lane & 31;
+  float keep[2 * MB];
+  int own_g = -1;
+  auto store_c = [&](int g, const float* val) {
+    const int n = kRgRows * g + ncol;
+#pragma unroll
+    for (int u = 0; u < 2 * MB; ++u) {
+      const int m = cw + 4 * (2 * u + (lane >> 5));
+      if (m < M && n < N) C[(long long)m * ldc + n] = epilogue(val[u], bias, n, act);
+    }
+  };
+  auto seg_end = [&](int g, long long a, long long b) {
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
-      for (int b = 0; b < MB; ++b)
+      for (int bb = 0; bb < MB; ++bb)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) red[(((cw * 2 + rb) * MB + b) * 4 + r) * 64 + lane] = acc[rb][b][r];
+        for (int r = 0; r < 4; ++r) red[(((cw * 2 + rb) * MB + bb) * 4 + r) * 64 + lane] = acc[rb][bb][r];
     __builtin_amdgcn_s_waitcnt(kLgkmZero);
     rg_barrier();
-    const int slot = w - wg_of_unit((long long)g * nkb, U, G);
-    const int n = lane & 31;
-    const int rb = n >> 4, qq = (n >> 2) & 3, r = n & 3;
+    const int rb = ncol >> 4, qq = (ncol >> 2) & 3, r = ncol & 3;
     constexpr int kWave = 2 * MB * 4 * 64;  // one wave's values
+    float val[2 * MB];
 #pragma unroll
     for (int u = 0; u < 2 * MB; ++u) {
       const int m = cw + 4 * (2 * u + (lane >> 5));
       const int e = ((rb * MB + (m >> 4)) * 4 + r) * 64 + 16 * qq + (m & 15);
-      const float s = ((red[e] + red[kWave + e]) + red[2 * kWave + e]) + red[3 * kWave + e];
-      if (m < M) P[((long long)(g * smax + slot) * M + m) * kRgRows + n] = s;
+      val[u] = ((red[e] + red[kWave + e]) + red[2 * kWave + e]) + red[3 * kWave + e];
+    }
+    const long long gs = (long long)g * nkb, ge = gs + nkb;
+    if (a == gs && b == ge) {
+      store_c(g, val);
+    } else if (b == ge) {
+#pragma unroll
+      for (int u = 0; u < 2 * MB; ++u) keep[u] = val[u];
+      own_g = g;
+    } else {
+      const int sl = w - wg_of_unit(gs, U, G);
+#pragma unroll
+      for (int u = 0; u < 2 * MB; ++u)
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(val[u]), prs, pofs(g, sl, u), 0, 16 /* sc1 */);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      if (lane == 0)
+        __hip_atomic_store(F + ((long long)g * smax + sl) * 4 + cw, epoch, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
     }
 #pragma unroll
     for (int rb2 = 0; rb2 < 2; ++rb2)
 #pragma unroll
-      for (int b = 0; b < MB; ++b) acc[rb2][b] = (f32x4v){0.f, 0.f, 0.f, 0.f};
+      for (int bb = 0; bb < MB; ++bb) acc[rb2][bb] = (f32x4v){0.f, 0.f, 0.f, 0.f};
   };
   __builtin_amdgcn_s_barrier();  // unit 0 has landed
   asm volatile("" ::: "memory");
   read_w(0, 0);
   int gcur = g0, tcur = t0;
+  long long seg_a = ub;  // first unit of the current run segment
   // unrolled 2 NX times so that both register rings are indexed statically
   for (int i0 = 0; i0 < nu; i0 += 2 * NX) {
 #pragma unroll
@@ -705,13 +753,41 @@ __global__ __launch_bounds__(512, 1) void sgemm_skinny_nt_ring(int M, int N, int
         if (i + 1 < nu) read_w((p + 1) & 1, i + 1);
         mma(p & 1, p % NX, 2, kRgK * tcur);
         const bool group_end = ++tcur == nkb;
-        if (group_end || i + 1 == nu) seg_end(gcur);
+        if (group_end || i + 1 == nu) {
+          seg_end(gcur, seg_a, ub + i + 1);
+          seg_a = ub + i + 1;
+        }
         if (group_end) {
           tcur = 0;
           ++gcur;
         }
       }
     }
+  }
+  if (own_g >= 0) {
+    // the contributors' blocks in k order, then this workgroup's own (the group's tail)
+    const int nprev = w - wg_of_unit((long long)own_g * nkb, U, G);
+    unsigned long long* fl = F + (long long)own_g * smax * 4 + cw;
+    bool ok = true;
+    float sum[2 * MB];
+#pragma unroll
+    for (int u = 0; u < 2 * MB; ++u) sum[u] = 0.f;
+    for (int sl = 0; sl < nprev; ++sl) {
+      unsigned n = 0;
+      while (__hip_atomic_load(fl + 4 * sl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != epoch && n < kRgSpin) {
+        __builtin_amdgcn_s_sleep(1);
+        ++n;
+      }
+      ok = ok && n < kRgSpin;
+#pragma unroll
+      for (int u = 0; u < 2 * MB; ++u)
+        sum[u] += __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(prs, pofs(own_g, sl, u), 0, 16 /* sc1 */));
+    }
+#pragma unroll
+    for (int u = 0; u < 2 * MB; ++u) sum[u] = ok ? sum[u] + keep[u] : __builtin_nanf("");
+    store_c(own_g, sum);
+    if (lane == 0)
+      for (int sl = 0; sl < nprev; ++sl) __hip_atomic_store(fl + 4 * sl, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -938,6 +1014,15 @@ NtPlan nt_plan(int n, int k) {
   return p;
 }
 
+// the ring kernel's partial blocks (M padded to 16 or 32), 256-byte aligned; its flags follow
+size_t nt_partial_bytes(const NtPlan& p, int m) {
+  const size_t b = sizeof(float) * (size_t)p.ng * (size_t)p.smax * 4 * (m <= 16 ? 2 : 4) * 64;
+  return (b + 255) & ~(size_t)255;
+}
+
+// one epoch per launch of the ring kernel, process-wide, never 0
+std::atomic<unsigned long long> g_nt_epoch{0};
+
 // Whole-row path for transposed weights: m <= 4, the staged A fits in LDS,
 // and every wave of every CU gets at least one row.
 int rows_mt(int m) { return m <= 1 ? 1 : m <= 2 ? 2 : 4; }
@@ -990,14 +1075,24 @@ hipError_t launch_sk(hipStream_t s, const SkPlan& p, int m, int n, int k, const 
   return hipGetLastError();
 }
 
+struct RingArgs {
+  float* P;
+  unsigned long long* F;
+  unsigned long long epoch;
+  float* C;
+  int ldc;
+  const float* bias;
+  int act;
+};
+
 template <int MB, bool EDGE>
 hipError_t launch_nt_ring(hipStream_t s, const NtPlan& p, int m, int n, int k, const float* A, int lda,
-                          const float* W, int ldw, float* P) {
+                          const float* W, int ldw, const RingArgs& r) {
   const void* f = reinterpret_cast<const void*>(sgemm_skinny_nt_ring<MB, EDGE>);
   hipError_t e = bch::ensure_dynamic_lds(f, rg_lds_bytes<MB>());
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL((sgemm_skinny_nt_ring<MB, EDGE>), dim3(p.G), dim3(512), rg_lds_bytes<MB>(), s, m, n, k, A, lda,
-                     W, ldw, P, p.U, p.G, p.nkb, p.smax);
+                     W, ldw, r.C, r.ldc, r.bias, r.act, r.P, r.F, r.epoch, p.U, p.G, p.nkb, p.smax);
   return hipGetLastError();
 }
 
@@ -1015,7 +1110,7 @@ bool sgemm_skinny_nt_applies(int m, int n, int k, const float* A, int lda, const
 size_t sgemm_skinny_nt_workspace_bytes(int m, int n, int k) {
   if (use_rows(m, n, k)) return 0;
   const NtPlan p = nt_plan(n, k);
-  return sizeof(float) * (size_t)p.ng * (size_t)p.smax * (size_t)m * kRgRows;
+  return nt_partial_bytes(p, m) + sizeof(unsigned long long) * (size_t)p.ng * (size_t)p.smax * 4;
 }
 
 hipError_t launch_sgemm_skinny_nt(hipStream_t s, int m, int n, int k, const float* A, int lda, const float* W,
@@ -1028,15 +1123,16 @@ hipError_t launch_sgemm_skinny_nt(hipStream_t s, int m, int n, int k, const floa
     return launch_rows<4>(s, m, n, k, A, lda, W, ldw, C, ldc, bias, act);
   }
   if (ws == nullptr || ws_bytes < sgemm_skinny_nt_workspace_bytes(m, n, k)) return hipErrorInvalidValue;
-  float* P = static_cast<float*>(ws);
   const NtPlan p = nt_plan(n, k);
+  RingArgs r{static_cast<float*>(ws),
+             reinterpret_cast<unsigned long long*>(static_cast<char*>(ws) + nt_partial_bytes(p, m)),
+             ++g_nt_epoch, C, ldc, bias, act};
   const bool edge = k % kRgK != 0;
-  hipError_t e = m <= 16 ? (edge ? launch_nt_ring<1, true>(s, p, m, n, k, A, lda, W, ldw, P)
-                                 : launch_nt_ring<1, false>(s, p, m, n, k, A, lda, W, ldw, P))
-                         : (edge ? launch_nt_ring<2, true>(s, p, m, n, k, A, lda, W, ldw, P)
-                                 : launch_nt_ring<2, false>(s, p, m, n, k, A, lda, W, ldw, P));
-  if (e != hipSuccess) return e;
-  return launch_sk_reduce(s, m, n, P, p.U, p.G, p.nkb, p.smax, C, ldc, bias, act, kRgRows);
+  if (m <= 16)
+    return edge ? launch_nt_ring<1, true>(s, p, m, n, k, A, lda, W, ldw, r)
+                : launch_nt_ring<1, false>(s, p, m, n, k, A, lda, W, ldw, r);
+  return edge ? launch_nt_ring<2, true>(s, p, m, n, k, A, lda, W, ldw, r)
+              : launch_nt_ring<2, false>(s, p, m, n, k, A, lda, W, ldw, r);
 }
 
 size_t sgemm_skinny_workspace_bytes(int m, int n, int k) {

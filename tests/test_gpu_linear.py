@@ -77,6 +77,38 @@ def test_sgemm_ex_transposed_decode_shapes(dev, m, n, k):
         assert O.max_rel_err(got, _ref(x, w, b, True, act == N.BCH_ACT_RELU)) <= TOL, act
 
 
+@pytest.mark.parametrize("m,n,k", [(8, 64, 16384), (32, 96, 8192), (13, 1000, 2100), (20, 11008, 4096),
+                                   (6, 33, 260)])
+def test_sgemm_ex_transposed_split_groups(dev, m, n, k):
+    """The in-kernel split-k combine of the 4 < m <= 32 path: a 32-row group spread over many
+    workgroups (n 64, k 16384: one unit per workgroup, 63 contributors per owner; n 96, k 8192),
+    k not a multiple of 256 (2100, 260), the decode shape at m = 20, and a ragged last group
+    (n 33).  Repeated calls reuse the workspace and its flags: each result is bit-identical."""
+    _say(f"sgemm_ex transposed split groups m={m} n={n} k={k}")
+    rng = O.Lcg(7 * m + n + k)
+    x = rng.normal((m, k))
+    w = rng.normal((n, k), 0.0, 0.05)
+    bias = rng.normal((n,))
+    for act, b in ((N.BCH_ACT_RELU, bias), (N.BCH_ACT_GELU, None)):
+        first = _sgemm_ex(dev, 1, x, w, b, act)
+        want = _ref(x, w, b, True, False)
+        want = np.maximum(want, 0.0) if act == N.BCH_ACT_RELU else O.gelu_f64(want)
+        assert O.max_rel_err(first, want) <= TOL, act
+        for _ in range(2):
+            assert np.array_equal(first, _sgemm_ex(dev, 1, x, w, b, act)), "not deterministic"
+
+
+def test_sgemm_ex_transposed_split_groups_exact_on_integers(dev):
+    _say("sgemm_ex transposed split groups, integers")
+    rng = np.random.default_rng(31)
+    for m, n, k in ((8, 64, 16384), (32, 200, 2052), (5, 4096, 4096)):
+        x = rng.integers(-8, 9, (m, k)).astype(np.float32)
+        w = rng.integers(-8, 9, (n, k)).astype(np.float32)
+        b = rng.integers(-100, 101, n).astype(np.float32)
+        want = x.astype(np.int64) @ w.astype(np.int64).T + b
+        assert np.array_equal(_sgemm_ex(dev, 1, x, w, b, N.BCH_ACT_NONE), want.astype(np.float32)), (m, n, k)
+
+
 @pytest.mark.parametrize("m,n,k", [(1, 2048, 4096), (2, 2053, 2052), (3, 5000, 1024), (4, 4100, 6144),
                                    (4, 2304, 4100), (1, 3000, 44000), (6, 3000, 2048)])
 def test_sgemm_ex_transposed_whole_rows(dev, m, n, k):
