@@ -66,7 +66,7 @@ def test_sgemm_ex_vs_f64(dev, m, n, k, transb):
 @pytest.mark.parametrize("m,n,k", [(1, 11008, 4096), (8, 4096, 4096), (32, 1024, 4096), (5, 300, 100), (17, 77, 36),
                                    (16, 129, 68), (32, 4, 4), (2, 200, 1028)])
 def test_sgemm_ex_transposed_decode_shapes(dev, m, n, k):
-    """m <= 32 with [n][k] weights: the weight-row-streaming kernel, bias + ReLU in its reduce."""
+    """m <= 32 with [n][k] weights: the weight-row-streaming kernels, bias + ReLU in their epilogue."""
     _say(f"sgemm_ex transposed decode m={m} n={n} k={k}")
     rng = O.Lcg(m * 11 + n + k)
     x = rng.normal((m, k))
@@ -96,6 +96,51 @@ def test_sgemm_ex_transposed_split_groups(dev, m, n, k):
         assert O.max_rel_err(first, want) <= TOL, act
         for _ in range(2):
             assert np.array_equal(first, _sgemm_ex(dev, 1, x, w, b, act)), "not deterministic"
+
+
+def test_sgemm_ex_transposed_split_groups_with_concurrent_work(dev):
+    """The ring kernel's owners wait for blocks from other workgroups of the same launch (only
+    lower-numbered ones, dispatched before them).  Run the decode calls while a second context's
+    stream keeps every CU busy with 4096^3 GEMMs, so the ring kernel's workgroups are dispatched
+    piecemeal as CUs free up: every result must equal the one from an idle device, bit for bit."""
+    from barracuda_amd import HipDevice
+    _say("sgemm_ex transposed split groups next to another stream's GEMMs")
+    other = HipDevice()
+    big = []  # the other context's tensors, released before it closes
+    try:
+        g = np.random.default_rng(3)
+        big += [_up(other, g.standard_normal((4096, 4096), dtype=np.float32)) for _ in range(2)]
+        big.append(Tensor.empty([4096, 4096], other))
+        ba, bb, bc = big
+        calls = []
+        for i, (m, n, k) in enumerate(((8, 11008, 4096), (32, 11008, 4096), (8, 64, 16384))):
+            rng = O.Lcg(40 + i)
+            x, w, b = rng.normal((m, k)), rng.normal((n, k), 0.0, 0.05), rng.normal((n,))
+            calls.append((m, n, k, _up(dev, x), _up(dev, w), _up(dev, b), Tensor.empty([m, n], dev)))
+
+        def run(m, n, k, tx, tw, tb, ty):
+            with dev._lock:
+                dev.check(dev._lib.bch_sgemm_ex(dev.ctx, 1, m, n, k, C.c_void_p(tx.ptr), k, C.c_void_p(tw.ptr), k,
+                                                C.c_void_p(tb.ptr), N.BCH_ACT_RELU, C.c_void_p(ty.ptr), n),
+                          "sgemm_ex")
+
+        want = []
+        for c in calls:
+            run(*c)
+            want.append(c[-1].to_numpy())
+        for _ in range(30):  # about 30 ms of work queued on the other stream, not waited for
+            with other._lock:
+                other.check(other._lib.bch_sgemm(other.ctx, 4096, 4096, 4096, C.c_void_p(ba.ptr), 4096,
+                                                 C.c_void_p(bb.ptr), 4096, C.c_void_p(bc.ptr), 4096), "sgemm")
+        for rep in range(10):
+            for c, ref in zip(calls, want):
+                run(*c)
+                assert np.array_equal(c[-1].to_numpy(), ref), (rep, c[:3])
+        other.sync()
+    finally:
+        ba = bb = bc = None
+        big.clear()
+        other.close()
 
 
 def test_sgemm_ex_transposed_split_groups_exact_on_integers(dev):
