@@ -473,7 +473,7 @@ __global__ __launch_bounds__(256) void sgemm_skinny_sk_reduce(int M, int N, cons
   C[(long long)m * ldc + n] = epilogue(s, bias, n, act);
 }
 
-// Launch the split-k reduce of a stream-K plan (cols: partial block width, 256 or 32).
+// Launch the split-k reduce of a stream-K plan (cols: partial block width, a power of two).
 hipError_t launch_sk_reduce(hipStream_t s, int m, int n, const float* P, long long U, int G, int kb, int smax,
                             float* C, int ldc, const float* bias, int act, int cols) {
   const dim3 grid((unsigned)((n + 255) / 256), (unsigned)m);
@@ -490,13 +490,17 @@ hipError_t launch_sk_reduce(hipStream_t s, int m, int n, const float* P, long lo
 // ---------------------------------------------------------------- transposed weights, 4 < m <= 32
 // C[m][n] = sum_k A[m][k] W[n][k]: the linear layer with W [out, in]
 // (shaders/misc/linear_f64.wgsl) at decode sizes.  Stream-K over units of
-// 32 rows of W (output columns n) x 256 k, ordered row group by row group:
-// every row of a unit is one 1 KB contiguous piece of W.  Workgroups of 8
+// R = 16 RB rows of W (output columns n) x KU = 8192 / R k -- 32 KB of W --
+// ordered row group by row group.  RB = 2 (32 x 256, every row one 1 KB
+// piece) for m <= 16; RB = 4 (64 x 128) for m > 16, which halves the bytes of
+// A read per byte of W (A's slice of a unit is m x KU).  Workgroups of 8
 // wavefronts, one per CU:
 //   * waves 4..7 copy units into a 3-slot LDS ring with direct-to-LDS loads
-//     (global_load_lds_dwordx4: 8 rows per wave, rows padded to 260 floats
-//     so that the operand reads below are free of bank conflicts), and wait
-//     for a unit with s_waitcnt on their own load count;
+//     (global_load_lds_dwordx4, 8 per wave and unit, each one 1 KB row or two
+//     512 B rows).  A slot holds its rows unpadded; the 16-byte chunks of row
+//     r are XOR-swizzled by r % 8 through the loads' global addresses, so the
+//     operand reads below are free of bank conflicts.  A loader waits for a
+//     unit with s_waitcnt on its own load count;
 //   * waves 0..3 run v_mfma_f32_16x16x4_f32 (C^T = W A^T on 16 n x 16 m
 //     blocks, m padded to 16 or 32) over k quarters of each unit: lane
 //     l = 16 q + i reads row i of a 16-row block at k = 16 t + 4 q .. + 3
@@ -515,34 +519,44 @@ hipError_t launch_sk_reduce(hipStream_t s, int m, int n, const float* P, long lo
 //   * every other one (a contributor, whose last segment it is) stores its
 //     block with agent-scope (sc1) stores, waits for their completion
 //     (s_waitcnt vmcnt(0)) and then sets its flag to the launch's epoch;
-//   * at the end of its run the owner waits for the flags of its
-//     contributors, loads their blocks (sc1), adds them in k order followed
-//     by its own, applies the epilogue, stores C and resets the flags.
+//   * at the end of its run the owner waits for the flags of all its
+//     contributors, then loads their blocks (sc1, up to four slots per
+//     batch), adds them in k order followed by its own, applies the
+//     epilogue, stores C and resets the flags.
 // An owner waits only on lower-numbered workgroups, which are dispatched
 // before it and never wait before storing their block, so the wait always
 // ends; it is bounded anyway (a block that never arrives turns the outputs
 // NaN).  The epoch (64-bit, one per launch) keeps stale flags from matching;
 // the reset keeps a replay of a captured launch, which reuses its epoch,
-// from matching the previous replay's flags.  EDGE (K % 256 != 0): loads past K read from K - 4 and both MFMA
-// operands of such k are zeroed where they are used; rows past N read row
-// N - 1 and are never stored.  Requires K % 4 == 0, lda % 4 == 0,
-// ldw % 4 == 0 and 16-byte aligned A and W.
-// Measured on one MI355X at K 4096, N 11008 (per call, M = 8 / 32): with a
-// separate reduce launch 34.6 / 48.5 us, against 35.8 / 51.9 us for the
-// kernel before it (units of 128 rows x 64 k loaded as 4 rows x 256 B per instruction and
-// re-laid per wave through LDS).  A pure read of the weights in this
-// schedule takes 30.2 us; whole-row ownership (each workgroup its own 43
-// rows over all K, no partials) measured 37.7 us at M = 8: the row blocks
-// left per workgroup are short and keep too few bytes in flight.
-constexpr int kRgRows = 32;                    // rows of W (output columns) per unit
-constexpr int kRgK = 256;                      // k per unit
-constexpr int kRgLdr = kRgK + 4;               // padded LDS row (floats)
-constexpr int kRgSlot = kRgRows * kRgLdr * 4;  // bytes per ring slot
-constexpr int kRgD = 3;                        // ring slots
+// from matching the previous replay's flags.  EDGE (K % KU != 0): loads past
+// K read from K - 4 and both MFMA operands of such k are zeroed where they
+// are used; rows past N read row N - 1 and are never stored.  Requires
+// K % 4 == 0, lda % 4 == 0, ldw % 4 == 0 and 16-byte aligned A and W.
+// Measured on one MI355X at K 4096, N 11008, kernel alone (M = 8 / 32):
+// 32 x 256 units padded to 260-float rows 30.9 / 45.7 us; swizzled 31.2 /
+// 43.3 us; 64 x 128 swizzled 32.6 / 38.1 us.  With A's loads removed the
+// padded kernel took 31.6 / 37.2 us: at m > 16 A's slice was as many bytes
+// as the weights.  A pure read of the weights in this schedule takes 30.2
+// us.  Whole-row ownership (each workgroup its own 43 rows over all K, no
+// partials) measured 37.7 us at M = 8: the row blocks left per workgroup are
+// short and keep too few bytes in flight.
+constexpr int kRgUnit = 32768;  // bytes of W per unit and ring slot
+constexpr int kRgD = 3;         // ring slots
 
-template <int MB>
+template <int RB>
+struct RgShape {
+  static constexpr int R = 16 * RB;       // rows of W (output columns) per unit
+  static constexpr int KU = 8192 / R;     // k per unit
+  static constexpr int KQ = KU / 4;       // k per MFMA wave and unit
+  static constexpr int TT = KQ / 16;      // 16-k steps per MFMA wave and unit
+  static constexpr int RPI = 256 / KU;    // rows per load instruction
+};
+
+int rg_rb(int m) { return m <= 16 ? 2 : 4; }
+
+template <int MB, int RB>
 constexpr int rg_lds_bytes() {
-  return kRgD * kRgSlot + 4 * 2 * MB * 4 * 64 * 4;  // ring, then the segment-end sums of 4 waves
+  return kRgD * kRgUnit + 4 * RB * MB * 4 * 64 * 4;  // ring, then the segment-end sums of 4 waves
 }
 
 typedef __attribute__((address_space(3))) void lds_void;
@@ -571,14 +585,16 @@ constexpr int kLgkmZero = 0xC07F;
 
 constexpr unsigned kRgSpin = 1u << 22;  // owner's polls of one flag (about 0.1 s) before giving up
 
-template <int MB, bool EDGE>
+template <int MB, int RB, bool EDGE>
 __global__ __launch_bounds__(512, 1) void sgemm_skinny_nt_ring(
     int M, int N, int K, const float* __restrict__ A, int lda, const float* __restrict__ W, int ldw,
     float* __restrict__ C, int ldc, const float* __restrict__ bias, int act, float* __restrict__ P,
     unsigned long long* __restrict__ F, unsigned long long epoch, long long U, int G, int nkb, int smax) {
+  using S = RgShape<RB>;
+  constexpr int R = S::R, KU = S::KU, KQ = S::KQ, TT = S::TT, RPI = S::RPI;
   extern __shared__ float4 smem4[];
   char* ring = reinterpret_cast<char*>(smem4);
-  float* red = reinterpret_cast<float*>(ring + kRgD * kRgSlot);  // [4 waves][2 rb][MB][4 r][64 lanes]
+  float* red = reinterpret_cast<float*>(ring + kRgD * kRgUnit);  // [4 waves][RB rb][MB][4 r][64 lanes]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int w = blockIdx.x;
   const long long ub = (long long)w * U / G, ue = (long long)(w + 1) * U / G;
@@ -586,18 +602,20 @@ __global__ __launch_bounds__(512, 1) void sgemm_skinny_nt_ring(
   const int g0 = (int)(ub / nkb), t0 = (int)(ub - (long long)g0 * nkb);
 
   if (wave >= 4) {
-    // ---- loader wave lw: rows 8 lw .. 8 lw + 7 of every unit
+    // ---- loader wave lw: rows 4 RB lw .. 4 RB lw + 4 RB - 1 of every unit, RPI rows per load
     const int lw = wave - 4;
+    const int lrow = lane / (64 / RPI), chunk = lane % (64 / RPI);  // this lane's row in a load, its chunk slot
     int lg = g0, lt = t0;
     auto issue = [&](int i) {
-      int kk = kRgK * lt + 4 * lane;
-      if (EDGE) kk = min(kk, K - 4);
-      char* dst = ring + (i % kRgD) * kRgSlot + 8 * lw * (kRgLdr * 4);
+      char* dst = ring + (i % kRgD) * kRgUnit;
 #pragma unroll
-      for (int r = 0; r < 8; ++r) {
-        const int row = min(kRgRows * lg + 8 * lw + r, N - 1);
-        __builtin_amdgcn_global_load_lds(W + (long long)row * ldw + kk, (lds_void*)(dst + r * kRgLdr * 4), 16, 0,
-                                         2 /* nt */);
+      for (int j = 0; j < 8; ++j) {
+        const int rl = 4 * RB * lw + RPI * j;  // first row of load j
+        const int row = rl + lrow;
+        int k = KU * lt + 4 * (chunk ^ (row & 7));
+        if (EDGE) k = min(k, K - 4);
+        const float* src = W + (long long)min(R * lg + row, N - 1) * ldw + k;
+        __builtin_amdgcn_global_load_lds(src, (lds_void*)(dst + rl * KU * 4), 16, 0, 2 /* nt */);
       }
       if (++lt == nkb) {
         lt = 0;
@@ -621,20 +639,20 @@ __global__ __launch_bounds__(512, 1) void sgemm_skinny_nt_ring(
     return;
   }
 
-  // ---- MFMA wave cw: k quarter [64 cw, 64 cw + 64) of every unit
+  // ---- MFMA wave cw: k quarter [KQ cw, KQ cw + KQ) of every unit
   const int cw = wave, q = lane >> 4, i16 = lane & 15;
   const float* arow[MB];
 #pragma unroll
   for (int b = 0; b < MB; ++b) arow[b] = A + (long long)min(16 * b + i16, M - 1) * lda;
   constexpr int PX = 2, NX = PX + 1;  // units of A in flight ahead of the MFMAs
-  float4 av[NX][MB][4];
+  float4 av[NX][MB][TT];
   int xt = t0, xn = 0;  // A cursor: advanced once per load, held at the last unit
   auto load_a = [&](int sb) {
 #pragma unroll
     for (int b = 0; b < MB; ++b)
 #pragma unroll
-      for (int tt = 0; tt < 4; ++tt) {
-        int k = kRgK * xt + 64 * cw + 16 * tt + 4 * q;
+      for (int tt = 0; tt < TT; ++tt) {
+        int k = KU * xt + KQ * cw + 16 * tt + 4 * q;
         if (EDGE) k = min(k, K - 4);  // zeroed where used
         av[sb][b][tt] = *reinterpret_cast<const float4*>(arow[b] + k);
       }
@@ -642,25 +660,27 @@ __global__ __launch_bounds__(512, 1) void sgemm_skinny_nt_ring(
   };
 #pragma unroll
   for (int p = 0; p < PX; ++p) load_a(p);
-  float4 wv[2][2][4];
+  float4 wv[2][RB][TT];
   auto read_w = [&](int sb, int i) {
-    const char* sl = ring + (i % kRgD) * kRgSlot + (64 * cw + 4 * q) * 4;
+    const char* sl = ring + (i % kRgD) * kRgUnit;
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb)
+    for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-      for (int tt = 0; tt < 4; ++tt)
-        wv[sb][rb][tt] = *reinterpret_cast<const float4*>(sl + (16 * rb + i16) * (kRgLdr * 4) + 64 * tt);
+      for (int tt = 0; tt < TT; ++tt) {
+        const int row = 16 * rb + i16, c = (KQ / 4) * cw + 4 * tt + q;
+        wv[sb][rb][tt] = *reinterpret_cast<const float4*>(sl + row * KU * 4 + ((c ^ (row & 7)) << 4));
+      }
   };
-  f32x4v acc[2][MB];
+  f32x4v acc[RB][MB];
 #pragma unroll
-  for (int rb = 0; rb < 2; ++rb)
+  for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
     for (int b = 0; b < MB; ++b) acc[rb][b] = (f32x4v){0.f, 0.f, 0.f, 0.f};
-  // steps t0_, t0_ + 1 of the unit whose k starts at kbase
-  auto mma = [&](int sw, int sx, int t0_, int kbase) {
+  // half h (steps [h TT / 2, (h + 1) TT / 2)) of the unit whose k starts at kbase
+  auto mma = [&](int sw, int sx, int h, int kbase) {
 #pragma unroll
-    for (int tt = t0_; tt < t0_ + 2; ++tt) {
-      const bool live = !EDGE || kbase + 64 * cw + 16 * tt + 4 * q < K;
+    for (int tt = h * TT / 2; tt < (h + 1) * TT / 2; ++tt) {
+      const bool live = !EDGE || kbase + KQ * cw + 16 * tt + 4 * q < K;
 #pragma unroll
       for (int c = 0; c < 4; ++c)
 #pragma unroll
@@ -669,7 +689,7 @@ __global__ __launch_bounds__(512, 1) void sgemm_skinny_nt_ring(
           float x = c == 0 ? a4.x : c == 1 ? a4.y : c == 2 ? a4.z : a4.w;
           if (EDGE) x = live ? x : 0.f;
 #pragma unroll
-          for (int rb = 0; rb < 2; ++rb) {
+          for (int rb = 0; rb < RB; ++rb) {
             const float4 w4 = wv[sw][rb][tt];
             float y = c == 0 ? w4.x : c == 1 ? w4.y : c == 2 ? w4.z : w4.w;
             if (EDGE) y = live ? y : 0.f;
@@ -679,37 +699,39 @@ __global__ __launch_bounds__(512, 1) void sgemm_skinny_nt_ring(
     }
   };
   // Segment end: value r of block (rb, b) at lane (q, i) is n = 16 rb + 4 q + r,
-  // m = 16 b + i.  After the exchange wave cw holds the sums of rows
-  // m = cw + 4 (2 u + lane / 32), n = lane % 32, u < 2 MB.
+  // m = 16 b + i.  After the exchange wave cw holds the sums of column n = lane % R
+  // for rows m = cw + 4 (u 4 / RB + lane / R), u < MB RB.
   // Partial block of (group g, slot sl): [sl][wave][u][lane] floats, lane-major.
+  constexpr int NV = MB * RB;  // sums per lane
   __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(P, 0, 0x7fffffff, 0x00020000);
-  auto pofs = [&](int g, int sl, int u) { return ((((g * smax + sl) * 4 + cw) * 2 * MB + u) * 64 + lane) * 4; };
-  const int ncol = lane & 31;
-  float keep[2 * MB];
+  auto pofs = [&](int g, int sl, int u) { return ((((g * smax + sl) * 4 + cw) * NV + u) * 64 + lane) * 4; };
+  const int ncol = lane % R;
+  auto row_of = [&](int u) { return cw + 4 * (u * (4 / RB) + lane / R); };
+  float keep[NV];
   int own_g = -1;
   auto store_c = [&](int g, const float* val) {
-    const int n = kRgRows * g + ncol;
+    const int n = R * g + ncol;
 #pragma unroll
-    for (int u = 0; u < 2 * MB; ++u) {
-      const int m = cw + 4 * (2 * u + (lane >> 5));
+    for (int u = 0; u < NV; ++u) {
+      const int m = row_of(u);
       if (m < M && n < N) C[(long long)m * ldc + n] = epilogue(val[u], bias, n, act);
     }
   };
   auto seg_end = [&](int g, long long a, long long b) {
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb)
+    for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
       for (int bb = 0; bb < MB; ++bb)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) red[(((cw * 2 + rb) * MB + bb) * 4 + r) * 64 + lane] = acc[rb][bb][r];
+        for (int r = 0; r < 4; ++r) red[(((cw * RB + rb) * MB + bb) * 4 + r) * 64 + lane] = acc[rb][bb][r];
     __builtin_amdgcn_s_waitcnt(kLgkmZero);
     rg_barrier();
     const int rb = ncol >> 4, qq = (ncol >> 2) & 3, r = ncol & 3;
-    constexpr int kWave = 2 * MB * 4 * 64;  // one wave's values
-    float val[2 * MB];
+    constexpr int kWave = RB * MB * 4 * 64;  // one wave's values
+    float val[NV];
 #pragma unroll
-    for (int u = 0; u < 2 * MB; ++u) {
-      const int m = cw + 4 * (2 * u + (lane >> 5));
+    for (int u = 0; u < NV; ++u) {
+      const int m = row_of(u);
       const int e = ((rb * MB + (m >> 4)) * 4 + r) * 64 + 16 * qq + (m & 15);
       val[u] = ((red[e] + red[kWave + e]) + red[2 * kWave + e]) + red[3 * kWave + e];
     }
@@ -718,12 +740,12 @@ __global__ __launch_bounds__(512, 1) void sgemm_skinny_nt_ring(
       store_c(g, val);
     } else if (b == ge) {
 #pragma unroll
-      for (int u = 0; u < 2 * MB; ++u) keep[u] = val[u];
+      for (int u = 0; u < NV; ++u) keep[u] = val[u];
       own_g = g;
     } else {
       const int sl = w - wg_of_unit(gs, U, G);
 #pragma unroll
-      for (int u = 0; u < 2 * MB; ++u)
+      for (int u = 0; u < NV; ++u)
         __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(val[u]), prs, pofs(g, sl, u), 0, 16 /* sc1 */);
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       if (lane == 0)
@@ -731,7 +753,7 @@ __global__ __launch_bounds__(512, 1) void sgemm_skinny_nt_ring(
                            __HIP_MEMORY_SCOPE_AGENT);
     }
 #pragma unroll
-    for (int rb2 = 0; rb2 < 2; ++rb2)
+    for (int rb2 = 0; rb2 < RB; ++rb2)
 #pragma unroll
       for (int bb = 0; bb < MB; ++bb) acc[rb2][bb] = (f32x4v){0.f, 0.f, 0.f, 0.f};
   };
@@ -747,11 +769,11 @@ __global__ __launch_bounds__(512, 1) void sgemm_skinny_nt_ring(
       const int i = i0 + p;
       if (i < nu) {
         load_a((p + PX) % NX);
-        mma(p & 1, p % NX, 0, kRgK * tcur);
+        mma(p & 1, p % NX, 0, KU * tcur);
         __builtin_amdgcn_s_waitcnt(kLgkmZero);  // this unit's ring reads are complete
         rg_barrier();
         if (i + 1 < nu) read_w((p + 1) & 1, i + 1);
-        mma(p & 1, p % NX, 2, kRgK * tcur);
+        mma(p & 1, p % NX, 1, KU * tcur);
         const bool group_end = ++tcur == nkb;
         if (group_end || i + 1 == nu) {
           seg_end(gcur, seg_a, ub + i + 1);
@@ -769,9 +791,10 @@ __global__ __launch_bounds__(512, 1) void sgemm_skinny_nt_ring(
     const int nprev = w - wg_of_unit((long long)own_g * nkb, U, G);
     unsigned long long* fl = F + (long long)own_g * smax * 4 + cw;
     bool ok = true;
-    float sum[2 * MB];
+    float sum[NV];
 #pragma unroll
-    for (int u = 0; u < 2 * MB; ++u) sum[u] = 0.f;
+    for (int u = 0; u < NV; ++u) sum[u] = 0.f;
+    // every flag first, then the blocks in batches of up to four slots (one round trip each)
     for (int sl = 0; sl < nprev; ++sl) {
       unsigned n = 0;
       while (__hip_atomic_load(fl + 4 * sl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != epoch && n < kRgSpin) {
@@ -779,12 +802,24 @@ __global__ __launch_bounds__(512, 1) void sgemm_skinny_nt_ring(
         ++n;
       }
       ok = ok && n < kRgSpin;
+    }
+    for (int s0 = 0; s0 < nprev; s0 += 4) {
+      float v[4][NV];
 #pragma unroll
-      for (int u = 0; u < 2 * MB; ++u)
-        sum[u] += __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(prs, pofs(own_g, sl, u), 0, 16 /* sc1 */));
+      for (int j = 0; j < 4; ++j) {
+        const int sl = min(s0 + j, nprev - 1);  // past the last slot: loaded again, not added
+#pragma unroll
+        for (int u = 0; u < NV; ++u)
+          v[j][u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(prs, pofs(own_g, sl, u), 0, 16 /* sc1 */));
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int u = 0; u < NV; ++u)
+          if (s0 + j < nprev) sum[u] += v[j][u];
     }
 #pragma unroll
-    for (int u = 0; u < 2 * MB; ++u) sum[u] = ok ? sum[u] + keep[u] : __builtin_nanf("");
+    for (int u = 0; u < NV; ++u) sum[u] = ok ? sum[u] + keep[u] : __builtin_nanf("");
     store_c(own_g, sum);
     if (lane == 0)
       for (int sl = 0; sl < nprev; ++sl) __hip_atomic_store(fl + 4 * sl, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -993,16 +1028,18 @@ W32Plan w32_plan(int n, int k) {
   return p;
 }
 
-// transposed-weight path: 32-row x 256-k units, one workgroup per CU
+// transposed-weight path: units of 16 rg_rb(m) rows x 8192 / (16 rg_rb(m)) k, one workgroup per CU
 struct NtPlan {
   long long U = 0;
-  int ng = 0, nkb = 0, G = 0, smax = 0;
+  int rb = 0, ng = 0, nkb = 0, G = 0, smax = 0;
 };
 
-NtPlan nt_plan(int n, int k) {
+NtPlan nt_plan(int m, int n, int k) {
   NtPlan p;
-  p.ng = (n + kRgRows - 1) / kRgRows;
-  p.nkb = (k + kRgK - 1) / kRgK;
+  p.rb = rg_rb(m);
+  const int rows = 16 * p.rb, ku = 8192 / rows;
+  p.ng = (n + rows - 1) / rows;
+  p.nkb = (k + ku - 1) / ku;
   p.U = (long long)p.ng * p.nkb;
   long long g = cu_count();
   if (g > p.U) g = p.U;
@@ -1014,9 +1051,9 @@ NtPlan nt_plan(int n, int k) {
   return p;
 }
 
-// the ring kernel's partial blocks (M padded to 16 or 32), 256-byte aligned; its flags follow
+// the ring kernel's partial blocks (MB RB sums per lane and wave), 256-byte aligned; its flags follow
 size_t nt_partial_bytes(const NtPlan& p, int m) {
-  const size_t b = sizeof(float) * (size_t)p.ng * (size_t)p.smax * 4 * (m <= 16 ? 2 : 4) * 64;
+  const size_t b = sizeof(float) * (size_t)p.ng * (size_t)p.smax * 4 * (m <= 16 ? 1 : 2) * p.rb * 64;
   return (b + 255) & ~(size_t)255;
 }
 
@@ -1085,14 +1122,14 @@ struct RingArgs {
   int act;
 };
 
-template <int MB, bool EDGE>
+template <int MB, int RB, bool EDGE>
 hipError_t launch_nt_ring(hipStream_t s, const NtPlan& p, int m, int n, int k, const float* A, int lda,
                           const float* W, int ldw, const RingArgs& r) {
-  const void* f = reinterpret_cast<const void*>(sgemm_skinny_nt_ring<MB, EDGE>);
-  hipError_t e = bch::ensure_dynamic_lds(f, rg_lds_bytes<MB>());
+  const void* f = reinterpret_cast<const void*>(sgemm_skinny_nt_ring<MB, RB, EDGE>);
+  hipError_t e = bch::ensure_dynamic_lds(f, rg_lds_bytes<MB, RB>());
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((sgemm_skinny_nt_ring<MB, EDGE>), dim3(p.G), dim3(512), rg_lds_bytes<MB>(), s, m, n, k, A, lda,
-                     W, ldw, r.C, r.ldc, r.bias, r.act, r.P, r.F, r.epoch, p.U, p.G, p.nkb, p.smax);
+  hipLaunchKernelGGL((sgemm_skinny_nt_ring<MB, RB, EDGE>), dim3(p.G), dim3(512), (rg_lds_bytes<MB, RB>()), s, m, n,
+                     k, A, lda, W, ldw, r.C, r.ldc, r.bias, r.act, r.P, r.F, r.epoch, p.U, p.G, p.nkb, p.smax);
   return hipGetLastError();
 }
 
@@ -1109,7 +1146,7 @@ bool sgemm_skinny_nt_applies(int m, int n, int k, const float* A, int lda, const
 
 size_t sgemm_skinny_nt_workspace_bytes(int m, int n, int k) {
   if (use_rows(m, n, k)) return 0;
-  const NtPlan p = nt_plan(n, k);
+  const NtPlan p = nt_plan(m, n, k);
   return nt_partial_bytes(p, m) + sizeof(unsigned long long) * (size_t)p.ng * (size_t)p.smax * 4;
 }
 
@@ -1123,16 +1160,18 @@ hipError_t launch_sgemm_skinny_nt(hipStream_t s, int m, int n, int k, const floa
     return launch_rows<4>(s, m, n, k, A, lda, W, ldw, C, ldc, bias, act);
   }
   if (ws == nullptr || ws_bytes < sgemm_skinny_nt_workspace_bytes(m, n, k)) return hipErrorInvalidValue;
-  const NtPlan p = nt_plan(n, k);
+  const NtPlan p = nt_plan(m, n, k);
   RingArgs r{static_cast<float*>(ws),
              reinterpret_cast<unsigned long long*>(static_cast<char*>(ws) + nt_partial_bytes(p, m)),
              ++g_nt_epoch, C, ldc, bias, act};
-  const bool edge = k % kRgK != 0;
-  if (m <= 16)
-    return edge ? launch_nt_ring<1, true>(s, p, m, n, k, A, lda, W, ldw, r)
-                : launch_nt_ring<1, false>(s, p, m, n, k, A, lda, W, ldw, r);
-  return edge ? launch_nt_ring<2, true>(s, p, m, n, k, A, lda, W, ldw, r)
-              : launch_nt_ring<2, false>(s, p, m, n, k, A, lda, W, ldw, r);
+  if (m <= 16) {  // rg_rb(m) == 2
+    const bool edge = k % RgShape<2>::KU != 0;
+    return edge ? launch_nt_ring<1, 2, true>(s, p, m, n, k, A, lda, W, ldw, r)
+                : launch_nt_ring<1, 2, false>(s, p, m, n, k, A, lda, W, ldw, r);
+  }
+  const bool edge = k % RgShape<4>::KU != 0;  // rg_rb(m) == 4
+  return edge ? launch_nt_ring<2, 4, true>(s, p, m, n, k, A, lda, W, ldw, r)
+              : launch_nt_ring<2, 4, false>(s, p, m, n, k, A, lda, W, ldw, r);
 }
 
 size_t sgemm_skinny_workspace_bytes(int m, int n, int k) {
