@@ -47,6 +47,7 @@ SIGNATURES = {
     "bch_ctx_create": (_i, [_i, C.c_char_p, C.POINTER(_vp)]),
     "bch_ctx_destroy": (None, [_vp]),
     "bch_ctx_is_lost": (_i, [_vp, C.POINTER(_i)]),
+    "bch_ctx_stream": (_i, [_vp, C.POINTER(_vp)]),
     "bch_last_error": (C.c_char_p, [_vp]),
     "bch_status_string": (C.c_char_p, [_i]),
     "bch_alloc": (_i, [_vp, _sz, C.POINTER(_vp)]),

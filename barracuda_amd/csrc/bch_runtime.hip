@@ -267,6 +267,12 @@ bch_status bch_ctx_is_lost(const bch_ctx* ctx, int* lost) {
   return BCH_OK;
 }
 
+bch_status bch_ctx_stream(const bch_ctx* ctx, void** stream) {
+  if (!ctx || !stream) return fail(nullptr, BCH_E_INVALID, "bch_ctx_stream: NULL argument");
+  *stream = ctx->stream;
+  return BCH_OK;
+}
+
 void bch_ctx_destroy(bch_ctx* ctx) {
   if (!ctx) return;
   (void)hipSetDevice(ctx->device);

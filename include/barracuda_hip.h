@@ -74,6 +74,16 @@ void bch_ctx_destroy(bch_ctx *ctx);
  * error (fault injection for this mapping; no kernel runs). */
 bch_status bch_ctx_is_lost(const bch_ctx *ctx, int *lost);
 
+/* *stream = the context's HIP stream (a hipStream_t).  No counterpart in
+ * the reference, whose wgpu queue is internal: it is for callers that order
+ * the context's work against their own streams or capture it into a HIP
+ * graph.  Capture only calls whose workspace already exists (make each call
+ * once outside the capture first): a call that has to grow the workspace
+ * allocates.  Every captured call replays correctly any number of times;
+ * replays and eager calls on one context must not overlap (they share the
+ * workspace). */
+bch_status bch_ctx_stream(const bch_ctx *ctx, void **stream);
+
 /* Message of the last failed call on ctx; with ctx == NULL, the calling
  * thread's last failure.  Never NULL ("" when none). */
 const char *bch_last_error(const bch_ctx *ctx);

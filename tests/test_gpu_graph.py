@@ -1,0 +1,118 @@
+"""HIP graph capture of the library's calls on a context's stream (bch_ctx_stream).
+
+Captured: the decode linear layer with [out, in] weights (the ring kernel, whose
+split-k blocks are combined in the kernel through epoch flags that every launch
+resets), the skinny GEMM (main kernel + reduce), row softmax and attention.  The
+graph is replayed several times with the program's own eager calls (which reuse the
+same workspace and flags) and synchronisations between the replays; every replay
+must reproduce the eager results bit for bit.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from barracuda_amd import Tensor
+from barracuda_amd import _native as N
+from oracle import bc_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+HIP_LIB = "/opt/rocm/lib/libamdhip64.so.7"  # the runtime libbarracuda_hip.so is linked against
+CAPTURE_RELAXED = 2                          # hipStreamCaptureModeRelaxed
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+def _hip():
+    h = C.CDLL(HIP_LIB)
+    h.hipStreamBeginCapture.argtypes = [C.c_void_p, C.c_int]
+    h.hipStreamEndCapture.argtypes = [C.c_void_p, C.POINTER(C.c_void_p)]
+    h.hipGraphInstantiate.argtypes = [C.POINTER(C.c_void_p), C.c_void_p, C.c_void_p, C.c_char_p, C.c_size_t]
+    h.hipGraphLaunch.argtypes = [C.c_void_p, C.c_void_p]
+    h.hipGraphExecDestroy.argtypes = [C.c_void_p]
+    h.hipGraphDestroy.argtypes = [C.c_void_p]
+    for f in ("hipStreamBeginCapture", "hipStreamEndCapture", "hipGraphInstantiate", "hipGraphLaunch",
+              "hipGraphExecDestroy", "hipGraphDestroy"):
+        getattr(h, f).restype = C.c_int
+    return h
+
+
+def _up(dev, a):
+    return Tensor.from_data(np.ascontiguousarray(a, dtype=np.float32), list(a.shape), dev)
+
+
+def test_graph_replays_match_eager(dev):
+    _say("graph capture: decode linear, skinny GEMM, softmax, attention")
+    hip = _hip()
+    lib = dev._lib
+    stream = C.c_void_p()
+    dev.check(lib.bch_ctx_stream(dev.ctx, C.byref(stream)), "ctx_stream")
+    assert stream.value
+
+    rng = O.Lcg(2024)
+    calls = []  # (name, zero-arg launcher, output tensor)
+    for m, n, k in ((8, 11008, 4096), (32, 11008, 4096), (8, 64, 16384)):
+        x, w, b = _up(dev, rng.normal((m, k))), _up(dev, rng.normal((n, k), 0.0, 0.05)), _up(dev, rng.normal((n,)))
+        y = Tensor.empty([m, n], dev)
+        calls.append((f"linear wT m={m} n={n} k={k}",
+                      lambda m=m, n=n, k=k, x=x, w=w, b=b, y=y: lib.bch_sgemm_ex(
+                          dev.ctx, 1, m, n, k, C.c_void_p(x.ptr), k, C.c_void_p(w.ptr), k, C.c_void_p(b.ptr),
+                          N.BCH_ACT_GELU, C.c_void_p(y.ptr), n), y))
+    m, n, k = 8, 11008, 4096
+    xa, wa = _up(dev, rng.normal((m, k))), _up(dev, rng.normal((k, n), 0.0, 0.02))
+    ya = Tensor.empty([m, n], dev)
+    calls.append(("skinny m=8", lambda: lib.bch_sgemm(dev.ctx, m, n, k, C.c_void_p(xa.ptr), k, C.c_void_p(wa.ptr), n,
+                                                       C.c_void_p(ya.ptr), n), ya))
+    rows, cols = 512, 2048
+    sx = _up(dev, rng.normal((rows, cols), 0.0, 3.0))
+    sy = Tensor.empty([rows, cols], dev)
+    calls.append(("softmax rows", lambda: lib.bch_softmax_rows(dev.ctx, rows, cols, C.c_void_p(sx.ptr),
+                                                                C.c_void_p(sy.ptr)), sy))
+    B, H, S, D = 1, 4, 256, 128
+    q, kk, v = (_up(dev, rng.normal((B, H, S, D))) for _ in range(3))
+    o = Tensor.empty([B, H, S, D], dev)
+    calls.append(("sdpa causal", lambda: lib.bch_sdpa_fwd(dev.ctx, B, H, S, S, D, C.c_float(D ** -0.5), 1,
+                                                           C.c_void_p(q.ptr), C.c_void_p(kk.ptr), C.c_void_p(v.ptr),
+                                                           C.c_void_p(o.ptr)), o))
+
+    # eager results (these calls also size the workspace, so the capture allocates nothing)
+    want = []
+    for name, run, out in calls:
+        with dev._lock:
+            dev.check(run(), name)
+        want.append(out.to_numpy())
+
+    graph, exe = C.c_void_p(), C.c_void_p()
+    with dev._lock:
+        assert hip.hipStreamBeginCapture(stream, CAPTURE_RELAXED) == 0
+        try:
+            for name, run, _ in calls:
+                dev.check(run(), name + " (captured)")
+        finally:
+            assert hip.hipStreamEndCapture(stream, C.byref(graph)) == 0
+    try:
+        assert hip.hipGraphInstantiate(C.byref(exe), graph, None, None, 0) == 0
+        nan_fill = [np.full(out.to_numpy().shape, np.nan, np.float32) for _, _, out in calls]
+        for rep in range(4):
+            for (_, _, out), fill in zip(calls, nan_fill):
+                dev.upload(out.ptr, fill)
+            with dev._lock:
+                assert hip.hipGraphLaunch(exe, stream) == 0
+            dev.sync()
+            for (name, _, out), ref in zip(calls, want):
+                assert np.array_equal(out.to_numpy(), ref), (rep, name)
+            # eager calls between the replays: the same workspace, flags and outputs
+            for (name, run, out), ref in zip(calls, want):
+                with dev._lock:
+                    dev.check(run(), name)
+                assert np.array_equal(out.to_numpy(), ref), (rep, name, "eager")
+    finally:
+        if exe.value:
+            hip.hipGraphExecDestroy(exe)
+        if graph.value:
+            hip.hipGraphDestroy(graph)
