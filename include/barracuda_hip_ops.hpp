@@ -261,6 +261,9 @@ class Tensor {
   inline Result<Tensor> batch_matmul(const Tensor& other) const;
   inline Result<Tensor> softmax() const;
   inline Result<Tensor> softmax_dim(size_t axis) const;
+  inline Result<Tensor> relu() const;                           // ops/relu.rs:106
+  inline Result<Tensor> gelu_wgsl() const;                      // ops/gelu_wgsl.rs:147
+  inline Result<Tensor> layer_norm_wgsl(float epsilon) const;   // ops/layer_norm_wgsl.rs:160-165
   inline Result<Tensor> attention(const Tensor& key, const Tensor& value) const;
   inline Result<Tensor> scaled_dot_product_attention(const Tensor& key, const Tensor& value) const;
   inline Result<Tensor> causal_attention(const Tensor& key, const Tensor& value) const;
@@ -377,6 +380,61 @@ inline std::optional<BarracudaError> validate_softmax_dim(const std::vector<size
                                       "Axis " + std::to_string(axis) + " out of bounds for shape " + shape_str(s));
   return std::nullopt;
 }
+
+namespace detail {
+// one element-wise op (bch_elementwise) from `in` into a new tensor of its shape
+inline Result<Tensor> unary(const Tensor& in, int op, const char* name) {
+  auto dev = in.device();
+  auto r = Tensor::empty(in.shape(), dev);
+  if (r.is_err() || in.len() == 0) return r;
+  Tensor out = std::move(r).unwrap();
+  std::lock_guard<std::mutex> g(dev->mutex());
+  if (auto e = dev->check(bch_elementwise(dev->ctx(), op, (long long)in.len(), in.data_ptr(), nullptr, nullptr, 0.0f,
+                                          out.data_ptr()),
+                          name))
+    return *e;
+  return out;
+}
+}  // namespace detail
+
+// ops/relu.rs: max(x, 0) over every element (relu_f64.wgsl)
+struct ReLU {
+  const Tensor& input;
+  Result<Tensor> execute() const { return detail::unary(input, BCH_EW_RELU, "relu"); }
+};
+
+// ops/gelu_wgsl.rs:33-141: 0.5 x (1 + tanh(0.7978845608 (x + 0.044715 x^3)))
+// over every element (gelu_f64.wgsl)
+struct GELU {
+  const Tensor& input;
+  Result<Tensor> execute() const { return detail::unary(input, BCH_EW_GELU, "gelu"); }
+};
+
+// ops/layer_norm_wgsl.rs:47-157: each row along the last dimension becomes
+// (x - mean) / sqrt(var + epsilon), biased variance, no affine parameters
+// (layer_norm_f64.wgsl)
+struct LayerNorm {
+  const Tensor& input;
+  float epsilon;
+  static std::optional<BarracudaError> validate(const std::vector<size_t>& s) {
+    if (s.empty()) return BarracudaError::invalid_op("LayerNorm", "Empty tensor not supported");
+    return std::nullopt;
+  }
+  Result<Tensor> execute() const {
+    if (auto e = validate(input.shape())) return *e;
+    auto dev = input.device();
+    auto r = Tensor::empty(input.shape(), dev);
+    if (r.is_err() || input.len() == 0) return r;
+    Tensor out = std::move(r).unwrap();
+    const size_t cols = input.shape().back(), rows = input.len() / cols;
+    std::lock_guard<std::mutex> g(dev->mutex());
+    if (auto e = dev->check(bch_layer_norm(dev->ctx(), (long long)rows, (long long)cols, epsilon, input.data_ptr(),
+                                           out.data_ptr()),
+                            "layer_norm"))
+      return *e;
+    return out;
+  }
+};
 
 namespace detail {
 inline Result<Tensor> sdpa(const Tensor& q, const Tensor& k, const Tensor& v, bool causal, const char* op, size_t B,
@@ -619,6 +677,9 @@ inline Result<Tensor> Tensor::matmul_ref(const Tensor& other) const { return Mat
 inline Result<Tensor> Tensor::matmul_tiled(const Tensor& other) const { return MatmulTiled{*this, other}.execute(); }
 inline Result<Tensor> Tensor::batch_matmul(const Tensor& other) const { return BatchMatMul{*this, other}.execute(); }
 inline Result<Tensor> Tensor::softmax() const { return Softmax{*this}.execute(); }
+inline Result<Tensor> Tensor::relu() const { return ReLU{*this}.execute(); }
+inline Result<Tensor> Tensor::gelu_wgsl() const { return GELU{*this}.execute(); }
+inline Result<Tensor> Tensor::layer_norm_wgsl(float epsilon) const { return LayerNorm{*this, epsilon}.execute(); }
 inline Result<Tensor> Tensor::softmax_dim(size_t axis) const {
   if (auto e = validate_softmax_dim(shape_, axis)) return *e;
   auto r = Tensor::empty(shape_, dev_);
@@ -654,8 +715,9 @@ inline Result<Tensor> Tensor::multi_head_attention(const Tensor& key, const Tens
 
 // ---------------------------------------------------------------- nn
 namespace nn {
-// nn/fused_mlp.rs:25-31
-enum class Activation { ReLU };
+// nn/fused_mlp.rs:25-31 (ReLU); GELU applies gelu_f64.wgsl's tanh form in the
+// same GEMM epilogue
+enum class Activation { ReLU, GELU };
 
 // nn/fused_mlp.rs:38-168: per layer y = relu(x W^T + b) (W [out, in]) or
 // relu(x W + b) (W [in, out]); the reference dispatches linear_f64.wgsl and
@@ -697,7 +759,7 @@ inline Result<Tensor> fused_mlp(const Tensor& input, const std::vector<Tensor>& 
     in_features = L.out;
   }
   auto dev = input.device();
-  const int act = activation == Activation::ReLU ? BCH_ACT_RELU : BCH_ACT_NONE;
+  const int act = activation == Activation::ReLU ? BCH_ACT_RELU : BCH_ACT_GELU;
   Tensor x = input;
   for (size_t i = 0; i < layers.size(); ++i) {
     const Layer& L = layers[i];

@@ -111,6 +111,11 @@ void cpu_tests() {
             "Invalid operation: multi_head_attention - d_model (64) must be divisible by num_heads (7)");
     REQUIRE(!MultiHeadAttention::validate(x, {2, 16, 64}, {2, 16, 64}, ws, 8));  // cross-attention
   });
+  run("validate_layer_norm", [] {  // ops/layer_norm_wgsl.rs:160-165
+    REQUIRE(LayerNorm::validate({})->message == "Invalid operation: LayerNorm - Empty tensor not supported");
+    REQUIRE(!LayerNorm::validate({3}));
+    REQUIRE(!LayerNorm::validate({2, 3, 4}));
+  });
   run("validate_fused_mlp", [] {  // nn/fused_mlp.rs:44-97 (runs before any device use)
     auto r = nn::fused_mlp(Tensor::null_for_tests({4, 8}), {}, {});
     REQUIRE(r.is_err() && r.error().message == "Invalid input: fused_mlp: at least one layer required");
@@ -358,6 +363,57 @@ void gpu_tests() {
       }
     }
     REQUIRE(out.to_vec().unwrap() == y);
+  });
+  run("test_relu_gelu_layer_norm", [] {  // ops/relu.rs, ops/gelu_wgsl.rs, ops/layer_norm_wgsl.rs:166-192
+    std::vector<float> x(3 * 1000);
+    for (size_t i = 0; i < x.size(); ++i) x[i] = 0.01f * (float)((int)(i * 37 % 1201) - 600);
+    auto t = T(x, {3, 1000});
+    // relu is one IEEE max per element: exact
+    auto r = t.relu().unwrap();
+    REQUIRE(r.shape() == t.shape());
+    auto rv = r.to_vec().unwrap();
+    for (size_t i = 0; i < x.size(); ++i) REQUIRE(rv[i] == std::fmax(x[i], 0.0f));
+    // gelu: the tanh form in double, |err| <= 1e-4 max(|ref|, 1)
+    auto gv = t.gelu_wgsl().unwrap().to_vec().unwrap();
+    for (size_t i = 0; i < x.size(); ++i) {
+      const double v = x[i], ref = 0.5 * v * (1.0 + std::tanh(0.7978845608028654 * (v + 0.044715 * v * v * v)));
+      REQUIRE(std::fabs(gv[i] - ref) <= 1e-4 * std::fmax(std::fabs(ref), 1.0));
+    }
+    REQUIRE(T({0.0f}, {1}).gelu_wgsl().unwrap().to_vec().unwrap()[0] == 0.0f);
+    // layer norm: [1, 2, 3, 4]'s closed form, zero row means, constant rows exactly 0
+    auto y = T({1, 2, 3, 4}, {1, 4}).layer_norm_wgsl(1e-5f).unwrap().to_vec().unwrap();
+    for (int i = 0; i < 4; ++i) REQUIRE(std::fabs(y[i] - (i + 1 - 2.5) / std::sqrt(1.25 + 1e-5)) < 1e-6);
+    auto lv = t.layer_norm_wgsl(1e-5f).unwrap().to_vec().unwrap();
+    for (size_t row = 0; row < 3; ++row) {
+      double mean = 0, var = 0;
+      for (size_t c = 0; c < 1000; ++c) mean += x[row * 1000 + c];
+      mean /= 1000;
+      for (size_t c = 0; c < 1000; ++c) var += (x[row * 1000 + c] - mean) * (x[row * 1000 + c] - mean);
+      var /= 1000;
+      for (size_t c = 0; c < 1000; ++c) {
+        const double ref = (x[row * 1000 + c] - mean) / std::sqrt(var + 1e-5);
+        REQUIRE(std::fabs(lv[row * 1000 + c] - ref) <= 1e-4 * std::fmax(std::fabs(ref), 1.0));
+      }
+    }
+    auto z = T(std::vector<float>(2 * 64, 3.0f), {2, 64}).layer_norm_wgsl(1e-5f).unwrap().to_vec().unwrap();
+    for (float v : z) REQUIRE(v == 0.0f);
+  });
+  run("test_fused_mlp_gelu", [] {  // GELU in the GEMM epilogue, W [out, in]
+    const size_t batch = 5, d0 = 64, d1 = 48;
+    std::vector<float> x(batch * d0), w(d1 * d0), b(d1);
+    for (size_t i = 0; i < x.size(); ++i) x[i] = 0.125f * (float)((int)(i % 9) - 4);
+    for (size_t i = 0; i < w.size(); ++i) w[i] = 0.0625f * (float)((int)(i % 7) - 3);
+    for (size_t i = 0; i < d1; ++i) b[i] = 0.25f * (float)((int)i % 5 - 2);
+    auto out = nn::fused_mlp(T(x, {batch, d0}), {T(w, {d1, d0})}, {T(b, {d1})}, nn::Activation::GELU).unwrap();
+    REQUIRE(out.shape() == (std::vector<size_t>{batch, d1}));
+    auto got = out.to_vec().unwrap();
+    for (size_t r = 0; r < batch; ++r)
+      for (size_t o = 0; o < d1; ++o) {
+        double s = b[o];
+        for (size_t i = 0; i < d0; ++i) s += (double)x[r * d0 + i] * w[o * d0 + i];
+        const double ref = 0.5 * s * (1.0 + std::tanh(0.7978845608028654 * (s + 0.044715 * s * s * s)));
+        REQUIRE(std::fabs(got[r * d1 + o] - ref) <= 1e-4 * std::fmax(std::fabs(ref), 1.0));
+      }
   });
   run("test_gemm_f64_basic_transpose_batched", [] {  // ops/linalg/gemm_f64.rs tests
     const std::vector<double> want{19, 22, 43, 50};

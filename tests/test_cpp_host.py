@@ -24,6 +24,7 @@ def test_cpp_host_validation_without_device():
     out = _run("--cpu")
     assert "PASS validate_matmul_inner_dim_mismatch" in out
     assert "PASS validate_fused_mlp" in out
+    assert "PASS validate_layer_norm" in out
     assert "PASS no_device_is_an_error_value" in out
 
 
@@ -34,5 +35,6 @@ def test_cpp_host_ops_on_gpu():
                  "test_softmax_dim_rows_and_columns", "test_attention_basic", "test_sdpa_and_causal",
                  "test_fault_injection_shape_mismatch", "test_grouped_query_attention_basic",
                  "test_mha_basic_and_cross_attention", "test_fused_mlp_two_layers",
-                 "test_gemm_f64_basic_transpose_batched"):
+                 "test_gemm_f64_basic_transpose_batched",
+                 "test_relu_gelu_layer_norm", "test_fused_mlp_gelu"):
         assert f"PASS {name}" in out
