@@ -64,9 +64,11 @@ SIGNATURES = {
     "bch_dgemm": (_i, [_vp, _i, _i, _i, _i, _i, _i, C.c_double, _vp, _i, _ll, _vp, _i, _ll, C.c_double, _vp,
                        _i, _ll]),
     "bch_softmax_rows": (_i, [_vp, _ll, _ll, _vp, _vp]),
+    "bch_softmax_rows_f64": (_i, [_vp, _ll, _ll, _vp, _vp]),
     "bch_elementwise": (_i, [_vp, _i, _ll, _vp, _vp, _vp, _f, _vp]),
     "bch_layer_norm": (_i, [_vp, _ll, _ll, _f, _vp, _vp]),
     "bch_layer_norm_kernel_name": (C.c_char_p, [_ll, _ll]),
+    "bch_softmax_rows_f64_kernel_name": (C.c_char_p, [_ll, _ll, _vp, _vp]),
     "bch_softmax_axis": (_i, [_vp, _ll, _ll, _ll, _vp, _vp]),
     "bch_sdpa_fwd": (_i, [_vp, _i, _i, _i, _i, _i, _f, _i, _vp, _vp, _vp, _vp]),
     "bch_sdpa_fwd_ex": (_i, [_vp, _i, _i, _i, _i, _i, _i, _f, _i, _vp, AttnLayout, _vp, AttnLayout, _vp,

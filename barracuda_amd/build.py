@@ -38,7 +38,8 @@ DEVICE_FLAGS = [
 ]
 SOURCES = ["bch_runtime.hip", "softmax_rows.hip", "sgemm_mfma.hip",
            "sgemm_skinny.hip", "sdpa_fwd.hip", "dgemm_mfma.hip",
-           "rng_fill.hip", "copy.hip", "elementwise.hip", "layer_norm.hip"]
+           "rng_fill.hip", "copy.hip", "elementwise.hip", "layer_norm.hip",
+           "softmax_f64.hip"]
 # Per-file code-generation flags.  The skinny GEMM keeps its MFMA
 # accumulators in VGPRs: with the default heuristics the compiler parks them
 # in AGPRs and copies them back and forth inside the k loop (measured: 716

@@ -103,6 +103,12 @@ hipError_t launch_softmax_axis(hipStream_t s, long long outer, long long axis,
 size_t softmax_axis_workspace_bytes(long long outer, long long axis,
                                     long long inner);
 const char* softmax_kernel_name(long long rows, long long cols);
+// Row softmax over a contiguous [rows, cols] f64 matrix (in may equal out);
+// no scratch.  aligned16: both matrices 16-byte aligned.
+hipError_t launch_softmax_rows_f64(hipStream_t s, long long rows, long long cols,
+                                   const double* in, double* out);
+const char* softmax_f64_kernel_name(long long rows, long long cols,
+                                    bool aligned16);
 
 // C[b] = A[b] . B[b] (row-major), b < batch.  ws/ws_bytes: device scratch
 // of at least sgemm_workspace_bytes(batch, m, n, k) bytes.
@@ -144,11 +150,15 @@ bool sgemm_skinny_applies(int m, int n, int k, const float* A, int lda,
 
 // f64 GEMM on the FP64 matrix cores: C[b] = alpha op(A[b]) op(B[b]) (+ beta
 // C[b] when beta != 0); transa: A stored [k][m]; transb: B stored [n][k].
+// ws/ws_bytes: device scratch of at least dgemm_workspace_bytes(batch, m, n,
+// k) bytes (the split-k partials; zero when k is not split).
 hipError_t launch_dgemm(hipStream_t s, bool transa, bool transb, int batch,
                         int m, int n, int k, double alpha, const double* A,
                         int lda, long long sA, const double* B, int ldb,
                         long long sB, double beta, double* C, int ldc,
-                        long long sC);
+                        long long sC, void* ws, size_t ws_bytes);
+size_t dgemm_workspace_bytes(int batch, int m, int n, int k);
+int dgemm_split_count(int batch, int m, int n, int k);
 
 // Seeded fills (rng.rs LCG / lattice Box-Muller); state is the value before.
 hipError_t launch_fill_uniform(hipStream_t s, float* out, uint64_t n, uint64_t state, double lo,

@@ -485,9 +485,14 @@ bch_status bch_dgemm(bch_ctx* ctx, int transa, int transb, int batch, int m, int
   if (!C || (k > 0 && (!A || !B))) return fail(ctx, BCH_E_INVALID, "gemm_f64: NULL buffer");
   bch_status st = use(ctx);
   if (st != BCH_OK) return st;
+  const size_t wsb = bch::dgemm_workspace_bytes(batch, m, n, k);
+  if (wsb) {
+    st = ensure_ws(ctx, wsb);
+    if (st != BCH_OK) return st;
+  }
   return from_hip(ctx,
                   bch::launch_dgemm(ctx->stream, transa != 0, transb != 0, batch, m, n, k, alpha, A, lda, strideA,
-                                    B, ldb, strideB, beta, C, ldc, strideC),
+                                    B, ldb, strideB, beta, C, ldc, strideC, ctx->ws, ctx->ws_bytes),
                   "gemm_f64 launch");
 }
 
@@ -505,6 +510,17 @@ bch_status bch_softmax_rows(bch_ctx* ctx, long long rows, long long cols, const 
   }
   return from_hip(ctx, bch::launch_softmax_rows(ctx->stream, rows, cols, in, out, ctx->ws, ctx->ws_bytes),
                   "softmax launch");
+}
+
+bch_status bch_softmax_rows_f64(bch_ctx* ctx, long long rows, long long cols, const double* in, double* out) {
+  if (rows < 1 || cols < 1)
+    return fail(ctx, BCH_E_SHAPE, "softmax_f64: empty dimension (rows=%lld, cols=%lld)", rows, cols);
+  if (rows > 0x7fffffffLL) return fail(ctx, BCH_E_UNSUPPORTED, "softmax_f64: %lld rows > 2^31 - 1", rows);
+  if (!ctx) return fail(ctx, BCH_E_INVALID, "softmax_f64: ctx is NULL");
+  if (!in || !out) return fail(ctx, BCH_E_INVALID, "softmax_f64: NULL buffer");
+  bch_status st = use(ctx);
+  if (st != BCH_OK) return st;
+  return from_hip(ctx, bch::launch_softmax_rows_f64(ctx->stream, rows, cols, in, out), "softmax_f64 launch");
 }
 
 bch_status bch_elementwise(bch_ctx* ctx, int op, long long n, const float* a, const float* b, const float* c,
@@ -719,6 +735,11 @@ void bch_event_destroy(bch_event* ev) {
 }
 
 const char* bch_sgemm_kernel_name(int m, int n, int k) { return bch::sgemm_kernel_name(m, n, k); }
+
+const char* bch_softmax_rows_f64_kernel_name(long long rows, long long cols, const double* in, const double* out) {
+  return bch::softmax_f64_kernel_name(
+      rows, cols, ((reinterpret_cast<uintptr_t>(in) | reinterpret_cast<uintptr_t>(out)) & 15) == 0);
+}
 
 const char* bch_layer_norm_kernel_name(long long rows, long long cols) {
   return bch::layer_norm_kernel_name(rows, cols);

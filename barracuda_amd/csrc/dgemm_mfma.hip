@@ -34,12 +34,22 @@
 //     4096^3 against loading one tile ahead and reading all fragments at the
 //     top of the tile: 59.7 -> 63.4 TFLOP/s.
 //   * Workgroup -> tile mapping is XCD-aware and grouped, as in the f32 GEMM.
+//   * Split k: when the output has fewer 128 x 128 tiles than the device has
+//     CUs (a skinny m or n, e.g. the P V product of an attention), the k
+//     range is cut into nsplit contiguous runs of whole 16-wide k-tiles
+//     (at least 8 k-tiles each); grid.y = batch x nsplit.  Each workgroup
+//     writes its raw accumulators to a partial [batch][nsplit][m][n] in the
+//     context's workspace, and dgemm_split_reduce adds the nsplit partials of
+//     each element in split order (deterministic), then applies alpha and
+//     beta C.
 //   * CHECK=false needs m % 128 == 0, n % 128 == 0, k % 16 == 0, even
 //     leading dimensions and batch strides, 16-byte aligned A and B; CHECK
 //     guards every load (zero fill) and store.
 #include "bch_internal.h"
 
 #include <stdint.h>
+
+#include <algorithm>
 
 namespace {
 
@@ -116,11 +126,14 @@ __device__ __forceinline__ void store_dtile(double* __restrict__ s, int tid, con
 
 // BM x BN block tile (2 x 2 waves of (BM/2) x (BN/2), TM x TN MFMA blocks each);
 // OCC workgroups per CU.
+// grid.y = batch * nsplit; with nsplit > 1 the workgroup covers k in
+// [split * ksplit, min(K, (split + 1) * ksplit)) and writes its raw sums to
+// P (dense [batch][nsplit][M][N]); alpha, beta and C are then unused.
 template <int BM, int BN, int OCC, bool TA, bool TB, bool CHECK>
 __global__ __launch_bounds__(kDT, OCC) void dgemm_mfma_kernel(
     int M, int N, int K, double alpha, const double* __restrict__ A, int lda, long long sA,
     const double* __restrict__ B, int ldb, long long sB, double beta, double* __restrict__ C, int ldc,
-    long long sC, int tiles_m, int tiles_n) {
+    long long sC, int tiles_m, int tiles_n, int nsplit, int ksplit, double* __restrict__ P) {
   constexpr int kDBM = BM, kDBN = BN, TM = BM / 32, TN = BN / 32;
   __shared__ double As[2][kDBM * kDLDK];
   __shared__ double Bs[2][kDBN * kDLDK];
@@ -138,7 +151,9 @@ __global__ __launch_bounds__(kDT, OCC) void dgemm_mfma_kernel(
   const int within = lt - g * group_size;
   const int m0 = (first_m + within % gm) * kDBM, n0 = (within / gm) * kDBN;
 
-  const long long bz = blockIdx.y;
+  const long long bz = blockIdx.y / nsplit;
+  const int split = blockIdx.y - (int)bz * nsplit;
+  const int kbeg = split * ksplit, kend = (int)min((long long)K, (long long)kbeg + ksplit);
   A += bz * sA;
   B += bz * sB;
   C += bz * sC;
@@ -162,8 +177,8 @@ __global__ __launch_bounds__(kDT, OCC) void dgemm_mfma_kernel(
   // barrier, phase 1 reads the first halves of tile t + 1 under the MFMAs of
   // steps 2, 3.  Tile indices past the end are clamped to the last tile
   // (reloaded, never used).  Scheduling groups pin the interleave.
-  const int nk = (K + kDBK - 1) / kDBK;
-  const int lastk = (nk - 1) * kDBK;
+  const int nk = (kend - kbeg + kDBK - 1) / kDBK;
+  const int lastk = kbeg + (nk - 1) * kDBK;
   d2 a[TM][2], b[TN][2];
   auto read_half = [&](int buf, int h) {
     const double* as = As[buf] + (wm + li) * kDLDK + 4 * lq + 2 * h;
@@ -192,12 +207,12 @@ __global__ __launch_bounds__(kDT, OCC) void dgemm_mfma_kernel(
   static_assert(NM >= 2 * NR, "half tile too small to cover its reads");
 
   if (nk > 0) {
-    load_dtile<BM, !TA, CHECK>(A, lda, M, K, m0, 0, tid, ra);
-    load_dtile<BN, TB, CHECK>(B, ldb, N, K, n0, 0, tid, rb);
+    load_dtile<BM, !TA, CHECK>(A, lda, M, kend, m0, kbeg, tid, ra);
+    load_dtile<BN, TB, CHECK>(B, ldb, N, kend, n0, kbeg, tid, rb);
     store_dtile<BM, !TA>(As[0], tid, ra);
     store_dtile<BN, TB>(Bs[0], tid, rb);
-    load_dtile<BM, !TA, CHECK>(A, lda, M, K, m0, min(kDBK, lastk), tid, ra);
-    load_dtile<BN, TB, CHECK>(B, ldb, N, K, n0, min(kDBK, lastk), tid, rb);
+    load_dtile<BM, !TA, CHECK>(A, lda, M, kend, m0, min(kbeg + kDBK, lastk), tid, ra);
+    load_dtile<BN, TB, CHECK>(B, ldb, N, kend, n0, min(kbeg + kDBK, lastk), tid, rb);
   }
   __syncthreads();
   if (nk > 0) read_half(0, 0);
@@ -206,8 +221,8 @@ __global__ __launch_bounds__(kDT, OCC) void dgemm_mfma_kernel(
     const int cur = t & 1;
     store_dtile<BM, !TA>(As[cur ^ 1], tid, ra);
     store_dtile<BN, TB>(Bs[cur ^ 1], tid, rb);
-    load_dtile<BM, !TA, CHECK>(A, lda, M, K, m0, min((t + 2) * kDBK, lastk), tid, ra);
-    load_dtile<BN, TB, CHECK>(B, ldb, N, K, n0, min((t + 2) * kDBK, lastk), tid, rb);
+    load_dtile<BM, !TA, CHECK>(A, lda, M, kend, m0, min(kbeg + (t + 2) * kDBK, lastk), tid, ra);
+    load_dtile<BN, TB, CHECK>(B, ldb, N, kend, n0, min(kbeg + (t + 2) * kDBK, lastk), tid, rb);
     __builtin_amdgcn_sched_barrier(0);
     read_half(cur, 1);
     mfma_half(0);
@@ -231,6 +246,21 @@ __global__ __launch_bounds__(kDT, OCC) void dgemm_mfma_kernel(
   }
 
   // ---- epilogue: value r of lane (lq, li) is row lq + 4 r, col li of the block ----
+  if (nsplit > 1) {
+    double* part = P + (bz * nsplit + split) * (long long)M * N;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int col = n0 + wn + 16 * j + li;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = m0 + wm + 16 * i + lq + 4 * r;
+          if (!CHECK || (row < M && col < N)) part[(long long)row * N + col] = acc[i][j][r];
+        }
+      }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
 #pragma unroll
@@ -249,14 +279,61 @@ __global__ __launch_bounds__(kDT, OCC) void dgemm_mfma_kernel(
   }
 }
 
+// C[b][row][col] = alpha * sum_{s < nsplit} P[b][s][row][col] (+ beta C when
+// beta != 0), the partials added in split order; one element per thread.
+__global__ __launch_bounds__(256) void dgemm_split_reduce(int M, int N, int nsplit, const double* __restrict__ P,
+                                                          double alpha, double beta, double* __restrict__ C, int ldc,
+                                                          long long sC, long long total) {
+  const long long e = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (e >= total) return;
+  const long long mn = (long long)M * N;
+  const long long b = e / mn, rc = e - b * mn;
+  const int row = (int)(rc / N), col = (int)(rc - (long long)row * N);
+  const double* p = P + b * nsplit * mn + rc;
+  double sum = 0.0;
+  for (int s = 0; s < nsplit; ++s) sum += p[s * mn];
+  double* c = C + b * sC + (long long)row * ldc + col;
+  const double v = alpha * sum;
+  *c = beta != 0.0 ? v + beta * *c : v;
+}
+
+struct SplitPlan {
+  int nsplit, ksplit;
+};
+
+// Split k only when the output has fewer tiles than the device has CUs, into
+// runs of at least 8 k-tiles, and never past grid.y's 65535.
+SplitPlan split_plan(int batch, int m, int n, int k, int BM, int BN) {
+  const long long tiles = (long long)((m + BM - 1) / BM) * ((n + BN - 1) / BN) * batch;
+  const int nk = (k + kDBK - 1) / kDBK;
+  const long long cus = bch::device_cu_count();
+  long long want = tiles >= cus ? 1 : (cus + tiles - 1) / tiles;
+  want = std::min<long long>(want, nk / 8);
+  want = std::min<long long>(want, 65535 / std::max(batch, 1));
+  if (want <= 1) return {1, nk * kDBK};
+  const int per = (int)((nk + want - 1) / want);  // k-tiles per split
+  return {(nk + per - 1) / per, per * kDBK};
+}
+
 template <int BM, int BN, int OCC, bool TA, bool TB, bool CHECK>
 hipError_t launch_d(hipStream_t s, int batch, int m, int n, int k, double alpha, const double* A, int lda,
                     long long sA, const double* B, int ldb, long long sB, double beta, double* C, int ldc,
-                    long long sC) {
+                    long long sC, void* ws, size_t ws_bytes) {
   const int tm = (m + BM - 1) / BM, tn = (n + BN - 1) / BN;
   if ((long long)tm * tn > 0x7fffffffLL || batch > 65535) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((dgemm_mfma_kernel<BM, BN, OCC, TA, TB, CHECK>), dim3(tm * tn, batch), dim3(kDT), 0, s, m, n, k,
-                     alpha, A, lda, sA, B, ldb, sB, beta, C, ldc, sC, tm, tn);
+  const SplitPlan sp = split_plan(batch, m, n, k, BM, BN);
+  const long long total = (long long)batch * m * n;
+  if (sp.nsplit > 1 && (!ws || ws_bytes < (size_t)total * sp.nsplit * sizeof(double))) return hipErrorInvalidValue;
+  double* P = sp.nsplit > 1 ? static_cast<double*>(ws) : nullptr;
+  hipLaunchKernelGGL((dgemm_mfma_kernel<BM, BN, OCC, TA, TB, CHECK>), dim3(tm * tn, batch * sp.nsplit), dim3(kDT), 0,
+                     s, m, n, k, alpha, A, lda, sA, B, ldb, sB, beta, C, ldc, sC, tm, tn, sp.nsplit,
+                     sp.nsplit > 1 ? sp.ksplit : (k > 0 ? k : 1), P);
+  if (sp.nsplit > 1) {
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(dgemm_split_reduce, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, m, n, sp.nsplit,
+                       P, alpha, beta, C, ldc, sC, total);
+  }
   return hipGetLastError();
 }
 
@@ -270,30 +347,45 @@ constexpr int kDTileM = BCH_DGEMM_TILE_M, kDTileN = BCH_DGEMM_TILE_N, kDOcc = BC
 template <bool TA, bool TB>
 hipError_t launch_ab(hipStream_t s, int batch, int m, int n, int k, double alpha, const double* A, int lda,
                      long long sA, const double* B, int ldb, long long sB, double beta, double* C, int ldc,
-                     long long sC) {
+                     long long sC, void* ws, size_t ws_bytes) {
   constexpr int BM = kDTileM, BN = kDTileN, OCC = kDOcc;
   const bool fast = m % BM == 0 && n % BN == 0 && k % kDBK == 0 && lda % 2 == 0 && ldb % 2 == 0 &&
                     sA % 2 == 0 && sB % 2 == 0 && (reinterpret_cast<uintptr_t>(A) & 15) == 0 &&
                     (reinterpret_cast<uintptr_t>(B) & 15) == 0;
   if (fast)
-    return launch_d<BM, BN, OCC, TA, TB, false>(s, batch, m, n, k, alpha, A, lda, sA, B, ldb, sB, beta, C, ldc, sC);
-  return launch_d<BM, BN, OCC, TA, TB, true>(s, batch, m, n, k, alpha, A, lda, sA, B, ldb, sB, beta, C, ldc, sC);
+    return launch_d<BM, BN, OCC, TA, TB, false>(s, batch, m, n, k, alpha, A, lda, sA, B, ldb, sB, beta, C, ldc, sC,
+                                                ws, ws_bytes);
+  return launch_d<BM, BN, OCC, TA, TB, true>(s, batch, m, n, k, alpha, A, lda, sA, B, ldb, sB, beta, C, ldc, sC,
+                                             ws, ws_bytes);
 }
 
 }  // namespace
 
 namespace bch {
 
+size_t dgemm_workspace_bytes(int batch, int m, int n, int k) {
+  if (batch <= 0 || m <= 0 || n <= 0) return 0;
+  const SplitPlan sp = split_plan(batch, m, n, k, kDTileM, kDTileN);
+  return sp.nsplit > 1 ? (size_t)batch * m * n * sp.nsplit * sizeof(double) : 0;
+}
+
+int dgemm_split_count(int batch, int m, int n, int k) {
+  if (batch <= 0 || m <= 0 || n <= 0) return 1;
+  return split_plan(batch, m, n, k, kDTileM, kDTileN).nsplit;
+}
+
 hipError_t launch_dgemm(hipStream_t s, bool transa, bool transb, int batch, int m, int n, int k, double alpha,
                         const double* A, int lda, long long sA, const double* B, int ldb, long long sB,
-                        double beta, double* C, int ldc, long long sC) {
+                        double beta, double* C, int ldc, long long sC, void* ws, size_t ws_bytes) {
   if (batch <= 0 || m <= 0 || n <= 0) return hipSuccess;
   if (transa) {
-    if (transb) return launch_ab<true, true>(s, batch, m, n, k, alpha, A, lda, sA, B, ldb, sB, beta, C, ldc, sC);
-    return launch_ab<true, false>(s, batch, m, n, k, alpha, A, lda, sA, B, ldb, sB, beta, C, ldc, sC);
+    if (transb)
+      return launch_ab<true, true>(s, batch, m, n, k, alpha, A, lda, sA, B, ldb, sB, beta, C, ldc, sC, ws, ws_bytes);
+    return launch_ab<true, false>(s, batch, m, n, k, alpha, A, lda, sA, B, ldb, sB, beta, C, ldc, sC, ws, ws_bytes);
   }
-  if (transb) return launch_ab<false, true>(s, batch, m, n, k, alpha, A, lda, sA, B, ldb, sB, beta, C, ldc, sC);
-  return launch_ab<false, false>(s, batch, m, n, k, alpha, A, lda, sA, B, ldb, sB, beta, C, ldc, sC);
+  if (transb)
+    return launch_ab<false, true>(s, batch, m, n, k, alpha, A, lda, sA, B, ldb, sB, beta, C, ldc, sC, ws, ws_bytes);
+  return launch_ab<false, false>(s, batch, m, n, k, alpha, A, lda, sA, B, ldb, sB, beta, C, ldc, sC, ws, ws_bytes);
 }
 
 }  // namespace bch

@@ -11,6 +11,9 @@ reference's control plane):
   tensor.batch.submit                 ipc/methods/batch.rs:58-283
   batch pre-validation                ipc/methods/batch.rs:287-350
   batch op helpers                    ipc/methods/batch.rs:352-537
+  tensor.matmul_inline                ipc/methods/tensor.rs:490-552
+  ml.attention                        ipc/methods/ml/forward.rs:80-165
+  extract_matrix                      ipc/methods/params.rs:21-30
   JSON-RPC error codes                ipc/jsonrpc.rs:51-59
   parse_shape                         ipc/methods/compute.rs:16-22
 
@@ -19,17 +22,21 @@ it and returns the same response object ({"jsonrpc", "result" | "error",
 "id"}), with the same validation order, error codes and message wording.
 The compute runs on the HIP path: tensor.matmul calls Tensor.matmul_ref
 (bch_sgemm) and tensor.batch.submit records and runs a TensorSession
-(bch_sgemm, bch_elementwise, bch_softmax_rows, bch_layer_norm).
+(bch_sgemm, bch_elementwise, bch_softmax_rows, bch_layer_norm).  The two
+inline-data handlers compute in f64, as the reference's do:
+tensor.matmul_inline on bch_dgemm, ml.attention on bch_dgemm (Q K^T, scaled)
+-> bch_softmax_rows_f64 -> bch_dgemm (P V).  Non-finite result values are
+written as null, as serde_json writes a non-finite f64.
 
 Deliberate difference: the reference keeps a CPU tensor store for headless
 hosts (CpuTensor, tensor.rs:97-114, 158-167).  This path has no CPU
 fallback: without a device, tensor.create answers INTERNAL_ERROR "No GPU
 device available", as tensor.batch.submit already does in the reference
 (batch.rs:95-97), and tensor.matmul finds no stored tensor ("Tensor not
-found", INVALID_PARAMS, the reference's answer for unknown ids).
-ml.attention (ml/forward.rs:83-165) and tensor.matmul_inline (tensor.rs:
-496-552) compute inline f64 data on the CPU in the reference; they are not
-routed here, since an f32 HIP route would change their precision.
+found", INVALID_PARAMS, the reference's answer for unknown ids).  The same
+holds for ml.attention and tensor.matmul_inline, which the reference computes
+on the host: their validation answers are unchanged, and a valid request
+without a device answers INTERNAL_ERROR "No GPU device available".
 """
 from __future__ import annotations
 
@@ -41,12 +48,13 @@ from typing import Any
 import numpy as np
 
 from .error import BarracudaError
+from .linalg import GemmF64, attention_f64
 from .session import SessionTensor, TensorSession
 from .tensor import HipDevice, Tensor
 
 __all__ = ["PARSE_ERROR", "INVALID_REQUEST", "METHOD_NOT_FOUND", "INVALID_PARAMS", "INTERNAL_ERROR",
            "PRIMAL_NAMESPACE", "TensorPrimal", "normalize_method", "dispatch", "tensor_create",
-           "tensor_matmul", "tensor_batch_submit", "ROUTED_METHODS"]
+           "tensor_matmul", "tensor_matmul_inline", "tensor_batch_submit", "ml_attention", "ROUTED_METHODS"]
 
 # ipc/jsonrpc.rs:51-59
 PARSE_ERROR = -32700
@@ -79,6 +87,22 @@ def _as_f64(v: Any):
     if isinstance(v, bool) or not isinstance(v, (int, float)):
         return None
     return float(v)
+
+
+def _json_num(x: float):
+    """serde_json's Value for an f64: a number, or null when not finite."""
+    x = float(x)
+    return x if np.isfinite(x) else None
+
+
+def _extract_matrix(params: dict, key: str):
+    """params.rs:21-30 extract_matrix: the array rows of params[key] (rows
+    that are not arrays are dropped), each row's numeric entries (others
+    dropped); None when params[key] is not an array."""
+    rows = params.get(key)
+    if not isinstance(rows, list):
+        return None
+    return [[x for x in (_as_f64(c) for c in row) if x is not None] for row in rows if isinstance(row, list)]
 
 
 def _parse_shape(arr: list) -> list[int]:
@@ -360,15 +384,86 @@ def tensor_batch_submit(primal: TensorPrimal, params: dict, id_: Any) -> dict:
             data = t.to_vec()
         except BarracudaError as e:
             return _error(id_, INTERNAL_ERROR, f"Readback of '{src}' failed: {e}")
-        outputs[rb_alias or src] = {"data": [float(x) for x in data], "shape": t.shape()}
+        outputs[rb_alias or src] = {"data": [_json_num(x) for x in data], "shape": t.shape()}
     return _success(id_, {"status": "completed", "outputs": outputs, "ops_executed": len(ops)})
 
 
-# method name -> handler (mod.rs:328-338, the tensor routes this path serves)
+# ---- inline-data f64 handlers -------------------------------------------------------------
+def tensor_matmul_inline(primal: TensorPrimal, params: dict, id_: Any) -> dict:
+    """tensor.rs:490-552: lhs [m x k] times rhs [k x n] sent inline, the
+    product returned inline (f64, on bch_dgemm)."""
+    lhs = _extract_matrix(params, "lhs") if isinstance(params, dict) else None
+    rhs = _extract_matrix(params, "rhs") if isinstance(params, dict) else None
+    if lhs is None or rhs is None:
+        return _error(id_, INVALID_PARAMS, "Missing required params: lhs and rhs (2D arrays)")
+    m = len(lhs)
+    if m == 0:
+        return _error(id_, INVALID_PARAMS, "lhs must be non-empty")
+    k = len(lhs[0])
+    if k == 0 or any(len(r) != k for r in lhs):
+        return _error(id_, INVALID_PARAMS, "lhs rows must have consistent length")
+    if not rhs:
+        return _error(id_, INVALID_PARAMS, "rhs must be non-empty")
+    n = len(rhs[0])
+    if len(rhs) != k or any(len(r) != n for r in rhs):
+        return _error(id_, INVALID_PARAMS, f"Shape mismatch: lhs is [{m}x{k}], rhs must be [{k}x{n}]")
+    dev = primal.device()
+    if dev is None:
+        return _error(id_, INTERNAL_ERROR, "No GPU device available")
+    if n == 0:
+        return _success(id_, {"result": [[] for _ in range(m)], "shape": [m, n]})
+    try:
+        c = GemmF64.execute(dev, np.asarray(lhs, dtype=np.float64), np.asarray(rhs, dtype=np.float64), m, k, n, 1)
+    except BarracudaError as e:
+        return _error(id_, INTERNAL_ERROR, f"Matmul failed: {e}")
+    result = [[_json_num(x) for x in row] for row in c.reshape(m, n)]
+    return _success(id_, {"result": result, "shape": [m, n]})
+
+
+def ml_attention(primal: TensorPrimal, params: dict, id_: Any) -> dict:
+    """ml/forward.rs:80-165: softmax(Q K^T / sqrt(d_k)) V on inline 2-D q, k,
+    v (f64: bch_dgemm, bch_softmax_rows_f64, bch_dgemm)."""
+    if not isinstance(params, dict):
+        params = {}
+    q = _extract_matrix(params, "q")
+    if q is None:
+        return _error(id_, INVALID_PARAMS, "Missing required param: q (2D array)")
+    k = _extract_matrix(params, "k")
+    if k is None:
+        return _error(id_, INVALID_PARAMS, "Missing required param: k (2D array)")
+    v = _extract_matrix(params, "v")
+    if v is None:
+        return _error(id_, INVALID_PARAMS, "Missing required param: v (2D array)")
+    if not q or not k or not v:
+        return _error(id_, INVALID_PARAMS, "q, k, v must be non-empty")
+    d_k = len(q[0])
+    if d_k == 0:
+        return _error(id_, INVALID_PARAMS, "Key dimension must be > 0")
+    seq_q, seq_k = len(q), len(k)
+    if any(len(r) != d_k for r in k) or any(len(r) != d_k for r in q):
+        return _error(id_, INVALID_PARAMS, "q and k must have matching inner dimension")
+    d_v = len(v[0])
+    if len(v) != seq_k or any(len(r) != d_v for r in v):
+        return _error(id_, INVALID_PARAMS, "v must have same sequence length as k with consistent column count")
+    dev = primal.device()
+    if dev is None:
+        return _error(id_, INTERNAL_ERROR, "No GPU device available")
+    try:
+        out = attention_f64(dev, np.asarray(q, dtype=np.float64), np.asarray(k, dtype=np.float64),
+                            np.asarray(v, dtype=np.float64).reshape(seq_k, d_v))
+    except BarracudaError as e:
+        return _error(id_, INTERNAL_ERROR, f"Attention failed: {e}")
+    return _success(id_, {"result": [[_json_num(x) for x in row] for row in out], "seq_q": seq_q,
+                          "seq_k": seq_k, "d_k": d_k, "d_v": d_v})
+
+
+# method name -> handler (mod.rs:315-338, the routes this path serves)
 ROUTED_METHODS = {
     "tensor.create": tensor_create,
     "tensor.matmul": tensor_matmul,
+    "tensor.matmul_inline": tensor_matmul_inline,
     "tensor.batch.submit": tensor_batch_submit,
+    "ml.attention": ml_attention,
 }
 
 

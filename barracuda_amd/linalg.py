@@ -1,10 +1,15 @@
-"""f64 dense matrix multiply over the FP64 matrix cores (bch_dgemm).
+"""f64 dense matrix multiply over the FP64 matrix cores (bch_dgemm), and the
+f64 attention of the ml.attention handler.
 
 Mirrors crates/barracuda/src/ops/linalg/gemm_f64.rs:
   GemmF64::{execute, execute_gemm, execute_gemm_ex}   gemm_f64.rs:77-249
   GemmCachedF64::{new, multiply, execute_to_buffer}   gemm_f64.rs:252-456
 Host slices in, host vectors out, as in the reference (execute_to_buffer
 returns the device buffer).  Same validation and messages.
+
+attention_f64 is the computation of crates/barracuda-core/src/ipc/methods/
+ml/forward.rs:121-150 (softmax(Q K^T / sqrt(d_k)) V in f64) on bch_dgemm and
+bch_softmax_rows_f64; softmax_rows_f64 is its row softmax alone.
 
 GemmCachedF64 in the reference dispatches (ceil(m/16), ceil(n/16)) workgroups
 to a shader that reads x as the column (n) index (gemm_f64.rs:424-427 vs
@@ -20,7 +25,7 @@ import numpy as np
 from .error import InvalidInput
 from .tensor import HipDevice, _Buffer, _check_i32
 
-__all__ = ["F64Buffer", "GemmCachedF64", "GemmF64"]
+__all__ = ["F64Buffer", "GemmCachedF64", "GemmF64", "attention_f64", "softmax_rows_f64"]
 
 
 class F64Buffer:
@@ -119,3 +124,45 @@ class GemmCachedF64:
         dc = F64Buffer(self.device, self.batch_size * m * self.n)
         _dgemm(self.device, da, self._b, dc, m, self.k, self.n, self.batch_size, 1.0, 0.0, False, False)
         return dc
+
+
+def _softmax_rows_f64(dev: HipDevice, x: F64Buffer, y: F64Buffer, rows: int, cols: int) -> None:
+    with dev._lock:
+        dev.check(dev._lib.bch_softmax_rows_f64(dev.ctx, rows, cols, C.c_void_p(x.ptr), C.c_void_p(y.ptr)),
+                  "softmax_f64")
+
+
+def softmax_rows_f64(device: HipDevice, x) -> np.ndarray:
+    """The row softmax of ml.attention (ml/forward.rs:130-140) over the last
+    axis of a float64 array: exp(x - max) / sum, the max skipping NaN."""
+    x = np.ascontiguousarray(np.asarray(x, dtype=np.float64))
+    if x.ndim == 0 or x.size == 0:
+        raise InvalidInput(f"softmax_rows_f64: empty input of shape {list(x.shape)}")
+    cols = x.shape[-1]
+    rows = x.size // cols
+    buf = F64Buffer(device, x.size).upload(x)
+    _softmax_rows_f64(device, buf, buf, rows, cols)
+    return buf.to_vec().reshape(x.shape)
+
+
+def attention_f64(device: HipDevice, q, k, v) -> np.ndarray:
+    """ml/forward.rs:121-150 on the device, for row-major q [seq_q, d_k],
+    k [seq_k, d_k], v [seq_k, d_v] (all non-empty, d_k >= 1):
+      scores = (Q K^T) * (1 / sqrt(d_k))     bch_dgemm, B transposed, alpha
+      P      = row softmax of scores         bch_softmax_rows_f64, in place
+      out    = P V                           bch_dgemm
+    Returns [seq_q, d_v] float64."""
+    q, k, v = (np.ascontiguousarray(np.asarray(a, dtype=np.float64)) for a in (q, k, v))
+    (sq, dk), (sk, dk2), (sk2, dv) = q.shape, k.shape, v.shape
+    if sq < 1 or sk < 1 or dk < 1 or dk2 != dk or sk2 != sk:
+        raise InvalidInput(f"attention_f64: q {list(q.shape)}, k {list(k.shape)}, v {list(v.shape)}")
+    if dv == 0:
+        return np.zeros((sq, 0), dtype=np.float64)
+    dq, dkb, dvb = (F64Buffer(device, a.size).upload(a) for a in (q, k, v))
+    scores = F64Buffer(device, sq * sk)
+    out = F64Buffer(device, sq * dv)
+    scale = 1.0 / float(np.sqrt(np.float64(dk)))
+    _dgemm(device, dq, dkb, scores, sq, dk, sk, 1, scale, 0.0, False, True)
+    _softmax_rows_f64(device, scores, scores, sq, sk)
+    _dgemm(device, scores, dvb, out, sq, sk, dv, 1, 1.0, 0.0, False, False)
+    return out.to_vec().reshape(sq, dv)

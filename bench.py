@@ -95,13 +95,15 @@ class Timer:
         if self.warmer is not None:
             self.warmer.run(self.warm_ms)
         for _ in range(warmup):
-            fn(0)
+            dev.check(fn(0) or 0, "bench warmup launch")
         dev.sync()
         t0 = time.perf_counter()
         dev.check(lib.bch_event_record(dev.ctx, self.e0), "event")
+        failed = 0
         for i in range(steps):
-            fn(i)
+            failed = failed or fn(i) or 0
         dev.check(lib.bch_event_record(dev.ctx, self.e1), "event")
+        dev.check(failed, "bench launch")
         dev.sync()
         t1 = time.perf_counter()
         ms = C.c_float()
@@ -146,7 +148,7 @@ def bench_gemm(dev, steps, warmup, warmer=None):
             "kernel": lib.bch_sgemm_kernel_name(n, n, n).decode()}, (a, b, c)
 
 
-WORKLOADS = ("softmax", "skinny", "batched", "sdpa", "linear", "dgemm", "norm", "copy")
+WORKLOADS = ("softmax", "skinny", "batched", "sdpa", "linear", "dgemm", "norm", "attn64", "copy")
 
 
 def bench_extra(dev, reps: int = 20, only=None, warmer=None):
@@ -181,6 +183,45 @@ def bench_extra(dev, reps: int = 20, only=None, warmer=None):
         out.update(_bench_dgemm(dev, T, reps))
     if "norm" in want:
         out.update(_bench_norm(dev, T, reps))
+    if "attn64" in want:
+        out.update(_bench_attn64(dev, T, reps))
+    return out
+
+
+def _bench_attn64(dev, T, reps):
+    """The f64 route of the ml.attention handler (ml/forward.rs:121-150):
+    its row softmax alone over [32768 x 2048] f64 (one read + one write,
+    16 B per element, HBM-bound), and the whole computation at seq_q = seq_k
+    = 2048, d_k = d_v = 128 (Q K^T and P V on bch_dgemm, the softmax between
+    them), operands resident in HBM."""
+    from barracuda_amd import F64Buffer
+    lib, ctx = dev._lib, dev.ctx
+    out = {}
+    rng = np.random.default_rng(5)
+    rows, cols = 32768, 2048
+    x = F64Buffer(dev, rows * cols).upload(rng.standard_normal(rows * cols) * 3.0)
+    y = F64Buffer(dev, rows * cols)
+    px, py = C.c_void_p(x.ptr), C.c_void_p(y.ptr)
+    nbytes = 2 * 8 * rows * cols
+    wall, ev = T.run(lambda i: lib.bch_softmax_rows_f64(ctx, rows, cols, px, py), reps, 3)
+    out["softmax_f64_32768x2048"] = {"GB/s": nbytes / (ev * 1e-3) / 1e9, "us": ev * 1e3, "bytes_per_launch": nbytes,
+                                     "hbm_frac": nbytes / (ev * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                                     "kernel": lib.bch_softmax_rows_f64_kernel_name(rows, cols, px, py).decode()}
+    del x, y
+    s, d = 2048, 128
+    q, k, v = (F64Buffer(dev, s * d).upload(rng.standard_normal(s * d)) for _ in range(3))
+    sc, o = F64Buffer(dev, s * s), F64Buffer(dev, s * d)
+    pq, pk, pv, ps, po = (C.c_void_p(t.ptr) for t in (q, k, v, sc, o))
+    scale = 1.0 / float(np.sqrt(d))
+
+    def step(i):
+        st = lib.bch_dgemm(ctx, 0, 1, 1, s, s, d, scale, pq, d, s * d, pk, d, s * d, 0.0, ps, s, s * s)
+        st = st or lib.bch_softmax_rows_f64(ctx, s, s, ps, ps)
+        return st or lib.bch_dgemm(ctx, 0, 0, 1, s, d, s, 1.0, ps, s, s * s, pv, d, s * d, 0.0, po, d, s * d)
+    wall, ev = T.run(step, reps, 3)
+    fl = 2.0 * 2 * s * s * d
+    out["ml_attention_f64_2048x2048x128"] = {"us": ev * 1e3, "TFLOP/s": fl / (ev * 1e-3) / 1e12,
+                                             "fp64_mfma_frac": fl / (ev * 1e-3) / 1e12 / FP64_MFMA_PEAK_TFLOPS}
     return out
 
 

@@ -189,6 +189,15 @@ bch_status bch_dgemm(bch_ctx *ctx, int transa, int transb, int batch, int m,
 bch_status bch_softmax_rows(bch_ctx *ctx, long long rows, long long cols,
                             const float *in, float *out);
 
+/* Row-wise f64 softmax: out[r,:] = exp(x - m_r) / sum_j exp(x_j - m_r), m_r
+ * the row maximum folded from -inf with f64::max (NaN entries skipped).
+ * rows, cols >= 1, rows <= 2^31 - 1; in == out is allowed.  Replaces the row
+ * softmax of the ml.attention handler (barracuda-core/src/ipc/methods/ml/
+ * forward.rs:130-140), the step between its two products (which run on
+ * bch_dgemm). */
+bch_status bch_softmax_rows_f64(bch_ctx *ctx, long long rows, long long cols,
+                                const double *in, double *out);
+
 /* Element-wise ops of TensorSession over n f32 elements:
  *   BCH_EW_ADD out = a + b      BCH_EW_SUB out = a - b     BCH_EW_MUL out = a * b
  *   BCH_EW_NEG out = -a         BCH_EW_FMA out = fma(a, b, c)
@@ -308,10 +317,14 @@ bch_status bch_event_record(bch_ctx *ctx, bch_event *ev);
 bch_status bch_event_elapsed_ms(bch_event *start, bch_event *stop, float *ms);
 void bch_event_destroy(bch_event *ev);
 
-/* Name of the kernel a bch_sgemm / bch_softmax_rows / bch_sdpa_fwd call of
- * this shape launches (for profilers and tests; NULL ctx allowed). */
+/* Name of the kernel a bch_sgemm / bch_layer_norm / bch_softmax_rows_f64
+ * call of this shape (and, for the f64 softmax, these buffers' alignment)
+ * launches, for profilers and tests. */
 const char *bch_sgemm_kernel_name(int m, int n, int k);
 const char *bch_layer_norm_kernel_name(long long rows, long long cols);
+const char *bch_softmax_rows_f64_kernel_name(long long rows, long long cols,
+                                             const double *in,
+                                             const double *out);
 
 #ifdef __cplusplus
 }

@@ -31,6 +31,13 @@
  *                        tolerances, exactness on integer-valued inputs, and
  *                        order-sensitivity probes that a transposed operand
  *                        or dropped term fails.
+ *   inline handlers   -- (section 5, f64 ml.attention and
+ *                        tensor.matmul_inline) the handler tests' vectors
+ *                        (ml_tests.rs:128-165, sprint56b_tests.rs:618-669),
+ *                        closed forms (one key -> its V row, equal scores ->
+ *                        the mean of V, the one-hot case), numpy longdouble
+ *                        brute force, and planted mistakes (no scale, V
+ *                        transposed, max not subtracted) that must fail.
  *
  * Build: oracle/Makefile (gcc -O2 -fopenmp -shared).  -ffp-contract=off so
  * that every fused multiply-add here is an explicit fma()/fmaf() call that
@@ -670,4 +677,84 @@ BCO_API void bco_layer_norm_f32(long rows, long cols, float eps,
         float sd = sqrtf(variance + eps);
         for (long i = 0; i < cols; ++i) yr[i] = (xr[i] - mean) / sd;
     }
+}
+
+/* ------------------------------------------------------------------------
+ * 5. Inline-data f64 handlers of the IPC wire paths (paths relative to
+ *    crates/barracuda-core/src/ipc/methods/ of the reference)
+ * ---------------------------------------------------------------------- */
+
+/* The row softmax of ml.attention (ml/forward.rs:130-140) on one row:
+ * max_val folded from -inf with f64::max (fmax: NaN entries skipped),
+ * val = exp(val - max_val) with the sum accumulated in order, then each
+ * value divided by the sum. */
+static void ml_softmax_row(long cols, double *row)
+{
+    double mx = -INFINITY;
+    for (long j = 0; j < cols; ++j) mx = fmax(mx, row[j]);
+    double sum = 0.0;
+    for (long j = 0; j < cols; ++j) {
+        row[j] = exp(row[j] - mx);
+        sum += row[j];
+    }
+    for (long j = 0; j < cols; ++j) row[j] /= sum;
+}
+
+BCO_API void bco_ml_softmax_rows_f64(long rows, long cols, const double *x,
+                                     double *y)
+{
+    #pragma omp parallel for schedule(static)
+    for (long r = 0; r < rows; ++r) {
+        double *yr = y + r * cols;
+        if (yr != x + r * cols) memcpy(yr, x + r * cols, (size_t)cols * sizeof(double));
+        ml_softmax_row(cols, yr);
+    }
+}
+
+/* ml.attention (ml/forward.rs:121-150) on row-major q [sq][dk], k [sk][dk],
+ * v [sk][dv] into out [sq][dv]:
+ *   scale = 1 / sqrt(dk)
+ *   score[i][j] = (sum over d, in order, of q[i][d] * k[j][d]) * scale
+ *                 (products rounded, then added: no fused multiply-add)
+ *   the row softmax above
+ *   out[i][c] = fma(w_ij, v[j][c], out[i][c]) over j in order, from 0. */
+BCO_API void bco_ml_attention_f64(int sq, int sk, int dk, int dv,
+                                  const double *q, const double *k,
+                                  const double *v, double *out)
+{
+    const double scale = 1.0 / sqrt((double)dk);
+    #pragma omp parallel for schedule(dynamic, 1)
+    for (int i = 0; i < sq; ++i) {
+        double *w = (double *)malloc((size_t)(sk > 0 ? sk : 1) * sizeof(double));
+        const double *qi = q + (long)i * dk;
+        for (int j = 0; j < sk; ++j) {
+            const double *kj = k + (long)j * dk;
+            double s = 0.0;
+            for (int d = 0; d < dk; ++d) s += qi[d] * kj[d];
+            w[j] = s * scale;
+        }
+        ml_softmax_row(sk, w);
+        double *oi = out + (long)i * dv;
+        for (int c = 0; c < dv; ++c) oi[c] = 0.0;
+        for (int j = 0; j < sk; ++j) {
+            const double *vj = v + (long)j * dv;
+            for (int c = 0; c < dv; ++c) oi[c] = fma(w[j], vj[c], oi[c]);
+        }
+        free(w);
+    }
+}
+
+/* tensor.matmul_inline (tensor.rs:540-548): lhs [m][k] times rhs [k][n],
+ * sum = fma(lhs[i][p], rhs[p][j], sum) over p in order, from 0. */
+BCO_API void bco_matmul_inline_f64(int m, int k, int n, const double *lhs,
+                                   const double *rhs, double *out)
+{
+    #pragma omp parallel for schedule(static)
+    for (int i = 0; i < m; ++i)
+        for (int j = 0; j < n; ++j) {
+            double sum = 0.0;
+            for (int p = 0; p < k; ++p)
+                sum = fma(lhs[(long)i * k + p], rhs[(long)p * n + j], sum);
+            out[(long)i * n + j] = sum;
+        }
 }

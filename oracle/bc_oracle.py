@@ -58,6 +58,9 @@ def lib() -> C.CDLL:
         L.bco_gelu_wgsl_f32.argtypes = [C.c_size_t, _fp, _fp]
         L.bco_layer_norm_f64.argtypes = [C.c_long, C.c_long, C.c_double, _fp, _dp]
         L.bco_layer_norm_f32.argtypes = [C.c_long, C.c_long, C.c_float, _fp, _fp]
+        L.bco_ml_softmax_rows_f64.argtypes = [C.c_long, C.c_long, _dp, _dp]
+        L.bco_ml_attention_f64.argtypes = [C.c_int] * 4 + [_dp, _dp, _dp, _dp]
+        L.bco_matmul_inline_f64.argtypes = [C.c_int] * 3 + [_dp, _dp, _dp]
         _lib = L
     return _lib
 
@@ -340,6 +343,38 @@ def layer_norm_f32(x, eps: float = 1e-5) -> np.ndarray:
     y = np.empty_like(x)
     lib().bco_layer_norm_f32(x.size // cols, cols, eps, _f(x), _f(y))
     return y
+
+
+# ---- inline-data f64 handlers (barracuda-core/src/ipc/methods/) --------------------
+def ml_softmax_rows_f64(x) -> np.ndarray:
+    """ml/forward.rs:130-140 on each row of a float64 matrix: f64::max fold
+    from -inf, exp(x - max), sequential sum, divide."""
+    x = np.ascontiguousarray(x, dtype=np.float64)
+    cols = x.shape[-1]
+    y = np.empty_like(x)
+    lib().bco_ml_softmax_rows_f64(x.size // cols, cols, _d(x), _d(y))
+    return y
+
+
+def ml_attention_f64(q, k, v) -> np.ndarray:
+    """ml/forward.rs:121-150: softmax(Q K^T / sqrt(d_k)) V in float64, the
+    handler's own operation order."""
+    q, k, v = (np.ascontiguousarray(a, dtype=np.float64) for a in (q, k, v))
+    (sq, dk), (sk, dv) = q.shape, v.shape
+    assert k.shape == (sk, dk)
+    out = np.empty((sq, dv), dtype=np.float64)
+    lib().bco_ml_attention_f64(sq, sk, dk, dv, _d(q), _d(k), _d(v), _d(out))
+    return out
+
+
+def matmul_inline_f64(lhs, rhs) -> np.ndarray:
+    """tensor.rs:540-548: sum = lhs[i][p].mul_add(rhs[p][j], sum) over p."""
+    lhs, rhs = (np.ascontiguousarray(a, dtype=np.float64) for a in (lhs, rhs))
+    (m, k), (k2, n) = lhs.shape, rhs.shape
+    assert k == k2
+    out = np.empty((m, n), dtype=np.float64)
+    lib().bco_matmul_inline_f64(m, k, n, _d(lhs), _d(rhs), _d(out))
+    return out
 
 
 # ---- metric (tolerances/mod.rs:44-54 scale) ---------------------------------------

@@ -209,6 +209,36 @@ def main() -> None:
                 "source": "crates/barracuda/src/ops/causal_attention.rs:85-122 (mask j <= i)"})
     g["attention"] = att
 
+    # ---- inline-data f64 handlers (tensor.matmul_inline, ml.attention): f64 throughout ----
+    inl = []
+    for name, lhs, rhs, src in (
+            ("matmul_inline_2x2", [[1.0, 2.0], [3.0, 4.0]], [[5.0, 6.0], [7.0, 8.0]],
+             "crates/barracuda-core/src/ipc/methods_coverage_tests/sprint56b_tests.rs:618-645"),
+            ("matmul_inline_non_square", [[1.0, 0.0, 2.0]], [[1.0], [0.0], [3.0]],
+             "crates/barracuda-core/src/ipc/methods_coverage_tests/sprint56b_tests.rs:647-669")):
+        m, k, n = len(lhs), len(rhs), len(rhs[0])
+        exp = [[float(sum(Fraction(lhs[i][p]) * Fraction(rhs[p][j]) for p in range(k))) for j in range(n)]
+               for i in range(m)]
+        inl.append({"name": name, "method": "tensor.matmul_inline", "params": {"lhs": lhs, "rhs": rhs},
+                    "expected": exp, "shape": [m, n], "tol": 0.0, "source": src})
+    # one key: its weight is exp(0) / exp(0) = 1 exactly, so the output is that V row exactly
+    inl.append({"name": "ml_attention_single_token", "method": "ml.attention",
+                "params": {"q": [[1.0, 0.0]], "k": [[1.0, 0.0]], "v": [[42.0, 7.0]]},
+                "expected": [[42.0, 7.0]], "tol": 0.0,
+                "source": "crates/barracuda-core/src/ipc/methods_coverage_tests/ml_tests.rs:147-165"})
+    # one-hot q and k: scores [[a, 0], [0, a]] with a = 1/sqrt(2); row i = softmax(scores_i) V
+    a = 1.0 / math.sqrt(2.0)
+    vv = [[10.0, 20.0], [30.0, 40.0]]
+    exp = []
+    for i in range(2):
+        p = softmax64([a if j == i else 0.0 for j in range(2)])
+        exp.append([p[0] * vv[0][d] + p[1] * vv[1][d] for d in range(2)])
+    inl.append({"name": "ml_attention_one_hot", "method": "ml.attention",
+                "params": {"q": [[1.0, 0.0], [0.0, 1.0]], "k": [[1.0, 0.0], [0.0, 1.0]], "v": vv},
+                "expected": exp, "tol": 1e-14,
+                "source": "crates/barracuda-core/src/ipc/methods_coverage_tests/ml_tests.rs:128-145"})
+    g["inline_f64"] = inl
+
     OUT.write_text(json.dumps(g, indent=1))
     print(f"wrote {OUT}")
 

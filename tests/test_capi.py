@@ -252,6 +252,21 @@ def test_sgemm_noalloc_validation_before_device():
     assert "ctx" in N.last_error(None)
 
 
+def test_softmax_f64_validation_and_routing_before_device():
+    lib = N.load()
+    nul = None
+    assert lib.bch_softmax_rows_f64(nul, 0, 4, nul, nul) == N.BCH_E_SHAPE
+    assert lib.bch_softmax_rows_f64(nul, 4, 0, nul, nul) == N.BCH_E_SHAPE
+    assert lib.bch_softmax_rows_f64(nul, 1 << 31, 4, nul, nul) == N.BCH_E_UNSUPPORTED
+    assert lib.bch_softmax_rows_f64(nul, 4, 4, nul, nul) == N.BCH_E_INVALID
+    name = lambda r, c, p: lib.bch_softmax_rows_f64_kernel_name(r, c, C.c_void_p(p), C.c_void_p(p))
+    assert name(65536, 2048, 0x1000) == b"softmax_f64_rows<4,2,4>"
+    assert name(65536, 2048, 0x1008) == b"softmax_f64_rows<8,1,4>"
+    assert name(3, 5, 0x1000) == b"softmax_f64_rows<1,1,1>"
+    assert name(3, 129, 0x1000) == b"softmax_f64_rows<4,1,1>"
+    assert name(3, 2049, 0x1000) == b"softmax_f64_block"
+
+
 def test_elementwise_and_layer_norm_validation_before_device():
     lib = N.load()
     nul = C.c_void_p()

@@ -115,3 +115,39 @@ def test_dgemm_empty_k_batched(dev, ta, tb):
     _say(f"dgemm batch=3 m=4 k=0 n=5 ta={ta} tb={tb}")
     got = GemmF64.execute_gemm_ex(dev, [], [], 4, 0, 5, 3, 1.0, 0.5, ta, tb)
     assert got.shape == (60,) and not np.any(got)
+
+
+@pytest.mark.parametrize("batch,m,k,n", [(1, 2048, 2048, 128), (1, 128, 4096, 64), (3, 100, 1000, 37),
+                                         (1, 64, 8192, 64), (2, 256, 2064, 256), (1, 1, 5000, 1)])
+@pytest.mark.parametrize("ta,tb", [(False, False), (True, True)])
+def test_dgemm_split_k_vs_longdouble(dev, batch, m, k, n, ta, tb):
+    """Outputs with fewer 128 x 128 tiles than CUs and long k: the k range is
+    split, the partials added in split order by a second kernel."""
+    _say(f"dgemm split-k batch={batch} m={m} k={k} n={n} ta={ta} tb={tb}")
+    rng = O.Lcg(batch * 11 + m + 3 * k + 7 * n + ta)
+    a = rng.uniform((batch * m * k,)).astype(np.float64)
+    b = rng.uniform((batch * k * n,)).astype(np.float64)
+    got = GemmF64.execute_gemm_ex(dev, a, b, m, k, n, batch, 1.0, 0.0, ta, tb)
+    assert _rel(got, O.gemm_longdouble(a, b, m, k, n, batch, ta, tb)) <= TOL
+    again = GemmF64.execute_gemm_ex(dev, a, b, m, k, n, batch, 1.0, 0.0, ta, tb)
+    assert np.array_equal(got, again)  # fixed summation order
+
+
+def test_dgemm_split_k_alpha_beta_and_integers(dev):
+    _say("dgemm split-k alpha/beta and integers")
+    m, k, n = 128, 4096, 128
+    rng = np.random.default_rng(8)
+    a = rng.integers(-32, 33, m * k).astype(np.float64)
+    b = rng.integers(-32, 33, k * n).astype(np.float64)
+    want = (a.astype(np.int64).reshape(m, k) @ b.astype(np.int64).reshape(k, n)).reshape(-1)
+    assert np.array_equal(GemmF64.execute(dev, a, b, m, k, n, 1), want.astype(np.float64))
+    cin = rng.uniform(-1, 1, m * n)
+    lib = dev._lib
+    for alpha, beta, c0 in ((0.5, -2.0, cin), (3.0, 0.0, np.full(m * n, np.nan))):
+        da, db = F64Buffer(dev, a.size).upload(a), F64Buffer(dev, b.size).upload(b)
+        dc = F64Buffer(dev, m * n).upload(c0)
+        with dev._lock:
+            dev.check(lib.bch_dgemm(dev.ctx, 0, 0, 1, m, n, k, alpha, C.c_void_p(da.ptr), k, m * k,
+                                    C.c_void_p(db.ptr), n, k * n, beta, C.c_void_p(dc.ptr), n, m * n), "dgemm")
+        ref = alpha * want.astype(np.float64) + (beta * c0 if beta != 0.0 else 0.0)
+        assert _rel(dc.to_vec(), ref) <= TOL

@@ -81,6 +81,45 @@ def test_tensor_matmul_error_vectors(headless):
     assert e["code"] == ipc.INTERNAL_ERROR and e["message"] == "No GPU device available"
 
 
+def test_inline_handler_error_vectors(headless):
+    """ml_tests.rs:84-126 and sprint56b_tests.rs:585-615, plus every other
+    validation answer of ml/forward.rs:83-117 and tensor.rs:496-537; a valid
+    request without a device is INTERNAL_ERROR."""
+    att = lambda params, i: ipc.dispatch(headless, "ml.attention", params, i)
+    for i, (params, msg) in enumerate((
+            ({"k": [[1.0]], "v": [[1.0]]}, "Missing required param: q (2D array)"),
+            ({"q": [[1.0]], "v": [[1.0]]}, "Missing required param: k (2D array)"),
+            ({"q": [[1.0]], "k": [[1.0]]}, "Missing required param: v (2D array)"),
+            ({"q": [], "k": [[1.0]], "v": [[1.0]]}, "q, k, v must be non-empty"),
+            ({"q": [[]], "k": [[1.0]], "v": [[1.0]]}, "Key dimension must be > 0"),
+            ({"q": [[1.0, 2.0]], "k": [[1.0]], "v": [[1.0]]}, "q and k must have matching inner dimension"),
+            ({"q": [[1.0], [1.0, 2.0]], "k": [[1.0]], "v": [[1.0]]}, "q and k must have matching inner dimension"),
+            ({"q": [[1.0]], "k": [[1.0], [2.0]], "v": [[1.0]]},
+             "v must have same sequence length as k with consistent column count"),
+            ({"q": [[1.0]], "k": [[1.0], [2.0]], "v": [[1.0], [1.0, 2.0]]},
+             "v must have same sequence length as k with consistent column count"),
+            ({"q": "x", "k": [[1.0]], "v": [[1.0]]}, "Missing required param: q (2D array)"))):
+        e = _err(att(params, 310 + i))
+        assert e["code"] == ipc.INVALID_PARAMS and e["message"] == msg, (params, e)
+    # params.rs:21-30: rows that are not arrays and entries that are not numbers are dropped
+    e = _err(att({"q": [[1.0, "a", True, 2.0], "row"], "k": [[1.0, 2.0]], "v": [[3.0]]}, 330))
+    assert e["code"] == ipc.INTERNAL_ERROR and e["message"] == "No GPU device available"
+    mm = lambda params, i: ipc.dispatch(headless, "barracuda.tensor.matmul_inline", params, i)
+    for i, (params, msg) in enumerate((
+            ({}, "Missing required params: lhs and rhs (2D arrays)"),
+            ({"lhs": [[1.0]]}, "Missing required params: lhs and rhs (2D arrays)"),
+            ({"lhs": [], "rhs": [[1.0]]}, "lhs must be non-empty"),
+            ({"lhs": [[]], "rhs": [[1.0]]}, "lhs rows must have consistent length"),
+            ({"lhs": [[1.0], [1.0, 2.0]], "rhs": [[1.0]]}, "lhs rows must have consistent length"),
+            ({"lhs": [[1.0]], "rhs": []}, "rhs must be non-empty"),
+            ({"lhs": [[1.0, 2.0]], "rhs": [[1.0], [2.0], [3.0]]}, "Shape mismatch: lhs is [1x2], rhs must be [2x1]"),
+            ({"lhs": [[1.0, 2.0]], "rhs": [[1.0, 2.0], [3.0]]}, "Shape mismatch: lhs is [1x2], rhs must be [2x2]"))):
+        e = _err(mm(params, 200 + i))
+        assert e["code"] == ipc.INVALID_PARAMS and e["message"] == msg, (params, e)
+    e = _err(mm({"lhs": [[1.0, 2.0]], "rhs": [[1.0], [2.0]]}, 220))
+    assert e["code"] == ipc.INTERNAL_ERROR and e["message"] == "No GPU device available"
+
+
 # ---- GPU: the handlers on the HIP path ----------------------------------------------
 @pytest.fixture
 def primal(dev):
@@ -188,3 +227,55 @@ def test_batch_submit_every_op_against_oracle(primal):
         {"op": "create", "alias": "x", "shape": [2, 3]},
         {"op": "layer_norm", "alias": "y", "input": "x", "feature_size": 4}]}, 79)
     assert _err(bad)["message"] == "ops[1]: layer_norm failed: Invalid input: layer_norm: total 6 not divisible by feature_size 4"
+
+
+@pytest.mark.gpu
+def test_inline_f64_handlers_golden_on_gpu(primal, golden):
+    """sprint56b_tests.rs:618-669 and ml_tests.rs:128-165 through dispatch
+    (bch_dgemm; bch_dgemm + bch_softmax_rows_f64 + bch_dgemm)."""
+    print("ipc inline f64 handlers: reference vectors", flush=True)
+    for i, case in enumerate(golden["inline_f64"]):
+        r = ipc.dispatch(primal, case["method"], case["params"], 500 + i)
+        assert "result" in r, (case["name"], r)
+        got = np.array(r["result"]["result"], dtype=np.float64)
+        want = np.array(case["expected"])
+        assert got.shape == want.shape, case["name"]
+        assert np.max(np.abs(got - want)) <= case["tol"] * max(1.0, np.max(np.abs(want))), case["name"]
+        if case["method"] == "tensor.matmul_inline":
+            assert r["result"]["shape"] == case["shape"]
+        else:
+            q, k, v = (case["params"][x] for x in "qkv")
+            assert (r["result"]["seq_q"], r["result"]["seq_k"], r["result"]["d_k"], r["result"]["d_v"]) == \
+                (len(q), len(k), len(q[0]), len(v[0]))
+
+
+@pytest.mark.gpu
+def test_inline_f64_handlers_vs_oracle_on_gpu(primal):
+    """Seeded inline data against the f64 restatements of the handlers'
+    loops (ml/forward.rs:121-150, tensor.rs:540-548): max |x - ref| /
+    max(|ref|, 1) <= 1e-12 (f64 against f64; only the summation order
+    differs).  Includes one-row, one-key, d_v = 0 and 300-key cases."""
+    print("ipc inline f64 handlers vs oracle", flush=True)
+    rng = O.Lcg(31)
+    for sq, sk, dk, dv in ((1, 1, 1, 1), (5, 3, 4, 2), (37, 300, 24, 17), (64, 64, 64, 64), (3, 2049, 8, 5),
+                           (2, 7, 3, 0)):
+        q, k, v = (rng.normal(s).astype(np.float64) for s in ((sq, dk), (sk, dk), (sk, dv)))
+        params = {"q": q.tolist(), "k": k.tolist(), "v": v.tolist() if dv else [[] for _ in range(sk)]}
+        r = ipc.dispatch(primal, "ml.attention", params, 600)
+        assert "result" in r, r
+        got = np.array(r["result"]["result"], dtype=np.float64).reshape(sq, dv)
+        want = O.ml_attention_f64(q, k, v)
+        assert np.max(np.abs(got - want), initial=0.0) <= 1e-12 * max(1.0, np.max(np.abs(want), initial=0.0)), \
+            (sq, sk, dk, dv)
+    for m, k_, n in ((1, 1, 1), (7, 13, 5), (33, 100, 65), (128, 64, 3)):
+        a, b = rng.normal((m, k_)).astype(np.float64), rng.normal((k_, n)).astype(np.float64)
+        r = ipc.dispatch(primal, "tensor.matmul_inline", {"lhs": a.tolist(), "rhs": b.tolist()}, 700)
+        assert r["result"]["shape"] == [m, n]
+        got = np.array(r["result"]["result"], dtype=np.float64)
+        want = O.matmul_inline_f64(a, b)
+        assert np.max(np.abs(got - want)) <= 1e-12 * max(1.0, np.max(np.abs(want))), (m, k_, n)
+    r = ipc.dispatch(primal, "tensor.matmul_inline", {"lhs": [[1.0, 2.0]], "rhs": [[], []]}, 701)
+    assert r["result"] == {"result": [[]], "shape": [1, 0]}
+    # scores that overflow to inf: inf - inf in the softmax, NaN weights, null outputs (serde_json)
+    r = ipc.dispatch(primal, "ml.attention", {"q": [[1e200]], "k": [[1e200], [1.0]], "v": [[1.0], [2.0]]}, 702)
+    assert r["result"]["result"] == [[None]]

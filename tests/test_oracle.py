@@ -351,3 +351,98 @@ def test_layer_norm_oracle_closed_forms():
 def test_layer_norm_f32_restatement_tracks_f64():
     x = O.Lcg(13).normal((256, 2048), 0.0, 3.0)
     assert O.max_rel_err(O.layer_norm_f32(x), O.layer_norm_f64(x)) < 1e-5
+
+
+# ---------------------------------------------------------------- inline-data f64 handlers
+def _ml_attention_longdouble(q, k, v, scale=True, subtract_max=True, v_t=False):
+    """softmax(Q K^T / sqrt(d_k)) V in numpy longdouble, the mistakes below
+    switchable (they are planted here, never in the oracle)."""
+    q, k, v = (np.asarray(a, dtype=np.longdouble) for a in (q, k, v))
+    s = q @ k.T
+    if scale:
+        s = s / np.sqrt(np.longdouble(q.shape[1]))
+    if subtract_max:
+        s = s - s.max(axis=1, keepdims=True)
+    e = np.exp(s)
+    p = e / e.sum(axis=1, keepdims=True)
+    return p @ (v.T if v_t else v)
+
+
+def test_inline_f64_golden(golden):
+    """sprint56b_tests.rs:618-669 and ml_tests.rs:128-165 through the oracle."""
+    for case in golden["inline_f64"]:
+        p = case["params"]
+        if case["method"] == "tensor.matmul_inline":
+            got = O.matmul_inline_f64(np.array(p["lhs"]), np.array(p["rhs"]))
+        else:
+            got = O.ml_attention_f64(np.array(p["q"]), np.array(p["k"]), np.array(p["v"]))
+        want = np.array(case["expected"])
+        assert got.shape == want.shape, case["name"]
+        assert np.max(np.abs(got - want)) <= case["tol"] * max(1.0, np.max(np.abs(want))), case["name"]
+
+
+def test_ml_softmax_rows_f64_closed_forms():
+    y = O.ml_softmax_rows_f64(np.full((3, 8), 2.5))
+    assert np.array_equal(y, np.full((3, 8), 0.125))               # equal row: exactly 1/8
+    y = O.ml_softmax_rows_f64(np.array([[0.0, math.log(2.0)]]))
+    assert np.max(np.abs(y - [[1 / 3, 2 / 3]])) < 1e-16
+    x = O.Lcg(7).normal((5, 300)).astype(np.float64) * 30.0
+    y = O.ml_softmax_rows_f64(x)
+    assert np.all(np.abs(y.sum(axis=1) - 1.0) < 1e-14)
+    assert np.max(np.abs(O.ml_softmax_rows_f64(x + 1000.0) - y)) < 1e-14  # shift invariance
+    e = np.exp((x - x.max(axis=1, keepdims=True)).astype(np.longdouble))
+    assert np.max(np.abs(y - (e / e.sum(axis=1, keepdims=True)).astype(np.float64))) < 1e-15
+    # f64::max skips NaN, so the max is 2; exp(NaN - 2) poisons the sum: the row is NaN
+    y = O.ml_softmax_rows_f64(np.array([[np.nan, 1.0, 2.0], [1000.0, 1001.0, 999.0]]))
+    assert np.all(np.isnan(y[0]))
+    assert np.all(np.isfinite(y[1])) and abs(y[1].sum() - 1.0) < 1e-15
+    # a planted missing max subtraction overflows on that second row
+    with np.errstate(over="ignore", invalid="ignore"):
+        assert not np.all(np.isfinite(np.exp([1000.0, 1001.0]) / np.exp([1000.0, 1001.0]).sum()))
+
+
+def test_ml_attention_f64_closed_forms_and_brute_force():
+    # equal scores (q = 0): every row is the mean of the V rows
+    v = np.arange(21, dtype=np.float64).reshape(7, 3) * 0.5
+    out = O.ml_attention_f64(np.zeros((4, 5)), np.ones((7, 5)), v)
+    assert np.max(np.abs(out - v.mean(axis=0))) < 1e-14
+    rng = O.Lcg(11)
+    for sq, sk, dk, dv in ((1, 1, 1, 1), (3, 5, 4, 2), (17, 33, 8, 17), (9, 9, 16, 9), (2, 300, 3, 7)):
+        q, k, v = (rng.normal(s).astype(np.float64) for s in ((sq, dk), (sk, dk), (sk, dv)))
+        got = O.ml_attention_f64(q, k, v)
+        want = _ml_attention_longdouble(q, k, v).astype(np.float64)
+        assert np.max(np.abs(got - want)) <= 1e-13 * max(1.0, np.max(np.abs(want))), (sq, sk, dk, dv)
+
+
+def test_ml_attention_planted_mistakes_fail():
+    """A dropped scale, a transposed V and a missing max subtraction each
+    fail the brute-force comparison that the oracle passes."""
+    rng = O.Lcg(12)
+    q, k, v = (rng.normal((9, 9)).astype(np.float64) * 3.0 for _ in range(3))
+    good = O.ml_attention_f64(q, k, v)
+    tol = 1e-13 * max(1.0, np.max(np.abs(good)))
+    assert np.max(np.abs(good - _ml_attention_longdouble(q, k, v).astype(np.float64))) <= tol
+    assert np.max(np.abs(good - _ml_attention_longdouble(q, k, v, scale=False).astype(np.float64))) > 1e-3
+    assert np.max(np.abs(good - _ml_attention_longdouble(q, k, v, v_t=True).astype(np.float64))) > 1e-3
+    big = q * 300.0  # scores of a few thousand: exp overflows f64 without the max subtraction
+    with np.errstate(over="ignore", invalid="ignore"):
+        e = np.exp(big @ k.T / 3.0)
+        bad = (e / e.sum(axis=1, keepdims=True)) @ v
+    ok = O.ml_attention_f64(big, k, v)
+    assert np.all(np.isfinite(ok)) and not np.all(np.isfinite(bad))
+    assert np.max(np.abs(ok - _ml_attention_longdouble(big, k, v).astype(np.float64))) <= 1e-12 * np.max(np.abs(ok))
+
+
+def test_matmul_inline_f64_brute_force_and_planted_transpose():
+    rng = O.Lcg(13)
+    for m, k, n in ((1, 1, 1), (3, 7, 5), (16, 33, 9), (64, 64, 64)):
+        a, b = rng.normal((m, k)).astype(np.float64), rng.normal((k, n)).astype(np.float64)
+        got = O.matmul_inline_f64(a, b)
+        want = (a.astype(np.longdouble) @ b.astype(np.longdouble)).astype(np.float64)
+        assert np.max(np.abs(got - want)) <= 1e-14 * max(1.0, np.max(np.abs(want))), (m, k, n)
+    a, b = rng.normal((6, 6)).astype(np.float64), rng.normal((6, 6)).astype(np.float64)
+    assert np.max(np.abs(O.matmul_inline_f64(a, b) - a @ b.T)) > 1e-3
+    # integers: exact (fma chain of exact products and sums)
+    ai = np.array(rng.uniform((8, 8), -50, 50), dtype=np.float64).round()
+    bi = np.array(rng.uniform((8, 8), -50, 50), dtype=np.float64).round()
+    assert np.array_equal(O.matmul_inline_f64(ai, bi), ai @ bi)
