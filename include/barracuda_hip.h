@@ -79,9 +79,12 @@ bch_status bch_ctx_is_lost(const bch_ctx *ctx, int *lost);
  * the context's work against their own streams or capture it into a HIP
  * graph.  Capture only calls whose workspace already exists (make each call
  * once outside the capture first): a call that has to grow the workspace
- * allocates.  Every captured call replays correctly any number of times;
- * replays and eager calls on one context must not overlap (they share the
- * workspace). */
+ * allocates.  Growing it also frees the previous workspace, which graphs
+ * captured earlier still read: once a graph exists, make no call on the
+ * context that needs a larger workspace than its captured calls did (size
+ * the workspace with the largest call first).  Every captured call replays
+ * correctly any number of times; replays and eager calls on one context
+ * must not overlap (they share the workspace). */
 bch_status bch_ctx_stream(const bch_ctx *ctx, void **stream);
 
 /* Message of the last failed call on ctx; with ctx == NULL, the calling
