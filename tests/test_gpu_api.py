@@ -98,6 +98,20 @@ def test_device_copy(dev):
         x.view(np.uint8)[8 + 4 * 99990: 8 + 4 * 99990 + 3].tolist()
 
 
+def test_device_copy_runs_and_streaming_path(dev):
+    """16-byte copies: sizes that end inside a wave's run and the >= 64 MB
+    non-temporal path; the bytes after the copied range stay untouched."""
+    import ctypes as C
+    for n in (4, 4100, 4 * 1024 * 7 + 12, (64 << 20) // 4 + 4 * 333):
+        _say(f"bch_copy {4 * n} bytes")
+        x = O.Lcg(n).uniform(n)
+        src = Tensor.from_data(x, [n], dev)
+        dst = Tensor.from_data(np.full(n + 8, -7.0, np.float32), [n + 8], dev)
+        dev.check(dev._lib.bch_copy(dev.ctx, C.c_void_p(dst.ptr), C.c_void_p(src.ptr), 4 * n), "copy")
+        got = dst.to_vec()
+        assert np.array_equal(got[:n], x) and np.all(got[n:] == -7.0)
+
+
 def test_two_contexts_from_two_threads():
     """Two contexts on the device, driven from two threads at once: the
     per-device launch set-up (dynamic-LDS limits) is shared and locked, and
