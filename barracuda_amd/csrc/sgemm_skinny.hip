@@ -43,6 +43,7 @@
 
 #include <stdint.h>
 
+#include <algorithm>
 #include <atomic>
 
 
@@ -487,9 +488,10 @@ hipError_t launch_sk_reduce(hipStream_t s, int m, int n, const float* P, long lo
   return hipGetLastError();
 }
 
-// ---------------------------------------------------------------- transposed weights, 4 < m <= 32
+// ---------------------------------------------------------------- transposed weights, 8 < m <= 32
 // C[m][n] = sum_k A[m][k] W[n][k]: the linear layer with W [out, in]
-// (shaders/misc/linear_f64.wgsl) at decode sizes.  Stream-K over units of
+// (shaders/misc/linear_f64.wgsl) at decode sizes (and m <= 8 when N is too
+// narrow for the whole-row kernel below).  Stream-K over units of
 // R = 16 RB rows of W (output columns n) x KU = 8192 / R k -- 32 KB of W --
 // ordered row group by row group.  RB = 2 (32 x 256, every row one 1 KB
 // piece) for m <= 16; RB = 4 (64 x 128) for m > 16, which halves the bytes of
@@ -826,32 +828,48 @@ __global__ __launch_bounds__(512, 1) void sgemm_skinny_nt_ring(
   }
 }
 
-// ---------------------------------------------------------------- transposed weights, m <= 4, whole rows
+// ---------------------------------------------------------------- transposed weights, m <= 8, whole rows
 // C[m][n] = sum_k A[m][k] W[n][k] with every workgroup owning whole rows of W
 // (a contiguous run of output columns) over all of K: one launch, no split-k
-// partials, no reduce kernel.  Rows of W are contiguous, so workgroup g
-// streams rows [g N / G, (g + 1) N / G) as one contiguous block of memory.
-// Wave w of the workgroup takes rows w, w + 8, ... of the block; a row is
-// cut into chunks of 1024 k, four 1 KB row loads each (lane l holds
-// k = 256 j + 4 l .. + 3 of load j), streamed one chunk ahead.  A is staged
-// in LDS once ([MT][nk * 1024], zero past M and K), so the FMA operand of a
-// load is one ds_read_b128 per row of A.  Each lane keeps four
-// partial sums per row of A (one per float4 component); at the end of a row
-// they are added, summed over the wavefront (DPP all-reduce, fixed order),
-// and the epilogue (+ bias[n], activation) is applied before the store.  The row
-// count per wave differs by at most one across the workgroup.  EDGE: K is
-// not a multiple of 1024, so loads past K are clamped and zeroed.  Requires
-// K % 4 == 0, lda % 4 == 0, ldw % 4 == 0 and 16-byte aligned A and W.
-// Measured at K 4096, N 11008 (per call, M = 1 / 2 / 4 / 8): chunks of 2048
-// k two ahead 32.7 / 33.9 / 37.9 / 40.5 us, one ahead 30.2 / 32.0 / 33.2 /
-// 38.6 us; chunks of 1024 k one ahead 30.4 / 31.1 / 32.4 / 38.7 us (two or
-// three ahead slower); 4 or 16 waves per workgroup slower.  At M = 8 the LDS
-// reads of A (one 16-byte read per W float4 per row of A) and the FMAs make
-// it slower than the MFMA split-k kernel (35.8 us), so M = 5..8 stay there.
-constexpr int kRowK = 1024;                 // k per chunk
-constexpr int kRowLoads = kRowK / 256;      // 1 KB row loads per chunk
-constexpr int kRowPF = 1;                   // chunks in flight ahead of the FMAs
-constexpr int kRowWaves = 8;                // wavefronts per workgroup (one workgroup per CU)
+// partials in HBM, no reduce kernel.  Rows of W are contiguous, so workgroup
+// g streams rows [g N / G, (g + 1) N / G) as one contiguous block of memory.
+// K is taken in passes of 4096; in a pass wave w owns k = 4096 p + 512 w ..
+// + 511 of every row of the block, as two 1 KB loads per row (lane l holds
+// k = 4096 p + 512 w + 256 j + 4 l .. + 3 of load j), so the eight waves
+// read each row together, 16 KB contiguous, one row ahead of the FMAs.  The
+// A values a lane multiplies are the same for every row: they sit in
+// registers for the whole pass (MT x 8 floats), so a W float4 costs 4 MT
+// FMAs and nothing else.  At the end of a row each lane folds its float4 of
+// sums per row of A to one value; the 64 lane values of a (row, m) are summed
+// in batches of 64 / MT rows through a per-wave LDS transpose (row stride 65
+// floats, conflict-free both ways): each lane writes its MT values, then
+// lane i adds the 64 values of (row, m) number i in a fixed order, which
+// costs about two instructions per (row, m) against some twelve for a
+// wavefront all-reduce.  The eight waves' k-slices of a row meet in LDS
+// (part[row][wave][m], accumulated over the passes) and are added in wave
+// order after the last pass, then the epilogue (+ bias[n], activation) is
+// applied and C stored.  Results are deterministic.  EDGE: K is not a
+// multiple of 4096, so loads past K are clamped and zeroed (a wave whose
+// whole slice lies past K loads nothing).  Requires K % 4 == 0,
+// lda % 4 == 0, ldw % 4 == 0 and 16-byte aligned A and W; the host keeps
+// every block at or below kRowCap(MT) rows (more workgroups than CUs for a
+// very wide N).
+// Measured at K 4096, N 11008, per call (M = 1 / 2 / 4 / 5 / 8): 28.7 /
+// 28.8 / 29.7 / 31.0 / 31.4 us.  Splitting K four ways over two row sets
+// (A in 16 MT registers per lane): 29.3 / - / 30.6 / - / 32.3 us; two rows
+// ahead 29.2 / 29.6 / 30.2 / - / 31.9 us.  The kernel it replaced (A staged
+// in LDS, each wave streaming whole rows, one ds_read_b128 of A per W float4
+// and row of A) took 29.4 / 30.7 / 31.8 us at M = 1 / 2 / 4, and 38.7 us at
+// M = 8, where the LDS reads of A carried eight times the bytes of W.  At
+// M = 16 (16 FMAs per W element) this layout is VALU-bound: 40 us, so
+// m > 8 takes the ring kernel.
+constexpr int kRowWaves = 8;                               // wavefronts per workgroup (one workgroup per CU)
+constexpr int kRowPass = 4096;                             // k per pass
+constexpr int kRowNJ = kRowPass / 256 / kRowWaves;         // 1 KB loads per wave and row
+constexpr int kRowTS = 65;                                 // transpose row stride (floats)
+constexpr int kRowRed = kRowWaves * 64 * kRowTS;           // floats of the transpose buffers
+// rows per workgroup whose part[] fits next to the transpose buffers
+constexpr int kRowCap(int mt) { return (kLdsBytes / 4 - kRowRed) / (kRowWaves * mt); }
 
 template <int MT, bool EDGE>
 __global__ __launch_bounds__(64 * kRowWaves, 1) void sgemm_skinny_nt_rows(int M, int N, int K,
@@ -860,88 +878,108 @@ __global__ __launch_bounds__(64 * kRowWaves, 1) void sgemm_skinny_nt_rows(int M,
                                                                          float* __restrict__ C, int ldc,
                                                                          const float* __restrict__ bias,
                                                                          int act) {
+  constexpr int RB = 64 / MT;  // rows per transpose batch
   extern __shared__ float4 smem4[];
-  float* as = reinterpret_cast<float*>(smem4);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int nk = (K + kRowK - 1) / kRowK;
-  const int KP = nk * kRowK;  // staged row length
-  for (int e = tid; e < MT * (KP / 4); e += 64 * kRowWaves) {
-    const int m = e / (KP / 4), k = 4 * (e - m * (KP / 4));
-    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (m < M && k < K) v = *reinterpret_cast<const float4*>(A + (long long)m * lda + k);
-    *reinterpret_cast<float4*>(as + m * KP + k) = v;
-  }
-  __syncthreads();
-
+  float* red = reinterpret_cast<float*>(smem4) + wave * 64 * kRowTS;  // this wave's [64 values][kRowTS]
+  float* part = reinterpret_cast<float*>(smem4) + kRowRed;            // [rows][kRowWaves][MT]
   const int r0 = (int)((long long)blockIdx.x * N / gridDim.x);
   const int r1 = (int)((long long)(blockIdx.x + 1) * N / gridDim.x);
-  const int nrows = r1 - r0 > wave ? (r1 - r0 - wave + kRowWaves - 1) / kRowWaves : 0;
-  const int nu = nrows * nk;  // chunks of this wave, row-major
-  if (nu == 0) return;        // no barrier follows
-  constexpr int PF = kRowPF, NB = kRowPF + 1;
+  const int nr = r1 - r0;
+  const int npass = (K + kRowPass - 1) / kRowPass;
+  constexpr int PF = 1, NB = 2;
 
-  float4 wv[NB][kRowLoads];
-  int lrow = 0, lchunk = 0, lcount = 0;  // load cursor: advanced once per load, held at the last chunk
-  auto load = [&](int sb) {
-    const float* wr = W + (long long)(r0 + wave + kRowWaves * lrow) * ldw;
-#pragma unroll
-    for (int j = 0; j < kRowLoads; ++j) {
-      const int k = kRowK * lchunk + 256 * j + 4 * lane;
-      wv[sb][j] = bch::load_nt(reinterpret_cast<const float4*>(wr + (EDGE ? min(k, K - 4) : k)));
-      if (EDGE && k >= K) wv[sb][j] = make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-    ++lcount;
-    const int adv = lcount < nu ? 1 : 0;
-    lchunk += adv;
-    const int wrap = lchunk == nk ? 1 : 0;
-    lchunk -= wrap * nk;
-    lrow += wrap;
-  };
-#pragma unroll
-  for (int p = 0; p < PF; ++p) load(p);
-
-  float4 acc[MT];
-#pragma unroll
-  for (int m = 0; m < MT; ++m) acc[m] = make_float4(0.f, 0.f, 0.f, 0.f);
-  int crow = 0, cchunk = 0;
-  auto fma_chunk = [&](int sb) {
-#pragma unroll
-    for (int j = 0; j < kRowLoads; ++j) {
-      const int k = kRowK * cchunk + 256 * j + 4 * lane;
-      const float4 w = wv[sb][j];
-#pragma unroll
-      for (int m = 0; m < MT; ++m) {
-        const float4 a = *reinterpret_cast<const float4*>(as + m * KP + k);
-        acc[m].x = fmaf(a.x, w.x, acc[m].x);
-        acc[m].y = fmaf(a.y, w.y, acc[m].y);
-        acc[m].z = fmaf(a.z, w.z, acc[m].z);
-        acc[m].w = fmaf(a.w, w.w, acc[m].w);
-      }
-    }
-  };
-  auto finish_row = [&]() {
-    const int n = r0 + wave + kRowWaves * crow;
+  for (int pass = 0; pass < npass; ++pass) {
+    const int kw = kRowPass * pass + 256 * kRowNJ * wave;  // first k of this wave's slice
+    const bool live = !EDGE || kw < K;                      // wave-uniform: the slice reaches below K
+    const int kl = kw + 4 * lane;
+    float4 a[MT][kRowNJ];
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
-      const float v = bch::wave_allreduce((acc[m].x + acc[m].y) + (acc[m].z + acc[m].w), bch::OpSum());
-      if (m < M && lane == 0) C[(long long)m * ldc + n] = epilogue(v, bias, n, act);
-      acc[m] = make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-  };
-  for (int i = 0; i < nu; i += NB) {
+      const float* ar = A + (long long)min(m, M - 1) * lda;
 #pragma unroll
-    for (int p = 0; p < NB; ++p) {
-      load((p + PF) % NB);
-      if (i + p < nu) {
-        fma_chunk(p);
-        if (++cchunk == nk) {
-          finish_row();
-          cchunk = 0;
-          ++crow;
+      for (int j = 0; j < kRowNJ; ++j) {
+        const int k = kl + 256 * j;
+        float4 v = *reinterpret_cast<const float4*>(ar + (EDGE ? min(k, K - 4) : k));
+        if (m >= M || (EDGE && k >= K)) v = make_float4(0.f, 0.f, 0.f, 0.f);
+        a[m][j] = v;
+      }
+    }
+    float4 wv[NB][kRowNJ];
+    int lrow = 0;  // load cursor, held at the last row
+    auto load = [&](int sb) {
+      const float* wr = W + (long long)(r0 + lrow) * ldw;
+#pragma unroll
+      for (int j = 0; j < kRowNJ; ++j) {
+        const int k = kl + 256 * j;
+        if (live) {
+          wv[sb][j] = bch::load_nt(reinterpret_cast<const float4*>(wr + (EDGE ? min(k, K - 4) : k)));
+          if (EDGE && k >= K) wv[sb][j] = make_float4(0.f, 0.f, 0.f, 0.f);
+        } else {
+          wv[sb][j] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+      }
+      lrow += lrow + 1 < nr ? 1 : 0;
+    };
+    if (nr > 0) load(0);
+    for (int i = 0; i < nr; i += NB) {
+#pragma unroll
+      for (int p = 0; p < NB; ++p) {
+        load((p + PF) % NB);
+        __builtin_amdgcn_sched_barrier(0);  // the next row's loads stay ahead of this row's FMAs
+        const int row = i + p;
+        if (row < nr) {
+          float s[MT];
+#pragma unroll
+          for (int m = 0; m < MT; ++m) {
+            float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+            for (int j = 0; j < kRowNJ; ++j) {
+              acc.x = fmaf(a[m][j].x, wv[p][j].x, acc.x);
+              acc.y = fmaf(a[m][j].y, wv[p][j].y, acc.y);
+              acc.z = fmaf(a[m][j].z, wv[p][j].z, acc.z);
+              acc.w = fmaf(a[m][j].w, wv[p][j].w, acc.w);
+            }
+            s[m] = (acc.x + acc.y) + (acc.z + acc.w);
+          }
+          const int b = row % RB;
+#pragma unroll
+          for (int m = 0; m < MT; ++m) red[(b * MT + m) * kRowTS + lane] = s[m];
+          if (b == RB - 1 || row == nr - 1) {
+            // this wave's LDS writes are complete before any lane reads them, and the reads before
+            // the next batch overwrites them (one wave: no workgroup barrier)
+            __builtin_amdgcn_s_waitcnt(kLgkmZero);
+            __builtin_amdgcn_wave_barrier();
+            if (lane < (b + 1) * MT) {
+              const float* src = red + lane * kRowTS;
+              float t0 = 0.f, t1 = 0.f, t2 = 0.f, t3 = 0.f;
+#pragma unroll
+              for (int q = 0; q < 64; q += 4) {
+                t0 += src[q];
+                t1 += src[q + 1];
+                t2 += src[q + 2];
+                t3 += src[q + 3];
+              }
+              const float v = (t0 + t1) + (t2 + t3);
+              float* dst = part + ((row - b + lane / MT) * kRowWaves + wave) * MT + lane % MT;
+              *dst = pass == 0 ? v : *dst + v;
+            }
+            __builtin_amdgcn_s_waitcnt(kLgkmZero);
+            __builtin_amdgcn_wave_barrier();
+          }
         }
       }
     }
+  }
+  __syncthreads();
+  for (int e = tid; e < nr * M; e += 64 * kRowWaves) {
+    const int m = e / nr, row = e - m * nr;
+    const float* pr = part + row * kRowWaves * MT + m;
+    float v = 0.f;
+#pragma unroll
+    for (int w = 0; w < kRowWaves; ++w) v += pr[w * MT];
+    C[(long long)m * ldc + r0 + row] = epilogue(v, bias, r0 + row, act);
   }
 }
 
@@ -1060,27 +1098,29 @@ size_t nt_partial_bytes(const NtPlan& p, int m) {
 // one epoch per launch of the ring kernel, process-wide, never 0
 std::atomic<unsigned long long> g_nt_epoch{0};
 
-// Whole-row path for transposed weights: m <= 4, the staged A fits in LDS,
-// and every wave of every CU gets at least one row.
-int rows_mt(int m) { return m <= 1 ? 1 : m <= 2 ? 2 : 4; }
+// Whole-row path for transposed weights: m <= 8 and every wave of every CU
+// gets at least one row.
+int rows_mt(int m) { return m <= 1 ? 1 : m <= 2 ? 2 : m <= 4 ? 4 : 8; }
 
 bool use_rows(int m, int n, int k) {
-  if (m > 4) return false;
-  const long long kp = (long long)((k + kRowK - 1) / kRowK) * kRowK;
-  if ((long long)rows_mt(m) * kp * (long long)sizeof(float) > kLdsBytes) return false;
-  return n >= kRowWaves * cu_count();
+  (void)k;
+  return m <= 8 && n >= kRowWaves * cu_count();
 }
 
 template <int MT>
 hipError_t launch_rows(hipStream_t s, int m, int n, int k, const float* A, int lda, const float* W, int ldw, float* C,
                        int ldc, const float* bias, int act) {
-  const bool edge = k % kRowK != 0;
+  const bool edge = k % kRowPass != 0;
   const void* f = edge ? reinterpret_cast<const void*>(sgemm_skinny_nt_rows<MT, true>)
                        : reinterpret_cast<const void*>(sgemm_skinny_nt_rows<MT, false>);
   hipError_t e = bch::ensure_dynamic_lds(f, kLdsBytes);
   if (e != hipSuccess) return e;
-  const int lds = (int)(sizeof(float) * MT * (size_t)((k + kRowK - 1) / kRowK) * kRowK);
-  const dim3 grid(cu_count()), block(64 * kRowWaves);
+  // one workgroup per CU, more when a block's rows would not fit in LDS
+  const int cap = kRowCap(MT);
+  const int g = std::max(cu_count(), (n + cap - 1) / cap);
+  const int rmax = (n + g - 1) / g;
+  const int lds = (int)(sizeof(float) * ((size_t)kRowRed + (size_t)rmax * kRowWaves * MT));
+  const dim3 grid(g), block(64 * kRowWaves);
   if (edge)
     hipLaunchKernelGGL((sgemm_skinny_nt_rows<MT, true>), grid, block, lds, s, m, n, k, A, lda, W, ldw, C, ldc, bias,
                        act);
@@ -1157,7 +1197,8 @@ hipError_t launch_sgemm_skinny_nt(hipStream_t s, int m, int n, int k, const floa
     const int mt = rows_mt(m);
     if (mt == 1) return launch_rows<1>(s, m, n, k, A, lda, W, ldw, C, ldc, bias, act);
     if (mt == 2) return launch_rows<2>(s, m, n, k, A, lda, W, ldw, C, ldc, bias, act);
-    return launch_rows<4>(s, m, n, k, A, lda, W, ldw, C, ldc, bias, act);
+    if (mt == 4) return launch_rows<4>(s, m, n, k, A, lda, W, ldw, C, ldc, bias, act);
+    return launch_rows<8>(s, m, n, k, A, lda, W, ldw, C, ldc, bias, act);
   }
   if (ws == nullptr || ws_bytes < sgemm_skinny_nt_workspace_bytes(m, n, k)) return hipErrorInvalidValue;
   const NtPlan p = nt_plan(m, n, k);

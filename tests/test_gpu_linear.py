@@ -155,12 +155,15 @@ def test_sgemm_ex_transposed_split_groups_exact_on_integers(dev):
 
 
 @pytest.mark.parametrize("m,n,k", [(1, 2048, 4096), (2, 2053, 2052), (3, 5000, 1024), (4, 4100, 6144),
-                                   (4, 2304, 4100), (1, 3000, 44000), (6, 3000, 2048)])
+                                   (4, 2304, 4100), (1, 3000, 44000), (6, 3000, 2048), (8, 11008, 4096),
+                                   (5, 2053, 8196), (7, 4100, 100), (8, 40000, 512)])
 def test_sgemm_ex_transposed_whole_rows(dev, m, n, k):
-    """m <= 4, n >= 8 waves x CUs: each workgroup owns whole weight rows (one launch, no partials).
-    Covers every row-block width (m = 1, 2, 3-4), rows per workgroup not a multiple of the wave
-    count, K past a 1024 chunk boundary (4100, 2052), a staged A too large for LDS (m = 1,
-    k = 44000: 176 KB), which takes the split-k kernel, and m = 6 next to it (split-k)."""
+    """m <= 8, n >= 8 waves x CUs: each workgroup owns whole weight rows (one launch, no partials),
+    its eight waves splitting K in passes of 4096.  Covers every row-block width (m = 1, 2, 3-4,
+    5-8), rows per workgroup not a multiple of the transpose batch, K past a pass boundary (4100,
+    6144, 8196: two and three passes, the last partial), K = 44000 (eleven passes), K = 100 (one
+    live wave), and n = 40000 (more rows than one workgroup's LDS holds: more workgroups than
+    CUs)."""
     _say(f"sgemm_ex transposed whole rows m={m} n={n} k={k}")
     rng = O.Lcg(m * 101 + n + 3 * k)
     x = rng.normal((m, k))
@@ -175,7 +178,7 @@ def test_sgemm_ex_transposed_whole_rows(dev, m, n, k):
 def test_sgemm_ex_transposed_whole_rows_exact_on_integers(dev):
     _say("sgemm_ex transposed whole rows, integers")
     rng = np.random.default_rng(23)
-    for m, n, k in ((1, 2048, 96), (4, 2100, 2056), (2, 2048, 1024)):
+    for m, n, k in ((1, 2048, 96), (4, 2100, 2056), (2, 2048, 1024), (8, 2048, 4100), (6, 2100, 8192)):
         x = rng.integers(-8, 9, (m, k)).astype(np.float32)
         w = rng.integers(-8, 9, (n, k)).astype(np.float32)
         b = rng.integers(-100, 101, n).astype(np.float32)
