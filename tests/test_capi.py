@@ -29,6 +29,23 @@ def test_library_exports_every_header_symbol():
     assert set(syms) <= exported
 
 
+def test_rust_binding_in_integration_doc_matches_header():
+    """The barracuda-hip-sys block a maintainer would paste declares exactly the
+    header's functions and status codes."""
+    import re
+    from pathlib import Path
+    root = Path(__file__).resolve().parents[1]
+    doc = (root / "INTEGRATION.md").read_text()
+    block = re.search(r'extern "C" \{(.*?)\n\}', doc, re.S).group(1)
+    assert set(re.findall(r"pub fn (bch_[a-z0-9_]+)", block)) == set(N.header_symbols())
+    header = (root / "include" / "barracuda_hip.h").read_text()
+    codes = dict(re.findall(r"#define (BCH_(?:OK|E_[A-Z_]+))\s+(\d+)", header))
+    rust = dict(re.findall(r"pub const (BCH_(?:OK|E_[A-Z_]+)): bch_status = (\d+);", doc))
+    assert codes and rust == codes
+    for code in codes:  # every status has a row in the error-mapping table (BCH_OK excepted)
+        assert code == "BCH_OK" or f"| `{code}` |" in doc, code
+
+
 def test_library_carries_gfx950_code():
     # the fat binary embedded in our own build names its target
     assert b"amdgcn-amd-amdhsa--gfx950" in N.LIB_PATH.read_bytes()
