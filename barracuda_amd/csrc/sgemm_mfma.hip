@@ -92,7 +92,7 @@ __device__ __forceinline__ float4 ld4(const float* p) {
   return *reinterpret_cast<const float4*>(p);
 }
 
-template <int BM, int BN, int BK, bool CHECK, bool TB, bool EPI>
+template <int BM, int BN, int BK, bool CHECK, bool TB, bool EPI, bool V4 = false>
 __global__ __launch_bounds__(kThreads) void sgemm_mfma_kernel(
     int M, int N, int K, const float* __restrict__ A, int lda, long long sA,
     const float* __restrict__ B, int ldb, long long sB, float* __restrict__ C,
@@ -148,6 +148,45 @@ __global__ __launch_bounds__(kThreads) void sgemm_mfma_kernel(
   float4 ra[G::A_F4];
   float4 rb[G::B_BLK][4];  // TB: rb[q][e] is float4 number 4q + e of the [n][k] tile rows
 
+  // V4 (with CHECK): K, N, the leading dimensions and strides are multiples
+  // of 4, A and B 16-byte aligned, and each operand's extent below 2 GiB.  A
+  // float4 then lies wholly inside or wholly outside the matrix, and the
+  // guarded load is one range-checked buffer load: outside, its offset is
+  // set past the resource's end and the hardware returns zeros.  The guard
+  // acts on the address only, so nothing waits on the data before the LDS
+  // store a tile later (a select on the loaded value made every load's
+  // latency exposed: 4000^3 at 87 TFLOP/s against 97 for scalar guards).
+  constexpr unsigned kBad = 0x80000000u;  // an offset past every resource's end
+  // (unused, and removed, unless CHECK && V4)
+  const int a_bytes = (int)(((long long)(M - 1) * lda + K) * 4);
+  const int b_bytes = TB ? (int)(((long long)(N - 1) * ldb + K) * 4) : (int)(((long long)(K - 1) * ldb + N) * 4);
+  const __amdgpu_buffer_rsrc_t ra_rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(A), 0, a_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rb_rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(B), 0, b_bytes, 0x00020000);
+  unsigned aoff[G::A_F4], boff[TB ? 4 * G::B_BLK : G::B_BLK];
+  if constexpr (CHECK && V4) {
+#pragma unroll
+    for (int f = 0; f < G::A_F4; ++f) {
+      const int gr = m0 + a_r + f * A_RSTEP;
+      aoff[f] = gr < M ? (unsigned)gr * (unsigned)lda * 4u : kBad;  // row start, or kBad
+    }
+    if constexpr (TB) {
+#pragma unroll
+      for (int f = 0; f < 4 * G::B_BLK; ++f) {
+        const int gr = n0 + a_r + f * A_RSTEP;
+        boff[f] = gr < N ? (unsigned)gr * (unsigned)ldb * 4u : kBad;
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < G::B_BLK; ++q) {
+        const int gn = n0 + 4 * ((tid + q * kThreads) / B_KQ);
+        boff[q] = gn < N ? (unsigned)gn * 4u : kBad;  // column, or kBad
+      }
+    }
+  }
+  auto ld4_rs = [&](__amdgpu_buffer_rsrc_t rs, unsigned off) {
+    typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+    return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
+  };
   auto load_tile = [&](int k0) {
 #pragma unroll
     for (int f = 0; f < G::A_F4; ++f) {
@@ -155,6 +194,8 @@ __global__ __launch_bounds__(kThreads) void sgemm_mfma_kernel(
       const int gr = m0 + r, gc = k0 + a_c;
       if (!CHECK) {
         ra[f] = ld4(A + (long long)gr * lda + gc);
+      } else if (V4) {
+        ra[f] = ld4_rs(ra_rs, (aoff[f] != kBad && gc < K) ? aoff[f] + (unsigned)gc * 4u : kBad);
       } else {
         float t[4];
 #pragma unroll
@@ -171,6 +212,8 @@ __global__ __launch_bounds__(kThreads) void sgemm_mfma_kernel(
         const int gr = n0 + r, gc = k0 + a_c;
         if (!CHECK) {
           rb[f >> 2][f & 3] = ld4(B + (long long)gr * ldb + gc);
+        } else if (V4) {
+          rb[f >> 2][f & 3] = ld4_rs(rb_rs, (boff[f] != kBad && gc < K) ? boff[f] + (unsigned)gc * 4u : kBad);
         } else {
           float t[4];
 #pragma unroll
@@ -189,6 +232,8 @@ __global__ __launch_bounds__(kThreads) void sgemm_mfma_kernel(
           const int gk = k0 + 4 * kq + e, gn = n0 + 4 * nq;
           if (!CHECK) {
             rb[q][e] = ld4(B + (long long)gk * ldb + gn);
+          } else if (V4) {
+            rb[q][e] = ld4_rs(rb_rs, (boff[q] != kBad && gk < K) ? (unsigned)gk * (unsigned)ldb * 4u + boff[q] : kBad);
           } else {
             float t[4];
 #pragma unroll
@@ -365,7 +410,7 @@ __global__ __launch_bounds__(kThreads) void sgemm_mfma_kernel(
   }
 }
 
-template <int BM, int BN, int BK, bool CHECK, bool TB, bool EPI>
+template <int BM, int BN, int BK, bool CHECK, bool TB, bool EPI, bool V4 = false>
 hipError_t launch_tiles(hipStream_t s, int batch, int m, int n, int k,
                         const float* A, int lda, long long sA, const float* B,
                         int ldb, long long sB, float* C, int ldc, long long sC,
@@ -373,7 +418,7 @@ hipError_t launch_tiles(hipStream_t s, int batch, int m, int n, int k,
   using G = Cfg<BM, BN, BK>;
   const int tm = (m + BM - 1) / BM, tn = (n + BN - 1) / BN;
   const size_t lds = sizeof(float) * G::LDS_FLOATS;
-  auto kern = sgemm_mfma_kernel<BM, BN, BK, CHECK, TB, EPI>;
+  auto kern = sgemm_mfma_kernel<BM, BN, BK, CHECK, TB, EPI, V4>;
   hipError_t e = bch::ensure_dynamic_lds(reinterpret_cast<const void*>(kern), (int)lds);
   if (e != hipSuccess) return e;
   if (batch > 65535) return hipErrorInvalidValue;
@@ -386,19 +431,33 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 
 
 constexpr int kBK = 32;
 
-// Tile choice: the largest block tile that still gives every CU of the
-// device at least one tile.  Measured on MI355X (f32, TFLOP/s): 4096^3 -- 128x128 108,
-// 256x128 125, 256x256 132; 16 x 1024^3 -- 109 / 120 / 126; 2048^3 --
-// 113 / 62 / 33 (too few tiles for the larger shapes).
+// Tile choice: the tile with the least modelled time, rounds x tile area /
+// efficiency, where a round is one workgroup per CU (one 256x256 workgroup
+// fits a CU; the smaller tiles are timed at full rounds) and the efficiencies
+// are the tiles' measured rates at whole rounds relative to 256x256 (TFLOP/s
+// on MI355X: 256x256 145 at 4096^3, 256x128 140 at 8192 x 1024 x 8192,
+// 128x128 128 at 2048^3).  The largest tile that still fills every CU is
+// what this gives when the counts come out even; otherwise a part-filled last
+// round of large tiles can cost more than more rounds of smaller ones
+// (6144^3: three rounds of 256x256, 107 TFLOP/s).
 enum class Tile { k256x256, k256x128, k128x128 };
 
 Tile pick_tile(int batch, int m, int n) {
-  const int kNumCU = bch::device_cu_count();
-  const long long t256 = (long long)batch * ((m + 255) / 256) * ((n + 255) / 256);
-  if (t256 >= kNumCU) return Tile::k256x256;
-  const long long t256x128 = (long long)batch * ((m + 255) / 256) * ((n + 127) / 128);
-  if (t256x128 >= kNumCU) return Tile::k256x128;
-  return Tile::k128x128;
+  const long long cu = bch::device_cu_count();
+  struct Opt { Tile t; int bm, bn; double eff; };
+  const Opt opts[] = {{Tile::k256x256, 256, 256, 1.0}, {Tile::k256x128, 256, 128, 0.966},
+                      {Tile::k128x128, 128, 128, 0.883}};
+  Tile best = Tile::k256x256;
+  double best_cost = 0.0;
+  for (const Opt& o : opts) {
+    const long long tiles = (long long)batch * ((m + o.bm - 1) / o.bm) * ((n + o.bn - 1) / o.bn);
+    const double cost = (double)((tiles + cu - 1) / cu) * o.bm * o.bn / o.eff;
+    if (o.t == Tile::k256x256 || cost < best_cost * 0.999) {
+      best = o.t;
+      best_cost = cost;
+    }
+  }
+  return best;
 }
 
 int tile_m(Tile t) { return t == Tile::k128x128 ? 128 : 256; }
@@ -410,37 +469,53 @@ bool fast_ok(Tile t, int m, int n, int k, const float* A, int lda, long long sA,
          sA % 4 == 0 && sB % 4 == 0 && aligned16(A) && aligned16(B);
 }
 
-template <bool CHECK, bool TB, bool EPI>
+// Guarded loads as whole float4: K and N multiples of 4 (a float4 along k, or
+// along n for a [k][n] B, is then wholly inside or wholly outside), leading
+// dimensions and batch strides multiples of 4, A and B 16-byte aligned, and
+// each operand's extent (per batch) below 2 GiB for the 32-bit buffer offsets.
+bool vec4_ok(bool transb, int m, int n, int k, const float* A, int lda, long long sA, const float* B, int ldb,
+             long long sB) {
+  const long long a_bytes = ((long long)(m - 1) * lda + k) * 4;
+  const long long b_bytes = (transb ? (long long)(n - 1) * ldb + k : (long long)(k - 1) * ldb + n) * 4;
+  return k >= 4 && k % 4 == 0 && n % 4 == 0 && lda % 4 == 0 && ldb % 4 == 0 && sA % 4 == 0 && sB % 4 == 0 &&
+         aligned16(A) && aligned16(B) && a_bytes < (1LL << 31) && b_bytes < (1LL << 31);
+}
+
+template <bool CHECK, bool TB, bool EPI, bool V4>
 hipError_t launch_tile(Tile t, hipStream_t s, int batch, int m, int n, int k, const float* A, int lda,
                        long long sA, const float* B, int ldb, long long sB, float* C, int ldc, long long sC,
                        const float* bias, int act) {
   switch (t) {
     case Tile::k256x256:
-      return launch_tiles<256, 256, kBK, CHECK, TB, EPI>(s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC,
-                                                         bias, act);
+      return launch_tiles<256, 256, kBK, CHECK, TB, EPI, V4>(s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC,
+                                                             bias, act);
     case Tile::k256x128:
-      return launch_tiles<256, 128, kBK, CHECK, TB, EPI>(s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC,
-                                                         bias, act);
+      return launch_tiles<256, 128, kBK, CHECK, TB, EPI, V4>(s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC,
+                                                             bias, act);
     default:
-      return launch_tiles<128, 128, kBK, CHECK, TB, EPI>(s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC,
-                                                         bias, act);
+      return launch_tiles<128, 128, kBK, CHECK, TB, EPI, V4>(s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC,
+                                                             bias, act);
   }
 }
 
+// mode 0: unguarded; 1: guarded float4 loads; 2: guarded scalar loads
 template <bool TB, bool EPI>
-hipError_t launch_tile_any(bool fast, Tile t, hipStream_t s, int batch, int m, int n, int k, const float* A,
+hipError_t launch_tile_any(int mode, Tile t, hipStream_t s, int batch, int m, int n, int k, const float* A,
                            int lda, long long sA, const float* B, int ldb, long long sB, float* C, int ldc,
                            long long sC, const float* bias, int act) {
-  return fast ? launch_tile<false, TB, EPI>(t, s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC, bias, act)
-              : launch_tile<true, TB, EPI>(t, s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC, bias, act);
+  if (mode == 0)
+    return launch_tile<false, TB, EPI, false>(t, s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC, bias, act);
+  if (mode == 1)
+    return launch_tile<true, TB, EPI, true>(t, s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC, bias, act);
+  return launch_tile<true, TB, EPI, false>(t, s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC, bias, act);
 }
 
-const char* tile_name(Tile t, bool check) {
-  switch (t) {
-    case Tile::k256x256: return check ? "sgemm_mfma_kernel<256,256,32,true>" : "sgemm_mfma_kernel<256,256,32,false>";
-    case Tile::k256x128: return check ? "sgemm_mfma_kernel<256,128,32,true>" : "sgemm_mfma_kernel<256,128,32,false>";
-    default: return check ? "sgemm_mfma_kernel<128,128,32,true>" : "sgemm_mfma_kernel<128,128,32,false>";
-  }
+const char* tile_name(Tile t, int mode) {
+  static const char* const names[3][3] = {
+      {"sgemm_mfma_kernel<256,256,32,false>", "sgemm_mfma_kernel<256,256,32,true,v4>", "sgemm_mfma_kernel<256,256,32,true>"},
+      {"sgemm_mfma_kernel<256,128,32,false>", "sgemm_mfma_kernel<256,128,32,true,v4>", "sgemm_mfma_kernel<256,128,32,true>"},
+      {"sgemm_mfma_kernel<128,128,32,false>", "sgemm_mfma_kernel<128,128,32,true,v4>", "sgemm_mfma_kernel<128,128,32,true>"}};
+  return names[static_cast<int>(t)][mode];
 }
 
 }  // namespace
@@ -451,8 +526,10 @@ const char* sgemm_kernel_name(int m, int n, int k) {
   if (m <= 32 && sgemm_skinny_applies(m, n, k, nullptr, k, nullptr, n))
     return sgemm_skinny_kernel_name(m);
   const Tile t = pick_tile(1, m, n);
+  // with lda = k and ldb = n, and 16-byte aligned operands
   const bool check = !(m % tile_m(t) == 0 && n % tile_n(t) == 0 && k % kBK == 0 && k % 4 == 0 && n % 4 == 0);
-  return tile_name(t, check);
+  const bool v4 = k >= 4 && k % 4 == 0 && n % 4 == 0;
+  return tile_name(t, !check ? 0 : v4 ? 1 : 2);
 }
 
 size_t sgemm_workspace_bytes(int batch, int m, int n, int k) {
@@ -476,15 +553,18 @@ hipError_t launch_sgemm_ex(hipStream_t s, bool transb, int batch, int m, int n, 
   if (transb && batch == 1 && sgemm_skinny_nt_applies(m, n, k, A, lda, B, ldb))
     return launch_sgemm_skinny_nt(s, m, n, k, A, lda, B, ldb, C, ldc, ws, ws_bytes, bias, act);
   const Tile t = pick_tile(batch, m, n);
-  // the [n][k] tile loads need the same alignment as the [k][n] ones (ldb, sB multiples of 4)
-  const bool fast = fast_ok(t, m, n, k, A, lda, sA, B, ldb, sB);
+  // the [n][k] tile loads need the same alignment as the [k][n] ones (ldb, sB multiples of 4); a
+  // [n][k] B needs only K % 4 == 0 for whole float4, but N % 4 is kept for one rule
+  const int mode = fast_ok(t, m, n, k, A, lda, sA, B, ldb, sB) ? 0
+                   : vec4_ok(transb, m, n, k, A, lda, sA, B, ldb, sB) ? 1
+                                                                 : 2;
   const bool epi = bias != nullptr || act != 0;
   if (transb)
-    return epi ? launch_tile_any<true, true>(fast, t, s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC, bias, act)
-               : launch_tile_any<true, false>(fast, t, s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC, bias,
+    return epi ? launch_tile_any<true, true>(mode, t, s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC, bias, act)
+               : launch_tile_any<true, false>(mode, t, s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC, bias,
                                               act);
-  return epi ? launch_tile_any<false, true>(fast, t, s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC, bias, act)
-             : launch_tile_any<false, false>(fast, t, s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC, bias,
+  return epi ? launch_tile_any<false, true>(mode, t, s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC, bias, act)
+             : launch_tile_any<false, false>(mode, t, s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC, bias,
                                              act);
 }
 

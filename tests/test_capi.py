@@ -105,9 +105,12 @@ def test_null_and_shape_errors_before_device():
 def test_kernel_routing_names():
     lib = N.load()
     assert lib.bch_sgemm_kernel_name(4096, 4096, 4096) == b"sgemm_mfma_kernel<256,256,32,false>"
-    assert lib.bch_sgemm_kernel_name(3072, 3072, 512) == b"sgemm_mfma_kernel<256,128,32,false>"
+    assert lib.bch_sgemm_kernel_name(3072, 3072, 512) == b"sgemm_mfma_kernel<128,128,32,false>"
+    assert lib.bch_sgemm_kernel_name(8192, 1024, 512) == b"sgemm_mfma_kernel<256,128,32,false>"
+    assert lib.bch_sgemm_kernel_name(4096, 11008, 4096) == b"sgemm_mfma_kernel<256,256,32,false>"
     assert lib.bch_sgemm_kernel_name(2048, 2048, 2048) == b"sgemm_mfma_kernel<128,128,32,false>"
-    assert lib.bch_sgemm_kernel_name(4100, 4096, 300) == b"sgemm_mfma_kernel<256,256,32,true>"
+    assert lib.bch_sgemm_kernel_name(4100, 4096, 300) == b"sgemm_mfma_kernel<128,128,32,true,v4>"
+    assert lib.bch_sgemm_kernel_name(4000, 4000, 4000) == b"sgemm_mfma_kernel<256,256,32,true,v4>"
     assert lib.bch_sgemm_kernel_name(1, 11008, 4096) == b"sgemm_skinny_fma"
     assert lib.bch_sgemm_kernel_name(8, 11008, 4096) == b"sgemm_skinny_sk<1>"
     assert lib.bch_sgemm_kernel_name(16, 11008, 4096) == b"sgemm_skinny_sk<1>"

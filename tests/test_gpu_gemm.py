@@ -187,17 +187,34 @@ def test_leading_dimensions_and_unaligned(dev):
     assert O.max_rel_err(tc2.to_numpy(), ref) <= TOL
 
 
-@pytest.mark.parametrize("m,n,k", [(3072, 3072, 512), (4100, 4096, 300), (2048, 2048, 96), (4096, 3968, 64)])
-def test_large_tile_paths(dev, m, n, k):
-    """The 256x256 / 256x128 block tiles, aligned and ragged (sampled rows vs f64)."""
-    _say(f"sgemm large tiles m={m} n={n} k={k} ({dev._lib.bch_sgemm_kernel_name(m, n, k).decode()})")
+LARGE_TILE_CASES = [  # (m, n, k, the kernel the shape takes)
+    (4096, 4096, 256, "sgemm_mfma_kernel<256,256,32,false>"),
+    (4096, 3968, 64, "sgemm_mfma_kernel<256,256,32,true,v4>"),
+    (4095, 4096, 33, "sgemm_mfma_kernel<256,256,32,true>"),
+    (8192, 1024, 64, "sgemm_mfma_kernel<256,128,32,false>"),
+    (8192, 1020, 68, "sgemm_mfma_kernel<256,128,32,true,v4>"),
+    (8190, 1024, 62, "sgemm_mfma_kernel<256,128,32,true>"),
+    (3072, 3072, 512, "sgemm_mfma_kernel<128,128,32,false>"),
+    (4100, 4096, 300, "sgemm_mfma_kernel<128,128,32,true,v4>"),
+    (2000, 2000, 95, "sgemm_mfma_kernel<128,128,32,true>"),
+]
+
+
+@pytest.mark.parametrize("m,n,k,kernel", LARGE_TILE_CASES)
+def test_large_tile_paths(dev, m, n, k, kernel):
+    """Every block tile (256x256, 256x128, 128x128) with every load mode: unguarded (whole tiles,
+    aligned), guarded float4 loads (ragged M or N, K and N multiples of 4) and guarded scalar
+    loads (K or N not a multiple of 4).  Sampled rows and columns vs f64, rows and columns on
+    both sides of tile boundaries and the ragged edges."""
+    assert dev._lib.bch_sgemm_kernel_name(m, n, k).decode() == kernel
+    _say(f"sgemm large tiles m={m} n={n} k={k} ({kernel})")
     rng = O.Lcg(m + n + k)
     a = rng.uniform((m, k))
     b = rng.uniform((k, n))
     got = _mm(dev, a, b)
-    rows = [0, 1, 255, 256, m // 2, m - 2, m - 1]
+    rows = [0, 1, 127, 128, 255, 256, m // 2, m - 2, m - 1]
     assert O.max_rel_err(got[rows], O.matmul_f64(a, b, rows=rows)) <= TOL
-    cols = [0, 127, 128, 255, 256, n - 1]
+    cols = [0, 127, 128, 255, 256, n - 3, n - 1]
     assert O.max_rel_err(got[:, cols], a.astype(np.float64) @ b[:, cols].astype(np.float64)) <= TOL
 
 
