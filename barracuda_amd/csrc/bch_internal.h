@@ -118,6 +118,8 @@ hipError_t launch_sgemm(hipStream_t s, int batch, int m, int n, int k,
                         float* C, int ldc, long long sC, void* ws,
                         size_t ws_bytes);
 size_t sgemm_workspace_bytes(int batch, int m, int n, int k);
+// Scratch of launch_sgemm_ex (the skinny paths' partials, or split-K partials).
+size_t sgemm_ex_workspace_bytes(bool transb, int batch, int m, int n, int k, int lda, int ldb);
 const char* sgemm_kernel_name(int m, int n, int k);
 // With B given as [n][k] when transb (C = A B^T), and the linear layer's
 // epilogue C = act(acc + bias[col]): bias nullable, act kActNone / kActRelu /

@@ -370,11 +370,7 @@ bch_status bch_sgemm_ex(bch_ctx* ctx, int transb, int m, int n, int k, const flo
   if (!C || (k > 0 && (!A || !B))) return fail(ctx, BCH_E_INVALID, "linear: NULL buffer");
   bch_status st = use(ctx);
   if (st != BCH_OK) return st;
-  size_t wsb = 0;
-  if (!transb)
-    wsb = bch::sgemm_workspace_bytes(1, m, n, k);
-  else if (bch::sgemm_skinny_nt_applies(m, n, k, nullptr, lda, nullptr, ldb))
-    wsb = bch::sgemm_skinny_nt_workspace_bytes(m, n, k);
+  size_t wsb = bch::sgemm_ex_workspace_bytes(transb != 0, 1, m, n, k, lda, ldb);
   if (wsb) {
     st = ensure_ws(ctx, wsb);
     if (st != BCH_OK) return st;

@@ -218,6 +218,39 @@ def test_large_tile_paths(dev, m, n, k, kernel):
     assert O.max_rel_err(got[:, cols], a.astype(np.float64) @ b[:, cols].astype(np.float64)) <= TOL
 
 
+SPLIT_K_CASES = [(1024, 1024, 1024), (512, 512, 8192), (128, 11008, 4096), (300, 4, 4096), (64, 4096, 4096),
+                 (200, 1000, 2048)]
+
+
+@pytest.mark.parametrize("m,n,k", SPLIT_K_CASES)
+def test_split_k_vs_f64(dev, m, n, k):
+    """Tiles filling at most half the CUs: K is cut into slices of whole k-tiles, the slices run
+    as one batched launch into the workspace and sgemm_splitk_reduce adds them in slice order.
+    Aligned and ragged (m 300, n 4 and 1000: the float4-guarded tiles), full f64 comparison on
+    sampled rows and every column; repeated calls are bit-identical."""
+    name = dev._lib.bch_sgemm_kernel_name(m, n, k).decode()
+    assert name.endswith("+sgemm_splitk_reduce"), name
+    _say(f"sgemm split-k m={m} n={n} k={k} ({name})")
+    rng = O.Lcg(m * 3 + n + k)
+    a = rng.uniform((m, k))
+    b = rng.uniform((k, n))
+    got = _mm(dev, a, b)
+    rows = sorted(set(r for r in (0, 1, 63, 64, 127, m // 2, m - 1) if r < m))
+    assert O.max_rel_err(got[rows], O.matmul_f64(a, b, rows=rows)) <= TOL
+    assert np.array_equal(got, _mm(dev, a, b)), "not deterministic"
+
+
+def test_split_k_exact_on_integers(dev):
+    """Small integers: every partial sum is exact in f32, whatever the slice order."""
+    rng = np.random.default_rng(17)
+    for m, n, k in ((1024, 1024, 1024), (64, 4096, 4096)):
+        _say(f"sgemm split-k integers m={m} n={n} k={k}")
+        a = rng.integers(-8, 9, (m, k)).astype(np.float32)
+        b = rng.integers(-8, 9, (k, n)).astype(np.float32)
+        want = (a.astype(np.int64) @ b.astype(np.int64)).astype(np.float32)
+        assert np.array_equal(_mm(dev, a, b), want), (m, n, k)
+
+
 def test_config_4096_cubed(dev):
     """BASELINE config 3a: 4096^3, U[-1,1), seed 2; f64 oracle on sampled rows."""
     _say("sgemm 4096^3 seed 2")
@@ -255,9 +288,14 @@ def test_config_batched_16x1024(dev):
         cols = [t * 256 + (bi * 53 + t * 29) % 256 for t in range(4)]
         errc = O.max_rel_err(got[bi][:, cols], ab.astype(np.float64) @ bb[:, cols].astype(np.float64))
         assert err <= TOL and errc <= TOL, (bi, rows, cols, err, errc)
-    # batches are independent: batch 3 equals the single GEMM of batch 3
+    # batches are independent: a two-batch call on batches 3 and 5 (the same kernel; a single
+    # 1024^3 GEMM takes split-K, which rounds differently) reproduces them bit for bit
+    a2, b2 = np.ascontiguousarray(a[[3, 5]]), np.ascontiguousarray(b[[3, 5]])
+    two = Tensor.from_data(a2, [2, 1024, 1024], dev).batch_matmul(Tensor.from_data(b2, [2, 1024, 1024], dev))
+    two = two.to_numpy()
+    assert np.array_equal(two[0], got[3]) and np.array_equal(two[1], got[5])
     single = _mm(dev, np.ascontiguousarray(a[3]), np.ascontiguousarray(b[3]))
-    assert np.array_equal(single, got[3])
+    assert O.max_rel_err(single, got[3].astype(np.float64)) <= TOL
 
 
 def test_batched_ragged(dev):

@@ -2,7 +2,8 @@
 scratch is a fixed per-GPU device array) against bch_sgemm, called through
 the C ABI: bit-identical outputs, on two calls in a row with the second
 smaller, on each kernel family (decode-shaped split-k paths that use the
-scratch, and the MFMA tile path that needs none), and a clear rejection of a
+scratch, the MFMA tile path that needs none, and the tile path's split-K
+over the scratch), and a clear rejection of a
 shape whose partials would not fit."""
 from __future__ import annotations
 
@@ -42,6 +43,8 @@ def _both(dev, m, n, k, seed):
     [(8, 11008, 4096), (1, 4096, 512)],
     [(1, 11008, 4096), (20, 1000, 300)],
     [(256, 512, 384), (32, 256, 64)],
+    # split-K (slices in the scratch, then the reduce), then a smaller split
+    [(1024, 1024, 1024), (64, 1024, 2048)],
 ])
 def test_noalloc_matches_sgemm_twice(dev, shapes):
     for i, (m, n, k) in enumerate(shapes):
