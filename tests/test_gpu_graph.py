@@ -2,7 +2,8 @@
 
 Captured: the decode linear layer with [out, in] weights (the ring kernel, whose
 split-k blocks are combined in the kernel through epoch flags that every launch
-resets), the skinny GEMM (main kernel + reduce), row softmax and attention.  The
+resets), the skinny GEMM (main kernel + reduce), the tile GEMM (one launch) and its
+split-K (slices into the workspace + reduce), row softmax and attention.  The
 graph is replayed several times with the program's own eager calls (which reuse the
 same workspace and flags) and synchronisations between the replays; every replay
 must reproduce the eager results bit for bit.
@@ -68,6 +69,13 @@ def test_graph_replays_match_eager(dev):
     ya = Tensor.empty([m, n], dev)
     calls.append(("skinny m=8", lambda: lib.bch_sgemm(dev.ctx, m, n, k, C.c_void_p(xa.ptr), k, C.c_void_p(wa.ptr), n,
                                                        C.c_void_p(ya.ptr), n), ya))
+    for m2, n2, k2 in ((3072, 3072, 1024), (1024, 1024, 1024)):  # tiles, split-K
+        xg, wg = _up(dev, rng.uniform((m2, k2))), _up(dev, rng.uniform((k2, n2)))
+        yg = Tensor.empty([m2, n2], dev)
+        calls.append((f"sgemm {m2}x{n2}x{k2} ({lib.bch_sgemm_kernel_name(m2, n2, k2).decode()})",
+                      lambda m2=m2, n2=n2, k2=k2, xg=xg, wg=wg, yg=yg: lib.bch_sgemm(
+                          dev.ctx, m2, n2, k2, C.c_void_p(xg.ptr), k2, C.c_void_p(wg.ptr), n2, C.c_void_p(yg.ptr), n2),
+                      yg))
     rows, cols = 512, 2048
     sx = _up(dev, rng.normal((rows, cols), 0.0, 3.0))
     sy = Tensor.empty([rows, cols], dev)

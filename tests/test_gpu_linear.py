@@ -51,7 +51,8 @@ def _ref(x, w, bias, transb, relu):
 
 @pytest.mark.parametrize("m,n,k", [(256, 256, 256), (512, 768, 1024), (100, 77, 33), (1, 1024, 512),
                                    (8, 11008, 256), (32, 512, 4096), (300, 129, 64), (500, 772, 1028),
-                                   (260, 1000, 4), (64, 4096, 4096), (200, 1000, 2048)])
+                                   (260, 1000, 4), (64, 4096, 4096), (200, 1000, 2048), (3072, 1024, 3072),
+                                   (3000, 3000, 1000)])
 @pytest.mark.parametrize("transb", [0, 1])
 def test_sgemm_ex_vs_f64(dev, m, n, k, transb):
     _say(f"sgemm_ex m={m} n={n} k={k} transb={transb}")
@@ -59,7 +60,7 @@ def test_sgemm_ex_vs_f64(dev, m, n, k, transb):
     x = rng.uniform((m, k))
     w = rng.uniform((n, k) if transb else (k, n))
     bias = rng.uniform((n,))
-    for act, b in ((N.BCH_ACT_RELU, bias), (N.BCH_ACT_NONE, bias), (N.BCH_ACT_RELU, None)):
+    for act, b in ((N.BCH_ACT_RELU, bias), (N.BCH_ACT_NONE, bias), (N.BCH_ACT_RELU, None), (N.BCH_ACT_NONE, None)):
         got = _sgemm_ex(dev, transb, x, w, b, act)
         assert O.max_rel_err(got, _ref(x, w, b, transb, act == N.BCH_ACT_RELU)) <= TOL, (act, b is None)
 
