@@ -94,7 +94,7 @@ __device__ __forceinline__ float4 ld4(const float* p) {
   return *reinterpret_cast<const float4*>(p);
 }
 
-template <int BM, int BN, int BK, bool CHECK, bool TB, bool EPI, bool V4 = false>
+template <int BM, int BN, int BK, bool CHECK, bool TB, bool EPI, bool V4 = false, bool KF = false>
 __global__ __launch_bounds__(kThreads) void sgemm_mfma_kernel(
     int M, int N, int K, const float* __restrict__ A, int lda, long long sA,
     const float* __restrict__ B, int ldb, long long sB, float* __restrict__ C,
@@ -158,6 +158,16 @@ __global__ __launch_bounds__(kThreads) void sgemm_mfma_kernel(
   // acts on the address only, so nothing waits on the data before the LDS
   // store a tile later (a select on the loaded value made every load's
   // latency exposed: 4000^3 at 87 TFLOP/s against 97 for scalar guards).
+  // Offsets stay below 2^32: kBad plus at most 2^31 - 1 (the host checks that
+  // (K + BK) rows of a [K][N] B fit in 2^31 bytes).  A row (column) outside
+  // the matrix keeps kBad in its base offset, so adding the column of the
+  // load leaves it past the end.  Only the k check remains: a [K][N] B never
+  // needs it (rows from K on are past the resource's end), and with K a
+  // multiple of BK (KF) no load of A or of a [N][K] B reaches past K either,
+  // so those loads are one add.  Against the compare-and-select on every
+  // load (same box, two runs each): 2000 x 8000 x 4096 +3.0%, 4100 x 4100 x
+  // 4096 (128 x 128 tile) +2.3%, 6000 x 6000 x 3200 +1.9%, 3000 x 3000 x 1000
+  // (ragged K, only the [K][N] check gone) +1.5-3.8%.
   constexpr unsigned kBad = 0x80000000u;  // an offset past every resource's end
   // (unused, and removed, unless CHECK && V4)
   const int a_bytes = (int)(((long long)(M - 1) * lda + K) * 4);
@@ -197,7 +207,8 @@ __global__ __launch_bounds__(kThreads) void sgemm_mfma_kernel(
       if (!CHECK) {
         ra[f] = ld4(A + (long long)gr * lda + gc);
       } else if (V4) {
-        ra[f] = ld4_rs(ra_rs, (aoff[f] != kBad && gc < K) ? aoff[f] + (unsigned)gc * 4u : kBad);
+        ra[f] = ld4_rs(ra_rs, KF ? aoff[f] + (unsigned)gc * 4u
+                                : (aoff[f] != kBad && gc < K) ? aoff[f] + (unsigned)gc * 4u : kBad);
       } else {
         float t[4];
 #pragma unroll
@@ -215,7 +226,8 @@ __global__ __launch_bounds__(kThreads) void sgemm_mfma_kernel(
         if (!CHECK) {
           rb[f >> 2][f & 3] = ld4(B + (long long)gr * ldb + gc);
         } else if (V4) {
-          rb[f >> 2][f & 3] = ld4_rs(rb_rs, (boff[f] != kBad && gc < K) ? boff[f] + (unsigned)gc * 4u : kBad);
+          rb[f >> 2][f & 3] = ld4_rs(rb_rs, KF ? boff[f] + (unsigned)gc * 4u
+                                           : (boff[f] != kBad && gc < K) ? boff[f] + (unsigned)gc * 4u : kBad);
         } else {
           float t[4];
 #pragma unroll
@@ -235,7 +247,7 @@ __global__ __launch_bounds__(kThreads) void sgemm_mfma_kernel(
           if (!CHECK) {
             rb[q][e] = ld4(B + (long long)gk * ldb + gn);
           } else if (V4) {
-            rb[q][e] = ld4_rs(rb_rs, (boff[q] != kBad && gk < K) ? (unsigned)gk * (unsigned)ldb * 4u + boff[q] : kBad);
+            rb[q][e] = ld4_rs(rb_rs, (unsigned)gk * (unsigned)ldb * 4u + boff[q]);
           } else {
             float t[4];
 #pragma unroll
@@ -412,7 +424,7 @@ __global__ __launch_bounds__(kThreads) void sgemm_mfma_kernel(
   }
 }
 
-template <int BM, int BN, int BK, bool CHECK, bool TB, bool EPI, bool V4 = false>
+template <int BM, int BN, int BK, bool CHECK, bool TB, bool EPI, bool V4 = false, bool KF = false>
 hipError_t launch_tiles(hipStream_t s, int batch, int m, int n, int k,
                         const float* A, int lda, long long sA, const float* B,
                         int ldb, long long sB, float* C, int ldc, long long sC,
@@ -420,7 +432,7 @@ hipError_t launch_tiles(hipStream_t s, int batch, int m, int n, int k,
   using G = Cfg<BM, BN, BK>;
   const int tm = (m + BM - 1) / BM, tn = (n + BN - 1) / BN;
   const size_t lds = sizeof(float) * G::LDS_FLOATS;
-  auto kern = sgemm_mfma_kernel<BM, BN, BK, CHECK, TB, EPI, V4>;
+  auto kern = sgemm_mfma_kernel<BM, BN, BK, CHECK, TB, EPI, V4, KF>;
   hipError_t e = bch::ensure_dynamic_lds(reinterpret_cast<const void*>(kern), (int)lds);
   if (e != hipSuccess) return e;
   if (batch > 65535) return hipErrorInvalidValue;
@@ -478,24 +490,25 @@ bool fast_ok(Tile t, int m, int n, int k, const float* A, int lda, long long sA,
 bool vec4_ok(bool transb, int m, int n, int k, const float* A, int lda, long long sA, const float* B, int ldb,
              long long sB) {
   const long long a_bytes = ((long long)(m - 1) * lda + k) * 4;
-  const long long b_bytes = (transb ? (long long)(n - 1) * ldb + k : (long long)(k - 1) * ldb + n) * 4;
+  // a [K][N] B's loads reach up to row K + kBK - 1 (past the resource's end, read as zeros)
+  const long long b_bytes = (transb ? (long long)(n - 1) * ldb + k : (long long)(k + kBK) * ldb) * 4;
   return k >= 4 && k % 4 == 0 && n % 4 == 0 && lda % 4 == 0 && ldb % 4 == 0 && sA % 4 == 0 && sB % 4 == 0 &&
          aligned16(A) && aligned16(B) && a_bytes < (1LL << 31) && b_bytes < (1LL << 31);
 }
 
-template <bool CHECK, bool TB, bool EPI, bool V4>
+template <bool CHECK, bool TB, bool EPI, bool V4, bool KF = false>
 hipError_t launch_tile(Tile t, hipStream_t s, int batch, int m, int n, int k, const float* A, int lda,
                        long long sA, const float* B, int ldb, long long sB, float* C, int ldc, long long sC,
                        const float* bias, int act) {
   switch (t) {
     case Tile::k256x256:
-      return launch_tiles<256, 256, kBK, CHECK, TB, EPI, V4>(s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC,
+      return launch_tiles<256, 256, kBK, CHECK, TB, EPI, V4, KF>(s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC,
                                                              bias, act);
     case Tile::k256x128:
-      return launch_tiles<256, 128, kBK, CHECK, TB, EPI, V4>(s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC,
+      return launch_tiles<256, 128, kBK, CHECK, TB, EPI, V4, KF>(s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC,
                                                              bias, act);
     default:
-      return launch_tiles<128, 128, kBK, CHECK, TB, EPI, V4>(s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC,
+      return launch_tiles<128, 128, kBK, CHECK, TB, EPI, V4, KF>(s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC,
                                                              bias, act);
   }
 }
@@ -507,6 +520,8 @@ hipError_t launch_tile_any(int mode, Tile t, hipStream_t s, int batch, int m, in
                            long long sC, const float* bias, int act) {
   if (mode == 0)
     return launch_tile<false, TB, EPI, false>(t, s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC, bias, act);
+  if (mode == 1 && k % kBK == 0)
+    return launch_tile<true, TB, EPI, true, true>(t, s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC, bias, act);
   if (mode == 1)
     return launch_tile<true, TB, EPI, true>(t, s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC, bias, act);
   return launch_tile<true, TB, EPI, false>(t, s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC, bias, act);
