@@ -118,7 +118,10 @@ hipError_t launch_sgemm(hipStream_t s, int batch, int m, int n, int k,
                         float* C, int ldc, long long sC, void* ws,
                         size_t ws_bytes);
 size_t sgemm_workspace_bytes(int batch, int m, int n, int k);
-// Scratch of launch_sgemm_ex (the skinny paths' partials, or split-K partials).
+// The part of it a launch cannot do without (the skinny paths' and split-K's
+// partials); with less than sgemm_workspace_bytes the hybrid plan is skipped.
+size_t sgemm_required_workspace_bytes(int batch, int m, int n, int k);
+// Scratch of launch_sgemm_ex (the skinny paths' partials, split-K partials, or the hybrid plan's).
 size_t sgemm_ex_workspace_bytes(bool transb, int batch, int m, int n, int k, int lda, int ldb);
 const char* sgemm_kernel_name(int m, int n, int k);
 // With B given as [n][k] when transb (C = A B^T), and the linear layer's

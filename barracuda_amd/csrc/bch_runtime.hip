@@ -418,16 +418,17 @@ bch_status bch_sgemm_noalloc(bch_ctx* ctx, int m, int n, int k, const float* A, 
   if (!C || (k > 0 && (!A || !B))) return fail(ctx, BCH_E_INVALID, "matmul: NULL buffer");
   bch_status st = use(ctx);
   if (st != BCH_OK) return st;
-  // sized with this device current (the stream-K plans take one workgroup per CU)
-  const size_t wsb = bch::sgemm_workspace_bytes(1, m, n, k);
+  // sized with this device current (the stream-K plans take one workgroup per CU); the tile
+  // path's optional hybrid-plan scratch is used when it fits in the fixed scratch
+  const size_t wsb = bch::sgemm_required_workspace_bytes(1, m, n, k);
   if (wsb > kNoAllocScratchBytes)
     return fail(ctx, BCH_E_UNSUPPORTED,
                 "matmul (no-alloc): m=%d n=%d k=%d needs %zu bytes of scratch, more than the fixed %zu",
                 m, n, k, wsb, kNoAllocScratchBytes);
   if (wsb && !ctx->scratch)
     return fail(ctx, BCH_E_DEVICE, "matmul (no-alloc): fixed scratch unavailable (%s)", ctx->scratch_error.c_str());
-  hipError_t e = bch::launch_sgemm(ctx->stream, 1, m, n, k, A, lda, 0, B, ldb, 0, C, ldc, 0,
-                                   wsb ? ctx->scratch : nullptr, wsb ? kNoAllocScratchBytes : 0);
+  hipError_t e = bch::launch_sgemm(ctx->stream, 1, m, n, k, A, lda, 0, B, ldb, 0, C, ldc, 0, ctx->scratch,
+                                   ctx->scratch ? kNoAllocScratchBytes : 0);
   return from_hip(ctx, e, "matmul (no-alloc) launch");
 }
 

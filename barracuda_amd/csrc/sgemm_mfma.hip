@@ -94,11 +94,12 @@ __device__ __forceinline__ float4 ld4(const float* p) {
   return *reinterpret_cast<const float4*>(p);
 }
 
-template <int BM, int BN, int BK, bool CHECK, bool TB, bool EPI, bool V4 = false, bool KF = false>
+template <int BM, int BN, int BK, bool CHECK, bool TB, bool EPI, bool V4 = false, bool KF = false, bool HY = false>
 __global__ __launch_bounds__(kThreads) void sgemm_mfma_kernel(
     int M, int N, int K, const float* __restrict__ A, int lda, long long sA,
     const float* __restrict__ B, int ldb, long long sB, float* __restrict__ C,
-    int ldc, long long sC, int tiles_m, int tiles_n, const float* __restrict__ bias, int act) {
+    int ldc, long long sC, int tiles_m, int tiles_n, const float* __restrict__ bias, int act,
+    int hy_ndp, int hy_r, int hy_kt, float* __restrict__ hy_P) {
   using G = Cfg<BM, BN, BK>;
   constexpr int LDK = G::LDK;
   extern __shared__ float4 smem4[];
@@ -110,7 +111,26 @@ __global__ __launch_bounds__(kThreads) void sgemm_mfma_kernel(
   const int ntiles = tiles_m * tiles_n;
   int p = blockIdx.x;
   int lt = p;
-  if ((ntiles & 7) == 0) lt = (p & 7) * (ntiles >> 3) + (p >> 3);
+  bool tail = false;  // HY: this workgroup computes one k-slice of one of the last hy_r tiles
+  int hy_slot = 0, hy_slice = 0;
+  if constexpr (!HY) {
+    if ((ntiles & 7) == 0) lt = (p & 7) * (ntiles >> 3) + (p >> 3);
+  } else {
+    // whole tiles 0 .. hy_ndp - 1 first (hy_ndp fills whole rounds), XCD-contiguous; then
+    // the k-slices of tiles hy_ndp .. hy_ndp + hy_r - 1, slice-major and XCD-contiguous,
+    // so that an XCD's workgroups run neighbouring tiles over the same k range
+    if (p < hy_ndp) {
+      if ((hy_ndp & 7) == 0) lt = (p & 7) * (hy_ndp >> 3) + (p >> 3);
+    } else {
+      const int nt = (int)gridDim.x - hy_ndp;
+      int q = p - hy_ndp;
+      if ((nt & 7) == 0) q = (q & 7) * (nt >> 3) + (q >> 3);
+      hy_slice = q / hy_r;
+      hy_slot = q - hy_slice * hy_r;
+      lt = hy_ndp + hy_slot;
+      tail = true;
+    }
+  }
   constexpr int GROUP = 8;
   const int group_size = GROUP * tiles_n;
   const int g = lt / group_size;
@@ -125,6 +145,14 @@ __global__ __launch_bounds__(kThreads) void sgemm_mfma_kernel(
   A += bz * sA;
   B += bz * sB;
   C += bz * sC;
+  if constexpr (HY) {
+    if (tail) {  // k-tiles hy_slice * hy_kt .. + hy_kt - 1, as a product of K = hy_kt * BK
+      const long long k0 = (long long)hy_slice * hy_kt * BK;
+      A += k0;
+      B += TB ? k0 : k0 * ldb;
+      K = hy_kt * BK;
+    }
+  }
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -389,6 +417,19 @@ __global__ __launch_bounds__(kThreads) void sgemm_mfma_kernel(
   }
 
   // ---- epilogue: value r of lane l is row 8*(r/4) + 4*lh + r%4, col li ----
+  if constexpr (HY) {
+    if (tail) {  // the slice's sums, a whole BM x BN tile, into its slot of the partials
+      float* Pt = hy_P + ((long long)hy_slice * hy_r + hy_slot) * (BM * BN);
+#pragma unroll
+      for (int i = 0; i < G::TM; ++i)
+#pragma unroll
+        for (int j = 0; j < G::TN; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            Pt[(wm + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3)) * BN + wn + j * 32 + li] = acc[i][j][r];
+      return;
+    }
+  }
   if constexpr (!EPI) {
 #pragma unroll
     for (int i = 0; i < G::TM; ++i) {
@@ -437,7 +478,23 @@ hipError_t launch_tiles(hipStream_t s, int batch, int m, int n, int k,
   if (e != hipSuccess) return e;
   if (batch > 65535) return hipErrorInvalidValue;
   hipLaunchKernelGGL(kern, dim3(tm * tn, batch), dim3(kThreads), lds, s, m, n, k,
-                     A, lda, sA, B, ldb, sB, C, ldc, sC, tm, tn, bias, act);
+                     A, lda, sA, B, ldb, sB, C, ldc, sC, tm, tn, bias, act, 0, 0, 0, nullptr);
+  return hipGetLastError();
+}
+
+// The hybrid launch (batch 1, K a multiple of BK): ndp whole tiles, then r tiles in
+// S k-slices of kt k-tiles each into P (see HybPlan).
+template <int BM, int BN, int BK, bool CHECK, bool TB, bool EPI, bool V4, bool KF>
+hipError_t launch_hyb_tiles(hipStream_t s, int m, int n, int k, const float* A, int lda, const float* B, int ldb,
+                            float* C, int ldc, const float* bias, int act, int ndp, int r, int S, int kt, float* P) {
+  using G = Cfg<BM, BN, BK>;
+  const int tm = (m + BM - 1) / BM, tn = (n + BN - 1) / BN;
+  const size_t lds = sizeof(float) * G::LDS_FLOATS;
+  auto kern = sgemm_mfma_kernel<BM, BN, BK, CHECK, TB, EPI, V4, KF, true>;
+  hipError_t e = bch::ensure_dynamic_lds(reinterpret_cast<const void*>(kern), (int)lds);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(kern, dim3(ndp + r * S), dim3(kThreads), lds, s, m, n, k, A, lda, 0LL, B, ldb, 0LL, C, ldc,
+                     0LL, tm, tn, bias, act, ndp, r, kt, P);
   return hipGetLastError();
 }
 
@@ -456,14 +513,15 @@ constexpr int kBK = 32;
 // (6144^3: three rounds of 256x256, 107 TFLOP/s).
 enum class Tile { k256x256, k256x128, k128x128 };
 
+struct TileOpt { Tile t; int bm, bn; double eff; };
+constexpr TileOpt kTileOpts[] = {{Tile::k256x256, 256, 256, 1.0}, {Tile::k256x128, 256, 128, 0.966},
+                                 {Tile::k128x128, 128, 128, 0.883}};
+
 Tile pick_tile(int batch, int m, int n) {
   const long long cu = bch::device_cu_count();
-  struct Opt { Tile t; int bm, bn; double eff; };
-  const Opt opts[] = {{Tile::k256x256, 256, 256, 1.0}, {Tile::k256x128, 256, 128, 0.966},
-                      {Tile::k128x128, 128, 128, 0.883}};
   Tile best = Tile::k256x256;
   double best_cost = 0.0;
-  for (const Opt& o : opts) {
+  for (const TileOpt& o : kTileOpts) {
     const long long tiles = (long long)batch * ((m + o.bm - 1) / o.bm) * ((n + o.bn - 1) / o.bn);
     const double cost = (double)((tiles + cu - 1) / cu) * o.bm * o.bn / o.eff;
     if (o.t == Tile::k256x256 || cost < best_cost * 0.999) {
@@ -602,6 +660,146 @@ __global__ __launch_bounds__(256) void sgemm_splitk_reduce(int M, int N, int S, 
   }
 }
 
+// ---- whole rounds data-parallel, the last round's tiles split over k (the hybrid plan) ----
+// With T tiles on CU compute units, R = T / CU whole rounds and r = T mod CU
+// tiles left over, the last round would run r workgroups of full length on
+// r CUs.  Instead one launch runs the R * CU whole tiles and then the r tiles
+// in S slices of equal k length (S * r <= CU), each slice's sums stored as a
+// compact BM x BN tile; sgemm_tail_reduce adds each tile's S slices in slice
+// order (deterministic) and applies the epilogue that the whole tiles apply
+// in the kernel.  Every slice covers the same k-tiles of neighbouring tiles,
+// so the slices of a round share A and B panels in L2 the way whole tiles do.
+// The plan is modelled like the tile choice (k-tiles x tile area /
+// efficiency per round; the partials' HBM traffic at 5 TB/s, one 256 x 256
+// k-tile taking 7.4 us) and used when it beats the best data-parallel tiling
+// by 3%.  It needs K a multiple of 32 and unguarded or float4-guarded loads;
+// without the workspace (up to kHybWsMax) the data-parallel tiling runs.
+constexpr size_t kHybWsMax = (size_t)256 << 20;
+
+struct HybPlan {
+  Tile t = Tile::k256x256;
+  int S = 0, ndp = 0, r = 0, kt = 0;  // slices, whole tiles, split tiles, k-tiles per slice
+};
+
+size_t hyb_bytes(const HybPlan& h) { return (size_t)h.S * h.r * tile_m(h.t) * tile_n(h.t) * sizeof(float); }
+
+bool hyb_plan(int batch, int m, int n, int k, HybPlan& out) {
+  if (batch != 1 || k <= 0 || k % kBK != 0 || split_slices(batch, m, n, k) > 1) return false;
+  const long long cu = bch::device_cu_count();
+  const int nk = k / kBK;
+  double best_dp = 0.0, best = 0.0;
+  bool found = false;
+  for (const TileOpt& o : kTileOpts) {
+    const long long T = (long long)((m + o.bm - 1) / o.bm) * ((n + o.bn - 1) / o.bn);
+    const double per = o.bm * o.bn / 65536.0 / o.eff;  // one k-tile of this tile, in 256 x 256 k-tiles
+    const double dp = (double)((T + cu - 1) / cu) * nk * per;
+    if (best_dp == 0.0 || dp < best_dp) best_dp = dp;
+    const long long R = T / cu, r = T % cu;
+    if (R < 1 || r == 0) continue;
+    int S = 0;
+    for (int sl = 8; sl >= 2; --sl)
+      if (sl * r <= cu && nk % sl == 0 && nk / sl >= kSplitMinKt &&
+          (size_t)sl * r * o.bm * o.bn * sizeof(float) <= kHybWsMax) {
+        S = sl;
+        break;
+      }
+    if (S == 0) continue;
+    const double cost = (double)(R * nk + nk / S) * per + (2.0 * S + 1.0) * r * (o.bm * o.bn / 65536.0) * 0.00709 + 0.3;
+    if (!found || cost < best) {
+      found = true;
+      best = cost;
+      out.t = o.t;
+      out.S = S;
+      out.ndp = (int)(R * cu);
+      out.r = (int)r;
+      out.kt = nk / S;
+    }
+  }
+  return found && best < 0.97 * best_dp;
+}
+
+// C[tile j's rows and columns] = act(sum over s < S of P[s][j] (+ bias)) for the r split
+// tiles j (logical tiles tile0 + j, in the kernel's grouped order); V: four columns per
+// thread (N % 4 == 0, ldc % 4 == 0, C and bias 16-byte aligned)
+template <bool V, int BM, int BN>
+__global__ __launch_bounds__(256) void sgemm_tail_reduce(int M, int N, int tiles_m, int tiles_n, int tile0, int r,
+                                                         int S, const float* __restrict__ P, float* __restrict__ C,
+                                                         int ldc, const float* __restrict__ bias, int act) {
+  constexpr int TS = BM * BN;
+  constexpr int w = V ? 4 : 1;
+  const long long total = (long long)r * TS / w;
+  for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (long long)gridDim.x * blockDim.x) {
+    const long long e = i * w;
+    const int j = (int)(e / TS), l = (int)(e - (long long)j * TS);
+    const int lr = l / BN, lc = l - lr * BN;
+    const int L = tile0 + j, group_size = 8 * tiles_n, g = L / group_size, first_m = g * 8;
+    const int gm = min(tiles_m - first_m, 8), within = L - g * group_size;
+    const int row = (first_m + within % gm) * BM + lr, col = (within / gm) * BN + lc;
+    if (row >= M || col >= N) continue;
+    const float* src = P + (long long)j * TS + l;
+    if constexpr (V) {
+      float4 acc = *reinterpret_cast<const float4*>(src);
+      for (int s = 1; s < S; ++s) {
+        const float4 x = *reinterpret_cast<const float4*>(src + (long long)s * r * TS);
+        acc.x += x.x;
+        acc.y += x.y;
+        acc.z += x.z;
+        acc.w += x.w;
+      }
+      if (bias) {
+        acc.x += bias[col];
+        acc.y += bias[col + 1];
+        acc.z += bias[col + 2];
+        acc.w += bias[col + 3];
+      }
+      acc = make_float4(bch::activate(acc.x, act), bch::activate(acc.y, act), bch::activate(acc.z, act),
+                        bch::activate(acc.w, act));
+      *reinterpret_cast<float4*>(C + (long long)row * ldc + col) = acc;
+    } else {
+      float acc = src[0];
+      for (int s = 1; s < S; ++s) acc += src[(long long)s * r * TS];
+      if (bias) acc += bias[col];
+      C[(long long)row * ldc + col] = bch::activate(acc, act);
+    }
+  }
+}
+
+template <int BM, int BN>
+hipError_t launch_tail_reduce(hipStream_t s, int m, int n, const HybPlan& h, const float* P, float* C, int ldc,
+                              const float* bias, int act) {
+  const int tm = (m + BM - 1) / BM, tn = (n + BN - 1) / BN;
+  const bool v = n % 4 == 0 && ldc % 4 == 0 && aligned16(C) && (bias == nullptr || aligned16(bias));
+  const long long work = (long long)h.r * BM * BN / (v ? 4 : 1);
+  const int blocks = (int)std::min<long long>((work + 255) / 256, 4096);
+  if (v)
+    hipLaunchKernelGGL((sgemm_tail_reduce<true, BM, BN>), dim3(blocks), dim3(256), 0, s, m, n, tm, tn, h.ndp, h.r,
+                       h.S, P, C, ldc, bias, act);
+  else
+    hipLaunchKernelGGL((sgemm_tail_reduce<false, BM, BN>), dim3(blocks), dim3(256), 0, s, m, n, tm, tn, h.ndp, h.r,
+                       h.S, P, C, ldc, bias, act);
+  return hipGetLastError();
+}
+
+// mode 0: unguarded loads; mode 1: float4-guarded (K % 32 == 0 here, so the one-add form)
+template <bool TB, bool EPI>
+hipError_t launch_hyb(int mode, const HybPlan& h, hipStream_t s, int m, int n, int k, const float* A, int lda,
+                      const float* B, int ldb, float* C, int ldc, const float* bias, int act, float* P) {
+#define BCH_HYB(BM_, BN_)                                                                                         \
+  (mode == 0 ? launch_hyb_tiles<BM_, BN_, kBK, false, TB, EPI, false, false>(s, m, n, k, A, lda, B, ldb, C, ldc,  \
+                                                                            bias, act, h.ndp, h.r, h.S, h.kt, P) \
+             : launch_hyb_tiles<BM_, BN_, kBK, true, TB, EPI, true, true>(s, m, n, k, A, lda, B, ldb, C, ldc, bias, \
+                                                                         act, h.ndp, h.r, h.S, h.kt, P))
+  hipError_t e = h.t == Tile::k256x256   ? BCH_HYB(256, 256)
+                 : h.t == Tile::k256x128 ? BCH_HYB(256, 128)
+                                         : BCH_HYB(128, 128);
+#undef BCH_HYB
+  if (e != hipSuccess) return e;
+  return h.t == Tile::k256x256   ? launch_tail_reduce<256, 256>(s, m, n, h, P, C, ldc, bias, act)
+         : h.t == Tile::k256x128 ? launch_tail_reduce<256, 128>(s, m, n, h, P, C, ldc, bias, act)
+                                 : launch_tail_reduce<128, 128>(s, m, n, h, P, C, ldc, bias, act);
+}
+
 }  // namespace
 
 namespace bch {
@@ -624,22 +822,44 @@ const char* sgemm_kernel_name(int m, int n, int k) {
          "sgemm_mfma_kernel<128,128,32,true>+sgemm_splitk_reduce"}};
     return split_names[static_cast<int>(t)][fast ? 0 : v4 ? 1 : 2];
   }
+  HybPlan h;
+  if (hyb_plan(1, m, n, k, h)) {
+    const bool fast = m % tile_m(h.t) == 0 && n % tile_n(h.t) == 0 && n % 4 == 0;
+    static const char* const hyb_names[3][2] = {
+        {"sgemm_mfma_kernel<256,256,32,false,hyb>+sgemm_tail_reduce", "sgemm_mfma_kernel<256,256,32,true,v4,hyb>+sgemm_tail_reduce"},
+        {"sgemm_mfma_kernel<256,128,32,false,hyb>+sgemm_tail_reduce", "sgemm_mfma_kernel<256,128,32,true,v4,hyb>+sgemm_tail_reduce"},
+        {"sgemm_mfma_kernel<128,128,32,false,hyb>+sgemm_tail_reduce", "sgemm_mfma_kernel<128,128,32,true,v4,hyb>+sgemm_tail_reduce"}};
+    if (fast || v4) return hyb_names[static_cast<int>(h.t)][fast ? 0 : 1];
+  }
   return tile_name(t, !check ? 0 : v4 ? 1 : 2);
+}
+
+// The tile path's scratch: split-K partials (required), or the hybrid plan's (optional:
+// without them the data-parallel tiling runs).
+static size_t tile_workspace_bytes(int batch, int m, int n, int k, bool optional) {
+  const int sl = split_slices(batch, m, n, k);
+  if (sl > 1) return (size_t)sl * m * n * sizeof(float);
+  HybPlan h;
+  return optional && hyb_plan(batch, m, n, k, h) ? hyb_bytes(h) : 0;
 }
 
 size_t sgemm_workspace_bytes(int batch, int m, int n, int k) {
   if (batch == 1 && sgemm_skinny_applies(m, n, k, nullptr, k, nullptr, n))
     return sgemm_skinny_workspace_bytes(m, n, k);
-  const int sl = split_slices(batch, m, n, k);
-  return sl > 1 ? (size_t)sl * m * n * sizeof(float) : 0;
+  return tile_workspace_bytes(batch, m, n, k, true);
+}
+
+size_t sgemm_required_workspace_bytes(int batch, int m, int n, int k) {
+  if (batch == 1 && sgemm_skinny_applies(m, n, k, nullptr, k, nullptr, n))
+    return sgemm_skinny_workspace_bytes(m, n, k);
+  return tile_workspace_bytes(batch, m, n, k, false);
 }
 
 size_t sgemm_ex_workspace_bytes(bool transb, int batch, int m, int n, int k, int lda, int ldb) {
   if (!transb) return sgemm_workspace_bytes(batch, m, n, k);
   if (batch == 1 && sgemm_skinny_nt_applies(m, n, k, nullptr, lda, nullptr, ldb))
     return sgemm_skinny_nt_workspace_bytes(m, n, k);
-  const int sl = split_slices(batch, m, n, k);
-  return sl > 1 ? (size_t)sl * m * n * sizeof(float) : 0;
+  return tile_workspace_bytes(batch, m, n, k, true);
 }
 
 hipError_t launch_sgemm(hipStream_t s, int batch, int m, int n, int k, const float* A, int lda, long long sA,
@@ -679,12 +899,26 @@ hipError_t launch_sgemm_ex(hipStream_t s, bool transb, int batch, int m, int n, 
       hipLaunchKernelGGL(sgemm_splitk_reduce<false>, dim3(blocks), dim3(256), 0, s, m, n, sl, P, C, ldc, bias, act);
     return hipGetLastError();
   }
+  const bool epi = bias != nullptr || act != 0;
+  HybPlan h;
+  if (hyb_plan(batch, m, n, k, h) && ws != nullptr && ws_bytes >= hyb_bytes(h)) {
+    const int hmode = fast_ok(h.t, m, n, k, A, lda, sA, B, ldb, sB)                ? 0
+                      : vec4_ok(transb, m, n, k, A, lda, sA, B, ldb, sB)          ? 1
+                                                                                   : 2;
+    if (hmode != 2) {
+      float* P = static_cast<float*>(ws);
+      if (transb)
+        return epi ? launch_hyb<true, true>(hmode, h, s, m, n, k, A, lda, B, ldb, C, ldc, bias, act, P)
+                   : launch_hyb<true, false>(hmode, h, s, m, n, k, A, lda, B, ldb, C, ldc, bias, act, P);
+      return epi ? launch_hyb<false, true>(hmode, h, s, m, n, k, A, lda, B, ldb, C, ldc, bias, act, P)
+                 : launch_hyb<false, false>(hmode, h, s, m, n, k, A, lda, B, ldb, C, ldc, bias, act, P);
+    }
+  }
   // the [n][k] tile loads need the same alignment as the [k][n] ones (ldb, sB multiples of 4); a
   // [n][k] B needs only K % 4 == 0 for whole float4, but N % 4 is kept for one rule
   const int mode = fast_ok(t, m, n, k, A, lda, sA, B, ldb, sB) ? 0
                    : vec4_ok(transb, m, n, k, A, lda, sA, B, ldb, sB) ? 1
                                                                  : 2;
-  const bool epi = bias != nullptr || act != 0;
   if (transb)
     return epi ? launch_tile_any<true, true>(mode, t, s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC, bias, act)
                : launch_tile_any<true, false>(mode, t, s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC, bias,

@@ -194,7 +194,7 @@ LARGE_TILE_CASES = [  # (m, n, k, the kernel the shape takes)
     (8192, 1024, 64, "sgemm_mfma_kernel<256,128,32,false>"),
     (8192, 1020, 68, "sgemm_mfma_kernel<256,128,32,true,v4>"),
     (8190, 1024, 62, "sgemm_mfma_kernel<256,128,32,true>"),
-    (3072, 3072, 512, "sgemm_mfma_kernel<128,128,32,false>"),
+    (2048, 2048, 512, "sgemm_mfma_kernel<128,128,32,false>"),
     (4100, 4096, 300, "sgemm_mfma_kernel<128,128,32,true,v4>"),
     (2000, 2000, 95, "sgemm_mfma_kernel<128,128,32,true>"),
 ]
@@ -245,6 +245,46 @@ def test_split_k_exact_on_integers(dev):
     rng = np.random.default_rng(17)
     for m, n, k in ((1024, 1024, 1024), (64, 4096, 4096)):
         _say(f"sgemm split-k integers m={m} n={n} k={k}")
+        a = rng.integers(-8, 9, (m, k)).astype(np.float32)
+        b = rng.integers(-8, 9, (k, n)).astype(np.float32)
+        want = (a.astype(np.int64) @ b.astype(np.int64)).astype(np.float32)
+        assert np.array_equal(_mm(dev, a, b), want), (m, n, k)
+
+
+HYBRID_CASES = [(3072, 3072, 1024, "sgemm_mfma_kernel<128,128,32,false,hyb>+sgemm_tail_reduce"),
+                (3000, 3000, 1024, "sgemm_mfma_kernel<128,128,32,true,v4,hyb>+sgemm_tail_reduce"),
+                (5120, 5120, 1024, "sgemm_mfma_kernel<256,128,32,false,hyb>+sgemm_tail_reduce"),
+                (4100, 4100, 1024, "sgemm_mfma_kernel<256,128,32,true,v4,hyb>+sgemm_tail_reduce"),
+                (6144, 6144, 1536, "sgemm_mfma_kernel<256,256,32,false,hyb>+sgemm_tail_reduce"),
+                (6000, 6000, 3200, "sgemm_mfma_kernel<256,256,32,true,v4,hyb>+sgemm_tail_reduce")]
+
+
+@pytest.mark.parametrize("m,n,k,kernel", HYBRID_CASES)
+def test_hybrid_vs_f64(dev, m, n, k, kernel):
+    """Tiles leaving the last round part-filled: whole rounds of tiles, then the leftover tiles
+    in k-slices whose sums sgemm_tail_reduce adds in slice order.  Every tile size with
+    unguarded and float4-guarded loads; rows across every tile row and columns across every
+    tile column (so every whole and every split tile is compared with f64); repeated calls
+    are bit-identical."""
+    assert dev._lib.bch_sgemm_kernel_name(m, n, k).decode() == kernel
+    _say(f"sgemm hybrid m={m} n={n} k={k} ({kernel})")
+    rng = O.Lcg(m + 5 * n + 3 * k)
+    a = rng.uniform((m, k))
+    b = rng.uniform((k, n))
+    got = _mm(dev, a, b)
+    rows = sorted(r for r in {0, 1, m - 1} | {t * 128 + (t * 37) % 128 for t in range((m + 127) // 128)} if r < m)
+    assert O.max_rel_err(got[rows], O.matmul_f64(a, b, rows=rows)) <= TOL
+    cols = sorted(c for c in {0, n - 1} | {t * 128 + (t * 53) % 128 for t in range((n + 127) // 128)} if c < n)
+    assert O.max_rel_err(got[:, cols], a.astype(np.float64) @ b[:, cols].astype(np.float64)) <= TOL
+    assert np.array_equal(got, _mm(dev, a, b)), "not deterministic"
+
+
+def test_hybrid_exact_on_integers(dev):
+    """Small integers: every slice's sums are exact in f32, so the split tiles equal the
+    whole-tile products bit for bit."""
+    rng = np.random.default_rng(31)
+    for m, n, k in ((3072, 3072, 1024), (4100, 4100, 1024)):
+        _say(f"sgemm hybrid integers m={m} n={n} k={k}")
         a = rng.integers(-8, 9, (m, k)).astype(np.float32)
         b = rng.integers(-8, 9, (k, n)).astype(np.float32)
         want = (a.astype(np.int64) @ b.astype(np.int64)).astype(np.float32)

@@ -2,8 +2,9 @@
 
 Captured: the decode linear layer with [out, in] weights (the ring kernel, whose
 split-k blocks are combined in the kernel through epoch flags that every launch
-resets), the skinny GEMM (main kernel + reduce), the tile GEMM (one launch) and its
-split-K (slices into the workspace + reduce), row softmax and attention.  The
+resets), the skinny GEMM (main kernel + reduce), the tile GEMM's hybrid plan (whole
+tiles and k-slices in one launch + reduce) and its split-K (slices into the workspace +
+reduce), row softmax and attention.  The
 graph is replayed several times with the program's own eager calls (which reuse the
 same workspace and flags) and synchronisations between the replays; every replay
 must reproduce the eager results bit for bit.
@@ -69,7 +70,7 @@ def test_graph_replays_match_eager(dev):
     ya = Tensor.empty([m, n], dev)
     calls.append(("skinny m=8", lambda: lib.bch_sgemm(dev.ctx, m, n, k, C.c_void_p(xa.ptr), k, C.c_void_p(wa.ptr), n,
                                                        C.c_void_p(ya.ptr), n), ya))
-    for m2, n2, k2 in ((3072, 3072, 1024), (1024, 1024, 1024)):  # tiles, split-K
+    for m2, n2, k2 in ((3072, 3072, 1024), (1024, 1024, 1024)):  # hybrid, split-K
         xg, wg = _up(dev, rng.uniform((m2, k2))), _up(dev, rng.uniform((k2, n2)))
         yg = Tensor.empty([m2, n2], dev)
         calls.append((f"sgemm {m2}x{n2}x{k2} ({lib.bch_sgemm_kernel_name(m2, n2, k2).decode()})",

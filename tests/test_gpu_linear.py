@@ -52,7 +52,7 @@ def _ref(x, w, bias, transb, relu):
 @pytest.mark.parametrize("m,n,k", [(256, 256, 256), (512, 768, 1024), (100, 77, 33), (1, 1024, 512),
                                    (8, 11008, 256), (32, 512, 4096), (300, 129, 64), (500, 772, 1028),
                                    (260, 1000, 4), (64, 4096, 4096), (200, 1000, 2048), (3072, 1024, 3072),
-                                   (3000, 3000, 1000)])
+                                   (3000, 3000, 1000), (3072, 3072, 512), (3000, 3000, 1024)])
 @pytest.mark.parametrize("transb", [0, 1])
 def test_sgemm_ex_vs_f64(dev, m, n, k, transb):
     _say(f"sgemm_ex m={m} n={n} k={k} transb={transb}")

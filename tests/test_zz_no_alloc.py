@@ -2,9 +2,10 @@
 scratch is a fixed per-GPU device array) against bch_sgemm, called through
 the C ABI: bit-identical outputs, on two calls in a row with the second
 smaller, on each kernel family (decode-shaped split-k paths that use the
-scratch, the MFMA tile path that needs none, and the tile path's split-K
-over the scratch), and a clear rejection of a
-shape whose partials would not fit."""
+scratch, the MFMA tile path that needs none, the tile path's split-K and
+hybrid plan over the scratch); the whole tiles where the hybrid plan's
+partials exceed the scratch; and a clear rejection of a shape whose
+required partials would not fit."""
 from __future__ import annotations
 
 import ctypes as C
@@ -45,6 +46,8 @@ def _both(dev, m, n, k, seed):
     [(256, 512, 384), (32, 256, 64)],
     # split-K (slices in the scratch, then the reduce), then a smaller split
     [(1024, 1024, 1024), (64, 1024, 2048)],
+    # the hybrid plan (16 MiB and 8.5 MiB of tail partials in the scratch)
+    [(3072, 3072, 1024), (2304, 2304, 1024)],
 ])
 def test_noalloc_matches_sgemm_twice(dev, shapes):
     for i, (m, n, k) in enumerate(shapes):
@@ -52,6 +55,18 @@ def test_noalloc_matches_sgemm_twice(dev, shapes):
         got, want, a, b = _both(dev, m, n, k, 1000 * i + m + n + k)
         assert np.array_equal(got, want), (m, n, k)
         rows = list(range(min(m, 4))) + [m - 1]
+        assert O.max_rel_err(got[rows], O.matmul_f64(a, b, rows=rows)) <= TOL
+
+
+def test_noalloc_takes_whole_tiles_where_the_hybrid_does_not_fit(dev):
+    """6144 x 6144 x 1536 takes the hybrid plan through bch_sgemm (64 MiB of tail partials,
+    more than the fixed scratch); the no-alloc call runs whole tiles instead, then a smaller
+    hybrid shape that fits.  Each within tolerance of bch_sgemm and of f64."""
+    for i, (m, n, k) in enumerate(((6144, 6144, 1536), (3000, 3000, 1024))):
+        _say(f"sgemm_noalloc call {i}: m={m} n={n} k={k} (bch_sgemm: {dev._lib.bch_sgemm_kernel_name(m, n, k).decode()})")
+        got, want, a, b = _both(dev, m, n, k, 7000 + i)
+        assert O.max_rel_err(got, want.astype(np.float64)) <= TOL
+        rows = [0, 1, m // 2, m - 1]
         assert O.max_rel_err(got[rows], O.matmul_f64(a, b, rows=rows)) <= TOL
 
 
