@@ -379,6 +379,24 @@ def _bench_batched(dev, T, reps):
     wall, ev = T.run(lambda i: lib.bch_sgemm(ctx, 256, 256, 256, pa, 256, pb, 256, pc, 256), reps, 3)
     out["matmul_256"] = {"us": ev * 1e3, "GFLOP/s": 2.0 * 256 ** 3 / (ev * 1e-3) / 1e9,
                          "kernel": lib.bch_sgemm_kernel_name(256, 256, 256).decode()}
+    del a, b, c
+    # MatMul at shapes whose tiles do not come out in whole rounds of the CUs: the tile
+    # choice, the hybrid plan (whole tiles + k-sliced leftover tiles), split-K and the
+    # float4-guarded ragged loads, beside the headline's whole-round 4096^3
+    shapes = {}
+    for m, n, k in ((3072, 3072, 3072), (5120, 5120, 5120), (6144, 6144, 6144), (4096, 11008, 4096),
+                    (4000, 4000, 4000), (1024, 1024, 1024)):
+        s1 = LcgStream(m + n + k, dev)
+        a, b = s1.uniform([m, k]), s1.uniform([k, n])
+        c = Tensor.empty([m, n], dev)
+        pa, pb, pc = C.c_void_p(a.ptr), C.c_void_p(b.ptr), C.c_void_p(c.ptr)
+        wall, ev = T.run(lambda i, m=m, n=n, k=k: lib.bch_sgemm(ctx, m, n, k, pa, k, pb, n, pc, n), reps, 3)
+        fl = 2.0 * m * n * k
+        shapes[f"{m}x{n}x{k}"] = {"TFLOP/s": fl / (ev * 1e-3) / 1e12, "us": ev * 1e3,
+                                  "mfma_frac": fl / (ev * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS,
+                                  "kernel": lib.bch_sgemm_kernel_name(m, n, k).decode()}
+        del a, b, c
+    out["sgemm_shapes"] = shapes
     return out
 
 
