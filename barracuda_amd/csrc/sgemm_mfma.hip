@@ -193,9 +193,9 @@ __global__ __launch_bounds__(kThreads) void sgemm_mfma_kernel(
   // needs it (rows from K on are past the resource's end), and with K a
   // multiple of BK (KF) no load of A or of a [N][K] B reaches past K either,
   // so those loads are one add.  Against the compare-and-select on every
-  // load (same box, two runs each): 2000 x 8000 x 4096 +3.0%, 4100 x 4100 x
-  // 4096 (128 x 128 tile) +2.3%, 6000 x 6000 x 3200 +1.9%, 3000 x 3000 x 1000
-  // (ragged K, only the [K][N] check gone) +1.5-3.8%.
+  // load (same box, clocks settled): 4100 x 4100 x 4096 and 6000 x 6000 x
+  // 3200 (128 x 128 tile) +3.2%, 3000 x 3000 x 1000 (ragged K, only the
+  // [K][N] check gone) +2.3%, 4000^3 +1.7%, 2000 x 8000 x 4096 +1.2%.
   constexpr unsigned kBad = 0x80000000u;  // an offset past every resource's end
   // (unused, and removed, unless CHECK && V4)
   const int a_bytes = (int)(((long long)(M - 1) * lda + K) * 4);
