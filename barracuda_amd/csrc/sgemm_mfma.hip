@@ -515,7 +515,7 @@ enum class Tile { k256x256, k256x128, k128x128 };
 
 struct TileOpt { Tile t; int bm, bn; double eff; };
 constexpr TileOpt kTileOpts[] = {{Tile::k256x256, 256, 256, 1.0}, {Tile::k256x128, 256, 128, 0.966},
-                                 {Tile::k128x128, 128, 128, 0.883}};
+                                 {Tile::k128x128, 128, 128, 0.92}};
 
 Tile pick_tile(int batch, int m, int n) {
   const long long cu = bch::device_cu_count();
