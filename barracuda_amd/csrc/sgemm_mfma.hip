@@ -94,11 +94,12 @@ __device__ __forceinline__ float4 ld4(const float* p) {
   return *reinterpret_cast<const float4*>(p);
 }
 
-// The full-tile kernel without epilogue stores C block by block during its last
-// k-tile (kernel's ES path) when set.  Against storing after the last k-tile
-// (same box, three runs each): 16 x 1024^3 batched 248.1 -> 244.4 us (+1.5%),
+// The kernel without epilogue stores C block by block during its last k-tile
+// (kernel's ES path) when set.  Against storing after the last k-tile (same
+// box, three runs each): 16 x 1024^3 batched 248.1 -> 244.4 us (+1.5%),
 // 16384 x 4096 x 512 +2.4%, 4096 x 4096 x 1024 +1.6%, 8192^3 +0.4%, 4096^3
-// +0.3%; the 128 x 128 tile at 2048 x 2048 x 4096 unchanged (-0.2%).
+// +0.3%, 4000^3 (float4 guards) +0.7%, 2000 x 2000 x 95 and 4095 x 4096 x 33
+// (scalar guards) +6% and +4%.
 constexpr bool kEarlyStore = true;
 
 template <int BM, int BN, int BK, bool CHECK, bool TB, bool EPI, bool V4 = false, bool KF = false, bool HY = false>
@@ -393,7 +394,9 @@ __global__ __launch_bounds__(kThreads) void sgemm_mfma_kernel(
   constexpr int MPW = (NM - NR) / NW >= 2 ? 2 : 1;         // MFMAs after each store
   static_assert(NM >= NR + MPW * NW, "chunk too small to cover its LDS traffic");
   // ES: the last k-tile is peeled (below) so that C leaves block by block
-  constexpr bool ES = kEarlyStore && !CHECK && !EPI && !HY && G::TN % 2 == 0;
+  // (256-row tiles in every load mode, and the scalar-guarded 128 x 128 tile: the
+  // float4-guarded and unguarded 128 x 128 tiles measured 0.2-1.1% slower with it)
+  constexpr bool ES = kEarlyStore && !EPI && !HY && G::TN % 2 == 0 && (BM == 256 || (CHECK && !V4));
   const int nloop = ES ? nk - 1 : nk;
   for (int t = 0; t < nloop; ++t) {
     const int cur = t & 1;
@@ -463,7 +466,7 @@ __global__ __launch_bounds__(kThreads) void sgemm_mfma_kernel(
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
             const int row = m0 + wm + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-            C[(long long)row * ldc + col] = acc[i][jj][r];
+            if (!CHECK || (row < M && col < N)) C[(long long)row * ldc + col] = acc[i][jj][r];
           }
         }
       };
@@ -475,8 +478,9 @@ __global__ __launch_bounds__(kThreads) void sgemm_mfma_kernel(
         __builtin_amdgcn_sched_barrier(0);
       }
       st_pair(NP - 1);
+      return;
     }
-    return;
+    // K = 0: no k-tile to peel; the epilogue below stores the zero accumulators
   }
 
   // ---- epilogue: value r of lane l is row 8*(r/4) + 4*lh + r%4, col li ----

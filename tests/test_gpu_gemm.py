@@ -53,7 +53,7 @@ def test_golden_vectors(dev, golden):
 
 @pytest.mark.parametrize("m,n,k", [(1, 1, 1), (2, 3, 1), (7, 5, 3), (33, 65, 17), (100, 70, 33),
                                    (128, 128, 32), (256, 128, 64), (129, 257, 100), (512, 384, 160),
-                                   (40, 11008, 64), (300, 4, 4096), (64, 64, 0)])
+                                   (40, 11008, 64), (300, 4, 4096), (64, 64, 0), (256, 256, 0), (2048, 8192, 0), (4095, 4096, 0)])
 def test_shapes_vs_f64(dev, m, n, k):
     _say(f"sgemm m={m} n={n} k={k}")
     rng = O.Lcg(m * 7 + n * 13 + k)
