@@ -660,31 +660,51 @@ const char* tile_name(Tile t, int mode) {
   return names[static_cast<int>(t)][mode];
 }
 
-// ---- split-K for shapes whose tiles fill at most half the CUs ----
+// ---- split-K for shapes whose tiles fill less than one round ----
 // K is cut into S slices of whole k-tiles; the slices run as one batched
 // launch of the tile kernel (slice j: A + j kc, B + j kc rows -- or columns
 // for B given as [n][k] -- into P[j], an m x n partial), then
 // sgemm_splitk_reduce sums the S partials of each output in slice order
-// (deterministic) and applies the epilogue.  The workspace is capped at
-// kSplitWsMax, the same 16 MiB as bch_sgemm_noalloc's fixed scratch, so both
-// entry points take the same path for a shape.  Measured at 1024^3 (64 tiles
-// of 128 x 128): 64.8 us on 64 CUs without the split.
-constexpr size_t kSplitWsMax = (size_t)16 << 20;
+// (deterministic) and applies the epilogue.  S is the modelled fastest:
+// rounds(tiles x S) x k-tiles per slice x the tile's k-tile time (7.4 us for
+// 256 x 256 at full rate, scaled by area / efficiency), plus the partials'
+// round trip ((2S + 1) M N floats at 5 TB/s) and a launch; S divides the
+// k-tile count, leaves at least kSplitMinKt k-tiles per slice, and its
+// partials fit the cap.  The plan is made against a fixed cap, not the
+// workspace at hand, so a shape always rounds the same way through
+// bch_sgemm; bch_sgemm_noalloc plans against its 16 MiB scratch and can take
+// fewer slices (within tolerance of bch_sgemm).  Several rounds of slices
+// can beat one part-filled round: 128 x 11008 x 4096 on 86 tiles of 128 x
+// 128 takes 8 slices in 3 rounds rather than 2 in one.  Measured at 1024^3
+// (64 tiles of 128 x 128): 64.8 us on 64 CUs without the split.
+constexpr size_t kSplitWsMax = (size_t)256 << 20;
+constexpr size_t kSplitWsSmall = (size_t)16 << 20;  // bch_sgemm_noalloc's fixed scratch
 constexpr int kSplitMinKt = 8;  // k-tiles per slice at least
 
-int split_slices(int batch, int m, int n, int k) {
+int split_slices(int batch, int m, int n, int k, size_t cap = kSplitWsMax) {
   if (batch != 1 || k <= 0 || k % kBK != 0) return 1;
   const long long cu = bch::device_cu_count();
   const Tile t = pick_tile(1, m, n);
   const long long tiles = (long long)((m + tile_m(t) - 1) / tile_m(t)) * ((n + tile_n(t) - 1) / tile_n(t));
-  if (2 * tiles > cu) return 1;
+  if (tiles >= cu) return 1;  // whole rounds: the data-parallel tiling or the hybrid plan
+  double eff = 1.0;
+  for (const TileOpt& o : kTileOpts)
+    if (o.t == t) eff = o.eff;
+  const double tk = 7.4 * tile_m(t) * tile_n(t) / 65536.0 / eff;  // us per k-tile of this tile
+  const double mn = (double)m * n * sizeof(float);
   const int nk = k / kBK;
-  int best = 1;
-  for (int sl = 2; sl <= nk; ++sl) {
-    if (tiles * sl > cu || nk / sl < kSplitMinKt || (size_t)sl * m * n * sizeof(float) > kSplitWsMax) break;
-    if (nk % sl == 0) best = sl;
+  double best = nk * tk;
+  int bs = 1;
+  for (int sl = 2; nk / sl >= kSplitMinKt; ++sl) {
+    if (nk % sl != 0) continue;
+    if ((size_t)sl * m * n * sizeof(float) > cap) break;
+    const double cost = (double)((tiles * sl + cu - 1) / cu) * (nk / sl) * tk + (2.0 * sl + 1.0) * mn / 5e6 + 2.0;
+    if (cost < best) {
+      best = cost;
+      bs = sl;
+    }
   }
-  return best;
+  return bs;
 }
 
 // C[m][n] = act(sum over j < S of P[j][m][n] (+ bias[n])); V: four columns per thread (n % 4 == 0,
@@ -901,10 +921,10 @@ const char* sgemm_kernel_name(int m, int n, int k) {
   return tile_name(t, !check ? 0 : v4 ? 1 : 2);
 }
 
-// The tile path's scratch: split-K partials (required), or the hybrid plan's (optional:
-// without them the data-parallel tiling runs).
+// The tile path's scratch: split-K partials, or the hybrid plan's.  `optional` false: the
+// plan within bch_sgemm_noalloc's 16 MiB (fewer split slices, no hybrid plan).
 static size_t tile_workspace_bytes(int batch, int m, int n, int k, bool optional) {
-  const int sl = split_slices(batch, m, n, k);
+  const int sl = split_slices(batch, m, n, k, optional ? kSplitWsMax : kSplitWsSmall);
   if (sl > 1) return (size_t)sl * m * n * sizeof(float);
   HybPlan h;
   return optional && hyb_plan(batch, m, n, k, h) ? hyb_bytes(h) : 0;
@@ -944,7 +964,9 @@ hipError_t launch_sgemm_ex(hipStream_t s, bool transb, int batch, int m, int n, 
   if (transb && batch == 1 && sgemm_skinny_nt_applies(m, n, k, A, lda, B, ldb))
     return launch_sgemm_skinny_nt(s, m, n, k, A, lda, B, ldb, C, ldc, ws, ws_bytes, bias, act);
   const Tile t = pick_tile(batch, m, n);
-  const int sl = split_slices(batch, m, n, k);
+  int sl = split_slices(batch, m, n, k);
+  if (sl > 1 && (ws == nullptr || ws_bytes < (size_t)sl * m * n * sizeof(float)))
+    sl = ws == nullptr ? 1 : split_slices(batch, m, n, k, ws_bytes);  // fewer slices within the scratch at hand
   if (sl > 1 && ws != nullptr && ws_bytes >= (size_t)sl * m * n * sizeof(float)) {
     const int kc = k / sl;
     float* P = static_cast<float*>(ws);

@@ -218,16 +218,18 @@ def test_large_tile_paths(dev, m, n, k, kernel):
     assert O.max_rel_err(got[:, cols], a.astype(np.float64) @ b[:, cols].astype(np.float64)) <= TOL
 
 
-SPLIT_K_CASES = [(1024, 1024, 1024), (512, 512, 8192), (128, 11008, 4096), (300, 4, 4096), (64, 4096, 4096),
-                 (200, 1000, 2048)]
+# the last three take several rounds of slices (8 / 4 / 8 slices over 86 / 172 / 86 tiles)
+SPLIT_K_CASES = [(1024, 1024, 1024), (512, 512, 8192), (300, 4, 4096), (64, 4096, 4096), (200, 1000, 2048),
+                 (128, 11008, 4096), (192, 11008, 4096), (48, 11008, 4096)]
 
 
 @pytest.mark.parametrize("m,n,k", SPLIT_K_CASES)
 def test_split_k_vs_f64(dev, m, n, k):
-    """Tiles filling at most half the CUs: K is cut into slices of whole k-tiles, the slices run
-    as one batched launch into the workspace and sgemm_splitk_reduce adds them in slice order.
-    Aligned and ragged (m 300, n 4 and 1000: the float4-guarded tiles), full f64 comparison on
-    sampled rows and every column; repeated calls are bit-identical."""
+    """Tiles filling less than one round: K is cut into slices of whole k-tiles, the slices run
+    as one batched launch (one or several rounds) into the workspace and sgemm_splitk_reduce
+    adds them in slice order.  Aligned and ragged (m 300, 192, 48, n 4 and 1000: the
+    float4-guarded tiles), full f64 comparison on sampled rows and every column; repeated
+    calls are bit-identical."""
     name = dev._lib.bch_sgemm_kernel_name(m, n, k).decode()
     assert name.endswith("+sgemm_splitk_reduce"), name
     _say(f"sgemm split-k m={m} n={n} k={k} ({name})")

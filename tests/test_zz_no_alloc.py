@@ -70,6 +70,18 @@ def test_noalloc_takes_whole_tiles_where_the_hybrid_does_not_fit(dev):
         assert O.max_rel_err(got[rows], O.matmul_f64(a, b, rows=rows)) <= TOL
 
 
+def test_noalloc_takes_fewer_slices_where_the_split_does_not_fit(dev):
+    """128 x 11008 x 4096 splits K 8 ways through bch_sgemm (45 MB of partials, more than the
+    fixed scratch); the no-alloc call plans within the scratch (2 slices), then a smaller split
+    shape.  Each within tolerance of bch_sgemm and of f64."""
+    for i, (m, n, k) in enumerate(((128, 11008, 4096), (64, 4096, 4096))):
+        _say(f"sgemm_noalloc call {i}: m={m} n={n} k={k} (bch_sgemm: {dev._lib.bch_sgemm_kernel_name(m, n, k).decode()})")
+        got, want, a, b = _both(dev, m, n, k, 8000 + i)
+        assert O.max_rel_err(got, want.astype(np.float64)) <= TOL
+        rows = [0, 1, m // 2, m - 1]
+        assert O.max_rel_err(got[rows], O.matmul_f64(a, b, rows=rows)) <= TOL
+
+
 def test_noalloc_rejects_what_does_not_fit(dev):
     """m = 32, n = 262144: the split-k partials exceed the fixed 16 MiB, so
     the call fails before any launch, with the sizes in the message."""
