@@ -134,7 +134,7 @@ hipError_t launch_sgemm_ex(hipStream_t s, bool transb, int batch, int m,
                            float* C, int ldc, long long sC, void* ws,
                            size_t ws_bytes);
 
-// Skinny (m <= 32) GEMM: streams B once; split-k partials go to ws; the
+// Skinny (m <= 64; above 32 with K % 4 == 0 and 16-byte aligned A) GEMM: streams B once; split-k partials go to ws; the
 // reduce applies the epilogue (bias nullable, act as above).
 hipError_t launch_sgemm_skinny(hipStream_t s, int m, int n, int k,
                                const float* A, int lda, const float* B,

@@ -892,8 +892,7 @@ hipError_t launch_hyb(int mode, const HybPlan& h, hipStream_t s, int m, int n, i
 namespace bch {
 
 const char* sgemm_kernel_name(int m, int n, int k) {
-  if (m <= 32 && sgemm_skinny_applies(m, n, k, nullptr, k, nullptr, n))
-    return sgemm_skinny_kernel_name(m);
+  if (sgemm_skinny_applies(m, n, k, nullptr, k, nullptr, n)) return sgemm_skinny_kernel_name(m);
   const Tile t = pick_tile(1, m, n);
   // with lda = k and ldb = n, and 16-byte aligned operands
   const bool check = !(m % tile_m(t) == 0 && n % tile_n(t) == 0 && k % kBK == 0 && k % 4 == 0 && n % 4 == 0);
@@ -937,7 +936,9 @@ size_t sgemm_workspace_bytes(int batch, int m, int n, int k) {
 }
 
 size_t sgemm_required_workspace_bytes(int batch, int m, int n, int k) {
-  if (batch == 1 && sgemm_skinny_applies(m, n, k, nullptr, k, nullptr, n))
+  // 32 < m <= 64 takes the tile path where the skinny partials exceed the small scratch
+  if (batch == 1 && sgemm_skinny_applies(m, n, k, nullptr, k, nullptr, n) &&
+      (m <= 32 || sgemm_skinny_workspace_bytes(m, n, k) <= kSplitWsSmall))
     return sgemm_skinny_workspace_bytes(m, n, k);
   return tile_workspace_bytes(batch, m, n, k, false);
 }
@@ -959,7 +960,10 @@ hipError_t launch_sgemm_ex(hipStream_t s, bool transb, int batch, int m, int n, 
                            long long sA, const float* B, int ldb, long long sB, const float* bias, int act,
                            float* C, int ldc, long long sC, void* ws, size_t ws_bytes) {
   if (batch <= 0 || m <= 0 || n <= 0) return hipSuccess;
-  if (!transb && batch == 1 && sgemm_skinny_applies(m, n, k, A, lda, B, ldb))
+  // m <= 32: the skinny kernels always (their partials sized by the caller); 32 < m <= 64:
+  // the 64-row skinny kernel when its partials fit the scratch at hand, else the tiles
+  if (!transb && batch == 1 && sgemm_skinny_applies(m, n, k, A, lda, B, ldb) &&
+      (m <= 32 || (ws != nullptr && ws_bytes >= sgemm_skinny_workspace_bytes(m, n, k))))
     return launch_sgemm_skinny(s, m, n, k, A, lda, B, ldb, C, ldc, ws, ws_bytes, bias, act);
   if (transb && batch == 1 && sgemm_skinny_nt_applies(m, n, k, A, lda, B, ldb))
     return launch_sgemm_skinny_nt(s, m, n, k, A, lda, B, ldb, C, ldc, ws, ws_bytes, bias, act);

@@ -318,7 +318,7 @@ constexpr int kW32Rows = 32;
 constexpr int kW32PF = 1;
 constexpr int kW32Lds = 96 * 1024;  // > half of the CU's 160 KB: one workgroup per CU
 
-template <int PF, bool EDGE>
+template <int PF, bool EDGE, int MB = 1>
 __global__ __launch_bounds__(256, 1) void sgemm_skinny_w32(int M, int N, int K, const float* __restrict__ A, int lda,
                                                            const float* __restrict__ B, int ldb,
                                                            float* __restrict__ P, long long U, int G, int nblk,
@@ -326,7 +326,7 @@ __global__ __launch_bounds__(256, 1) void sgemm_skinny_w32(int M, int N, int K, 
   typedef float f32x16v __attribute__((ext_vector_type(16)));
   extern __shared__ float4 smem4[];
   constexpr int LDR = 128 + 4;
-  float* red = reinterpret_cast<float*>(smem4);  // [2 column halves][32 m][LDR]
+  float* red = reinterpret_cast<float*>(smem4);  // [2 column halves][32 MB m][LDR]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int ch = wave & 1, rs = wave >> 1;
   const int lh = lane >> 5, lm = lane & 31;
@@ -335,10 +335,12 @@ __global__ __launch_bounds__(256, 1) void sgemm_skinny_w32(int M, int N, int K, 
   const int nu = (int)(ue - ub);
   const int g0 = (int)(ub / nblk), t0 = (int)(ub - (long long)g0 * nblk);
   constexpr int NB = PF + 1;
-  const float* arow = A + (long long)(lm < M ? lm : M - 1) * lda;  // rows m >= M compute columns never stored
+  const float* arow[MB];  // row block rb: rows 32 rb + lm; rows m >= M compute columns never stored
+#pragma unroll
+  for (int rb = 0; rb < MB; ++rb) arow[rb] = A + (long long)min(32 * rb + lm, M - 1) * lda;
 
   float4 bv[NB][8];
-  float4 av[NB][2];
+  float4 av[NB][MB][2];
   int lg = g0, lt = t0, lcount = 0;  // load cursor: advanced once per load, held at the last unit
   auto load = [&](int sb) {
     const int col = min(lg * kSkCols + 128 * ch + 4 * lm, N - 4);
@@ -346,16 +348,22 @@ __global__ __launch_bounds__(256, 1) void sgemm_skinny_w32(int M, int N, int K, 
 #pragma unroll
     for (int p = 0; p < 8; ++p)
       bv[sb][p] = bch::load_nt(reinterpret_cast<const float4*>(B + (long long)min(r0 + p, K - 1) * ldb + col));
-    av[sb][0] = *reinterpret_cast<const float4*>(arow + min(r0, K - 4));
-    av[sb][1] = *reinterpret_cast<const float4*>(arow + min(r0 + 4, K - 4));
+#pragma unroll
+    for (int rb = 0; rb < MB; ++rb) {
+      av[sb][rb][0] = *reinterpret_cast<const float4*>(arow[rb] + min(r0, K - 4));
+      av[sb][rb][1] = *reinterpret_cast<const float4*>(arow[rb] + min(r0 + 4, K - 4));
+    }
     if (EDGE) {  // rows past K (last unit when K % 32 != 0): zero both operands
 #pragma unroll
       for (int p = 0; p < 8; ++p)
         if (r0 + p >= K) bv[sb][p] = make_float4(0.f, 0.f, 0.f, 0.f);
-      float* a = reinterpret_cast<float*>(&av[sb][0]);
 #pragma unroll
-      for (int c = 0; c < 8; ++c)
-        if (r0 + c >= K) a[c] = 0.f;
+      for (int rb = 0; rb < MB; ++rb) {
+        float* a = reinterpret_cast<float*>(&av[sb][rb][0]);
+#pragma unroll
+        for (int c = 0; c < 8; ++c)
+          if (r0 + c >= K) a[c] = 0.f;
+      }
     }
     ++lcount;
     lt += lcount < nu ? 1 : 0;
@@ -373,51 +381,69 @@ __global__ __launch_bounds__(256, 1) void sgemm_skinny_w32(int M, int N, int K, 
     __builtin_amdgcn_sched_barrier(0);
   }
 
-  f32x16v acc[4];
+  f32x16v acc[MB][4];
 #pragma unroll
-  for (int c = 0; c < 4; ++c)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) acc[c][r] = 0.f;
-
-  int gcur = g0, tcur = t0;
-  int slot = w - wg_of_unit((long long)g0 * nblk, U, G);
-  // value r of block c: row m = lm, column 4 i + c of the wave's half, i = 8 (r / 4) + 4 lh + r % 4
-  auto flush = [&]() {
-    float* rb = red + ch * 32 * LDR;
-    if (rs == 1) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int i = 8 * (r >> 2) + 4 * lh + (r & 3);
-        *reinterpret_cast<float4*>(rb + lm * LDR + 4 * i) = make_float4(acc[0][r], acc[1][r], acc[2][r], acc[3][r]);
-      }
-    }
-    __syncthreads();
-    if (rs == 0 && lm < M) {
-      float* pt = P + (long long)(gcur * smax + slot) * M * kSkCols + 128 * ch + lm * kSkCols;
-      const int nrem = N - gcur * kSkCols - 128 * ch;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int i = 8 * (r >> 2) + 4 * lh + (r & 3);
-        const float4 o = *reinterpret_cast<const float4*>(rb + lm * LDR + 4 * i);
-        if (4 * i < nrem)
-          *reinterpret_cast<float4*>(pt + 4 * i) =
-              make_float4(acc[0][r] + o.x, acc[1][r] + o.y, acc[2][r] + o.z, acc[3][r] + o.w);
-      }
-    }
-    __syncthreads();
+  for (int rb = 0; rb < MB; ++rb)
 #pragma unroll
     for (int c = 0; c < 4; ++c)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[c][r] = 0.f;
+      for (int r = 0; r < 16; ++r) acc[rb][c][r] = 0.f;
+
+  int gcur = g0, tcur = t0;
+  int slot = w - wg_of_unit((long long)g0 * nblk, U, G);
+  // value r of block c, row block rb: row m = 32 rb + lm, column 4 i + c of the wave's half,
+  // i = 8 (r / 4) + 4 lh + r % 4
+  auto flush = [&]() {
+    float* rbuf = red + ch * 32 * MB * LDR;
+    if (rs == 1) {
+#pragma unroll
+      for (int rb = 0; rb < MB; ++rb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int i = 8 * (r >> 2) + 4 * lh + (r & 3);
+          *reinterpret_cast<float4*>(rbuf + (32 * rb + lm) * LDR + 4 * i) =
+              make_float4(acc[rb][0][r], acc[rb][1][r], acc[rb][2][r], acc[rb][3][r]);
+        }
+    }
+    __syncthreads();
+    if (rs == 0) {
+      const int nrem = N - gcur * kSkCols - 128 * ch;
+#pragma unroll
+      for (int rb = 0; rb < MB; ++rb) {
+        const int m = 32 * rb + lm;
+        if (m < M) {
+          float* pt = P + (long long)(gcur * smax + slot) * M * kSkCols + 128 * ch + m * kSkCols;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int i = 8 * (r >> 2) + 4 * lh + (r & 3);
+            const float4 o = *reinterpret_cast<const float4*>(rbuf + m * LDR + 4 * i);
+            if (4 * i < nrem)
+              *reinterpret_cast<float4*>(pt + 4 * i) =
+                  make_float4(acc[rb][0][r] + o.x, acc[rb][1][r] + o.y, acc[rb][2][r] + o.z, acc[rb][3][r] + o.w);
+          }
+        }
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int rb = 0; rb < MB; ++rb)
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[rb][c][r] = 0.f;
   };
   auto mma = [&](int sb) {
-    const float a8[8] = {av[sb][0].x, av[sb][0].y, av[sb][0].z, av[sb][0].w,
-                         av[sb][1].x, av[sb][1].y, av[sb][1].z, av[sb][1].w};
 #pragma unroll
-    for (int p = 0; p < 8; ++p) {
-      const float b4[4] = {bv[sb][p].x, bv[sb][p].y, bv[sb][p].z, bv[sb][p].w};
+    for (int rb = 0; rb < MB; ++rb) {
+      const float a8[8] = {av[sb][rb][0].x, av[sb][rb][0].y, av[sb][rb][0].z, av[sb][rb][0].w,
+                           av[sb][rb][1].x, av[sb][rb][1].y, av[sb][rb][1].z, av[sb][rb][1].w};
 #pragma unroll
-      for (int c = 0; c < 4; ++c) acc[c] = __builtin_amdgcn_mfma_f32_32x32x2f32(b4[c], a8[p], acc[c], 0, 0, 0);
+      for (int p = 0; p < 8; ++p) {
+        const float b4[4] = {bv[sb][p].x, bv[sb][p].y, bv[sb][p].z, bv[sb][p].w};
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          acc[rb][c] = __builtin_amdgcn_mfma_f32_32x32x2f32(b4[c], a8[p], acc[rb][c], 0, 0, 0);
+      }
     }
   };
   for (int i = 0; i < nu; i += NB) {
@@ -1130,13 +1156,13 @@ hipError_t launch_rows(hipStream_t s, int m, int n, int k, const float* A, int l
   return hipGetLastError();
 }
 
-template <bool EDGE>
+template <bool EDGE, int MB>
 hipError_t launch_w32(hipStream_t s, const W32Plan& p, int m, int n, int k, const float* A, int lda, const float* B,
                       int ldb, float* P) {
-  hipError_t e = bch::ensure_dynamic_lds(reinterpret_cast<const void*>(sgemm_skinny_w32<kW32PF, EDGE>), kW32Lds);
+  hipError_t e = bch::ensure_dynamic_lds(reinterpret_cast<const void*>(sgemm_skinny_w32<kW32PF, EDGE, MB>), kW32Lds);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((sgemm_skinny_w32<kW32PF, EDGE>), dim3(p.G), dim3(256), kW32Lds, s, m, n, k, A, lda, B, ldb, P,
-                     p.U, p.G, p.nblk, p.smax);
+  hipLaunchKernelGGL((sgemm_skinny_w32<kW32PF, EDGE, MB>), dim3(p.G), dim3(256), kW32Lds, s, m, n, k, A, lda, B,
+                     ldb, P, p.U, p.G, p.nblk, p.smax);
   return hipGetLastError();
 }
 
@@ -1224,6 +1250,7 @@ size_t sgemm_skinny_workspace_bytes(int m, int n, int k) {
   // the largest of the MFMA paths' needs (which one runs depends on A's alignment)
   size_t bytes = 0;
   for (const bool areg : {false, true}) {
+    if (m > 32) break;  // 32 < m <= 64: the 64-row w32 kernel only
     const SkPlan p = sk_plan(m, n, k, areg);
     const size_t b1 = sizeof(float) * (size_t)p.cg * (size_t)p.smax * (size_t)m * kSkCols;
     if (b1 > bytes) bytes = b1;
@@ -1237,16 +1264,16 @@ size_t sgemm_skinny_workspace_bytes(int m, int n, int k) {
 }
 
 bool sgemm_skinny_applies(int m, int n, int k, const float* A, int lda, const float* B, int ldb) {
-  (void)A;
-  (void)lda;
-  if (m < 1 || m > 32 || n < 4 || k < 1) return false;
+  if (m < 1 || m > 64 || n < 4 || k < 1) return false;
   if (n % 4 != 0 || ldb % 4 != 0) return false;
+  if (m > 32 && !use_w32(m, k, A, lda)) return false;  // 32 < m <= 64: the 64-row w32 kernel only
   if (B && (reinterpret_cast<uintptr_t>(B) & 15) != 0) return false;
   return true;
 }
 
 const char* sgemm_skinny_kernel_name(int m) {
   if (use_fma(m)) return "sgemm_skinny_fma";
+  if (m > 32) return "sgemm_skinny_w32<2>";  // two 32-row blocks per unit
   if (m > 16) return "sgemm_skinny_w32";  // with K % 4 == 0 and aligned A, as at the configs
   return sk_mb(m) == 1 ? "sgemm_skinny_sk<1>" : "sgemm_skinny_sk<2>";
 }
@@ -1274,8 +1301,10 @@ hipError_t launch_sgemm_skinny(hipStream_t s, int m, int n, int k, const float* 
   }
   if (use_w32(m, k, A, lda)) {
     const W32Plan q = w32_plan(n, k);
-    hipError_t e = k % kW32Rows == 0 ? launch_w32<false>(s, q, m, n, k, A, lda, B, ldb, P)
-                                     : launch_w32<true>(s, q, m, n, k, A, lda, B, ldb, P);
+    hipError_t e = m > 32 ? (k % kW32Rows == 0 ? launch_w32<false, 2>(s, q, m, n, k, A, lda, B, ldb, P)
+                                               : launch_w32<true, 2>(s, q, m, n, k, A, lda, B, ldb, P))
+                          : (k % kW32Rows == 0 ? launch_w32<false, 1>(s, q, m, n, k, A, lda, B, ldb, P)
+                                               : launch_w32<true, 1>(s, q, m, n, k, A, lda, B, ldb, P));
     if (e != hipSuccess) return e;
     return launch_sk_reduce(s, m, n, P, q.U, q.G, q.nblk, q.smax, C, ldc, bias, act, kSkCols);
   }

@@ -99,7 +99,7 @@ def test_skinny_ragged(dev, m, n, k):
     assert O.max_rel_err(_mm(dev, a, b), O.matmul_f64(a, b)) <= TOL
 
 
-@pytest.mark.parametrize("m", [5, 8, 16, 17, 32])
+@pytest.mark.parametrize("m", [5, 8, 16, 17, 32, 48, 64])
 def test_skinny_exact_integers(dev, m):
     """Small-integer inputs make every partial sum exact in f32, so the split-k
     stream-K path must match the int64 product bit for bit (K 4096, N 11008)."""
@@ -146,6 +146,41 @@ def test_skinny_m_over_16_routes(dev, m, n, k, lda_pad, a_off):
     dev.check(dev._lib.bch_sgemm(dev.ctx, m, n, k, C.c_void_p(ta.ptr + 4 * a_off), lda, C.c_void_p(tb.ptr), n,
                                  C.c_void_p(tc.ptr), n), "sgemm")
     assert O.max_rel_err(tc.to_numpy(), O.matmul_f64(a, b)) <= TOL
+
+
+@pytest.mark.parametrize("m,n,k,lda_pad,a_off,skinny", [
+    (33, 11008, 4096, 0, 0, True),   # the config's K and N, one row into the second block
+    (48, 11008, 4096, 0, 0, True),
+    (64, 11008, 4096, 0, 0, True),
+    (40, 100, 36, 0, 0, True),       # ragged last column group, K % 32 != 0
+    (64, 8, 4096, 0, 0, True),       # fewer units than CUs
+    (50, 520, 68, 4, 0, True),       # lda = k + 4 (still a multiple of 4)
+    (64, 512, 640, 1, 0, False),     # lda % 4 != 0: the tiles
+    (45, 256, 64, 0, 1, False),      # A misaligned by one float: the tiles
+])
+def test_skinny_64_rows(dev, m, n, k, lda_pad, a_off, skinny):
+    """32 < m <= 64: the 32x32x2 stream-K kernel with two 32-row blocks per streamed unit of B
+    (aligned A, K % 4 == 0), else the tile path; called through the C ABI with an explicit lda."""
+    if lda_pad == 0 and a_off == 0:
+        name = dev._lib.bch_sgemm_kernel_name(m, n, k).decode()
+        assert (name == "sgemm_skinny_w32<2>") == skinny, name
+    _say(f"skinny 64-row m={m} n={n} k={k} lda=k+{lda_pad} a_off={a_off}")
+    rng = O.Lcg(m * 3 + n + k)
+    a = rng.normal((m, k))
+    b = rng.normal((k, n), 0.0, 0.02)
+    lda = k + lda_pad
+    a_buf = np.zeros(a_off + m * lda, dtype=np.float32)
+    a_buf[a_off:].reshape(m, lda)[:, :k] = a
+    ta = Tensor.from_data(a_buf, [a_buf.size], dev)
+    tb = Tensor.from_data(b, [k, n], dev)
+    tc = Tensor.empty([m, n], dev)
+    call = lambda: dev._lib.bch_sgemm(dev.ctx, m, n, k, C.c_void_p(ta.ptr + 4 * a_off), lda, C.c_void_p(tb.ptr), n,
+                                      C.c_void_p(tc.ptr), n)
+    dev.check(call(), "sgemm")
+    got = tc.to_numpy()
+    assert O.max_rel_err(got, O.matmul_f64(a, b)) <= TOL
+    dev.check(call(), "sgemm")
+    assert np.array_equal(tc.to_numpy(), got), "not deterministic"
 
 
 def test_skinny_repeated_calls_and_unaligned_a(dev):
@@ -218,16 +253,16 @@ def test_large_tile_paths(dev, m, n, k, kernel):
     assert O.max_rel_err(got[:, cols], a.astype(np.float64) @ b[:, cols].astype(np.float64)) <= TOL
 
 
-# the last three take several rounds of slices (8 / 4 / 8 slices over 86 / 172 / 86 tiles)
-SPLIT_K_CASES = [(1024, 1024, 1024), (512, 512, 8192), (300, 4, 4096), (64, 4096, 4096), (200, 1000, 2048),
-                 (128, 11008, 4096), (192, 11008, 4096), (48, 11008, 4096)]
+# the last three take several rounds of slices over 86 / 172 / 86 tiles
+SPLIT_K_CASES = [(1024, 1024, 1024), (512, 512, 8192), (300, 4, 4096), (96, 4096, 4096), (200, 1000, 2048),
+                 (128, 11008, 4096), (192, 11008, 4096), (96, 11008, 4096)]
 
 
 @pytest.mark.parametrize("m,n,k", SPLIT_K_CASES)
 def test_split_k_vs_f64(dev, m, n, k):
     """Tiles filling less than one round: K is cut into slices of whole k-tiles, the slices run
     as one batched launch (one or several rounds) into the workspace and sgemm_splitk_reduce
-    adds them in slice order.  Aligned and ragged (m 300, 192, 48, n 4 and 1000: the
+    adds them in slice order.  Aligned and ragged (m 300, 192, 96, n 4 and 1000: the
     float4-guarded tiles), full f64 comparison on sampled rows and every column; repeated
     calls are bit-identical."""
     name = dev._lib.bch_sgemm_kernel_name(m, n, k).decode()

@@ -45,7 +45,7 @@ def _both(dev, m, n, k, seed):
     [(1, 11008, 4096), (20, 1000, 300)],
     [(256, 512, 384), (32, 256, 64)],
     # split-K (slices in the scratch, then the reduce), then a smaller split
-    [(1024, 1024, 1024), (64, 1024, 2048)],
+    [(1024, 1024, 1024), (96, 1024, 2048)],
     # the hybrid plan (16 MiB and 8.5 MiB of tail partials in the scratch)
     [(3072, 3072, 1024), (2304, 2304, 1024)],
 ])
@@ -74,9 +74,21 @@ def test_noalloc_takes_fewer_slices_where_the_split_does_not_fit(dev):
     """128 x 11008 x 4096 splits K 8 ways through bch_sgemm (45 MB of partials, more than the
     fixed scratch); the no-alloc call plans within the scratch (2 slices), then a smaller split
     shape.  Each within tolerance of bch_sgemm and of f64."""
-    for i, (m, n, k) in enumerate(((128, 11008, 4096), (64, 4096, 4096))):
+    for i, (m, n, k) in enumerate(((128, 11008, 4096), (96, 4096, 4096))):
         _say(f"sgemm_noalloc call {i}: m={m} n={n} k={k} (bch_sgemm: {dev._lib.bch_sgemm_kernel_name(m, n, k).decode()})")
         got, want, a, b = _both(dev, m, n, k, 8000 + i)
+        assert O.max_rel_err(got, want.astype(np.float64)) <= TOL
+        rows = [0, 1, m // 2, m - 1]
+        assert O.max_rel_err(got[rows], O.matmul_f64(a, b, rows=rows)) <= TOL
+
+
+def test_noalloc_takes_the_tiles_where_64_row_skinny_partials_do_not_fit(dev):
+    """64 x 11008 x 4096 runs the 64-row skinny kernel through bch_sgemm (about 20 MB of split-k
+    partials, more than the fixed scratch); the no-alloc call takes the tile path, then a smaller
+    64-row skinny shape whose partials fit.  Each within tolerance of bch_sgemm and of f64."""
+    for i, (m, n, k) in enumerate(((64, 11008, 4096), (48, 4096, 1024))):
+        _say(f"sgemm_noalloc call {i}: m={m} n={n} k={k} (bch_sgemm: {dev._lib.bch_sgemm_kernel_name(m, n, k).decode()})")
+        got, want, a, b = _both(dev, m, n, k, 9000 + i)
         assert O.max_rel_err(got, want.astype(np.float64)) <= TOL
         rows = [0, 1, m // 2, m - 1]
         assert O.max_rel_err(got[rows], O.matmul_f64(a, b, rows=rows)) <= TOL
