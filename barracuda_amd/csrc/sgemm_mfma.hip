@@ -887,6 +887,14 @@ hipError_t launch_hyb(int mode, const HybPlan& h, hipStream_t s, int m, int n, i
                                  : launch_tail_reduce<128, 128>(s, m, n, h, P, C, ldc, bias, act);
 }
 
+// [n][k] weights with 32 < m <= 64 and n >= 8192: two passes of the m <= 32 path.  Same box,
+// two runs each, against the tile path (bias + ReLU): 33 / 48 / 64 x 11008 x 4096 99.5 / 100.9
+// / 103.0 -> 70.7 / 76.0 / 83.0 us; at n = 4096 the tiles fill the CUs and stay ahead (48 x 4096
+// x 4096 40.0 against 44.1 us, 64 x 4096 x 11008 91.5 against 93.6).
+bool nt_two_pass(int m, int n, int k, const float* A, int lda, const float* B, int ldb) {
+  return m > 32 && m <= 64 && n >= 8192 && bch::sgemm_skinny_nt_applies(32, n, k, A, lda, B, ldb);
+}
+
 }  // namespace
 
 namespace bch {
@@ -947,6 +955,8 @@ size_t sgemm_ex_workspace_bytes(bool transb, int batch, int m, int n, int k, int
   if (!transb) return sgemm_workspace_bytes(batch, m, n, k);
   if (batch == 1 && sgemm_skinny_nt_applies(m, n, k, nullptr, lda, nullptr, ldb))
     return sgemm_skinny_nt_workspace_bytes(m, n, k);
+  if (batch == 1 && nt_two_pass(m, n, k, nullptr, lda, nullptr, ldb))
+    return std::max(sgemm_skinny_nt_workspace_bytes(32, n, k), sgemm_skinny_nt_workspace_bytes(m - 32, n, k));
   return tile_workspace_bytes(batch, m, n, k, true);
 }
 
@@ -967,6 +977,14 @@ hipError_t launch_sgemm_ex(hipStream_t s, bool transb, int batch, int m, int n, 
     return launch_sgemm_skinny(s, m, n, k, A, lda, B, ldb, C, ldc, ws, ws_bytes, bias, act);
   if (transb && batch == 1 && sgemm_skinny_nt_applies(m, n, k, A, lda, B, ldb))
     return launch_sgemm_skinny_nt(s, m, n, k, A, lda, B, ldb, C, ldc, ws, ws_bytes, bias, act);
+  // 32 < m <= 64 with [n][k] weights: the 32-row kernels twice, on rows 0..31 and 32..m-1 (the
+  // second pass streams the weights again, largely from the Infinity Cache)
+  if (transb && batch == 1 && nt_two_pass(m, n, k, A, lda, B, ldb)) {
+    hipError_t e = launch_sgemm_skinny_nt(s, 32, n, k, A, lda, B, ldb, C, ldc, ws, ws_bytes, bias, act);
+    if (e != hipSuccess) return e;
+    return launch_sgemm_skinny_nt(s, m - 32, n, k, A + 32LL * lda, lda, B, ldb, C + 32LL * ldc, ldc, ws, ws_bytes,
+                                  bias, act);
+  }
   const Tile t = pick_tile(batch, m, n);
   int sl = split_slices(batch, m, n, k);
   if (sl > 1 && (ws == nullptr || ws_bytes < (size_t)sl * m * n * sizeof(float)))

@@ -66,9 +66,12 @@ def test_sgemm_ex_vs_f64(dev, m, n, k, transb):
 
 
 @pytest.mark.parametrize("m,n,k", [(1, 11008, 4096), (8, 4096, 4096), (32, 1024, 4096), (5, 300, 100), (17, 77, 36),
-                                   (16, 129, 68), (32, 4, 4), (2, 200, 1028)])
+                                   (16, 129, 68), (32, 4, 4), (2, 200, 1028), (33, 11008, 4096), (64, 8200, 1000),
+                                   (40, 9000, 4096)])
 def test_sgemm_ex_transposed_decode_shapes(dev, m, n, k):
-    """m <= 32 with [n][k] weights: the weight-row-streaming kernels, bias + ReLU in their epilogue."""
+    """m <= 32 with [n][k] weights: the weight-row-streaming kernels, bias + ReLU in their epilogue;
+    32 < m <= 64 at n >= 8192: the same kernels twice, on rows 0..31 and 32..m-1 (the second pass
+    on the whole-row kernel for 33 and 40)."""
     _say(f"sgemm_ex transposed decode m={m} n={n} k={k}")
     rng = O.Lcg(m * 11 + n + k)
     x = rng.normal((m, k))
