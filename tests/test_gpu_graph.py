@@ -2,12 +2,12 @@
 
 Captured: the decode linear layer with [out, in] weights (the ring kernel, whose
 split-k blocks are combined in the kernel through epoch flags that every launch
-resets), the skinny GEMM (main kernel + reduce), the tile GEMM's hybrid plan (whole
-tiles and k-slices in one launch + reduce) and its split-K (slices into the workspace +
-reduce), row softmax and attention.  The
-graph is replayed several times with the program's own eager calls (which reuse the
-same workspace and flags) and synchronisations between the replays; every replay
-must reproduce the eager results bit for bit.
+resets; at m = 48 in two passes), the skinny GEMM (main kernel + reduce; the one-
+and two-block kernels), the tile GEMM's hybrid plan (whole tiles and k-slices in
+one launch + reduce) and its split-K (slices into the workspace + reduce), row
+softmax and attention.  The graph is replayed several times with the program's
+own eager calls (which reuse the same workspace and flags) and synchronisations
+between the replays; every replay must reproduce the eager results bit for bit.
 """
 from __future__ import annotations
 
@@ -58,18 +58,18 @@ def test_graph_replays_match_eager(dev):
 
     rng = O.Lcg(2024)
     calls = []  # (name, zero-arg launcher, output tensor)
-    for m, n, k in ((8, 11008, 4096), (32, 11008, 4096), (8, 64, 16384)):
+    for m, n, k in ((8, 11008, 4096), (32, 11008, 4096), (8, 64, 16384), (48, 11008, 4096)):  # 48: two passes
         x, w, b = _up(dev, rng.normal((m, k))), _up(dev, rng.normal((n, k), 0.0, 0.05)), _up(dev, rng.normal((n,)))
         y = Tensor.empty([m, n], dev)
         calls.append((f"linear wT m={m} n={n} k={k}",
                       lambda m=m, n=n, k=k, x=x, w=w, b=b, y=y: lib.bch_sgemm_ex(
                           dev.ctx, 1, m, n, k, C.c_void_p(x.ptr), k, C.c_void_p(w.ptr), k, C.c_void_p(b.ptr),
                           N.BCH_ACT_GELU, C.c_void_p(y.ptr), n), y))
-    m, n, k = 8, 11008, 4096
-    xa, wa = _up(dev, rng.normal((m, k))), _up(dev, rng.normal((k, n), 0.0, 0.02))
-    ya = Tensor.empty([m, n], dev)
-    calls.append(("skinny m=8", lambda: lib.bch_sgemm(dev.ctx, m, n, k, C.c_void_p(xa.ptr), k, C.c_void_p(wa.ptr), n,
-                                                       C.c_void_p(ya.ptr), n), ya))
+    for m, n, k in ((8, 11008, 4096), (48, 11008, 4096)):  # 48: the 64-row skinny kernel
+        xa, wa = _up(dev, rng.normal((m, k))), _up(dev, rng.normal((k, n), 0.0, 0.02))
+        ya = Tensor.empty([m, n], dev)
+        calls.append((f"skinny m={m}", lambda m=m, n=n, k=k, xa=xa, wa=wa, ya=ya: lib.bch_sgemm(
+            dev.ctx, m, n, k, C.c_void_p(xa.ptr), k, C.c_void_p(wa.ptr), n, C.c_void_p(ya.ptr), n), ya))
     for m2, n2, k2 in ((3072, 3072, 1024), (1024, 1024, 1024)):  # hybrid, split-K
         xg, wg = _up(dev, rng.uniform((m2, k2))), _up(dev, rng.uniform((k2, n2)))
         yg = Tensor.empty([m2, n2], dev)
