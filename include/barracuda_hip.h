@@ -117,7 +117,10 @@ bch_status bch_sync(bch_ctx *ctx);
  * matmul_gpu_evolved_f64.wgsl, K2 matmul_cpu_tiled_f64.wgsl, K3
  * matmul_tiled_f64.wgsl) and MatmulTiled::execute (ops/matmul_tiled.rs:
  * 62-122).  Routes m <= 32 (decode shapes) to the skinny HBM-streaming
- * kernel and everything else to the FP32-MFMA tiled kernel. */
+ * kernels, 32 < m <= 64 with K % 4 == 0 and 16-byte aligned A to their
+ * two-block form, and everything else to the FP32-MFMA tiled kernel (split
+ * over k when the tiles fill less than one round of the CUs; whole rounds
+ * plus k-sliced leftover tiles when the last round would be part-filled). */
 bch_status bch_sgemm(bch_ctx *ctx, int m, int n, int k,
                      const float *A, int lda, const float *B, int ldb,
                      float *C, int ldc);
@@ -129,10 +132,15 @@ bch_status bch_sgemm(bch_ctx *ctx, int m, int n, int k,
  * (m <= 32) path's split-k partials go to a fixed 16 MiB device array
  * (one per GPU, held until the process ends) instead of the context's
  * workspace; shapes needing more return BCH_E_UNSUPPORTED (e.g. m = 32 with
- * n above ~65000).  No kernel relies on the array's earlier contents.
+ * n above ~65000).  The tiled kernel's split-k and leftover-tile partials
+ * use the same array where they fit; otherwise the call takes fewer k
+ * slices or whole tiles, as 32 < m <= 64 takes the tiles when its skinny
+ * partials do not fit.  No kernel relies on the array's earlier contents.
  * Every call on one GPU shares that GPU's array, so calls that overlap in
  * time on one GPU (two contexts or streams) race: serialise them.  Results
- * are bit-identical to bch_sgemm's. */
+ * are bit-identical to bch_sgemm's where both calls take the same kernels,
+ * and within the f32 tolerance where this one takes fewer slices or whole
+ * tiles. */
 bch_status bch_sgemm_noalloc(bch_ctx *ctx, int m, int n, int k,
                              const float *A, int lda, const float *B, int ldb,
                              float *C, int ldc);
