@@ -107,7 +107,7 @@ __global__ __launch_bounds__(kThreads) void sgemm_mfma_kernel(
     int M, int N, int K, const float* __restrict__ A, int lda, long long sA,
     const float* __restrict__ B, int ldb, long long sB, float* __restrict__ C,
     int ldc, long long sC, int tiles_m, int tiles_n, const float* __restrict__ bias, int act,
-    int hy_ndp, int hy_r, int hy_kt, float* __restrict__ hy_P) {
+    int hy_ndp, int hy_r, int hy_kt, float* __restrict__ hy_P, long long sAz, long long sBz, long long sCz) {
   using G = Cfg<BM, BN, BK>;
   constexpr int LDK = G::LDK;
   extern __shared__ float4 smem4[];
@@ -153,6 +153,12 @@ __global__ __launch_bounds__(kThreads) void sgemm_mfma_kernel(
   A += bz * sA;
   B += bz * sB;
   C += bz * sC;
+  if (gridDim.z > 1) {  // split over k: blockIdx.z is the slice (its A, B offset and partial)
+    const long long zz = blockIdx.z;
+    A += zz * sAz;
+    B += zz * sBz;
+    C += zz * sCz;
+  }
   if constexpr (HY) {
     if (tail) {  // k-tiles hy_slice * hy_kt .. + hy_kt - 1, as a product of K = hy_kt * BK
       const long long k0 = (long long)hy_slice * hy_kt * BK;
@@ -536,16 +542,17 @@ template <int BM, int BN, int BK, bool CHECK, bool TB, bool EPI, bool V4 = false
 hipError_t launch_tiles(hipStream_t s, int batch, int m, int n, int k,
                         const float* A, int lda, long long sA, const float* B,
                         int ldb, long long sB, float* C, int ldc, long long sC,
-                        const float* bias, int act) {
+                        const float* bias, int act, int nz = 1, long long sAz = 0, long long sBz = 0,
+                        long long sCz = 0) {
   using G = Cfg<BM, BN, BK>;
   const int tm = (m + BM - 1) / BM, tn = (n + BN - 1) / BN;
   const size_t lds = sizeof(float) * G::LDS_FLOATS;
   auto kern = sgemm_mfma_kernel<BM, BN, BK, CHECK, TB, EPI, V4, KF>;
   hipError_t e = bch::ensure_dynamic_lds(reinterpret_cast<const void*>(kern), (int)lds);
   if (e != hipSuccess) return e;
-  if (batch > 65535) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(kern, dim3(tm * tn, batch), dim3(kThreads), lds, s, m, n, k,
-                     A, lda, sA, B, ldb, sB, C, ldc, sC, tm, tn, bias, act, 0, 0, 0, nullptr);
+  if (batch > 65535 || nz > 65535) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(kern, dim3(tm * tn, batch, nz), dim3(kThreads), lds, s, m, n, k,
+                     A, lda, sA, B, ldb, sB, C, ldc, sC, tm, tn, bias, act, 0, 0, 0, nullptr, sAz, sBz, sCz);
   return hipGetLastError();
 }
 
@@ -561,7 +568,7 @@ hipError_t launch_hyb_tiles(hipStream_t s, int m, int n, int k, const float* A, 
   hipError_t e = bch::ensure_dynamic_lds(reinterpret_cast<const void*>(kern), (int)lds);
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(kern, dim3(ndp + r * S), dim3(kThreads), lds, s, m, n, k, A, lda, 0LL, B, ldb, 0LL, C, ldc,
-                     0LL, tm, tn, bias, act, ndp, r, kt, P);
+                     0LL, tm, tn, bias, act, ndp, r, kt, P, 0LL, 0LL, 0LL);
   return hipGetLastError();
 }
 
@@ -621,20 +628,26 @@ bool vec4_ok(bool transb, int m, int n, int k, const float* A, int lda, long lon
          aligned16(A) && aligned16(B) && a_bytes < (1LL << 31) && b_bytes < (1LL << 31);
 }
 
+// k slices in grid.z (the split-K launch): slice z adds z * (sA, sB, sC) to the batch's operands
+struct ZSplit {
+  int nz = 1;
+  long long sA = 0, sB = 0, sC = 0;
+};
+
 template <bool CHECK, bool TB, bool EPI, bool V4, bool KF = false>
 hipError_t launch_tile(Tile t, hipStream_t s, int batch, int m, int n, int k, const float* A, int lda,
                        long long sA, const float* B, int ldb, long long sB, float* C, int ldc, long long sC,
-                       const float* bias, int act) {
+                       const float* bias, int act, const ZSplit& z) {
   switch (t) {
     case Tile::k256x256:
       return launch_tiles<256, 256, kBK, CHECK, TB, EPI, V4, KF>(s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC,
-                                                             bias, act);
+                                                             bias, act, z.nz, z.sA, z.sB, z.sC);
     case Tile::k256x128:
       return launch_tiles<256, 128, kBK, CHECK, TB, EPI, V4, KF>(s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC,
-                                                             bias, act);
+                                                             bias, act, z.nz, z.sA, z.sB, z.sC);
     default:
       return launch_tiles<128, 128, kBK, CHECK, TB, EPI, V4, KF>(s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC,
-                                                             bias, act);
+                                                             bias, act, z.nz, z.sA, z.sB, z.sC);
   }
 }
 
@@ -642,14 +655,15 @@ hipError_t launch_tile(Tile t, hipStream_t s, int batch, int m, int n, int k, co
 template <bool TB, bool EPI>
 hipError_t launch_tile_any(int mode, Tile t, hipStream_t s, int batch, int m, int n, int k, const float* A,
                            int lda, long long sA, const float* B, int ldb, long long sB, float* C, int ldc,
-                           long long sC, const float* bias, int act) {
+                           long long sC, const float* bias, int act, const ZSplit& z = ZSplit{}) {
   if (mode == 0)
-    return launch_tile<false, TB, EPI, false>(t, s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC, bias, act);
+    return launch_tile<false, TB, EPI, false>(t, s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC, bias, act, z);
   if (mode == 1 && k % kBK == 0)
-    return launch_tile<true, TB, EPI, true, true>(t, s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC, bias, act);
+    return launch_tile<true, TB, EPI, true, true>(t, s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC, bias, act,
+                                                  z);
   if (mode == 1)
-    return launch_tile<true, TB, EPI, true>(t, s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC, bias, act);
-  return launch_tile<true, TB, EPI, false>(t, s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC, bias, act);
+    return launch_tile<true, TB, EPI, true>(t, s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC, bias, act, z);
+  return launch_tile<true, TB, EPI, false>(t, s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC, bias, act, z);
 }
 
 const char* tile_name(Tile t, int mode) {
@@ -661,11 +675,13 @@ const char* tile_name(Tile t, int mode) {
 }
 
 // ---- split-K for shapes whose tiles fill less than one round ----
-// K is cut into S slices of whole k-tiles; the slices run as one batched
-// launch of the tile kernel (slice j: A + j kc, B + j kc rows -- or columns
-// for B given as [n][k] -- into P[j], an m x n partial), then
-// sgemm_splitk_reduce sums the S partials of each output in slice order
-// (deterministic) and applies the epilogue.  S is the modelled fastest:
+// K is cut into S slices of whole k-tiles; the slices run as one launch of
+// the tile kernel with the slice in grid.z (batch b, slice j: A + b sA + j kc,
+// B + b sB + j kc rows -- or columns for B given as [n][k] -- into P[b][j],
+// an m x n partial), then sgemm_splitk_reduce sums the S partials of each
+// output in slice order (deterministic) and applies the epilogue.  Batches
+// split the same way when all of their tiles together fill less than a
+// round (4 x 512 x 512 x 4096: 64 tiles).  S is the modelled fastest:
 // rounds(tiles x S) x k-tiles per slice x the tile's k-tile time (7.4 us for
 // 256 x 256 at full rate, scaled by area / efficiency), plus the partials'
 // round trip ((2S + 1) M N floats at 5 TB/s) and a launch; S divides the
@@ -682,22 +698,23 @@ constexpr size_t kSplitWsSmall = (size_t)16 << 20;  // bch_sgemm_noalloc's fixed
 constexpr int kSplitMinKt = 8;  // k-tiles per slice at least
 
 int split_slices(int batch, int m, int n, int k, size_t cap = kSplitWsMax) {
-  if (batch != 1 || k <= 0 || k % kBK != 0) return 1;
+  if (batch < 1 || k <= 0 || k % kBK != 0) return 1;
   const long long cu = bch::device_cu_count();
-  const Tile t = pick_tile(1, m, n);
-  const long long tiles = (long long)((m + tile_m(t) - 1) / tile_m(t)) * ((n + tile_n(t) - 1) / tile_n(t));
+  const Tile t = pick_tile(batch, m, n);
+  const long long tiles =
+      (long long)batch * ((m + tile_m(t) - 1) / tile_m(t)) * ((n + tile_n(t) - 1) / tile_n(t));
   if (tiles >= cu) return 1;  // whole rounds: the data-parallel tiling or the hybrid plan
   double eff = 1.0;
   for (const TileOpt& o : kTileOpts)
     if (o.t == t) eff = o.eff;
   const double tk = 7.4 * tile_m(t) * tile_n(t) / 65536.0 / eff;  // us per k-tile of this tile
-  const double mn = (double)m * n * sizeof(float);
+  const double mn = (double)batch * m * n * sizeof(float);
   const int nk = k / kBK;
   double best = nk * tk;
   int bs = 1;
   for (int sl = 2; nk / sl >= kSplitMinKt; ++sl) {
     if (nk % sl != 0) continue;
-    if ((size_t)sl * m * n * sizeof(float) > cap) break;
+    if ((size_t)sl * batch * m * n * sizeof(float) > cap) break;
     const double cost = (double)((tiles * sl + cu - 1) / cu) * (nk / sl) * tk + (2.0 * sl + 1.0) * mn / 5e6 + 2.0;
     if (cost < best) {
       best = cost;
@@ -707,23 +724,26 @@ int split_slices(int batch, int m, int n, int k, size_t cap = kSplitWsMax) {
   return bs;
 }
 
-// C[m][n] = act(sum over j < S of P[j][m][n] (+ bias[n])); V: four columns per thread (n % 4 == 0,
-// ldc % 4 == 0, C 16-byte aligned)
+// C[b][m][n] = act(sum over j < S of P[b][j][m][n] (+ bias[n])) for each of `batch` matrices
+// (C[b] at C + b sC); V: four columns per thread (n % 4 == 0, ldc % 4 == 0, C 16-byte aligned)
 template <bool V>
-__global__ __launch_bounds__(256) void sgemm_splitk_reduce(int M, int N, int S, const float* __restrict__ P,
-                                                           float* __restrict__ C, int ldc,
+__global__ __launch_bounds__(256) void sgemm_splitk_reduce(int M, int N, int S, int batch, const float* __restrict__ P,
+                                                           float* __restrict__ C, int ldc, long long sC,
                                                            const float* __restrict__ bias, int act) {
   const long long per = (long long)M * N;
   const int w = V ? 4 : 1;
-  const long long total = per / w;
+  const long long total = per * batch / w;
   for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < total;
        i += (long long)gridDim.x * blockDim.x) {
-    const long long e = i * w;
+    const long long ea = i * w;
+    const long long b = ea / per, e = ea - b * per;
     const int m = (int)(e / N), n = (int)(e - (long long)m * N);
+    const float* pb = P + b * S * per + e;
+    float* cb = C + b * sC + (long long)m * ldc + n;
     if constexpr (V) {
-      float4 acc = *reinterpret_cast<const float4*>(P + e);
+      float4 acc = *reinterpret_cast<const float4*>(pb);
       for (int j = 1; j < S; ++j) {
-        const float4 x = *reinterpret_cast<const float4*>(P + j * per + e);
+        const float4 x = *reinterpret_cast<const float4*>(pb + j * per);
         acc.x += x.x;
         acc.y += x.y;
         acc.z += x.z;
@@ -737,12 +757,12 @@ __global__ __launch_bounds__(256) void sgemm_splitk_reduce(int M, int N, int S, 
       }
       acc = make_float4(bch::activate(acc.x, act), bch::activate(acc.y, act), bch::activate(acc.z, act),
                         bch::activate(acc.w, act));
-      *reinterpret_cast<float4*>(C + (long long)m * ldc + n) = acc;
+      *reinterpret_cast<float4*>(cb) = acc;
     } else {
-      float acc = P[e];
-      for (int j = 1; j < S; ++j) acc += P[j * per + e];
+      float acc = pb[0];
+      for (int j = 1; j < S; ++j) acc += pb[j * per];
       if (bias) acc += bias[n];
-      C[(long long)m * ldc + n] = bch::activate(acc, act);
+      *cb = bch::activate(acc, act);
     }
   }
 }
@@ -932,7 +952,7 @@ const char* sgemm_kernel_name(int m, int n, int k) {
 // plan within bch_sgemm_noalloc's 16 MiB (fewer split slices, no hybrid plan).
 static size_t tile_workspace_bytes(int batch, int m, int n, int k, bool optional) {
   const int sl = split_slices(batch, m, n, k, optional ? kSplitWsMax : kSplitWsSmall);
-  if (sl > 1) return (size_t)sl * m * n * sizeof(float);
+  if (sl > 1) return (size_t)sl * batch * m * n * sizeof(float);
   HybPlan h;
   return optional && hyb_plan(batch, m, n, k, h) ? hyb_bytes(h) : 0;
 }
@@ -987,27 +1007,39 @@ hipError_t launch_sgemm_ex(hipStream_t s, bool transb, int batch, int m, int n, 
   }
   const Tile t = pick_tile(batch, m, n);
   int sl = split_slices(batch, m, n, k);
-  if (sl > 1 && (ws == nullptr || ws_bytes < (size_t)sl * m * n * sizeof(float)))
+  const size_t pbytes = (size_t)batch * m * n * sizeof(float);  // one slice's partials, every batch
+  if (sl > 1 && (ws == nullptr || ws_bytes < (size_t)sl * pbytes))
     sl = ws == nullptr ? 1 : split_slices(batch, m, n, k, ws_bytes);  // fewer slices within the scratch at hand
-  if (sl > 1 && ws != nullptr && ws_bytes >= (size_t)sl * m * n * sizeof(float)) {
+  if (sl > 1 && ws != nullptr && ws_bytes >= (size_t)sl * pbytes) {
+    // batch b, slice j (grid.z): A + b sA + j kc, B + b sB + j kc rows (columns for [n][k]),
+    // into P[b][j] (m x n)
     const int kc = k / sl;
     float* P = static_cast<float*>(ws);
-    const long long sAj = kc, sBj = transb ? (long long)kc : (long long)kc * ldb, sCj = (long long)m * n;
-    const int mode = fast_ok(t, m, n, kc, A, lda, sAj, B, ldb, sBj)               ? 0
-                     : vec4_ok(transb, m, n, kc, A, lda, sAj, B, ldb, sBj) ? 1
-                                                                             : 2;
-    hipError_t e = transb ? launch_tile_any<true, false>(mode, t, s, sl, m, n, kc, A, lda, sAj, B, ldb, sBj, P, n,
-                                                         sCj, nullptr, 0)
-                          : launch_tile_any<false, false>(mode, t, s, sl, m, n, kc, A, lda, sAj, B, ldb, sBj, P, n,
-                                                          sCj, nullptr, 0);
+    const long long per = (long long)m * n;
+    ZSplit z;
+    z.nz = sl;
+    z.sA = kc;
+    z.sB = transb ? (long long)kc : (long long)kc * ldb;
+    z.sC = per;
+    // the slice offsets (kc a multiple of 32, times ldb) keep the batch strides' alignment
+    const int mode = fast_ok(t, m, n, kc, A, lda, sA, B, ldb, sB)               ? 0
+                     : vec4_ok(transb, m, n, kc, A, lda, sA, B, ldb, sB) ? 1
+                                                                           : 2;
+    hipError_t e = transb ? launch_tile_any<true, false>(mode, t, s, batch, m, n, kc, A, lda, sA, B, ldb, sB, P, n,
+                                                         sl * per, nullptr, 0, z)
+                          : launch_tile_any<false, false>(mode, t, s, batch, m, n, kc, A, lda, sA, B, ldb, sB, P, n,
+                                                          sl * per, nullptr, 0, z);
     if (e != hipSuccess) return e;
-    const bool v = n % 4 == 0 && ldc % 4 == 0 && aligned16(C) && (bias == nullptr || aligned16(bias));
-    const long long work = (long long)m * n / (v ? 4 : 1);
+    const bool v = n % 4 == 0 && ldc % 4 == 0 && aligned16(C) && (batch == 1 || sC % 4 == 0) &&
+                   (bias == nullptr || aligned16(bias));
+    const long long work = per * batch / (v ? 4 : 1);
     const int blocks = (int)std::min<long long>((work + 255) / 256, 4096);
     if (v)
-      hipLaunchKernelGGL(sgemm_splitk_reduce<true>, dim3(blocks), dim3(256), 0, s, m, n, sl, P, C, ldc, bias, act);
+      hipLaunchKernelGGL(sgemm_splitk_reduce<true>, dim3(blocks), dim3(256), 0, s, m, n, sl, batch, P, C, ldc, sC,
+                         bias, act);
     else
-      hipLaunchKernelGGL(sgemm_splitk_reduce<false>, dim3(blocks), dim3(256), 0, s, m, n, sl, P, C, ldc, bias, act);
+      hipLaunchKernelGGL(sgemm_splitk_reduce<false>, dim3(blocks), dim3(256), 0, s, m, n, sl, batch, P, C, ldc, sC,
+                         bias, act);
     return hipGetLastError();
   }
   const bool epi = bias != nullptr || act != 0;

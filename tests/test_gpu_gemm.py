@@ -365,14 +365,34 @@ def test_config_batched_16x1024(dev):
         cols = [t * 256 + (bi * 53 + t * 29) % 256 for t in range(4)]
         errc = O.max_rel_err(got[bi][:, cols], ab.astype(np.float64) @ bb[:, cols].astype(np.float64))
         assert err <= TOL and errc <= TOL, (bi, rows, cols, err, errc)
-    # batches are independent: a two-batch call on batches 3 and 5 (the same kernel; a single
-    # 1024^3 GEMM takes split-K, which rounds differently) reproduces them bit for bit
-    a2, b2 = np.ascontiguousarray(a[[3, 5]]), np.ascontiguousarray(b[[3, 5]])
-    two = Tensor.from_data(a2, [2, 1024, 1024], dev).batch_matmul(Tensor.from_data(b2, [2, 1024, 1024], dev))
-    two = two.to_numpy()
-    assert np.array_equal(two[0], got[3]) and np.array_equal(two[1], got[5])
+    # batches are independent: the 16 batches in reverse order (the same kernel; fewer batches
+    # split over k, which rounds differently) reproduce them bit for bit
+    a2, b2 = np.ascontiguousarray(a[::-1]), np.ascontiguousarray(b[::-1])
+    rev = Tensor.from_data(a2, [16, 1024, 1024], dev).batch_matmul(Tensor.from_data(b2, [16, 1024, 1024], dev))
+    rev = rev.to_numpy()
+    assert all(np.array_equal(rev[15 - i], got[i]) for i in range(16))
     single = _mm(dev, np.ascontiguousarray(a[3]), np.ascontiguousarray(b[3]))
     assert O.max_rel_err(single, got[3].astype(np.float64)) <= TOL
+
+
+@pytest.mark.parametrize("batch,m,n,k", [(2, 1024, 1024, 1024), (4, 512, 512, 4096), (8, 256, 256, 8192),
+                                         (3, 300, 200, 2048), (5, 130, 260, 1024)])
+def test_batched_split_k(dev, batch, m, n, k):
+    """Batches whose tiles together fill less than one round of the CUs split over k too
+    (slices in grid.z, partials per batch and slice, a batch-aware reduce); aligned and ragged
+    shapes, each batch against f64 on sampled rows and every column; repeated calls are
+    bit-identical."""
+    _say(f"batched split-k {batch}x{m}x{n}x{k}")
+    rng = O.Lcg(batch * 1000 + m + n + k)
+    a = rng.uniform((batch, m, k))
+    b = rng.uniform((batch, k, n))
+    ta, tb = Tensor.from_data(a, [batch, m, k], dev), Tensor.from_data(b, [batch, k, n], dev)
+    got = ta.batch_matmul(tb).to_numpy()
+    for bi in range(batch):
+        rows = sorted({0, m - 1, m // 2, (bi * 37) % m})
+        assert O.max_rel_err(got[bi][rows], O.matmul_f64(np.ascontiguousarray(a[bi]), np.ascontiguousarray(b[bi]),
+                                                         rows=rows)) <= TOL, bi
+    assert np.array_equal(ta.batch_matmul(tb).to_numpy(), got), "not deterministic"
 
 
 def test_batched_ragged(dev):
