@@ -20,8 +20,11 @@
 //     the whole chip busy instead of one CU per row.
 //   * anything else: one workgroup per row, an online (max, sum) pass and a
 //     second read that writes; scalar loads, any cols.
-//   * axis != last: one thread per (outer, inner) slice, coalesced across
-//     inner, online (max, sum) then a writing pass.
+//   * axis != last: each [axis][inner] slice is a column softmax; workgroups
+//     take 64-column strips (or whole rows when inner < 64) over chunks of
+//     the axis, merge their threads' online states in LDS, and write; long
+//     axes on few strips are cut into chunks whose states a second kernel
+//     merges before writing.
 // exp(x) is 2^(x log2 e) on v_exp_f32 with the product's rounding error
 // carried as a first-order correction (x*log2e split into p + e exactly with
 // one fma), which keeps it within ~2 ulp of a correctly rounded expf over
@@ -245,19 +248,116 @@ __global__ __launch_bounds__(256) void softmax_split_write(
   }
 }
 
-// Softmax along the middle axis of [outer, axis, inner], thread per slice.
-__global__ __launch_bounds__(256) void softmax_axis_strided(
-    const float* in, float* out, long long outer,
-    long long axis, long long inner) {
-  const long long t = (long long)blockIdx.x * 256 + threadIdx.x;
-  if (t >= outer * inner) return;
-  const long long o = t / inner, i = t % inner;
-  const float* x = in + o * axis * inner + i;
-  float* y = out + o * axis * inner + i;
+// Softmax along the middle axis of [outer, axis, inner]: X[o] = in + o axis inner is an
+// [axis][inner] matrix (inner contiguous) and every column is one softmax.  Workgroup
+// (o, chunk, strip), strip fastest, covers columns strip cw .. strip cw + cw - 1 (cw = 64, or
+// inner when it is smaller) of the chunk's rows; thread (g, c), g < 256 / cw, takes rows
+// g, g + 256 / cw, ... of column c, so each wavefront reads contiguous memory: 64 columns of one
+// row, or 64 / inner whole rows.  The threads' online (max, sum) states meet in LDS and are
+// merged in g order.  ONE: the chunk is the whole axis, and the workgroup goes on to write the
+// column's outputs (read, read, write); otherwise it stores the chunk's state per column, and
+// softmax_cols_write merges a column's chunk states in chunk order before writing its chunk.
+struct ColWg {
+  long long o;
+  int chunk, strip;
+};
+
+__device__ __forceinline__ ColWg col_wg(int strips, int nchunks) {
+  long long wg = blockIdx.x;
+  ColWg r;
+  r.strip = (int)(wg % strips);
+  wg /= strips;
+  r.chunk = (int)(wg % nchunks);
+  r.o = wg / nchunks;
+  return r;
+}
+
+template <bool ONE>
+__global__ __launch_bounds__(256) void softmax_cols(const float* in, float* out, long long axis,
+                                                    long long inner, int cw, int strips, int nchunks,
+                                                    long long rpc, float* __restrict__ part) {
+  __shared__ float sm[256], ss[256];
+  const ColWg w = col_wg(strips, nchunks);
+  const int rgs = 256 / cw;
+  const int g = threadIdx.x / cw, c = threadIdx.x - g * cw;
+  const long long col = (long long)w.strip * cw + c;
+  const bool on = g < rgs && col < inner;
+  const long long r0 = (long long)w.chunk * rpc, r1 = r0 + rpc < axis ? r0 + rpc : axis;
+  const float* x = in + w.o * axis * inner + col;
   float m = -INFINITY, s = 0.0f;
-  for (long long j = 0; j < axis; ++j) online_push(m, s, x[j * inner]);
+  if (on) {
+    long long r = r0 + g;
+    for (; r + 3 * rgs < r1; r += 4 * rgs) {  // four independent loads before the math
+      const float v0 = x[r * inner], v1 = x[(r + rgs) * inner], v2 = x[(r + 2 * rgs) * inner],
+                  v3 = x[(r + 3 * rgs) * inner];
+      online_push(m, s, v0);
+      online_push(m, s, v1);
+      online_push(m, s, v2);
+      online_push(m, s, v3);
+    }
+    for (; r < r1; r += rgs) online_push(m, s, x[r * inner]);
+  }
+  sm[threadIdx.x] = m;
+  ss[threadIdx.x] = s;
+  __syncthreads();
+  if (g == 0 && col < inner) {  // threads 0 .. cw - 1: merge the column's states in g order
+    for (int gg = 1; gg < rgs; ++gg) merge_state(m, s, sm[gg * cw + c], ss[gg * cw + c]);
+    if (ONE) {
+      sm[c] = m;  // slot c is read by no other merging thread (they read slots >= cw)
+      ss[c] = s;
+    } else {
+      const long long p = 2 * (((long long)w.o * nchunks + w.chunk) * inner + col);
+      part[p] = m;
+      part[p + 1] = s;
+    }
+  }
+  if (!ONE) return;
+  __syncthreads();
+  if (!on) return;
+  const float mx = sm[c], inv = 1.0f / ss[c];
+  float* y = out + w.o * axis * inner + col;
+  for (long long r = r0 + g; r < r1; r += rgs) y[r * inner] = exp_f32(x[r * inner] - mx) * inv;
+}
+
+__global__ __launch_bounds__(256) void softmax_cols_write(const float* in, float* out, long long axis,
+                                                          long long inner, int cw, int strips, int nchunks,
+                                                          long long rpc, const float* __restrict__ part) {
+  const ColWg w = col_wg(strips, nchunks);
+  const int rgs = 256 / cw;
+  const int g = threadIdx.x / cw, c = threadIdx.x - g * cw;
+  const long long col = (long long)w.strip * cw + c;
+  if (g >= rgs || col >= inner) return;
+  const float* pc = part + 2 * ((long long)w.o * nchunks * inner + col);
+  float m = -INFINITY, s = 0.0f;
+  for (int k = 0; k < nchunks; ++k) merge_state(m, s, pc[2LL * k * inner], pc[2LL * k * inner + 1]);
   const float inv = 1.0f / s;
-  for (long long j = 0; j < axis; ++j) y[j * inner] = exp_f32(x[j * inner] - m) * inv;
+  const long long r0 = (long long)w.chunk * rpc, r1 = r0 + rpc < axis ? r0 + rpc : axis;
+  const float* x = in + w.o * axis * inner + col;
+  float* y = out + w.o * axis * inner + col;
+  for (long long r = r0 + g; r < r1; r += rgs) y[r * inner] = exp_f32(x[r * inner] - m) * inv;
+}
+
+// Chunking of the middle-axis softmax: enough workgroups for ~4 per CU, at least 256 rows a chunk.
+struct ColPlan {
+  int cw = 1, strips = 1, nchunks = 1;
+  long long rpc = 1;
+};
+
+ColPlan col_plan(long long outer, long long axis, long long inner) {
+  ColPlan p;
+  p.cw = inner >= 64 ? 64 : (int)inner;
+  p.strips = (int)((inner + p.cw - 1) / p.cw);
+  const long long wgs = outer * p.strips;
+  const long long target = 4LL * bch::device_cu_count();
+  long long nc = 1;
+  if (wgs < target) {
+    nc = (target + wgs - 1) / wgs;
+    const long long most = axis / 256 > 1 ? axis / 256 : 1;
+    if (nc > most) nc = most;
+  }
+  p.rpc = (axis + nc - 1) / nc;
+  p.nchunks = (int)((axis + p.rpc - 1) / p.rpc);
+  return p;
 }
 
 int pick_nv(long long cols) {
@@ -316,7 +416,9 @@ size_t softmax_workspace_bytes(long long rows, long long cols) {
 }
 
 size_t softmax_axis_workspace_bytes(long long outer, long long axis, long long inner) {
-  return inner == 1 ? softmax_workspace_bytes(outer, axis) : 0;
+  if (inner == 1) return softmax_workspace_bytes(outer, axis);
+  const ColPlan p = col_plan(outer, axis, inner);
+  return p.nchunks > 1 ? sizeof(float) * 2 * (size_t)outer * p.nchunks * (size_t)inner : 0;
 }
 
 const char* softmax_kernel_name(long long rows, long long cols) {
@@ -378,10 +480,23 @@ hipError_t launch_softmax_axis(hipStream_t s, long long outer, long long axis,
                                void* ws, size_t ws_bytes) {
   if (outer <= 0 || axis <= 0 || inner <= 0) return hipSuccess;
   if (inner == 1) return launch_softmax_rows(s, outer, axis, in, out, ws, ws_bytes);
-  const long long slices = outer * inner;
-  const long long blocks = (slices + 255) / 256;
+  const ColPlan p = col_plan(outer, axis, inner);
+  const long long blocks = outer * p.nchunks * p.strips;
   if (blocks > 0x7fffffffLL) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(softmax_axis_strided, dim3((unsigned)blocks), dim3(256), 0, s, in, out, outer, axis, inner);
+  if (p.nchunks == 1) {
+    hipLaunchKernelGGL(softmax_cols<true>, dim3((unsigned)blocks), dim3(256), 0, s, in, out, axis, inner, p.cw,
+                       p.strips, 1, p.rpc, nullptr);
+    return hipGetLastError();
+  }
+  const size_t need = sizeof(float) * 2 * (size_t)outer * p.nchunks * (size_t)inner;
+  if (ws == nullptr || ws_bytes < need) return hipErrorInvalidValue;
+  float* part = static_cast<float*>(ws);
+  hipLaunchKernelGGL(softmax_cols<false>, dim3((unsigned)blocks), dim3(256), 0, s, in, out, axis, inner, p.cw,
+                     p.strips, p.nchunks, p.rpc, part);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(softmax_cols_write, dim3((unsigned)blocks), dim3(256), 0, s, in, out, axis, inner, p.cw,
+                     p.strips, p.nchunks, p.rpc, part);
   return hipGetLastError();
 }
 

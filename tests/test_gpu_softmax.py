@@ -92,6 +92,31 @@ def test_axis_and_inplace(dev):
     assert O.max_rel_err(ty.to_numpy(), O.softmax_rows_f64(y)) <= TOL
 
 
+@pytest.mark.parametrize("outer,axis,inner", [
+    (8, 2048, 320),    # 64-column strips, one chunk, ragged last strip
+    (2, 4096, 1000),
+    (3000, 512, 5),    # whole rows per wavefront (inner < 64)
+    (1, 300, 3),
+    (7, 1, 9),         # a one-element axis
+    (1, 65536, 96),    # few strips: the axis in chunks, states merged by a second kernel
+    (2, 70000, 2),
+])
+def test_softmax_middle_axis(dev, outer, axis, inner):
+    """softmax_dim over a non-last axis: the column softmax of each [axis][inner] slice, against
+    f64, and in place (in == out) on the same shape."""
+    _say(f"softmax middle axis outer={outer} axis={axis} inner={inner}")
+    x = O.Lcg(outer + axis + inner).normal((outer, axis, inner), 0.0, 3.0)
+    want = np.ascontiguousarray(np.moveaxis(O.softmax_rows_f64(np.ascontiguousarray(np.moveaxis(x, 1, -1))), -1, 1))
+    tx = Tensor.from_data(x, [outer, axis, inner], dev)
+    ty = Tensor.empty([outer, axis, inner], dev)
+    lib = dev._lib
+    dev.check(lib.bch_softmax_axis(dev.ctx, outer, axis, inner, C.c_void_p(tx.ptr), C.c_void_p(ty.ptr)), "axis")
+    got = ty.to_numpy()
+    assert O.max_rel_err(got, want) <= TOL
+    dev.check(lib.bch_softmax_axis(dev.ctx, outer, axis, inner, C.c_void_p(tx.ptr), C.c_void_p(tx.ptr)), "axis")
+    assert np.array_equal(tx.to_numpy(), got), "in place differs"
+
+
 def test_code_object_dispatch(dev):
     """dispatch_binary path: the same row softmax from the prebuilt .hsaco."""
     _say("softmax via bch_launch_code_object")
