@@ -20,11 +20,18 @@
 //     the whole chip busy instead of one CU per row.
 //   * anything else: one workgroup per row, an online (max, sum) pass and a
 //     second read that writes; scalar loads, any cols.
-//   * axis != last: each [axis][inner] slice is a column softmax; workgroups
-//     take 64-column strips (or whole rows when inner < 64) over chunks of
-//     the axis, merge their threads' online states in LDS, and write; long
-//     axes on few strips are cut into chunks whose states a second kernel
-//     merges before writing.
+//   * axis != last: each [axis][inner] slice is a column softmax.  With
+//     inner % 4 == 0 and 16-byte aligned pointers, lanes take float4
+//     columns: 8 lanes a row (a whole 128-byte line) in 512-thread
+//     workgroups, or 4 / 2 / 1 lanes a row in 256-thread ones for narrow
+//     inner, 64 rows a pass.  Where the axis fits in 32 float4 registers a
+//     lane and the strips fill the CUs, the workgroup keeps its whole strip
+//     in registers: read once, max and sum by xor shuffles and LDS, write
+//     once.  Otherwise the axis is cut into chunks: a stats kernel from
+//     registers, then a streaming kernel that merges the chunk states and
+//     writes.  Any other inner: scalar lanes over 64-column strips, online
+//     states merged in LDS.  Block numbers are renumbered so that each XCD
+//     reads a contiguous run of strips.
 // exp(x) is 2^(x log2 e) on v_exp_f32 with the product's rounding error
 // carried as a first-order correction (x*log2e split into p + e exactly with
 // one fma), which keeps it within ~2 ulp of a correctly rounded expf over
@@ -262,8 +269,16 @@ struct ColWg {
   int chunk, strip;
 };
 
+// Workgroups are dispatched to the 8 XCDs round robin (block b to XCD b % 8); renumbering the
+// first gridDim.x & ~7 blocks as (b % 8) * (that / 8) + b / 8 hands each XCD a contiguous run of
+// strips, so the strips that share 128-byte lines of a row are read through the same L2.
+__device__ __forceinline__ long long xcd_block() {
+  const long long b = blockIdx.x, full = (long long)gridDim.x & ~7LL;
+  return b < full ? (b & 7) * (full >> 3) + (b >> 3) : b;
+}
+
 __device__ __forceinline__ ColWg col_wg(int strips, int nchunks) {
-  long long wg = blockIdx.x;
+  long long wg = xcd_block();
   ColWg r;
   r.strip = (int)(wg % strips);
   wg /= strips;
@@ -335,6 +350,199 @@ __global__ __launch_bounds__(256) void softmax_cols_write(const float* in, float
   const float* x = in + w.o * axis * inner + col;
   float* y = out + w.o * axis * inner + col;
   for (long long r = r0 + g; r < r1; r += rgs) y[r * inner] = exp_f32(x[r * inner] - m) * inv;
+}
+
+// Middle-axis softmax with a whole column strip in registers (inner % 4 == 0, 16-byte aligned,
+// axis <= R * 256 / W): workgroup (o, strip) covers float4 columns strip W .. strip W + W - 1;
+// lane (g, c), c < W, holds column strip W + c of rows g, g + 256 / W, ... as R float4, so x is
+// read once and y written once.  A wavefront reads W * 16 bytes of each of 64 / W rows per load.
+// The column's max, then its sum of exp(x - max), meet across the lanes of the column by xor
+// shuffles within the wavefront (lanes l and l ^ kW share c), then across the four wavefronts in
+// LDS in wavefront order.  Rows past the axis load as -inf and add exp(-inf) = 0.
+template <int W, int NW>
+__device__ __forceinline__ float4 col_reduce(float4 a, float4 (*red)[W], bool is_max) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+#pragma unroll
+  for (int off = W; off < 64; off <<= 1) {
+    const float4 b = make_float4(__shfl_xor(a.x, off), __shfl_xor(a.y, off), __shfl_xor(a.z, off),
+                                 __shfl_xor(a.w, off));
+    a = is_max ? make_float4(fmaxf(a.x, b.x), fmaxf(a.y, b.y), fmaxf(a.z, b.z), fmaxf(a.w, b.w))
+               : make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+  }
+  if (lane < W) red[wv][lane] = a;
+  __syncthreads();
+  const int c = lane % W;
+  float4 r = red[0][c];
+#pragma unroll
+  for (int i = 1; i < NW; ++i) {
+    const float4 b = red[i][c];
+    r = is_max ? make_float4(fmaxf(r.x, b.x), fmaxf(r.y, b.y), fmaxf(r.z, b.z), fmaxf(r.w, b.w))
+               : make_float4(r.x + b.x, r.y + b.y, r.z + b.z, r.w + b.w);
+  }
+  return r;
+}
+
+template <int R, int W, int NT, bool STATS>
+__global__ __launch_bounds__(NT) void softmax_cols_reg(const float* in, float* out, long long axis,
+                                                       long long inner4, long long strips, long long nchunks,
+                                                       float4* __restrict__ part, long long plane) {
+  constexpr int kRpp = NT / W, kNW = NT / 64;
+  __shared__ float4 redm[kNW][W], reds[kNW][W];
+  const long long b = xcd_block();
+  const long long t = b / strips, strip = b - t * strips;
+  const long long o = t / nchunks, chunk = t - o * nchunks;
+  const int c = threadIdx.x % W, g = threadIdx.x / W;
+  const long long col4 = strip * W + c;
+  const bool on = col4 < inner4;
+  const long long r0 = chunk * (R * kRpp);
+  const long long r1 = r0 + R * kRpp < axis ? r0 + R * kRpp : axis;
+  const float4* x = reinterpret_cast<const float4*>(in) + o * axis * inner4 + col4;
+  float4* y = reinterpret_cast<float4*>(out) + o * axis * inner4 + col4;
+  const float ninf = -INFINITY;
+  float4 v[R];
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    const long long r = r0 + g + (long long)i * kRpp;
+    v[i] = on && r < r1 ? bch::load_nt(x + r * inner4) : make_float4(ninf, ninf, ninf, ninf);
+  }
+  float4 mx = v[0];
+#pragma unroll
+  for (int i = 1; i < R; ++i)
+    mx = make_float4(fmaxf(mx.x, v[i].x), fmaxf(mx.y, v[i].y), fmaxf(mx.z, v[i].z), fmaxf(mx.w, v[i].w));
+  mx = col_reduce<W, kNW>(mx, redm, true);
+  float4 sm = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    v[i] = make_float4(exp_f32(v[i].x - mx.x), exp_f32(v[i].y - mx.y), exp_f32(v[i].z - mx.z),
+                       exp_f32(v[i].w - mx.w));
+    sm = make_float4(sm.x + v[i].x, sm.y + v[i].y, sm.z + v[i].z, sm.w + v[i].w);
+  }
+  sm = col_reduce<W, kNW>(sm, reds, false);
+  if (!on) return;
+  if (STATS) {  // the chunk's (max, sum) per column; an all -inf chunk is the empty state (-inf, 0)
+    if (g == 0) {
+      const long long p = (o * nchunks + chunk) * inner4 + col4;
+      part[p] = mx;
+      part[plane + p] = make_float4(mx.x == ninf ? 0.0f : sm.x, mx.y == ninf ? 0.0f : sm.y,
+                                    mx.z == ninf ? 0.0f : sm.z, mx.w == ninf ? 0.0f : sm.w);
+    }
+    return;
+  }
+  const float4 inv = make_float4(1.0f / sm.x, 1.0f / sm.y, 1.0f / sm.z, 1.0f / sm.w);
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    const long long r = r0 + g + (long long)i * kRpp;
+    if (r < r1)
+      bch::store_nt(make_float4(v[i].x * inv.x, v[i].y * inv.y, v[i].z * inv.z, v[i].w * inv.w), y + r * inner4);
+  }
+}
+
+// Second kernel of the chunked float4 path: lanes g == 0 merge the column's chunk states in chunk
+// order, and the workgroup writes its chunk of rows (rpc = R * NT / W rows) from a second read of x.
+template <int W, int NT>
+__global__ __launch_bounds__(NT) void softmax_cols_vwrite(const float* in, float* out, long long axis,
+                                                          long long inner4, long long strips, long long nchunks,
+                                                          long long rpc, const float4* __restrict__ part,
+                                                          long long plane) {
+  constexpr int kRpp = NT / W;
+  __shared__ float4 stm[W], sts[W];
+  const long long b = xcd_block();
+  const long long t = b / strips, strip = b - t * strips;
+  const long long o = t / nchunks, chunk = t - o * nchunks;
+  const int c = threadIdx.x % W, g = threadIdx.x / W;
+  const long long col4 = strip * W + c;
+  const bool on = col4 < inner4;
+  if (g == 0 && on) {
+    const float4* pm = part + o * nchunks * inner4 + col4;
+    float4 m = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY), sm = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (long long k = 0; k < nchunks; ++k) {
+      const float4 m2 = pm[k * inner4], s2 = pm[plane + k * inner4];
+      merge_state(m.x, sm.x, m2.x, s2.x);
+      merge_state(m.y, sm.y, m2.y, s2.y);
+      merge_state(m.z, sm.z, m2.z, s2.z);
+      merge_state(m.w, sm.w, m2.w, s2.w);
+    }
+    stm[c] = m;
+    sts[c] = sm;
+  }
+  __syncthreads();
+  if (!on) return;
+  const float4 m = stm[c], sm = sts[c];
+  const float4 inv = make_float4(1.0f / sm.x, 1.0f / sm.y, 1.0f / sm.z, 1.0f / sm.w);
+  const long long r0 = chunk * rpc, r1 = r0 + rpc < axis ? r0 + rpc : axis;
+  const float4* x = reinterpret_cast<const float4*>(in) + o * axis * inner4 + col4;
+  float4* y = reinterpret_cast<float4*>(out) + o * axis * inner4 + col4;
+#pragma unroll 4
+  for (long long r = r0 + g; r < r1; r += kRpp) {
+    const float4 v = bch::load_nt(x + r * inner4);
+    bch::store_nt(make_float4(exp_f32(v.x - m.x) * inv.x, exp_f32(v.y - m.y) * inv.y,
+                              exp_f32(v.z - m.z) * inv.z, exp_f32(v.w - m.w) * inv.w),
+                  y + r * inner4);
+  }
+}
+
+// Float4 plan (inner % 4 == 0, 16-byte aligned): W lanes a row (float4 columns) in workgroups of
+// NT threads, R float4 registers a lane, so R * NT / W rows a chunk.  Strips of 8 float4 (a whole
+// 128-byte line of each row) in 512-thread workgroups where inner has 8 or more float4, so that no
+// line is split between workgroups; 64 rows a pass either way.  One chunk when the axis fits in
+// registers (R <= 32) and the strips fill the CUs: read once, write once.  Otherwise chunks of
+// the largest R that still gives 2 workgroups a CU (R >= 4): a stats kernel and a write kernel.
+struct VecPlan {
+  int w = 0, nt = 256, r = 0;
+  long long strips = 0, nchunks = 1, rpc = 0;
+};
+
+VecPlan vec_plan(long long outer, long long axis, long long inner) {
+  VecPlan p;
+  if (inner % 4 != 0) return p;
+  const long long inner4 = inner / 4;
+  const int w = inner4 >= 8 ? 8 : inner4 >= 3 ? 4 : (int)inner4;
+  const int nt = w == 8 ? 512 : 256, rpp = nt / w;
+  const long long strips = (inner4 + w - 1) / w;
+  const long long cu = bch::device_cu_count();
+  int r = 4;
+  while (r < 32 && (long long)r * rpp < axis) r *= 2;
+  if ((long long)r * rpp < axis || outer * strips < cu) {  // chunks: 2 workgroups a CU where possible
+    r = 32;
+    while (r > 4 && outer * strips * ((axis + (long long)r * rpp - 1) / ((long long)r * rpp)) < 2 * cu) r /= 2;
+  }
+  p.w = w;
+  p.nt = nt;
+  p.r = r;
+  p.strips = strips;
+  p.rpc = (long long)r * rpp;
+  p.nchunks = (axis + p.rpc - 1) / p.rpc;
+  if (outer * strips * p.nchunks > 0x7fffffffLL) p.w = 0;
+  return p;
+}
+
+bool vec_aligned(const void* in, const void* out) {
+  return (reinterpret_cast<uintptr_t>(in) % 16) == 0 && (reinterpret_cast<uintptr_t>(out) % 16) == 0;
+}
+
+template <int W, int NT, bool STATS>
+void launch_cols_vec_r(hipStream_t s, const VecPlan& p, long long blocks, long long axis, long long inner4,
+                       const float* in, float* out, float4* part, long long plane) {
+  const dim3 grid((unsigned)blocks), block(NT);
+  switch (p.r) {
+    case 4: hipLaunchKernelGGL((softmax_cols_reg<4, W, NT, STATS>), grid, block, 0, s, in, out, axis, inner4, p.strips, p.nchunks, part, plane); break;
+    case 8: hipLaunchKernelGGL((softmax_cols_reg<8, W, NT, STATS>), grid, block, 0, s, in, out, axis, inner4, p.strips, p.nchunks, part, plane); break;
+    case 16: hipLaunchKernelGGL((softmax_cols_reg<16, W, NT, STATS>), grid, block, 0, s, in, out, axis, inner4, p.strips, p.nchunks, part, plane); break;
+    default: hipLaunchKernelGGL((softmax_cols_reg<32, W, NT, STATS>), grid, block, 0, s, in, out, axis, inner4, p.strips, p.nchunks, part, plane); break;
+  }
+  if (STATS)
+    hipLaunchKernelGGL((softmax_cols_vwrite<W, NT>), grid, block, 0, s, in, out, axis, inner4, p.strips, p.nchunks,
+                       p.rpc, part, plane);
+}
+
+template <int W, int NT>
+void launch_cols_vec_w(hipStream_t s, const VecPlan& p, long long outer, long long axis, long long inner4,
+                       const float* in, float* out, float4* part) {
+  const long long blocks = outer * p.strips * p.nchunks;
+  if (p.nchunks == 1)
+    launch_cols_vec_r<W, NT, false>(s, p, blocks, axis, inner4, in, out, nullptr, 0);
+  else
+    launch_cols_vec_r<W, NT, true>(s, p, blocks, axis, inner4, in, out, part, outer * p.nchunks * inner4);
 }
 
 // Chunking of the middle-axis softmax: enough workgroups for ~4 per CU, at least 256 rows a chunk.
@@ -417,8 +625,11 @@ size_t softmax_workspace_bytes(long long rows, long long cols) {
 
 size_t softmax_axis_workspace_bytes(long long outer, long long axis, long long inner) {
   if (inner == 1) return softmax_workspace_bytes(outer, axis);
+  // the float4 plan's chunks, or the scalar plan's when the pointers turn out unaligned
   const ColPlan p = col_plan(outer, axis, inner);
-  return p.nchunks > 1 ? sizeof(float) * 2 * (size_t)outer * p.nchunks * (size_t)inner : 0;
+  const VecPlan vp = vec_plan(outer, axis, inner);
+  const long long nc = vp.w && vp.nchunks > p.nchunks ? vp.nchunks : p.nchunks;
+  return nc > 1 ? sizeof(float) * 2 * (size_t)outer * nc * (size_t)inner : 0;
 }
 
 const char* softmax_kernel_name(long long rows, long long cols) {
@@ -480,6 +691,21 @@ hipError_t launch_softmax_axis(hipStream_t s, long long outer, long long axis,
                                void* ws, size_t ws_bytes) {
   if (outer <= 0 || axis <= 0 || inner <= 0) return hipSuccess;
   if (inner == 1) return launch_softmax_rows(s, outer, axis, in, out, ws, ws_bytes);
+  const VecPlan vp = vec_plan(outer, axis, inner);
+  if (vp.w && vec_aligned(in, out)) {
+    float4* part = nullptr;
+    if (vp.nchunks > 1) {
+      if (ws == nullptr || ws_bytes < sizeof(float) * 2 * (size_t)(outer * vp.nchunks * inner)) return hipErrorInvalidValue;
+      part = static_cast<float4*>(ws);
+    }
+    switch (vp.w) {
+      case 1: launch_cols_vec_w<1, 256>(s, vp, outer, axis, inner / 4, in, out, part); break;
+      case 2: launch_cols_vec_w<2, 256>(s, vp, outer, axis, inner / 4, in, out, part); break;
+      case 4: launch_cols_vec_w<4, 256>(s, vp, outer, axis, inner / 4, in, out, part); break;
+      default: launch_cols_vec_w<8, 512>(s, vp, outer, axis, inner / 4, in, out, part); break;
+    }
+    return hipGetLastError();
+  }
   const ColPlan p = col_plan(outer, axis, inner);
   const long long blocks = outer * p.nchunks * p.strips;
   if (blocks > 0x7fffffffLL) return hipErrorInvalidValue;

@@ -242,7 +242,9 @@ bch_status bch_layer_norm(bch_ctx *ctx, long long rows, long long cols,
 /* Softmax along a middle axis of a tensor viewed as [outer, axis, inner]
  * (element (o,j,i) at (o*axis + j)*inner + i).  inner == 1 is the row case.
  * Replaces Tensor::softmax_dim (ops/tensor_axis_ops.rs:67-126) for
- * axis != last. */
+ * axis != last.  A long axis on few columns is cut into chunks whose
+ * per-column (max, sum) states use the context's workspace (grown on
+ * demand); in == out is allowed. */
 bch_status bch_softmax_axis(bch_ctx *ctx, long long outer, long long axis,
                             long long inner, const float *in, float *out);
 

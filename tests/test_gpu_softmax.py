@@ -100,12 +100,23 @@ def test_axis_and_inplace(dev):
     (7, 1, 9),         # a one-element axis
     (1, 65536, 96),    # few strips: the axis in chunks, states merged by a second kernel
     (2, 70000, 2),
+    # inner % 4 == 0 with enough strips: the whole column strip in registers, read once
+    (16, 2048, 1024),  # 4 float4 lanes a row, 32 registers a lane
+    (300, 2048, 16),
+    (300, 1000, 12),   # 3 float4 columns on 4 lanes
+    (400, 1500, 8),    # 2 lanes a row
+    (512, 700, 4),     # 1 lane a row
+    (256, 37, 40),     # most register rows past the axis
 ])
 def test_softmax_middle_axis(dev, outer, axis, inner):
     """softmax_dim over a non-last axis: the column softmax of each [axis][inner] slice, against
     f64, and in place (in == out) on the same shape."""
     _say(f"softmax middle axis outer={outer} axis={axis} inner={inner}")
     x = O.Lcg(outer + axis + inner).normal((outer, axis, inner), 0.0, 3.0)
+    if axis > 1:
+        x[0, :: 7, 0] = -np.inf  # -inf elements add exp(-inf) = 0 to their column
+    if axis >= 600 and inner > 1:
+        x[0, :300, 1] = -np.inf  # whole chunks of -inf: the empty state in the merge
     want = np.ascontiguousarray(np.moveaxis(O.softmax_rows_f64(np.ascontiguousarray(np.moveaxis(x, 1, -1))), -1, 1))
     tx = Tensor.from_data(x, [outer, axis, inner], dev)
     ty = Tensor.empty([outer, axis, inner], dev)
