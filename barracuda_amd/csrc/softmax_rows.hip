@@ -437,37 +437,55 @@ __global__ __launch_bounds__(NT) void softmax_cols_reg(const float* in, float* o
   }
 }
 
-// Second kernel of the chunked float4 path: lanes g == 0 merge the column's chunk states in chunk
-// order, and the workgroup writes its chunk of rows (rpc = R * NT / W rows) from a second read of x.
+// Second kernel of the chunked float4 path: row group g loads the column's states of chunks g,
+// g + NT / W, ... (merged in that order), a shuffle-down tree merges them into lanes g == 0 of each
+// wavefront, and every lane merges the wavefronts' states from LDS in wavefront order (the same
+// order in every lane, so each lane of a column gets the same bits); then the workgroup writes its
+// chunk of rows (rpc = R * NT / W rows) from a second read of x.
+__device__ __forceinline__ void merge_state4(float4& m, float4& s, float4 m2, float4 s2) {
+  merge_state(m.x, s.x, m2.x, s2.x);
+  merge_state(m.y, s.y, m2.y, s2.y);
+  merge_state(m.z, s.z, m2.z, s2.z);
+  merge_state(m.w, s.w, m2.w, s2.w);
+}
+
 template <int W, int NT>
 __global__ __launch_bounds__(NT) void softmax_cols_vwrite(const float* in, float* out, long long axis,
                                                           long long inner4, long long strips, long long nchunks,
                                                           long long rpc, const float4* __restrict__ part,
                                                           long long plane) {
-  constexpr int kRpp = NT / W;
-  __shared__ float4 stm[W], sts[W];
+  constexpr int kRpp = NT / W, kNW = NT / 64;
+  __shared__ float4 stm[kNW][W], sts[kNW][W];
   const long long b = xcd_block();
   const long long t = b / strips, strip = b - t * strips;
   const long long o = t / nchunks, chunk = t - o * nchunks;
-  const int c = threadIdx.x % W, g = threadIdx.x / W;
+  const int c = threadIdx.x % W, g = threadIdx.x / W, lane = threadIdx.x & 63;
   const long long col4 = strip * W + c;
   const bool on = col4 < inner4;
-  if (g == 0 && on) {
-    const float4* pm = part + o * nchunks * inner4 + col4;
+  {
     float4 m = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY), sm = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    for (long long k = 0; k < nchunks; ++k) {
-      const float4 m2 = pm[k * inner4], s2 = pm[plane + k * inner4];
-      merge_state(m.x, sm.x, m2.x, s2.x);
-      merge_state(m.y, sm.y, m2.y, s2.y);
-      merge_state(m.z, sm.z, m2.z, s2.z);
-      merge_state(m.w, sm.w, m2.w, s2.w);
+    if (on) {
+      const float4* pm = part + o * nchunks * inner4 + col4;
+      for (long long k = g; k < nchunks; k += kRpp) merge_state4(m, sm, pm[k * inner4], pm[plane + k * inner4]);
     }
-    stm[c] = m;
-    sts[c] = sm;
+#pragma unroll
+    for (int off = 32; off >= W; off >>= 1) {  // lanes < off take lane + off's state
+      const float4 m2 = make_float4(__shfl_down(m.x, off), __shfl_down(m.y, off), __shfl_down(m.z, off),
+                                    __shfl_down(m.w, off));
+      const float4 s2 = make_float4(__shfl_down(sm.x, off), __shfl_down(sm.y, off), __shfl_down(sm.z, off),
+                                    __shfl_down(sm.w, off));
+      merge_state4(m, sm, m2, s2);
+    }
+    if (lane < W) {
+      stm[threadIdx.x >> 6][lane] = m;
+      sts[threadIdx.x >> 6][lane] = sm;
+    }
   }
   __syncthreads();
   if (!on) return;
-  const float4 m = stm[c], sm = sts[c];
+  float4 m = stm[0][c], sm = sts[0][c];
+#pragma unroll
+  for (int i = 1; i < kNW; ++i) merge_state4(m, sm, stm[i][c], sts[i][c]);
   const float4 inv = make_float4(1.0f / sm.x, 1.0f / sm.y, 1.0f / sm.z, 1.0f / sm.w);
   const long long r0 = chunk * rpc, r1 = r0 + rpc < axis ? r0 + rpc : axis;
   const float4* x = reinterpret_cast<const float4*>(in) + o * axis * inner4 + col4;
@@ -486,7 +504,8 @@ __global__ __launch_bounds__(NT) void softmax_cols_vwrite(const float* in, float
 // 128-byte line of each row) in 512-thread workgroups where inner has 8 or more float4, so that no
 // line is split between workgroups; 64 rows a pass either way.  One chunk when the axis fits in
 // registers (R <= 32) and the strips fill the CUs: read once, write once.  Otherwise chunks of
-// the largest R that still gives 2 workgroups a CU (R >= 4): a stats kernel and a write kernel.
+// the largest R <= 16 that still gives 2 workgroups a CU (R >= 4; 16 rather than 32 keeps two
+// 512-thread stats workgroups on a CU): a stats kernel and a write kernel.
 struct VecPlan {
   int w = 0, nt = 256, r = 0;
   long long strips = 0, nchunks = 1, rpc = 0;
@@ -503,7 +522,7 @@ VecPlan vec_plan(long long outer, long long axis, long long inner) {
   int r = 4;
   while (r < 32 && (long long)r * rpp < axis) r *= 2;
   if ((long long)r * rpp < axis || outer * strips < cu) {  // chunks: 2 workgroups a CU where possible
-    r = 32;
+    r = 16;
     while (r > 4 && outer * strips * ((axis + (long long)r * rpp - 1) / ((long long)r * rpp)) < 2 * cu) r /= 2;
   }
   p.w = w;

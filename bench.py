@@ -326,6 +326,14 @@ def _bench_softmax(dev, T, reps):
                                   "bytes_per_call": nbytes, "traffic": load_traffic("softmax_global_2^27"),
                                   "hbm_frac": nbytes / (ev * 1e-3) / 1e9 / HBM_PEAK_GBS,
                                   "hbm_frac_of_12B_floor": 1.5 * nbytes / (ev * 1e-3) / 1e9 / HBM_PEAK_GBS}
+    # softmax_dim over a middle axis of the same 2^27 elements: [64, 2048, 1024] (whole column
+    # strips in registers, one read) and [1, 65536, 2048] (a chunked axis, read twice)
+    for (o, a, inn), path in (((64, 2048, 1024), "column strips in registers"),
+                              ((1, 65536, 2048), "chunked axis: stats + streaming write")):
+        wall, ev = T.run(lambda i: lib.bch_softmax_axis(ctx, o, a, inn, px, py), reps, 3)
+        out[f"softmax_axis_{o}x{a}x{inn}"] = {"GB/s": nbytes / (ev * 1e-3) / 1e9, "us": ev * 1e3,
+                                              "bytes_per_call": nbytes, "path": path,
+                                              "hbm_frac": nbytes / (ev * 1e-3) / 1e9 / HBM_PEAK_GBS}
     return out
 
 
