@@ -15,8 +15,11 @@
 //     registers; the sum and the sum of squared deviations are wavefront
 //     all-reductions (DPP row ops + v_readlane), so the two passes of the
 //     reference cost no second read; the output is written once.
+//   * 4096 < cols <= 32768, cols % 4 == 0, aligned: one 256-thread
+//     workgroup per row, 8 / 16 / 32 float4 per thread in registers, block
+//     reductions; read once, write once.
 //   * anything else: one 256-thread workgroup per row, the same two passes
-//     with block reductions over a second read of the row (from cache).
+//     with block reductions over further reads of the row (from cache).
 #include "bch_internal.h"
 
 #include <math.h>
@@ -93,6 +96,53 @@ __global__ __launch_bounds__(256) void layer_norm_block(const float* in, float* 
   for (long long j = threadIdx.x; j < cols; j += 256) y[j] = (x[j] - mean) * rstd;
 }
 
+// 4096 < cols <= 1024 NV (cols % 4 == 0, 16-byte aligned): one 256-thread workgroup per row, thread
+// t holding float4 t, t + 256, ... (NV of them) in registers, so the row is read once and written
+// once; the sums are block reductions (wavefront all-reductions, then LDS).
+template <int NV>
+__global__ __launch_bounds__(256) void layer_norm_wg(const float* in, float* out, int cols, float eps) {
+  __shared__ float sh[4];
+  const long long row = blockIdx.x;
+  const int nvec = cols >> 2;
+  const float4* src = reinterpret_cast<const float4*>(in + row * (long long)cols);
+  float4* dst = reinterpret_cast<float4*>(out + row * (long long)cols);
+  float4 v[NV];
+  float s = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int idx = i * 256 + (int)threadIdx.x;
+    v[i] = idx < nvec ? bch::load_nt(src + idx) : make_float4(0.f, 0.f, 0.f, 0.f);
+    s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
+  }
+  const float mean = block_sum(s, sh) / (float)cols;
+  float q = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    if (i * 256 + (int)threadIdx.x < nvec) {
+      const float dx = v[i].x - mean, dy = v[i].y - mean, dz = v[i].z - mean, dw = v[i].w - mean;
+      q += fmaf(dx, dx, dy * dy) + fmaf(dz, dz, dw * dw);
+    }
+  }
+  const float var = block_sum(q, sh) / (float)cols;
+  const float rstd = 1.0f / sqrtf(var + eps);
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int idx = i * 256 + (int)threadIdx.x;
+    if (idx < nvec)
+      bch::store_nt(make_float4((v[i].x - mean) * rstd, (v[i].y - mean) * rstd, (v[i].z - mean) * rstd,
+                                (v[i].w - mean) * rstd),
+                    dst + idx);
+  }
+}
+
+int pick_wg_nv(long long cols) {
+  if (cols % 4 != 0 || cols <= 4096) return 0;
+  if (cols <= 8192) return 8;
+  if (cols <= 16384) return 16;
+  if (cols <= 32768) return 32;
+  return 0;
+}
+
 int pick_nv(long long cols) {
   if (cols <= 256) return 1;
   if (cols <= 512) return 2;
@@ -123,6 +173,12 @@ const char* layer_norm_kernel_name(long long rows, long long cols) {
       default: break;
     }
   }
+  switch (pick_wg_nv(cols)) {
+    case 8: return "layer_norm_wg<8>";
+    case 16: return "layer_norm_wg<16>";
+    case 32: return "layer_norm_wg<32>";
+    default: break;
+  }
   return "layer_norm_block";
 }
 
@@ -137,6 +193,16 @@ hipError_t launch_layer_norm(hipStream_t s, long long rows, long long cols, floa
       case 4: hipLaunchKernelGGL(layer_norm_wave<4>, grid, block, 0, s, in, out, rows, c, eps); break;
       case 8: hipLaunchKernelGGL(layer_norm_wave<8>, grid, block, 0, s, in, out, rows, c, eps); break;
       default: hipLaunchKernelGGL(layer_norm_wave<16>, grid, block, 0, s, in, out, rows, c, eps); break;
+    }
+    return hipGetLastError();
+  }
+  if (rows > 0x7fffffffLL) return hipErrorInvalidValue;
+  if (pick_wg_nv(cols) > 0 && (reinterpret_cast<uintptr_t>(in) & 15) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0) {
+    const dim3 grid((unsigned)rows), block(256);
+    switch (pick_wg_nv(cols)) {
+      case 8: hipLaunchKernelGGL(layer_norm_wg<8>, grid, block, 0, s, in, out, (int)cols, eps); break;
+      case 16: hipLaunchKernelGGL(layer_norm_wg<16>, grid, block, 0, s, in, out, (int)cols, eps); break;
+      default: hipLaunchKernelGGL(layer_norm_wg<32>, grid, block, 0, s, in, out, (int)cols, eps); break;
     }
     return hipGetLastError();
   }
