@@ -18,6 +18,8 @@
 //     one wavefront per row with the row's 32 doubles per lane (occupancy 4)
 //     5.1 TB/s, non-temporal 5.6 TB/s, two wavefronts per row 5.8-6.1 TB/s,
 //     four 6.1-6.4 TB/s.
+//   * 2048 < cols <= 8192: the same kernel with the workgroup's four
+//     wavefronts per row and up to 32 doubles per lane (occupancy 4).
 //   * longer rows: one 256-thread workgroup per row, three sweeps (max; sum
 //     of exp; write), the second and third reading the row again from cache.
 // in may equal out: every value is read before any value of its row is
@@ -165,12 +167,14 @@ struct RowPlan {
   int nv, vec, w;  // nv == 0: the three-sweep block kernel
 };
 
-// At most 8 doubles per lane: one wavefront per row up to 512 columns, four
-// up to 2048.
+// At most 8 doubles per lane up to 2048 columns (one wavefront per row up to
+// 512, four up to 2048), then up to 32 doubles per lane on four wavefronts
+// per row up to 8192 (occupancy 4 instead of a three-sweep block kernel).
 RowPlan row_plan(long long cols, bool aligned16) {
   const int vec = aligned16 && cols % 2 == 0 ? 2 : 1;
   const int w = cols <= 512 ? 1 : 4;
-  for (int nv = 1; nv * vec <= 8; nv *= 2)
+  const int most = cols <= 2048 ? 8 : 32;
+  for (int nv = 1; nv * vec <= most; nv *= 2)
     if (cols <= 64LL * w * nv * vec) return {nv, vec, w};
   return {0, vec, 1};
 }
@@ -182,11 +186,20 @@ hipError_t launch_rows(hipStream_t s, int nv, long long rows, int cols, const do
     case 1: hipLaunchKernelGGL((softmax_f64_rows<1, VEC, W>), grid, block, 0, s, in, out, rows, cols); break;
     case 2: hipLaunchKernelGGL((softmax_f64_rows<2, VEC, W>), grid, block, 0, s, in, out, rows, cols); break;
     case 4: hipLaunchKernelGGL((softmax_f64_rows<4, VEC, W>), grid, block, 0, s, in, out, rows, cols); break;
-    default:
-      if constexpr (VEC == 1) {
-        hipLaunchKernelGGL((softmax_f64_rows<8, 1, W>), grid, block, 0, s, in, out, rows, cols);
+    case 8: hipLaunchKernelGGL((softmax_f64_rows<8, VEC, W>), grid, block, 0, s, in, out, rows, cols); break;
+    case 16:
+      if constexpr (W == 4) {
+        hipLaunchKernelGGL((softmax_f64_rows<16, VEC, 4>), grid, block, 0, s, in, out, rows, cols);
         break;
       }
+      return hipErrorInvalidValue;
+    case 32:
+      if constexpr (W == 4 && VEC == 1) {
+        hipLaunchKernelGGL((softmax_f64_rows<32, 1, 4>), grid, block, 0, s, in, out, rows, cols);
+        break;
+      }
+      return hipErrorInvalidValue;
+    default:
       return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -198,11 +211,14 @@ namespace bch {
 
 const char* softmax_f64_kernel_name(long long rows, long long cols, bool aligned16) {
   (void)rows;
-  static const char* const names[2][2][4] = {
-      {{"softmax_f64_rows<1,1,1>", "softmax_f64_rows<2,1,1>", "softmax_f64_rows<4,1,1>", "softmax_f64_rows<8,1,1>"},
-       {"softmax_f64_rows<1,1,4>", "softmax_f64_rows<2,1,4>", "softmax_f64_rows<4,1,4>", "softmax_f64_rows<8,1,4>"}},
-      {{"softmax_f64_rows<1,2,1>", "softmax_f64_rows<2,2,1>", "softmax_f64_rows<4,2,1>", ""},
-       {"softmax_f64_rows<1,2,4>", "softmax_f64_rows<2,2,4>", "softmax_f64_rows<4,2,4>", ""}}};
+  static const char* const names[2][2][6] = {
+      {{"softmax_f64_rows<1,1,1>", "softmax_f64_rows<2,1,1>", "softmax_f64_rows<4,1,1>", "softmax_f64_rows<8,1,1>", "",
+        ""},
+       {"softmax_f64_rows<1,1,4>", "softmax_f64_rows<2,1,4>", "softmax_f64_rows<4,1,4>", "softmax_f64_rows<8,1,4>",
+        "softmax_f64_rows<16,1,4>", "softmax_f64_rows<32,1,4>"}},
+      {{"softmax_f64_rows<1,2,1>", "softmax_f64_rows<2,2,1>", "softmax_f64_rows<4,2,1>", "", "", ""},
+       {"softmax_f64_rows<1,2,4>", "softmax_f64_rows<2,2,4>", "softmax_f64_rows<4,2,4>", "softmax_f64_rows<8,2,4>",
+        "softmax_f64_rows<16,2,4>", ""}}};
   const RowPlan p = row_plan(cols, aligned16);
   if (p.nv == 0) return "softmax_f64_block";
   return names[p.vec - 1][p.w == 4][__builtin_ctz(p.nv)];

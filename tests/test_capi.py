@@ -288,7 +288,9 @@ def test_softmax_f64_validation_and_routing_before_device():
     assert name(65536, 2048, 0x1008) == b"softmax_f64_rows<8,1,4>"
     assert name(3, 5, 0x1000) == b"softmax_f64_rows<1,1,1>"
     assert name(3, 129, 0x1000) == b"softmax_f64_rows<4,1,1>"
-    assert name(3, 2049, 0x1000) == b"softmax_f64_block"
+    assert name(3, 2049, 0x1000) == b"softmax_f64_rows<16,1,4>"
+    assert name(3, 8192, 0x1000) == b"softmax_f64_rows<16,2,4>"
+    assert name(3, 8193, 0x1000) == b"softmax_f64_block"
 
 
 def test_elementwise_and_layer_norm_validation_before_device():
@@ -308,4 +310,7 @@ def test_elementwise_and_layer_norm_validation_before_device():
     assert lib.bch_sgemm_ex(nul, 1, 4, 4, 4, nul, 4, nul, 4, nul, N.BCH_ACT_GELU, nul, 4) == N.BCH_E_INVALID
     assert "ctx" in N.last_error(None)
     assert lib.bch_layer_norm_kernel_name(65536, 2048) == b"layer_norm_wave<8>"
-    assert lib.bch_layer_norm_kernel_name(3, 4100) == b"layer_norm_block"
+    assert lib.bch_layer_norm_kernel_name(3, 4100) == b"layer_norm_wg<8>"
+    assert lib.bch_layer_norm_kernel_name(3, 32768) == b"layer_norm_wg<32>"
+    assert lib.bch_layer_norm_kernel_name(3, 32772) == b"layer_norm_block"
+    assert lib.bch_layer_norm_kernel_name(3, 4099) == b"layer_norm_block"

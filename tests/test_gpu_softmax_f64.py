@@ -53,7 +53,10 @@ def _close(got, want):
     (9, 300, 0, "softmax_f64_rows<4,2,1>"), (4, 512, 1, "softmax_f64_rows<8,1,1>"),
     (3, 513, 0, "softmax_f64_rows<4,1,4>"), (6, 2048, 0, "softmax_f64_rows<4,2,4>"),
     (5, 2047, 0, "softmax_f64_rows<8,1,4>"), (7, 1030, 0, "softmax_f64_rows<4,2,4>"),
-    (2, 2049, 0, "softmax_f64_block"), (3, 100003, 0, "softmax_f64_block"),
+    (2, 2049, 0, "softmax_f64_rows<16,1,4>"), (3, 100003, 0, "softmax_f64_block"),
+    (3, 4096, 0, "softmax_f64_rows<8,2,4>"), (2, 8192, 0, "softmax_f64_rows<16,2,4>"),
+    (2, 8191, 0, "softmax_f64_rows<32,1,4>"), (3, 6000, 1, "softmax_f64_rows<32,1,4>"),
+    (2, 8194, 0, "softmax_f64_block"),
     (4099, 128, 0, "softmax_f64_rows<1,2,1>"), (1025, 1000, 1, "softmax_f64_rows<4,1,4>"),
     (4097, 700, 0, "softmax_f64_rows<2,2,4>")])
 def test_softmax_f64_shapes_vs_oracle(dev, rows, cols, offset, kernel):
