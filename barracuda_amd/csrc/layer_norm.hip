@@ -15,9 +15,9 @@
 //     registers; the sum and the sum of squared deviations are wavefront
 //     all-reductions (DPP row ops + v_readlane), so the two passes of the
 //     reference cost no second read; the output is written once.
-//   * 4096 < cols <= 32768, cols % 4 == 0, aligned: one 256-thread
-//     workgroup per row, 8 / 16 / 32 float4 per thread in registers, block
-//     reductions; read once, write once.
+//   * 4096 < cols <= 65536, cols % 4 == 0, aligned: one workgroup per row,
+//     8 / 16 / 32 float4 per thread in registers (1024 threads with 16 each
+//     above 32768), block reductions; read once, write once.
 //   * anything else: one 256-thread workgroup per row, the same two passes
 //     with block reductions over further reads of the row (from cache).
 #include "bch_internal.h"
@@ -69,13 +69,18 @@ __global__ __launch_bounds__(256) void layer_norm_wave(const float* in, float* o
 
 // Sum over the 256 threads of a workgroup; every thread gets it.  Must be
 // reached by all threads of the block.
+template <int NW = 4>
 __device__ __forceinline__ float block_sum(float v, float* sh) {
   v = wave_allreduce(v, OpSum());
   const int w = threadIdx.x >> 6;
   __syncthreads();  // sh may still be read from the previous call
   if ((threadIdx.x & 63) == 0) sh[w] = v;
   __syncthreads();
-  return (sh[0] + sh[1]) + (sh[2] + sh[3]);
+  if (NW == 4) return (sh[0] + sh[1]) + (sh[2] + sh[3]);
+  float r = sh[0];
+#pragma unroll
+  for (int i = 1; i < NW; ++i) r += sh[i];
+  return r;
 }
 
 __global__ __launch_bounds__(256) void layer_norm_block(const float* in, float* out, long long cols, float eps) {
@@ -96,12 +101,12 @@ __global__ __launch_bounds__(256) void layer_norm_block(const float* in, float* 
   for (long long j = threadIdx.x; j < cols; j += 256) y[j] = (x[j] - mean) * rstd;
 }
 
-// 4096 < cols <= 1024 NV (cols % 4 == 0, 16-byte aligned): one 256-thread workgroup per row, thread
-// t holding float4 t, t + 256, ... (NV of them) in registers, so the row is read once and written
+// 4096 < cols <= 4 NT NV (cols % 4 == 0, 16-byte aligned): one NT-thread workgroup per row (256, or
+// 1024 above 32768 columns), thread t holding float4 t, t + NT, ... (NV of them) in registers, so the row is read once and written
 // once; the sums are block reductions (wavefront all-reductions, then LDS).
-template <int NV>
-__global__ __launch_bounds__(256) void layer_norm_wg(const float* in, float* out, int cols, float eps) {
-  __shared__ float sh[4];
+template <int NV, int NT>
+__global__ __launch_bounds__(NT) void layer_norm_wg(const float* in, float* out, int cols, float eps) {
+  __shared__ float sh[NT / 64];
   const long long row = blockIdx.x;
   const int nvec = cols >> 2;
   const float4* src = reinterpret_cast<const float4*>(in + row * (long long)cols);
@@ -110,24 +115,24 @@ __global__ __launch_bounds__(256) void layer_norm_wg(const float* in, float* out
   float s = 0.0f;
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
-    const int idx = i * 256 + (int)threadIdx.x;
+    const int idx = i * NT + (int)threadIdx.x;
     v[i] = idx < nvec ? bch::load_nt(src + idx) : make_float4(0.f, 0.f, 0.f, 0.f);
     s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
   }
-  const float mean = block_sum(s, sh) / (float)cols;
+  const float mean = block_sum<NT / 64>(s, sh) / (float)cols;
   float q = 0.0f;
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
-    if (i * 256 + (int)threadIdx.x < nvec) {
+    if (i * NT + (int)threadIdx.x < nvec) {
       const float dx = v[i].x - mean, dy = v[i].y - mean, dz = v[i].z - mean, dw = v[i].w - mean;
       q += fmaf(dx, dx, dy * dy) + fmaf(dz, dz, dw * dw);
     }
   }
-  const float var = block_sum(q, sh) / (float)cols;
+  const float var = block_sum<NT / 64>(q, sh) / (float)cols;
   const float rstd = 1.0f / sqrtf(var + eps);
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
-    const int idx = i * 256 + (int)threadIdx.x;
+    const int idx = i * NT + (int)threadIdx.x;
     if (idx < nvec)
       bch::store_nt(make_float4((v[i].x - mean) * rstd, (v[i].y - mean) * rstd, (v[i].z - mean) * rstd,
                                 (v[i].w - mean) * rstd),
@@ -140,6 +145,7 @@ int pick_wg_nv(long long cols) {
   if (cols <= 8192) return 8;
   if (cols <= 16384) return 16;
   if (cols <= 32768) return 32;
+  if (cols <= 65536) return 64;  // 1024 threads, 16 float4 each
   return 0;
 }
 
@@ -177,6 +183,7 @@ const char* layer_norm_kernel_name(long long rows, long long cols) {
     case 8: return "layer_norm_wg<8>";
     case 16: return "layer_norm_wg<16>";
     case 32: return "layer_norm_wg<32>";
+    case 64: return "layer_norm_wg<16, 1024>";
     default: break;
   }
   return "layer_norm_block";
@@ -200,9 +207,10 @@ hipError_t launch_layer_norm(hipStream_t s, long long rows, long long cols, floa
   if (pick_wg_nv(cols) > 0 && (reinterpret_cast<uintptr_t>(in) & 15) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0) {
     const dim3 grid((unsigned)rows), block(256);
     switch (pick_wg_nv(cols)) {
-      case 8: hipLaunchKernelGGL(layer_norm_wg<8>, grid, block, 0, s, in, out, (int)cols, eps); break;
-      case 16: hipLaunchKernelGGL(layer_norm_wg<16>, grid, block, 0, s, in, out, (int)cols, eps); break;
-      default: hipLaunchKernelGGL(layer_norm_wg<32>, grid, block, 0, s, in, out, (int)cols, eps); break;
+      case 8: hipLaunchKernelGGL((layer_norm_wg<8, 256>), grid, block, 0, s, in, out, (int)cols, eps); break;
+      case 16: hipLaunchKernelGGL((layer_norm_wg<16, 256>), grid, block, 0, s, in, out, (int)cols, eps); break;
+      case 32: hipLaunchKernelGGL((layer_norm_wg<32, 256>), grid, block, 0, s, in, out, (int)cols, eps); break;
+      default: hipLaunchKernelGGL((layer_norm_wg<16, 1024>), grid, dim3(1024), 0, s, in, out, (int)cols, eps); break;
     }
     return hipGetLastError();
   }

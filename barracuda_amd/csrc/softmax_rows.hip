@@ -18,8 +18,9 @@
 //     to scratch; pass 2 merges the row's chunk states in every workgroup
 //     and writes its chunk.  Read, read, write: 12 bytes per element, with
 //     the whole chip busy instead of one CU per row.
-//   * 4096 < cols <= 32768, cols % 4 == 0, rows left whole: one workgroup
-//     per row, 8 / 16 / 32 float4 per thread in registers; read once.
+//   * 4096 < cols <= 65536, cols % 4 == 0, rows left whole: one workgroup
+//     per row, 8 / 16 / 32 float4 per thread in registers (1024 threads with
+//     16 each above 32768); read once.
 //   * anything else: one workgroup per row, an online (max, sum) pass and a
 //     second read that writes; scalar loads, any cols.
 //   * axis != last: each [axis][inner] slice is a column softmax.  With
@@ -170,21 +171,26 @@ __global__ __launch_bounds__(256) void softmax_rows_block(
   for (long long j = threadIdx.x; j < cols; j += 256) y[j] = exp_f32(x[j] - m) * inv;
 }
 
-// Rows of 4096 < cols <= 1024 NV (cols % 4 == 0, 16-byte aligned) that the split plan leaves
-// whole: one 256-thread workgroup per row, thread t holding float4 t, t + 256, ... (NV of them), so
+// Rows of 4096 < cols <= 4 NT NV (cols % 4 == 0, 16-byte aligned) that the split plan leaves
+// whole: one NT-thread workgroup per row (256, or 1024 above 32768 columns), thread t holding
+// float4 t, t + NT, ... (NV of them), so
 // the row is read once and written once, as in the wavefront-per-row kernel; max and sum are
-// wavefront all-reductions, then the four wavefronts' values in LDS.
-template <class Op>
-__device__ __forceinline__ float block_allreduce4(float v, Op op, float* red) {
+// wavefront all-reductions, then the wavefronts' values in LDS.
+template <int NW, class Op>
+__device__ __forceinline__ float block_allreduce_nw(float v, Op op, float* red) {
   v = wave_allreduce(v, op);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
   __syncthreads();
-  return op(op(red[0], red[1]), op(red[2], red[3]));
+  if (NW == 4) return op(op(red[0], red[1]), op(red[2], red[3]));
+  float r = red[0];
+#pragma unroll
+  for (int i = 1; i < NW; ++i) r = op(r, red[i]);
+  return r;
 }
 
-template <int NV>
-__global__ __launch_bounds__(256) void softmax_rows_wg(const float* in, float* out, int cols) {
-  __shared__ float redm[4], reds[4];
+template <int NV, int NT>
+__global__ __launch_bounds__(NT) void softmax_rows_wg(const float* in, float* out, int cols) {
+  __shared__ float redm[NT / 64], reds[NT / 64];
   const long long row = blockIdx.x;
   const int nvec = cols >> 2;
   const float4* src = reinterpret_cast<const float4*>(in + row * (long long)cols);
@@ -193,26 +199,26 @@ __global__ __launch_bounds__(256) void softmax_rows_wg(const float* in, float* o
   float4 v[NV];
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
-    const int idx = i * 256 + (int)threadIdx.x;
+    const int idx = i * NT + (int)threadIdx.x;
     v[i] = idx < nvec ? bch::load_nt(src + idx) : make_float4(ninf, ninf, ninf, ninf);
   }
   float mx = ninf;
 #pragma unroll
   for (int i = 0; i < NV; ++i) mx = fmaxf(mx, fmaxf(fmaxf(v[i].x, v[i].y), fmaxf(v[i].z, v[i].w)));
-  mx = block_allreduce4(mx, OpMax(), redm);
+  mx = block_allreduce_nw<NT / 64>(mx, OpMax(), redm);
   float s = 0.0f;
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
-    if (i * 256 + (int)threadIdx.x < nvec) {
+    if (i * NT + (int)threadIdx.x < nvec) {
       v[i] = make_float4(exp_f32(v[i].x - mx), exp_f32(v[i].y - mx), exp_f32(v[i].z - mx), exp_f32(v[i].w - mx));
       s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
     }
   }
-  s = block_allreduce4(s, OpSum(), reds);
+  s = block_allreduce_nw<NT / 64>(s, OpSum(), reds);
   const float inv = 1.0f / s;
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
-    const int idx = i * 256 + (int)threadIdx.x;
+    const int idx = i * NT + (int)threadIdx.x;
     if (idx < nvec) bch::store_nt(make_float4(v[i].x * inv, v[i].y * inv, v[i].z * inv, v[i].w * inv), dst + idx);
   }
 }
@@ -222,6 +228,7 @@ int pick_wg_nv(long long cols) {
   if (cols <= 8192) return 8;
   if (cols <= 16384) return 16;
   if (cols <= 32768) return 32;
+  if (cols <= 65536) return 64;  // 1024 threads, 16 float4 each
   return 0;
 }
 
@@ -724,6 +731,7 @@ const char* softmax_kernel_name(long long rows, long long cols) {
     case 8: return "softmax_rows_wg<8>";
     case 16: return "softmax_rows_wg<16>";
     case 32: return "softmax_rows_wg<32>";
+    case 64: return "softmax_rows_wg<16, 1024>";
     default: break;
   }
   return "softmax_rows_block";
@@ -766,9 +774,10 @@ hipError_t launch_softmax_rows(hipStream_t s, long long rows, long long cols,
     if (rows > 0x7fffffffLL) return hipErrorInvalidValue;
     const dim3 grid((unsigned)rows), block(256);
     switch (pick_wg_nv(cols)) {
-      case 8: hipLaunchKernelGGL(softmax_rows_wg<8>, grid, block, 0, s, in, out, (int)cols); break;
-      case 16: hipLaunchKernelGGL(softmax_rows_wg<16>, grid, block, 0, s, in, out, (int)cols); break;
-      default: hipLaunchKernelGGL(softmax_rows_wg<32>, grid, block, 0, s, in, out, (int)cols); break;
+      case 8: hipLaunchKernelGGL((softmax_rows_wg<8, 256>), grid, block, 0, s, in, out, (int)cols); break;
+      case 16: hipLaunchKernelGGL((softmax_rows_wg<16, 256>), grid, block, 0, s, in, out, (int)cols); break;
+      case 32: hipLaunchKernelGGL((softmax_rows_wg<32, 256>), grid, block, 0, s, in, out, (int)cols); break;
+      default: hipLaunchKernelGGL((softmax_rows_wg<16, 1024>), dim3((unsigned)rows), dim3(1024), 0, s, in, out, (int)cols); break;
     }
   } else {
     if (rows > 0x7fffffffLL) return hipErrorInvalidValue;

@@ -312,5 +312,6 @@ def test_elementwise_and_layer_norm_validation_before_device():
     assert lib.bch_layer_norm_kernel_name(65536, 2048) == b"layer_norm_wave<8>"
     assert lib.bch_layer_norm_kernel_name(3, 4100) == b"layer_norm_wg<8>"
     assert lib.bch_layer_norm_kernel_name(3, 32768) == b"layer_norm_wg<32>"
-    assert lib.bch_layer_norm_kernel_name(3, 32772) == b"layer_norm_block"
+    assert lib.bch_layer_norm_kernel_name(3, 32772) == b"layer_norm_wg<16, 1024>"
+    assert lib.bch_layer_norm_kernel_name(3, 65540) == b"layer_norm_block"
     assert lib.bch_layer_norm_kernel_name(3, 4099) == b"layer_norm_block"

@@ -92,7 +92,8 @@ def test_elementwise_ops_exact(dev, offset, n):
 @pytest.mark.parametrize("rows,cols", [(1, 1), (3, 5), (7, 256), (9, 257), (4, 1000), (33, 2048), (8, 4096),
                                        (3, 4100), (2, 10000), (1, 65536),
                                        # one workgroup per row, the row in registers (4096 < cols <= 32768)
-                                       (5, 4104), (300, 8192), (64, 32768), (2, 32772)])
+                                       (5, 4104), (300, 8192), (64, 32768), (2, 32772), (40, 40000), (3, 65536),
+                                       (2, 65540)])
 def test_layer_norm_shapes(dev, rows, cols):
     _say(f"layer_norm rows={rows} cols={cols}")
     x = O.Lcg(rows * 7 + cols).normal((rows, cols), 1.5, 3.0)

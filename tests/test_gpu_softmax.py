@@ -47,7 +47,8 @@ def test_golden_vectors(dev, golden):
 @pytest.mark.parametrize("rows,cols", [(1, 1), (3, 3), (5, 4), (7, 256), (9, 257), (4, 1000),
                                        (33, 2048), (8, 4096), (3, 4100), (2, 10000), (1, 65536),
                                        # one workgroup per row, the row in registers (4096 < cols <= 32768)
-                                       (5, 4104), (300, 8192), (257, 16384), (1024, 32768)])
+                                       (5, 4104), (300, 8192), (257, 16384), (1024, 32768),
+                                       (1024, 40000)])  # 1024-thread workgroups above 32768
 def test_shapes_vs_f64(dev, rows, cols):
     _say(f"softmax rows={rows} cols={cols}")
     x = O.Lcg(rows * 1000 + cols).normal((rows, cols), 0.0, 3.0)
