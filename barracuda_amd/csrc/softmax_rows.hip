@@ -21,6 +21,9 @@
 //   * 4096 < cols <= 65536, cols % 4 == 0, rows left whole: one workgroup
 //     per row, 8 / 16 / 32 float4 per thread in registers (1024 threads with
 //     16 each above 32768); read once.
+//   * other widths (cols % 4 != 0, or unaligned) up to 32768, rows left
+//     whole: one workgroup per row with up to 32 elements per thread in
+//     registers, scalar loads; read once.
 //   * anything else: one workgroup per row, an online (max, sum) pass and a
 //     second read that writes; scalar loads, any cols.
 //   * axis != last: each [axis][inner] slice is a column softmax.  With
@@ -221,6 +224,50 @@ __global__ __launch_bounds__(NT) void softmax_rows_wg(const float* in, float* ou
     const int idx = i * NT + (int)threadIdx.x;
     if (idx < nvec) bch::store_nt(make_float4(v[i].x * inv, v[i].y * inv, v[i].z * inv, v[i].w * inv), dst + idx);
   }
+}
+
+// Rows of any width up to NT NS that the float4 kernels cannot take (cols % 4 != 0, or unaligned
+// buffers), left whole by the split plan: one NT-thread workgroup per row, thread t holding elements
+// t, t + NT, ... (NS of them) in registers; scalar loads, read once, write once.
+template <int NS, int NT>
+__global__ __launch_bounds__(NT) void softmax_rows_wgs(const float* in, float* out, int cols) {
+  __shared__ float redm[NT / 64], reds[NT / 64];
+  const float* x = in + (long long)blockIdx.x * cols;
+  float* y = out + (long long)blockIdx.x * cols;
+  float v[NS];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < NS; ++i) {
+    const int j = i * NT + (int)threadIdx.x;
+    v[i] = j < cols ? __builtin_nontemporal_load(x + j) : -INFINITY;
+    mx = fmaxf(mx, v[i]);
+  }
+  mx = block_allreduce_nw<NT / 64>(mx, OpMax(), redm);
+  float s = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NS; ++i) {
+    if (i * NT + (int)threadIdx.x < cols) {
+      v[i] = exp_f32(v[i] - mx);
+      s += v[i];
+    }
+  }
+  s = block_allreduce_nw<NT / 64>(s, OpSum(), reds);
+  const float inv = 1.0f / s;
+#pragma unroll
+  for (int i = 0; i < NS; ++i) {
+    const int j = i * NT + (int)threadIdx.x;
+    if (j < cols) __builtin_nontemporal_store(v[i] * inv, y + j);
+  }
+}
+
+// Scalar register kernel for a row of cols: (NS, NT) coded as NS * 10000 + NT, 0 above 32768 (64
+// elements per thread on 1024 threads spill).
+int pick_wgs(long long cols) {
+  if (cols <= 1024) return 4 * 10000 + 256;
+  if (cols <= 4096) return 16 * 10000 + 256;
+  if (cols <= 16384) return 16 * 10000 + 1024;
+  if (cols <= 32768) return 32 * 10000 + 1024;
+  return 0;
 }
 
 int pick_wg_nv(long long cols) {
@@ -734,6 +781,13 @@ const char* softmax_kernel_name(long long rows, long long cols) {
     case 64: return "softmax_rows_wg<16, 1024>";
     default: break;
   }
+  switch (pick_wgs(cols)) {
+    case 40256: return "softmax_rows_wgs<4, 256>";
+    case 160256: return "softmax_rows_wgs<16, 256>";
+    case 161024: return "softmax_rows_wgs<16, 1024>";
+    case 321024: return "softmax_rows_wgs<32, 1024>";
+    default: break;
+  }
   return "softmax_rows_block";
 }
 
@@ -778,6 +832,16 @@ hipError_t launch_softmax_rows(hipStream_t s, long long rows, long long cols,
       case 16: hipLaunchKernelGGL((softmax_rows_wg<16, 256>), grid, block, 0, s, in, out, (int)cols); break;
       case 32: hipLaunchKernelGGL((softmax_rows_wg<32, 256>), grid, block, 0, s, in, out, (int)cols); break;
       default: hipLaunchKernelGGL((softmax_rows_wg<16, 1024>), dim3((unsigned)rows), dim3(1024), 0, s, in, out, (int)cols); break;
+    }
+  } else if (pick_wgs(cols) > 0) {
+    if (rows > 0x7fffffffLL) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)rows);
+    const int c = (int)cols;
+    switch (pick_wgs(cols)) {
+      case 40256: hipLaunchKernelGGL((softmax_rows_wgs<4, 256>), grid, dim3(256), 0, s, in, out, c); break;
+      case 160256: hipLaunchKernelGGL((softmax_rows_wgs<16, 256>), grid, dim3(256), 0, s, in, out, c); break;
+      case 161024: hipLaunchKernelGGL((softmax_rows_wgs<16, 1024>), grid, dim3(1024), 0, s, in, out, c); break;
+      default: hipLaunchKernelGGL((softmax_rows_wgs<32, 1024>), grid, dim3(1024), 0, s, in, out, c); break;
     }
   } else {
     if (rows > 0x7fffffffLL) return hipErrorInvalidValue;

@@ -48,7 +48,10 @@ def test_golden_vectors(dev, golden):
                                        (33, 2048), (8, 4096), (3, 4100), (2, 10000), (1, 65536),
                                        # one workgroup per row, the row in registers (4096 < cols <= 32768)
                                        (5, 4104), (300, 8192), (257, 16384), (1024, 32768),
-                                       (1024, 40000)])  # 1024-thread workgroups above 32768
+                                       (1024, 40000),  # 1024-thread workgroups above 32768
+                                       # other widths: scalar loads, the row in registers
+                                       (65, 2047), (300, 4099), (1100, 30001),
+                                       (1030, 50257)])  # above 32768: the block kernel
 def test_shapes_vs_f64(dev, rows, cols):
     _say(f"softmax rows={rows} cols={cols}")
     x = O.Lcg(rows * 1000 + cols).normal((rows, cols), 0.0, 3.0)
