@@ -18,6 +18,9 @@
 //   * 4096 < cols <= 65536, cols % 4 == 0, aligned: one workgroup per row,
 //     8 / 16 / 32 float4 per thread in registers (1024 threads with 16 each
 //     above 32768), block reductions; read once, write once.
+//   * other widths (cols % 4 != 0, or unaligned) up to 32768: one workgroup
+//     per row with up to 32 elements per thread in registers, scalar loads;
+//     read once.
 //   * anything else: one 256-thread workgroup per row, the same two passes
 //     with block reductions over further reads of the row (from cache).
 #include "bch_internal.h"
@@ -140,6 +143,49 @@ __global__ __launch_bounds__(NT) void layer_norm_wg(const float* in, float* out,
   }
 }
 
+// Rows of any width up to NT NS that the float4 kernels cannot take (cols % 4 != 0, or unaligned
+// buffers): one NT-thread workgroup per row, thread t holding elements t, t + NT, ... (NS of them)
+// in registers; scalar loads, read once, write once.
+template <int NS, int NT>
+__global__ __launch_bounds__(NT) void layer_norm_wgs(const float* in, float* out, int cols, float eps) {
+  __shared__ float sh[NT / 64];
+  const float* x = in + (long long)blockIdx.x * cols;
+  float* y = out + (long long)blockIdx.x * cols;
+  float v[NS];
+  float s = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NS; ++i) {
+    const int j = i * NT + (int)threadIdx.x;
+    v[i] = j < cols ? __builtin_nontemporal_load(x + j) : 0.0f;
+    s += v[i];
+  }
+  const float mean = block_sum<NT / 64>(s, sh) / (float)cols;
+  float q = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NS; ++i) {
+    if (i * NT + (int)threadIdx.x < cols) {
+      const float d = v[i] - mean;
+      q = fmaf(d, d, q);
+    }
+  }
+  const float var = block_sum<NT / 64>(q, sh) / (float)cols;
+  const float rstd = 1.0f / sqrtf(var + eps);
+#pragma unroll
+  for (int i = 0; i < NS; ++i) {
+    const int j = i * NT + (int)threadIdx.x;
+    if (j < cols) __builtin_nontemporal_store((v[i] - mean) * rstd, y + j);
+  }
+}
+
+// Scalar register kernel for a row of cols: (NS, NT) coded as NS * 10000 + NT, 0 above 32768.
+int pick_wgs(long long cols) {
+  if (cols <= 1024) return 4 * 10000 + 256;
+  if (cols <= 4096) return 16 * 10000 + 256;
+  if (cols <= 16384) return 16 * 10000 + 1024;
+  if (cols <= 32768) return 32 * 10000 + 1024;
+  return 0;
+}
+
 int pick_wg_nv(long long cols) {
   if (cols % 4 != 0 || cols <= 4096) return 0;
   if (cols <= 8192) return 8;
@@ -186,6 +232,13 @@ const char* layer_norm_kernel_name(long long rows, long long cols) {
     case 64: return "layer_norm_wg<16, 1024>";
     default: break;
   }
+  switch (pick_wgs(cols)) {
+    case 40256: return "layer_norm_wgs<4, 256>";
+    case 160256: return "layer_norm_wgs<16, 256>";
+    case 161024: return "layer_norm_wgs<16, 1024>";
+    case 321024: return "layer_norm_wgs<32, 1024>";
+    default: break;
+  }
   return "layer_norm_block";
 }
 
@@ -211,6 +264,17 @@ hipError_t launch_layer_norm(hipStream_t s, long long rows, long long cols, floa
       case 16: hipLaunchKernelGGL((layer_norm_wg<16, 256>), grid, block, 0, s, in, out, (int)cols, eps); break;
       case 32: hipLaunchKernelGGL((layer_norm_wg<32, 256>), grid, block, 0, s, in, out, (int)cols, eps); break;
       default: hipLaunchKernelGGL((layer_norm_wg<16, 1024>), grid, dim3(1024), 0, s, in, out, (int)cols, eps); break;
+    }
+    return hipGetLastError();
+  }
+  if (pick_wgs(cols) > 0) {
+    const dim3 grid((unsigned)rows);
+    const int c = (int)cols;
+    switch (pick_wgs(cols)) {
+      case 40256: hipLaunchKernelGGL((layer_norm_wgs<4, 256>), grid, dim3(256), 0, s, in, out, c, eps); break;
+      case 160256: hipLaunchKernelGGL((layer_norm_wgs<16, 256>), grid, dim3(256), 0, s, in, out, c, eps); break;
+      case 161024: hipLaunchKernelGGL((layer_norm_wgs<16, 1024>), grid, dim3(1024), 0, s, in, out, c, eps); break;
+      default: hipLaunchKernelGGL((layer_norm_wgs<32, 1024>), grid, dim3(1024), 0, s, in, out, c, eps); break;
     }
     return hipGetLastError();
   }

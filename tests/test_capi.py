@@ -314,4 +314,5 @@ def test_elementwise_and_layer_norm_validation_before_device():
     assert lib.bch_layer_norm_kernel_name(3, 32768) == b"layer_norm_wg<32>"
     assert lib.bch_layer_norm_kernel_name(3, 32772) == b"layer_norm_wg<16, 1024>"
     assert lib.bch_layer_norm_kernel_name(3, 65540) == b"layer_norm_block"
-    assert lib.bch_layer_norm_kernel_name(3, 4099) == b"layer_norm_block"
+    assert lib.bch_layer_norm_kernel_name(3, 4099) == b"layer_norm_wgs<16, 1024>"
+    assert lib.bch_layer_norm_kernel_name(3, 32771) == b"layer_norm_block"

@@ -93,7 +93,9 @@ def test_elementwise_ops_exact(dev, offset, n):
                                        (3, 4100), (2, 10000), (1, 65536),
                                        # one workgroup per row, the row in registers (4096 < cols <= 32768)
                                        (5, 4104), (300, 8192), (64, 32768), (2, 32772), (40, 40000), (3, 65536),
-                                       (2, 65540)])
+                                       (2, 65540),
+                                       # other widths: scalar loads, the row in registers
+                                       (65, 2047), (300, 4099), (70, 30001)])
 def test_layer_norm_shapes(dev, rows, cols):
     _say(f"layer_norm rows={rows} cols={cols}")
     x = O.Lcg(rows * 7 + cols).normal((rows, cols), 1.5, 3.0)
