@@ -70,6 +70,8 @@ SIGNATURES = {
     "bch_layer_norm_kernel_name": (C.c_char_p, [_ll, _ll]),
     "bch_softmax_rows_f64_kernel_name": (C.c_char_p, [_ll, _ll, _vp, _vp]),
     "bch_softmax_axis": (_i, [_vp, _ll, _ll, _ll, _vp, _vp]),
+    "bch_head_split": (_i, [_vp, _i, _i, _i, _i, _vp, _vp]),
+    "bch_head_concat": (_i, [_vp, _i, _i, _i, _i, _vp, _vp]),
     "bch_sdpa_fwd": (_i, [_vp, _i, _i, _i, _i, _i, _f, _i, _vp, _vp, _vp, _vp]),
     "bch_sdpa_fwd_ex": (_i, [_vp, _i, _i, _i, _i, _i, _i, _f, _i, _vp, AttnLayout, _vp, AttnLayout, _vp,
                              AttnLayout, _vp, AttnLayout]),

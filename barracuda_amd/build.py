@@ -37,8 +37,8 @@ DEVICE_FLAGS = [
     "-Wall", "-Wno-unused-function", "-Wno-unused-result",
 ]
 SOURCES = ["bch_runtime.hip", "softmax_rows.hip", "sgemm_mfma.hip",
-           "sgemm_skinny.hip", "sdpa_fwd.hip", "dgemm_mfma.hip",
-           "rng_fill.hip", "copy.hip", "elementwise.hip", "layer_norm.hip",
+           "sgemm_skinny.hip", "sdpa_fwd.hip", "sdpa_wide.hip", "dgemm_mfma.hip",
+           "rng_fill.hip", "copy.hip", "elementwise.hip", "layer_norm.hip", "head_permute.hip",
            "softmax_f64.hip"]
 # Per-file code-generation flags.  The skinny GEMM keeps its MFMA
 # accumulators in VGPRs: with the default heuristics the compiler parks them

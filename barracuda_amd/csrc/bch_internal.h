@@ -191,6 +191,11 @@ hipError_t launch_layer_norm(hipStream_t s, long long rows, long long cols, floa
                              float* out);
 const char* layer_norm_kernel_name(long long rows, long long cols);
 
+// head_split (concat false): [B, S, H*D] -> [B, H, S, D]; head_concat
+// (concat true): the inverse.  in and out must not overlap.
+hipError_t launch_head_permute(hipStream_t s, bool concat, int B, int S, int H, int D, const float* in,
+                               float* out);
+
 // Device-to-device copy (16-byte path when aligned).
 hipError_t launch_copy(hipStream_t s, void* dst, const void* src, size_t bytes);
 
@@ -206,10 +211,23 @@ struct SdpaLayout {
 struct SdpaStrides {
   SdpaLayout q, k, v, o;
 };
+// The fused kernel serves D <= kSdpaFusedMaxD.
+constexpr int kSdpaFusedMaxD = 256;
 hipError_t launch_sdpa_strided(hipStream_t s, int B, int H, int Hkv, int Sq,
                                int Skv, int D, float scale, int causal,
                                const float* q, const float* k,
                                const float* v, float* o,
                                const SdpaStrides& st);
+// D > kSdpaFusedMaxD: scores materialised one query chunk at a time (GEMM,
+// scaled and masked row softmax, GEMM) in ws, which must hold
+// sdpa_wide_workspace_bytes(...) bytes (q_row, k_row: the row strides of q
+// and k; 0 when a row stride exceeds 2^31 - 1, which the launch rejects).
+size_t sdpa_wide_workspace_bytes(int Hkv, int Sq, int Skv, int D, int causal,
+                                 long long q_row, long long k_row);
+hipError_t launch_sdpa_wide(hipStream_t s, int B, int H, int Hkv, int Sq,
+                            int Skv, int D, float scale, int causal,
+                            const float* q, const float* k, const float* v,
+                            float* o, const SdpaStrides& st, void* ws,
+                            size_t ws_bytes);
 
 }  // namespace bch

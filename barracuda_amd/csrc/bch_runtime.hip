@@ -546,6 +546,33 @@ bch_status bch_layer_norm(bch_ctx* ctx, long long rows, long long cols, float ep
   return from_hip(ctx, bch::launch_layer_norm(ctx->stream, rows, cols, eps, in, out), "layer_norm launch");
 }
 
+namespace {
+
+bch_status head_permute(bch_ctx* ctx, bool concat, int B, int S, int H, int D, const float* in, float* out) {
+  const char* op = concat ? "head_concat" : "head_split";
+  if (B < 1 || S < 1 || H < 1 || D < 1)
+    return fail(ctx, BCH_E_SHAPE, "%s: empty dimension (B=%d, S=%d, H=%d, D=%d)", op, B, S, H, D);
+  if ((long long)H * D > 0x7fffffffLL || (long long)S * D > 0x7fffffffLL)
+    return fail(ctx, BCH_E_UNSUPPORTED, "%s: S*D or H*D above 2^31 - 1 (S=%d, H=%d, D=%d)", op, S, H, D);
+  if (!ctx) return fail(ctx, BCH_E_INVALID, "%s: ctx is NULL", op);
+  if (!in || !out) return fail(ctx, BCH_E_INVALID, "%s: NULL buffer", op);
+  if (in == out) return fail(ctx, BCH_E_INVALID, "%s: in and out must be different buffers", op);
+  bch_status st = use(ctx);
+  if (st != BCH_OK) return st;
+  return from_hip(ctx, bch::launch_head_permute(ctx->stream, concat, B, S, H, D, in, out),
+                  concat ? "head_concat launch" : "head_split launch");
+}
+
+}  // namespace
+
+bch_status bch_head_split(bch_ctx* ctx, int B, int S, int H, int D, const float* in, float* out) {
+  return head_permute(ctx, false, B, S, H, D, in, out);
+}
+
+bch_status bch_head_concat(bch_ctx* ctx, int B, int S, int H, int D, const float* in, float* out) {
+  return head_permute(ctx, true, B, S, H, D, in, out);
+}
+
 bch_status bch_softmax_axis(bch_ctx* ctx, long long outer, long long axis, long long inner,
                             const float* in, float* out) {
   if (outer < 1 || axis < 1 || inner < 1)
@@ -565,6 +592,33 @@ bch_status bch_softmax_axis(bch_ctx* ctx, long long outer, long long axis, long 
                   "softmax_dim launch");
 }
 
+namespace {
+
+// Both attention entry points after validation: the fused kernel up to
+// D = kSdpaFusedMaxD, the chunked three-step path (in the workspace) above.
+bch_status sdpa_run(bch_ctx* ctx, int B, int H, int Hkv, int Sq, int Skv, int D, float scale, int causal,
+                    const float* q, const float* k, const float* v, float* o, const bch::SdpaStrides& s) {
+  bch_status st = use(ctx);
+  if (st != BCH_OK) return st;
+  if (D <= bch::kSdpaFusedMaxD)
+    return from_hip(ctx, bch::launch_sdpa_strided(ctx->stream, B, H, Hkv, Sq, Skv, D, scale, causal, q, k, v, o, s),
+                    "attention launch");
+  if (s.q.row > 0x7fffffffLL || s.k.row > 0x7fffffffLL || s.v.row > 0x7fffffffLL || s.o.row > 0x7fffffffLL)
+    return fail(ctx, BCH_E_UNSUPPORTED, "attention: head dimension %d > %d needs row strides below 2^31", D,
+                bch::kSdpaFusedMaxD);
+  if (Hkv > 65535)
+    return fail(ctx, BCH_E_UNSUPPORTED, "attention: head dimension %d > %d needs at most 65535 key/value heads", D,
+                bch::kSdpaFusedMaxD);
+  st = ensure_ws(ctx, bch::sdpa_wide_workspace_bytes(Hkv, Sq, Skv, D, causal, s.q.row, s.k.row));
+  if (st != BCH_OK) return st;
+  return from_hip(ctx,
+                  bch::launch_sdpa_wide(ctx->stream, B, H, Hkv, Sq, Skv, D, scale, causal, q, k, v, o, s, ctx->ws,
+                                        ctx->ws_bytes),
+                  "attention launch");
+}
+
+}  // namespace
+
 bch_status bch_sdpa_fwd(bch_ctx* ctx, int B, int H, int Sq, int Skv, int D, float scale, int causal,
                         const float* q, const float* k, const float* v, float* o) {
   if (B < 1 || H < 1 || Sq < 1 || Skv < 1 || D < 1)
@@ -572,13 +626,12 @@ bch_status bch_sdpa_fwd(bch_ctx* ctx, int B, int H, int Sq, int Skv, int D, floa
                 Skv, D);
   if (causal && Sq != Skv)
     return fail(ctx, BCH_E_SHAPE, "attention: causal mask needs Sq == Skv (shape mismatch %d vs %d)", Sq, Skv);
-  if (D > 128) return fail(ctx, BCH_E_UNSUPPORTED, "attention: head dimension %d > 128", D);
   if (!ctx) return fail(ctx, BCH_E_INVALID, "attention: ctx is NULL");
   if (!q || !k || !v || !o) return fail(ctx, BCH_E_INVALID, "attention: NULL buffer");
-  bch_status st = use(ctx);
-  if (st != BCH_OK) return st;
-  return from_hip(ctx, bch::launch_sdpa(ctx->stream, B, H, Sq, Skv, D, scale, causal, q, k, v, o),
-                  "attention launch");
+  bch::SdpaStrides s;
+  s.q = s.o = bch::SdpaLayout{(long long)H * Sq * D, (long long)Sq * D, D};
+  s.k = s.v = bch::SdpaLayout{(long long)H * Skv * D, (long long)Skv * D, D};
+  return sdpa_run(ctx, B, H, H, Sq, Skv, D, scale, causal, q, k, v, o, s);
 }
 
 bch_status bch_sdpa_fwd_ex(bch_ctx* ctx, int B, int H, int Hkv, int Sq, int Skv, int D, float scale, int causal,
@@ -591,7 +644,6 @@ bch_status bch_sdpa_fwd_ex(bch_ctx* ctx, int B, int H, int Hkv, int Sq, int Skv,
     return fail(ctx, BCH_E_INVALID, "num_q_heads (%d) must be divisible by num_kv_heads (%d)", H, Hkv);
   if (causal && Sq != Skv)
     return fail(ctx, BCH_E_SHAPE, "attention: causal mask needs Sq == Skv (shape mismatch %d vs %d)", Sq, Skv);
-  if (D > 128) return fail(ctx, BCH_E_UNSUPPORTED, "attention: head dimension %d > 128", D);
   const bch_attn_layout* ls[4] = {&ql, &kl, &vl, &ol};
   for (int i = 0; i < 4; ++i)
     if (ls[i]->batch_stride < 0 || ls[i]->head_stride < 0 || ls[i]->row_stride < D)
@@ -601,15 +653,12 @@ bch_status bch_sdpa_fwd_ex(bch_ctx* ctx, int B, int H, int Hkv, int Sq, int Skv,
                   "qkvo"[i], ls[i]->batch_stride, ls[i]->head_stride, ls[i]->row_stride, D);
   if (!ctx) return fail(ctx, BCH_E_INVALID, "attention: ctx is NULL");
   if (!q || !k || !v || !o) return fail(ctx, BCH_E_INVALID, "attention: NULL buffer");
-  bch_status st = use(ctx);
-  if (st != BCH_OK) return st;
   bch::SdpaStrides s;
   s.q = {ql.batch_stride, ql.head_stride, ql.row_stride};
   s.k = {kl.batch_stride, kl.head_stride, kl.row_stride};
   s.v = {vl.batch_stride, vl.head_stride, vl.row_stride};
   s.o = {ol.batch_stride, ol.head_stride, ol.row_stride};
-  return from_hip(ctx, bch::launch_sdpa_strided(ctx->stream, B, H, Hkv, Sq, Skv, D, scale, causal, q, k, v, o, s),
-                  "attention launch");
+  return sdpa_run(ctx, B, H, Hkv, Sq, Skv, D, scale, causal, q, k, v, o, s);
 }
 
 bch_status bch_fill_uniform(bch_ctx* ctx, float* dst, size_t n, unsigned long long* state, double lo,

@@ -95,6 +95,7 @@ struct SdpaCfg {
   static constexpr int KD4 = DP / 4;                   // float4 per K row
   static constexpr int K_F4 = kBKV * DP / 4 / NT;      // float4 of K per thread
   static constexpr int V_BLK = kBKV * DP / 16;          // 4x4 V blocks per tile
+  static constexpr int V_PER = (V_BLK + NT - 1) / NT;    // 4x4 V blocks per thread
   static constexpr int LDS_FLOATS = 2 * (kBKV * KLD + DP * kVLD);
   static_assert(K_F4 >= 1, "K tile must cover the workgroup");
 };
@@ -107,7 +108,7 @@ using f32v = float __attribute__((ext_vector_type(N)));
 template <int DP, int NT>
 struct KvRegs {
   f32v<4 * SdpaCfg<DP, NT>::K_F4> k;
-  f32v<16> v;
+  f32v<16 * SdpaCfg<DP, NT>::V_PER> v;
 };
 
 // x combined with x from lane l ^ 32, the same value in both halves.
@@ -149,21 +150,25 @@ template <int DP, int NT, bool FULL>
 __device__ __forceinline__ void load_v(const float* __restrict__ vh, long long ldv, int Skv, int D, int kb, int tid,
                                        KvRegs<DP, NT>& r) {
   using G = SdpaCfg<DP, NT>;
-  const int blk = tid < G::V_BLK ? tid : 0;  // threads past the tile reload block 0 (unused)
-  const int kq = blk / G::KD4, dq = blk % G::KD4;
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int gk = kb + 4 * kq + e, d0 = 4 * dq;
-    float t[4];
-    if (FULL) {
-      const float4 x = get4(vh + gk * ldv + d0);
-      t[0] = x.x; t[1] = x.y; t[2] = x.z; t[3] = x.w;
-    } else {
+  for (int p = 0; p < G::V_PER; ++p) {
+    const int idx = tid + p * NT;
+    const int blk = idx < G::V_BLK ? idx : 0;  // threads past the tile reload block 0 (unused)
+    const int kq = blk / G::KD4, dq = blk % G::KD4;
 #pragma unroll
-      for (int c = 0; c < 4; ++c) t[c] = (gk < Skv && d0 + c < D) ? vh[gk * ldv + d0 + c] : 0.0f;
+    for (int e = 0; e < 4; ++e) {
+      const int gk = kb + 4 * kq + e, d0 = 4 * dq;
+      float t[4];
+      if (FULL) {
+        const float4 x = get4(vh + gk * ldv + d0);
+        t[0] = x.x; t[1] = x.y; t[2] = x.z; t[3] = x.w;
+      } else {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) t[c] = (gk < Skv && d0 + c < D) ? vh[gk * ldv + d0 + c] : 0.0f;
+      }
+#pragma unroll
+      for (int c = 0; c < 4; ++c) r.v[16 * p + 4 * e + c] = t[c];
     }
-#pragma unroll
-    for (int c = 0; c < 4; ++c) r.v[4 * e + c] = t[c];
   }
 }
 
@@ -178,18 +183,23 @@ __device__ __forceinline__ void store_kv(float* __restrict__ ks, float* __restri
     *reinterpret_cast<float4*>(ks + key * G::KLD + d0) =
         make_float4(r.k[4 * f], r.k[4 * f + 1], r.k[4 * f + 2], r.k[4 * f + 3]);
   }
-  if (tid < G::V_BLK) {
-    // transpose the 4(key) x 4(d) block: row d of Vt gets keys 4kq .. 4kq + 3
-    const int kq = tid / G::KD4, dq = tid % G::KD4;
-    float* base = vt + (4 * dq) * kVLD + 4 * kq;
 #pragma unroll
-    for (int c = 0; c < 4; ++c)
-      *reinterpret_cast<float4*>(base + c * kVLD) = make_float4(r.v[c], r.v[4 + c], r.v[8 + c], r.v[12 + c]);
+  for (int p = 0; p < G::V_PER; ++p) {
+    const int idx = tid + p * NT;
+    if (G::V_BLK % NT == 0 || idx < G::V_BLK) {
+      // transpose the 4(key) x 4(d) block: row d of Vt gets keys 4kq .. 4kq + 3
+      const int kq = idx / G::KD4, dq = idx % G::KD4;
+      float* base = vt + (4 * dq) * kVLD + 4 * kq;
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        *reinterpret_cast<float4*>(base + c * kVLD) =
+            make_float4(r.v[16 * p + c], r.v[16 * p + 4 + c], r.v[16 * p + 8 + c], r.v[16 * p + 12 + c]);
+    }
   }
 }
 
 template <int DP, bool FULL, int NT>
-__global__ __launch_bounds__(NT, 2) void sdpa_fwd_kernel(
+__global__ __launch_bounds__(NT, DP > 128 ? 1 : 2) void sdpa_fwd_kernel(
     int H, int group, int BH, int Sq, int Skv, int D, float qscale, int causal, const float* __restrict__ q,
     const float* __restrict__ k, const float* __restrict__ v, float* __restrict__ o, bch::SdpaStrides st,
     int qblocks) {
@@ -399,6 +409,10 @@ hipError_t launch_sdpa_strided(hipStream_t s, int B, int H, int Hkv, int Sq, int
   if (D <= 32) return launch_d<32>(s, B, H, Hkv, Sq, Skv, D, scale, causal, q, k, v, o, st);
   if (D <= 64) return launch_d<64>(s, B, H, Hkv, Sq, Skv, D, scale, causal, q, k, v, o, st);
   if (D <= 128) return launch_d<128>(s, B, H, Hkv, Sq, Skv, D, scale, causal, q, k, v, o, st);
+  if (D <= 160) return launch_d<160>(s, B, H, Hkv, Sq, Skv, D, scale, causal, q, k, v, o, st);
+  if (D <= 192) return launch_d<192>(s, B, H, Hkv, Sq, Skv, D, scale, causal, q, k, v, o, st);
+  if (D <= 224) return launch_d<224>(s, B, H, Hkv, Sq, Skv, D, scale, causal, q, k, v, o, st);
+  if (D <= 256) return launch_d<256>(s, B, H, Hkv, Sq, Skv, D, scale, causal, q, k, v, o, st);
   return hipErrorInvalidValue;
 }
 

@@ -10,6 +10,7 @@ Mirrors crates/barracuda/src/session/:
   TensorSession::softmax                                   session/mod.rs:364-371
   TensorSession::layer_norm                                session/mod.rs:379-398
   TensorSession::reshape                                   session/mod.rs:403-415
+  TensorSession::{head_split, head_concat}                 session/mod.rs:423-480
   TensorSession::attention                                 session/mod.rs:481-518
   TensorSession::run                                       session/mod.rs:521-540
   SessionTensor::{shape, len, is_empty, to_vec, to_tensor} session/tensor.rs:14-68
@@ -37,8 +38,10 @@ softmax(Q K^T / sqrt(D)) V over [B, H, S, D].
 
 The element-wise ops, ReLU and GELU run on bch_elementwise; layer_norm on
 bch_layer_norm with the epsilon the reference session passes (1e-5,
-dispatch.rs:221-240).  head_split / head_concat are not provided: the fused
-attention reads projection outputs through strides instead.
+dispatch.rs:221-240).  head_split / head_concat move [B, S, H*D] <-> [B, H, S, D]
+on bch_head_split / bch_head_concat (an HBM-streaming permutation, bit-exact),
+so the reference's recipe -- projection matmul, head_split, attention,
+head_concat, output matmul -- runs as recorded.  attention takes any head_dim.
 """
 from __future__ import annotations
 
@@ -257,6 +260,33 @@ class TensorSession:
             raise ShapeMismatch(new_shape, a._shape)
         return SessionTensor(self, a.buffer_id, new_shape)
 
+    def head_split(self, a: SessionTensor, dims: AttentionDims) -> SessionTensor:
+        """[B, S, H*D] -> [B, H, S, D] for multi-head attention (session/mod.rs:423-446):
+        InvalidInput when a's length is not B*S*H*D."""
+        return self._head_permute("head_split", a, dims, "B×S×H×D",
+                                  [dims.batch_size, dims.n_heads, dims.seq_len, dims.head_dim])
+
+    def head_concat(self, a: SessionTensor, dims: AttentionDims) -> SessionTensor:
+        """[B, H, S, D] -> [B, S, H*D] after multi-head attention (session/mod.rs:451-480):
+        InvalidInput when a's length is not B*H*S*D."""
+        return self._head_permute("head_concat", a, dims, "B×H×S×D",
+                                  [dims.batch_size, dims.seq_len, dims.n_heads * dims.head_dim])
+
+    def _head_permute(self, kind: str, a: SessionTensor, dims: AttentionDims, what: str,
+                      out_shape: list[int]) -> SessionTensor:
+        self._own(a)
+        expected = dims.total_elements()
+        if a.len() != expected:
+            raise InvalidInput(f"{kind}: input len {a.len()} ≠ {what}={expected}")
+        dims.as_u32()
+        _check_i32(kind, self.device, batch=dims.batch_size, heads=dims.n_heads, seq=dims.seq_len,
+                   head_dim=dims.head_dim, seq_x_head_dim=dims.seq_len * dims.head_dim,
+                   heads_x_head_dim=dims.n_heads * dims.head_dim)
+        out = self._alloc_output(out_shape)
+        self._ops.append((kind, a.buffer_id, out.buffer_id, dims.batch_size, dims.seq_len, dims.n_heads,
+                          dims.head_dim))
+        return out
+
     # -- ops ---------------------------------------------------------------
     def matmul(self, a: SessionTensor, b: SessionTensor) -> SessionTensor:
         """output[m x n] = a[m x k] b[k x n] (session/mod.rs:305-333)."""
@@ -292,9 +322,8 @@ class TensorSession:
             if t.len() != expected:
                 raise InvalidInput(f"attention: {name} len {t.len()} ≠ B×H×S×D={expected}")
         dims.as_u32()
-        if dims.head_dim > 128:
-            raise UnsupportedOperation("attention", f"{self.device.name()} (head_dim {dims.head_dim} > 128)")
-        _check_i32("attention", self.device, batch=dims.batch_size, heads=dims.n_heads, seq=dims.seq_len)
+        _check_i32("attention", self.device, batch=dims.batch_size, heads=dims.n_heads, seq=dims.seq_len,
+                   head_dim=dims.head_dim)
         out = self._alloc_output([dims.batch_size, dims.n_heads, dims.seq_len, dims.head_dim])
         self._ops.append(("attention", q.buffer_id, k.buffer_id, v.buffer_id, out.buffer_id,
                           dims.batch_size, dims.n_heads, dims.seq_len, dims.head_dim))
@@ -340,6 +369,11 @@ class TensorSession:
                         scale = float(np.float32(1.0) / np.sqrt(np.float32(d)))
                         dev.check(lib.bch_sdpa_fwd(ctx, b, h, s, s, d, scale, 0, ptr[q], ptr[k], ptr[v],
                                                    ptr[o]), "attention")
+                elif kind in ("head_split", "head_concat"):
+                    _, a, o, b, s, h, d = op
+                    if b * s * h * d:
+                        fn = lib.bch_head_split if kind == "head_split" else lib.bch_head_concat
+                        dev.check(fn(ctx, b, s, h, d, ptr[a], ptr[o]), kind)
                 else:  # pragma: no cover - ops are only appended above
                     raise ExecutionError(f"unknown session op {kind}")
             dev.check(lib.bch_sync(ctx), "run")

@@ -493,9 +493,7 @@ class LayerNorm:
 
 def _sdpa(dev: HipDevice, q: Tensor, k: Tensor, v: Tensor, causal: bool, op: str,
           b: int, h: int, sq: int, skv: int, d: int) -> Tensor:
-    if d > 128:
-        raise UnsupportedOperation(op, f"{dev.name()} (head_dim {d} > 128)")
-    _check_i32(op, dev, batch=b, heads=h, q_len=sq, kv_len=skv)
+    _check_i32(op, dev, batch=b, heads=h, q_len=sq, kv_len=skv, head_dim=d)
     out = Tensor.empty(q.shape(), dev)
     if b * h * sq * d == 0:
         return out
@@ -605,9 +603,7 @@ def _sdpa_ex(dev: HipDevice, op: str, b: int, h: int, hkv: int, sq: int, skv: in
              q: Tensor, ql: N.AttnLayout, k: Tensor, kl: N.AttnLayout, v: Tensor, vl: N.AttnLayout,
              o: Tensor, ol: N.AttnLayout) -> None:
     """bch_sdpa_fwd_ex: strided operands, hkv key/value heads, scale 1/sqrt(d)."""
-    if d > 128:
-        raise UnsupportedOperation(op, f"{dev.name()} (head_dim {d} > 128)")
-    _check_i32(op, dev, batch=b, heads=h, kv_heads=hkv, q_len=sq, kv_len=skv)
+    _check_i32(op, dev, batch=b, heads=h, kv_heads=hkv, q_len=sq, kv_len=skv, head_dim=d)
     if b * h * sq * d == 0:
         return
     if skv == 0:

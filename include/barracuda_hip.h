@@ -239,6 +239,20 @@ bch_status bch_elementwise(bch_ctx *ctx, int op, long long n, const float *a,
 bch_status bch_layer_norm(bch_ctx *ctx, long long rows, long long cols,
                           float eps, const float *in, float *out);
 
+/* Multi-head layout changes of TensorSession (session/mod.rs:423-480):
+ *   bch_head_split:  in [B, S, H*D] -> out [B, H, S, D]
+ *                    (out[b][h][s][d] = in[b][s][h*D + d],
+ *                    shaders/tensor/head_split_f64.wgsl)
+ *   bch_head_concat: in [B, H, S, D] -> out [B, S, H*D]
+ *                    (the inverse map, head_concat_f64.wgsl)
+ * Dense f32 buffers; in and out must not overlap (BCH_E_INVALID when
+ * in == out).  Bit-exact copies (HBM-streaming, 8 bytes per element).
+ * Dimensions >= 1; B*S*H*D*4 bytes each. */
+bch_status bch_head_split(bch_ctx *ctx, int B, int S, int H, int D,
+                          const float *in, float *out);
+bch_status bch_head_concat(bch_ctx *ctx, int B, int S, int H, int D,
+                           const float *in, float *out);
+
 /* Softmax along a middle axis of a tensor viewed as [outer, axis, inner]
  * (element (o,j,i) at (o*axis + j)*inner + i).  inner == 1 is the row case.
  * Replaces Tensor::softmax_dim (ops/tensor_axis_ops.rs:67-126) for
@@ -252,8 +266,12 @@ bch_status bch_softmax_axis(bch_ctx *ctx, long long outer, long long axis,
  *   o[b,h,i,:] = sum_j softmax_j(scale * q_i . k_j) v_j
  * with j <= i when causal (causal requires Sq == Skv, as the reference's
  * causal ops take one seq_len).  Non-causal Sq may differ from Skv
- * (cross-attention).  1 <= D <= 128.  Never materialises the
- * Sq x Skv score matrix.  Replaces Attention::execute (ops/attention/
+ * (cross-attention).  Any D >= 1, as the reference's ops take: up to
+ * D = 256 one fused kernel that never materialises the Sq x Skv score
+ * matrix and uses no scratch; above D = 256 the scores of one chunk of
+ * query rows at a time (at most 256 MiB) go through the context's
+ * workspace (grown on demand, like the GEMM's) in three steps -- Q K^T,
+ * scaled and masked row softmax, P V -- on the MFMA GEMM.  Replaces Attention::execute (ops/attention/
  * compute.rs:21-111: K6 attention_matmul_f64.wgsl -> K7 -> K9
  * attention_apply_f64.wgsl), ScaledDotProductAttention (ops/
  * scaled_dot_product_attention/compute.rs:19-108), CausalAttention (ops/
@@ -278,7 +296,8 @@ typedef struct bch_attn_layout {
  * the H query heads (query head h reads key/value head h / (H / Hkv);
  * H % Hkv == 0, else BCH_E_INVALID "num_q_heads (H) must be divisible by
  * num_kv_heads (Hkv)").  q, o have H heads and Sq rows; k, v have Hkv heads
- * and Skv rows.  Strides >= 0, row_stride >= D.  Replaces
+ * and Skv rows.  Strides >= 0, row_stride >= D (and below 2^31 when
+ * D > 256).  Replaces
  * GroupedQueryAttention::execute (ops/grouped_query_attention/compute.rs:
  * 27-121: gqa_matmul_f64.wgsl -> gqa_softmax_f64.wgsl -> gqa_apply_f64.wgsl;
  * validation mod.rs:84-147) with Hkv < H, and the attention core of

@@ -440,8 +440,7 @@ namespace detail {
 inline Result<Tensor> sdpa(const Tensor& q, const Tensor& k, const Tensor& v, bool causal, const char* op, size_t B,
                            size_t H, size_t Sq, size_t Skv, size_t D) {
   auto dev = q.device();
-  if (D > 128) return BarracudaError::unsupported(op, dev->name() + " (head_dim " + std::to_string(D) + " > 128)");
-  if (auto e = check_i32(op, {B, H, Sq, Skv})) return *e;
+  if (auto e = check_i32(op, {B, H, Sq, Skv, D})) return *e;
   auto r = Tensor::empty(q.shape(), dev);
   if (r.is_err() || (size_t)B * H * Sq * D == 0) return r;
   if (Skv == 0) return BarracudaError::invalid_op(op, "key sequence is empty (shape/dimension mismatch)");
@@ -556,8 +555,7 @@ inline std::optional<BarracudaError> sdpa_ex(const std::shared_ptr<HipDevice>& d
                                              const Tensor& q, bch_attn_layout ql, const Tensor& k,
                                              bch_attn_layout kl, const Tensor& v, bch_attn_layout vl,
                                              const Tensor& o, bch_attn_layout ol) {
-  if (D > 128) return BarracudaError::unsupported(op, dev->name() + " (head_dim " + std::to_string(D) + " > 128)");
-  if (auto e = check_i32(op, {B, H, Hkv, Sq, Skv})) return *e;
+  if (auto e = check_i32(op, {B, H, Hkv, Sq, Skv, D})) return *e;
   if (B * H * Sq * D == 0) return std::nullopt;
   if (Skv == 0) return BarracudaError::invalid_op(op, "key sequence is empty (shape/dimension mismatch)");
   const float scale = 1.0f / std::sqrt((float)D);
@@ -1017,6 +1015,15 @@ class TensorSession {
     return out;
   }
 
+  // session/mod.rs:423-446: [B, S, H*D] -> [B, H, S, D] (head_split_f64.wgsl)
+  Result<SessionTensor> head_split(const SessionTensor& a, const AttentionDims& dims) {
+    return head_permute(false, a, dims);
+  }
+  // session/mod.rs:451-480: [B, H, S, D] -> [B, S, H*D] (head_concat_f64.wgsl)
+  Result<SessionTensor> head_concat(const SessionTensor& a, const AttentionDims& dims) {
+    return head_permute(true, a, dims);
+  }
+
   // session/mod.rs:481-518: softmax(Q K^T / sqrt(D)) V over [B, H, S, D]
   Result<SessionTensor> attention(const SessionTensor& q, const SessionTensor& k, const SessionTensor& v,
                                   const AttentionDims& dims) {
@@ -1028,10 +1035,8 @@ class TensorSession {
         return BarracudaError::invalid_input(std::string("attention: ") + name + " len " + std::to_string(t->len()) +
                                              " ≠ B×H×S×D=" + std::to_string(expected));
     if (auto e = dims.as_u32(); e.is_err()) return e.error();
-    if (dims.head_dim > 128)
-      return BarracudaError::unsupported("attention",
-                                         dev_->name() + " (head_dim " + std::to_string(dims.head_dim) + " > 128)");
-    if (auto e = detail::check_i32("attention", {dims.batch_size, dims.n_heads, dims.seq_len})) return *e;
+    if (auto e = detail::check_i32("attention", {dims.batch_size, dims.n_heads, dims.seq_len, dims.head_dim}))
+      return *e;
     auto out = alloc_output({dims.batch_size, dims.n_heads, dims.seq_len, dims.head_dim});
     if (out.is_ok())
       ops_.push_back({Op::Attention, {q.id_, k.id_, v.id_, out.value().id_},
@@ -1069,6 +1074,16 @@ class TensorSession {
                               p(op.buf[0]), p(op.buf[1]), p(op.buf[2]), p(op.buf[3]));
           break;
         }
+        case Op::HeadSplit:
+        case Op::HeadConcat: {
+          const size_t B = op.dim[0], S = op.dim[1], H = op.dim[2], D = op.dim[3];
+          const bool concat = op.kind == Op::HeadConcat;
+          name = concat ? "head_concat" : "head_split";
+          if (B * S * H * D != 0)
+            st = (concat ? bch_head_concat : bch_head_split)(c, (int)B, (int)S, (int)H, (int)D, p(op.buf[0]),
+                                                              p(op.buf[1]));
+          break;
+        }
       }
       if (auto e = dev_->check(st, name)) return *e;
     }
@@ -1079,10 +1094,29 @@ class TensorSession {
 
  private:
   struct Op {
-    enum Kind { MatMul, Softmax, Attention } kind;
+    enum Kind { MatMul, Softmax, Attention, HeadSplit, HeadConcat } kind;
     size_t buf[4];
     size_t dim[4];
   };
+
+  Result<SessionTensor> head_permute(bool concat, const SessionTensor& a, const AttentionDims& dims) {
+    if (auto e = own({&a})) return *e;
+    const char* op = concat ? "head_concat" : "head_split";
+    const size_t expected = dims.total_elements();
+    if (a.len() != expected)
+      return BarracudaError::invalid_input(std::string(op) + ": input len " + std::to_string(a.len()) + " ≠ " +
+                                           (concat ? "B×H×S×D=" : "B×S×H×D=") + std::to_string(expected));
+    if (auto e = dims.as_u32(); e.is_err()) return e.error();
+    if (auto e = detail::check_i32(op, {dims.batch_size, dims.n_heads, dims.seq_len, dims.head_dim,
+                                        dims.seq_len * dims.head_dim, dims.n_heads * dims.head_dim}))
+      return *e;
+    auto out = concat ? alloc_output({dims.batch_size, dims.seq_len, dims.n_heads * dims.head_dim})
+                      : alloc_output({dims.batch_size, dims.n_heads, dims.seq_len, dims.head_dim});
+    if (out.is_ok())
+      ops_.push_back({concat ? Op::HeadConcat : Op::HeadSplit, {a.id_, out.value().id_, 0, 0},
+                      {dims.batch_size, dims.seq_len, dims.n_heads, dims.head_dim}});
+    return out;
+  }
 
   Result<std::shared_ptr<detail::DeviceBuffer>> alloc(const std::vector<size_t>& shape, bool zero) {
     auto buf = std::make_shared<detail::DeviceBuffer>();

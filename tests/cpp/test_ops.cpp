@@ -498,6 +498,42 @@ void gpu_tests() {
     auto got = sc.to_vec().unwrap();
     for (size_t i = 0; i < ref.size(); ++i) REQUIRE(std::fabs(got[i] - ref[i]) <= 1e-4f * std::fmax(1.0f, std::fabs(ref[i])));
   });
+  run("test_session_head_split_concat", [] {  // session/mod.rs:423-480 with the recipe of :481-518
+    const size_t B = 2, S = 5, H = 3, D = 6;
+    std::vector<float> x(B * S * H * D);
+    for (size_t i = 0; i < x.size(); ++i) x[i] = (float)i;  // exact in f32
+    TensorSession s(g_dev);
+    AttentionDims dims{B, H, S, D};
+    auto in = s.tensor_with_shape(x, {B, S, H * D}).unwrap();
+    auto split = s.head_split(in, dims).unwrap();
+    REQUIRE((split.shape() == std::vector<size_t>{B, H, S, D}));
+    auto att = s.attention(split, split, split, dims).unwrap();
+    auto back = s.head_concat(split, dims).unwrap();
+    auto cat = s.head_concat(att, dims).unwrap();
+    REQUIRE((back.shape() == std::vector<size_t>{B, S, H * D}));
+    REQUIRE(s.num_ops() == 4);
+    s.run().unwrap();
+    auto sp = split.to_vec().unwrap();
+    for (size_t b = 0; b < B; ++b)
+      for (size_t h = 0; h < H; ++h)
+        for (size_t t = 0; t < S; ++t)
+          for (size_t d = 0; d < D; ++d)  // head_split_f64.wgsl: out[b][h][s][d] = in[b][s][h*D + d]
+            REQUIRE(sp[((b * H + h) * S + t) * D + d] == x[(b * S + t) * H * D + h * D + d]);
+    REQUIRE(back.to_vec().unwrap() == x);  // head_concat inverts head_split
+    // the concat of attention output equals attention on the Tensor API then the same permutation
+    auto ref = T(sp, {B, H, S, D}).attention(T(sp, {B, H, S, D}), T(sp, {B, H, S, D})).unwrap().to_vec().unwrap();
+    auto got = cat.to_vec().unwrap();
+    for (size_t b = 0; b < B; ++b)
+      for (size_t h = 0; h < H; ++h)
+        for (size_t t = 0; t < S; ++t)
+          for (size_t d = 0; d < D; ++d)
+            REQUIRE(got[(b * S + t) * H * D + h * D + d] == ref[((b * H + h) * S + t) * D + d]);
+    auto bad = s.tensor(std::vector<float>(7)).unwrap();
+    auto e = s.head_split(bad, dims);
+    REQUIRE(e.is_err() && e.error().message == "Invalid input: head_split: input len 7 ≠ B×S×H×D=180");
+    e = s.head_concat(bad, dims);
+    REQUIRE(e.is_err() && e.error().message == "Invalid input: head_concat: input len 7 ≠ B×H×S×D=180");
+  });
   run("test_session_validation", [] {
     TensorSession s(g_dev);
     auto r = s.tensor_with_shape({0, 0, 0, 0, 0}, {2, 3});

@@ -90,7 +90,9 @@ def test_null_and_shape_errors_before_device():
     assert lib.bch_softmax_axis(nul, 1, 0, 1, nul, nul) == N.BCH_E_SHAPE
     assert lib.bch_sdpa_fwd(nul, 1, 1, 4, 8, 16, 0.25, 1, nul, nul, nul, nul) == N.BCH_E_SHAPE
     assert "causal" in N.last_error(None)
-    assert lib.bch_sdpa_fwd(nul, 1, 1, 4, 4, 256, 0.25, 0, nul, nul, nul, nul) == N.BCH_E_UNSUPPORTED
+    # any head dimension is accepted (the reference's ops take any); only the NULL ctx fails here
+    assert lib.bch_sdpa_fwd(nul, 1, 1, 4, 4, 512, 0.25, 0, nul, nul, nul, nul) == N.BCH_E_INVALID
+    assert "ctx is NULL" in N.last_error(None)
     assert lib.bch_sdpa_fwd(nul, 0, 1, 4, 4, 16, 0.25, 0, nul, nul, nul, nul) == N.BCH_E_SHAPE
     grid = (C.c_uint * 3)(1, 1, 1)
     assert lib.bch_launch_code_object(nul, None, 0, b"x", grid, grid, None, 0, 0) == N.BCH_E_INVALID

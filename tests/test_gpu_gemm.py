@@ -335,15 +335,22 @@ def test_config_4096_cubed(dev):
     a = rng.uniform((4096, 4096))
     b = rng.uniform((4096, 4096))
     got = _mm(dev, a, b)
-    rows = [0, 1, 127, 128, 2047, 2048, 4095] + list(range(513, 4096, 257))
+    # one row in each of the 16 tile rows of 256 (the position inside the tile
+    # moves with the tile) plus edge and interior rows: every 256x256 output
+    # tile has a whole checked row
+    rows = sorted({0, 1, 127, 128, 2047, 2048, 4095} | set(range(513, 4096, 257)) |
+                  {t * 256 + (t * 37 + 11) % 256 for t in range(16)})
     ref = O.matmul_f64(a, b, rows=rows)
     err = O.max_rel_err(got[rows], ref)
-    _say(f"  max rel err (sampled rows) = {err:.3e}")
+    _say(f"  max rel err ({len(rows)} sampled rows) = {err:.3e}")
     assert err <= TOL
-    # a column sample too: C[:, j] = A @ B[:, j]
-    cols = [0, 31, 32, 4000, 4095]
+    # and one column in each of the 16 tile columns: C[:, j] = A @ B[:, j]
+    cols = sorted({0, 31, 32, 4000, 4095} | {t * 256 + (t * 53 + 29) % 256 for t in range(16)})
     refc = a.astype(np.float64) @ b[:, cols].astype(np.float64)
-    assert O.max_rel_err(got[:, cols], refc) <= TOL
+    errc = O.max_rel_err(got[:, cols], refc)
+    _say(f"  max rel err ({len(cols)} sampled columns) = {errc:.3e}")
+    assert errc <= TOL
+    assert {r // 256 for r in rows} == set(range(16)) and {c // 256 for c in cols} == set(range(16))
 
 
 def test_config_batched_16x1024(dev):

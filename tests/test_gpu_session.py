@@ -13,8 +13,7 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
-from barracuda_amd import (AttentionDims, InvalidInput, InvalidShape, ShapeMismatch, Tensor, TensorSession,
-                           UnsupportedOperation)
+from barracuda_amd import AttentionDims, InvalidInput, InvalidShape, ShapeMismatch, Tensor, TensorSession
 from oracle import bc_oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -95,6 +94,65 @@ def test_session_attention_full_seq(dev):
     assert O.max_rel_err(got[heads], ref) <= TOL
 
 
+@pytest.mark.parametrize("B,S,H,D", [(2, 5, 3, 6), (2, 64, 8, 64), (1, 33, 4, 129), (3, 17, 2, 256), (1, 1, 1, 1),
+                                     (2, 2048, 16, 128)])
+def test_session_head_split_concat_bit_exact(dev, B, S, H, D):
+    """head_split [B, S, H*D] -> [B, H, S, D] and head_concat back
+    (session/mod.rs:423-480; head_split_f64.wgsl reads element (b, s, h*D + d)
+    for output (b, h, s, d)): bit-exact against numpy's transpose, float4 and
+    scalar paths (D % 4 != 0), and concat(split(x)) == x."""
+    _say(f"session head_split/concat B={B} S={S} H={H} D={D}")
+    x = O.Lcg(B + S + H + D).normal((B, S, H * D))
+    y = O.Lcg(7 + B + S + H + D).normal((B, H, S, D))
+    s = TensorSession(dev)
+    dims = AttentionDims(B, H, S, D)
+    sp = s.head_split(s.tensor_with_shape(x, [B, S, H * D]), dims)
+    back = s.head_concat(sp, dims)
+    cat = s.head_concat(s.tensor_with_shape(y, [B, H, S, D]), dims)
+    assert sp.shape() == [B, H, S, D] and back.shape() == [B, S, H * D] and cat.shape() == [B, S, H * D]
+    s.run()
+    want = x.reshape(B, S, H, D).transpose(0, 2, 1, 3)
+    assert np.array_equal(sp.to_vec().reshape(B, H, S, D), want)
+    assert np.array_equal(back.to_vec().reshape(B, S, H * D), x)
+    assert np.array_equal(cat.to_vec().reshape(B, S, H, D), y.transpose(0, 2, 1, 3))
+
+
+@pytest.mark.parametrize("B,S,Dm,H", [(2, 64, 256, 4), (1, 100, 512, 1), (2, 40, 96, 3)])
+def test_session_mha_recipe(dev, B, S, Dm, H):
+    """The reference session's multi-head recipe (session/mod.rs:481-518: "use
+    head_split after projection"): projection matmuls, head_split, attention,
+    head_concat, output matmul, in one run(), against the f64 multi-head
+    attention oracle (projections [D, D], scale 1/sqrt(D/H))."""
+    _say(f"session mha recipe B={B} S={S} Dm={Dm} H={H}")
+    rng = O.Lcg(B * 3 + S + Dm + H)
+    x = rng.normal((B, S, Dm))
+    ws = [rng.normal((Dm, Dm), 0.0, 1.0 / np.sqrt(Dm)) for _ in range(4)]
+    s = TensorSession(dev)
+    hd = Dm // H
+    dims = AttentionDims(B, H, S, hd)
+    tx = s.tensor_with_shape(x.reshape(B * S, Dm), [B * S, Dm])
+    tw = [s.tensor_with_shape(w, [Dm, Dm]) for w in ws]
+    heads = [s.head_split(s.matmul(tx, tw[i]), dims) for i in range(3)]
+    att = s.attention(*heads, dims)
+    cat = s.reshape(s.head_concat(att, dims), [B * S, Dm])
+    out = s.matmul(cat, tw[3])
+    assert s.num_ops() == 9
+    s.run()
+    assert O.max_rel_err(out.to_vec().reshape(B, S, Dm), O.mha_f64(x, x, x, *ws, H)) <= TOL
+
+
+def test_session_attention_wide_head(dev):
+    """attention at head_dim 256 and 512 (any head_dim, as the reference's session takes)."""
+    for (B, H, S, D) in [(1, 2, 70, 256), (1, 1, 40, 512)]:
+        _say(f"session attention {B}x{H}x{S}x{D}")
+        rng = O.Lcg(B + H * 5 + S * 11 + D)
+        q, k, v = (rng.normal((B, H, S, D)) for _ in range(3))
+        s = TensorSession(dev)
+        o = s.attention(s.tensor(q), s.tensor(k), s.tensor(v), AttentionDims(B, H, S, D))
+        s.run()
+        assert O.max_rel_err(o.to_vec().reshape(B, H, S, D), O.sdpa_f64(q, k, v, False)) <= TOL
+
+
 def test_session_chain_one_run(dev):
     """Ops read earlier outputs in recording order within one run()."""
     _say("session chain")
@@ -172,8 +230,10 @@ def test_session_validation(dev):
     dims = AttentionDims(1, 2, 4, 2)
     with pytest.raises(InvalidInput, match="attention: k len 15 ≠ B×H×S×D=16"):
         s.attention(q, bad, q, dims)
-    with pytest.raises(UnsupportedOperation):
-        s.attention(*(s.tensor([0.0] * 256) for _ in range(3)), AttentionDims(1, 1, 1, 256))
+    with pytest.raises(InvalidInput, match="head_split: input len 15 ≠ B×S×H×D=16"):
+        s.head_split(bad, dims)
+    with pytest.raises(InvalidInput, match="head_concat: input len 15 ≠ B×H×S×D=16"):
+        s.head_concat(bad, dims)
     other = TensorSession(dev)
     with pytest.raises(InvalidInput):
         s.softmax(other.tensor([1.0]))
