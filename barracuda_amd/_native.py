@@ -48,6 +48,8 @@ SIGNATURES = {
     "bch_ctx_destroy": (None, [_vp]),
     "bch_ctx_is_lost": (_i, [_vp, C.POINTER(_i)]),
     "bch_ctx_stream": (_i, [_vp, C.POINTER(_vp)]),
+    "bch_ctx_reserve": (_i, [_vp, _sz]),
+    "bch_ctx_workspace_bytes": (_i, [_vp, C.POINTER(_sz)]),
     "bch_last_error": (C.c_char_p, [_vp]),
     "bch_status_string": (C.c_char_p, [_i]),
     "bch_alloc": (_i, [_vp, _sz, C.POINTER(_vp)]),

@@ -21,6 +21,7 @@
 #include <set>
 #include <tuple>
 #include <string>
+#include <vector>
 
 #include "../../include/barracuda_hip.h"
 #include "bch_internal.h"
@@ -41,6 +42,11 @@ struct bch_ctx {
   std::map<std::string, hipModule_t> modules;
   void* ws = nullptr;
   size_t ws_bytes = 0;
+  // Set once the context's stream has been seen under capture: a workspace
+  // replaced after that may still be read by a captured graph, so it is kept
+  // (in `retired`) until bch_ctx_destroy instead of being freed.
+  bool seen_capture = false;
+  std::vector<void*> retired;
   // Sticky: set by the first HIP error that leaves the device context
   // unusable (a kernel fault, an ECC error); every later call that would
   // touch the device fails with BCH_E_DEVICE_LOST.  The reference flags its
@@ -120,6 +126,17 @@ bch_status from_hip(bch_ctx* ctx, hipError_t e, const char* what) {
   return fail(ctx, st, "%s: %s (%d)", what, hipGetErrorString(e), (int)e);
 }
 
+// The context's stream is being captured into a graph (or a capture on it
+// was invalidated and not yet ended).
+bool capturing(bch_ctx* ctx) {
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(ctx->stream, &cs) != hipSuccess) {
+    (void)hipGetLastError();
+    return false;
+  }
+  return cs != hipStreamCaptureStatusNone;
+}
+
 // Every call that touches the device starts here.
 bch_status use(bch_ctx* ctx) {
   if (ctx->lost) return fail(ctx, BCH_E_DEVICE_LOST, "device lost: %s", ctx->lost_reason.c_str());
@@ -129,7 +146,9 @@ bch_status use(bch_ctx* ctx) {
     return from_hip(ctx, e, "injected by BARRACUDA_HIP_INJECT_HIP_ERROR");
   }
   hipError_t e = hipSetDevice(ctx->device);
-  return from_hip(ctx, e, "hipSetDevice");
+  if (e != hipSuccess) return from_hip(ctx, e, "hipSetDevice");
+  if (capturing(ctx)) ctx->seen_capture = true;
+  return BCH_OK;
 }
 
 std::string lib_dir() {
@@ -144,10 +163,20 @@ std::string lib_dir() {
 
 bch_status ensure_ws(bch_ctx* ctx, size_t bytes) {
   if (bytes <= ctx->ws_bytes) return BCH_OK;
+  // Growing allocates, and under capture it would also record the clear into
+  // the caller's graph and leave earlier captures reading freed memory.
+  if (capturing(ctx))
+    return fail(ctx, BCH_E_UNSUPPORTED,
+                "workspace of %zu bytes needed while the context's stream is being captured (it holds %zu): "
+                "size it before the capture (an eager call or bch_ctx_reserve) or use bch_sgemm_noalloc",
+                bytes, ctx->ws_bytes);
   if (ctx->ws) {
     hipError_t e = hipStreamSynchronize(ctx->stream);
     if (e != hipSuccess) return from_hip(ctx, e, "hipStreamSynchronize");
-    (void)hipFree(ctx->ws);
+    if (ctx->seen_capture)
+      ctx->retired.push_back(ctx->ws);  // captured graphs may still read it
+    else
+      (void)hipFree(ctx->ws);
     ctx->ws = nullptr;
     ctx->ws_bytes = 0;
   }
@@ -273,12 +302,27 @@ bch_status bch_ctx_stream(const bch_ctx* ctx, void** stream) {
   return BCH_OK;
 }
 
+bch_status bch_ctx_reserve(bch_ctx* ctx, size_t bytes) {
+  if (!ctx) return fail(ctx, BCH_E_INVALID, "bch_ctx_reserve: ctx is NULL");
+  if (bytes <= ctx->ws_bytes) return BCH_OK;
+  bch_status st = use(ctx);
+  if (st != BCH_OK) return st;
+  return ensure_ws(ctx, bytes);
+}
+
+bch_status bch_ctx_workspace_bytes(const bch_ctx* ctx, size_t* bytes) {
+  if (!ctx || !bytes) return fail(nullptr, BCH_E_INVALID, "bch_ctx_workspace_bytes: NULL argument");
+  *bytes = ctx->ws_bytes;
+  return BCH_OK;
+}
+
 void bch_ctx_destroy(bch_ctx* ctx) {
   if (!ctx) return;
   (void)hipSetDevice(ctx->device);
   if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
   for (auto& kv : ctx->modules) (void)hipModuleUnload(kv.second);
   if (ctx->ws) (void)hipFree(ctx->ws);
+  for (void* p : ctx->retired) (void)hipFree(p);
   if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
   delete ctx;
 }

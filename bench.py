@@ -442,6 +442,23 @@ def _bench_sdpa(dev, T, reps):
     out["gqa_hkv8_noncausal"] = {"ms": ev, "TFLOP/s": fl / (ev * 1e-3) / 1e12,
                                  "mfma_frac": fl / (ev * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS}
     del q, kg, vg, o
+    # config 5's shape at wider heads (the reference's attention ops take any head_dim): D = 256 on
+    # the fused kernel's widest instance, D = 512 on the chunked GEMM / softmax / GEMM path
+    for Dw in (256, 512):
+        s = LcgStream(4, dev)
+        q, k, v = (s.normal([Bb, H, S, Dw]) for _ in range(3))
+        o = Tensor.empty([Bb, H, S, Dw], dev)
+        pq, pk, pv, po = (C.c_void_p(t.ptr) for t in (q, k, v, o))
+        scale = 1.0 / math.sqrt(Dw)
+        for causal in (0, 1):
+            wall, ev = T.run(lambda i: lib.bch_sdpa_fwd(ctx, Bb, H, S, S, Dw, scale, causal, pq, pk, pv, po),
+                             max(5, reps // 2), 2)
+            fl = 4.0 * Bb * H * S * S * Dw if not causal else 4.0 * Bb * H * (S * (S + 1) / 2) * Dw
+            key = f"sdpa_d{Dw}_{'causal' if causal else 'noncausal'}"
+            out[key] = {"ms": ev, "TFLOP/s": fl / (ev * 1e-3) / 1e12,
+                        "mfma_frac": fl / (ev * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS,
+                        "path": "fused" if Dw <= 256 else "chunked (GEMM, masked softmax, GEMM)"}
+        del q, k, v, o
     return out
 
 

@@ -78,14 +78,22 @@ bch_status bch_ctx_is_lost(const bch_ctx *ctx, int *lost);
  * the reference, whose wgpu queue is internal: it is for callers that order
  * the context's work against their own streams or capture it into a HIP
  * graph.  Capture only calls whose workspace already exists (make each call
- * once outside the capture first): a call that has to grow the workspace
- * allocates.  Growing it also frees the previous workspace, which graphs
- * captured earlier still read: once a graph exists, make no call on the
- * context that needs a larger workspace than its captured calls did (size
- * the workspace with the largest call first).  Every captured call replays
- * correctly any number of times; replays and eager calls on one context
- * must not overlap (they share the workspace). */
+ * once outside the capture first, or bch_ctx_reserve): a call that would
+ * have to grow the workspace while the stream is being captured fails with
+ * BCH_E_UNSUPPORTED and enqueues nothing.  Once a capture has been seen on
+ * the context, a later eager call that grows the workspace keeps the old
+ * one alive (captured graphs still read it) until bch_ctx_destroy.  Every
+ * captured call replays correctly any number of times; replays and eager
+ * calls on one context must not overlap (they share the workspace). */
 bch_status bch_ctx_stream(const bch_ctx *ctx, void **stream);
+
+/* Grow the context's workspace to at least `bytes` now (outside any
+ * capture), so that later calls -- captured or not -- need no allocation.
+ * *bytes = the workspace's current size (0 for a fresh context).  No
+ * counterpart in the reference (its buffer pool is internal); for callers
+ * that capture the context's work or must not allocate in a hot loop. */
+bch_status bch_ctx_reserve(bch_ctx *ctx, size_t bytes);
+bch_status bch_ctx_workspace_bytes(const bch_ctx *ctx, size_t *bytes);
 
 /* Message of the last failed call on ctx; with ctx == NULL, the calling
  * thread's last failure.  Never NULL ("" when none). */

@@ -24,6 +24,7 @@ pytestmark = pytest.mark.gpu
 
 HIP_LIB = "/opt/rocm/lib/libamdhip64.so.7"  # the runtime libbarracuda_hip.so is linked against
 CAPTURE_RELAXED = 2                          # hipStreamCaptureModeRelaxed
+CAPTURE_GLOBAL = 0                           # hipStreamCaptureModeGlobal
 
 
 def _say(msg):
@@ -38,8 +39,9 @@ def _hip():
     h.hipGraphLaunch.argtypes = [C.c_void_p, C.c_void_p]
     h.hipGraphExecDestroy.argtypes = [C.c_void_p]
     h.hipGraphDestroy.argtypes = [C.c_void_p]
+    h.hipGraphGetNodes.argtypes = [C.c_void_p, C.c_void_p, C.POINTER(C.c_size_t)]
     for f in ("hipStreamBeginCapture", "hipStreamEndCapture", "hipGraphInstantiate", "hipGraphLaunch",
-              "hipGraphExecDestroy", "hipGraphDestroy"):
+              "hipGraphExecDestroy", "hipGraphDestroy", "hipGraphGetNodes"):
         getattr(h, f).restype = C.c_int
     return h
 
@@ -124,4 +126,131 @@ def test_graph_replays_match_eager(dev):
         if exe.value:
             hip.hipGraphExecDestroy(exe)
         if graph.value:
+            hip.hipGraphDestroy(graph)
+
+
+class _FreshCtx:
+    """A context of its own (its workspace starts empty), destroyed on exit."""
+
+    def __init__(self, dev):
+        self.lib = dev._lib
+        self.ctx = C.c_void_p()
+        assert self.lib.bch_ctx_create(0, None, C.byref(self.ctx)) == N.BCH_OK
+        self.stream = C.c_void_p()
+        assert self.lib.bch_ctx_stream(self.ctx, C.byref(self.stream)) == N.BCH_OK
+
+    def ws_bytes(self) -> int:
+        n = C.c_size_t()
+        assert self.lib.bch_ctx_workspace_bytes(self.ctx, C.byref(n)) == N.BCH_OK
+        return n.value
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.lib.bch_ctx_destroy(self.ctx)
+
+
+def test_capture_that_would_grow_the_workspace_is_refused(dev):
+    """A fresh context whose first call (split-K GEMM, needs a workspace) is made under
+    capture: BCH_E_UNSUPPORTED with the reason, nothing recorded, no allocation; the same
+    call then works eagerly, captures and replays.  After an eager call grows the
+    workspace, the graph captured before still replays correctly: the old workspace it
+    reads is kept alive, not freed."""
+    _say("capture refusal, then capture after an eager call, then growth after the capture")
+    hip = _hip()
+    rng = O.Lcg(77)
+    m = n = k = 1024  # split-K: slices in the workspace, then the reduce
+    a, b = _up(dev, rng.uniform((m, k))), _up(dev, rng.uniform((k, n)))
+    c = Tensor.empty([m, n], dev)
+    want = a.to_numpy().astype(np.float64) @ b.to_numpy().astype(np.float64)
+    with _FreshCtx(dev) as f:
+        lib = f.lib
+        call = lambda: lib.bch_sgemm(f.ctx, m, n, k, C.c_void_p(a.ptr), k, C.c_void_p(b.ptr), n,
+                                     C.c_void_p(c.ptr), n)
+        assert f.ws_bytes() == 0
+        graph = C.c_void_p()
+        assert hip.hipStreamBeginCapture(f.stream, CAPTURE_RELAXED) == 0
+        st = call()
+        assert hip.hipStreamEndCapture(f.stream, C.byref(graph)) == 0
+        assert st == N.BCH_E_UNSUPPORTED
+        assert "captured" in N.last_error(f.ctx) and "bch_ctx_reserve" in N.last_error(f.ctx)
+        nodes = C.c_size_t()
+        assert hip.hipGraphGetNodes(graph, None, C.byref(nodes)) == 0 and nodes.value == 0
+        hip.hipGraphDestroy(graph)
+        assert f.ws_bytes() == 0  # refused before any allocation
+        assert call() == N.BCH_OK and lib.bch_sync(f.ctx) == N.BCH_OK  # eager: sizes the workspace
+        ws0 = f.ws_bytes()
+        assert ws0 > 0
+        assert O.max_rel_err(c.to_numpy(), want) <= 1e-4
+        eager = c.to_numpy()
+        graph, exe = C.c_void_p(), C.c_void_p()
+        assert hip.hipStreamBeginCapture(f.stream, CAPTURE_RELAXED) == 0
+        st = call()
+        assert hip.hipStreamEndCapture(f.stream, C.byref(graph)) == 0
+        assert st == N.BCH_OK
+        try:
+            assert hip.hipGraphInstantiate(C.byref(exe), graph, None, None, 0) == 0
+            # an eager call that needs a larger workspace replaces it after the capture
+            assert lib.bch_ctx_reserve(f.ctx, 4 * ws0) == N.BCH_OK
+            assert f.ws_bytes() >= 4 * ws0
+            for rep in range(3):
+                dev.upload(c.ptr, np.full((m, n), np.nan, np.float32))
+                assert hip.hipGraphLaunch(exe, f.stream) == 0
+                assert lib.bch_sync(f.ctx) == N.BCH_OK
+                assert np.array_equal(c.to_numpy(), eager), rep
+        finally:
+            if exe.value:
+                hip.hipGraphExecDestroy(exe)
+            hip.hipGraphDestroy(graph)
+
+
+def test_reserve_then_capture_allocates_nothing(dev):
+    """bch_ctx_reserve sizes a fresh context's workspace up front; calls captured in global
+    mode (where an allocation fails) then record only kernels, and replays match the eager
+    results of another context."""
+    _say("reserve, then global-mode capture of split-K GEMM, softmax over few long rows, wide attention")
+    hip = _hip()
+    rng = O.Lcg(78)
+    a, b = _up(dev, rng.uniform((1024, 1024))), _up(dev, rng.uniform((1024, 1024)))
+    c, c_ref = Tensor.empty([1024, 1024], dev), Tensor.empty([1024, 1024], dev)
+    x = _up(dev, rng.normal((1, 1 << 20), 0.0, 3.0))
+    y, y_ref = Tensor.empty([1, 1 << 20], dev), Tensor.empty([1, 1 << 20], dev)
+    B, H, S, D = 1, 2, 96, 320
+    q, kk, v = (_up(dev, rng.normal((B, H, S, D))) for _ in range(3))
+    o, o_ref = Tensor.empty([B, H, S, D], dev), Tensor.empty([B, H, S, D], dev)
+    P = lambda t: C.c_void_p(t.ptr)
+    calls = [
+        lambda ctx, out: dev._lib.bch_sgemm(ctx, 1024, 1024, 1024, P(a), 1024, P(b), 1024, P(out), 1024),
+        lambda ctx, out: dev._lib.bch_softmax_rows(ctx, 1, 1 << 20, P(x), P(out)),
+        lambda ctx, out: dev._lib.bch_sdpa_fwd(ctx, B, H, S, S, D, C.c_float(D ** -0.5), 1, P(q), P(kk), P(v),
+                                               P(out)),
+    ]
+    outs, refs = [c, y, o], [c_ref, y_ref, o_ref]
+    with dev._lock:
+        for call, r in zip(calls, refs):
+            dev.check(call(dev.ctx, r), "eager reference")
+    dev.sync()
+    with _FreshCtx(dev) as f:
+        assert f.lib.bch_ctx_reserve(f.ctx, 64 << 20) == N.BCH_OK and f.lib.bch_sync(f.ctx) == N.BCH_OK
+        ws = f.ws_bytes()
+        assert ws >= 64 << 20
+        graph, exe = C.c_void_p(), C.c_void_p()
+        assert hip.hipStreamBeginCapture(f.stream, CAPTURE_GLOBAL) == 0
+        sts = [call(f.ctx, out) for call, out in zip(calls, outs)]
+        assert hip.hipStreamEndCapture(f.stream, C.byref(graph)) == 0
+        assert sts == [N.BCH_OK] * 3, [N.last_error(f.ctx)]
+        assert f.ws_bytes() == ws
+        try:
+            assert hip.hipGraphInstantiate(C.byref(exe), graph, None, None, 0) == 0
+            for rep in range(3):
+                for out in outs:
+                    dev.upload(out.ptr, np.full(out.shape(), np.nan, np.float32))
+                assert hip.hipGraphLaunch(exe, f.stream) == 0
+                assert f.lib.bch_sync(f.ctx) == N.BCH_OK
+                for out, r in zip(outs, refs):
+                    assert np.array_equal(out.to_numpy(), r.to_numpy()), rep
+        finally:
+            if exe.value:
+                hip.hipGraphExecDestroy(exe)
             hip.hipGraphDestroy(graph)

@@ -5,7 +5,11 @@ smaller, on each kernel family (decode-shaped split-k paths that use the
 scratch, the MFMA tile path that needs none, the tile path's split-K and
 hybrid plan over the scratch); the whole tiles where the hybrid plan's
 partials exceed the scratch; and a clear rejection of a shape whose
-required partials would not fit."""
+required partials would not fit.  The property itself -- no allocation --
+is tested on fresh contexts (workspace never grown) whose first call is
+the no-alloc one, made under a global-mode stream capture (where an
+allocation fails), replayed and compared with bch_sgemm; the fresh
+context's workspace must still be empty afterwards."""
 from __future__ import annotations
 
 import ctypes as C
@@ -108,3 +112,70 @@ def test_noalloc_rejects_what_does_not_fit(dev):
     assert "scratch" in msg and str(16 << 20) in msg
     # the context stays usable
     dev.sync()
+
+
+HIP_LIB = "/opt/rocm/lib/libamdhip64.so.7"  # the runtime libbarracuda_hip.so is linked against
+CAPTURE_GLOBAL = 0                           # hipStreamCaptureModeGlobal
+
+
+def _hip():
+    h = C.CDLL(HIP_LIB)
+    h.hipStreamBeginCapture.argtypes = [C.c_void_p, C.c_int]
+    h.hipStreamEndCapture.argtypes = [C.c_void_p, C.POINTER(C.c_void_p)]
+    h.hipGraphInstantiate.argtypes = [C.POINTER(C.c_void_p), C.c_void_p, C.c_void_p, C.c_char_p, C.c_size_t]
+    h.hipGraphLaunch.argtypes = [C.c_void_p, C.c_void_p]
+    h.hipGraphExecDestroy.argtypes = [C.c_void_p]
+    h.hipGraphDestroy.argtypes = [C.c_void_p]
+    for f in ("hipStreamBeginCapture", "hipStreamEndCapture", "hipGraphInstantiate", "hipGraphLaunch",
+              "hipGraphExecDestroy", "hipGraphDestroy"):
+        getattr(h, f).restype = C.c_int
+    return h
+
+
+@pytest.mark.parametrize("family,shapes", [
+    ("skinny split-k m=32 then m=8", [(32, 11008, 4096), (8, 3000, 1024)]),
+    ("skinny fma m=1 then m=20", [(1, 11008, 4096), (20, 1000, 300)]),
+    ("tiles (no scratch) then skinny", [(256, 512, 384), (32, 256, 64)]),
+    ("split-K then a smaller split", [(1024, 1024, 1024), (96, 1024, 2048)]),
+    ("hybrid plan then a smaller hybrid", [(3072, 3072, 1024), (2304, 2304, 1024)]),
+])
+def test_noalloc_allocates_nothing_under_global_capture(dev, family, shapes):
+    hip = _hip()
+    lib = dev._lib
+    for i, (m, n, k) in enumerate(shapes):
+        _say(f"sgemm_noalloc captured on a fresh context ({family}), call {i}: m={m} n={n} k={k}")
+        rng = O.Lcg(500 + 1000 * i + m + n + k)
+        a, b = rng.normal((m, k)), rng.normal((k, n), 0.0, 0.02)
+        ta, tb = Tensor.from_data(a, [m, k], dev), Tensor.from_data(b, [k, n], dev)
+        c_ref, c_na = Tensor.empty([m, n], dev), Tensor.empty([m, n], dev)
+        pa, pb = C.c_void_p(ta.ptr), C.c_void_p(tb.ptr)
+        dev.check(lib.bch_sgemm(dev.ctx, m, n, k, pa, k, pb, n, C.c_void_p(c_ref.ptr), n), "sgemm")
+        want = c_ref.to_numpy()
+        ctx, stream = C.c_void_p(), C.c_void_p()
+        assert lib.bch_ctx_create(0, None, C.byref(ctx)) == N.BCH_OK
+        graph, exe = C.c_void_p(), C.c_void_p()
+        try:
+            assert lib.bch_ctx_stream(ctx, C.byref(stream)) == N.BCH_OK
+            ws = C.c_size_t(1)
+            assert lib.bch_ctx_workspace_bytes(ctx, C.byref(ws)) == N.BCH_OK and ws.value == 0
+            assert hip.hipStreamBeginCapture(stream, CAPTURE_GLOBAL) == 0
+            st = lib.bch_sgemm_noalloc(ctx, m, n, k, pa, k, pb, n, C.c_void_p(c_na.ptr), n)
+            assert hip.hipStreamEndCapture(stream, C.byref(graph)) == 0
+            assert st == N.BCH_OK, N.last_error(ctx)
+            assert lib.bch_ctx_workspace_bytes(ctx, C.byref(ws)) == N.BCH_OK and ws.value == 0
+            assert hip.hipGraphInstantiate(C.byref(exe), graph, None, None, 0) == 0
+            for rep in range(2):
+                dev.upload(c_na.ptr, np.full((m, n), np.nan, np.float32))
+                assert hip.hipGraphLaunch(exe, stream) == 0
+                assert lib.bch_sync(ctx) == N.BCH_OK
+                got = c_na.to_numpy()
+                assert np.array_equal(got, want), (family, rep)  # the same kernels and plan as bch_sgemm
+                rows = list(range(min(m, 4))) + [m - 1]
+                assert O.max_rel_err(got[rows], O.matmul_f64(a, b, rows=rows)) <= TOL
+            assert lib.bch_ctx_workspace_bytes(ctx, C.byref(ws)) == N.BCH_OK and ws.value == 0
+        finally:
+            if exe.value:
+                hip.hipGraphExecDestroy(exe)
+            if graph.value:
+                hip.hipGraphDestroy(graph)
+            lib.bch_ctx_destroy(ctx)
