@@ -151,7 +151,7 @@ def bench_gemm(dev, steps, warmup, warmer=None):
 WORKLOADS = ("softmax", "skinny", "batched", "sdpa", "linear", "dgemm", "norm", "attn64", "copy")
 
 
-def bench_extra(dev, reps: int = 20, only=None, warmer=None):
+def bench_extra(dev, reps: int = 20, only=None, warmer=None, skinny_n: int = 11008):
     """The other BASELINE configs, each timed over `reps` launches."""
     from barracuda_amd import LcgStream, Tensor
     lib, ctx = dev._lib, dev.ctx
@@ -172,7 +172,7 @@ def bench_extra(dev, reps: int = 20, only=None, warmer=None):
     if "softmax" in want:
         out.update(_bench_softmax(dev, T, reps))
     if "skinny" in want:
-        out.update(_bench_skinny(dev, T, reps))
+        out.update(_bench_skinny(dev, T, reps, skinny_n))
     if "batched" in want:
         out.update(_bench_batched(dev, T, reps))
     if "sdpa" in want:
@@ -337,13 +337,15 @@ def _bench_softmax(dev, T, reps):
     return out
 
 
-def _bench_skinny(dev, T, reps):
+def _bench_skinny(dev, T, reps, N: int = 11008):
     from barracuda_amd import LcgStream, Tensor
     lib, ctx = dev._lib, dev.ctx
     out = {}
     # config 4: skinny GEMM M in {1, 8, 32}, K 4096, N 11008; X ~ N(0,1), W ~ N(0,0.02), seed 3.
-    # Three weight copies (541 MB > the 256 MB Infinity Cache) are rotated.
-    K, N = 4096, 11008
+    # Three weight copies (541 MB > the 256 MB Infinity Cache) are rotated.  A larger N
+    # (--skinny-n, profiling only) lengthens each launch so that per-dispatch counter windows
+    # are dominated by the kernel.
+    K = 4096
     for m in (1, 8, 32):
         s = LcgStream(3, dev)
         xs = s.normal([m, K])
@@ -353,7 +355,7 @@ def _bench_skinny(dev, T, reps):
         pws = [C.c_void_p(w.ptr) for w in ws]
         wall, ev = T.run(lambda i: lib.bch_sgemm(ctx, m, N, K, pxs, K, pws[i % 3], N, pys, N), reps, 3)
         nbytes = 4 * (K * N + m * K + m * N)
-        out[f"skinny_m{m}"] = {"GB/s": nbytes / (ev * 1e-3) / 1e9, "us": ev * 1e3,
+        out[f"skinny_m{m}" + ("" if N == 11008 else f"_n{N}")] = {"GB/s": nbytes / (ev * 1e-3) / 1e9, "us": ev * 1e3,
                                "bytes_per_call": nbytes,
                                "hbm_frac": nbytes / (ev * 1e-3) / 1e9 / HBM_PEAK_GBS,
                                "TFLOP/s": 2.0 * m * K * N / (ev * 1e-3) / 1e12,
@@ -587,6 +589,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=30)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="only the headline GEMM")
+    ap.add_argument("--skinny-n", type=int, default=11008,
+                    help="N of the skinny workload under --only (profiling; the config is 11008)")
     ap.add_argument("--only", default=None,
                     help="comma list of " + ",".join(("gemm",) + WORKLOADS) + ": time just these "
                          "(profiling runs); prints their results as the JSON line")
@@ -608,7 +612,7 @@ def main() -> int:
             del keep
         rest = [w for w in sel if w != "gemm"]
         if rest:
-            res.update(bench_extra(dev, only=rest, warmer=warmer))
+            res.update(bench_extra(dev, only=rest, warmer=warmer, skinny_n=args.skinny_n))
         print(json.dumps({"only": sel, "results": res}), flush=True)
         return 0
     log(f"gemm 4096^3: {args.warmup} warmup + {args.steps} timed launches")
