@@ -18,6 +18,10 @@
 // [B,S,H*D] <-> [B,H,S,D] through head_split_f64.wgsl / head_concat_f64.wgsl;
 // here the kernel reads and writes the [B,S,H,D] projections in place).
 //
+// Head dimensions: D <= 128 run sdpa_fwd_kernel (below); 128 < D <= 256
+// run sdpa_fwd16_kernel (16 queries per wavefront, further down); larger D
+// take the chunked three-step path of sdpa_wide.hip.
+//
 // Design (FP32 MFMA for both products, v_mfma_f32_32x32x2_f32):
 //   * A workgroup = 4 wavefronts = 128 queries of one (b,h); wavefront w owns
 //     queries q0 + 32w .. +31, lane l's query is l % 32.  Key blocks of 32 are
@@ -93,7 +97,8 @@ struct SdpaCfg {
   static constexpr int BQ = NT / 2;                    // queries per workgroup
   static constexpr int KLD = DP + 4;
   static constexpr int KD4 = DP / 4;                   // float4 per K row
-  static constexpr int K_F4 = kBKV * DP / 4 / NT;      // float4 of K per thread
+  static constexpr int K_TOT = kBKV * DP / 4;          // float4 of K per tile
+  static constexpr int K_F4 = (K_TOT + NT - 1) / NT;    // float4 of K per thread
   static constexpr int V_BLK = kBKV * DP / 16;          // 4x4 V blocks per tile
   static constexpr int V_PER = (V_BLK + NT - 1) / NT;    // 4x4 V blocks per thread
   static constexpr int LDS_FLOATS = 2 * (kBKV * KLD + DP * kVLD);
@@ -130,7 +135,8 @@ __device__ __forceinline__ void load_k(const float* __restrict__ kh, long long l
   using G = SdpaCfg<DP, NT>;
 #pragma unroll
   for (int f = 0; f < G::K_F4; ++f) {
-    const int idx = tid + f * NT;
+    const int idx0 = tid + f * NT;
+    const int idx = (G::K_TOT % NT == 0 || idx0 < G::K_TOT) ? idx0 : 0;  // past the tile: reload float4 0 (unused)
     const int key = idx / G::KD4, d0 = (idx % G::KD4) * 4;
     const int gk = kb + key;
     float t[4];
@@ -179,9 +185,11 @@ __device__ __forceinline__ void store_kv(float* __restrict__ ks, float* __restri
 #pragma unroll
   for (int f = 0; f < G::K_F4; ++f) {
     const int idx = tid + f * NT;
-    const int key = idx / G::KD4, d0 = (idx % G::KD4) * 4;
-    *reinterpret_cast<float4*>(ks + key * G::KLD + d0) =
-        make_float4(r.k[4 * f], r.k[4 * f + 1], r.k[4 * f + 2], r.k[4 * f + 3]);
+    if (G::K_TOT % NT == 0 || idx < G::K_TOT) {
+      const int key = idx / G::KD4, d0 = (idx % G::KD4) * 4;
+      *reinterpret_cast<float4*>(ks + key * G::KLD + d0) =
+          make_float4(r.k[4 * f], r.k[4 * f + 1], r.k[4 * f + 2], r.k[4 * f + 3]);
+    }
   }
 #pragma unroll
   for (int p = 0; p < G::V_PER; ++p) {
@@ -199,7 +207,7 @@ __device__ __forceinline__ void store_kv(float* __restrict__ ks, float* __restri
 }
 
 template <int DP, bool FULL, int NT>
-__global__ __launch_bounds__(NT, DP > 128 ? 1 : 2) void sdpa_fwd_kernel(
+__global__ __launch_bounds__(NT, 2) void sdpa_fwd_kernel(
     int H, int group, int BH, int Sq, int Skv, int D, float qscale, int causal, const float* __restrict__ q,
     const float* __restrict__ k, const float* __restrict__ v, float* __restrict__ o, bch::SdpaStrides st,
     int qblocks) {
@@ -368,6 +376,237 @@ __global__ __launch_bounds__(NT, DP > 128 ? 1 : 2) void sdpa_fwd_kernel(
   }
 }
 
+// ---- 128 < D <= 256: v_mfma_f32_16x16x4_f32, 16 queries per wavefront ----
+// The 32x32 layout above keeps D/2 floats of q and D/2 of O per lane: at
+// D = 256 that is 256 registers before staging and scores, one wavefront per
+// SIMD, with the softmax of each block exposed on its SIMD.  Here a
+// wavefront owns 16 queries, so q and O take D/4 floats each (64 + 64 at
+// D = 256) and two wavefronts share each SIMD: 8 wavefronts = 128 queries
+// per workgroup, the same K/V tile reuse and LDS layout as the 32x32 kernel
+// (one workgroup per CU at 137 KB of LDS for D = 256).
+//   S^T = K Q^T on 16 x 16 blocks: lane (g = l / 16, i = l % 16) supplies
+//     K[key 16 sb + i][d] and q[query i][d] with d = 16 c + 4 g + e in step
+//     (c, e), so one 128-bit LDS read of K and one register float4 of q feed
+//     four MFMAs; value r of the result is key 16 sb + 4 g + r of query i.
+//     A 32-key block is two such chains (sb = 0, 1): 8 scores per lane.
+//   Row max and sum: in-lane over the 8, then across the four lanes
+//     i, i + 16, i + 32, i + 48 of a query (v_permlane16_swap then
+//     v_permlane32_swap; every lane of a query gets the same bits).
+//   O^T += V^T P^T: step (sb, r) contracts key 16 sb + 4 g + r, whose P is
+//     this lane's score r of chain sb; V^T comes from the transposed V tile
+//     as one 128-bit read per four MFMAs.  Value r of O block db is
+//     d = 16 db + 4 g + r of query i: the epilogue stores a float4.
+// The online softmax (lazy reference max), causal skipping and masking and
+// the workgroup order are those of sdpa_fwd_kernel.
+// Measured at B=4, H=32, S=2048, D=256 (one box): 4.27 / 2.27 ms non-causal /
+// causal (81.9% / 77.1% of FP32 MFMA peak), against 5.01 / 2.75 ms for
+// sdpa_fwd_kernel at D = 256 (one wavefront per SIMD, accumulators in
+// AGPRs).  D = 160 / 192 / 224: 75% / 77% / 79% non-causal.  For D <= 128
+// this layout is slower than the 32x32 kernel (2.15 against 2.05 ms at
+// config 5, 4 wavefronts per SIMD), so it starts above 128.
+constexpr int kNT16 = 512;        // threads per workgroup: 8 wavefronts
+constexpr int kBQ16 = kNT16 / 4;  // queries per workgroup (16 per wavefront)
+
+typedef float f32x4v __attribute__((ext_vector_type(4)));
+
+// x combined over the lanes l, l ^ 16, l ^ 32, l ^ 48 (the four lanes of one
+// query), the same bits in all four: v_permlane16_swap of (x, x) returns
+// {x[l & ~16], x[l | 16]} and v_permlane32_swap {x[l & ~32], x[l | 32]}.
+__device__ __forceinline__ float quad_swap_max(float x) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float quad_swap_sum(float x) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+template <int DP, bool FULL>
+__global__ __launch_bounds__(kNT16, 2) void sdpa_fwd16_kernel(
+    int H, int group, int BH, int Sq, int Skv, int D, float qscale, int causal, const float* __restrict__ q,
+    const float* __restrict__ k, const float* __restrict__ v, float* __restrict__ o, bch::SdpaStrides st,
+    int qblocks) {
+  using G = SdpaCfg<DP, kNT16>;
+  constexpr int KLD = G::KLD, NT = kNT16;
+  extern __shared__ float4 smem4[];
+  float* smem = reinterpret_cast<float*>(smem4);
+  float* Ks = smem;                        // [2][kBKV][KLD]
+  float* Vt = smem + 2 * kBKV * KLD;       // [2][DP][kVLD]
+
+  int qi, bh;
+  if (causal) {
+    qi = blockIdx.x / BH;
+    bh = blockIdx.x % BH;
+  } else {
+    const int nb = gridDim.x;
+    int L = blockIdx.x;
+    if ((nb & 7) == 0) L = (L & 7) * (nb >> 3) + (L >> 3);
+    bh = L / qblocks;
+    qi = L - bh * qblocks;
+  }
+  const int qb = causal ? qblocks - 1 - qi : qi;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int li = lane & 15, lg = lane >> 4;
+  const int q0w = qb * kBQ16 + wave * 16;  // first query of this wavefront
+  const int myq = q0w + li;
+
+  const int bi = bh / H, hq = bh - bi * H, hk = hq / group;
+  const float* qh = q + bi * st.q.batch + hq * st.q.head;
+  const float* kh = k + bi * st.k.batch + hk * st.k.head;
+  const float* vh = v + bi * st.v.batch + hk * st.v.head;
+  float* oh = o + bi * st.o.batch + hq * st.o.head;
+
+  // ---- q operand: qf[c] = q[myq][16c + 4lg .. +3] * scale * log2(e) ----
+  float4 qf[DP / 16];
+#pragma unroll
+  for (int c = 0; c < DP / 16; ++c) {
+    const int d0 = 16 * c + 4 * lg;
+    float t[4];
+    if (FULL) {
+      const float4 x = *reinterpret_cast<const float4*>(qh + myq * st.q.row + d0);
+      t[0] = x.x; t[1] = x.y; t[2] = x.z; t[3] = x.w;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) t[e] = (myq < Sq && d0 + e < D) ? qh[myq * st.q.row + d0 + e] : 0.0f;
+    }
+    qf[c] = make_float4(t[0] * qscale, t[1] * qscale, t[2] * qscale, t[3] * qscale);
+  }
+
+  f32x4v oacc[DP / 16];
+#pragma unroll
+  for (int b = 0; b < DP / 16; ++b) oacc[b] = (f32x4v){0.f, 0.f, 0.f, 0.f};
+  float m_ref = -INFINITY, l_run = 0.0f;
+
+  int kend = Skv;
+  if (causal) kend = min(Skv, qb * kBQ16 + kBQ16);
+  const int nkb = (kend + kBKV - 1) / kBKV;
+
+  KvRegs<DP, NT> kv;
+  load_k<DP, NT, FULL>(kh, st.k.row, Skv, D, 0, tid, kv);
+  load_v<DP, NT, FULL>(vh, st.v.row, Skv, D, 0, tid, kv);
+  store_kv<DP, NT>(Ks, Vt, tid, kv);
+  load_k<DP, NT, FULL>(kh, st.k.row, Skv, D, min(1, nkb - 1) * kBKV, tid, kv);
+  load_v<DP, NT, FULL>(vh, st.v.row, Skv, D, min(1, nkb - 1) * kBKV, tid, kv);
+  __syncthreads();
+
+  for (int t = 0; t < nkb; ++t) {
+    const int cur = t & 1;
+    const int kb = t * kBKV;
+    store_kv<DP, NT>(Ks + (cur ^ 1) * kBKV * KLD, Vt + (cur ^ 1) * DP * kVLD, tid, kv);
+    const int kbn = min(t + 2, nkb - 1) * kBKV;
+    load_k<DP, NT, FULL>(kh, st.k.row, Skv, D, kbn, tid, kv);
+    load_v<DP, NT, FULL>(vh, st.v.row, Skv, D, kbn, tid, kv);
+
+    const bool active = (q0w < Sq) && !(causal && kb > q0w + 15);
+    if (active) {
+      const float* ks = Ks + cur * kBKV * KLD + li * KLD + 4 * lg;
+      f32x4v s[2];
+      s[0] = s[1] = (f32x4v){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < DP / 16; ++c) {
+#pragma unroll
+        for (int sb = 0; sb < 2; ++sb) {
+          const float4 kf = *reinterpret_cast<const float4*>(ks + sb * 16 * KLD + 16 * c);
+          s[sb] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.x, qf[c].x, s[sb], 0, 0, 0);
+          s[sb] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.y, qf[c].y, s[sb], 0, 0, 0);
+          s[sb] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.z, qf[c].z, s[sb], 0, 0, 0);
+          s[sb] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.w, qf[c].w, s[sb], 0, 0, 0);
+        }
+      }
+      // value r of chain sb: key kb + 16 sb + 4 lg + r, query myq
+      const bool need_mask = (!FULL && kb + kBKV > Skv) || (causal && kb + kBKV - 1 > q0w);
+      if (need_mask) {
+#pragma unroll
+        for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int key = kb + 16 * sb + 4 * lg + r;
+            if (key >= Skv || (causal && key > myq)) s[sb][r] = -INFINITY;
+          }
+      }
+      float bm = s[0][0];
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) bm = fmaxf(bm, s[sb][r]);
+      bm = quad_swap_max(bm);
+      const bool move = bm > m_ref + kLazy;
+      if (__any(move)) {
+        const float m_new = move ? bm : m_ref;
+        const float alpha = (m_ref == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m_ref - m_new);
+        l_run *= alpha;
+#pragma unroll
+        for (int b = 0; b < DP / 16; ++b) oacc[b] *= alpha;
+        m_ref = m_new;
+      }
+      const float m_use = (m_ref == -INFINITY) ? 0.0f : m_ref;
+      float rs = 0.0f;
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          s[sb][r] = __builtin_amdgcn_exp2f(s[sb][r] - m_use);
+          rs += s[sb][r];
+        }
+      rs = quad_swap_sum(rs);
+      l_run += rs;
+
+      const float* vs = Vt + cur * DP * kVLD + li * kVLD + 4 * lg;
+#pragma unroll
+      for (int db = 0; db < DP / 16; ++db) {
+#pragma unroll
+        for (int sb = 0; sb < 2; ++sb) {
+          const float4 vf = *reinterpret_cast<const float4*>(vs + db * 16 * kVLD + 16 * sb);
+          oacc[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf.x, s[sb][0], oacc[db], 0, 0, 0);
+          oacc[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf.y, s[sb][1], oacc[db], 0, 0, 0);
+          oacc[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf.z, s[sb][2], oacc[db], 0, 0, 0);
+          oacc[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf.w, s[sb][3], oacc[db], 0, 0, 0);
+        }
+      }
+    }
+    __syncthreads();
+  }
+
+  // ---- epilogue: value r of block db is d = 16 db + 4 lg + r ----
+  if (myq < Sq) {
+    const float inv = 1.0f / l_run;
+#pragma unroll
+    for (int db = 0; db < DP / 16; ++db) {
+      const int d0 = 16 * db + 4 * lg;
+      if (FULL) {
+        *reinterpret_cast<float4*>(oh + myq * st.o.row + d0) =
+            make_float4(oacc[db][0] * inv, oacc[db][1] * inv, oacc[db][2] * inv, oacc[db][3] * inv);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (d0 + r < D) oh[myq * st.o.row + d0 + r] = oacc[db][r] * inv;
+      }
+    }
+  }
+}
+
+template <int DP, bool FULL>
+hipError_t launch_dp16(hipStream_t s, int B, int H, int Hkv, int Sq, int Skv, int D, float scale, int causal,
+                       const float* q, const float* k, const float* v, float* o, const bch::SdpaStrides& st) {
+  using G = SdpaCfg<DP, kNT16>;
+  const int qblocks = (Sq + kBQ16 - 1) / kBQ16;
+  const long long blocks = (long long)B * H * qblocks;
+  if (blocks > 0x7fffffffLL) return hipErrorInvalidValue;
+  const size_t lds = sizeof(float) * G::LDS_FLOATS;
+  auto kern = sdpa_fwd16_kernel<DP, FULL>;
+  hipError_t e = bch::ensure_dynamic_lds(reinterpret_cast<const void*>(kern), (int)lds);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(kNT16), lds, s, H, H / Hkv, B * H, Sq, Skv, D,
+                     scale * kLog2E, causal, q, k, v, o, st, qblocks);
+  return hipGetLastError();
+}
+
 template <int DP, bool FULL, int NT>
 hipError_t launch_dp(hipStream_t s, int B, int H, int Hkv, int Sq, int Skv, int D, float scale, int causal,
                      const float* q, const float* k, const float* v, float* o, const bch::SdpaStrides& st) {
@@ -398,6 +637,16 @@ hipError_t launch_d(hipStream_t s, int B, int H, int Hkv, int Sq, int Skv, int D
   return launch_dp<DP, false, NT>(s, B, H, Hkv, Sq, Skv, D, scale, causal, q, k, v, o, st);
 }
 
+// 128 < D <= 256: the 16-query-per-wavefront kernel
+template <int DP>
+hipError_t launch_d16(hipStream_t s, int B, int H, int Hkv, int Sq, int Skv, int D, float scale, int causal,
+                      const float* q, const float* k, const float* v, float* o, const bch::SdpaStrides& st) {
+  const bool full = D == DP && Sq % kBQ16 == 0 && Skv % kBKV == 0 && aligned16(q) && aligned16(k) && aligned16(v) &&
+                    aligned16(o) && mult4(st.q) && mult4(st.k) && mult4(st.v) && mult4(st.o);
+  if (full) return launch_dp16<DP, true>(s, B, H, Hkv, Sq, Skv, D, scale, causal, q, k, v, o, st);
+  return launch_dp16<DP, false>(s, B, H, Hkv, Sq, Skv, D, scale, causal, q, k, v, o, st);
+}
+
 }  // namespace
 
 namespace bch {
@@ -409,10 +658,10 @@ hipError_t launch_sdpa_strided(hipStream_t s, int B, int H, int Hkv, int Sq, int
   if (D <= 32) return launch_d<32>(s, B, H, Hkv, Sq, Skv, D, scale, causal, q, k, v, o, st);
   if (D <= 64) return launch_d<64>(s, B, H, Hkv, Sq, Skv, D, scale, causal, q, k, v, o, st);
   if (D <= 128) return launch_d<128>(s, B, H, Hkv, Sq, Skv, D, scale, causal, q, k, v, o, st);
-  if (D <= 160) return launch_d<160>(s, B, H, Hkv, Sq, Skv, D, scale, causal, q, k, v, o, st);
-  if (D <= 192) return launch_d<192>(s, B, H, Hkv, Sq, Skv, D, scale, causal, q, k, v, o, st);
-  if (D <= 224) return launch_d<224>(s, B, H, Hkv, Sq, Skv, D, scale, causal, q, k, v, o, st);
-  if (D <= 256) return launch_d<256>(s, B, H, Hkv, Sq, Skv, D, scale, causal, q, k, v, o, st);
+  if (D <= 160) return launch_d16<160>(s, B, H, Hkv, Sq, Skv, D, scale, causal, q, k, v, o, st);
+  if (D <= 192) return launch_d16<192>(s, B, H, Hkv, Sq, Skv, D, scale, causal, q, k, v, o, st);
+  if (D <= 224) return launch_d16<224>(s, B, H, Hkv, Sq, Skv, D, scale, causal, q, k, v, o, st);
+  if (D <= 256) return launch_d16<256>(s, B, H, Hkv, Sq, Skv, D, scale, causal, q, k, v, o, st);
   return hipErrorInvalidValue;
 }
 
