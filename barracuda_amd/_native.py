@@ -69,7 +69,7 @@ SIGNATURES = {
     "bch_softmax_rows_f64": (_i, [_vp, _ll, _ll, _vp, _vp]),
     "bch_elementwise": (_i, [_vp, _i, _ll, _vp, _vp, _vp, _f, _vp]),
     "bch_layer_norm": (_i, [_vp, _ll, _ll, _f, _vp, _vp]),
-    "bch_layer_norm_kernel_name": (C.c_char_p, [_ll, _ll]),
+    "bch_layer_norm_kernel_name": (C.c_char_p, [_ll, _ll, _vp, _vp]),
     "bch_softmax_rows_f64_kernel_name": (C.c_char_p, [_ll, _ll, _vp, _vp]),
     "bch_softmax_axis": (_i, [_vp, _ll, _ll, _ll, _vp, _vp]),
     "bch_head_split": (_i, [_vp, _i, _i, _i, _i, _vp, _vp]),

@@ -102,7 +102,9 @@ hipError_t launch_softmax_axis(hipStream_t s, long long outer, long long axis,
                                void* ws, size_t ws_bytes);
 size_t softmax_axis_workspace_bytes(long long outer, long long axis,
                                     long long inner);
-const char* softmax_kernel_name(long long rows, long long cols);
+// The kernel a launch_softmax_rows with these buffers runs (the split plan's
+// write kernel when few long rows are split).
+const char* softmax_kernel_name(long long rows, long long cols, const float* in, const float* out);
 // Row softmax over a contiguous [rows, cols] f64 matrix (in may equal out);
 // no scratch.  aligned16: both matrices 16-byte aligned.
 hipError_t launch_softmax_rows_f64(hipStream_t s, long long rows, long long cols,
@@ -189,7 +191,15 @@ hipError_t launch_elementwise(hipStream_t s, int op, long long n, const float* a
 // Layer norm over the last axis of [rows, cols]: (x - mean) / sqrt(var + eps).
 hipError_t launch_layer_norm(hipStream_t s, long long rows, long long cols, float eps, const float* in,
                              float* out);
-const char* layer_norm_kernel_name(long long rows, long long cols);
+// The kernel a launch_layer_norm with these buffers runs.
+const char* layer_norm_kernel_name(long long rows, long long cols, const float* in, const float* out);
+
+// Row kernels (softmax, layer norm) launch at most kRowsPerLaunch rows at a
+// time: with up to 1024 threads a row, a grid then stays below 2^32 threads
+// and 2^31 workgroups whatever the row count.  row_launches(rows) is the
+// number of launches a call over `rows` rows makes.
+constexpr long long kRowsPerLaunch = 1LL << 21;
+long long row_launches(long long rows);
 
 // head_split (concat false): [B, S, H*D] -> [B, H, S, D]; head_concat
 // (concat true): the inverse.  in and out must not overlap.

@@ -556,7 +556,6 @@ bch_status bch_softmax_rows(bch_ctx* ctx, long long rows, long long cols, const 
 bch_status bch_softmax_rows_f64(bch_ctx* ctx, long long rows, long long cols, const double* in, double* out) {
   if (rows < 1 || cols < 1)
     return fail(ctx, BCH_E_SHAPE, "softmax_f64: empty dimension (rows=%lld, cols=%lld)", rows, cols);
-  if (rows > 0x7fffffffLL) return fail(ctx, BCH_E_UNSUPPORTED, "softmax_f64: %lld rows > 2^31 - 1", rows);
   if (!ctx) return fail(ctx, BCH_E_INVALID, "softmax_f64: ctx is NULL");
   if (!in || !out) return fail(ctx, BCH_E_INVALID, "softmax_f64: NULL buffer");
   bch_status st = use(ctx);
@@ -582,7 +581,6 @@ bch_status bch_layer_norm(bch_ctx* ctx, long long rows, long long cols, float ep
   if (rows < 1 || cols < 1)
     return fail(ctx, BCH_E_SHAPE, "layer_norm: empty dimension (rows=%lld, cols=%lld)", rows, cols);
   if (!(eps >= 0.0f)) return fail(ctx, BCH_E_INVALID, "layer_norm: epsilon must be >= 0 (got %g)", (double)eps);
-  if (rows > 0x7fffffffLL) return fail(ctx, BCH_E_UNSUPPORTED, "layer_norm: %lld rows > 2^31 - 1", rows);
   if (!ctx) return fail(ctx, BCH_E_INVALID, "layer_norm: ctx is NULL");
   if (!in || !out) return fail(ctx, BCH_E_INVALID, "layer_norm: NULL buffer");
   bch_status st = use(ctx);
@@ -831,8 +829,8 @@ const char* bch_softmax_rows_f64_kernel_name(long long rows, long long cols, con
       rows, cols, ((reinterpret_cast<uintptr_t>(in) | reinterpret_cast<uintptr_t>(out)) & 15) == 0);
 }
 
-const char* bch_layer_norm_kernel_name(long long rows, long long cols) {
-  return bch::layer_norm_kernel_name(rows, cols);
+const char* bch_layer_norm_kernel_name(long long rows, long long cols, const float* in, const float* out) {
+  return bch::layer_norm_kernel_name(rows, cols, in, out);
 }
 
 }  // extern "C"

@@ -209,77 +209,117 @@ bool wave_path(long long cols, const float* in, const float* out) {
          (reinterpret_cast<uintptr_t>(out) & 15) == 0;
 }
 
+// Which kernel a call runs: the wavefront-per-row register kernel (sel = NV),
+// the workgroup-per-row float4 register kernel (sel = NV, 64 meaning 16 on
+// 1024 threads), the scalar register kernel (sel = NS * 10000 + NT), or the
+// block kernel.  The float4 kernels need 16-byte aligned buffers; the launch
+// and the reported name both come from this one choice.
+enum class LnKind { kWave, kWg, kWgs, kBlock };
+struct LnPlan {
+  LnKind kind;
+  int sel;
+};
+
+LnPlan ln_plan(long long cols, const float* in, const float* out) {
+  const bool al = (reinterpret_cast<uintptr_t>(in) & 15) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0;
+  if (wave_path(cols, in, out)) return {LnKind::kWave, pick_nv(cols)};
+  if (pick_wg_nv(cols) > 0 && al) return {LnKind::kWg, pick_wg_nv(cols)};
+  if (pick_wgs(cols) > 0) return {LnKind::kWgs, pick_wgs(cols)};
+  return {LnKind::kBlock, 0};
+}
+
+// One launch over n rows (n <= kLnRowsPerLaunch).
+hipError_t launch_rows(hipStream_t s, const LnPlan& p, long long n, long long cols, float eps, const float* in,
+                       float* out) {
+  const int c = (int)cols;
+  switch (p.kind) {
+    case LnKind::kWave: {
+      const dim3 grid((unsigned)((n + 3) / 4)), block(256);
+      switch (p.sel) {
+        case 1: hipLaunchKernelGGL(layer_norm_wave<1>, grid, block, 0, s, in, out, n, c, eps); break;
+        case 2: hipLaunchKernelGGL(layer_norm_wave<2>, grid, block, 0, s, in, out, n, c, eps); break;
+        case 4: hipLaunchKernelGGL(layer_norm_wave<4>, grid, block, 0, s, in, out, n, c, eps); break;
+        case 8: hipLaunchKernelGGL(layer_norm_wave<8>, grid, block, 0, s, in, out, n, c, eps); break;
+        default: hipLaunchKernelGGL(layer_norm_wave<16>, grid, block, 0, s, in, out, n, c, eps); break;
+      }
+      break;
+    }
+    case LnKind::kWg: {
+      const dim3 grid((unsigned)n), block(256);
+      switch (p.sel) {
+        case 8: hipLaunchKernelGGL((layer_norm_wg<8, 256>), grid, block, 0, s, in, out, c, eps); break;
+        case 16: hipLaunchKernelGGL((layer_norm_wg<16, 256>), grid, block, 0, s, in, out, c, eps); break;
+        case 32: hipLaunchKernelGGL((layer_norm_wg<32, 256>), grid, block, 0, s, in, out, c, eps); break;
+        default: hipLaunchKernelGGL((layer_norm_wg<16, 1024>), grid, dim3(1024), 0, s, in, out, c, eps); break;
+      }
+      break;
+    }
+    case LnKind::kWgs: {
+      const dim3 grid((unsigned)n);
+      switch (p.sel) {
+        case 40256: hipLaunchKernelGGL((layer_norm_wgs<4, 256>), grid, dim3(256), 0, s, in, out, c, eps); break;
+        case 160256: hipLaunchKernelGGL((layer_norm_wgs<16, 256>), grid, dim3(256), 0, s, in, out, c, eps); break;
+        case 161024: hipLaunchKernelGGL((layer_norm_wgs<16, 1024>), grid, dim3(1024), 0, s, in, out, c, eps); break;
+        default: hipLaunchKernelGGL((layer_norm_wgs<32, 1024>), grid, dim3(1024), 0, s, in, out, c, eps); break;
+      }
+      break;
+    }
+    default:
+      hipLaunchKernelGGL(layer_norm_block, dim3((unsigned)n), dim3(256), 0, s, in, out, cols, eps);
+      break;
+  }
+  return hipGetLastError();
+}
+
 }  // namespace
 
 namespace bch {
 
-const char* layer_norm_kernel_name(long long rows, long long cols) {
+const char* layer_norm_kernel_name(long long rows, long long cols, const float* in, const float* out) {
   (void)rows;
-  if (cols % 4 == 0) {
-    switch (pick_nv(cols)) {
-      case 1: return "layer_norm_wave<1>";
-      case 2: return "layer_norm_wave<2>";
-      case 4: return "layer_norm_wave<4>";
-      case 8: return "layer_norm_wave<8>";
-      case 16: return "layer_norm_wave<16>";
-      default: break;
-    }
+  const LnPlan p = ln_plan(cols, in, out);
+  switch (p.kind) {
+    case LnKind::kWave:
+      switch (p.sel) {
+        case 1: return "layer_norm_wave<1>";
+        case 2: return "layer_norm_wave<2>";
+        case 4: return "layer_norm_wave<4>";
+        case 8: return "layer_norm_wave<8>";
+        default: return "layer_norm_wave<16>";
+      }
+    case LnKind::kWg:
+      switch (p.sel) {
+        case 8: return "layer_norm_wg<8>";
+        case 16: return "layer_norm_wg<16>";
+        case 32: return "layer_norm_wg<32>";
+        default: return "layer_norm_wg<16, 1024>";
+      }
+    case LnKind::kWgs:
+      switch (p.sel) {
+        case 40256: return "layer_norm_wgs<4, 256>";
+        case 160256: return "layer_norm_wgs<16, 256>";
+        case 161024: return "layer_norm_wgs<16, 1024>";
+        default: return "layer_norm_wgs<32, 1024>";
+      }
+    default:
+      return "layer_norm_block";
   }
-  switch (pick_wg_nv(cols)) {
-    case 8: return "layer_norm_wg<8>";
-    case 16: return "layer_norm_wg<16>";
-    case 32: return "layer_norm_wg<32>";
-    case 64: return "layer_norm_wg<16, 1024>";
-    default: break;
-  }
-  switch (pick_wgs(cols)) {
-    case 40256: return "layer_norm_wgs<4, 256>";
-    case 160256: return "layer_norm_wgs<16, 256>";
-    case 161024: return "layer_norm_wgs<16, 1024>";
-    case 321024: return "layer_norm_wgs<32, 1024>";
-    default: break;
-  }
-  return "layer_norm_block";
 }
+
+long long row_launches(long long rows) { return rows <= 0 ? 0 : (rows + kRowsPerLaunch - 1) / kRowsPerLaunch; }
 
 hipError_t launch_layer_norm(hipStream_t s, long long rows, long long cols, float eps, const float* in, float* out) {
   if (rows <= 0 || cols <= 0) return hipSuccess;
-  if (wave_path(cols, in, out)) {
-    const dim3 grid((unsigned)((rows + 3) / 4)), block(256);
-    const int c = (int)cols;
-    switch (pick_nv(cols)) {
-      case 1: hipLaunchKernelGGL(layer_norm_wave<1>, grid, block, 0, s, in, out, rows, c, eps); break;
-      case 2: hipLaunchKernelGGL(layer_norm_wave<2>, grid, block, 0, s, in, out, rows, c, eps); break;
-      case 4: hipLaunchKernelGGL(layer_norm_wave<4>, grid, block, 0, s, in, out, rows, c, eps); break;
-      case 8: hipLaunchKernelGGL(layer_norm_wave<8>, grid, block, 0, s, in, out, rows, c, eps); break;
-      default: hipLaunchKernelGGL(layer_norm_wave<16>, grid, block, 0, s, in, out, rows, c, eps); break;
-    }
-    return hipGetLastError();
+  const LnPlan p = ln_plan(cols, in, out);
+  // rows in launches of at most kRowsPerLaunch, so that no grid reaches 2^32
+  // threads (up to 1024 a row); a chunk starts a whole number of rows in, so
+  // the buffers' 16-byte alignment is kept where the float4 kernels need it
+  for (long long r0 = 0; r0 < rows; r0 += kRowsPerLaunch) {
+    const long long n = rows - r0 < kRowsPerLaunch ? rows - r0 : kRowsPerLaunch;
+    const hipError_t e = launch_rows(s, p, n, cols, eps, in + r0 * cols, out + r0 * cols);
+    if (e != hipSuccess) return e;
   }
-  if (rows > 0x7fffffffLL) return hipErrorInvalidValue;
-  if (pick_wg_nv(cols) > 0 && (reinterpret_cast<uintptr_t>(in) & 15) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0) {
-    const dim3 grid((unsigned)rows), block(256);
-    switch (pick_wg_nv(cols)) {
-      case 8: hipLaunchKernelGGL((layer_norm_wg<8, 256>), grid, block, 0, s, in, out, (int)cols, eps); break;
-      case 16: hipLaunchKernelGGL((layer_norm_wg<16, 256>), grid, block, 0, s, in, out, (int)cols, eps); break;
-      case 32: hipLaunchKernelGGL((layer_norm_wg<32, 256>), grid, block, 0, s, in, out, (int)cols, eps); break;
-      default: hipLaunchKernelGGL((layer_norm_wg<16, 1024>), grid, dim3(1024), 0, s, in, out, (int)cols, eps); break;
-    }
-    return hipGetLastError();
-  }
-  if (pick_wgs(cols) > 0) {
-    const dim3 grid((unsigned)rows);
-    const int c = (int)cols;
-    switch (pick_wgs(cols)) {
-      case 40256: hipLaunchKernelGGL((layer_norm_wgs<4, 256>), grid, dim3(256), 0, s, in, out, c, eps); break;
-      case 160256: hipLaunchKernelGGL((layer_norm_wgs<16, 256>), grid, dim3(256), 0, s, in, out, c, eps); break;
-      case 161024: hipLaunchKernelGGL((layer_norm_wgs<16, 1024>), grid, dim3(1024), 0, s, in, out, c, eps); break;
-      default: hipLaunchKernelGGL((layer_norm_wgs<32, 1024>), grid, dim3(1024), 0, s, in, out, c, eps); break;
-    }
-    return hipGetLastError();
-  }
-  hipLaunchKernelGGL(layer_norm_block, dim3((unsigned)rows), dim3(256), 0, s, in, out, cols, eps);
-  return hipGetLastError();
+  return hipSuccess;
 }
 
 }  // namespace bch

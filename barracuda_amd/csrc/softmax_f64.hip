@@ -228,14 +228,27 @@ hipError_t launch_softmax_rows_f64(hipStream_t s, long long rows, long long cols
   if (rows <= 0 || cols <= 0) return hipSuccess;
   const bool aligned16 = ((reinterpret_cast<uintptr_t>(in) | reinterpret_cast<uintptr_t>(out)) & 15) == 0;
   const RowPlan p = row_plan(cols, aligned16);
-  if (p.nv > 0) {
-    const int c = (int)cols;
-    if (p.vec == 2)
-      return p.w == 1 ? launch_rows<2, 1>(s, p.nv, rows, c, in, out) : launch_rows<2, 4>(s, p.nv, rows, c, in, out);
-    return p.w == 1 ? launch_rows<1, 1>(s, p.nv, rows, c, in, out) : launch_rows<1, 4>(s, p.nv, rows, c, in, out);
+  // rows in launches of at most kRowsPerLaunch (grids below 2^32 threads); a
+  // chunk starts a whole number of rows in (an even count of doubles where
+  // the 16-byte path runs), so the alignment the plan was chosen for holds
+  for (long long r0 = 0; r0 < rows; r0 += kRowsPerLaunch) {
+    const long long n = rows - r0 < kRowsPerLaunch ? rows - r0 : kRowsPerLaunch;
+    const double* x = in + r0 * cols;
+    double* y = out + r0 * cols;
+    hipError_t e;
+    if (p.nv > 0) {
+      const int c = (int)cols;
+      if (p.vec == 2)
+        e = p.w == 1 ? launch_rows<2, 1>(s, p.nv, n, c, x, y) : launch_rows<2, 4>(s, p.nv, n, c, x, y);
+      else
+        e = p.w == 1 ? launch_rows<1, 1>(s, p.nv, n, c, x, y) : launch_rows<1, 4>(s, p.nv, n, c, x, y);
+    } else {
+      hipLaunchKernelGGL(softmax_f64_block, dim3((unsigned)n), dim3(256), 0, s, x, y, cols);
+      e = hipGetLastError();
+    }
+    if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL(softmax_f64_block, dim3((unsigned)rows), dim3(256), 0, s, in, out, cols);
-  return hipGetLastError();
+  return hipSuccess;
 }
 
 }  // namespace bch

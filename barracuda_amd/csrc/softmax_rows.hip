@@ -762,33 +762,104 @@ size_t softmax_axis_workspace_bytes(long long outer, long long axis, long long i
   return nc > 1 ? sizeof(float) * 2 * (size_t)outer * nc * (size_t)inner : 0;
 }
 
-const char* softmax_kernel_name(long long rows, long long cols) {
-  if (split_plan(rows, cols).splits > 1) return "softmax_split_write";
-  if ((cols % 4) == 0) {
-    switch (pick_nv(cols)) {
-      case 1: return "softmax_rows_wave<1>";
-      case 2: return "softmax_rows_wave<2>";
-      case 4: return "softmax_rows_wave<4>";
-      case 8: return "softmax_rows_wave<8>";
-      case 16: return "softmax_rows_wave<16>";
-      default: break;
+}  // namespace bch
+
+namespace {
+
+// Which kernel a row softmax that is not split runs: the wavefront-per-row
+// register kernel (sel = NV), the workgroup-per-row float4 register kernel
+// (sel = NV, 64 meaning 16 on 1024 threads), the scalar register kernel
+// (sel = NS * 10000 + NT), or the block kernel.  The launch and the reported
+// name both come from this one choice.
+enum class SmKind { kWave, kWg, kWgs, kBlock };
+struct SmPlan {
+  SmKind kind;
+  int sel;
+};
+
+SmPlan sm_plan(long long cols, const float* in, const float* out) {
+  const bool al = (reinterpret_cast<uintptr_t>(in) % 16) == 0 && (reinterpret_cast<uintptr_t>(out) % 16) == 0;
+  if (wave_path(cols, in, out)) return {SmKind::kWave, pick_nv(cols)};
+  if (pick_wg_nv(cols) > 0 && al) return {SmKind::kWg, pick_wg_nv(cols)};
+  if (pick_wgs(cols) > 0) return {SmKind::kWgs, pick_wgs(cols)};
+  return {SmKind::kBlock, 0};
+}
+
+// One launch over n rows (n <= kRowsPerLaunch).
+hipError_t launch_sm_rows(hipStream_t s, const SmPlan& p, long long n, long long cols, const float* in, float* out) {
+  const int c = (int)cols;
+  switch (p.kind) {
+    case SmKind::kWave: {
+      const dim3 grid((unsigned)((n + 3) / 4)), block(256);
+      switch (p.sel) {
+        case 1: hipLaunchKernelGGL(softmax_rows_wave<1>, grid, block, 0, s, in, out, n, c); break;
+        case 2: hipLaunchKernelGGL(softmax_rows_wave<2>, grid, block, 0, s, in, out, n, c); break;
+        case 4: hipLaunchKernelGGL(softmax_rows_wave<4>, grid, block, 0, s, in, out, n, c); break;
+        case 8: hipLaunchKernelGGL(softmax_rows_wave<8>, grid, block, 0, s, in, out, n, c); break;
+        default: hipLaunchKernelGGL(softmax_rows_wave<16>, grid, block, 0, s, in, out, n, c); break;
+      }
+      break;
     }
+    case SmKind::kWg: {
+      const dim3 grid((unsigned)n), block(256);
+      switch (p.sel) {
+        case 8: hipLaunchKernelGGL((softmax_rows_wg<8, 256>), grid, block, 0, s, in, out, c); break;
+        case 16: hipLaunchKernelGGL((softmax_rows_wg<16, 256>), grid, block, 0, s, in, out, c); break;
+        case 32: hipLaunchKernelGGL((softmax_rows_wg<32, 256>), grid, block, 0, s, in, out, c); break;
+        default: hipLaunchKernelGGL((softmax_rows_wg<16, 1024>), grid, dim3(1024), 0, s, in, out, c); break;
+      }
+      break;
+    }
+    case SmKind::kWgs: {
+      const dim3 grid((unsigned)n);
+      switch (p.sel) {
+        case 40256: hipLaunchKernelGGL((softmax_rows_wgs<4, 256>), grid, dim3(256), 0, s, in, out, c); break;
+        case 160256: hipLaunchKernelGGL((softmax_rows_wgs<16, 256>), grid, dim3(256), 0, s, in, out, c); break;
+        case 161024: hipLaunchKernelGGL((softmax_rows_wgs<16, 1024>), grid, dim3(1024), 0, s, in, out, c); break;
+        default: hipLaunchKernelGGL((softmax_rows_wgs<32, 1024>), grid, dim3(1024), 0, s, in, out, c); break;
+      }
+      break;
+    }
+    default:
+      hipLaunchKernelGGL(softmax_rows_block, dim3((unsigned)n), dim3(256), 0, s, in, out, n, cols);
+      break;
   }
-  switch (pick_wg_nv(cols)) {
-    case 8: return "softmax_rows_wg<8>";
-    case 16: return "softmax_rows_wg<16>";
-    case 32: return "softmax_rows_wg<32>";
-    case 64: return "softmax_rows_wg<16, 1024>";
-    default: break;
+  return hipGetLastError();
+}
+
+}  // namespace
+
+namespace bch {
+
+const char* softmax_kernel_name(long long rows, long long cols, const float* in, const float* out) {
+  if (split_plan(rows, cols).splits > 1) return "softmax_split_write";
+  const SmPlan p = sm_plan(cols, in, out);
+  switch (p.kind) {
+    case SmKind::kWave:
+      switch (p.sel) {
+        case 1: return "softmax_rows_wave<1>";
+        case 2: return "softmax_rows_wave<2>";
+        case 4: return "softmax_rows_wave<4>";
+        case 8: return "softmax_rows_wave<8>";
+        default: return "softmax_rows_wave<16>";
+      }
+    case SmKind::kWg:
+      switch (p.sel) {
+        case 8: return "softmax_rows_wg<8>";
+        case 16: return "softmax_rows_wg<16>";
+        case 32: return "softmax_rows_wg<32>";
+        default: return "softmax_rows_wg<16, 1024>";
+      }
+    case SmKind::kWgs:
+      switch (p.sel) {
+        case 40256: return "softmax_rows_wgs<4, 256>";
+        case 160256: return "softmax_rows_wgs<16, 256>";
+        case 161024: return "softmax_rows_wgs<16, 1024>";
+        default: return "softmax_rows_wgs<32, 1024>";
+      }
+    default:
+      return "softmax_rows_block";
   }
-  switch (pick_wgs(cols)) {
-    case 40256: return "softmax_rows_wgs<4, 256>";
-    case 160256: return "softmax_rows_wgs<16, 256>";
-    case 161024: return "softmax_rows_wgs<16, 1024>";
-    case 321024: return "softmax_rows_wgs<32, 1024>";
-    default: break;
-  }
-  return "softmax_rows_block";
 }
 
 hipError_t launch_softmax_rows(hipStream_t s, long long rows, long long cols,
@@ -812,42 +883,16 @@ hipError_t launch_softmax_rows(hipStream_t s, long long rows, long long cols,
     }
     return hipGetLastError();
   }
-  if (wave_path(cols, in, out)) {
-    const long long blocks = (rows + 3) / 4;
-    if (blocks > 0x7fffffffLL) return hipErrorInvalidValue;
-    dim3 grid((unsigned)blocks), block(256);
-    switch (pick_nv(cols)) {
-      case 1: hipLaunchKernelGGL(softmax_rows_wave<1>, grid, block, 0, s, in, out, rows, (int)cols); break;
-      case 2: hipLaunchKernelGGL(softmax_rows_wave<2>, grid, block, 0, s, in, out, rows, (int)cols); break;
-      case 4: hipLaunchKernelGGL(softmax_rows_wave<4>, grid, block, 0, s, in, out, rows, (int)cols); break;
-      case 8: hipLaunchKernelGGL(softmax_rows_wave<8>, grid, block, 0, s, in, out, rows, (int)cols); break;
-      default: hipLaunchKernelGGL(softmax_rows_wave<16>, grid, block, 0, s, in, out, rows, (int)cols); break;
-    }
-  } else if (pick_wg_nv(cols) > 0 && (reinterpret_cast<uintptr_t>(in) % 16) == 0 &&
-             (reinterpret_cast<uintptr_t>(out) % 16) == 0) {
-    if (rows > 0x7fffffffLL) return hipErrorInvalidValue;
-    const dim3 grid((unsigned)rows), block(256);
-    switch (pick_wg_nv(cols)) {
-      case 8: hipLaunchKernelGGL((softmax_rows_wg<8, 256>), grid, block, 0, s, in, out, (int)cols); break;
-      case 16: hipLaunchKernelGGL((softmax_rows_wg<16, 256>), grid, block, 0, s, in, out, (int)cols); break;
-      case 32: hipLaunchKernelGGL((softmax_rows_wg<32, 256>), grid, block, 0, s, in, out, (int)cols); break;
-      default: hipLaunchKernelGGL((softmax_rows_wg<16, 1024>), dim3((unsigned)rows), dim3(1024), 0, s, in, out, (int)cols); break;
-    }
-  } else if (pick_wgs(cols) > 0) {
-    if (rows > 0x7fffffffLL) return hipErrorInvalidValue;
-    const dim3 grid((unsigned)rows);
-    const int c = (int)cols;
-    switch (pick_wgs(cols)) {
-      case 40256: hipLaunchKernelGGL((softmax_rows_wgs<4, 256>), grid, dim3(256), 0, s, in, out, c); break;
-      case 160256: hipLaunchKernelGGL((softmax_rows_wgs<16, 256>), grid, dim3(256), 0, s, in, out, c); break;
-      case 161024: hipLaunchKernelGGL((softmax_rows_wgs<16, 1024>), grid, dim3(1024), 0, s, in, out, c); break;
-      default: hipLaunchKernelGGL((softmax_rows_wgs<32, 1024>), grid, dim3(1024), 0, s, in, out, c); break;
-    }
-  } else {
-    if (rows > 0x7fffffffLL) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(softmax_rows_block, dim3((unsigned)rows), dim3(256), 0, s, in, out, rows, cols);
+  const SmPlan p = sm_plan(cols, in, out);
+  // rows in launches of at most kRowsPerLaunch (grids below 2^32 threads); a
+  // chunk starts a whole number of rows in, which keeps the alignment the
+  // float4 kernels were chosen for
+  for (long long r0 = 0; r0 < rows; r0 += kRowsPerLaunch) {
+    const long long n = rows - r0 < kRowsPerLaunch ? rows - r0 : kRowsPerLaunch;
+    const hipError_t e = launch_sm_rows(s, p, n, cols, in + r0 * cols, out + r0 * cols);
+    if (e != hipSuccess) return e;
   }
-  return hipGetLastError();
+  return hipSuccess;
 }
 
 hipError_t launch_softmax_axis(hipStream_t s, long long outer, long long axis,

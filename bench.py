@@ -242,7 +242,7 @@ def _bench_norm(dev, T, reps):
     wall, ev = T.run(lambda i: lib.bch_layer_norm(ctx, rows, cols, 1e-5, px, py), reps, 3)
     out["layer_norm_65536x2048"] = {"GB/s": nbytes / (ev * 1e-3) / 1e9, "us": ev * 1e3, "bytes_per_launch": nbytes,
                                     "hbm_frac": nbytes / (ev * 1e-3) / 1e9 / HBM_PEAK_GBS,
-                                    "kernel": lib.bch_layer_norm_kernel_name(rows, cols).decode()}
+                                    "kernel": lib.bch_layer_norm_kernel_name(rows, cols, px, py).decode()}
     n = rows * cols
     wall, ev = T.run(lambda i: lib.bch_elementwise(ctx, N.BCH_EW_GELU, n, px, None, None, 0.0, py), reps, 3)
     out["gelu_2^27"] = {"GB/s": nbytes / (ev * 1e-3) / 1e9, "us": ev * 1e3, "bytes_per_launch": nbytes,

@@ -210,7 +210,8 @@ bch_status bch_softmax_rows(bch_ctx *ctx, long long rows, long long cols,
 
 /* Row-wise f64 softmax: out[r,:] = exp(x - m_r) / sum_j exp(x_j - m_r), m_r
  * the row maximum folded from -inf with f64::max (NaN entries skipped).
- * rows, cols >= 1, rows <= 2^31 - 1; in == out is allowed.  Replaces the row
+ * rows, cols >= 1 (any row count: long row counts run in several launches);
+ * in == out is allowed.  Replaces the row
  * softmax of the ml.attention handler (barracuda-core/src/ipc/methods/ml/
  * forward.rs:130-140), the step between its two products (which run on
  * bch_dgemm). */
@@ -240,7 +241,8 @@ bch_status bch_elementwise(bch_ctx *ctx, int op, long long n, const float *a,
 
 /* Layer normalisation of each row of a [rows, cols] f32 matrix:
  *   out = (x - mean) / sqrt(var + eps), mean and (biased) var over the row.
- * No affine parameters; in == out is allowed.  Replaces
+ * No affine parameters; in == out is allowed; any row count (long row
+ * counts run in several launches).  Replaces
  * TensorSession::layer_norm (session/mod.rs:379-398, epsilon 1e-5 at
  * dispatch.rs:221-240) and LayerNorm::execute / Tensor::layer_norm_wgsl
  * (ops/layer_norm_wgsl.rs, shaders/norm/layer_norm_f64.wgsl). */
@@ -358,10 +360,12 @@ bch_status bch_event_elapsed_ms(bch_event *start, bch_event *stop, float *ms);
 void bch_event_destroy(bch_event *ev);
 
 /* Name of the kernel a bch_sgemm / bch_layer_norm / bch_softmax_rows_f64
- * call of this shape (and, for the f64 softmax, these buffers' alignment)
- * launches, for profilers and tests. */
+ * call of this shape (and, for layer norm and the f64 softmax, these
+ * buffers: their 16-byte alignment picks the kernel) launches, for
+ * profilers and tests. */
 const char *bch_sgemm_kernel_name(int m, int n, int k);
-const char *bch_layer_norm_kernel_name(long long rows, long long cols);
+const char *bch_layer_norm_kernel_name(long long rows, long long cols,
+                                       const float *in, const float *out);
 const char *bch_softmax_rows_f64_kernel_name(long long rows, long long cols,
                                              const double *in,
                                              const double *out);

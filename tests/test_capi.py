@@ -283,7 +283,7 @@ def test_softmax_f64_validation_and_routing_before_device():
     nul = None
     assert lib.bch_softmax_rows_f64(nul, 0, 4, nul, nul) == N.BCH_E_SHAPE
     assert lib.bch_softmax_rows_f64(nul, 4, 0, nul, nul) == N.BCH_E_SHAPE
-    assert lib.bch_softmax_rows_f64(nul, 1 << 31, 4, nul, nul) == N.BCH_E_UNSUPPORTED
+    assert lib.bch_softmax_rows_f64(nul, 1 << 31, 4, nul, nul) == N.BCH_E_INVALID  # any row count; ctx NULL
     assert lib.bch_softmax_rows_f64(nul, 4, 4, nul, nul) == N.BCH_E_INVALID
     name = lambda r, c, p: lib.bch_softmax_rows_f64_kernel_name(r, c, C.c_void_p(p), C.c_void_p(p))
     assert name(65536, 2048, 0x1000) == b"softmax_f64_rows<4,2,4>"
@@ -305,16 +305,25 @@ def test_elementwise_and_layer_norm_validation_before_device():
     assert lib.bch_layer_norm(nul, 0, 4, 1e-5, nul, nul) == N.BCH_E_SHAPE
     assert lib.bch_layer_norm(nul, 4, 4, -1.0, nul, nul) == N.BCH_E_INVALID
     assert lib.bch_layer_norm(nul, 4, 4, float("nan"), nul, nul) == N.BCH_E_INVALID
-    assert lib.bch_layer_norm(nul, 1 << 31, 4, 1e-5, nul, nul) == N.BCH_E_UNSUPPORTED
+    assert lib.bch_layer_norm(nul, 1 << 31, 4, 1e-5, nul, nul) == N.BCH_E_INVALID  # any row count; ctx NULL
     assert lib.bch_layer_norm(nul, 4, 4, 1e-5, nul, nul) == N.BCH_E_INVALID
     assert "ctx" in N.last_error(None)
     assert lib.bch_sgemm_ex(nul, 0, 4, 4, 4, nul, 4, nul, 4, nul, 3, nul, 4) == N.BCH_E_INVALID
     assert lib.bch_sgemm_ex(nul, 1, 4, 4, 4, nul, 4, nul, 4, nul, N.BCH_ACT_GELU, nul, 4) == N.BCH_E_INVALID
     assert "ctx" in N.last_error(None)
-    assert lib.bch_layer_norm_kernel_name(65536, 2048) == b"layer_norm_wave<8>"
-    assert lib.bch_layer_norm_kernel_name(3, 4100) == b"layer_norm_wg<8>"
-    assert lib.bch_layer_norm_kernel_name(3, 32768) == b"layer_norm_wg<32>"
-    assert lib.bch_layer_norm_kernel_name(3, 32772) == b"layer_norm_wg<16, 1024>"
-    assert lib.bch_layer_norm_kernel_name(3, 65540) == b"layer_norm_block"
-    assert lib.bch_layer_norm_kernel_name(3, 4099) == b"layer_norm_wgs<16, 1024>"
-    assert lib.bch_layer_norm_kernel_name(3, 32771) == b"layer_norm_block"
+    # the name follows the buffers' alignment, as the launch does
+    name = lambda r, c, p=0x1000, q=None: lib.bch_layer_norm_kernel_name(r, c, C.c_void_p(p),
+                                                                         C.c_void_p(p if q is None else q))
+    assert name(65536, 2048) == b"layer_norm_wave<8>"
+    assert name(3, 4100) == b"layer_norm_wg<8>"
+    assert name(3, 32768) == b"layer_norm_wg<32>"
+    assert name(3, 32772) == b"layer_norm_wg<16, 1024>"
+    assert name(3, 65540) == b"layer_norm_block"
+    assert name(3, 4099) == b"layer_norm_wgs<16, 1024>"
+    assert name(3, 32771) == b"layer_norm_block"
+    # one float off 16-byte alignment (input or output): the scalar register kernels
+    assert name(65536, 2048, 0x1004) == b"layer_norm_wgs<16, 256>"
+    assert name(65536, 2048, 0x1000, 0x2004) == b"layer_norm_wgs<16, 256>"
+    assert name(3, 8192, 0x1004) == b"layer_norm_wgs<16, 1024>"
+    assert name(3, 32768, 0x1004) == b"layer_norm_wgs<32, 1024>"
+    assert name(3, 65536, 0x1004) == b"layer_norm_block"

@@ -100,7 +100,7 @@ def test_layer_norm_shapes(dev, rows, cols):
     _say(f"layer_norm rows={rows} cols={cols}")
     x = O.Lcg(rows * 7 + cols).normal((rows, cols), 1.5, 3.0)
     got = LayerNorm(Tensor.from_data(x, [rows, cols], dev), 1e-5).execute().to_numpy()
-    _say(f"  kernel {dev._lib.bch_layer_norm_kernel_name(rows, cols).decode()}")
+    _say(f"  kernel {dev._lib.bch_layer_norm_kernel_name(rows, cols, None, None).decode()}")
     assert O.max_rel_err(got, O.layer_norm_f64(x)) <= TOL
     assert O.max_rel_err(got, O.layer_norm_f32(x)) <= TOL
 
@@ -241,3 +241,51 @@ def test_session_new_op_errors(dev):
     with pytest.raises(ShapeMismatch):
         s.reshape(x, [5, 2])
     assert s.num_ops() == 0
+
+
+def _rows_offset(dev, fn, x, offset_in, offset_out):
+    """Run fn(ctx, rows, cols, pin, pout) on buffers whose data starts offset_* floats into a larger
+    allocation (so the pointers are 4-byte but not 16-byte aligned when the offset is odd)."""
+    rows, cols = x.shape
+    n = rows * cols
+    tin = Tensor.from_data(np.concatenate([np.zeros(offset_in, np.float32), x.reshape(-1)]), [n + offset_in], dev)
+    tout = Tensor.from_data(np.full(n + offset_out + 3, 7.0, np.float32), [n + offset_out + 3], dev)
+    pin, pout = C.c_void_p(tin.ptr + 4 * offset_in), C.c_void_p(tout.ptr + 4 * offset_out)
+    with dev._lock:
+        dev.check(fn(dev.ctx, rows, cols, pin, pout), "row op")
+    out = tout.to_numpy()
+    assert np.all(out[:offset_out] == 7.0) and np.all(out[offset_out + n:] == 7.0)  # nothing written outside
+    return out[offset_out:offset_out + n].reshape(rows, cols), pin, pout
+
+
+@pytest.mark.parametrize("rows,cols", [(300, 2048), (40, 8192), (6, 32768)])
+@pytest.mark.parametrize("oin,oout", [(1, 1), (1, 0), (0, 1)])
+def test_layer_norm_unaligned_buffers(dev, rows, cols, oin, oout):
+    """Widths divisible by 4 on buffers one float off 16-byte alignment take the scalar
+    register kernels; the reported kernel name follows the same choice."""
+    x = O.Lcg(rows + cols + oin).normal((rows, cols), 1.5, 3.0)
+    lib = dev._lib
+    got, pin, pout = _rows_offset(dev, lambda c, r, k, a, b: lib.bch_layer_norm(c, r, k, 1e-5, a, b), x, oin, oout)
+    name = lib.bch_layer_norm_kernel_name(rows, cols, pin, pout).decode()
+    _say(f"layer_norm unaligned rows={rows} cols={cols} in+{oin} out+{oout}: {name}")
+    assert name.startswith("layer_norm_wgs")
+    assert O.max_rel_err(got, O.layer_norm_f64(x)) <= TOL
+
+
+def test_layer_norm_row_count_past_one_grid(dev):
+    """2^26 + 3 rows of 4: the wavefront-per-row kernel in one grid would need more than 2^32
+    threads; the call runs in launches of 2^21 rows.  Rows at every launch boundary and a sample
+    against f64; every row's mean is ~0."""
+    rows, cols = (1 << 26) + 3, 4
+    _say(f"layer_norm rows={rows} cols={cols}")
+    from barracuda_amd import LcgStream
+    x = LcgStream(44, dev).normal([rows, cols], 0.5, 2.0)
+    y = Tensor.empty([rows, cols], dev)
+    with dev._lock:
+        dev.check(dev._lib.bch_layer_norm(dev.ctx, rows, cols, 1e-5, C.c_void_p(x.ptr), C.c_void_p(y.ptr)), "ln")
+    xs, ys = x.to_numpy().reshape(rows, cols), y.to_numpy().reshape(rows, cols)
+    # every row's mean is ~0 (rows whose variance is near eps amplify the f32 rounding of x - mean)
+    assert np.max(np.abs(ys.astype(np.float64).mean(axis=1))) < 1e-4
+    edge = [b + d for b in range(0, rows + 1, 1 << 21) for d in (-1, 0, 1)]
+    sample = sorted({r for r in edge if 0 <= r < rows} | set(range(0, rows, 99991)) | {rows - 1})
+    assert O.max_rel_err(ys[sample], O.layer_norm_f64(np.ascontiguousarray(xs[sample]))) <= TOL

@@ -220,3 +220,39 @@ def test_global_softmax_large(dev):
     assert O.max_rel_err(ty.to_vec(), O.softmax_rows_f64(y.reshape(1, m)).reshape(-1)) <= TOL
     y[12345] = np.nan
     assert np.all(np.isnan(Tensor.from_data(y, [m], dev).softmax().to_vec()))
+
+
+@pytest.mark.parametrize("rows,cols", [(300, 2048), (40, 8192), (6, 32768)])
+@pytest.mark.parametrize("oin,oout", [(1, 1), (1, 0), (0, 1)])
+def test_rows_on_unaligned_buffers(dev, rows, cols, oin, oout):
+    """Widths divisible by 4 on buffers one float off 16-byte alignment (the C ABI takes any
+    4-byte aligned pointer): the scalar register kernels; nothing written outside the output."""
+    _say(f"softmax unaligned rows={rows} cols={cols} in+{oin} out+{oout}")
+    x = O.Lcg(rows + cols + 3 * oin + oout).normal((rows, cols), 0.0, 3.0)
+    n = rows * cols
+    tin = Tensor.from_data(np.concatenate([np.zeros(oin, np.float32), x.reshape(-1)]), [n + oin], dev)
+    tout = Tensor.from_data(np.full(n + oout + 3, 7.0, np.float32), [n + oout + 3], dev)
+    with dev._lock:
+        dev.check(dev._lib.bch_softmax_rows(dev.ctx, rows, cols, C.c_void_p(tin.ptr + 4 * oin),
+                                            C.c_void_p(tout.ptr + 4 * oout)), "softmax")
+    out = tout.to_numpy()
+    assert np.all(out[:oout] == 7.0) and np.all(out[oout + n:] == 7.0)
+    assert O.max_rel_err(out[oout:oout + n].reshape(rows, cols), O.softmax_rows_f64(x)) <= TOL
+
+
+def test_row_count_past_one_grid(dev):
+    """2^26 + 3 rows of 4: one grid of the wavefront-per-row kernel would need more than 2^32
+    threads; the call runs in launches of 2^21 rows.  Every row sums to 1; rows at every launch
+    boundary and a sample against f64."""
+    from barracuda_amd import LcgStream
+    rows, cols = (1 << 26) + 3, 4
+    _say(f"softmax rows={rows} cols={cols}")
+    x = LcgStream(45, dev).normal([rows, cols], 0.0, 3.0)
+    y = Tensor.empty([rows, cols], dev)
+    with dev._lock:
+        dev.check(dev._lib.bch_softmax_rows(dev.ctx, rows, cols, C.c_void_p(x.ptr), C.c_void_p(y.ptr)), "softmax")
+    xs, ys = x.to_numpy().reshape(rows, cols), y.to_numpy().reshape(rows, cols)
+    assert np.max(np.abs(ys.sum(axis=1, dtype=np.float64) - 1.0)) < 1e-5
+    edge = [b + d for b in range(0, rows + 1, 1 << 21) for d in (-1, 0, 1)]
+    sample = sorted({r for r in edge if 0 <= r < rows} | set(range(0, rows, 99991)) | {rows - 1})
+    assert O.max_rel_err(ys[sample], O.softmax_rows_f64(np.ascontiguousarray(xs[sample]))) <= TOL

@@ -106,3 +106,19 @@ def test_attention_f64_vs_oracle(dev, sq, sk, dk, dv):
     got = linalg.attention_f64(dev, q, k, v)
     want = O.ml_attention_f64(q, k, v)
     assert np.max(np.abs(got - want)) <= 1e-12 * max(1.0, np.max(np.abs(want)))
+
+
+def test_softmax_f64_row_count_past_one_grid(dev):
+    """2^26 + 3 rows of 2 doubles: one grid of the wavefront-per-row kernel would need more than
+    2^32 threads; the call runs in launches of 2^21 rows.  Rows at every launch boundary and a
+    sample against the handler's loop restated."""
+    rows, cols = (1 << 26) + 3, 2
+    _say(f"softmax_f64 rows={rows} cols={cols}")
+    rng = np.random.default_rng(46)
+    x = rng.normal(0.0, 3.0, (rows, cols))
+    got, name = _run(dev, x)
+    _say(f"  kernel {name}")
+    edge = [b + d for b in range(0, rows + 1, 1 << 21) for d in (-1, 0, 1)]
+    sample = sorted({r for r in edge if 0 <= r < rows} | set(range(0, rows, 99991)) | {rows - 1})
+    _close(got[sample], O.ml_softmax_rows_f64(np.ascontiguousarray(x[sample])))
+    assert np.max(np.abs(got.sum(axis=1) - 1.0)) < 1e-12
