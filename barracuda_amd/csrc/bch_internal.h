@@ -174,6 +174,20 @@ hipError_t launch_fill_normal(hipStream_t s, float* out, uint64_t n, uint64_t st
                               double sigma);
 uint64_t lcg_advance(uint64_t state, uint64_t inc, uint64_t n);
 
+// Launch controls of the calling context, set by the C ABI on the calling
+// thread before a call's launches (a context's calls run on the thread that
+// makes them, one at a time).  fault: a device-visible word in pinned host
+// memory that the [out, in] skinny GEMM's in-kernel split-k combine sets when
+// an owner gives up waiting for a contributor (its outputs are then NaN);
+// the context reports BCH_E_DEVICE_LOST at its next synchronisation and
+// every later call.  spin: that wait's poll limit (0 gives up at once: a
+// host-side way to force the path in tests, every kernel still exiting).
+struct LaunchCtl {
+  unsigned* fault = nullptr;
+  unsigned spin = 1u << 22;
+};
+LaunchCtl& launch_ctl();
+
 // Compute units of the current device, cached per device; kDefaultCUs
 // (MI355X) when no device is visible, so launch plans and kernel names can
 // be computed without a GPU.

@@ -63,6 +63,15 @@ struct bch_ctx {
   // with the reason in scratch_error.
   void* scratch = nullptr;
   std::string scratch_error;
+  // Fault word in pinned host memory (device-visible): set by a kernel that
+  // gave up a bounded wait (the skinny ring GEMM's split-k combine); read on
+  // the host after every synchronisation and at every call, it marks the
+  // context lost.  ring_spin: that wait's poll limit
+  // (BARRACUDA_HIP_RING_SPIN, read at bch_ctx_create, forces the path in
+  // tests).
+  unsigned* fault_host = nullptr;
+  unsigned* fault_dev = nullptr;
+  unsigned ring_spin = 1u << 22;
 };
 
 struct bch_event {
@@ -73,6 +82,7 @@ struct bch_event {
 namespace {
 
 thread_local std::string t_last_error;
+thread_local bch::LaunchCtl t_launch_ctl;
 
 bch_status fail(bch_ctx* ctx, bch_status st, const char* fmt, ...) {
   char buf[512];
@@ -126,6 +136,19 @@ bch_status from_hip(bch_ctx* ctx, hipError_t e, const char* what) {
   return fail(ctx, st, "%s: %s (%d)", what, hipGetErrorString(e), (int)e);
 }
 
+// A kernel on this context gave up a bounded wait: the context is lost.
+bch_status check_fault(bch_ctx* ctx) {
+  if (!ctx->fault_host || *reinterpret_cast<volatile unsigned*>(ctx->fault_host) == 0) return BCH_OK;
+  bch_status st = fail(ctx, BCH_E_DEVICE_LOST,
+                       "split-k combine timed out in the [out, in] skinny GEMM (a partial block never arrived; "
+                       "its outputs were set to NaN)");
+  if (!ctx->lost) {
+    ctx->lost = true;
+    ctx->lost_reason = ctx->last_error;
+  }
+  return st;
+}
+
 // The context's stream is being captured into a graph (or a capture on it
 // was invalidated and not yet ended).
 bool capturing(bch_ctx* ctx) {
@@ -140,6 +163,9 @@ bool capturing(bch_ctx* ctx) {
 // Every call that touches the device starts here.
 bch_status use(bch_ctx* ctx) {
   if (ctx->lost) return fail(ctx, BCH_E_DEVICE_LOST, "device lost: %s", ctx->lost_reason.c_str());
+  if (check_fault(ctx) != BCH_OK) return BCH_E_DEVICE_LOST;
+  bch::launch_ctl().fault = ctx->fault_dev;
+  bch::launch_ctl().spin = ctx->ring_spin;
   if (ctx->inject_hip_error) {
     const hipError_t e = static_cast<hipError_t>(ctx->inject_hip_error);
     ctx->inject_hip_error = 0;
@@ -225,6 +251,10 @@ void resolve_scratch(bch_ctx* ctx) {
 
 }  // namespace
 
+namespace bch {
+LaunchCtl& launch_ctl() { return t_launch_ctl; }
+}  // namespace bch
+
 extern "C" {
 
 const char* bch_status_string(bch_status s) {
@@ -286,6 +316,19 @@ bch_status bch_ctx_create(int device, const char* code_object_dir, bch_ctx** out
     return st;
   }
   resolve_scratch(ctx);
+  if (const char* sp = getenv("BARRACUDA_HIP_RING_SPIN")) ctx->ring_spin = (unsigned)strtoul(sp, nullptr, 10);
+  void* fh = nullptr;
+  void* fd = nullptr;
+  if (hipHostMalloc(&fh, 64, hipHostMallocMapped) == hipSuccess && fh) {
+    *static_cast<volatile unsigned*>(fh) = 0;
+    if (hipHostGetDevicePointer(&fd, fh, 0) == hipSuccess && fd) {
+      ctx->fault_host = static_cast<unsigned*>(fh);
+      ctx->fault_dev = static_cast<unsigned*>(fd);
+    } else {
+      (void)hipHostFree(fh);
+    }
+  }
+  (void)hipGetLastError();
   *out = ctx;
   return BCH_OK;
 }
@@ -323,6 +366,7 @@ void bch_ctx_destroy(bch_ctx* ctx) {
   for (auto& kv : ctx->modules) (void)hipModuleUnload(kv.second);
   if (ctx->ws) (void)hipFree(ctx->ws);
   for (void* p : ctx->retired) (void)hipFree(p);
+  if (ctx->fault_host) (void)hipHostFree(ctx->fault_host);
   if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
   delete ctx;
 }
@@ -372,7 +416,8 @@ bch_status bch_download(bch_ctx* ctx, void* dst, const void* src, size_t bytes) 
   if (st != BCH_OK) return st;
   hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
-  return from_hip(ctx, e, "bch_download");
+  st = from_hip(ctx, e, "bch_download");
+  return st != BCH_OK ? st : check_fault(ctx);
 }
 
 bch_status bch_memset(bch_ctx* ctx, void* dst, int value, size_t bytes) {
@@ -395,7 +440,8 @@ bch_status bch_sync(bch_ctx* ctx) {
   if (!ctx) return fail(ctx, BCH_E_INVALID, "bch_sync: ctx is NULL");
   bch_status st = use(ctx);
   if (st != BCH_OK) return st;
-  return from_hip(ctx, hipStreamSynchronize(ctx->stream), "bch_sync");
+  st = from_hip(ctx, hipStreamSynchronize(ctx->stream), "bch_sync");
+  return st != BCH_OK ? st : check_fault(ctx);
 }
 
 bch_status bch_sgemm_ex(bch_ctx* ctx, int transb, int m, int n, int k, const float* A, int lda, const float* B,

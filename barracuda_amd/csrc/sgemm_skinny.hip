@@ -553,10 +553,14 @@ hipError_t launch_sk_reduce(hipStream_t s, int m, int n, const float* P, long lo
 //     epilogue, stores C and resets the flags.
 // An owner waits only on lower-numbered workgroups, which are dispatched
 // before it and never wait before storing their block, so the wait always
-// ends; it is bounded anyway (a block that never arrives turns the outputs
-// NaN).  The epoch (64-bit, one per launch) keeps stale flags from matching;
-// the reset keeps a replay of a captured launch, which reuses its epoch,
-// from matching the previous replay's flags.  EDGE (K % KU != 0): loads past
+// ends; it is bounded anyway (LaunchCtl::spin polls, 2^22 by default, about
+// 0.1 s): a block that never arrives turns the outputs NaN and sets the
+// calling context's fault word, so the host reports a lost device at its
+// next synchronisation instead of returning NaN silently.  The epoch (64-bit,
+// one per launch) keeps stale flags from matching; the reset keeps a replay
+// of a captured launch, which reuses its epoch, from matching the previous
+// replay's flags (a contributor that sets its flag after its owner gave up
+// could match a later replay's owner, but the context is lost by then).  EDGE (K % KU != 0): loads past
 // K read from K - 4 and both MFMA operands of such k are zeroed where they
 // are used; rows past N read row N - 1 and are never stored.  Requires
 // K % 4 == 0, lda % 4 == 0, ldw % 4 == 0 and 16-byte aligned A and W.
@@ -611,13 +615,13 @@ __device__ __forceinline__ void rg_barrier() {
 // s_waitcnt lgkmcnt(0) (vmcnt and expcnt left at their maximum)
 constexpr int kLgkmZero = 0xC07F;
 
-constexpr unsigned kRgSpin = 1u << 22;  // owner's polls of one flag (about 0.1 s) before giving up
 
 template <int MB, int RB, bool EDGE>
 __global__ __launch_bounds__(512, 1) void sgemm_skinny_nt_ring(
     int M, int N, int K, const float* __restrict__ A, int lda, const float* __restrict__ W, int ldw,
     float* __restrict__ C, int ldc, const float* __restrict__ bias, int act, float* __restrict__ P,
-    unsigned long long* __restrict__ F, unsigned long long epoch, long long U, int G, int nkb, int smax) {
+    unsigned long long* __restrict__ F, unsigned long long epoch, long long U, int G, int nkb, int smax,
+    unsigned* __restrict__ fault, unsigned spin) {
   using S = RgShape<RB>;
   constexpr int R = S::R, KU = S::KU, KQ = S::KQ, TT = S::TT, RPI = S::RPI;
   extern __shared__ float4 smem4[];
@@ -825,12 +829,17 @@ __global__ __launch_bounds__(512, 1) void sgemm_skinny_nt_ring(
     // every flag first, then the blocks in batches of up to four slots (one round trip each)
     for (int sl = 0; sl < nprev; ++sl) {
       unsigned n = 0;
-      while (__hip_atomic_load(fl + 4 * sl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != epoch && n < kRgSpin) {
+      while (__hip_atomic_load(fl + 4 * sl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != epoch && n < spin) {
         __builtin_amdgcn_s_sleep(1);
         ++n;
       }
-      ok = ok && n < kRgSpin;
+      ok = ok && n < spin;
     }
+    // a block that never arrived: the outputs become NaN and the context's
+    // fault word (pinned host memory) is set, which the host reports as a
+    // lost device at its next synchronisation
+    if (!ok && lane == 0 && fault != nullptr)
+      __hip_atomic_store(fault, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     for (int s0 = 0; s0 < nprev; s0 += 4) {
       float v[4][NV];
 #pragma unroll
@@ -1195,7 +1204,8 @@ hipError_t launch_nt_ring(hipStream_t s, const NtPlan& p, int m, int n, int k, c
   hipError_t e = bch::ensure_dynamic_lds(f, rg_lds_bytes<MB, RB>());
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL((sgemm_skinny_nt_ring<MB, RB, EDGE>), dim3(p.G), dim3(512), (rg_lds_bytes<MB, RB>()), s, m, n,
-                     k, A, lda, W, ldw, r.C, r.ldc, r.bias, r.act, r.P, r.F, r.epoch, p.U, p.G, p.nkb, p.smax);
+                     k, A, lda, W, ldw, r.C, r.ldc, r.bias, r.act, r.P, r.F, r.epoch, p.U, p.G, p.nkb, p.smax,
+                     bch::launch_ctl().fault, bch::launch_ctl().spin);
   return hipGetLastError();
 }
 

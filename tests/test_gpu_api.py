@@ -197,3 +197,41 @@ def test_injected_recoverable_errors_keep_the_context(monkeypatch, hip_error, ki
     t = Tensor.from_data(np.ones(8, np.float32), [2, 4], d)
     assert np.array_equal(t.to_vec(), np.ones(8, np.float32))
     d.close()
+
+
+def test_ring_combine_timeout_is_reported(monkeypatch):
+    """The [out, in] decode GEMM combines split-k blocks in its kernel with a bounded wait.
+    BARRACUDA_HIP_RING_SPIN=0 (read at context creation) makes every owner give up at once,
+    with every kernel still exiting normally: the outputs it could not combine are NaN, and the
+    context reports DeviceLost at its next synchronisation and on every later call instead of
+    returning NaN silently.  Another context computes the same call correctly."""
+    _say("ring combine timeout forced from the host")
+    import ctypes as C
+    from barracuda_amd import DeviceLost, HipDevice
+    m, n, k = 16, 11008, 4096  # 8 < m <= 32: the ring kernel with split groups
+    good = HipDevice(0)
+    rng = O.Lcg(616)
+    x, w = rng.normal((m, k)), rng.normal((n, k), 0.0, 0.02)
+    tx, tw = Tensor.from_data(x, [m, k], good), Tensor.from_data(w, [n, k], good)
+    ty = Tensor.from_data(np.zeros((m, n), np.float32), [m, n], good)
+    monkeypatch.setenv("BARRACUDA_HIP_RING_SPIN", "0")
+    d = HipDevice(0)
+    monkeypatch.delenv("BARRACUDA_HIP_RING_SPIN")
+    lib = d._lib
+    st = lib.bch_sgemm_ex(d.ctx, 1, m, n, k, C.c_void_p(tx.ptr), k, C.c_void_p(tw.ptr), k, None, 0,
+                          C.c_void_p(ty.ptr), n)
+    assert st == 0
+    with pytest.raises(DeviceLost, match="split-k combine timed out"):
+        d.sync()
+    assert d.is_lost()
+    with pytest.raises(DeviceLost):
+        d.sync()
+    got = ty.to_numpy()  # through the healthy context
+    assert np.isnan(got).any()
+    d.close()
+    good.check(lib.bch_sgemm_ex(good.ctx, 1, m, n, k, C.c_void_p(tx.ptr), k, C.c_void_p(tw.ptr), k, None, 0,
+                                C.c_void_p(ty.ptr), n), "sgemm_ex")
+    assert O.max_rel_err(ty.to_numpy(), O.matmul_f64(x, np.ascontiguousarray(w.T))) <= 1e-4
+    assert not good.is_lost()
+    del tx, tw, ty
+    good.close()
