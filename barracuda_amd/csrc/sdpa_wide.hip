@@ -16,10 +16,11 @@
 //   2. S = scale * S with the causal mask (keys past the query set to -inf),
 //      then the HBM-streaming row softmax in place;
 //   3. O = P V on the same GEMM, written through O's row stride.
-// At D > 256 the two products carry 4 D flops per score against 8 bytes of
-// score traffic per step, so the GEMMs (MFMA-bound at 86-93%) dominate: at
-// B=4, H=32, S=2048, D=512 the three steps of one query chunk move 2 x 256
-// MiB of scores against 2 x 68.7 GFLOP.
+// At D > 256 the two products carry 4 D flops per score against about 24
+// bytes of score traffic (stored, scaled and masked, normalised, read back),
+// above the FP32 ridge of 19.7 FLOP/B, so the GEMMs dominate.  Measured at
+// B=4, H=32, S=2048, D=512 (one box): 9.76 ms non-causal (71.6% of FP32 MFMA
+// peak), 6.21 ms causal (56.3%).
 //
 // Layout of the passes: for each batch b and query head g of a key/value
 // group (query head h = hk * G + g reads key/value head hk), one batched GEMM
