@@ -35,9 +35,10 @@
 //     in registers: read once, max and sum by xor shuffles and LDS, write
 //     once.  Otherwise the axis is cut into chunks: a stats kernel from
 //     registers, then a streaming kernel that merges the chunk states and
-//     writes.  Any other inner: scalar lanes over 64-column strips, online
-//     states merged in LDS.  Block numbers are renumbered so that each XCD
-//     reads a contiguous run of strips.
+//     writes; with inner >= 1024 the three passes (stats, merge, write)
+//     read whole 4 KB row segments instead.  Any other inner: scalar lanes
+//     over 64-column strips, online states merged in LDS.  Block numbers are
+//     renumbered so that each XCD reads a contiguous run of strips.
 // exp(x) is 2^(x log2 e) on v_exp_f32 with the product's rounding error
 // carried as a first-order correction (x*log2e split into p + e exactly with
 // one fma), which keeps it within ~2 ulp of a correctly rounded expf over
@@ -675,6 +676,196 @@ void launch_cols_vec_w(hipStream_t s, const VecPlan& p, long long outer, long lo
     launch_cols_vec_r<W, NT, true>(s, p, blocks, axis, inner4, in, out, part, outer * p.nchunks * inner4);
 }
 
+// ---- Wide rows, long axis: [outer, axis, inner] with inner >= 1024 (float4, aligned) and an
+// axis too long for a column strip in registers.  The strips of the float4 plan (8 float4 of a row
+// per workgroup, rows 8 KB apart at inner = 2048) streamed the write pass at 4.5 TB/s; here every
+// pass reads whole rows: a workgroup of 256 threads covers 256 float4 columns (4 KB of a row) and
+// walks a chunk of rows, so each wavefront touches 1 KB contiguous per row and the workgroup's rows
+// follow each other in memory.
+//   stats: per column, a running (max, sum) over the chunk's rows in register batches of kWideRb
+//          rows (batch max, one rescale, batch sum), stored per chunk as (max, sum);
+//   merge: per column, the chunks' states merged in a fixed order (kMergeSlots chunk slots a
+//          column, each taking every kMergeSlots-th chunk, then a shuffle-down tree and the
+//          wavefronts in order), stored as (max, 1 / sum);
+//   write: per column, y = exp(x - max) / sum, streamed; write chunk c takes rows c, c + nchunks,
+//          ..., so the workgroups in flight cover neighbouring rows (186 us against 194 us for
+//          contiguous chunks at 1 x 65536 x 2048; the stats pass is faster on contiguous chunks).
+// An all -inf chunk is the empty state (-inf, 0); NaN anywhere in a column makes it all NaN, as
+// the float4 plan does.
+constexpr int kWideCols = 256;  // float4 columns per workgroup (one per thread)
+constexpr int kWideRb = 8;      // rows per register batch
+
+struct WidePlan {
+  bool on = false;
+  long long ncb = 0, ch = 0, nchunks = 0;  // column blocks, rows per chunk, chunks
+};
+
+WidePlan wide_plan(long long outer, long long axis, long long inner) {
+  WidePlan p;
+  if (inner % 4 != 0 || inner / 4 < kWideCols) return p;
+  const VecPlan vp = vec_plan(outer, axis, inner);
+  if (vp.w == 0 || vp.nchunks == 1) return p;  // the strips fit in registers: read once, write once
+  const long long inner4 = inner / 4;
+  p.ncb = (inner4 + kWideCols - 1) / kWideCols;
+  // about 4 workgroups a CU over the whole tensor, rows a multiple of the batch, 16..4096
+  const long long target = 4LL * bch::device_cu_count();
+  long long ch = (outer * p.ncb * axis + target - 1) / target;
+  ch = (ch + kWideRb - 1) / kWideRb * kWideRb;
+  ch = ch < 16 ? 16 : ch > 4096 ? 4096 : ch;
+  p.ch = ch;
+  p.nchunks = (axis + ch - 1) / ch;
+  p.on = outer * p.nchunks * p.ncb <= 0x7fffffffLL && outer * inner4 <= 0x7fffffffLL;
+  return p;
+}
+
+size_t wide_bytes(long long outer, long long inner, const WidePlan& p) {
+  // per-chunk states (max, sum), then the merged (max, 1 / sum), all float4 per column
+  return sizeof(float) * 2 * (size_t)outer * (size_t)inner * (size_t)(p.nchunks + 1);
+}
+
+__device__ __forceinline__ float4 max4(float4 a, float4 b) {
+  return make_float4(fmaxf(a.x, b.x), fmaxf(a.y, b.y), fmaxf(a.z, b.z), fmaxf(a.w, b.w));
+}
+
+// running state (m, s) merged with a batch whose max is bm and whose values are v[0..n)
+__device__ __forceinline__ void wide_batch(float& m, float& s, float bm, const float* v, int n) {
+  const float mn = fmaxf(m, bm);
+  if (mn == -INFINITY) return;  // all -inf so far: the empty state
+  float acc = m == -INFINITY ? 0.0f : s * exp_f32(m - mn);
+  for (int i = 0; i < n; ++i) acc += exp_f32(v[i] - mn);
+  s = acc;
+  m = mn;
+}
+
+__global__ __launch_bounds__(256) void softmax_cols_wide_stats(const float4* __restrict__ in, long long axis,
+                                                               long long inner4, long long ncb, long long nchunks,
+                                                               long long ch, float4* __restrict__ part,
+                                                               long long plane) {
+  const long long b = blockIdx.x;
+  const long long cb = b % ncb, t = b / ncb, chunk = t % nchunks, o = t / nchunks;
+  const long long col4 = cb * kWideCols + threadIdx.x;
+  if (col4 >= inner4) return;
+  const long long r0 = chunk * ch, r1 = r0 + ch < axis ? r0 + ch : axis;
+  const float4* x = in + o * axis * inner4 + col4;
+  const float ninf = -INFINITY;
+  float4 m = make_float4(ninf, ninf, ninf, ninf), sm = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  for (long long r = r0; r < r1; r += kWideRb) {
+    float4 v[kWideRb];
+#pragma unroll
+    for (int i = 0; i < kWideRb; ++i)
+      v[i] = r + i < r1 ? bch::load_nt(x + (r + i) * inner4) : make_float4(ninf, ninf, ninf, ninf);
+    float4 bm = v[0];
+#pragma unroll
+    for (int i = 1; i < kWideRb; ++i) bm = max4(bm, v[i]);
+    float c[kWideRb];
+#pragma unroll
+    for (int i = 0; i < kWideRb; ++i) c[i] = v[i].x;
+    wide_batch(m.x, sm.x, bm.x, c, kWideRb);
+#pragma unroll
+    for (int i = 0; i < kWideRb; ++i) c[i] = v[i].y;
+    wide_batch(m.y, sm.y, bm.y, c, kWideRb);
+#pragma unroll
+    for (int i = 0; i < kWideRb; ++i) c[i] = v[i].z;
+    wide_batch(m.z, sm.z, bm.z, c, kWideRb);
+#pragma unroll
+    for (int i = 0; i < kWideRb; ++i) c[i] = v[i].w;
+    wide_batch(m.w, sm.w, bm.w, c, kWideRb);
+  }
+  const long long p = (o * nchunks + chunk) * inner4 + col4;
+  part[p] = m;
+  part[plane + p] = sm;
+}
+
+// A workgroup of 256 merges kMergeCols adjacent float4 columns q (of one outer index): thread t
+// takes column t % kMergeCols and chunk slot j = t / kMergeCols, i.e. chunks j, j + kMergeSlots,
+// ..., so a wavefront's loads are runs of kMergeCols * 16 bytes; a shuffle-down tree over the
+// slots of a wavefront and then the four wavefronts, in order, finish each column.  Workgroups
+// are renumbered XCD-major (xcd_block), so the workgroups whose columns share 128-byte lines read
+// them through one L2.  fin[q] = max, fin[nq + q] = 1 / sum.
+constexpr int kMergeCols = 1;
+constexpr int kMergeSlots = 256 / kMergeCols;
+__global__ __launch_bounds__(256) void softmax_cols_wide_merge(const float4* __restrict__ part, long long plane,
+                                                               long long nchunks, long long inner4, long long nq,
+                                                               float4* __restrict__ fin) {
+  __shared__ float4 wm[4][kMergeCols], wsum[4][kMergeCols];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, c = threadIdx.x % kMergeCols;
+  const long long per = (inner4 + kMergeCols - 1) / kMergeCols;  // column groups of one outer index
+  const long long b = xcd_block();
+  const long long o = b / per, col4 = (b - o * per) * kMergeCols + c;
+  const float ninf = -INFINITY;
+  float4 m = make_float4(ninf, ninf, ninf, ninf), sm = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  if (col4 < inner4) {
+    const float4* pm = part + o * nchunks * inner4 + col4;
+    for (long long k = threadIdx.x / kMergeCols; k < nchunks; k += kMergeSlots)
+      merge_state4(m, sm, pm[k * inner4], pm[plane + k * inner4]);
+  }
+#pragma unroll
+  for (int off = 32; off >= kMergeCols; off >>= 1) {  // lanes < off take lane + off's state
+    const float4 m2 = make_float4(__shfl_down(m.x, off), __shfl_down(m.y, off), __shfl_down(m.z, off),
+                                  __shfl_down(m.w, off));
+    const float4 s2 = make_float4(__shfl_down(sm.x, off), __shfl_down(sm.y, off), __shfl_down(sm.z, off),
+                                  __shfl_down(sm.w, off));
+    merge_state4(m, sm, m2, s2);
+  }
+  if (lane < kMergeCols) {
+    wm[w][lane] = m;
+    wsum[w][lane] = sm;
+  }
+  __syncthreads();
+  if (threadIdx.x < kMergeCols && col4 < inner4) {
+    m = wm[0][c];
+    sm = wsum[0][c];
+#pragma unroll
+    for (int i = 1; i < 4; ++i) merge_state4(m, sm, wm[i][c], wsum[i][c]);
+    const long long q = o * inner4 + col4;
+    fin[q] = m;
+    fin[nq + q] = make_float4(1.0f / sm.x, 1.0f / sm.y, 1.0f / sm.z, 1.0f / sm.w);
+  }
+}
+
+__global__ __launch_bounds__(256) void softmax_cols_wide_write(const float4* __restrict__ in, float4* __restrict__ out,
+                                                               long long axis, long long inner4, long long ncb,
+                                                               long long nchunks, const float4* __restrict__ fin,
+                                                               long long nq) {
+  const long long b = blockIdx.x;
+  const long long cb = b % ncb, t = b / ncb, chunk = t % nchunks, o = t / nchunks;
+  const long long col4 = cb * kWideCols + threadIdx.x;
+  if (col4 >= inner4) return;
+  const long long q = o * inner4 + col4;
+  const float4 m = fin[q], inv = fin[nq + q];
+  const float4* x = in + o * axis * inner4 + col4;
+  float4* y = out + o * axis * inner4 + col4;
+#pragma unroll 8
+  for (long long r = chunk; r < axis; r += nchunks) {
+    const float4 v = bch::load_nt(x + r * inner4);
+    bch::store_nt(make_float4(exp_f32(v.x - m.x) * inv.x, exp_f32(v.y - m.y) * inv.y,
+                              exp_f32(v.z - m.z) * inv.z, exp_f32(v.w - m.w) * inv.w),
+                  y + r * inner4);
+  }
+}
+
+hipError_t launch_cols_wide(hipStream_t s, const WidePlan& p, long long outer, long long axis, long long inner,
+                            const float* in, float* out, void* ws) {
+  const long long inner4 = inner / 4, nq = outer * inner4;
+  float4* part = static_cast<float4*>(ws);
+  const long long plane = outer * p.nchunks * inner4;
+  float4* fin = part + 2 * plane;
+  const long long blocks = outer * p.nchunks * p.ncb;
+  const float4* x = reinterpret_cast<const float4*>(in);
+  hipLaunchKernelGGL(softmax_cols_wide_stats, dim3((unsigned)blocks), dim3(256), 0, s, x, axis, inner4, p.ncb,
+                     p.nchunks, p.ch, part, plane);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const long long mblocks = outer * ((inner4 + kMergeCols - 1) / kMergeCols);
+  hipLaunchKernelGGL(softmax_cols_wide_merge, dim3((unsigned)mblocks), dim3(256), 0, s, part, plane,
+                     p.nchunks, inner4, nq, fin);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(softmax_cols_wide_write, dim3((unsigned)blocks), dim3(256), 0, s, x,
+                     reinterpret_cast<float4*>(out), axis, inner4, p.ncb, p.nchunks, fin, nq);
+  return hipGetLastError();
+}
+
 // Chunking of the middle-axis softmax: enough workgroups for ~4 per CU, at least 256 rows a chunk.
 struct ColPlan {
   int cw = 1, strips = 1, nchunks = 1;
@@ -755,11 +946,14 @@ size_t softmax_workspace_bytes(long long rows, long long cols) {
 
 size_t softmax_axis_workspace_bytes(long long outer, long long axis, long long inner) {
   if (inner == 1) return softmax_workspace_bytes(outer, axis);
-  // the float4 plan's chunks, or the scalar plan's when the pointers turn out unaligned
+  // the wide-row plan's, the float4 plan's chunks, or the scalar plan's when the pointers turn
+  // out unaligned: the most any of them can take
+  const WidePlan wp = wide_plan(outer, axis, inner);
   const ColPlan p = col_plan(outer, axis, inner);
   const VecPlan vp = vec_plan(outer, axis, inner);
   const long long nc = vp.w && vp.nchunks > p.nchunks ? vp.nchunks : p.nchunks;
-  return nc > 1 ? sizeof(float) * 2 * (size_t)outer * nc * (size_t)inner : 0;
+  const size_t b = nc > 1 ? sizeof(float) * 2 * (size_t)outer * nc * (size_t)inner : 0;
+  return wp.on && wide_bytes(outer, inner, wp) > b ? wide_bytes(outer, inner, wp) : b;
 }
 
 }  // namespace bch
@@ -900,6 +1094,11 @@ hipError_t launch_softmax_axis(hipStream_t s, long long outer, long long axis,
                                void* ws, size_t ws_bytes) {
   if (outer <= 0 || axis <= 0 || inner <= 0) return hipSuccess;
   if (inner == 1) return launch_softmax_rows(s, outer, axis, in, out, ws, ws_bytes);
+  const WidePlan wp = wide_plan(outer, axis, inner);
+  if (wp.on && vec_aligned(in, out)) {
+    if (ws == nullptr || ws_bytes < wide_bytes(outer, inner, wp)) return hipErrorInvalidValue;
+    return launch_cols_wide(s, wp, outer, axis, inner, in, out, ws);
+  }
   const VecPlan vp = vec_plan(outer, axis, inner);
   if (vp.w && vec_aligned(in, out)) {
     float4* part = nullptr;

@@ -115,6 +115,10 @@ def test_axis_and_inplace(dev):
     (400, 1500, 8),    # 2 lanes a row
     (512, 700, 4),     # 1 lane a row
     (256, 37, 40),     # most register rows past the axis
+    # inner >= 1024 with a long axis: whole-row passes (stats, merge, write)
+    (1, 16384, 1024),
+    (2, 5000, 1028),   # a second column block of one float4, a ragged last chunk
+    (1, 3000, 4096),
 ])
 def test_softmax_middle_axis(dev, outer, axis, inner):
     """softmax_dim over a non-last axis: the column softmax of each [axis][inner] slice, against
