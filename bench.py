@@ -229,7 +229,8 @@ def _bench_norm(dev, T, reps):
     """The steps either side of the path (TensorSession::layer_norm and
     ::gelu, session/mod.rs:349-398) at the softmax config's size: layer norm
     of [65536 x 2048] (one read + one write, 8 B per element) and GELU over
-    the same 2^27 elements, both HBM-bound."""
+    the same 2^27 elements; the session's head_split / head_concat at the
+    attention config's shape.  All HBM-bound."""
     from barracuda_amd import LcgStream, Tensor
     from barracuda_amd import _native as N
     lib, ctx = dev._lib, dev.ctx
@@ -247,6 +248,20 @@ def _bench_norm(dev, T, reps):
     wall, ev = T.run(lambda i: lib.bch_elementwise(ctx, N.BCH_EW_GELU, n, px, None, None, 0.0, py), reps, 3)
     out["gelu_2^27"] = {"GB/s": nbytes / (ev * 1e-3) / 1e9, "us": ev * 1e3, "bytes_per_launch": nbytes,
                         "hbm_frac": nbytes / (ev * 1e-3) / 1e9 / HBM_PEAK_GBS}
+    del x, y
+    # TensorSession::head_split / head_concat (session/mod.rs:423-480) at the attention
+    # config's shape: [4, 2048, 32*128] <-> [4, 32, 2048, 128], a copy (8 B per element)
+    B, S, H, D = 4, 2048, 32, 128
+    n = B * S * H * D
+    x = LcgStream(3, dev).normal([n], 0.0, 1.0)
+    y = Tensor.empty([n], dev)
+    px, py = C.c_void_p(x.ptr), C.c_void_p(y.ptr)
+    nbytes = 2 * 4 * n
+    for name, fn in (("head_split", lib.bch_head_split), ("head_concat", lib.bch_head_concat)):
+        wall, ev = T.run(lambda i: fn(ctx, B, S, H, D, px, py), reps, 3)
+        out[f"{name}_4x2048x32x128"] = {"GB/s": nbytes / (ev * 1e-3) / 1e9, "us": ev * 1e3,
+                                        "bytes_per_launch": nbytes,
+                                        "hbm_frac": nbytes / (ev * 1e-3) / 1e9 / HBM_PEAK_GBS}
     return out
 
 
@@ -329,7 +344,7 @@ def _bench_softmax(dev, T, reps):
     # softmax_dim over a middle axis of the same 2^27 elements: [64, 2048, 1024] (whole column
     # strips in registers, one read) and [1, 65536, 2048] (a chunked axis, read twice)
     for (o, a, inn), path in (((64, 2048, 1024), "column strips in registers"),
-                              ((1, 65536, 2048), "chunked axis: stats + streaming write")):
+                              ((1, 65536, 2048), "chunked axis, whole-row passes: stats + merge + write")):
         wall, ev = T.run(lambda i: lib.bch_softmax_axis(ctx, o, a, inn, px, py), reps, 3)
         out[f"softmax_axis_{o}x{a}x{inn}"] = {"GB/s": nbytes / (ev * 1e-3) / 1e9, "us": ev * 1e3,
                                               "bytes_per_call": nbytes, "path": path,
