@@ -85,6 +85,95 @@ def test_edge_values(dev):
     assert np.all(got2[:, :3] == 0.0)
 
 
+def _rows_gpu(dev, x2d: np.ndarray) -> np.ndarray:
+    rows, cols = x2d.shape
+    tx, ty = Tensor.from_data(x2d, [rows, cols], dev), Tensor.empty([rows, cols], dev)
+    dev.check(dev._lib.bch_softmax_rows(dev.ctx, rows, cols, C.c_void_p(tx.ptr), C.c_void_p(ty.ptr)), "rows")
+    return ty.to_numpy().reshape(rows, cols)
+
+
+def _axis_gpu(dev, x: np.ndarray) -> np.ndarray:
+    outer, axis, inner = x.shape
+    tx, ty = Tensor.from_data(x, [outer, axis, inner], dev), Tensor.empty([outer, axis, inner], dev)
+    dev.check(dev._lib.bch_softmax_axis(dev.ctx, outer, axis, inner, C.c_void_p(tx.ptr), C.c_void_p(ty.ptr)),
+              "axis")
+    return ty.to_numpy().reshape(outer, axis, inner)
+
+
+# one shape per kernel path (few rows of a wide row are split, so the row-per-workgroup kernels
+# above 16384 columns need >= 1024 rows): wavefront per row, workgroup per row (256 / 1024
+# threads), scalar rows in registers, the block kernel, split rows (float4, scalar, several
+# rows); column strips in registers (4 and 1 float4 lanes a row), chunked strips, whole-row
+# passes, 64-column strips, whole rows per wavefront, scalar chunks
+NONFINITE_ROWS = [(4, 2048), (4, 8192), (1024, 40000), (4, 2047), (1100, 30001), (1030, 50257), (1, 100000),
+                  (1, 100003), (3, 50257)]
+NONFINITE_AXES = [(16, 2048, 1024), (300, 1000, 12), (1, 65536, 96), (1, 3000, 1028), (8, 2048, 320),
+                  (3000, 512, 5), (2, 70000, 2)]
+
+
+@pytest.mark.parametrize("rows,cols", NONFINITE_ROWS)
+def test_nonfinite_rows_every_path(dev, rows, cols):
+    """A row holding +inf, one holding NaN and one of nothing but -inf come out all NaN on every
+    kernel path (the max taken first, or online states whose merge rescales a +inf state by
+    exp(inf - inf)), while the other rows match the f64 oracle.  The reference's host softmax_dim leaves such rows un-normalised
+    (its `if sum > 0.0`, ops/tensor_axis_ops.rs:108-114) and its global softmax shader divides
+    by the NaN sum (all NaN, softmax_simple_f64.wgsl:45-50); one kernel serves both here."""
+    _say(f"softmax non-finite rows={rows} cols={cols}")
+    base = O.Lcg(rows * 7 + cols).normal((rows, cols), 0.0, 3.0)
+
+    def spoil(x, kind, r):
+        if kind == "+inf":
+            x[r, cols // 3] = np.inf
+        elif kind == "nan":
+            x[r, cols // 2 + 1] = np.nan
+        else:
+            x[r, :] = -np.inf
+
+    kinds = ("+inf", "nan", "-inf row")
+    # three rows or more: one input with rows 0, 1, 2 spoiled; a single row: one input per kind
+    inputs = []
+    if rows >= 3:
+        x = base.copy()
+        for r, kind in enumerate(kinds):
+            spoil(x, kind, r)
+        inputs.append((x, [0, 1, 2]))
+    else:
+        for kind in kinds:
+            x = base.copy()
+            spoil(x, kind, 0)
+            inputs.append((x, [0]))
+    for x, bad in inputs:
+        got = _rows_gpu(dev, x)
+        for b in bad:
+            assert np.all(np.isnan(got[b])), b
+        good = [i for i in range(rows) if i not in bad]
+        if good:
+            assert O.max_rel_err(got[good], O.softmax_rows_f64(x[good])) <= TOL
+
+
+@pytest.mark.parametrize("outer,axis,inner", NONFINITE_AXES)
+def test_nonfinite_columns_every_path(dev, outer, axis, inner):
+    """The same for softmax over a middle axis: the column holding +inf, the one holding NaN
+    and the all -inf one come out all NaN; every other column matches the f64 oracle."""
+    _say(f"softmax non-finite columns outer={outer} axis={axis} inner={inner}")
+    x = O.Lcg(outer + axis * 3 + inner).normal((outer, axis, inner), 0.0, 3.0)
+    x[0, axis // 3, 0] = np.inf
+    x[0, axis // 2 + 1, 1] = np.nan
+    bad = [0, 1]
+    if inner >= 3:
+        x[0, :, 2] = -np.inf
+        bad.append(2)
+    got = _axis_gpu(dev, x)
+    for c in bad:
+        assert np.all(np.isnan(got[0, :, c])), c
+    want = np.moveaxis(O.softmax_rows_f64(np.ascontiguousarray(np.moveaxis(x, 1, -1))), -1, 1)
+    keep = np.ones((outer, inner), bool)
+    keep[0, bad] = False
+    g = np.moveaxis(got, 1, -1)[keep]
+    w = np.moveaxis(want, 1, -1)[keep]
+    assert O.max_rel_err(np.ascontiguousarray(g), np.ascontiguousarray(w)) <= TOL
+
+
 def test_axis_and_inplace(dev):
     _say("softmax axis / in-place")
     x = O.Lcg(9).normal((4, 37, 12), 0.0, 2.0)
