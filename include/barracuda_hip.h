@@ -45,7 +45,10 @@ typedef int bch_status;
                              * faulted (memory fault, trap, assert, watchdog),
                              * an uncorrectable ECC error, or the context is
                              * gone.  Sticky: every later call on the context
-                             * that touches the device returns it too.
+                             * that touches the device returns it too.  HIP
+                             * graphs captured on the context's stream are
+                             * to be discarded with it (a replay would not
+                             * go through the library's checks).
                              *                             -> DeviceLost(String) (error.rs:59) */
 
 typedef struct bch_ctx bch_ctx;
