@@ -69,6 +69,7 @@
 #include <stdint.h>
 
 #include <algorithm>
+#include <string>
 
 namespace {
 
@@ -697,7 +698,7 @@ constexpr size_t kSplitWsMax = (size_t)256 << 20;
 constexpr size_t kSplitWsSmall = (size_t)16 << 20;  // bch_sgemm_noalloc's fixed scratch
 constexpr int kSplitMinKt = 8;  // k-tiles per slice at least
 
-int split_slices(int batch, int m, int n, int k, size_t cap = kSplitWsMax) {
+int split_slices(int batch, int m, int n, int k, size_t cap = kSplitWsMax, double* cost_us = nullptr) {
   if (batch < 1 || k <= 0 || k % kBK != 0) return 1;
   const long long cu = bch::device_cu_count();
   const Tile t = pick_tile(batch, m, n);
@@ -721,6 +722,7 @@ int split_slices(int batch, int m, int n, int k, size_t cap = kSplitWsMax) {
       bs = sl;
     }
   }
+  if (cost_us) *cost_us = best;
   return bs;
 }
 
@@ -790,7 +792,9 @@ struct HybPlan {
 
 size_t hyb_bytes(const HybPlan& h) { return (size_t)h.S * h.r * tile_m(h.t) * tile_n(h.t) * sizeof(float); }
 
-bool hyb_plan(int batch, int m, int n, int k, HybPlan& out) {
+// cost_us (nullable): the modelled time of what the tile path then runs, the hybrid plan or the
+// best data-parallel tiling (7.4 us per 256 x 256 k-tile)
+bool hyb_plan(int batch, int m, int n, int k, HybPlan& out, double* cost_us = nullptr) {
   if (batch != 1 || k <= 0 || k % kBK != 0 || split_slices(batch, m, n, k) > 1) return false;
   const long long cu = bch::device_cu_count();
   const int nk = k / kBK;
@@ -822,7 +826,83 @@ bool hyb_plan(int batch, int m, int n, int k, HybPlan& out) {
       out.kt = nk / S;
     }
   }
-  return found && best < 0.97 * best_dp;
+  const bool use = found && best < 0.97 * best_dp;
+  if (cost_us) *cost_us = 7.4 * (use ? best : best_dp);
+  return use;
+}
+
+// Modelled time (us) of a batch-1 call on the tile path: split-K, the hybrid plan or the best
+// data-parallel tiling, whichever the tile path takes (given its workspace).
+double tile_path_cost_us(int m, int n, int k) {
+  double c = 0.0;
+  if (split_slices(1, m, n, k, kSplitWsMax, &c) > 1) return c;
+  HybPlan h;
+  if (k > 0 && k % kBK == 0) {
+    hyb_plan(1, m, n, k, h, &c);
+    return c;
+  }
+  // K not a multiple of the k-tile: data-parallel only
+  const long long cu = bch::device_cu_count();
+  double best = 0.0;
+  for (const TileOpt& o : kTileOpts) {
+    const long long T = (long long)((m + o.bm - 1) / o.bm) * ((n + o.bn - 1) / o.bn);
+    const double t = (double)((T + cu - 1) / cu) * ((k + kBK - 1) / kBK) * 7.4 * o.bm * o.bn / 65536.0 / o.eff;
+    if (best == 0.0 || t < best) best = t;
+  }
+  return best;
+}
+
+// ---- whole rounds of 256 x 256 tiles on part of C, the rest planned on its own (the mixed plan) ----
+// The hybrid plan's split tiles and the smaller tiles it picks to fill the last round cost
+// efficiency over the whole matrix.  Where the 256 x 256 tiles make at least one whole round,
+// the mixed plan runs j whole rounds of them on the first rows (or columns) of C, data-parallel,
+// then the remaining rows (or columns) as a call of their own (split-K, hybrid or
+// data-parallel, as planned for that shape).  Same box, two runs each, TFLOP/s, against the
+// plan for the whole matrix: 4096 x 11008 x 4096 138.9 -> 141.5 (columns 0..8191 first),
+// 11008 x 4096 x 4096 139.2 -> 141.5 (rows 0..8191), 8192 x 11008 x 4096 140.2 -> 144.6,
+// 3072 x 11008 x 4096 138.4 -> 140.0, 4096 x 14336 x 4096 143.3 -> 145.0; 5120^3 142.1 ->
+// 138.7, which the model rejects.  Chosen when the model puts it 1% ahead of the whole-matrix
+// plan; the split runs along rows or columns, with j from 1 to the whole rounds available.
+// Only the first level splits: the rest is planned without the mixed plan.
+// The second launch's fixed cost in the model: its prologue, the first launch's last C stores
+// that nothing overlaps, and the gap between the launches.  At 16 us the model picks, among
+// 26 shapes measured both ways (K 1024 and 4096), every one that gained (1.1-6.0%) at K 4096
+// and leaves out the two that lost (6144 x 6144 x 1024 -2.9%, 4100 x 4100 x 1024 -1.2%); two
+// it still takes at K 1024 measured within 0.4% either way.
+constexpr double kMixFixedUs = 16.0;
+
+struct MixPlan {
+  int axis = -1;  // 0: rows [0, split) first; 1: columns [0, split) first
+  int split = 0;
+};
+
+bool mix_plan(int batch, int m, int n, int k, MixPlan& out) {
+  if (batch != 1 || k <= 0 || k % kBK != 0) return false;
+  const long long cu = bch::device_cu_count();
+  const int mt = (m + 255) / 256, nt = (n + 255) / 256;
+  const long long rounds = (long long)mt * nt / cu;
+  if (rounds < 1) return false;
+  const double nk = k / kBK;
+  double best = 0.99 * tile_path_cost_us(m, n, k);
+  bool found = false;
+  for (int axis = 0; axis < 2; ++axis) {
+    const int along = axis == 0 ? mt : nt, across = axis == 0 ? nt : mt;
+    for (long long j = rounds; j >= 1; --j) {
+      const long long c = j * cu / across;  // whole tile rows (columns) that fit j rounds
+      if (c < 1 || c >= along) continue;
+      const int split = (int)(256 * c);
+      const double first = (double)((c * across + cu - 1) / cu) * nk * 7.4;
+      const double rest = axis == 0 ? tile_path_cost_us(m - split, n, k) : tile_path_cost_us(m, n - split, k);
+      const double cost = first + rest + kMixFixedUs;
+      if (cost < best) {
+        best = cost;
+        found = true;
+        out.axis = axis;
+        out.split = split;
+      }
+    }
+  }
+  return found;
 }
 
 // C[tile j's rows and columns] = act(sum over s < S of P[s][j] (+ bias)) for the r split
@@ -919,8 +999,25 @@ bool nt_two_pass(int m, int n, int k, const float* A, int lda, const float* B, i
 
 namespace bch {
 
+static const char* tile_path_name(int m, int n, int k, bool allow_mix);
+
 const char* sgemm_kernel_name(int m, int n, int k) {
   if (sgemm_skinny_applies(m, n, k, nullptr, k, nullptr, n)) return sgemm_skinny_kernel_name(m);
+  return tile_path_name(m, n, k, true);
+}
+
+// The tile path's kernels for lda = k, ldb = n and 16-byte aligned operands.
+static const char* tile_path_name(int m, int n, int k, bool allow_mix) {
+  MixPlan mp;
+  if (allow_mix && mix_plan(1, m, n, k, mp)) {
+    const int m1 = mp.axis == 0 ? mp.split : m, n1 = mp.axis == 1 ? mp.split : n;
+    const bool fast = m1 % 256 == 0 && n1 % 256 == 0 && n % 4 == 0;
+    thread_local std::string name;
+    name = std::string(fast ? "sgemm_mfma_kernel<256,256,32,false>" : "sgemm_mfma_kernel<256,256,32,true,v4>") +
+           (mp.axis == 0 ? " rows then " : " columns then ") +
+           (mp.axis == 0 ? tile_path_name(m - m1, n, k, false) : tile_path_name(m, n - n1, k, false));
+    return name.c_str();
+  }
   const Tile t = pick_tile(1, m, n);
   // with lda = k and ldb = n, and 16-byte aligned operands
   const bool check = !(m % tile_m(t) == 0 && n % tile_n(t) == 0 && k % kBK == 0 && k % 4 == 0 && n % 4 == 0);
@@ -950,7 +1047,11 @@ const char* sgemm_kernel_name(int m, int n, int k) {
 
 // The tile path's scratch: split-K partials, or the hybrid plan's.  `optional` false: the
 // plan within bch_sgemm_noalloc's 16 MiB (fewer split slices, no hybrid plan).
-static size_t tile_workspace_bytes(int batch, int m, int n, int k, bool optional) {
+static size_t tile_workspace_bytes(int batch, int m, int n, int k, bool optional, bool allow_mix = true) {
+  MixPlan mp;
+  if (allow_mix && mix_plan(batch, m, n, k, mp))  // the whole tiles need none; the rest is a call of its own
+    return mp.axis == 0 ? tile_workspace_bytes(1, m - mp.split, n, k, optional, false)
+                        : tile_workspace_bytes(1, m, n - mp.split, k, optional, false);
   const int sl = split_slices(batch, m, n, k, optional ? kSplitWsMax : kSplitWsSmall);
   if (sl > 1) return (size_t)sl * batch * m * n * sizeof(float);
   HybPlan h;
@@ -986,6 +1087,20 @@ hipError_t launch_sgemm(hipStream_t s, int batch, int m, int n, int k, const flo
   return launch_sgemm_ex(s, false, batch, m, n, k, A, lda, sA, B, ldb, sB, nullptr, 0, C, ldc, sC, ws, ws_bytes);
 }
 
+}  // namespace bch
+
+namespace {
+
+// The tile path of launch_sgemm_ex: split-K, the mixed plan (allow_mix), the hybrid plan or the
+// data-parallel tiling.
+hipError_t launch_tile_path(hipStream_t s, bool transb, int batch, int m, int n, int k, const float* A, int lda,
+                            long long sA, const float* B, int ldb, long long sB, const float* bias, int act,
+                            float* C, int ldc, long long sC, void* ws, size_t ws_bytes, bool allow_mix);
+
+}  // namespace
+
+namespace bch {
+
 hipError_t launch_sgemm_ex(hipStream_t s, bool transb, int batch, int m, int n, int k, const float* A, int lda,
                            long long sA, const float* B, int ldb, long long sB, const float* bias, int act,
                            float* C, int ldc, long long sC, void* ws, size_t ws_bytes) {
@@ -1005,6 +1120,17 @@ hipError_t launch_sgemm_ex(hipStream_t s, bool transb, int batch, int m, int n, 
     return launch_sgemm_skinny_nt(s, m - 32, n, k, A + 32LL * lda, lda, B, ldb, C + 32LL * ldc, ldc, ws, ws_bytes,
                                   bias, act);
   }
+  return launch_tile_path(s, transb, batch, m, n, k, A, lda, sA, B, ldb, sB, bias, act, C, ldc, sC, ws, ws_bytes,
+                          true);
+}
+
+}  // namespace bch
+
+namespace {
+
+hipError_t launch_tile_path(hipStream_t s, bool transb, int batch, int m, int n, int k, const float* A, int lda,
+                            long long sA, const float* B, int ldb, long long sB, const float* bias, int act,
+                            float* C, int ldc, long long sC, void* ws, size_t ws_bytes, bool allow_mix) {
   const Tile t = pick_tile(batch, m, n);
   int sl = split_slices(batch, m, n, k);
   const size_t pbytes = (size_t)batch * m * n * sizeof(float);  // one slice's partials, every batch
@@ -1043,6 +1169,31 @@ hipError_t launch_sgemm_ex(hipStream_t s, bool transb, int batch, int m, int n, 
     return hipGetLastError();
   }
   const bool epi = bias != nullptr || act != 0;
+  MixPlan mp;
+  if (allow_mix && mix_plan(batch, m, n, k, mp)) {
+    // whole rounds of 256 x 256 tiles on the first rows (columns) of C, then the rest as a call
+    // of its own; the offsets are multiples of 256 rows (columns), which keeps the alignment
+    const int m1 = mp.axis == 0 ? mp.split : m, n1 = mp.axis == 1 ? mp.split : n;
+    const int mode1 = fast_ok(Tile::k256x256, m1, n1, k, A, lda, sA, B, ldb, sB)      ? 0
+                      : vec4_ok(transb, m1, n1, k, A, lda, sA, B, ldb, sB) ? 1
+                                                                             : 2;
+    hipError_t e =
+        transb ? (epi ? launch_tile_any<true, true>(mode1, Tile::k256x256, s, 1, m1, n1, k, A, lda, sA, B, ldb, sB, C,
+                                                    ldc, sC, bias, act)
+                      : launch_tile_any<true, false>(mode1, Tile::k256x256, s, 1, m1, n1, k, A, lda, sA, B, ldb, sB,
+                                                     C, ldc, sC, bias, act))
+               : (epi ? launch_tile_any<false, true>(mode1, Tile::k256x256, s, 1, m1, n1, k, A, lda, sA, B, ldb, sB,
+                                                     C, ldc, sC, bias, act)
+                      : launch_tile_any<false, false>(mode1, Tile::k256x256, s, 1, m1, n1, k, A, lda, sA, B, ldb, sB,
+                                                      C, ldc, sC, bias, act));
+    if (e != hipSuccess) return e;
+    if (mp.axis == 0)
+      return launch_tile_path(s, transb, 1, m - m1, n, k, A + (long long)m1 * lda, lda, sA, B, ldb, sB, bias, act,
+                              C + (long long)m1 * ldc, ldc, sC, ws, ws_bytes, false);
+    const float* B2 = transb ? B + (long long)n1 * ldb : B + n1;
+    return launch_tile_path(s, transb, 1, m, n - n1, k, A, lda, sA, B2, ldb, sB, bias ? bias + n1 : nullptr, act,
+                            C + n1, ldc, sC, ws, ws_bytes, false);
+  }
   HybPlan h;
   if (hyb_plan(batch, m, n, k, h) && ws != nullptr && ws_bytes >= hyb_bytes(h)) {
     const int hmode = fast_ok(h.t, m, n, k, A, lda, sA, B, ldb, sB)                ? 0
@@ -1071,4 +1222,4 @@ hipError_t launch_sgemm_ex(hipStream_t s, bool transb, int batch, int m, int n, 
                                              act);
 }
 
-}  // namespace bch
+}  // namespace

@@ -406,11 +406,12 @@ def _bench_batched(dev, T, reps):
                          "kernel": lib.bch_sgemm_kernel_name(256, 256, 256).decode()}
     del a, b, c
     # MatMul at shapes whose tiles do not come out in whole rounds of the CUs: the tile
-    # choice, the hybrid plan (whole tiles + k-sliced leftover tiles), split-K and the
+    # choice, the hybrid plan (whole tiles + k-sliced leftover tiles), the mixed plan (whole
+    # rounds of 256x256 tiles on the first columns / rows, then the rest), split-K and the
     # float4-guarded ragged loads, beside the headline's whole-round 4096^3
     shapes = {}
     for m, n, k in ((3072, 3072, 3072), (5120, 5120, 5120), (6144, 6144, 6144), (4096, 11008, 4096),
-                    (4000, 4000, 4000), (1024, 1024, 1024)):
+                    (11008, 4096, 4096), (4000, 4000, 4000), (1024, 1024, 1024)):
         s1 = LcgStream(m + n + k, dev)
         a, b = s1.uniform([m, k]), s1.uniform([k, n])
         c = Tensor.empty([m, n], dev)

@@ -111,7 +111,10 @@ def test_kernel_routing_names():
     assert lib.bch_sgemm_kernel_name(2048, 2048, 512) == b"sgemm_mfma_kernel<128,128,32,false>"
     assert lib.bch_sgemm_kernel_name(3000, 3000, 1000) == b"sgemm_mfma_kernel<128,128,32,true,v4>"
     assert lib.bch_sgemm_kernel_name(8192, 1024, 512) == b"sgemm_mfma_kernel<256,128,32,false>"
-    assert lib.bch_sgemm_kernel_name(4096, 11008, 4096) == b"sgemm_mfma_kernel<256,128,32,false,hyb>+sgemm_tail_reduce"
+    assert lib.bch_sgemm_kernel_name(4096, 11008, 4096) == (b"sgemm_mfma_kernel<256,256,32,false> columns then "
+                                                            b"sgemm_mfma_kernel<128,128,32,false>")
+    assert lib.bch_sgemm_kernel_name(11008, 4096, 4096) == (b"sgemm_mfma_kernel<256,256,32,false> rows then "
+                                                            b"sgemm_mfma_kernel<128,128,32,false>")
     assert lib.bch_sgemm_kernel_name(3072, 3072, 3072) == b"sgemm_mfma_kernel<256,128,32,false,hyb>+sgemm_tail_reduce"
     assert lib.bch_sgemm_kernel_name(1024, 1024, 1024) == b"sgemm_mfma_kernel<128,128,32,false>+sgemm_splitk_reduce"
     assert lib.bch_sgemm_kernel_name(2048, 2048, 2048) == b"sgemm_mfma_kernel<128,128,32,false>"

@@ -328,6 +328,75 @@ def test_hybrid_exact_on_integers(dev):
         assert np.array_equal(_mm(dev, a, b), want), (m, n, k)
 
 
+MIXED_CASES = [(4096, 11008, 4096, "columns"), (11008, 4096, 4096, "rows"), (4096, 11000, 4096, "columns"),
+               (11000, 4096, 4096, "rows"), (4100, 4096, 4096, "rows"), (2048, 11008, 4096, "columns")]
+
+
+def _seam_sample(size: int):
+    """One index in every 128 block, both ends, and both sides of the splits the mixed plan
+    takes at these sizes (4096, 8192)."""
+    idx = {0, size - 1, 4095, 4096, 8191, 8192} | {t * 128 + (t * 37) % 128 for t in range((size + 127) // 128)}
+    return sorted(i for i in idx if i < size)
+
+
+@pytest.mark.parametrize("m,n,k,axis", MIXED_CASES)
+def test_mixed_vs_f64(dev, m, n, k, axis):
+    """The mixed plan: whole rounds of 256x256 tiles on the first rows (columns) of C, then the
+    rest planned on its own (data-parallel, split-K or hybrid; aligned and float4-guarded).
+    Rows across every 128-row block and columns across every 128-column block, the seam
+    between the two launches included, against f64 (B scaled by 1/sqrt(k)); repeated calls are
+    bit-identical."""
+    name = dev._lib.bch_sgemm_kernel_name(m, n, k).decode()
+    assert f" {axis} then " in name, name
+    _say(f"sgemm mixed m={m} n={n} k={k} ({name})")
+    rng = O.Lcg(m + 7 * n + k)
+    a = rng.uniform((m, k))
+    # B scaled by 1/sqrt(k): outputs of order 1, so the bar measures the plan, not f32 rounding
+    # of sums of order sqrt(k) (the exact-integer test below pins every element bit for bit)
+    b = (rng.uniform((k, n)) / np.float32(np.sqrt(k))).astype(np.float32)
+    got = _mm(dev, a, b)
+    rows = _seam_sample(m)
+    assert O.max_rel_err(got[rows], O.matmul_f64(a, b, rows=rows)) <= TOL
+    cols = _seam_sample(n)
+    assert O.max_rel_err(got[:, cols], a.astype(np.float64) @ b[:, cols].astype(np.float64)) <= TOL
+    assert np.array_equal(got, _mm(dev, a, b)), "not deterministic"
+
+
+def test_mixed_exact_on_integers(dev):
+    """Small integers: every product is exact in f32 whatever the plan, so both launches of the
+    mixed plan (and the split-K rest) match the integer product bit for bit."""
+    rng = np.random.default_rng(41)
+    for m, n, k in ((4096, 4100, 4096), (4100, 4096, 4096)):
+        _say(f"sgemm mixed integers m={m} n={n} k={k}")
+        a = rng.integers(-8, 9, (m, k)).astype(np.float32)
+        b = rng.integers(-8, 9, (k, n)).astype(np.float32)
+        # every partial sum is an integer below 2^18: the float64 product is exact
+        want = (a.astype(np.float64) @ b.astype(np.float64)).astype(np.float32)
+        assert np.array_equal(_mm(dev, a, b), want), (m, n, k)
+
+
+def test_mixed_linear_bias_gelu(dev):
+    """The linear layer (bch_sgemm_ex, [out, in] weights, bias, GELU) on the mixed plan: the
+    rest's weights, bias and output start at column 8192 (weight row 8192)."""
+    m, n, k = 4096, 11008, 4096
+    _say(f"linear mixed m={m} n={n} k={k} bias + GELU")
+    rng = O.Lcg(4242)
+    x = rng.uniform((m, k))
+    w = (rng.uniform((n, k)) / np.float32(np.sqrt(k))).astype(np.float32)
+    bias = rng.uniform((n,))
+    tx, tw, tb = (Tensor.from_data(t, list(t.shape), dev) for t in (x, w, bias))
+    ty = Tensor.empty([m, n], dev)
+    dev.check(dev._lib.bch_sgemm_ex(dev.ctx, 1, m, n, k, C.c_void_p(tx.ptr), k, C.c_void_p(tw.ptr), k,
+                                    C.c_void_p(tb.ptr), 2, C.c_void_p(ty.ptr), n), "sgemm_ex")
+    got = ty.to_numpy().reshape(m, n)
+    rows = _seam_sample(m)[::3]
+    pre = x[rows].astype(np.float64) @ w.T.astype(np.float64) + bias.astype(np.float64)
+    assert O.max_rel_err(got[rows], O.gelu_f64(pre.astype(np.float32))) <= TOL
+    cols = _seam_sample(n)
+    pre = x.astype(np.float64) @ w[cols].T.astype(np.float64) + bias[cols].astype(np.float64)
+    assert O.max_rel_err(np.ascontiguousarray(got[:, cols]), O.gelu_f64(pre.astype(np.float32))) <= TOL
+
+
 def test_config_4096_cubed(dev):
     """BASELINE config 3a: 4096^3, U[-1,1), seed 2; f64 oracle on sampled rows."""
     _say("sgemm 4096^3 seed 2")
