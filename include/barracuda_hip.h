@@ -131,7 +131,9 @@ bch_status bch_sync(bch_ctx *ctx);
  * kernels, 32 < m <= 64 with K % 4 == 0 and 16-byte aligned A to their
  * two-block form, and everything else to the FP32-MFMA tiled kernel (split
  * over k when the tiles fill less than one round of the CUs; whole rounds
- * plus k-sliced leftover tiles when the last round would be part-filled). */
+ * plus k-sliced leftover tiles when the last round would be part-filled; or
+ * whole rounds of 256x256 tiles on the first rows or columns of C and the
+ * rest planned on its own, where that is modelled faster). */
 bch_status bch_sgemm(bch_ctx *ctx, int m, int n, int k,
                      const float *A, int lda, const float *B, int ldb,
                      float *C, int ldc);
