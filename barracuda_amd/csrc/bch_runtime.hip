@@ -21,6 +21,7 @@
 #include <set>
 #include <tuple>
 #include <string>
+#include <unordered_map>
 #include <vector>
 
 #include "../../include/barracuda_hip.h"
@@ -72,6 +73,14 @@ struct bch_ctx {
   unsigned* fault_host = nullptr;
   unsigned* fault_dev = nullptr;
   unsigned ring_spin = 1u << 22;
+  // Device memory handed out by bch_alloc: `live` maps each block to its
+  // bucket size; bch_free parks the block in `cached` for the next bch_alloc
+  // of that bucket instead of freeing it (see pool_bucket).  pool_max caps
+  // the parked bytes (BARRACUDA_HIP_POOL_MAX_MB, read at bch_ctx_create).
+  std::unordered_map<void*, size_t> live;
+  std::map<size_t, std::vector<void*>> cached;
+  size_t cached_bytes = 0;
+  size_t pool_max = (size_t)8 << 30;
 };
 
 struct bch_event {
@@ -317,6 +326,7 @@ bch_status bch_ctx_create(int device, const char* code_object_dir, bch_ctx** out
   }
   resolve_scratch(ctx);
   if (const char* sp = getenv("BARRACUDA_HIP_RING_SPIN")) ctx->ring_spin = (unsigned)strtoul(sp, nullptr, 10);
+  if (const char* pm = getenv("BARRACUDA_HIP_POOL_MAX_MB")) ctx->pool_max = (size_t)strtoull(pm, nullptr, 10) << 20;
   void* fh = nullptr;
   void* fd = nullptr;
   if (hipHostMalloc(&fh, 64, hipHostMallocMapped) == hipSuccess && fh) {
@@ -363,12 +373,54 @@ void bch_ctx_destroy(bch_ctx* ctx) {
   if (!ctx) return;
   (void)hipSetDevice(ctx->device);
   if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+  for (auto& kv : ctx->cached)
+    for (void* p : kv.second) (void)hipFree(p);
   for (auto& kv : ctx->modules) (void)hipModuleUnload(kv.second);
   if (ctx->ws) (void)hipFree(ctx->ws);
   for (void* p : ctx->retired) (void)hipFree(p);
   if (ctx->fault_host) (void)hipHostFree(ctx->fault_host);
   if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
   delete ctx;
+}
+
+// ---- device memory: freed blocks are kept per context and handed out again ----
+// The reference hands each op's output from a pool of power-of-two buckets
+// (device/tensor_context/pool.rs:268-334, acquire_pooled; ops/matmul.rs:128
+// "zero allocation in steady state").  Here bch_free parks a block in its
+// bucket and the next bch_alloc of that bucket takes it back, so a loop of
+// ops on fresh outputs makes no hipMalloc and no hipFree (which waits for the
+// device) after its first pass.  Reuse needs no wait: every call of a context
+// runs in order on its one stream, so work queued after bch_alloc returns a
+// parked block runs after the work that still read it.  Buckets: powers of
+// two from 256 bytes to 64 MiB, then multiples of 2 MiB (a large block
+// wastes at most 2 MiB).  A failed hipMalloc releases the parked blocks and
+// tries once more; parked bytes beyond pool_max are freed at once.
+constexpr size_t kPoolMinBytes = 256;
+constexpr size_t kPoolPow2Max = (size_t)64 << 20;
+constexpr size_t kPoolLargeStep = (size_t)2 << 20;
+
+static size_t pool_bucket(size_t bytes) {
+  if (bytes <= kPoolMinBytes) return kPoolMinBytes;
+  if (bytes <= kPoolPow2Max) {
+    size_t b = kPoolMinBytes;
+    while (b < bytes) b <<= 1;
+    return b;
+  }
+  return (bytes + kPoolLargeStep - 1) / kPoolLargeStep * kPoolLargeStep;
+}
+
+// Frees every parked block (after the stream's queued work).
+static hipError_t pool_release(bch_ctx* ctx) {
+  if (ctx->cached_bytes == 0) return hipSuccess;
+  hipError_t e = hipStreamSynchronize(ctx->stream);
+  for (auto& kv : ctx->cached)
+    for (void* p : kv.second) {
+      const hipError_t f = hipFree(p);
+      if (e == hipSuccess) e = f;
+    }
+  ctx->cached.clear();
+  ctx->cached_bytes = 0;
+  return e;
 }
 
 bch_status bch_alloc(bch_ctx* ctx, size_t bytes, void** dptr) {
@@ -379,12 +431,27 @@ bch_status bch_alloc(bch_ctx* ctx, size_t bytes, void** dptr) {
     return fail(ctx, BCH_E_OOM, "bch_alloc: allocation of %zu bytes failed (injected by BARRACUDA_HIP_FAIL_ALLOC)", bytes);
   bch_status st = use(ctx);
   if (st != BCH_OK) return st;
-  hipError_t e = hipMalloc(dptr, bytes);
+  const size_t b = pool_bucket(bytes);
+  auto it = ctx->cached.find(b);
+  if (it != ctx->cached.end() && !it->second.empty()) {
+    *dptr = it->second.back();
+    it->second.pop_back();
+    ctx->cached_bytes -= b;
+    ctx->live[*dptr] = b;
+    return BCH_OK;
+  }
+  hipError_t e = hipMalloc(dptr, b);
+  if (e == hipErrorOutOfMemory && ctx->cached_bytes > 0) {
+    (void)hipGetLastError();
+    e = pool_release(ctx);
+    if (e == hipSuccess) e = hipMalloc(dptr, b);
+  }
   if (e != hipSuccess) {
     *dptr = nullptr;
     (void)hipGetLastError();
     return from_hip(ctx, e, "bch_alloc");
   }
+  ctx->live[*dptr] = b;
   return BCH_OK;
 }
 
@@ -393,7 +460,18 @@ bch_status bch_free(bch_ctx* ctx, void* dptr) {
   if (!dptr) return BCH_OK;
   bch_status st = use(ctx);
   if (st != BCH_OK) return st;
-  // Work queued on this context may still read the buffer.
+  auto it = ctx->live.find(dptr);
+  if (it != ctx->live.end()) {
+    const size_t b = it->second;
+    ctx->live.erase(it);
+    if (ctx->cached_bytes + b <= ctx->pool_max) {
+      ctx->cached[b].push_back(dptr);
+      ctx->cached_bytes += b;
+      return BCH_OK;
+    }
+  }
+  // Not parked (over the cap, or memory bch_alloc did not hand out): work queued
+  // on this context may still read it.
   hipError_t e = hipStreamSynchronize(ctx->stream);
   if (e == hipSuccess) e = hipFree(dptr);
   return from_hip(ctx, e, "bch_free");

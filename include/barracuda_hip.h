@@ -106,7 +106,17 @@ const char *bch_status_string(bch_status s);
 /* backend.rs alloc_buffer / alloc_buffer_init / upload / download.
  * bch_alloc of 0 bytes returns a NULL pointer and BCH_OK.  Env
  * BARRACUDA_HIP_FAIL_ALLOC=1 makes every bch_alloc fail with BCH_E_OOM
- * (fault injection for OutOfMemory handling). */
+ * (fault injection for OutOfMemory handling).
+ * Like the reference's buffer pool (device/tensor_context/pool.rs:268-334),
+ * bch_free keeps the block for the context's next bch_alloc of the same
+ * size class (powers of two from 256 bytes to 64 MiB, then multiples of
+ * 2 MiB) and returns without waiting: work queued on ctx that still reads
+ * it runs before anything queued after its reuse.  Work on other streams
+ * that reads a block must be complete before the block is freed.  Parked
+ * blocks are released when an allocation would otherwise fail, beyond
+ * BARRACUDA_HIP_POOL_MAX_MB (default 8192) of them, and by
+ * bch_ctx_destroy.  Memory that bch_alloc did not hand out is freed after
+ * ctx's queued work, as before. */
 bch_status bch_alloc(bch_ctx *ctx, size_t bytes, void **dptr);
 bch_status bch_free(bch_ctx *ctx, void *dptr);
 bch_status bch_upload(bch_ctx *ctx, void *dst, const void *src, size_t bytes);

@@ -112,6 +112,74 @@ def test_device_copy_runs_and_streaming_path(dev):
         assert np.array_equal(got[:n], x) and np.all(got[n:] == -7.0)
 
 
+def test_pool_hands_freed_blocks_back(dev):
+    """bch_free parks a block for the next bch_alloc of its size class (powers of two from
+    256 bytes to 64 MiB, then multiples of 2 MiB), as the reference's buffer pool does."""
+    import ctypes as C
+    _say("pool: freed blocks come back by size class")
+    lib, ctx = dev._lib, dev.ctx
+
+    def alloc(nbytes):
+        p = C.c_void_p()
+        dev.check(lib.bch_alloc(ctx, nbytes, C.byref(p)), "alloc")
+        return p.value
+
+    def free(p):
+        dev.check(lib.bch_free(ctx, C.c_void_p(p)), "free")
+
+    p1 = alloc(1000)
+    free(p1)
+    assert alloc(900) == p1            # the same 1 KiB class
+    p2 = alloc(3000)                   # a 4 KiB class: a new block
+    assert p2 != p1
+    free(p1)
+    free(p2)
+    big = alloc((100 << 20) + 5)       # above 64 MiB: multiples of 2 MiB
+    free(big)
+    assert alloc((101 << 20) + 7) == big
+    free(big)
+
+
+def test_pool_reuse_is_ordered_on_the_stream(dev):
+    """A block freed while queued copies still read it, taken back at once by bch_alloc and
+    overwritten by an upload: the copies see the old contents, because the upload queues
+    behind them on the context's stream (bch_free does not wait)."""
+    import ctypes as C
+    _say("pool: reuse is ordered behind the work that reads the block")
+    lib, ctx = dev._lib, dev.ctx
+    n = (256 << 20) // 4
+    x = O.Lcg(77).uniform(n)
+    p = C.c_void_p()
+    dev.check(lib.bch_alloc(ctx, 4 * n, C.byref(p)), "alloc")
+    src = p.value
+    dev.check(lib.bch_upload(ctx, C.c_void_p(src), x.ctypes.data_as(C.c_void_p), 4 * n), "upload")
+    dsts = [Tensor.empty([n], dev) for _ in range(4)]
+    for d in dsts:  # ~0.35 ms of copies queued that read the block
+        dev.check(lib.bch_copy(ctx, C.c_void_p(d.ptr), C.c_void_p(src), 4 * n), "copy")
+    dev.check(lib.bch_free(ctx, C.c_void_p(src)), "free")
+    q = C.c_void_p()
+    dev.check(lib.bch_alloc(ctx, 4 * n, C.byref(q)), "alloc")
+    assert q.value == src
+    zeros = np.zeros(n, np.float32)
+    dev.check(lib.bch_upload(ctx, q, zeros.ctypes.data_as(C.c_void_p), 4 * n), "upload")
+    for d in dsts:
+        assert np.array_equal(d.to_vec(), x)
+    dev.check(lib.bch_free(ctx, q), "free")
+
+
+def test_pool_recycles_tensor_outputs(dev):
+    """A loop of ops on fresh output tensors reuses the same device memory once the previous
+    results are dropped (no allocation per op in steady state)."""
+    _say("pool: tensor outputs recycled")
+    a = Tensor.from_data(O.Lcg(5).uniform((256, 256)), [256, 256], dev)
+    seen = set()
+    for i in range(6):
+        c = a.matmul(a)
+        seen.add(c.ptr)
+        del c
+    assert len(seen) <= 2, seen
+
+
 def test_two_contexts_from_two_threads():
     """Two contexts on the device, driven from two threads at once: the
     per-device launch set-up (dynamic-LDS limits) is shared and locked, and
