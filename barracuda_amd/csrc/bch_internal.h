@@ -90,16 +90,19 @@ __device__ __forceinline__ float wave_allreduce(float v, Op op) {
 
 // Row softmax over a contiguous [rows, cols] f32 matrix (in may equal out).
 // ws/ws_bytes: device scratch of at least softmax_workspace_bytes(rows, cols)
-// bytes (zero when few long rows are not split across workgroups).
+// bytes (zero when few long rows are not split across workgroups).  guard:
+// a row whose sum is not > 0 (NaN, +inf or only -inf in it) keeps its
+// exp(x - max) un-normalised, as Tensor::softmax_dim's host loop does;
+// without it the row is divided like any other (all NaN).
 hipError_t launch_softmax_rows(hipStream_t s, long long rows, long long cols,
                                const float* in, float* out, void* ws,
-                               size_t ws_bytes);
+                               size_t ws_bytes, bool guard = false);
 size_t softmax_workspace_bytes(long long rows, long long cols);
 // Softmax along the middle axis of [outer, axis, inner]; the scratch rule of
-// launch_softmax_rows applies when inner == 1.
+// launch_softmax_rows applies when inner == 1, and guard as there.
 hipError_t launch_softmax_axis(hipStream_t s, long long outer, long long axis,
                                long long inner, const float* in, float* out,
-                               void* ws, size_t ws_bytes);
+                               void* ws, size_t ws_bytes, bool guard = false);
 size_t softmax_axis_workspace_bytes(long long outer, long long axis,
                                     long long inner);
 // The kernel a launch_softmax_rows with these buffers runs (the split plan's

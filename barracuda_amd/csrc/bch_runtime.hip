@@ -753,8 +753,9 @@ bch_status bch_softmax_axis(bch_ctx* ctx, long long outer, long long axis, long 
     st = ensure_ws(ctx, wsb);
     if (st != BCH_OK) return st;
   }
+  // softmax_dim's own semantics: a slice whose sum is not > 0 stays un-normalised
   return from_hip(ctx, bch::launch_softmax_axis(ctx->stream, outer, axis, inner, in, out, ctx->ws,
-                                                ctx->ws_bytes),
+                                                ctx->ws_bytes, true),
                   "softmax_dim launch");
 }
 

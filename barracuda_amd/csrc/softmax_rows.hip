@@ -69,11 +69,21 @@ using bch::OpMax;
 using bch::OpSum;
 using bch::wave_allreduce;
 
+// The factor that normalises a row (a column) of sum s: 1 / s, or 1 where `guard` is set and s
+// is not > 0 (a NaN sum: the row holds NaN or +inf; or nothing but -inf).  With guard the slice
+// then keeps its exp(x - max) un-normalised, as the host loop of Tensor::softmax_dim does
+// (ops/tensor_axis_ops.rs:108-114, `if sum > 0.0`); without it the division makes it NaN, as the
+// global softmax's shader does (softmax_simple_f64.wgsl:45-50).  Finite rows are unaffected.
+__device__ __forceinline__ float norm_inv(float s, int guard) { return guard && !(s > 0.0f) ? 1.0f : 1.0f / s; }
+__device__ __forceinline__ float4 norm_inv4(float4 s, int guard) {
+  return make_float4(norm_inv(s.x, guard), norm_inv(s.y, guard), norm_inv(s.z, guard), norm_inv(s.w, guard));
+}
+
 // One wavefront per row, NV float4 per lane (cols <= 256 * NV, cols % 4 == 0).
 template <int NV>
 __device__ __forceinline__ void softmax_rows_wave_body(
     const float* in, float* out, long long rows,
-    int cols) {
+    int cols, int guard) {
   const int lane = threadIdx.x & 63;
   const long long row = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;  // wave-uniform
@@ -105,7 +115,7 @@ __device__ __forceinline__ void softmax_rows_wave_body(
     }
   }
   s = wave_allreduce(s, OpSum());
-  const float inv = 1.0f / s;
+  const float inv = norm_inv(s, guard);
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     int idx = i * 64 + lane;
@@ -119,8 +129,8 @@ __device__ __forceinline__ void softmax_rows_wave_body(
 template <int NV>
 __global__ __launch_bounds__(256) void softmax_rows_wave(
     const float* in, float* out, long long rows,
-    int cols) {
-  softmax_rows_wave_body<NV>(in, out, rows, cols);
+    int cols, int guard) {
+  softmax_rows_wave_body<NV>(in, out, rows, cols, guard);
 }
 
 // Online update of (max m, sum s) with one element v; -inf contributes 0.
@@ -164,14 +174,14 @@ __device__ __forceinline__ void block_merge(float& m, float& s) {
 // One workgroup (256 threads) per row, any cols.
 __global__ __launch_bounds__(256) void softmax_rows_block(
     const float* in, float* out, long long rows,
-    long long cols) {
+    long long cols, int guard) {
   const long long row = blockIdx.x;
   const float* x = in + row * cols;
   float* y = out + row * cols;
   float m = -INFINITY, s = 0.0f;
   for (long long j = threadIdx.x; j < cols; j += 256) online_push(m, s, x[j]);
   block_merge(m, s);
-  const float inv = 1.0f / s;
+  const float inv = norm_inv(s, guard);
   for (long long j = threadIdx.x; j < cols; j += 256) y[j] = exp_f32(x[j] - m) * inv;
 }
 
@@ -193,7 +203,7 @@ __device__ __forceinline__ float block_allreduce_nw(float v, Op op, float* red) 
 }
 
 template <int NV, int NT>
-__global__ __launch_bounds__(NT) void softmax_rows_wg(const float* in, float* out, int cols) {
+__global__ __launch_bounds__(NT) void softmax_rows_wg(const float* in, float* out, int cols, int guard) {
   __shared__ float redm[NT / 64], reds[NT / 64];
   const long long row = blockIdx.x;
   const int nvec = cols >> 2;
@@ -219,7 +229,7 @@ __global__ __launch_bounds__(NT) void softmax_rows_wg(const float* in, float* ou
     }
   }
   s = block_allreduce_nw<NT / 64>(s, OpSum(), reds);
-  const float inv = 1.0f / s;
+  const float inv = norm_inv(s, guard);
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int idx = i * NT + (int)threadIdx.x;
@@ -231,7 +241,7 @@ __global__ __launch_bounds__(NT) void softmax_rows_wg(const float* in, float* ou
 // buffers), left whole by the split plan: one NT-thread workgroup per row, thread t holding elements
 // t, t + NT, ... (NS of them) in registers; scalar loads, read once, write once.
 template <int NS, int NT>
-__global__ __launch_bounds__(NT) void softmax_rows_wgs(const float* in, float* out, int cols) {
+__global__ __launch_bounds__(NT) void softmax_rows_wgs(const float* in, float* out, int cols, int guard) {
   __shared__ float redm[NT / 64], reds[NT / 64];
   const float* x = in + (long long)blockIdx.x * cols;
   float* y = out + (long long)blockIdx.x * cols;
@@ -253,7 +263,7 @@ __global__ __launch_bounds__(NT) void softmax_rows_wgs(const float* in, float* o
     }
   }
   s = block_allreduce_nw<NT / 64>(s, OpSum(), reds);
-  const float inv = 1.0f / s;
+  const float inv = norm_inv(s, guard);
 #pragma unroll
   for (int i = 0; i < NS; ++i) {
     const int j = i * NT + (int)threadIdx.x;
@@ -335,13 +345,13 @@ __global__ __launch_bounds__(256) void softmax_split_stats(
 template <bool VEC>
 __global__ __launch_bounds__(256) void softmax_split_write(
     const float* in, float* out, long long cols,
-    long long chunk, const float* __restrict__ part) {
+    long long chunk, const float* __restrict__ part, int guard) {
   const long long r = blockIdx.y;
   const float* pr = part + 2 * r * gridDim.x;
   float m = -INFINITY, s = 0.0f;
   for (unsigned c = threadIdx.x; c < gridDim.x; c += 256) merge_state(m, s, pr[2 * c], pr[2 * c + 1]);
   block_merge(m, s);
-  const float inv = 1.0f / s;
+  const float inv = norm_inv(s, guard);
   const long long j0 = (long long)blockIdx.x * chunk;
   const long long j1 = j0 + chunk < cols ? j0 + chunk : cols;
   const float* x = in + r * cols;
@@ -402,7 +412,7 @@ __device__ __forceinline__ ColWg col_wg(int strips, int nchunks) {
 template <bool ONE>
 __global__ __launch_bounds__(256) void softmax_cols(const float* in, float* out, long long axis,
                                                     long long inner, int cw, int strips, int nchunks,
-                                                    long long rpc, float* __restrict__ part) {
+                                                    long long rpc, float* __restrict__ part, int guard) {
   __shared__ float sm[256], ss[256];
   const ColWg w = col_wg(strips, nchunks);
   const int rgs = 256 / cw;
@@ -441,14 +451,15 @@ __global__ __launch_bounds__(256) void softmax_cols(const float* in, float* out,
   if (!ONE) return;
   __syncthreads();
   if (!on) return;
-  const float mx = sm[c], inv = 1.0f / ss[c];
+  const float mx = sm[c], inv = norm_inv(ss[c], guard);
   float* y = out + w.o * axis * inner + col;
   for (long long r = r0 + g; r < r1; r += rgs) y[r * inner] = exp_f32(x[r * inner] - mx) * inv;
 }
 
 __global__ __launch_bounds__(256) void softmax_cols_write(const float* in, float* out, long long axis,
                                                           long long inner, int cw, int strips, int nchunks,
-                                                          long long rpc, const float* __restrict__ part) {
+                                                          long long rpc, const float* __restrict__ part,
+                                                          int guard) {
   const ColWg w = col_wg(strips, nchunks);
   const int rgs = 256 / cw;
   const int g = threadIdx.x / cw, c = threadIdx.x - g * cw;
@@ -457,7 +468,7 @@ __global__ __launch_bounds__(256) void softmax_cols_write(const float* in, float
   const float* pc = part + 2 * ((long long)w.o * nchunks * inner + col);
   float m = -INFINITY, s = 0.0f;
   for (int k = 0; k < nchunks; ++k) merge_state(m, s, pc[2LL * k * inner], pc[2LL * k * inner + 1]);
-  const float inv = 1.0f / s;
+  const float inv = norm_inv(s, guard);
   const long long r0 = (long long)w.chunk * rpc, r1 = r0 + rpc < axis ? r0 + rpc : axis;
   const float* x = in + w.o * axis * inner + col;
   float* y = out + w.o * axis * inner + col;
@@ -497,7 +508,7 @@ __device__ __forceinline__ float4 col_reduce(float4 a, float4 (*red)[W], bool is
 template <int R, int W, int NT, bool STATS>
 __global__ __launch_bounds__(NT) void softmax_cols_reg(const float* in, float* out, long long axis,
                                                        long long inner4, long long strips, long long nchunks,
-                                                       float4* __restrict__ part, long long plane) {
+                                                       float4* __restrict__ part, long long plane, int guard) {
   constexpr int kRpp = NT / W, kNW = NT / 64;
   __shared__ float4 redm[kNW][W], reds[kNW][W];
   const long long b = xcd_block();
@@ -540,7 +551,7 @@ __global__ __launch_bounds__(NT) void softmax_cols_reg(const float* in, float* o
     }
     return;
   }
-  const float4 inv = make_float4(1.0f / sm.x, 1.0f / sm.y, 1.0f / sm.z, 1.0f / sm.w);
+  const float4 inv = norm_inv4(sm, guard);
 #pragma unroll
   for (int i = 0; i < R; ++i) {
     const long long r = r0 + g + (long long)i * kRpp;
@@ -565,7 +576,7 @@ template <int W, int NT>
 __global__ __launch_bounds__(NT) void softmax_cols_vwrite(const float* in, float* out, long long axis,
                                                           long long inner4, long long strips, long long nchunks,
                                                           long long rpc, const float4* __restrict__ part,
-                                                          long long plane) {
+                                                          long long plane, int guard) {
   constexpr int kRpp = NT / W, kNW = NT / 64;
   __shared__ float4 stm[kNW][W], sts[kNW][W];
   const long long b = xcd_block();
@@ -598,7 +609,7 @@ __global__ __launch_bounds__(NT) void softmax_cols_vwrite(const float* in, float
   float4 m = stm[0][c], sm = sts[0][c];
 #pragma unroll
   for (int i = 1; i < kNW; ++i) merge_state4(m, sm, stm[i][c], sts[i][c]);
-  const float4 inv = make_float4(1.0f / sm.x, 1.0f / sm.y, 1.0f / sm.z, 1.0f / sm.w);
+  const float4 inv = norm_inv4(sm, guard);
   const long long r0 = chunk * rpc, r1 = r0 + rpc < axis ? r0 + rpc : axis;
   const float4* x = reinterpret_cast<const float4*>(in) + o * axis * inner4 + col4;
   float4* y = reinterpret_cast<float4*>(out) + o * axis * inner4 + col4;
@@ -653,27 +664,27 @@ bool vec_aligned(const void* in, const void* out) {
 
 template <int W, int NT, bool STATS>
 void launch_cols_vec_r(hipStream_t s, const VecPlan& p, long long blocks, long long axis, long long inner4,
-                       const float* in, float* out, float4* part, long long plane) {
+                       const float* in, float* out, float4* part, long long plane, int guard) {
   const dim3 grid((unsigned)blocks), block(NT);
   switch (p.r) {
-    case 4: hipLaunchKernelGGL((softmax_cols_reg<4, W, NT, STATS>), grid, block, 0, s, in, out, axis, inner4, p.strips, p.nchunks, part, plane); break;
-    case 8: hipLaunchKernelGGL((softmax_cols_reg<8, W, NT, STATS>), grid, block, 0, s, in, out, axis, inner4, p.strips, p.nchunks, part, plane); break;
-    case 16: hipLaunchKernelGGL((softmax_cols_reg<16, W, NT, STATS>), grid, block, 0, s, in, out, axis, inner4, p.strips, p.nchunks, part, plane); break;
-    default: hipLaunchKernelGGL((softmax_cols_reg<32, W, NT, STATS>), grid, block, 0, s, in, out, axis, inner4, p.strips, p.nchunks, part, plane); break;
+    case 4: hipLaunchKernelGGL((softmax_cols_reg<4, W, NT, STATS>), grid, block, 0, s, in, out, axis, inner4, p.strips, p.nchunks, part, plane, guard); break;
+    case 8: hipLaunchKernelGGL((softmax_cols_reg<8, W, NT, STATS>), grid, block, 0, s, in, out, axis, inner4, p.strips, p.nchunks, part, plane, guard); break;
+    case 16: hipLaunchKernelGGL((softmax_cols_reg<16, W, NT, STATS>), grid, block, 0, s, in, out, axis, inner4, p.strips, p.nchunks, part, plane, guard); break;
+    default: hipLaunchKernelGGL((softmax_cols_reg<32, W, NT, STATS>), grid, block, 0, s, in, out, axis, inner4, p.strips, p.nchunks, part, plane, guard); break;
   }
   if (STATS)
     hipLaunchKernelGGL((softmax_cols_vwrite<W, NT>), grid, block, 0, s, in, out, axis, inner4, p.strips, p.nchunks,
-                       p.rpc, part, plane);
+                       p.rpc, part, plane, guard);
 }
 
 template <int W, int NT>
 void launch_cols_vec_w(hipStream_t s, const VecPlan& p, long long outer, long long axis, long long inner4,
-                       const float* in, float* out, float4* part) {
+                       const float* in, float* out, float4* part, int guard) {
   const long long blocks = outer * p.strips * p.nchunks;
   if (p.nchunks == 1)
-    launch_cols_vec_r<W, NT, false>(s, p, blocks, axis, inner4, in, out, nullptr, 0);
+    launch_cols_vec_r<W, NT, false>(s, p, blocks, axis, inner4, in, out, nullptr, 0, guard);
   else
-    launch_cols_vec_r<W, NT, true>(s, p, blocks, axis, inner4, in, out, part, outer * p.nchunks * inner4);
+    launch_cols_vec_r<W, NT, true>(s, p, blocks, axis, inner4, in, out, part, outer * p.nchunks * inner4, guard);
 }
 
 // ---- Wide rows, long axis: [outer, axis, inner] with inner >= 1024 (float4, aligned) and an
@@ -690,8 +701,8 @@ void launch_cols_vec_w(hipStream_t s, const VecPlan& p, long long outer, long lo
 //   write: per column, y = exp(x - max) / sum, streamed; write chunk c takes rows c, c + nchunks,
 //          ..., so the workgroups in flight cover neighbouring rows (186 us against 194 us for
 //          contiguous chunks at 1 x 65536 x 2048; the stats pass is faster on contiguous chunks).
-// An all -inf chunk is the empty state (-inf, 0); NaN anywhere in a column makes it all NaN, as
-// the float4 plan does.
+// An all -inf chunk is the empty state (-inf, 0); NaN or +inf anywhere in a column makes its sum
+// NaN, and the merge stores the normaliser norm_inv gives for it, as the float4 plan does.
 constexpr int kWideCols = 256;  // float4 columns per workgroup (one per thread)
 constexpr int kWideRb = 8;      // rows per register batch
 
@@ -786,7 +797,7 @@ constexpr int kMergeCols = 1;
 constexpr int kMergeSlots = 256 / kMergeCols;
 __global__ __launch_bounds__(256) void softmax_cols_wide_merge(const float4* __restrict__ part, long long plane,
                                                                long long nchunks, long long inner4, long long nq,
-                                                               float4* __restrict__ fin) {
+                                                               float4* __restrict__ fin, int guard) {
   __shared__ float4 wm[4][kMergeCols], wsum[4][kMergeCols];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, c = threadIdx.x % kMergeCols;
   const long long per = (inner4 + kMergeCols - 1) / kMergeCols;  // column groups of one outer index
@@ -819,7 +830,7 @@ __global__ __launch_bounds__(256) void softmax_cols_wide_merge(const float4* __r
     for (int i = 1; i < 4; ++i) merge_state4(m, sm, wm[i][c], wsum[i][c]);
     const long long q = o * inner4 + col4;
     fin[q] = m;
-    fin[nq + q] = make_float4(1.0f / sm.x, 1.0f / sm.y, 1.0f / sm.z, 1.0f / sm.w);
+    fin[nq + q] = norm_inv4(sm, guard);
   }
 }
 
@@ -845,7 +856,7 @@ __global__ __launch_bounds__(256) void softmax_cols_wide_write(const float4* __r
 }
 
 hipError_t launch_cols_wide(hipStream_t s, const WidePlan& p, long long outer, long long axis, long long inner,
-                            const float* in, float* out, void* ws) {
+                            const float* in, float* out, void* ws, int guard) {
   const long long inner4 = inner / 4, nq = outer * inner4;
   float4* part = static_cast<float4*>(ws);
   const long long plane = outer * p.nchunks * inner4;
@@ -858,7 +869,7 @@ hipError_t launch_cols_wide(hipStream_t s, const WidePlan& p, long long outer, l
   if (e != hipSuccess) return e;
   const long long mblocks = outer * ((inner4 + kMergeCols - 1) / kMergeCols);
   hipLaunchKernelGGL(softmax_cols_wide_merge, dim3((unsigned)mblocks), dim3(256), 0, s, part, plane,
-                     p.nchunks, inner4, nq, fin);
+                     p.nchunks, inner4, nq, fin, guard);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(softmax_cols_wide_write, dim3((unsigned)blocks), dim3(256), 0, s, x,
@@ -980,42 +991,43 @@ SmPlan sm_plan(long long cols, const float* in, const float* out) {
 }
 
 // One launch over n rows (n <= kRowsPerLaunch).
-hipError_t launch_sm_rows(hipStream_t s, const SmPlan& p, long long n, long long cols, const float* in, float* out) {
+hipError_t launch_sm_rows(hipStream_t s, const SmPlan& p, long long n, long long cols, const float* in, float* out,
+                          int guard) {
   const int c = (int)cols;
   switch (p.kind) {
     case SmKind::kWave: {
       const dim3 grid((unsigned)((n + 3) / 4)), block(256);
       switch (p.sel) {
-        case 1: hipLaunchKernelGGL(softmax_rows_wave<1>, grid, block, 0, s, in, out, n, c); break;
-        case 2: hipLaunchKernelGGL(softmax_rows_wave<2>, grid, block, 0, s, in, out, n, c); break;
-        case 4: hipLaunchKernelGGL(softmax_rows_wave<4>, grid, block, 0, s, in, out, n, c); break;
-        case 8: hipLaunchKernelGGL(softmax_rows_wave<8>, grid, block, 0, s, in, out, n, c); break;
-        default: hipLaunchKernelGGL(softmax_rows_wave<16>, grid, block, 0, s, in, out, n, c); break;
+        case 1: hipLaunchKernelGGL(softmax_rows_wave<1>, grid, block, 0, s, in, out, n, c, guard); break;
+        case 2: hipLaunchKernelGGL(softmax_rows_wave<2>, grid, block, 0, s, in, out, n, c, guard); break;
+        case 4: hipLaunchKernelGGL(softmax_rows_wave<4>, grid, block, 0, s, in, out, n, c, guard); break;
+        case 8: hipLaunchKernelGGL(softmax_rows_wave<8>, grid, block, 0, s, in, out, n, c, guard); break;
+        default: hipLaunchKernelGGL(softmax_rows_wave<16>, grid, block, 0, s, in, out, n, c, guard); break;
       }
       break;
     }
     case SmKind::kWg: {
       const dim3 grid((unsigned)n), block(256);
       switch (p.sel) {
-        case 8: hipLaunchKernelGGL((softmax_rows_wg<8, 256>), grid, block, 0, s, in, out, c); break;
-        case 16: hipLaunchKernelGGL((softmax_rows_wg<16, 256>), grid, block, 0, s, in, out, c); break;
-        case 32: hipLaunchKernelGGL((softmax_rows_wg<32, 256>), grid, block, 0, s, in, out, c); break;
-        default: hipLaunchKernelGGL((softmax_rows_wg<16, 1024>), grid, dim3(1024), 0, s, in, out, c); break;
+        case 8: hipLaunchKernelGGL((softmax_rows_wg<8, 256>), grid, block, 0, s, in, out, c, guard); break;
+        case 16: hipLaunchKernelGGL((softmax_rows_wg<16, 256>), grid, block, 0, s, in, out, c, guard); break;
+        case 32: hipLaunchKernelGGL((softmax_rows_wg<32, 256>), grid, block, 0, s, in, out, c, guard); break;
+        default: hipLaunchKernelGGL((softmax_rows_wg<16, 1024>), grid, dim3(1024), 0, s, in, out, c, guard); break;
       }
       break;
     }
     case SmKind::kWgs: {
       const dim3 grid((unsigned)n);
       switch (p.sel) {
-        case 40256: hipLaunchKernelGGL((softmax_rows_wgs<4, 256>), grid, dim3(256), 0, s, in, out, c); break;
-        case 160256: hipLaunchKernelGGL((softmax_rows_wgs<16, 256>), grid, dim3(256), 0, s, in, out, c); break;
-        case 161024: hipLaunchKernelGGL((softmax_rows_wgs<16, 1024>), grid, dim3(1024), 0, s, in, out, c); break;
-        default: hipLaunchKernelGGL((softmax_rows_wgs<32, 1024>), grid, dim3(1024), 0, s, in, out, c); break;
+        case 40256: hipLaunchKernelGGL((softmax_rows_wgs<4, 256>), grid, dim3(256), 0, s, in, out, c, guard); break;
+        case 160256: hipLaunchKernelGGL((softmax_rows_wgs<16, 256>), grid, dim3(256), 0, s, in, out, c, guard); break;
+        case 161024: hipLaunchKernelGGL((softmax_rows_wgs<16, 1024>), grid, dim3(1024), 0, s, in, out, c, guard); break;
+        default: hipLaunchKernelGGL((softmax_rows_wgs<32, 1024>), grid, dim3(1024), 0, s, in, out, c, guard); break;
       }
       break;
     }
     default:
-      hipLaunchKernelGGL(softmax_rows_block, dim3((unsigned)n), dim3(256), 0, s, in, out, n, cols);
+      hipLaunchKernelGGL(softmax_rows_block, dim3((unsigned)n), dim3(256), 0, s, in, out, n, cols, guard);
       break;
   }
   return hipGetLastError();
@@ -1058,7 +1070,7 @@ const char* softmax_kernel_name(long long rows, long long cols, const float* in,
 
 hipError_t launch_softmax_rows(hipStream_t s, long long rows, long long cols,
                                const float* in, float* out, void* ws,
-                               size_t ws_bytes) {
+                               size_t ws_bytes, bool guard) {
   if (rows <= 0 || cols <= 0) return hipSuccess;
   const SplitPlan sp = split_plan(rows, cols);
   if (sp.splits > 1) {
@@ -1070,10 +1082,10 @@ hipError_t launch_softmax_rows(hipStream_t s, long long rows, long long cols,
     dim3 grid((unsigned)sp.splits, (unsigned)rows), block(256);
     if (vec) {
       hipLaunchKernelGGL(softmax_split_stats<true>, grid, block, 0, s, in, cols, sp.chunk, part);
-      hipLaunchKernelGGL(softmax_split_write<true>, grid, block, 0, s, in, out, cols, sp.chunk, part);
+      hipLaunchKernelGGL(softmax_split_write<true>, grid, block, 0, s, in, out, cols, sp.chunk, part, guard);
     } else {
       hipLaunchKernelGGL(softmax_split_stats<false>, grid, block, 0, s, in, cols, sp.chunk, part);
-      hipLaunchKernelGGL(softmax_split_write<false>, grid, block, 0, s, in, out, cols, sp.chunk, part);
+      hipLaunchKernelGGL(softmax_split_write<false>, grid, block, 0, s, in, out, cols, sp.chunk, part, guard);
     }
     return hipGetLastError();
   }
@@ -1083,7 +1095,7 @@ hipError_t launch_softmax_rows(hipStream_t s, long long rows, long long cols,
   // float4 kernels were chosen for
   for (long long r0 = 0; r0 < rows; r0 += kRowsPerLaunch) {
     const long long n = rows - r0 < kRowsPerLaunch ? rows - r0 : kRowsPerLaunch;
-    const hipError_t e = launch_sm_rows(s, p, n, cols, in + r0 * cols, out + r0 * cols);
+    const hipError_t e = launch_sm_rows(s, p, n, cols, in + r0 * cols, out + r0 * cols, guard);
     if (e != hipSuccess) return e;
   }
   return hipSuccess;
@@ -1091,13 +1103,13 @@ hipError_t launch_softmax_rows(hipStream_t s, long long rows, long long cols,
 
 hipError_t launch_softmax_axis(hipStream_t s, long long outer, long long axis,
                                long long inner, const float* in, float* out,
-                               void* ws, size_t ws_bytes) {
+                               void* ws, size_t ws_bytes, bool guard) {
   if (outer <= 0 || axis <= 0 || inner <= 0) return hipSuccess;
-  if (inner == 1) return launch_softmax_rows(s, outer, axis, in, out, ws, ws_bytes);
+  if (inner == 1) return launch_softmax_rows(s, outer, axis, in, out, ws, ws_bytes, guard);
   const WidePlan wp = wide_plan(outer, axis, inner);
   if (wp.on && vec_aligned(in, out)) {
     if (ws == nullptr || ws_bytes < wide_bytes(outer, inner, wp)) return hipErrorInvalidValue;
-    return launch_cols_wide(s, wp, outer, axis, inner, in, out, ws);
+    return launch_cols_wide(s, wp, outer, axis, inner, in, out, ws, guard);
   }
   const VecPlan vp = vec_plan(outer, axis, inner);
   if (vp.w && vec_aligned(in, out)) {
@@ -1107,10 +1119,10 @@ hipError_t launch_softmax_axis(hipStream_t s, long long outer, long long axis,
       part = static_cast<float4*>(ws);
     }
     switch (vp.w) {
-      case 1: launch_cols_vec_w<1, 256>(s, vp, outer, axis, inner / 4, in, out, part); break;
-      case 2: launch_cols_vec_w<2, 256>(s, vp, outer, axis, inner / 4, in, out, part); break;
-      case 4: launch_cols_vec_w<4, 256>(s, vp, outer, axis, inner / 4, in, out, part); break;
-      default: launch_cols_vec_w<8, 512>(s, vp, outer, axis, inner / 4, in, out, part); break;
+      case 1: launch_cols_vec_w<1, 256>(s, vp, outer, axis, inner / 4, in, out, part, guard); break;
+      case 2: launch_cols_vec_w<2, 256>(s, vp, outer, axis, inner / 4, in, out, part, guard); break;
+      case 4: launch_cols_vec_w<4, 256>(s, vp, outer, axis, inner / 4, in, out, part, guard); break;
+      default: launch_cols_vec_w<8, 512>(s, vp, outer, axis, inner / 4, in, out, part, guard); break;
     }
     return hipGetLastError();
   }
@@ -1119,18 +1131,18 @@ hipError_t launch_softmax_axis(hipStream_t s, long long outer, long long axis,
   if (blocks > 0x7fffffffLL) return hipErrorInvalidValue;
   if (p.nchunks == 1) {
     hipLaunchKernelGGL(softmax_cols<true>, dim3((unsigned)blocks), dim3(256), 0, s, in, out, axis, inner, p.cw,
-                       p.strips, 1, p.rpc, nullptr);
+                       p.strips, 1, p.rpc, nullptr, guard);
     return hipGetLastError();
   }
   const size_t need = sizeof(float) * 2 * (size_t)outer * p.nchunks * (size_t)inner;
   if (ws == nullptr || ws_bytes < need) return hipErrorInvalidValue;
   float* part = static_cast<float*>(ws);
   hipLaunchKernelGGL(softmax_cols<false>, dim3((unsigned)blocks), dim3(256), 0, s, in, out, axis, inner, p.cw,
-                     p.strips, p.nchunks, p.rpc, part);
+                     p.strips, p.nchunks, p.rpc, part, guard);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(softmax_cols_write, dim3((unsigned)blocks), dim3(256), 0, s, in, out, axis, inner, p.cw,
-                     p.strips, p.nchunks, p.rpc, part);
+                     p.strips, p.nchunks, p.rpc, part, guard);
   return hipGetLastError();
 }
 
@@ -1140,5 +1152,5 @@ hipError_t launch_softmax_axis(hipStream_t s, long long outer, long long axis,
 // cols == 2048 register-resident row softmax, 4 rows per 256-thread block.
 extern "C" __global__ __launch_bounds__(256) void bch_softmax_rows_2048(
     const float* in, float* out, long long rows) {
-  softmax_rows_wave_body<8>(in, out, rows, 2048);
+  softmax_rows_wave_body<8>(in, out, rows, 2048, 0);
 }

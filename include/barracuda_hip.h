@@ -215,11 +215,13 @@ bch_status bch_dgemm(bch_ctx *ctx, int transa, int transb, int batch, int m,
                      long long strideC);
 
 /* Row-wise numerically stable softmax: out[r,:] = exp(x - max_r) / sum.
- * rows, cols >= 1; in == out is allowed.  Replaces Tensor::softmax_dim
- * (ops/tensor_axis_ops.rs:67-126) for the last axis, the attention row
- * softmax K7 (shaders/activation/attention_softmax_f64.wgsl:24-58), and,
+ * rows, cols >= 1; in == out is allowed.  Replaces the attention row
+ * softmax K7 (shaders/activation/attention_softmax_f64.wgsl:24-58) and,
  * with rows == 1, the global Softmax::execute (ops/softmax.rs:58-133, K11
- * softmax_simple_f64.wgsl). */
+ * softmax_simple_f64.wgsl), which divide by the sum whatever it is: a row
+ * holding NaN or +inf, or nothing but -inf, comes out all NaN.  For
+ * Tensor::softmax_dim over the last axis use bch_softmax_axis with
+ * inner == 1 (the same kernels, with softmax_dim's handling of such rows). */
 bch_status bch_softmax_rows(bch_ctx *ctx, long long rows, long long cols,
                             const float *in, float *out);
 
@@ -280,10 +282,12 @@ bch_status bch_head_concat(bch_ctx *ctx, int B, int S, int H, int D,
 
 /* Softmax along a middle axis of a tensor viewed as [outer, axis, inner]
  * (element (o,j,i) at (o*axis + j)*inner + i).  inner == 1 is the row case.
- * Replaces Tensor::softmax_dim (ops/tensor_axis_ops.rs:67-126) for
- * axis != last.  A long axis on few columns is cut into chunks whose
- * per-column (max, sum) states use the context's workspace (grown on
- * demand); in == out is allowed. */
+ * Replaces Tensor::softmax_dim (ops/tensor_axis_ops.rs:67-126) for any
+ * axis, with its host loop's handling of a slice whose sum is not > 0
+ * (one holding NaN or +inf, or nothing but -inf): the slice keeps its
+ * exp(x - max) un-normalised (:108-114, `if sum > 0.0`).  A long axis on
+ * few columns is cut into chunks whose per-column (max, sum) states use the
+ * context's workspace (grown on demand); in == out is allowed. */
 bch_status bch_softmax_axis(bch_ctx *ctx, long long outer, long long axis,
                             long long inner, const float *in, float *out);
 

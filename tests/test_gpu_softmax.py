@@ -111,13 +111,25 @@ NONFINITE_AXES = [(16, 2048, 1024), (300, 1000, 12), (1, 65536, 96), (1, 3000, 1
                   (3000, 512, 5), (2, 70000, 2)]
 
 
+def _assert_softmax_dim(got, want):
+    """NaN exactly where the reference's softmax_dim has NaN; elsewhere within the bar."""
+    got = np.asarray(got, np.float32).reshape(-1)
+    want = np.asarray(want, np.float32).reshape(-1)
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    ok = ~np.isnan(want)
+    assert O.max_rel_err(np.ascontiguousarray(got[ok]), np.ascontiguousarray(want[ok]).astype(np.float64)) <= TOL
+
+
 @pytest.mark.parametrize("rows,cols", NONFINITE_ROWS)
 def test_nonfinite_rows_every_path(dev, rows, cols):
-    """A row holding +inf, one holding NaN and one of nothing but -inf come out all NaN on every
-    kernel path (the max taken first, or online states whose merge rescales a +inf state by
-    exp(inf - inf)), while the other rows match the f64 oracle.  The reference's host softmax_dim leaves such rows un-normalised
-    (its `if sum > 0.0`, ops/tensor_axis_ops.rs:108-114) and its global softmax shader divides
-    by the NaN sum (all NaN, softmax_simple_f64.wgsl:45-50); one kernel serves both here."""
+    """A row holding +inf, one holding NaN and one of nothing but -inf, on every kernel path (the
+    max taken first, or online states whose merge rescales a +inf state by exp(inf - inf)):
+      * bch_softmax_rows (the global softmax's and attention's semantics: divide by the sum)
+        makes them all NaN, as softmax_simple_f64.wgsl:45-50 does;
+      * bch_softmax_axis with inner == 1 (Tensor::softmax_dim over the last axis) leaves them
+        un-normalised where the sum is not > 0 (ops/tensor_axis_ops.rs:108-114): equal to the
+        reference's host loop restated (oracle softmax_dim_f32), NaN for NaN.
+    The other rows match the f64 oracle."""
     _say(f"softmax non-finite rows={rows} cols={cols}")
     base = O.Lcg(rows * 7 + cols).normal((rows, cols), 0.0, 3.0)
 
@@ -149,12 +161,18 @@ def test_nonfinite_rows_every_path(dev, rows, cols):
         good = [i for i in range(rows) if i not in bad]
         if good:
             assert O.max_rel_err(got[good], O.softmax_rows_f64(x[good])) <= TOL
+        dim = _axis_gpu(dev, x.reshape(rows, cols, 1)).reshape(rows, cols)
+        _assert_softmax_dim(dim[bad], O.softmax_dim_f32(x[bad]))
+        if good:
+            assert O.max_rel_err(dim[good], O.softmax_rows_f64(x[good])) <= TOL
 
 
 @pytest.mark.parametrize("outer,axis,inner", NONFINITE_AXES)
 def test_nonfinite_columns_every_path(dev, outer, axis, inner):
-    """The same for softmax over a middle axis: the column holding +inf, the one holding NaN
-    and the all -inf one come out all NaN; every other column matches the f64 oracle."""
+    """softmax_dim over a middle axis (bch_softmax_axis) on every column path: the column
+    holding +inf, the one holding NaN and the all -inf one equal the reference's host loop
+    restated (un-normalised where the sum is not > 0, NaN for NaN); every other column matches
+    the f64 oracle."""
     _say(f"softmax non-finite columns outer={outer} axis={axis} inner={inner}")
     x = O.Lcg(outer + axis * 3 + inner).normal((outer, axis, inner), 0.0, 3.0)
     x[0, axis // 3, 0] = np.inf
@@ -164,8 +182,9 @@ def test_nonfinite_columns_every_path(dev, outer, axis, inner):
         x[0, :, 2] = -np.inf
         bad.append(2)
     got = _axis_gpu(dev, x)
+    ref_dim = O.softmax_dim_f32(x, axis=1)
     for c in bad:
-        assert np.all(np.isnan(got[0, :, c])), c
+        _assert_softmax_dim(got[0, :, c], ref_dim[0, :, c])
     want = np.moveaxis(O.softmax_rows_f64(np.ascontiguousarray(np.moveaxis(x, 1, -1))), -1, 1)
     keep = np.ones((outer, inner), bool)
     keep[0, bad] = False
