@@ -151,3 +151,46 @@ def test_dgemm_split_k_alpha_beta_and_integers(dev):
                                     C.c_void_p(db.ptr), n, k * n, beta, C.c_void_p(dc.ptr), n, m * n), "dgemm")
         ref = alpha * want.astype(np.float64) + (beta * c0 if beta != 0.0 else 0.0)
         assert _rel(dc.to_vec(), ref) <= TOL
+
+
+def _dgemm_raw(dev, ta, tb, batch, m, n, k, A, lda, sA, B, ldb, sB, ldc, sC, a_shift=0, b_shift=0):
+    """bch_dgemm on host arrays laid out with the given leading dimensions and
+    batch strides; a_shift / b_shift move the operand base by that many
+    doubles (8 bytes each: not 16-byte aligned when odd)."""
+    da = F64Buffer(dev, A.size + a_shift).upload(np.concatenate([np.zeros(a_shift), A]))
+    db = F64Buffer(dev, B.size + b_shift).upload(np.concatenate([np.zeros(b_shift), B]))
+    dc = F64Buffer(dev, batch * sC).upload(np.full(batch * sC, 7.25))
+    with dev._lock:
+        dev.check(dev._lib.bch_dgemm(dev.ctx, int(ta), int(tb), batch, m, n, k, 1.0,
+                                     C.c_void_p(da.ptr + 8 * a_shift), lda, sA, C.c_void_p(db.ptr + 8 * b_shift),
+                                     ldb, sB, 0.0, C.c_void_p(dc.ptr), ldc, sC), "dgemm")
+    return dc.to_vec()
+
+
+# Ragged shapes whose paired dimension is even take the 128-bit pair-guarded
+# loads (every transpose; batched; split k); the odd and misaligned ones take
+# the scalar guards.  Each result is compared with longdouble, the padding
+# of C (ldc > n) must keep its fill.
+@pytest.mark.parametrize("batch,m,k,n", [(1, 130, 34, 258), (3, 62, 98, 200), (1, 258, 2050, 130),
+                                         (2, 100, 1000, 38), (1, 4, 4096, 6)])
+@pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True), (True, True)])
+@pytest.mark.parametrize("pad,shift", [(0, 0), (2, 0), (2, 1)])
+def test_dgemm_guarded_pair_loads(dev, batch, m, k, n, ta, tb, pad, shift):
+    _say(f"dgemm guarded batch={batch} m={m} k={k} n={n} ta={ta} tb={tb} pad={pad} shift={shift}")
+    rng = np.random.default_rng(batch * 7 + m + 3 * k + 5 * n + 2 * ta + tb + 11 * pad + shift)
+    a = rng.uniform(-1, 1, (batch, k, m) if ta else (batch, m, k))
+    b = rng.uniform(-1, 1, (batch, n, k) if tb else (batch, k, n))
+    lda, ldb, ldc = a.shape[2] + pad, b.shape[2] + 2 * pad, n + pad
+    sA, sB, sC = a.shape[1] * lda + pad, b.shape[1] * ldb, m * ldc + 2 * pad
+    A = np.full(batch * sA, np.nan)  # padding reads would poison the sums
+    B = np.full(batch * sB, np.nan)
+    for z in range(batch):
+        A[z * sA:z * sA + a.shape[1] * lda].reshape(a.shape[1], lda)[:, :a.shape[2]] = a[z]
+        B[z * sB:z * sB + b.shape[1] * ldb].reshape(b.shape[1], ldb)[:, :b.shape[2]] = b[z]
+    got = _dgemm_raw(dev, ta, tb, batch, m, n, k, A, lda, sA, B, ldb, sB, ldc, sC, a_shift=shift, b_shift=shift)
+    want = O.gemm_longdouble(a.reshape(-1), b.reshape(-1), m, k, n, batch, ta, tb).reshape(batch, m, n)
+    for z in range(batch):
+        block = got[z * sC:z * sC + m * ldc].reshape(m, ldc)
+        assert _rel(block[:, :n], want[z]) <= TOL
+        assert np.all(block[:, n:] == 7.25)
+        assert np.all(got[z * sC + m * ldc:(z + 1) * sC] == 7.25)
