@@ -35,11 +35,11 @@
 //     top of the tile: 59.7 -> 63.4 TFLOP/s.
 //   * The LDS stores and global loads of a tile are spread between the
 //     MFMAs of the first half (one of each per two MFMAs) rather than issued
-//     as a burst at the top of the tile.  A register-only loop of
-//     independent v_mfma_f64_16x16x4_f64 reaches 46% of the FP64 matrix
-//     peak with one wavefront per SIMD and 99% with two, so every stretch in
-//     which one of a SIMD's two wavefronts issues no MFMA costs about half
-//     the matrix core.  4096^3: 67.6 -> 72.5 TFLOP/s (86.0% -> 92.2%).
+//     as a burst at the top of the tile, where the four wavefronts of a
+//     workgroup arrive together from the barrier: 4096^3 67.6 -> 72.5
+//     TFLOP/s (86.0% -> 92.2%).  A register-only loop of independent
+//     v_mfma_f64_16x16x4_f64 sustains 99% of the FP64 matrix peak from one
+//     wavefront per SIMD, so what remains is the barrier and memory issue.
 //   * Workgroup -> tile mapping is XCD-aware and grouped, as in the f32 GEMM.
 //   * Split k: when the output has fewer 128 x 128 tiles than the device has
 //     CUs (a skinny m or n, e.g. the P V product of an attention), the k
@@ -264,9 +264,8 @@ __global__ __launch_bounds__(kDT, OCC) void dgemm_mfma_kernel(
     mfma_half(0);
     // Phase 0 order: the second-half reads of tile t, one per 2 MFMAs, then
     // the LDS stores of tile t + 1 and the global loads of tile t + 2, a
-    // store and a load per 2 MFMAs.  A wavefront then never leaves the matrix
-    // core for a burst of memory instructions (one wavefront alone keeps
-    // the f64 matrix core less than half busy).
+    // store and a load per 2 MFMAs, so no burst of memory instructions
+    // holds up a wavefront's MFMAs.
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
