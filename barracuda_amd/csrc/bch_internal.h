@@ -105,6 +105,14 @@ hipError_t launch_softmax_axis(hipStream_t s, long long outer, long long axis,
                                void* ws, size_t ws_bytes, bool guard = false);
 size_t softmax_axis_workspace_bytes(long long outer, long long axis,
                                     long long inner);
+// The row softmax (guard off) of x * scale with a causal mask, the scaled
+// scores of an attention pass: row r of [rows][cols] holds the keys of query
+// r0 + r % m, and with causal its columns past that query are -inf.  One
+// pass, the wavefront-per-row kernel; only where softmax_rows_scaled_supported
+// (cols % 4 == 0, cols <= 4096, 16-byte aligned buffers), else an error.
+bool softmax_rows_scaled_supported(long long cols, const float* in, const float* out);
+hipError_t launch_softmax_rows_scaled(hipStream_t s, long long rows, long long cols, const float* in, float* out,
+                                      float scale, int causal, int m, int r0);
 // The kernel a launch_softmax_rows with these buffers runs (the split plan's
 // write kernel when few long rows are split).
 const char* softmax_kernel_name(long long rows, long long cols, const float* in, const float* out);

@@ -14,13 +14,16 @@
 //   1. S = Q K^T on the FP32-MFMA GEMM with K as the [n][k] operand (the
 //      linear layer's transposed-B tiles), batched over key/value heads;
 //   2. S = scale * S with the causal mask (keys past the query set to -inf),
-//      then the HBM-streaming row softmax in place;
+//      then the HBM-streaming row softmax in place -- one pass where the
+//      scores' rows take the wavefront-per-row kernel (the scale and mask
+//      applied as it loads them), else a scale-and-mask pass first;
 //   3. O = P V on the same GEMM, written through O's row stride.
-// At D > 256 the two products carry 4 D flops per score against about 24
-// bytes of score traffic (stored, scaled and masked, normalised, read back),
+// At D > 256 the two products carry 4 D flops per score against about 16
+// bytes of score traffic (stored, normalised in place, read back),
 // above the FP32 ridge of 19.7 FLOP/B, so the GEMMs dominate.  Measured at
-// B=4, H=32, S=2048, D=512 (one box): 9.76 ms non-causal (71.6% of FP32 MFMA
-// peak), 6.21 ms causal (56.3%).
+// B=4, H=32, S=2048, D=512 (one box): 8.81 ms non-causal (79.4% of FP32 MFMA
+// peak), 5.71 ms causal (61.3%); 9.76 / 6.21 ms with the scale and mask in a
+// pass of their own.
 //
 // Layout of the passes: for each batch b and query head g of a key/value
 // group (query head h = hk * G + g reads key/value head hk), one batched GEMM
@@ -133,11 +136,16 @@ hipError_t launch_sdpa_wide(hipStream_t s, int B, int H, int Hkv, int Sq, int Sk
                                        st.k.head, nullptr, kActNone, S, n, per, xws, xbytes);
         if (e != hipSuccess) return e;
         const long long rows = (long long)Hkv * m;
-        hipLaunchKernelGGL(sdpa_scale_mask_kernel, dim3((unsigned)std::min(rows, 65536LL)), dim3(256), 0, s, S,
-                           rows, n, m, r0, scale, causal);
-        e = hipGetLastError();
-        if (e != hipSuccess) return e;
-        e = launch_softmax_rows(s, rows, n, S, S, xws, xbytes);
+        if (softmax_rows_scaled_supported(n, S, S)) {
+          // scale and mask on the softmax's own load: one pass over the scores
+          e = launch_softmax_rows_scaled(s, rows, n, S, S, scale, causal, m, r0);
+        } else {
+          hipLaunchKernelGGL(sdpa_scale_mask_kernel, dim3((unsigned)std::min(rows, 65536LL)), dim3(256), 0, s, S,
+                             rows, n, m, r0, scale, causal);
+          e = hipGetLastError();
+          if (e != hipSuccess) return e;
+          e = launch_softmax_rows(s, rows, n, S, S, xws, xbytes);
+        }
         if (e != hipSuccess) return e;
         e = launch_sgemm(s, Hkv, m, D, n, S, n, per, vb, vr, st.v.head, ob + (long long)r0 * orow, orow,
                          G * st.o.head, xws, xbytes);

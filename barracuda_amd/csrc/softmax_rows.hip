@@ -80,10 +80,13 @@ __device__ __forceinline__ float4 norm_inv4(float4 s, int guard) {
 }
 
 // One wavefront per row, NV float4 per lane (cols <= 256 * NV, cols % 4 == 0).
-template <int NV>
+// PRE (the attention scores of the wide path): each loaded x first becomes
+// x * scale, or -inf where causal and its column is past key pr0 + (prow0 +
+// row) % pm -- the same f32 values a separate scale-and-mask pass writes.
+template <int NV, bool PRE = false>
 __device__ __forceinline__ void softmax_rows_wave_body(
     const float* in, float* out, long long rows,
-    int cols, int guard) {
+    int cols, int guard, float scale = 1.0f, int causal = 0, int pm = 1, long long prow0 = 0, int pr0 = 0) {
   const int lane = threadIdx.x & 63;
   const long long row = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;  // wave-uniform
@@ -97,6 +100,17 @@ __device__ __forceinline__ void softmax_rows_wave_body(
     int idx = i * 64 + lane;
     v[i] = idx < nvec ? bch::load_nt(src + idx)
                       : make_float4(ninf, ninf, ninf, ninf);
+  }
+  if constexpr (PRE) {
+    const int lim = causal ? pr0 + (int)((prow0 + row) % pm) : 0x7fffffff;  // last key kept
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int c0 = 4 * (i * 64 + lane);
+      v[i].x = c0 > lim ? ninf : v[i].x * scale;
+      v[i].y = c0 + 1 > lim ? ninf : v[i].y * scale;
+      v[i].z = c0 + 2 > lim ? ninf : v[i].z * scale;
+      v[i].w = c0 + 3 > lim ? ninf : v[i].w * scale;
+    }
   }
   float mx = ninf;
 #pragma unroll
@@ -131,6 +145,13 @@ __global__ __launch_bounds__(256) void softmax_rows_wave(
     const float* in, float* out, long long rows,
     int cols, int guard) {
   softmax_rows_wave_body<NV>(in, out, rows, cols, guard);
+}
+
+template <int NV>
+__global__ __launch_bounds__(256) void softmax_rows_wave_scaled(const float* in, float* out, long long rows, int cols,
+                                                                float scale, int causal, int pm, long long prow0,
+                                                                int pr0) {
+  softmax_rows_wave_body<NV, true>(in, out, rows, cols, 0, scale, causal, pm, prow0, pr0);
 }
 
 // Online update of (max m, sum s) with one element v; -inf contributes 0.
@@ -1096,6 +1117,33 @@ hipError_t launch_softmax_rows(hipStream_t s, long long rows, long long cols,
   for (long long r0 = 0; r0 < rows; r0 += kRowsPerLaunch) {
     const long long n = rows - r0 < kRowsPerLaunch ? rows - r0 : kRowsPerLaunch;
     const hipError_t e = launch_sm_rows(s, p, n, cols, in + r0 * cols, out + r0 * cols, guard);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
+bool softmax_rows_scaled_supported(long long cols, const float* in, const float* out) {
+  return wave_path(cols, in, out);
+}
+
+hipError_t launch_softmax_rows_scaled(hipStream_t s, long long rows, long long cols, const float* in, float* out,
+                                      float scale, int causal, int m, int r0) {
+  if (rows <= 0 || cols <= 0) return hipSuccess;
+  if (!wave_path(cols, in, out) || m < 1) return hipErrorInvalidValue;
+  const int c = (int)cols;
+  for (long long b = 0; b < rows; b += kRowsPerLaunch) {
+    const long long n = rows - b < kRowsPerLaunch ? rows - b : kRowsPerLaunch;
+    const dim3 grid((unsigned)((n + 3) / 4)), block(256);
+    const float* i0 = in + b * cols;
+    float* o0 = out + b * cols;
+    switch (pick_nv(cols)) {
+      case 1: hipLaunchKernelGGL(softmax_rows_wave_scaled<1>, grid, block, 0, s, i0, o0, n, c, scale, causal, m, b, r0); break;
+      case 2: hipLaunchKernelGGL(softmax_rows_wave_scaled<2>, grid, block, 0, s, i0, o0, n, c, scale, causal, m, b, r0); break;
+      case 4: hipLaunchKernelGGL(softmax_rows_wave_scaled<4>, grid, block, 0, s, i0, o0, n, c, scale, causal, m, b, r0); break;
+      case 8: hipLaunchKernelGGL(softmax_rows_wave_scaled<8>, grid, block, 0, s, i0, o0, n, c, scale, causal, m, b, r0); break;
+      default: hipLaunchKernelGGL(softmax_rows_wave_scaled<16>, grid, block, 0, s, i0, o0, n, c, scale, causal, m, b, r0); break;
+    }
+    const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
   return hipSuccess;

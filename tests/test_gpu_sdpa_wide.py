@@ -48,7 +48,10 @@ def _sdpa(dev, q, k, v, causal):
     (1, 2, 300, 300, 256, True), (1, 1, 1, 1, 256, False), (1, 1, 5, 9, 129, False),
     # D > 256: the chunked path
     (1, 2, 129, 129, 512, True), (1, 2, 64, 150, 512, False), (2, 1, 33, 33, 320, True),
-    (1, 1, 40, 40, 1000, True), (1, 2, 257, 100, 260, False), (1, 1, 1, 1, 513, False)])
+    (1, 1, 40, 40, 1000, True), (1, 2, 257, 100, 260, False), (1, 1, 1, 1, 513, False),
+    # causal chunks of 256 query rows over several heads, widths that take the
+    # softmax with the scale and mask on its load (n % 4 == 0) and one that does not
+    (1, 3, 600, 600, 320, True), (2, 2, 520, 520, 384, True), (1, 2, 514, 514, 300, True)])
 def test_head_dims_vs_f64(dev, B, H, Sq, Skv, D, causal):
     _say(f"sdpa wide B={B} H={H} Sq={Sq} Skv={Skv} D={D} causal={causal}")
     rng = O.Lcg(B * 131 + H * 17 + Sq * 3 + Skv + D)
