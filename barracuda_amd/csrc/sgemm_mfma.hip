@@ -398,7 +398,10 @@ __global__ __launch_bounds__(kThreads) void sgemm_mfma_kernel(
   constexpr int NR = G::TM + G::TN;                        // LDS reads per chunk
   constexpr int NW = G::A_F4 + 4 * G::B_BLK;               // LDS stores per tile
   constexpr int NM = 4 * G::TM * G::TN;                    // MFMAs per chunk
-  constexpr int MPW = (NM - NR) / NW >= 2 ? 2 : 1;         // MFMAs after each store
+  // the small tile (one MFMA block per wavefront) has too few MFMAs in a chunk to pin its
+  // stores between them; they go where the scheduler puts them within their chunk
+  constexpr bool PIN = NM >= NR + NW;
+  constexpr int MPW = !PIN ? 0 : (NM - NR) / NW >= 2 ? 2 : 1;  // MFMAs after each store
   static_assert(NM >= NR + MPW * NW, "chunk too small to cover its LDS traffic");
   // ES: the last k-tile is peeled (below) so that C leaves block by block
   // (256-row tiles in every load mode, and the scalar-guarded 128 x 128 tile: the
@@ -422,7 +425,7 @@ __global__ __launch_bounds__(kThreads) void sgemm_mfma_kernel(
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       }
-      if (c == NC - 2) {
+      if (PIN && c == NC - 2) {
 #pragma unroll
         for (int w = 0; w < NW; ++w) {
           __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
@@ -726,6 +729,39 @@ int split_slices(int batch, int m, int n, int k, size_t cap = kSplitWsMax, doubl
   return bs;
 }
 
+// ---- small shapes: 64 x 64 x 64 tiles ----
+// Where the planned tiles fill less than one round, 64 x 64 tiles (each wavefront one 32 x 32
+// MFMA block; k-tiles of 64 so that a tile's loads split evenly over the 256 threads) put 16x
+// the workgroups of the 128 x 128 tiling on the CUs, with no k split, partials or reduce
+// launch.  A 64 x 64 x 64 k-tile takes ~1.32 us at any count of tiles up to a round (256^3 to
+// 1024^3; 63% of the matrix cores' rate, against 92% for 128 x 128).  Taken when its modelled
+// time, rounds x k-tiles x 1.32 us, is under 0.9 of the split-K plan's; unguarded loads only
+// (m, n, k multiples of 64, aligned operands), else the usual path.  Same box, two runs each,
+// against the split-K plan: 256^3 19.4 -> 8.8 us, 512^3 23.0 -> 13.9, 768^3 25.8 -> 19.3,
+// 1024^3 28.3 -> 24.4; where split-K stays ahead the model keeps it (1024 x 1024 x 4096 74
+// against 89 us, 512 x 1024 x 2048 28.7 against 46.9).
+constexpr int kSmallBK = 64;
+constexpr double kSmallKtUs = 1.32;
+
+bool small_tile_plan(int batch, int m, int n, int k) {
+  if (batch < 1 || m % 64 != 0 || n % 64 != 0 || k <= 0 || k % kSmallBK != 0) return false;
+  const long long cu = bch::device_cu_count();
+  const Tile t = pick_tile(batch, m, n);
+  const long long tiles =
+      (long long)batch * ((m + tile_m(t) - 1) / tile_m(t)) * ((n + tile_n(t) - 1) / tile_n(t));
+  if (tiles >= cu) return false;
+  double cur = 0.0;
+  split_slices(batch, m, n, k, kSplitWsMax, &cur);
+  const long long t64 = (long long)batch * (m / 64) * (n / 64);
+  return (double)((t64 + cu - 1) / cu) * (k / kSmallBK) * kSmallKtUs < 0.9 * cur;
+}
+
+bool small_tile_ok(int batch, int m, int n, int k, const float* A, int lda, long long sA, const float* B, int ldb,
+                   long long sB) {
+  return small_tile_plan(batch, m, n, k) && lda % 4 == 0 && ldb % 4 == 0 && sA % 4 == 0 && sB % 4 == 0 &&
+         aligned16(A) && aligned16(B);
+}
+
 // C[b][m][n] = act(sum over j < S of P[b][j][m][n] (+ bias[n])) for each of `batch` matrices
 // (C[b] at C + b sC); V: four columns per thread (n % 4 == 0, ldc % 4 == 0, C 16-byte aligned)
 template <bool V>
@@ -1018,6 +1054,7 @@ static const char* tile_path_name(int m, int n, int k, bool allow_mix) {
            (mp.axis == 0 ? tile_path_name(m - m1, n, k, false) : tile_path_name(m, n - n1, k, false));
     return name.c_str();
   }
+  if (small_tile_plan(1, m, n, k)) return "sgemm_mfma_kernel<64,64,64,false>";
   const Tile t = pick_tile(1, m, n);
   // with lda = k and ldb = n, and 16-byte aligned operands
   const bool check = !(m % tile_m(t) == 0 && n % tile_n(t) == 0 && k % kBK == 0 && k % 4 == 0 && n % 4 == 0);
@@ -1131,6 +1168,14 @@ namespace {
 hipError_t launch_tile_path(hipStream_t s, bool transb, int batch, int m, int n, int k, const float* A, int lda,
                             long long sA, const float* B, int ldb, long long sB, const float* bias, int act,
                             float* C, int ldc, long long sC, void* ws, size_t ws_bytes, bool allow_mix) {
+  if (small_tile_ok(batch, m, n, k, A, lda, sA, B, ldb, sB)) {
+    const bool epi = bias != nullptr || act != 0;
+#define BCH_SMALL(TB_, EPI_)                                                                                       \
+  launch_tiles<64, 64, kSmallBK, false, TB_, EPI_>(s, batch, m, n, k, A, lda, sA, B, ldb, sB, C, ldc, sC, bias, act)
+    return transb ? (epi ? BCH_SMALL(true, true) : BCH_SMALL(true, false))
+                  : (epi ? BCH_SMALL(false, true) : BCH_SMALL(false, false));
+#undef BCH_SMALL
+  }
   const Tile t = pick_tile(batch, m, n);
   int sl = split_slices(batch, m, n, k);
   const size_t pbytes = (size_t)batch * m * n * sizeof(float);  // one slice's partials, every batch

@@ -139,8 +139,9 @@ bch_status bch_sync(bch_ctx *ctx);
  * matmul_tiled_f64.wgsl) and MatmulTiled::execute (ops/matmul_tiled.rs:
  * 62-122).  Routes m <= 32 (decode shapes) to the skinny HBM-streaming
  * kernels, 32 < m <= 64 with K % 4 == 0 and 16-byte aligned A to their
- * two-block form, and everything else to the FP32-MFMA tiled kernel (split
- * over k when the tiles fill less than one round of the CUs; whole rounds
+ * two-block form, and everything else to the FP32-MFMA tiled kernel (64x64
+ * tiles, or a split over k, when the tiles fill less than one round of the
+ * CUs, whichever is modelled faster; whole rounds
  * plus k-sliced leftover tiles when the last round would be part-filled; or
  * whole rounds of 256x256 tiles on the first rows or columns of C and the
  * rest planned on its own, where that is modelled faster). */

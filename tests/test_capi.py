@@ -116,7 +116,8 @@ def test_kernel_routing_names():
     assert lib.bch_sgemm_kernel_name(11008, 4096, 4096) == (b"sgemm_mfma_kernel<256,256,32,false> rows then "
                                                             b"sgemm_mfma_kernel<128,128,32,false>")
     assert lib.bch_sgemm_kernel_name(3072, 3072, 3072) == b"sgemm_mfma_kernel<256,128,32,false,hyb>+sgemm_tail_reduce"
-    assert lib.bch_sgemm_kernel_name(1024, 1024, 1024) == b"sgemm_mfma_kernel<128,128,32,false>+sgemm_splitk_reduce"
+    assert lib.bch_sgemm_kernel_name(1024, 1024, 1024) == b"sgemm_mfma_kernel<64,64,64,false>"
+    assert lib.bch_sgemm_kernel_name(1024, 1024, 4096) == b"sgemm_mfma_kernel<128,128,32,false>+sgemm_splitk_reduce"
     assert lib.bch_sgemm_kernel_name(2048, 2048, 2048) == b"sgemm_mfma_kernel<128,128,32,false>"
     assert lib.bch_sgemm_kernel_name(4100, 4096, 300) == b"sgemm_mfma_kernel<128,128,32,true,v4>"
     assert lib.bch_sgemm_kernel_name(4000, 4000, 4000) == b"sgemm_mfma_kernel<256,256,32,true,v4>"

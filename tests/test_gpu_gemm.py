@@ -254,7 +254,7 @@ def test_large_tile_paths(dev, m, n, k, kernel):
 
 
 # the last three take several rounds of slices over 86 / 172 / 86 tiles
-SPLIT_K_CASES = [(1024, 1024, 1024), (512, 512, 8192), (300, 4, 4096), (96, 4096, 4096), (200, 1000, 2048),
+SPLIT_K_CASES = [(1024, 1024, 4096), (512, 512, 8192), (300, 4, 4096), (96, 4096, 4096), (200, 1000, 2048),
                  (128, 11008, 4096), (192, 11008, 4096), (96, 11008, 4096)]
 
 
@@ -280,12 +280,75 @@ def test_split_k_vs_f64(dev, m, n, k):
 def test_split_k_exact_on_integers(dev):
     """Small integers: every partial sum is exact in f32, whatever the slice order."""
     rng = np.random.default_rng(17)
-    for m, n, k in ((1024, 1024, 1024), (64, 4096, 4096)):
+    for m, n, k in ((1024, 1024, 4096), (64, 4096, 4096)):
         _say(f"sgemm split-k integers m={m} n={n} k={k}")
         a = rng.integers(-8, 9, (m, k)).astype(np.float32)
         b = rng.integers(-8, 9, (k, n)).astype(np.float32)
         want = (a.astype(np.int64) @ b.astype(np.int64)).astype(np.float32)
         assert np.array_equal(_mm(dev, a, b), want), (m, n, k)
+
+
+# 64 x 64 x 64 tiles: shapes whose usual tiles fill less than one round and whose k is short
+SMALL_CASES = [(128, 128, 128), (256, 256, 256), (192, 320, 256), (128, 1024, 512), (512, 512, 512), (768, 768, 768),
+               (1024, 1024, 1024)]
+
+
+@pytest.mark.parametrize("m,n,k", SMALL_CASES)
+def test_small_tiles_vs_f64(dev, m, n, k):
+    """The 64 x 64 x 64 tile (one 32 x 32 MFMA block per wavefront, no k split): every element
+    against f64 (inputs scaled by 1/sqrt(k)), then the same shape with the operands' leading
+    dimensions padded by 4 (the same kernel) and with A one float off 16-byte alignment (the
+    usual tiles), and the linear layer's forms ([n][k] weights, bias, ReLU and GELU)."""
+    name = dev._lib.bch_sgemm_kernel_name(m, n, k).decode()
+    assert name == "sgemm_mfma_kernel<64,64,64,false>", name
+    _say(f"sgemm small tiles m={m} n={n} k={k}")
+    rng = O.Lcg(m * 5 + n * 3 + k)
+    a = rng.uniform((m, k)) / np.float32(np.sqrt(k))
+    b = rng.uniform((k, n))
+    want = a.astype(np.float64) @ b.astype(np.float64)
+    got = _mm(dev, a, b)
+    assert O.max_rel_err(got, want) <= TOL
+    assert np.array_equal(got, _mm(dev, a, b)), "not deterministic"
+    lib = dev._lib
+    for pad, shift in ((4, 0), (0, 1)):
+        ap = np.zeros(m * (k + pad) + shift, dtype=np.float32)
+        ap[shift:].reshape(m, k + pad)[:, :k] = a
+        bp = np.zeros((k, n + pad), dtype=np.float32)
+        bp[:, :n] = b
+        ta, tb = Tensor.from_data(ap, [ap.size], dev), Tensor.from_data(bp, [k, n + pad], dev)
+        tc = Tensor.empty([m, n], dev)
+        with dev._lock:
+            dev.check(lib.bch_sgemm(dev.ctx, m, n, k, C.c_void_p(ta.ptr + 4 * shift), k + pad, C.c_void_p(tb.ptr),
+                                    n + pad, C.c_void_p(tc.ptr), n), "sgemm")
+        assert O.max_rel_err(tc.to_numpy(), want) <= TOL, (pad, shift)
+    w = rng.uniform((n, k))
+    bias = rng.uniform((n,))
+    tx, tw, tbias = (Tensor.from_data(x, list(x.shape), dev) for x in (a, w, bias))
+    lin = a.astype(np.float64) @ w.astype(np.float64).T + bias.astype(np.float64)
+    for act in (1, 2):  # BCH_ACT_RELU, BCH_ACT_GELU
+        ty = Tensor.empty([m, n], dev)
+        with dev._lock:
+            dev.check(lib.bch_sgemm_ex(dev.ctx, 1, m, n, k, C.c_void_p(tx.ptr), k, C.c_void_p(tw.ptr), k,
+                                       C.c_void_p(tbias.ptr), act, C.c_void_p(ty.ptr), n), "sgemm_ex")
+        ref = np.maximum(lin, 0.0) if act == 1 else O.gelu_f64(lin.astype(np.float32))
+        assert O.max_rel_err(ty.to_numpy(), ref) <= TOL, act
+
+
+def test_small_tiles_exact_on_integers_and_batched(dev):
+    """Small integers are exact in f32 whatever the order; batches of small shapes take the
+    same tiles (grid.y = batch)."""
+    rng = np.random.default_rng(23)
+    a = rng.integers(-8, 9, (512, 1024)).astype(np.float32)
+    b = rng.integers(-8, 9, (1024, 768)).astype(np.float32)
+    want = (a.astype(np.int64) @ b.astype(np.int64)).astype(np.float32)
+    assert np.array_equal(_mm(dev, a, b), want)
+    _say("batched small tiles 3x(192x320x256)")
+    r = O.Lcg(31)
+    ab, bb = r.uniform((3, 192, 256)), r.uniform((3, 256, 320))
+    ta, tb = Tensor.from_data(ab, [3, 192, 256], dev), Tensor.from_data(bb, [3, 256, 320], dev)
+    got = ta.batch_matmul(tb).to_numpy()
+    for i in range(3):
+        assert O.max_rel_err(got[i], ab[i].astype(np.float64) @ bb[i].astype(np.float64)) <= TOL, i
 
 
 HYBRID_CASES = [(3072, 3072, 1024, "sgemm_mfma_kernel<128,128,32,false,hyb>+sgemm_tail_reduce"),

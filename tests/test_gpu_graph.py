@@ -72,7 +72,7 @@ def test_graph_replays_match_eager(dev):
         ya = Tensor.empty([m, n], dev)
         calls.append((f"skinny m={m}", lambda m=m, n=n, k=k, xa=xa, wa=wa, ya=ya: lib.bch_sgemm(
             dev.ctx, m, n, k, C.c_void_p(xa.ptr), k, C.c_void_p(wa.ptr), n, C.c_void_p(ya.ptr), n), ya))
-    for m2, n2, k2 in ((3072, 3072, 1024), (1024, 1024, 1024)):  # hybrid, split-K
+    for m2, n2, k2 in ((3072, 3072, 1024), (1024, 1024, 4096), (512, 512, 512)):  # hybrid, split-K, 64x64 tiles
         xg, wg = _up(dev, rng.uniform((m2, k2))), _up(dev, rng.uniform((k2, n2)))
         yg = Tensor.empty([m2, n2], dev)
         calls.append((f"sgemm {m2}x{n2}x{k2} ({lib.bch_sgemm_kernel_name(m2, n2, k2).decode()})",
@@ -212,7 +212,7 @@ def test_reserve_then_capture_allocates_nothing(dev):
     _say("reserve, then global-mode capture of split-K GEMM, softmax over few long rows, wide attention")
     hip = _hip()
     rng = O.Lcg(78)
-    a, b = _up(dev, rng.uniform((1024, 1024))), _up(dev, rng.uniform((1024, 1024)))
+    a, b = _up(dev, rng.uniform((1024, 4096))), _up(dev, rng.uniform((4096, 1024)))
     c, c_ref = Tensor.empty([1024, 1024], dev), Tensor.empty([1024, 1024], dev)
     x = _up(dev, rng.normal((1, 1 << 20), 0.0, 3.0))
     y, y_ref = Tensor.empty([1, 1 << 20], dev), Tensor.empty([1, 1 << 20], dev)
@@ -221,7 +221,7 @@ def test_reserve_then_capture_allocates_nothing(dev):
     o, o_ref = Tensor.empty([B, H, S, D], dev), Tensor.empty([B, H, S, D], dev)
     P = lambda t: C.c_void_p(t.ptr)
     calls = [
-        lambda ctx, out: dev._lib.bch_sgemm(ctx, 1024, 1024, 1024, P(a), 1024, P(b), 1024, P(out), 1024),
+        lambda ctx, out: dev._lib.bch_sgemm(ctx, 1024, 1024, 4096, P(a), 4096, P(b), 1024, P(out), 1024),
         lambda ctx, out: dev._lib.bch_softmax_rows(ctx, 1, 1 << 20, P(x), P(out)),
         lambda ctx, out: dev._lib.bch_sdpa_fwd(ctx, B, H, S, S, D, C.c_float(D ** -0.5), 1, P(q), P(kk), P(v),
                                                P(out)),

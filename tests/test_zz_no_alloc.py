@@ -49,7 +49,7 @@ def _both(dev, m, n, k, seed):
     [(1, 11008, 4096), (20, 1000, 300)],
     [(256, 512, 384), (32, 256, 64)],
     # split-K (slices in the scratch, then the reduce), then a smaller split
-    [(1024, 1024, 1024), (96, 1024, 2048)],
+    [(1024, 1024, 4096), (96, 1024, 2048)],
     # the hybrid plan (16 MiB and 8.5 MiB of tail partials in the scratch)
     [(3072, 3072, 1024), (2304, 2304, 1024)],
 ])
@@ -136,7 +136,7 @@ def _hip():
     ("skinny split-k m=32 then m=8", [(32, 11008, 4096), (8, 3000, 1024)]),
     ("skinny fma m=1 then m=20", [(1, 11008, 4096), (20, 1000, 300)]),
     ("tiles (no scratch) then skinny", [(256, 512, 384), (32, 256, 64)]),
-    ("split-K then a smaller split", [(1024, 1024, 1024), (96, 1024, 2048)]),
+    ("split-K then a smaller split", [(1024, 1024, 4096), (96, 1024, 2048)]),
     ("hybrid plan then a smaller hybrid", [(3072, 3072, 1024), (2304, 2304, 1024)]),
 ])
 def test_noalloc_allocates_nothing_under_global_capture(dev, family, shapes):
