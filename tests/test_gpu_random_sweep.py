@@ -1,7 +1,7 @@
 """Seeded random parity sweep on the MI355X: shapes, leading dimensions, pointer offsets and
 layouts drawn at random for each hot-path entry point, against the f64 oracle.
 
-Entry points: bch_sgemm_ex, bch_sgemm_strided_batched, bch_sdpa_fwd_ex, bch_softmax_rows,
+Entry points: bch_sgemm_ex, bch_sgemm_strided_batched, bch_dgemm, bch_sdpa_fwd_ex, bch_softmax_rows,
 bch_softmax_axis, bch_layer_norm, bch_head_split and bch_head_concat.  The hand-picked tests
 pin each kernel path at its boundaries; this sweep draws the arguments
 those tests do not combine (odd leading dimensions with misaligned pointers, a transposed
@@ -70,11 +70,33 @@ def _gemm_cases(n_cases: int, seed: int):
                    bias=bool(rng.integers(0, 2)), act=int(rng.integers(0, 3)))
 
 
+def _gemm64_cases(n_cases: int, seed: int):
+    """Multiples of 64 up to 1024: the 64 x 64 x 64 tiles where the leading dimensions and
+    pointers allow, split-K or the usual tiles where they do not."""
+    rng = np.random.default_rng(seed)
+    for _ in range(n_cases):
+        yield dict(m=64 * int(rng.integers(1, 17)), n=64 * int(rng.integers(1, 17)), k=64 * int(rng.integers(1, 17)),
+                   transb=int(rng.integers(0, 2)), pa=int(rng.choice([0, 0, 4, 1])), pb=int(rng.choice([0, 0, 8, 3])),
+                   pc=int(rng.choice([0, 0, 4])), oa=int(rng.choice([0, 0, 0, 1])), ob=int(rng.choice([0, 0, 4])),
+                   oc=int(rng.choice([0, 0, 1])), bias=bool(rng.integers(0, 2)), act=int(rng.integers(0, 3)))
+
+
 @pytest.mark.parametrize("case", list(_gemm_cases(150, 2026)), ids=lambda c: "m{m}n{n}k{k}t{transb}".format(**c))
 def test_sgemm_ex_random(dev, case):
     """bch_sgemm_ex: C = act(A op(B) + bias) with padded leading dimensions and misaligned
     pointers, every kernel family (skinny, two-block skinny, tiles, split-K, hybrid)."""
-    _say(f"sgemm_ex random {case}")
+    _check_sgemm_ex(dev, case)
+
+
+@pytest.mark.parametrize("case", list(_gemm64_cases(40, 6464)), ids=lambda c: "m{m}n{n}k{k}t{transb}".format(**c))
+def test_sgemm_ex_random_multiples_of_64(dev, case):
+    """bch_sgemm_ex at shapes in multiples of 64 (the small tiles' domain) with the same
+    random padding, offsets, bias and activation."""
+    _check_sgemm_ex(dev, case)
+
+
+def _check_sgemm_ex(dev, case):
+    _say(f"sgemm_ex random {case} ({dev._lib.bch_sgemm_kernel_name(case['m'], case['n'], case['k']).decode()})")
     m, n, k, tb = case["m"], case["n"], case["k"], case["transb"]
     rng = np.random.default_rng(m * 1000003 + n * 1009 + k)
     lda, ldc = k + case["pa"], n + case["pc"]
@@ -104,6 +126,65 @@ def test_sgemm_ex_random(dev, case):
     assert O.max_rel_err(np.ascontiguousarray(got[:, :n]), ref) <= TOL
     assert np.all(got[:, n:] == -3.5), "padding columns of C written"
     assert Cb.guards_intact() and A.guards_intact() and B.guards_intact()
+
+
+def _dgemm_cases(n_cases: int, seed: int):
+    rng = np.random.default_rng(seed)
+    for _ in range(n_cases):
+        yield dict(batch=int(rng.integers(1, 4)), m=int(rng.choice([rng.integers(1, 140), 2 * rng.integers(64, 160)])),
+                   n=int(rng.choice([rng.integers(1, 140), 2 * rng.integers(64, 160)])),
+                   k=int(rng.choice([rng.integers(1, 64), 2 * rng.integers(32, 700)])),
+                   ta=int(rng.integers(0, 2)), tb=int(rng.integers(0, 2)), pa=int(rng.choice([0, 0, 2, 1])),
+                   pb=int(rng.choice([0, 0, 2, 3])), pc=int(rng.choice([0, 0, 1])), ga=int(rng.choice([0, 0, 2, 1])),
+                   gb=int(rng.choice([0, 0, 4])), gc=int(rng.choice([0, 0, 3])), oa=int(rng.choice([0, 0, 0, 1])),
+                   ob=int(rng.choice([0, 0, 2])), alpha=float(rng.choice([1.0, -0.75])),
+                   beta=float(rng.choice([0.0, 0.0, 1.5])))
+
+
+@pytest.mark.parametrize("case", list(_dgemm_cases(60, 6402)),
+                         ids=lambda c: "b{batch}m{m}n{n}k{k}t{ta}{tb}".format(**c))
+def test_dgemm_random(dev, case):
+    """bch_dgemm: C = alpha op(A) op(B) (+ beta C) with padded leading dimensions, gaps between
+    batches and operands 8 bytes off 16-byte alignment; the pair-guarded and scalar-guarded
+    tiles, split k.  Against a longdouble product within 1e-12; padding and the memory around C
+    are left alone."""
+    _say(f"dgemm random {case}")
+    from barracuda_amd import F64Buffer
+    bt, m, n, k, ta, tb = case["batch"], case["m"], case["n"], case["k"], case["ta"], case["tb"]
+    rng = np.random.default_rng(bt * 7 + m * 1009 + n * 31 + k + 2 * ta + tb)
+    ar, ac = (k, m) if ta else (m, k)  # stored A rows x cols
+    br, bc = (n, k) if tb else (k, n)
+    lda, ldb, ldc = ac + case["pa"], bc + case["pb"], n + case["pc"]
+    sA, sB, sC = ar * lda + case["ga"], br * ldb + case["gb"], m * ldc + case["gc"]
+    a = rng.uniform(-1, 1, (bt, ar, ac))
+    b = rng.uniform(-1, 1, (bt, br, bc))
+    c0 = rng.uniform(-1, 1, (bt, m, n))
+    A = np.full(case["oa"] + bt * sA + 8, 7.25)
+    B = np.full(case["ob"] + bt * sB + 8, 7.25)
+    Cb = np.full(bt * sC + 8, 7.25)
+    for z in range(bt):
+        A[case["oa"] + z * sA:case["oa"] + z * sA + ar * lda].reshape(ar, lda)[:, :ac] = a[z]
+        B[case["ob"] + z * sB:case["ob"] + z * sB + br * ldb].reshape(br, ldb)[:, :bc] = b[z]
+        Cb[z * sC:z * sC + m * ldc].reshape(m, ldc)[:, :n] = c0[z]
+    da, db, dc = (F64Buffer(dev, x.size).upload(x) for x in (A, B, Cb))
+    with dev._lock:
+        dev.check(dev._lib.bch_dgemm(dev.ctx, ta, tb, bt, m, n, k, case["alpha"], C.c_void_p(da.ptr + 8 * case["oa"]),
+                                     lda, sA, C.c_void_p(db.ptr + 8 * case["ob"]), ldb, sB, case["beta"],
+                                     C.c_void_p(dc.ptr), ldc, sC), "dgemm")
+    out = dc.to_vec()
+    for z in range(bt):
+        opa = a[z].astype(np.longdouble).T if ta else a[z].astype(np.longdouble)
+        opb = b[z].astype(np.longdouble).T if tb else b[z].astype(np.longdouble)
+        ref = case["alpha"] * (opa @ opb)
+        if case["beta"] != 0.0:
+            ref = ref + case["beta"] * c0[z].astype(np.longdouble)
+        blk = out[z * sC:z * sC + m * ldc].reshape(m, ldc)
+        err = float(np.max(np.abs(blk[:, :n] - ref.astype(np.float64)) / np.maximum(np.abs(ref.astype(np.float64)), 1.0)))
+        assert err <= 1e-12, (z, err)
+        keep = Cb[z * sC:z * sC + m * ldc].reshape(m, ldc)[:, n:]
+        assert np.array_equal(blk[:, n:], keep), "padding columns of C written"
+        assert np.all(out[z * sC + m * ldc:(z + 1) * sC] == 7.25), "gap between batches written"
+    assert np.all(out[bt * sC:] == 7.25), "memory after C written"
 
 
 def _batched_cases(n_cases: int, seed: int):
