@@ -734,14 +734,17 @@ int split_slices(int batch, int m, int n, int k, size_t cap = kSplitWsMax, doubl
 // MFMA block; k-tiles of 64 so that a tile's loads split evenly over the 256 threads) put 16x
 // the workgroups of the 128 x 128 tiling on the CUs, with no k split, partials or reduce
 // launch.  A 64 x 64 x 64 k-tile takes ~1.32 us at any count of tiles up to a round (256^3 to
-// 1024^3; 63% of the matrix cores' rate, against 92% for 128 x 128).  Taken when its modelled
-// time, rounds x k-tiles x 1.32 us, is under 0.9 of the split-K plan's; unguarded loads only
-// (m, n, k multiples of 64, aligned operands), else the usual path.  Same box, two runs each,
-// against the split-K plan: 256^3 19.4 -> 8.8 us, 512^3 23.0 -> 13.9, 768^3 25.8 -> 19.3,
-// 1024^3 28.3 -> 24.4; where split-K stays ahead the model keeps it (1024 x 1024 x 4096 74
-// against 89 us, 512 x 1024 x 2048 28.7 against 46.9).
+// 1024^3; 63% of the matrix cores' rate, against 92% for 128 x 128); two workgroups share a CU
+// (70 KB of LDS each) at ~2.29 us per k-tile of both.  Taken when its modelled time, rounds x
+// k-tiles x that time, is under 0.9 of the split-K plan's; unguarded loads only (m, n, k
+// multiples of 64, aligned operands), else the usual path.  Same box, two runs each, against
+// the split-K plan: 256^3 19.4 -> 8.8 us, 512^3 23.0 -> 13.9, 768^3 25.8 -> 19.3, 1024^3 28.3
+// -> 24.4, 1024 x 2048 x 1024 43.9 -> 40.1 (two per CU); where split-K stays ahead the model
+// keeps it (1024 x 1024 x 4096 74 against 89 us, 1024 x 1024 x 2048 43.5 against 47.6, 512 x
+// 1024 x 2048 28.7 against 46.9).
 constexpr int kSmallBK = 64;
-constexpr double kSmallKtUs = 1.32;
+constexpr double kSmallKtUs = 1.32;   // one workgroup per CU
+constexpr double kSmallKt2Us = 2.29;  // two per CU, both k-tiles
 
 bool small_tile_plan(int batch, int m, int n, int k) {
   if (batch < 1 || m % 64 != 0 || n % 64 != 0 || k <= 0 || k % kSmallBK != 0) return false;
@@ -753,7 +756,9 @@ bool small_tile_plan(int batch, int m, int n, int k) {
   double cur = 0.0;
   split_slices(batch, m, n, k, kSplitWsMax, &cur);
   const long long t64 = (long long)batch * (m / 64) * (n / 64);
-  return (double)((t64 + cu - 1) / cu) * (k / kSmallBK) * kSmallKtUs < 0.9 * cur;
+  const double nk = k / kSmallBK;
+  const double small = t64 <= cu ? nk * kSmallKtUs : (double)((t64 + 2 * cu - 1) / (2 * cu)) * nk * kSmallKt2Us;
+  return small < 0.9 * cur;
 }
 
 bool small_tile_ok(int batch, int m, int n, int k, const float* A, int lda, long long sA, const float* B, int ldb,

@@ -290,7 +290,7 @@ def test_split_k_exact_on_integers(dev):
 
 # 64 x 64 x 64 tiles: shapes whose usual tiles fill less than one round and whose k is short
 SMALL_CASES = [(128, 128, 128), (256, 256, 256), (192, 320, 256), (128, 1024, 512), (512, 512, 512), (768, 768, 768),
-               (1024, 1024, 1024)]
+               (1024, 1024, 1024), (1024, 2048, 1024)]
 
 
 @pytest.mark.parametrize("m,n,k", SMALL_CASES)
@@ -514,7 +514,7 @@ def test_config_batched_16x1024(dev):
     assert O.max_rel_err(single, got[3].astype(np.float64)) <= TOL
 
 
-@pytest.mark.parametrize("batch,m,n,k", [(2, 1024, 1024, 1024), (4, 512, 512, 4096), (8, 256, 256, 8192),
+@pytest.mark.parametrize("batch,m,n,k", [(2, 1024, 1024, 2048), (4, 512, 512, 4096), (8, 256, 256, 8192),
                                          (3, 300, 200, 2048), (5, 130, 260, 1024)])
 def test_batched_split_k(dev, batch, m, n, k):
     """Batches whose tiles together fill less than one round of the CUs split over k too
