@@ -19,7 +19,9 @@
 //     B as well, B tiles are stored k-contiguous ([n][k]) in LDS: each thread
 //     loads a 4(k) x 4(n) block with four 128-bit global loads and writes it
 //     transposed with four 128-bit LDS stores, the lanes of a store phase
-//     covering one LDS row.
+//     covering one LDS row.  The unguarded 256-row tiles instead keep B
+//     row-major in LDS and read each lane's four k as four 32-bit values
+//     (BROW in the kernel).
 //   * Block tile BM x BN x BK (256x256, 256x128 or 128x128 by shape, see
 //     pick_tile), four wavefronts in a 2x2 grid, each owning a (BM/2) x (BN/2)
 //     sub-tile of (BM/64) x (BN/64) MFMA blocks.  LDS rows
@@ -189,6 +191,21 @@ __global__ __launch_bounds__(kThreads) void sgemm_mfma_kernel(
   //    they wrote rows 4 apart, 16-way conflicted (measured: 130.5 vs 134.3
   //    TFLOP/s at 4096^3).  A global load still covers whole 128-byte lines.
   constexpr int B_KQ = BK / 4;
+  // BROW (unguarded [K][N] B, 256-row tiles): B is kept row-major in LDS ([k][LDN], rows
+  // copied with 128-bit loads and stores like A) and its fragments are read as four 32-bit
+  // values per block.  The 4 x 4 transpose through registers it replaces left the staged
+  // registers permuted across the loop's back edge, so every iteration ended copying them
+  // behind a wait for all of the next tile's loads.  Same box, two runs each, TFLOP/s: 4096^3
+  // 145.4 -> 147.1, 16 x 1024^3 batched 135.7 -> 138.5, 8192 x 8192 x 2048 144.2 -> 145.8,
+  // 4096 x 4096 x 1024 138.2 -> 139.3, 3072^3 (256 x 128 tiles) 137.0 -> 137.8; the 128 x 128
+  // tile, with 16 MFMAs a chunk for its 8 extra LDS reads, lost (2048 x 2048 x 4096 136.1 ->
+  // 121.5) and keeps the transpose.
+  constexpr bool BROW = !TB && !CHECK && BM == 256;
+  constexpr int LDN = BN + 4;                   // padded [k] row of B (floats)
+  constexpr int B_TPR = BN / 4;                 // threads per B row
+  constexpr int B_RSTEP = kThreads / B_TPR;     // B rows per float4 round
+  static_assert(!BROW || (BK * LDN <= BN * LDK && 4 * G::B_BLK * B_RSTEP == BK), "B row layout");
+  const int b_r = tid / B_TPR, b_c = (tid % B_TPR) * 4;
 
   float4 ra[G::A_F4];
   float4 rb[G::B_BLK][4];  // TB: rb[q][e] is float4 number 4q + e of the [n][k] tile rows
@@ -279,6 +296,10 @@ __global__ __launch_bounds__(kThreads) void sgemm_mfma_kernel(
           rb[f >> 2][f & 3] = make_float4(t[0], t[1], t[2], t[3]);
         }
       }
+    } else if constexpr (BROW) {
+#pragma unroll
+      for (int f = 0; f < 4 * G::B_BLK; ++f)
+        rb[f >> 2][f & 3] = ld4(B + (long long)(k0 + b_r + f * B_RSTEP) * ldb + n0 + b_c);
     } else {
 #pragma unroll
       for (int q = 0; q < G::B_BLK; ++q) {
@@ -319,6 +340,12 @@ __global__ __launch_bounds__(kThreads) void sgemm_mfma_kernel(
       }
       return;
     }
+    if constexpr (BROW) {
+#pragma unroll
+      for (int f = 0; f < 4 * G::B_BLK; ++f)
+        *reinterpret_cast<float4*>(bs + (b_r + f * B_RSTEP) * LDN + b_c) = rb[f >> 2][f & 3];
+      return;
+    }
 #pragma unroll
     for (int q = 0; q < G::B_BLK; ++q) {
       const int blk = tid + q * kThreads;
@@ -356,11 +383,19 @@ __global__ __launch_bounds__(kThreads) void sgemm_mfma_kernel(
   float4 fa[2][G::TM], fb[2][G::TN];
   auto read_frags = [&](int buf, int c, float4 (&a)[G::TM], float4 (&b)[G::TN]) {
     const float* as = As + buf * BM * LDK + (wm + li) * LDK + 4 * lh + 8 * c;
-    const float* bs = Bs + buf * BN * LDK + (wn + li) * LDK + 4 * lh + 8 * c;
 #pragma unroll
     for (int i = 0; i < G::TM; ++i) a[i] = *reinterpret_cast<const float4*>(as + i * 32 * LDK);
+    if constexpr (BROW) {
+      // B[k = 8c + 4lh + s][n = wn + 32j + li], s = 0..3: four rows of the [k][n] tile
+      const float* bs = Bs + buf * BN * LDK + (8 * c + 4 * lh) * LDN + wn + li;
 #pragma unroll
-    for (int j = 0; j < G::TN; ++j) b[j] = *reinterpret_cast<const float4*>(bs + j * 32 * LDK);
+      for (int j = 0; j < G::TN; ++j)
+        b[j] = make_float4(bs[j * 32], bs[LDN + j * 32], bs[2 * LDN + j * 32], bs[3 * LDN + j * 32]);
+    } else {
+      const float* bs = Bs + buf * BN * LDK + (wn + li) * LDK + 4 * lh + 8 * c;
+#pragma unroll
+      for (int j = 0; j < G::TN; ++j) b[j] = *reinterpret_cast<const float4*>(bs + j * 32 * LDK);
+    }
   };
   auto mfma_chunk = [&](const float4 (&a)[G::TM], const float4 (&b)[G::TN]) {
 #pragma unroll
@@ -395,7 +430,7 @@ __global__ __launch_bounds__(kThreads) void sgemm_mfma_kernel(
   // The order is pinned with scheduling groups (mask 0x008 MFMA, 0x100 LDS
   // read, 0x200 LDS write): left alone, the scheduler sank the global loads
   // to the end of the body behind a vmcnt(0) and clustered the LDS traffic.
-  constexpr int NR = G::TM + G::TN;                        // LDS reads per chunk
+  constexpr int NR = G::TM + (BROW ? 4 : 1) * G::TN;       // LDS reads per chunk
   constexpr int NW = G::A_F4 + 4 * G::B_BLK;               // LDS stores per tile
   constexpr int NM = 4 * G::TM * G::TN;                    // MFMAs per chunk
   // the small tile (one MFMA block per wavefront) has too few MFMAs in a chunk to pin its
