@@ -26,7 +26,14 @@
 //     [n][k]) is copied row by row (8 lanes x 16 bytes per 128-byte row);
 //     one whose rows run along m or n (B [k][n], or A^T stored [k][m]) is
 //     loaded as 2 x 2 blocks and written transposed, the 8 lanes of a store
-//     phase covering one LDS row (no bank conflicts).
+//     phase covering one LDS row (no bank conflicts) -- except on the
+//     unguarded path, where B [k][n] (and A^T beside it) stays [k][rows] in
+//     LDS and a fragment's two k are read as one ds_read2_b64.  The
+//     transpose through registers left the staged registers permuted across
+//     the loop's back edge, and every iteration ended copying them into
+//     place behind a wait for all of the next tile's loads.  4096^3 NN
+//     72.5-72.9 -> 73.9-74.0 TFLOP/s, TN 71.2-71.5 -> 74.1-74.2, 2048^3
+//     69.0 -> 71.2 (one box, two runs each).
 //   * Software pipeline: a k-tile's fragments are read in two halves, the
 //     second half of tile t under the MFMAs of its first two steps and the
 //     first half of tile t + 1 (after the one barrier per tile) under its
@@ -154,6 +161,29 @@ __device__ __forceinline__ void store_dtile(double* __restrict__ s, int tid, con
   }
 }
 
+// An unguarded operand stored [k][rows] (B as [k][n], or A^T as [k][m]) is kept the same
+// way in LDS, [16][ROWS + 2] doubles: rows of the tile copied with 128-bit loads and stores,
+// ROWS / 2 threads per k row.  Its fragments are then read as two 64-bit values (k and k + 1)
+// instead of one 128-bit read of a transposed tile.
+template <int ROWS>
+__device__ __forceinline__ void load_krow(const double* __restrict__ X, int ld, int r0, int k0, int tid,
+                                          d2 (&reg)[ROWS / 32]) {
+  constexpr int TPR = ROWS / 2, RSTEP = kDT / TPR;
+  const int kr = tid / TPR, c = 2 * (tid % TPR);
+  const double* base = X + (long long)(k0 + kr) * ld + r0 + c;
+  const long long step = (long long)RSTEP * ld;  // wave-uniform
+#pragma unroll
+  for (int f = 0; f < ROWS / 32; ++f) reg[f] = ld2(base + f * step);
+}
+
+template <int ROWS>
+__device__ __forceinline__ void store_krow(double* __restrict__ s, int tid, const d2 (&reg)[ROWS / 32]) {
+  constexpr int TPR = ROWS / 2, RSTEP = kDT / TPR;
+  const int kr = tid / TPR, c = 2 * (tid % TPR);
+#pragma unroll
+  for (int f = 0; f < ROWS / 32; ++f) *reinterpret_cast<d2*>(s + (kr + f * RSTEP) * (ROWS + 2) + c) = reg[f];
+}
+
 // BM x BN block tile (2 x 2 waves of (BM/2) x (BN/2), TM x TN MFMA blocks each);
 // OCC workgroups per CU.
 // grid.y = batch * nsplit; with nsplit > 1 the workgroup covers k in
@@ -215,13 +245,39 @@ __global__ __launch_bounds__(kDT, OCC) void dgemm_mfma_kernel(
   const int nk = (kend - kbeg + kDBK - 1) / kDBK;
   const int lastk = kbeg + (nk - 1) * kDBK;
   d2 a[TM][2], b[TN][2];
+  constexpr bool AROW = TA && !TB && !CHECK, BROW = !TB && !CHECK;
+  static_assert(16 * (BM + 2) <= BM * kDLDK && 16 * (BN + 2) <= BN * kDLDK, "k-row tiles fit the buffers");
   auto read_half = [&](int buf, int h) {
-    const double* as = As[buf] + (wm + li) * kDLDK + 4 * lq + 2 * h;
-    const double* bs = Bs[buf] + (wn + li) * kDLDK + 4 * lq + 2 * h;
+    if constexpr (AROW) {
+      const double* as = As[buf] + (4 * lq + 2 * h) * (BM + 2) + wm + li;
 #pragma unroll
-    for (int i = 0; i < TM; ++i) a[i][h] = *reinterpret_cast<const d2*>(as + i * 16 * kDLDK);
+      for (int i = 0; i < TM; ++i) a[i][h] = d2{as[16 * i], as[BM + 2 + 16 * i]};
+    } else {
+      const double* as = As[buf] + (wm + li) * kDLDK + 4 * lq + 2 * h;
 #pragma unroll
-    for (int j = 0; j < TN; ++j) b[j][h] = *reinterpret_cast<const d2*>(bs + j * 16 * kDLDK);
+      for (int i = 0; i < TM; ++i) a[i][h] = *reinterpret_cast<const d2*>(as + i * 16 * kDLDK);
+    }
+    if constexpr (BROW) {
+      const double* bs = Bs[buf] + (4 * lq + 2 * h) * (BN + 2) + wn + li;
+#pragma unroll
+      for (int j = 0; j < TN; ++j) b[j][h] = d2{bs[16 * j], bs[BN + 2 + 16 * j]};
+    } else {
+      const double* bs = Bs[buf] + (wn + li) * kDLDK + 4 * lq + 2 * h;
+#pragma unroll
+      for (int j = 0; j < TN; ++j) b[j][h] = *reinterpret_cast<const d2*>(bs + j * 16 * kDLDK);
+    }
+  };
+  auto load_tiles = [&](int k0) {
+    if constexpr (AROW) load_krow<BM>(A, lda, m0, k0, tid, ra);
+    else load_dtile<BM, !TA, CHECK, V2>(A, rsa, lda, M, kend, m0, k0, tid, ra);
+    if constexpr (BROW) load_krow<BN>(B, ldb, n0, k0, tid, rb);
+    else load_dtile<BN, TB, CHECK, V2>(B, rsb, ldb, N, kend, n0, k0, tid, rb);
+  };
+  auto store_tiles = [&](int buf) {
+    if constexpr (AROW) store_krow<BM>(As[buf], tid, ra);
+    else store_dtile<BM, !TA>(As[buf], tid, ra);
+    if constexpr (BROW) store_krow<BN>(Bs[buf], tid, rb);
+    else store_dtile<BN, TB>(Bs[buf], tid, rb);
   };
   auto mfma_half = [&](int h) {
     // step s = 2h + e uses k = 4 lq + s
@@ -237,30 +293,44 @@ __global__ __launch_bounds__(kDT, OCC) void dgemm_mfma_kernel(
         }
       }
   };
-  constexpr int NR = TM + TN;        // LDS reads per half
-  constexpr int NM = 2 * TM * TN;    // MFMAs per half
+  // LDS reads per half: one per block either way (a k-row operand's two 64-bit values, 130 or
+  // more doubles apart, are one ds_read2_b64)
+  constexpr int NR = TM + TN;
+  constexpr int NM = 2 * TM * TN;                                 // MFMAs per half
   static_assert(NM >= 2 * NR, "half tile too small to cover its reads");
 
   if (nk > 0) {
-    load_dtile<BM, !TA, CHECK, V2>(A, rsa, lda, M, kend, m0, kbeg, tid, ra);
-    load_dtile<BN, TB, CHECK, V2>(B, rsb, ldb, N, kend, n0, kbeg, tid, rb);
-    store_dtile<BM, !TA>(As[0], tid, ra);
-    store_dtile<BN, TB>(Bs[0], tid, rb);
-    load_dtile<BM, !TA, CHECK, V2>(A, rsa, lda, M, kend, m0, min(kbeg + kDBK, lastk), tid, ra);
-    load_dtile<BN, TB, CHECK, V2>(B, rsb, ldb, N, kend, n0, min(kbeg + kDBK, lastk), tid, rb);
+    if constexpr (AROW || BROW) {
+      load_tiles(kbeg);
+      store_tiles(0);
+      load_tiles(min(kbeg + kDBK, lastk));
+    } else {
+      load_dtile<BM, !TA, CHECK, V2>(A, rsa, lda, M, kend, m0, kbeg, tid, ra);
+      load_dtile<BN, TB, CHECK, V2>(B, rsb, ldb, N, kend, n0, kbeg, tid, rb);
+      store_dtile<BM, !TA>(As[0], tid, ra);
+      store_dtile<BN, TB>(Bs[0], tid, rb);
+      load_dtile<BM, !TA, CHECK, V2>(A, rsa, lda, M, kend, m0, min(kbeg + kDBK, lastk), tid, ra);
+      load_dtile<BN, TB, CHECK, V2>(B, rsb, ldb, N, kend, n0, min(kbeg + kDBK, lastk), tid, rb);
+    }
   }
   __syncthreads();
   if (nk > 0) read_half(0, 0);
 
   constexpr int NW = BM / 32 + BN / 32;  // LDS stores (= 128-bit global loads) per thread per tile
-  static_assert(NM >= 2 * NR + 2 * NW, "half tile too small to cover its reads, stores and loads");
+  constexpr int RM = NM >= 2 * NR + 2 * NW ? 2 : 1;  // MFMAs after each read in phase 0
+  static_assert(NM >= RM * NR + 2 * NW, "half tile too small to cover its reads, stores and loads");
   for (int t = 0; t < nk; ++t) {
     const int cur = t & 1;
     read_half(cur, 1);
-    store_dtile<BM, !TA>(As[cur ^ 1], tid, ra);
-    store_dtile<BN, TB>(Bs[cur ^ 1], tid, rb);
-    load_dtile<BM, !TA, CHECK, V2>(A, rsa, lda, M, kend, m0, min(kbeg + (t + 2) * kDBK, lastk), tid, ra);
-    load_dtile<BN, TB, CHECK, V2>(B, rsb, ldb, N, kend, n0, min(kbeg + (t + 2) * kDBK, lastk), tid, rb);
+    if constexpr (AROW || BROW) {
+      store_tiles(cur ^ 1);
+      load_tiles(min(kbeg + (t + 2) * kDBK, lastk));
+    } else {
+      store_dtile<BM, !TA>(As[cur ^ 1], tid, ra);
+      store_dtile<BN, TB>(Bs[cur ^ 1], tid, rb);
+      load_dtile<BM, !TA, CHECK, V2>(A, rsa, lda, M, kend, m0, min(kbeg + (t + 2) * kDBK, lastk), tid, ra);
+      load_dtile<BN, TB, CHECK, V2>(B, rsb, ldb, N, kend, n0, min(kbeg + (t + 2) * kDBK, lastk), tid, rb);
+    }
     mfma_half(0);
     // Phase 0 order: the second-half reads of tile t, one per 2 MFMAs, then
     // the LDS stores of tile t + 1 and the global loads of tile t + 2, a
@@ -269,7 +339,7 @@ __global__ __launch_bounds__(kDT, OCC) void dgemm_mfma_kernel(
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, RM, 0);
     }
 #pragma unroll
     for (int r = 0; r < NW; ++r) {
@@ -277,7 +347,7 @@ __global__ __launch_bounds__(kDT, OCC) void dgemm_mfma_kernel(
       __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
     }
-    if (NM > 2 * NR + 2 * NW) __builtin_amdgcn_sched_group_barrier(0x008, NM - 2 * NR - 2 * NW, 0);
+    if (NM > RM * NR + 2 * NW) __builtin_amdgcn_sched_group_barrier(0x008, NM - RM * NR - 2 * NW, 0);
     __builtin_amdgcn_sched_barrier(0);
     __syncthreads();
     read_half(cur ^ 1, 0);
