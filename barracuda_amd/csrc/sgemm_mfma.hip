@@ -49,7 +49,8 @@
 //     round-robin over 8 XCDs, so consecutive workgroup ids are remapped to
 //     one XCD's contiguous range of tiles, then walked in groups of 8 tile
 //     rows so concurrently running tiles share A and B panels in that
-//     XCD's L2.
+//     XCD's L2.  A batched launch gives each XCD a contiguous run of
+//     (batch, tile) slots, i.e. whole batches where they divide the run.
 //   * CHECK=false needs m % BM == 0, n % BN == 0, k % BK == 0, lda/ldb/
 //     strides multiples of 4 and 16-byte aligned A/B; CHECK=true guards
 //     every load (zero fill) and store and handles any shape and alignment.
@@ -121,11 +122,32 @@ __global__ __launch_bounds__(kThreads) void sgemm_mfma_kernel(
   // ---- tile mapping (XCD-aware, grouped) ----
   const int ntiles = tiles_m * tiles_n;
   int p = blockIdx.x;
+  long long bz = blockIdx.y;
+  bool by_xcd = false;  // batches: (batch, tile) slots remapped XCD-contiguously
+  if constexpr (!HY && !CHECK) {
+    // Workgroups are dispatched round-robin over the 8 XCDs in linear id order (x fastest), so
+    // a batch's tiles were spread over all eight L2s.  Each XCD takes a contiguous run of the
+    // (batch, tile) slots instead: whole batches where a batch's tiles divide the run, each
+    // batch's A and B then read into one L2.  Same box, three runs each (us): 16 x 1024^3
+    // 248.5-251.0 -> 246.9-247.3, 8 x 1024^3 130.3-130.8 -> 127.4-127.8, 24 x 1024^3
+    // 388-399 -> 381-383, 64 x 512^3 135.1-136.0 -> 132.4-133.1, 32 x 1024 x 1024 x 512 +0.9%,
+    // 4 x 2048 x 2048 x 1024 +1%, 16 x 1024 x 1024 x 4096 unchanged.  Unguarded loads only: in
+    // the float4-guarded 256 x 256 instantiations it doubled the k-loop's code and moved its
+    // load waits.
+    const long long slots = (long long)gridDim.x * gridDim.y;
+    if (gridDim.y > 1 && gridDim.z == 1 && (slots & 7) == 0) {
+      const long long L = (long long)blockIdx.y * gridDim.x + blockIdx.x;
+      const long long q = (L & 7) * (slots >> 3) + (L >> 3);
+      bz = q / gridDim.x;
+      p = (int)(q - bz * gridDim.x);
+      by_xcd = true;
+    }
+  }
   int lt = p;
   bool tail = false;  // HY: this workgroup computes one k-slice of one of the last hy_r tiles
   int hy_slot = 0, hy_slice = 0;
   if constexpr (!HY) {
-    if ((ntiles & 7) == 0) lt = (p & 7) * (ntiles >> 3) + (p >> 3);
+    if ((ntiles & 7) == 0 && !by_xcd) lt = (p & 7) * (ntiles >> 3) + (p >> 3);
   } else {
     // whole tiles 0 .. hy_ndp - 1 first (hy_ndp fills whole rounds), XCD-contiguous; then
     // the k-slices of tiles hy_ndp .. hy_ndp + hy_r - 1, slice-major and XCD-contiguous,
@@ -152,7 +174,6 @@ __global__ __launch_bounds__(kThreads) void sgemm_mfma_kernel(
   const int tile_n = within / gm;
   const int m0 = tile_m * BM, n0 = tile_n * BN;
 
-  const long long bz = blockIdx.y;
   A += bz * sA;
   B += bz * sB;
   C += bz * sC;

@@ -514,6 +514,30 @@ def test_config_batched_16x1024(dev):
     assert O.max_rel_err(single, got[3].astype(np.float64)) <= TOL
 
 
+@pytest.mark.parametrize("batch,m,n,k", [(20, 1024, 1024, 256), (72, 512, 512, 64), (24, 1024, 768, 128)])
+def test_batched_xcd_runs(dev, batch, m, n, k):
+    """Batched launches whose (batch, tile) slots are handed to the XCDs in contiguous runs
+    (2.5 batches a run at 20 x 16 tiles, 9 at 72 x 4, and 24 x 12 tiles): every tile of every
+    batch against f64 (one row per 256-row tile and one column per 256-column tile, at positions
+    that move with the batch), and the batches in reverse order reproduce them bit for bit."""
+    _say(f"batched xcd runs {batch}x{m}x{n}x{k}")
+    rng = O.Lcg(batch * 7 + m + n + k)
+    a = rng.uniform((batch, m, k))
+    b = rng.uniform((batch, k, n))
+    ta, tb = Tensor.from_data(a, [batch, m, k], dev), Tensor.from_data(b, [batch, k, n], dev)
+    got = ta.batch_matmul(tb).to_numpy()
+    for bi in range(batch):
+        rows = sorted({t * 256 + (bi * 37 + t * 101) % 256 for t in range(m // 256)} | {(bi * 13) % m})
+        cols = sorted({t * 256 + (bi * 53 + t * 29) % 256 for t in range(n // 256)} | {(bi * 7) % n})
+        ab, bb = np.ascontiguousarray(a[bi]), np.ascontiguousarray(b[bi])
+        err = O.max_rel_err(got[bi][rows], O.matmul_f64(ab, bb, rows=rows))
+        errc = O.max_rel_err(got[bi][:, cols], ab.astype(np.float64) @ bb[:, cols].astype(np.float64))
+        assert err <= TOL and errc <= TOL, (bi, err, errc)
+    a2, b2 = np.ascontiguousarray(a[::-1]), np.ascontiguousarray(b[::-1])
+    rev = Tensor.from_data(a2, [batch, m, k], dev).batch_matmul(Tensor.from_data(b2, [batch, k, n], dev)).to_numpy()
+    assert all(np.array_equal(rev[batch - 1 - i], got[i]) for i in range(batch))
+
+
 @pytest.mark.parametrize("batch,m,n,k", [(2, 1024, 1024, 2048), (4, 512, 512, 4096), (8, 256, 256, 8192),
                                          (3, 300, 200, 2048), (5, 130, 260, 1024)])
 def test_batched_split_k(dev, batch, m, n, k):
