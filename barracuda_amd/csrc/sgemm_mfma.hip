@@ -220,7 +220,10 @@ __global__ __launch_bounds__(kThreads) void sgemm_mfma_kernel(
   // 145.4 -> 147.1, 16 x 1024^3 batched 135.7 -> 138.5, 8192 x 8192 x 2048 144.2 -> 145.8,
   // 4096 x 4096 x 1024 138.2 -> 139.3, 3072^3 (256 x 128 tiles) 137.0 -> 137.8; the 128 x 128
   // tile, with 16 MFMAs a chunk for its 8 extra LDS reads, lost (2048 x 2048 x 4096 136.1 ->
-  // 121.5) and keeps the transpose.
+  // 121.5) and keeps the transpose.  (The compiler pairs those reads into ds_read2_b32; with the
+  // scheduling groups counting the pairs its loop waits only for the previous tile's loads, and
+  // it measured even: 128 x 11008 x 4096 109.2-110.3 -> 108.2 us, 2048 x 2048 x 4096 250.2 ->
+  // 252.8, 2048 x 2048 x 1024 68.9 -> 68.3, 1024 x 1024 x 4096 unchanged.)
   constexpr bool BROW = !TB && !CHECK && BM == 256;
   constexpr int LDN = BN + 4;                   // padded [k] row of B (floats)
   constexpr int B_TPR = BN / 4;                 // threads per B row
