@@ -133,7 +133,8 @@ __global__ __launch_bounds__(kThreads) void sgemm_mfma_kernel(
     // 388-399 -> 381-383, 64 x 512^3 135.1-136.0 -> 132.4-133.1, 32 x 1024 x 1024 x 512 +0.9%,
     // 4 x 2048 x 2048 x 1024 +1%, 16 x 1024 x 1024 x 4096 unchanged.  Unguarded loads only: in
     // the float4-guarded 256 x 256 instantiations it doubled the k-loop's code and moved its
-    // load waits.
+    // load waits.  Split-K grids (slices in z) keep the dispatch order: remapped the same way
+    // they measured even or slower (1024 x 1024 x 2048 43.3-43.6 -> 44.3-44.4 us).
     const long long slots = (long long)gridDim.x * gridDim.y;
     if (gridDim.y > 1 && gridDim.z == 1 && (slots & 7) == 0) {
       const long long L = (long long)blockIdx.y * gridDim.x + blockIdx.x;
