@@ -31,8 +31,8 @@
  *                        tolerances, exactness on integer-valued inputs, and
  *                        order-sensitivity probes that a transposed operand
  *                        or dropped term fails.
- *   inline handlers   -- (section 5, f64 ml.attention and
- *                        tensor.matmul_inline) the handler tests' vectors
+ *   inline handlers   -- (the f64 ml.attention and
+ *                        tensor.matmul_inline handlers) the handler tests' vectors
  *                        (ml_tests.rs:128-165, sprint56b_tests.rs:618-669),
  *                        closed forms (one key -> its V row, equal scores ->
  *                        the mean of V, the one-hot case), numpy longdouble

@@ -30,8 +30,8 @@ def test_library_exports_every_header_symbol():
 
 
 def test_rust_binding_in_integration_doc_matches_header():
-    """The barracuda-hip-sys block a maintainer would paste declares exactly the
-    header's functions and status codes."""
+    """The barracuda-hip-sys block a maintainer would paste (the integration guide at the
+    repository root) declares exactly the header's functions and status codes."""
     import re
     from pathlib import Path
     root = Path(__file__).resolve().parents[1]
