@@ -514,12 +514,14 @@ def test_config_batched_16x1024(dev):
     assert O.max_rel_err(single, got[3].astype(np.float64)) <= TOL
 
 
-@pytest.mark.parametrize("batch,m,n,k", [(20, 1024, 1024, 256), (72, 512, 512, 64), (24, 1024, 768, 128)])
+@pytest.mark.parametrize("batch,m,n,k", [(20, 1024, 1024, 256), (72, 512, 512, 64), (24, 1024, 768, 128),
+                                         (8, 192, 320, 256)])
 def test_batched_xcd_runs(dev, batch, m, n, k):
     """Batched launches whose (batch, tile) slots are handed to the XCDs in contiguous runs
-    (2.5 batches a run at 20 x 16 tiles, 9 at 72 x 4, and 24 x 12 tiles): every tile of every
-    batch against f64 (one row per 256-row tile and one column per 256-column tile, at positions
-    that move with the batch), and the batches in reverse order reproduce them bit for bit."""
+    (2.5 batches a run at 20 x 16 tiles, 9 at 72 x 4, 24 x 12 tiles, and the 64 x 64 tiles at
+    8 x 15): every tile of every batch against f64 (one row per 256-row tile and one column per
+    256-column tile, at positions that move with the batch; every element below 256 rows), and
+    the batches in reverse order reproduce them bit for bit."""
     _say(f"batched xcd runs {batch}x{m}x{n}x{k}")
     rng = O.Lcg(batch * 7 + m + n + k)
     a = rng.uniform((batch, m, k))
@@ -529,6 +531,8 @@ def test_batched_xcd_runs(dev, batch, m, n, k):
     for bi in range(batch):
         rows = sorted({t * 256 + (bi * 37 + t * 101) % 256 for t in range(m // 256)} | {(bi * 13) % m})
         cols = sorted({t * 256 + (bi * 53 + t * 29) % 256 for t in range(n // 256)} | {(bi * 7) % n})
+        if m < 256:
+            rows = list(range(m))
         ab, bb = np.ascontiguousarray(a[bi]), np.ascontiguousarray(b[bi])
         err = O.max_rel_err(got[bi][rows], O.matmul_f64(ab, bb, rows=rows))
         errc = O.max_rel_err(got[bi][:, cols], ab.astype(np.float64) @ bb[:, cols].astype(np.float64))
