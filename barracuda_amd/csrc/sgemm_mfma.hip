@@ -24,7 +24,8 @@
 //     (BROW in the kernel).
 //   * Block tile BM x BN x BK (256x256, 256x128 or 128x128 by shape, see
 //     pick_tile), four wavefronts in a 2x2 grid, each owning a (BM/2) x (BN/2)
-//     sub-tile of (BM/64) x (BN/64) MFMA blocks.  LDS rows
+//     sub-tile of (BM/64) x (BN/64) MFMA blocks (the 256x256 tile with the
+//     bias and activation epilogue: eight wavefronts, 2 x 4).  LDS rows
 //     are padded by 4 floats so the 128-bit reads of 32 consecutive rows do
 //     not collide on banks.  LDS is double-buffered, with one register set
 //     staging the global loads: tile t + 1 goes from registers to the other
@@ -78,20 +79,29 @@ namespace {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int kThreads = 256;
 
-template <int BM, int BN, int BK>
+// W8: eight wavefronts (2 x 4, each (BM/2) x (BN/4)) instead of four, two per SIMD.  Taken by the
+// 256x256 tile with the bias and activation epilogue, where a SIMD's second wavefront overlaps
+// the epilogue's VALU work.  Same box, two runs each (us, 4 -> 8 wavefronts, [out, in] weights
+// with bias): GELU 4096^3 951.6 -> 940.0-940.5, 8192 x 4096 x 4096 1895-1897 -> 1873-1874,
+// 4096 x 11008 x 4096 2630-2631 -> 2603-2607, 6144^3 3164-3165 -> 3144-3145, 4000^3 (float4
+// guards) 941-942 -> 917-918; ReLU 4000^3 922-924 -> 904-905, the others within 0.3%.  Without
+// an epilogue the 256x256 tile stays on four wavefronts: eight took 4096^3 146.5 -> 144.8
+// TFLOP/s.
+template <int BM, int BN, int BK, bool W8 = false>
 struct Cfg {
+  static constexpr int NT = W8 ? 512 : 256;          // threads per workgroup
+  static constexpr int WN = NT / 128;                // waves along n (2 or 4)
   static constexpr int LDK = BK + 4;                 // padded LDS row (floats)
-  static constexpr int A_F4 = BM * BK / 4 / kThreads;  // float4 of A per thread
-  static constexpr int B_BLK = BK * BN / 16 / kThreads;  // 4x4 B blocks per thread
+  static constexpr int A_F4 = BM * BK / 4 / NT;  // float4 of A per thread
+  static constexpr int B_BLK = BK * BN / 16 / NT;  // 4x4 B blocks per thread
   static constexpr int TM = BM / 64;                 // MFMA blocks per wave (m)
-  static constexpr int TN = BN / 64;                 // MFMA blocks per wave (n)
+  static constexpr int TN = BN / 32 / WN;            // MFMA blocks per wave (n)
   static constexpr int LDS_FLOATS = 2 * (BM + BN) * LDK;
   static_assert(BM % 64 == 0 && BN % 64 == 0, "tile must be a multiple of 64");
   static_assert(BK % 8 == 0, "BK must be a multiple of 8");
-  static_assert(A_F4 * kThreads * 4 == BM * BK, "A tile must split evenly");
-  static_assert(B_BLK * kThreads * 16 == BK * BN, "B tile must split evenly");
+  static_assert(A_F4 * NT * 4 == BM * BK, "A tile must split evenly");
+  static_assert(B_BLK * NT * 16 == BK * BN, "B tile must split evenly");
 };
 
 __device__ __forceinline__ float4 ld4(const float* p) {
@@ -107,12 +117,12 @@ __device__ __forceinline__ float4 ld4(const float* p) {
 constexpr bool kEarlyStore = true;
 
 template <int BM, int BN, int BK, bool CHECK, bool TB, bool EPI, bool V4 = false, bool KF = false, bool HY = false>
-__global__ __launch_bounds__(kThreads) void sgemm_mfma_kernel(
+__global__ __launch_bounds__((EPI && BM == 256 && BN == 256) ? 512 : 256) void sgemm_mfma_kernel(
     int M, int N, int K, const float* __restrict__ A, int lda, long long sA,
     const float* __restrict__ B, int ldb, long long sB, float* __restrict__ C,
     int ldc, long long sC, int tiles_m, int tiles_n, const float* __restrict__ bias, int act,
     int hy_ndp, int hy_r, int hy_kt, float* __restrict__ hy_P, long long sAz, long long sBz, long long sCz) {
-  using G = Cfg<BM, BN, BK>;
+  using G = Cfg<BM, BN, BK, EPI && BM == 256 && BN == 256>;
   constexpr int LDK = G::LDK;
   extern __shared__ float4 smem4[];
   float* smem = reinterpret_cast<float*>(smem4);
@@ -197,17 +207,17 @@ __global__ __launch_bounds__(kThreads) void sgemm_mfma_kernel(
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int li = lane & 31, lh = lane >> 5;
-  const int wm = (wave >> 1) * (BM / 2);
-  const int wn = (wave & 1) * (BN / 2);
+  const int wm = (wave / G::WN) * (BM / 2);
+  const int wn = (wave % G::WN) * (BN / G::WN);
 
   // ---- global -> register staging ----
-  // A: float4 f covers row (tid / (BK/4)) + f * (kThreads / (BK/4)), cols
+  // A: float4 f covers row (tid / (BK/4)) + f * (NT / (BK/4)), cols
   //    4*(tid % (BK/4)) .. +3 of the k-tile.
   constexpr int A_TPR = BK / 4;                 // threads per A row
-  constexpr int A_RSTEP = kThreads / A_TPR;     // rows per float4 round
+  constexpr int A_RSTEP = G::NT / A_TPR;     // rows per float4 round
   const int a_r = tid / A_TPR, a_c = (tid % A_TPR) * 4;
   // B: 4x4 block q covers k rows 4*kq .. +3 and n cols 4*nq .. +3 where
-  //    blk = tid + q*kThreads, kq = blk % (BK/4), nq = blk / (BK/4).  The 8
+  //    blk = tid + q*NT, kq = blk % (BK/4), nq = blk / (BK/4).  The 8
   //    lanes of an LDS store phase then write one row's 8 consecutive float4
   //    (128 contiguous bytes, no bank conflict); with nq varying fastest
   //    they wrote rows 4 apart, 16-way conflicted (measured: 130.5 vs 134.3
@@ -228,7 +238,7 @@ __global__ __launch_bounds__(kThreads) void sgemm_mfma_kernel(
   constexpr bool BROW = !TB && !CHECK && BM == 256;
   constexpr int LDN = BN + 4;                   // padded [k] row of B (floats)
   constexpr int B_TPR = BN / 4;                 // threads per B row
-  constexpr int B_RSTEP = kThreads / B_TPR;     // B rows per float4 round
+  constexpr int B_RSTEP = G::NT / B_TPR;     // B rows per float4 round
   static_assert(!BROW || (BK * LDN <= BN * LDK && 4 * G::B_BLK * B_RSTEP == BK), "B row layout");
   const int b_r = tid / B_TPR, b_c = (tid % B_TPR) * 4;
 
@@ -275,7 +285,7 @@ __global__ __launch_bounds__(kThreads) void sgemm_mfma_kernel(
     } else {
 #pragma unroll
       for (int q = 0; q < G::B_BLK; ++q) {
-        const int gn = n0 + 4 * ((tid + q * kThreads) / B_KQ);
+        const int gn = n0 + 4 * ((tid + q * G::NT) / B_KQ);
         boff[q] = gn < N ? (unsigned)gn * 4u : kBad;  // column, or kBad
       }
     }
@@ -328,7 +338,7 @@ __global__ __launch_bounds__(kThreads) void sgemm_mfma_kernel(
     } else {
 #pragma unroll
       for (int q = 0; q < G::B_BLK; ++q) {
-        const int blk = tid + q * kThreads;
+        const int blk = tid + q * G::NT;
         const int kq = blk % B_KQ, nq = blk / B_KQ;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -373,7 +383,7 @@ __global__ __launch_bounds__(kThreads) void sgemm_mfma_kernel(
     }
 #pragma unroll
     for (int q = 0; q < G::B_BLK; ++q) {
-      const int blk = tid + q * kThreads;
+      const int blk = tid + q * G::NT;
       const int kq = blk % B_KQ, nq = blk / B_KQ;
       // transpose the 4(k) x 4(n) block: column c of rb -> LDS row n
       float* base = bs + (4 * nq) * LDK + 4 * kq;
@@ -608,14 +618,14 @@ hipError_t launch_tiles(hipStream_t s, int batch, int m, int n, int k,
                         int ldb, long long sB, float* C, int ldc, long long sC,
                         const float* bias, int act, int nz = 1, long long sAz = 0, long long sBz = 0,
                         long long sCz = 0) {
-  using G = Cfg<BM, BN, BK>;
+  using G = Cfg<BM, BN, BK, EPI && BM == 256 && BN == 256>;
   const int tm = (m + BM - 1) / BM, tn = (n + BN - 1) / BN;
   const size_t lds = sizeof(float) * G::LDS_FLOATS;
   auto kern = sgemm_mfma_kernel<BM, BN, BK, CHECK, TB, EPI, V4, KF>;
   hipError_t e = bch::ensure_dynamic_lds(reinterpret_cast<const void*>(kern), (int)lds);
   if (e != hipSuccess) return e;
   if (batch > 65535 || nz > 65535) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(kern, dim3(tm * tn, batch, nz), dim3(kThreads), lds, s, m, n, k,
+  hipLaunchKernelGGL(kern, dim3(tm * tn, batch, nz), dim3(G::NT), lds, s, m, n, k,
                      A, lda, sA, B, ldb, sB, C, ldc, sC, tm, tn, bias, act, 0, 0, 0, nullptr, sAz, sBz, sCz);
   return hipGetLastError();
 }
@@ -625,13 +635,13 @@ hipError_t launch_tiles(hipStream_t s, int batch, int m, int n, int k,
 template <int BM, int BN, int BK, bool CHECK, bool TB, bool EPI, bool V4, bool KF>
 hipError_t launch_hyb_tiles(hipStream_t s, int m, int n, int k, const float* A, int lda, const float* B, int ldb,
                             float* C, int ldc, const float* bias, int act, int ndp, int r, int S, int kt, float* P) {
-  using G = Cfg<BM, BN, BK>;
+  using G = Cfg<BM, BN, BK, EPI && BM == 256 && BN == 256>;
   const int tm = (m + BM - 1) / BM, tn = (n + BN - 1) / BN;
   const size_t lds = sizeof(float) * G::LDS_FLOATS;
   auto kern = sgemm_mfma_kernel<BM, BN, BK, CHECK, TB, EPI, V4, KF, true>;
   hipError_t e = bch::ensure_dynamic_lds(reinterpret_cast<const void*>(kern), (int)lds);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(kern, dim3(ndp + r * S), dim3(kThreads), lds, s, m, n, k, A, lda, 0LL, B, ldb, 0LL, C, ldc,
+  hipLaunchKernelGGL(kern, dim3(ndp + r * S), dim3(G::NT), lds, s, m, n, k, A, lda, 0LL, B, ldb, 0LL, C, ldc,
                      0LL, tm, tn, bias, act, ndp, r, kt, P, 0LL, 0LL, 0LL);
   return hipGetLastError();
 }
