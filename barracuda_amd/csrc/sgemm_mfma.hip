@@ -474,9 +474,17 @@ __global__ __launch_bounds__((EPI && BM == 256 && BN == 256) ? 512 : 256) void s
   constexpr int MPW = !PIN ? 0 : (NM - NR) / NW >= 2 ? 2 : 1;  // MFMAs after each store
   static_assert(NM >= NR + MPW * NW, "chunk too small to cover its LDS traffic");
   // ES: the last k-tile is peeled (below) so that C leaves block by block
-  // (256-row tiles in every load mode, and the scalar-guarded 128 x 128 tile: the
-  // float4-guarded and unguarded 128 x 128 tiles measured 0.2-1.1% slower with it)
-  constexpr bool ES = kEarlyStore && !EPI && !HY && G::TN % 2 == 0 && (BM == 256 || (CHECK && !V4));
+  // (the 256 x 128 tile in every load mode, and the scalar-guarded 128 x 128 tile: the
+  // float4-guarded and unguarded 128 x 128 tiles measured 0.2-1.1% slower with it).  The
+  // 256 x 256 tile stores after the loop: with B row-major in LDS, holding the last tile's four
+  // chunks of fragments spilled 64-101 VGPRs to scratch in every load mode, and without the peel
+  // it spills none.  Same box, two runs each (us, peeled -> not): 16 x 1024^3 246.3-247.9 ->
+  // 243.7-243.8, 32 x 1024 x 1024 x 512 264.5 -> 254.5-254.8, 16384 x 4096 x 512 518-520 ->
+  // 502, 4096 x 4096 x 1024 247.3-247.5 -> 243.9-244.5, 4095 x 4096 x 33 (scalar guards)
+  // 38.9-39.0 -> 35.0, 4096^3 and 8192^3 even, 4000^3 (float4 guards) 922.5-924.7 ->
+  // 925.6-927.9.
+  constexpr bool ES = kEarlyStore && !EPI && !HY && G::TN % 2 == 0 && !(BM == 256 && BN == 256) &&
+                      (BM == 256 || (CHECK && !V4));
   const int nloop = ES ? nk - 1 : nk;
   for (int t = 0; t < nloop; ++t) {
     const int cur = t & 1;
