@@ -221,6 +221,27 @@ def test_sgemm_ex_exact_on_integers(dev, transb):
             assert np.array_equal(got, O.linear_f32(x, w, b, relu=True))
 
 
+@pytest.mark.parametrize("m,n,k,transb", [(1024, 1024, 512, 1), (1024, 1024, 512, 0), (1000, 1024, 512, 1),
+                                          (1001, 1003, 515, 0), (6144, 6144, 1536, 1)])
+def test_epilogue_tile_gelu(dev, m, n, k, transb):
+    """The 256 x 256 tile with the bias and activation epilogue (eight wavefronts, two per SIMD)
+    in each load mode -- unguarded, float4-guarded, scalar-guarded -- and in the hybrid plan
+    (6144^2 x 1536), with bias + GELU and bias + ReLU: one row from every 256-row tile against
+    f64."""
+    _say(f"epilogue tile m={m} n={n} k={k} transb={transb}")
+    rng = O.Lcg(m + 5 * n + 3 * k + transb)
+    x = rng.uniform((m, k))
+    w = rng.uniform((n, k) if transb else (k, n))
+    bias = rng.uniform((n,))
+    rows = sorted({t * 256 + (t * 97 + 13) % 256 for t in range(m // 256)} | {0, m - 1})
+    rows = [r for r in rows if r < m]
+    z = _ref(x[rows], w, bias, transb, False)
+    gelu = 0.5 * z * (1.0 + np.tanh(0.7978845608 * (z + 0.044715 * z ** 3)))
+    for act, want in ((N.BCH_ACT_GELU, gelu), (N.BCH_ACT_RELU, np.maximum(z, 0.0))):
+        got = _sgemm_ex(dev, transb, x, w, bias, act)[rows]
+        assert O.max_rel_err(got, want) <= TOL, act
+
+
 @pytest.mark.parametrize("batch,dims", [(256, [512, 1024, 256, 64]), (7, [33, 65, 17]), (1, [4096, 1024, 4096]),
                                         (1024, [256, 256, 256])])
 def test_fused_mlp_vs_f64(dev, batch, dims):
