@@ -33,7 +33,9 @@
 //     the loop's back edge, and every iteration ended copying them into
 //     place behind a wait for all of the next tile's loads.  4096^3 NN
 //     72.5-72.9 -> 73.9-74.0 TFLOP/s, TN 71.2-71.5 -> 74.1-74.2, 2048^3
-//     69.0 -> 71.2 (one box, two runs each).
+//     69.0 -> 71.2 (one box, two runs each); A^T kept [k][m] with B^T given
+//     [n][k] (TT), 72.6-72.7 -> 73.6-73.9 (one 4-byte spill, outside the
+//     loop).
 //   * Software pipeline: a k-tile's fragments are read in two halves, the
 //     second half of tile t under the MFMAs of its first two steps and the
 //     first half of tile t + 1 (after the one barrier per tile) under its
@@ -245,7 +247,7 @@ __global__ __launch_bounds__(kDT, OCC) void dgemm_mfma_kernel(
   const int nk = (kend - kbeg + kDBK - 1) / kDBK;
   const int lastk = kbeg + (nk - 1) * kDBK;
   d2 a[TM][2], b[TN][2];
-  constexpr bool AROW = TA && !TB && !CHECK, BROW = !TB && !CHECK;
+  constexpr bool AROW = TA && !CHECK, BROW = !TB && !CHECK;
   static_assert(16 * (BM + 2) <= BM * kDLDK && 16 * (BN + 2) <= BN * kDLDK, "k-row tiles fit the buffers");
   auto read_half = [&](int buf, int h) {
     if constexpr (AROW) {
