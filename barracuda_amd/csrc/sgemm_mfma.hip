@@ -235,7 +235,13 @@ __global__ __launch_bounds__((EPI && BM == 256 && BN == 256) ? 512 : 256) void s
   // scheduling groups counting the pairs its loop waits only for the previous tile's loads, and
   // it measured even: 128 x 11008 x 4096 109.2-110.3 -> 108.2 us, 2048 x 2048 x 4096 250.2 ->
   // 252.8, 2048 x 2048 x 1024 68.9 -> 68.3, 1024 x 1024 x 4096 unchanged.)
-  constexpr bool BROW = !TB && !CHECK && BM == 256;
+  // The 64 x 64 small tile (BK 64) takes the row layout too, with its fragments' B values counted
+  // as read pairs in the scheduling groups (the compiler merges them into ds_read2_b32; counted
+  // singly they overfill its 4-MFMA chunks): its loop had ended copying the staged B registers
+  // behind a wait for the next tile's loads.  Same box, two runs each (us): 256^3 8.6-8.7 ->
+  // 8.0-8.1, 512^3 13.5-13.7 -> 13.4, 768^3 19.1-19.2 -> 18.8-18.9, 1024^3 24.4 -> 24.5-24.6,
+  // 1024 x 2048 x 1024 even.
+  constexpr bool BROW = !TB && !CHECK && (BM == 256 || (BM == 64 && BN == 64));
   constexpr int LDN = BN + 4;                   // padded [k] row of B (floats)
   constexpr int B_TPR = BN / 4;                 // threads per B row
   constexpr int B_RSTEP = G::NT / B_TPR;     // B rows per float4 round
@@ -465,7 +471,7 @@ __global__ __launch_bounds__((EPI && BM == 256 && BN == 256) ? 512 : 256) void s
   // The order is pinned with scheduling groups (mask 0x008 MFMA, 0x100 LDS
   // read, 0x200 LDS write): left alone, the scheduler sank the global loads
   // to the end of the body behind a vmcnt(0) and clustered the LDS traffic.
-  constexpr int NR = G::TM + (BROW ? 4 : 1) * G::TN;       // LDS reads per chunk
+  constexpr int NR = G::TM + (BROW ? (BM == 64 ? 2 : 4) : 1) * G::TN;       // LDS reads per chunk
   constexpr int NW = G::A_F4 + 4 * G::B_BLK;               // LDS stores per tile
   constexpr int NM = 4 * G::TM * G::TN;                    // MFMAs per chunk
   // the small tile (one MFMA block per wavefront) has too few MFMAs in a chunk to pin its
